@@ -1,0 +1,253 @@
+"""Benchmark of the int8-KV attention hot path on one MI355X.
+
+Headline (BASELINE metric): split-K int8-KV decode attention at B=64, ctx=4096, Hq=16, Hkv=8,
+D=128 — µs per layer and achieved HBM GB/s against the 8 TB/s peak. One step = one
+`decode_attention` call (split kernel + reduce kernel) over the whole batch, inputs resident in
+HBM. Distinct cache sets are rotated between steps so the 256 MB MALL cannot serve a repeat.
+
+Also reported beside it (extra keys): config-4 KV quantize-on-write and chunked-prefill
+attention, each timed with HIP events on the stream the kernels run on.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--sweep]
+"""
+
+import argparse
+import importlib
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import torch
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO))
+
+METRIC = "int8-KV decode attn µs/layer + HBM GB/s (% of 8 TB/s), B=64 ctx=4096"
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2516.6
+SCALE = 128 ** -0.5
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def _events(n):
+    return [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+
+
+def time_decode(ie, wls, steps, warmup):
+    """Whole-step time (events at the ends) and the split kernel's own average duration
+    (events around each launch, separate pass)."""
+    K = ie.kernels
+    outs = [torch.empty_like(w.q) for w in wls]
+    wss = [K.decode_attention_workspace(w.q) for w in wls]
+
+    def run(i):
+        w = wls[i % len(wls)]
+        K.decode_attention_split(w.q, w.cache, w.cached_lens, w.slot_ids, w.num_decoding, SCALE,
+                                 outs[i % len(wls)], wss[i % len(wls)])
+        K.decode_attention_combine(w.q, w.cache, w.cached_lens, w.num_decoding,
+                                   outs[i % len(wls)], wss[i % len(wls)])
+
+    for i in range(warmup):
+        run(i)
+    torch.cuda.synchronize()
+    e0, e1 = _events(2)
+    e0.record()
+    for i in range(steps):
+        run(i)
+    e1.record()
+    torch.cuda.synchronize()
+    step_ms = e0.elapsed_time(e1) / steps
+
+    ev = _events(3 * steps)
+    for i in range(steps):
+        w = wls[i % len(wls)]
+        o, ws = outs[i % len(wls)], wss[i % len(wls)]
+        ev[3 * i].record()
+        K.decode_attention_split(w.q, w.cache, w.cached_lens, w.slot_ids, w.num_decoding, SCALE,
+                                 o, ws)
+        ev[3 * i + 1].record()
+        K.decode_attention_combine(w.q, w.cache, w.cached_lens, w.num_decoding, o, ws)
+        ev[3 * i + 2].record()
+    torch.cuda.synchronize()
+    split_ms = sum(ev[3 * i].elapsed_time(ev[3 * i + 1]) for i in range(steps)) / steps
+    comb_ms = sum(ev[3 * i + 1].elapsed_time(ev[3 * i + 2]) for i in range(steps)) / steps
+    return step_ms, split_ms, comb_ms
+
+
+def time_op(fn, steps, warmup):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    ev = _events(2 * steps)
+    for i in range(steps):
+        ev[2 * i].record()
+        fn()
+        ev[2 * i + 1].record()
+    torch.cuda.synchronize()
+    return sum(ev[2 * i].elapsed_time(ev[2 * i + 1]) for i in range(steps)) / steps
+
+
+def cpu_baseline(wl_gpu, sample_seqs):
+    """The numpy oracle (the reference math restated) on `sample_seqs` sequences of the
+    headline batch, one thread, scaled to the whole batch."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+
+    from oracle import attention as oat
+    from oracle import kv_cache as okv
+
+    idx = list(range(sample_seqs))
+    slots = wl_gpu.slot_ids[idx].long()
+    c = wl_gpu.cache
+    cache = okv.CacheArrays(*(t[slots].cpu().numpy() for t in
+                              (c.k, c.v, c.k_scale, c.v_scale, c.k_calibration)))
+    q = wl_gpu.q[idx].float().cpu().numpy()
+    lens = wl_gpu.cached_lens[idx].cpu().numpy()
+    with threadpool_limits(1):
+        t0 = time.perf_counter()
+        oat.decode_attention(q, cache, lens, np.arange(sample_seqs), sample_seqs, SCALE)
+        dt = time.perf_counter() - t0
+    B = len(wl_gpu.ctx)
+    us_layer = dt * 1e6 * B / sample_seqs
+    return us_layer, dt
+
+
+def read_traffic():
+    """HBM bytes per launch of the split kernel from the committed rocprofv3 PMC summary."""
+    p = REPO / "profiles" / "decode_attention_B64_ctx4096_pmc.md"
+    if not p.exists():
+        return None
+    for line in p.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":")[1].strip())
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--batch", type=int, default=64)
+    ap.add_argument("--ctx", type=int, default=4096)
+    ap.add_argument("--rotate", type=int, default=2, help="distinct cache sets cycled per step")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-sample", type=int, default=8)
+    ap.add_argument("--sweep", action="store_true", help="also time the config-3 shape sweep")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(decode attention shards by sequence or KV head without exchange); "
+              "run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    ie = importlib.import_module("inference-engine_amd")
+    W = importlib.import_module("inference-engine_amd.workloads")
+    K = ie.kernels
+    dev = "cuda:0"
+    torch.cuda.set_device(0)
+
+    ctx = [args.ctx] * args.batch
+    log(f"building {args.rotate} cache sets B={args.batch} ctx={args.ctx}")
+    wls = [W.decode_workload(ctx, seed=s, device=dev) for s in range(args.rotate)]
+    torch.cuda.synchronize()
+    alg_bytes = wls[0].algorithmic_bytes()
+    log("timing decode attention")
+    step_ms, split_ms, comb_ms = time_decode(ie, wls, args.steps, args.warmup)
+    gbs = alg_bytes / (step_ms * 1e-3) / 1e9
+    split_gbs = alg_bytes / (split_ms * 1e-3) / 1e9
+    log(f"decode step {step_ms*1e3:.2f} us ({gbs:.0f} GB/s); split kernel {split_ms*1e3:.2f} us "
+        f"({split_gbs:.0f} GB/s), combine {comb_ms*1e3:.2f} us")
+
+    extra = {}
+    # ---- config 4: KV write + chunked prefill ----
+    try:
+        mw = W.mixed_to(W.config4(seed=0), dev)
+        gi = mw.inputs
+        kv_ms = time_op(lambda: K.quantize_kv_prefill(mw.k, mw.v, gi["cu_seqlens"],
+                                                      gi["slot_ids"], gi["cached_lens"],
+                                                      gi["num_decoding"], mw.cache),
+                        args.steps, args.warmup)
+        n_new = sum(L for L, _ in mw.chunks)
+        kv_bytes = n_new * 8 * (128 * 2 * 2 + 128 * 2 + 8)
+        extra["kv_write_config4"] = {"us": round(kv_ms * 1e3, 3),
+                                     "GBps": round(kv_bytes / (kv_ms * 1e-3) / 1e9, 1),
+                                     "bytes": kv_bytes}
+        log(f"kv write config4 {kv_ms*1e3:.2f} us")
+        flops = W.prefill_flops(mw.chunks)
+        try:
+            pf_ms = time_op(lambda: K.prefill_attention(
+                mw.q, mw.k, mw.v, gi["seq_ids"], gi["cu_seqlens"], gi["tile_start"], mw.cache,
+                gi["slot_ids"], gi["cu_cached"], mw.block_m), args.steps, args.warmup)
+            tf = flops / (pf_ms * 1e-3) / 1e12
+            extra["prefill_config4"] = {"us": round(pf_ms * 1e3, 3), "TFLOPs": round(tf, 1),
+                                        "mfma_frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
+                                        "flops": flops}
+            log(f"prefill config4 {pf_ms*1e3:.2f} us {tf:.1f} TFLOP/s")
+        except RuntimeError as e:
+            extra["prefill_config4"] = {"error": str(e).splitlines()[0][:200]}
+    except Exception as e:  # reported, never silently replaced
+        extra["config4_error"] = str(e).splitlines()[0][:200]
+
+    if args.sweep:
+        sweep = {}
+        for b in (16, 64, 256):
+            for c in (1024, 4096):
+                ws = [W.decode_workload([c] * b, seed=s, device=dev) for s in range(2)]
+                sm, spm, _ = time_decode(ie, ws, 20, 5)
+                by = ws[0].algorithmic_bytes()
+                sweep[f"B{b}_ctx{c}"] = {"us": round(sm * 1e3, 2),
+                                         "GBps": round(by / (sm * 1e-3) / 1e9, 1)}
+                log(f"sweep B={b} ctx={c}: {sm*1e3:.2f} us")
+                del ws
+                torch.cuda.empty_cache()
+        extra["decode_sweep"] = sweep
+
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline (numpy oracle, 1 thread)")
+        us_cpu, dt = cpu_baseline(wls[0], args.cpu_sample)
+        cpu = {"value": round(alg_bytes / (us_cpu * 1e-6) / 1e9, 3), "unit": "GB/s",
+               "us_per_layer": round(us_cpu, 1), "cores": 1, "kind": "port",
+               "sample": f"{args.cpu_sample} of {args.batch} sequences at ctx {args.ctx} "
+                         f"({dt:.2f} s), scaled x{args.batch / args.cpu_sample:g}",
+               "cpu": os.uname().machine}
+    traffic = read_traffic()
+    line = {
+        "metric": METRIC,
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_ms, 5),
+        "us_per_layer": round(step_ms * 1e3, 2),
+        "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": "decode_attention B=64 ctx=4096 (BASELINE config 3 headline)",
+                   "batch": args.batch, "ctx": args.ctx, "q_heads": 16, "kv_heads": 8,
+                   "head_dim": 128, "rotated_cache_sets": args.rotate,
+                   "algorithmic_bytes": alg_bytes},
+        "roofline": {"bound": "hbm", "achieved": round(split_gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(split_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": traffic, "kernel": "decode_split_kernel",
+                     "kernel_us": round(split_ms * 1e3, 2)},
+        "cpu_baseline": cpu,
+        "combine_us": round(comb_ms * 1e3, 2),
+        **extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

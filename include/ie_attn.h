@@ -1,0 +1,201 @@
+/*
+ * ie_attn.h — C ABI of the MI355X (gfx950) int8-KV attention path.
+ *
+ * One shared library, libie_attn.so, exports these entry points. Every pointer is a device
+ * pointer, every stride is in elements (not bytes), every call is asynchronous on `stream`,
+ * allocates nothing, never synchronises, and reads per-step counts (`num_decoding`,
+ * `cached_lens`, `cu_seqlens`, ...) on the device only, so every call can be captured into a
+ * hipGraph. Grids depend on shapes alone.
+ *
+ * Geometry supported by the kernels: head_dim 128, 2 query heads per KV head (Qwen3-1.7B:
+ * 16 query heads over 8 KV heads). Other geometries return hipErrorInvalidValue.
+ *
+ * Each entry point replaces one Python wrapper of kbwal/inference-engine's Triton kernel API,
+ * cited as qwen3-1.7b/kernels.py:<line>, with the same argument meaning. Bit-level contracts:
+ *   - int8 values and fp32 scales written by the two quantizing entry points are computed with
+ *     IEEE round-to-nearest-even fp32 operations in a fixed order (documented per function),
+ *   - attention outputs are bf16, rounded to nearest even from fp32 accumulators.
+ */
+#ifndef IE_ATTN_H
+#define IE_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* bf16 values travel as their 16-bit patterns. */
+typedef uint16_t ie_bf16;
+
+/*
+ * One layer's int8 KV cache (qwen3-1.7b/kernels.py:11-17 `LayerKVCache`; allocated by
+ * qwen3-1.7b/engine.py:472-492). Layout, unchanged from the reference:
+ *   k, v           int8  [pool, num_kv_heads, max_len, head_dim]
+ *   k_scale,v_scale fp32 [pool, num_kv_heads, max_len]
+ *   k_calibration  fp32  [pool, num_kv_heads, 1, head_dim]
+ * k and v share one set of strides, k_scale and v_scale share another
+ * (the reference asserts both, kernels.py:284-287). head_dim and the token axis of the scales
+ * must be unit-stride.
+ */
+typedef struct ie_kv_cache {
+    int8_t* k;
+    int8_t* v;
+    float* k_scale;
+    float* v_scale;
+    float* k_calibration;
+    int64_t pool;
+    int64_t num_kv_heads;
+    int64_t max_len;
+    int64_t head_dim;
+    int64_t stride_slot;       /* k/v stride of dim 0 */
+    int64_t stride_head;       /* k/v stride of dim 1 */
+    int64_t stride_tok;        /* k/v stride of dim 2 */
+    int64_t scale_stride_slot; /* k_scale/v_scale stride of dim 0 */
+    int64_t scale_stride_head; /* k_scale/v_scale stride of dim 1 */
+    int64_t cal_stride_slot;   /* k_calibration stride of dim 0 */
+    int64_t cal_stride_head;   /* k_calibration stride of dim 1 */
+} ie_kv_cache;
+
+/* Library version, (major << 16) | minor. */
+int32_t ie_attn_version(void);
+
+/* Human-readable name of the last argument error seen on this thread, or "" if none. */
+const char* ie_attn_last_error(void);
+
+/*
+ * Quantize-on-write for prefilling entries.
+ * Replaces qwen3-1.7b/kernels.py:826-865 `quantize_kv_prefill(k, v, cu_seqlens, slot_ids,
+ * cached_lens, num_decoding, cache)` (kernel kernels.py:717-823).
+ *
+ * k, v: bf16 [N, num_kv_heads, head_dim], any token/head strides (v is usually a strided view of
+ * the fused qkv output). Entry b (num_decoding[0] <= b < num_entries, chunk_len > 0) writes its
+ * packed tokens [cu_seqlens[b], cu_seqlens[b+1]) to cache row slot_ids[b] starting at column
+ * cached_lens[b]. When cached_lens[b] == 0 the per-channel K calibration of that row is first
+ * recomputed as max(1e-3, max_t |k[t, d]|) over the chunk and stored; otherwise it is read.
+ * Per token and head: x = k / cal; s = max(max|x|, 1e-6) / 127; q = clamp(rint(x / s), ±127).
+ * V uses the same formula with cal = 1.
+ */
+hipError_t ie_quantize_kv_prefill(const ie_bf16* k, int64_t k_stride_tok, int64_t k_stride_head,
+                                  const ie_bf16* v, int64_t v_stride_tok, int64_t v_stride_head,
+                                  int64_t num_tokens,
+                                  const int32_t* cu_seqlens, const int32_t* slot_ids,
+                                  const int32_t* cached_lens, const int32_t* num_decoding,
+                                  int32_t num_entries, const ie_kv_cache* cache,
+                                  hipStream_t stream);
+
+/*
+ * Decode-side q/k RMSNorm + RoPE + calibration fold + K/V quantize-on-write.
+ * Replaces qwen3-1.7b/kernels.py:483-544 `fused_rope_kv_decode(q, k, v, q_norm_weight,
+ * k_norm_weight, cos, sin, slot_ids, kv_cache, cached_lens, num_decoding, eps)`
+ * (kernel kernels.py:364-480).
+ *
+ * q: bf16 [B, num_q_heads, head_dim]; k, v: bf16 [B, num_kv_heads, head_dim] (strided views
+ * allowed); q_norm_weight, k_norm_weight: bf16 [head_dim]; cos, sin: bf16 [B, 1, head_dim/2].
+ * For b < num_decoding[0]: q_out[b, h] = bf16(rope(rmsnorm(q[b, h])) * cal[slot, h / 2]) and the
+ * int8 K (rope(rmsnorm(k)) / cal) and V with their scales are written at column cached_lens[b]
+ * of row slot_ids[b]. Rows b >= num_decoding[0] of q_out are left untouched.
+ * RMSNorm: sum of squares of each 64-element half by a butterfly over lane distance
+ * 32,16,8,4,2,1, halves added, / head_dim, + eps, rstd = 1 / sqrt(.) (both IEEE).
+ */
+hipError_t ie_fused_rope_kv_decode(const ie_bf16* q, int64_t q_stride_b, int64_t q_stride_h,
+                                   const ie_bf16* k, int64_t k_stride_b, int64_t k_stride_h,
+                                   const ie_bf16* v, int64_t v_stride_b, int64_t v_stride_h,
+                                   const ie_bf16* q_norm_weight, const ie_bf16* k_norm_weight,
+                                   const ie_bf16* cos, int64_t cos_stride_b,
+                                   const ie_bf16* sin, int64_t sin_stride_b,
+                                   const int32_t* slot_ids, const int32_t* cached_lens,
+                                   const int32_t* num_decoding, int32_t batch,
+                                   int32_t num_q_heads, float eps, const ie_kv_cache* cache,
+                                   ie_bf16* q_out, int64_t q_out_stride_b,
+                                   int64_t q_out_stride_h, hipStream_t stream);
+
+/*
+ * Bytes of device workspace ie_decode_attention needs for `batch` sequences on the current
+ * device (fp32 split-K partials [batch, num_q_heads, max_splits, head_dim + 2]).
+ */
+size_t ie_decode_attention_workspace_size(int32_t batch, int32_t num_q_heads, int32_t head_dim);
+
+/* Upper bound on splits per sequence on the current device (the partial buffer stride). */
+int32_t ie_decode_attention_max_splits(int32_t num_kv_heads);
+
+/*
+ * Split-K GQA decode attention over the int8 cache, then the partial-softmax reduce.
+ * Replaces qwen3-1.7b/kernels.py:272-361 `decode_attention(q, kv_cache, cached_lens, slot_ids,
+ * num_decoding, scale, out)` (kernels kernels.py:73-213 and 216-264, work split 20-70).
+ *
+ * q: bf16 [B, num_q_heads, head_dim], calibration already folded in. Sequence b < num_decoding[0]
+ * attends to tokens [0, cached_lens[b] + 1) of cache row slot_ids[b]:
+ *   out[b, h] = sum_t softmax_t(scale * k_scale[t] * <q[b, h], k[t]>) * v_scale[t] * v[t].
+ * Only rows b < num_decoding[0] of out are written. `workspace` must hold
+ * ie_decode_attention_workspace_size(B, num_q_heads, head_dim) bytes.
+ */
+hipError_t ie_decode_attention(const ie_bf16* q, int64_t q_stride_b, int64_t q_stride_h,
+                               int32_t batch, int32_t num_q_heads, const ie_kv_cache* cache,
+                               const int32_t* cached_lens, const int32_t* slot_ids,
+                               const int32_t* num_decoding, float scale, ie_bf16* out,
+                               int64_t out_stride_b, int64_t out_stride_h, void* workspace,
+                               size_t workspace_bytes, hipStream_t stream);
+
+/*
+ * The two launches of ie_decode_attention, exposed separately so a profiler harness can time
+ * the split kernel on its own: ie_decode_attention == split followed by combine, same args.
+ */
+hipError_t ie_decode_attention_split(const ie_bf16* q, int64_t q_stride_b, int64_t q_stride_h,
+                                     int32_t batch, int32_t num_q_heads,
+                                     const ie_kv_cache* cache, const int32_t* cached_lens,
+                                     const int32_t* slot_ids, const int32_t* num_decoding,
+                                     float scale, ie_bf16* out, int64_t out_stride_b,
+                                     int64_t out_stride_h, void* workspace,
+                                     size_t workspace_bytes, hipStream_t stream);
+hipError_t ie_decode_attention_combine(int32_t batch, int32_t num_q_heads, int32_t head_dim,
+                                       int32_t num_kv_heads, const int32_t* cached_lens,
+                                       const int32_t* num_decoding, ie_bf16* out,
+                                       int64_t out_stride_b, int64_t out_stride_h,
+                                       void* workspace, size_t workspace_bytes,
+                                       hipStream_t stream);
+
+/*
+ * int8 cache prefix -> bf16 (k = bf16((q * k_scale) * cal), v = bf16(q * v_scale)).
+ * Replaces qwen3-1.7b/kernels.py:935-970 `dequantize_kv_prefix(cache, cu_cached, slot_ids,
+ * k_out, v_out)` (kernel kernels.py:868-932). Entry b's prefix, cache row slot_ids[b] columns
+ * [0, cu_cached[b+1] - cu_cached[b]), goes to rows [cu_cached[b], cu_cached[b+1]) of
+ * k_out/v_out: bf16 [num_kv_heads, >= total, head_dim].
+ */
+hipError_t ie_dequantize_kv_prefix(const ie_kv_cache* cache, const int32_t* cu_cached,
+                                   const int32_t* slot_ids, int32_t num_entries,
+                                   ie_bf16* k_out, ie_bf16* v_out, int64_t out_stride_head,
+                                   int64_t out_stride_tok, hipStream_t stream);
+
+/*
+ * Causal chunked-prefill attention that reads each entry's cached prefix straight from the int8
+ * cache (dequantized in LDS with the same rounding as ie_dequantize_kv_prefix) and runs QK^T and
+ * PV on bf16 MFMA.
+ * Replaces qwen3-1.7b/kernels.py:1129-1175 `prefill_attention(q, k, v, seq_ids, cu_seqlens,
+ * tile_start, k_prefix, v_prefix, cu_cached, PREFILL_BLOCK_M)` (kernel kernels.py:987-1126)
+ * together with the dequantize_kv_prefix call that fed it (qwen3-1.7b/architecture.py:151-170):
+ * the bf16 prefix buffers are replaced by (cache, slot_ids).
+ *
+ * q: bf16 [N, num_q_heads, head_dim]; k, v: bf16 [N, num_kv_heads, head_dim] (the new chunk,
+ * strided views allowed); tile_start: int32 [num_tiles], first packed row of each tile of
+ * block_m rows, -1 = no work; every tile lies inside one entry. Row m of entry e attends to the
+ * e's prefix (cache row slot_ids[e], columns [0, cu_cached[e+1] - cu_cached[e])) and to its own
+ * chunk rows [cu_seqlens[e], m]. Rows of out that no tile covers are left untouched.
+ */
+hipError_t ie_prefill_attention(const ie_bf16* q, int64_t q_stride_tok, int64_t q_stride_head,
+                                const ie_bf16* k, int64_t k_stride_tok, int64_t k_stride_head,
+                                const ie_bf16* v, int64_t v_stride_tok, int64_t v_stride_head,
+                                int64_t num_tokens, int32_t num_q_heads,
+                                const int32_t* seq_ids, const int32_t* cu_seqlens,
+                                const int32_t* tile_start, int32_t num_tiles, int32_t block_m,
+                                const ie_kv_cache* cache, const int32_t* slot_ids,
+                                const int32_t* cu_cached, ie_bf16* out, int64_t out_stride_tok,
+                                int64_t out_stride_head, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* IE_ATTN_H */

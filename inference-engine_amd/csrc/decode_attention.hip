@@ -1,0 +1,492 @@
+// Split-K GQA decode attention over the int8 KV cache, for gfx950.
+//
+// Work split (same rule as qwen3-1.7b/kernels.py:20-70): every decoding sequence's tokens
+// [0, cached_len + 1) are cut into pieces of `piece` tokens, piece = roundup(max(MIN_PIECE,
+// cdiv(total_tokens, TARGET)), MIN_PIECE) with TARGET = CUs * WG_PER_CU / Hkv workgroups per KV
+// head. The pieces of all sequences form one work list; workgroup (w, kv head) takes entry w.
+// The grid is (TARGET + B, Hkv): it depends on shapes only, so the launch is graph-capturable,
+// and each workgroup finds its (sequence, piece) on the device from cached_lens.
+//
+// One workgroup = 4 waves = one (sequence, piece, kv head), i.e. both query heads of the GQA
+// pair. Lane (g, c) of a wave (g = lane / 8, c = lane % 8) owns channels [16c, 16c+16) of the
+// four tokens 4g..4g+3 of the wave's 32-token block: each K and V row (128 int8) is read by 8
+// lanes with 16-byte loads, so one load instruction of a wave covers 8 full 128-byte rows.
+//
+// Arithmetic (all VALU, no MFMA: the op is HBM-bound):
+//   int8 -> fp16 by byte permute into the fp16 pattern 0x64xx (= 1024 + byte) after flipping
+//   the sign bit, i.e. the fp16 value 1152 + x exactly; the 1152 offset is removed once per
+//   score (q . 1152 = 1152 * sum(q)) and once per output (sum of P).
+//   q is scaled by a power of two per head so it is exact in fp16; QK^T and PV use the
+//   fp32-accumulating v_dot2_f32_f16. QK partial dots are reduced across the 8 lanes of a row
+//   with DPP. Online softmax in base 2 per lane group; groups and waves are merged at the end
+//   (log-sum-exp), then either the output is written (one piece) or fp32 partials
+//   (m, l, acc) go to the workspace for the combine kernel (kernels.py:216-264).
+#include "ie_common.h"
+
+#ifndef IE_DECODE_WG_PER_CU
+#define IE_DECODE_WG_PER_CU 4
+#endif
+
+namespace ie {
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+constexpr int DA_THREADS = 256;
+constexpr int DA_WAVES = DA_THREADS / IE_WAVE;
+constexpr int DA_U = 4;                            // tokens per lane group per block
+constexpr int DA_TOK_WAVE = 8 * DA_U;              // 32 tokens per wave block
+constexpr int DA_TOK_WG = DA_WAVES * DA_TOK_WAVE;  // 128 tokens per workgroup step
+constexpr int DA_MIN_PIECE = 128;
+constexpr int DA_D = 128;
+constexpr uint32_t K64 = 0x64646464u;
+constexpr float OFFSET = 1152.0f;  // fp16(0x64xx) = 1024 + byte, byte = x + 128
+
+__host__ __device__ inline int cdiv_i(int a, int b) { return (a + b - 1) / b; }
+
+int decode_target(int num_kv_heads) {
+    return std::max(1, device_cu_count() * IE_DECODE_WG_PER_CU / std::max(1, num_kv_heads));
+}
+
+__device__ __forceinline__ int wave_sum_i(int x) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m, IE_WAVE);
+    return x;
+}
+__device__ __forceinline__ int wave_incl_scan_i(int x) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int y = __shfl_up(x, d, IE_WAVE);
+        if (lane >= d) x += y;
+    }
+    return x;
+}
+
+// Piece size for this step (kernels.py:20-37); wave-uniform, every lane returns it.
+__device__ int decode_piece(const int32_t* __restrict__ cached_lens, int nd, int target) {
+    const int lane = threadIdx.x & 63;
+    int total = 0;
+    for (int b0 = 0; b0 < nd; b0 += 64) {
+        const int b = b0 + lane;
+        total += wave_sum_i(b < nd ? cached_lens[b] + 1 : 0);
+    }
+    int piece = max(DA_MIN_PIECE, cdiv_i(total, target));
+    return cdiv_i(piece, DA_MIN_PIECE) * DA_MIN_PIECE;
+}
+
+struct Work {
+    int b, split, needed, piece;
+};
+
+// Entry `w` of the work list (kernels.py:40-70); needed == 0 for idle workgroups.
+__device__ Work decode_assign(const int32_t* __restrict__ cached_lens, int nd, int w, int target) {
+    Work r{0, 0, 0, decode_piece(cached_lens, nd, target)};
+    const int lane = threadIdx.x & 63;
+    int before = 0;
+    for (int b0 = 0; b0 < nd; b0 += 64) {
+        const int b = b0 + lane;
+        const int s = b < nd ? cdiv_i(cached_lens[b] + 1, r.piece) : 0;
+        const int incl = wave_incl_scan_i(s) + before;
+        const int excl = incl - s;
+        const unsigned long long hit = __ballot(s > 0 && excl <= w && w < incl);
+        if (hit) {
+            const int src = __ffsll((long long)hit) - 1;
+            r.b = b0 + src;
+            r.split = w - __shfl(excl, src, IE_WAVE);
+            r.needed = __shfl(s, src, IE_WAVE);
+            return r;
+        }
+        before = __shfl(incl, 63, IE_WAVE);
+    }
+    return r;
+}
+
+__device__ __forceinline__ half2_t as_h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
+__device__ __forceinline__ float fdot2(half2_t a, half2_t b, float c) {
+    return __builtin_amdgcn_fdot2(a, b, c, false);
+}
+__device__ __forceinline__ float exp2_safe(float x) { return __builtin_amdgcn_exp2f(x); }
+
+struct DecodeArgs {
+    const uint16_t* q;
+    int64_t q_sb, q_sh;
+    ie_kv_cache c;
+    const int32_t* cached_lens;
+    const int32_t* slot_ids;
+    const int32_t* num_decoding;
+    float scale_log2;  // softmax scale * log2(e)
+    uint16_t* out;
+    int64_t o_sb, o_sh;
+    float* part_acc;  // [B, Hq, max_splits, 128]
+    float* part_m;    // [B, Hq, max_splits]
+    float* part_l;    // [B, Hq, max_splits]
+    int target, max_splits, hq;
+};
+
+__global__ __launch_bounds__(DA_THREADS) void decode_split_kernel(DecodeArgs a) {
+    const int nd = a.num_decoding[0];
+    const int hk = blockIdx.y;
+    const Work wk = decode_assign(a.cached_lens, nd, blockIdx.x, a.target);
+    if (wk.needed == 0) return;
+
+    const int b = wk.b;
+    const int n_end = a.cached_lens[b] + 1;
+    const int t_begin = wk.split * wk.piece;
+    const int t_end = min(t_begin + wk.piece, n_end);
+    const int slot = a.slot_ids[b];
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int g = lane >> 3, cc = lane & 7;
+
+    // ---- q of the two heads of this KV head, channels [16cc, 16cc + 16) ----
+    half2_t qh[2][8];
+    float qsum[2], kmul[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const uint16_t* qp = a.q + b * a.q_sb + (2 * hk + h) * a.q_sh + 16 * cc;
+        const uint4 u0 = *reinterpret_cast<const uint4*>(qp);
+        const uint4 u1 = *reinterpret_cast<const uint4*>(qp + 8);
+        const uint32_t w[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+        float f[16];
+        float amax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            f[2 * i] = bf16lo(w[i]);
+            f[2 * i + 1] = bf16hi(w[i]);
+            amax = fmaxf(amax, fmaxf(fabsf(f[2 * i]), fabsf(f[2 * i + 1])));
+        }
+        amax = fmaxf(amax, dpp<DPP_XOR1>(amax));
+        amax = fmaxf(amax, dpp<DPP_XOR2>(amax));
+        amax = fmaxf(amax, dpp<DPP_HALF_MIRROR>(amax));
+        int e = 0;
+        frexpf(amax, &e);
+        const float sc = amax > 0.0f ? ldexpf(1.0f, 14 - e) : 1.0f;  // amax*sc in [2^13, 2^14)
+        float s = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const _Float16 lo = (_Float16)(f[2 * i] * sc), hi = (_Float16)(f[2 * i + 1] * sc);
+            qh[h][i] = half2_t{lo, hi};
+            s += (float)lo + (float)hi;
+        }
+        qsum[h] = sum8(s) * OFFSET;
+        kmul[h] = a.scale_log2 / sc;
+    }
+
+    const int8_t* kb = a.c.k + slot * a.c.stride_slot + hk * a.c.stride_head + 16 * cc;
+    const int8_t* vb = a.c.v + slot * a.c.stride_slot + hk * a.c.stride_head + 16 * cc;
+    const float* ksb = a.c.k_scale + slot * a.c.scale_stride_slot + hk * a.c.scale_stride_head;
+    const float* vsb = a.c.v_scale + slot * a.c.scale_stride_slot + hk * a.c.scale_stride_head;
+
+    float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.0f, 0.0f}, ps[2] = {0.0f, 0.0f};
+    float acc[2][16];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) acc[h][j] = 0.0f;
+
+    for (int t0 = t_begin + wave * DA_TOK_WAVE; t0 < t_end; t0 += DA_TOK_WG) {
+        uint4 kr[DA_U], vr[DA_U];
+        float ks[DA_U], vs[DA_U];
+        bool valid[DA_U];
+#pragma unroll
+        for (int u = 0; u < DA_U; ++u) {
+            const int t = t0 + 4 * g + u;
+            valid[u] = t < t_end;
+            const int tl = valid[u] ? t : t_end - 1;  // masked tokens re-read a valid row
+            kr[u] = *reinterpret_cast<const uint4*>(kb + (int64_t)tl * DA_D);
+            vr[u] = *reinterpret_cast<const uint4*>(vb + (int64_t)tl * DA_D);
+            ks[u] = ksb[tl];
+            vs[u] = vsb[tl];
+        }
+        // ---- scores (base 2) ----
+        float s[DA_U][2];
+#pragma unroll
+        for (int u = 0; u < DA_U; ++u) {
+            const uint32_t kw[4] = {kr[u].x, kr[u].y, kr[u].z, kr[u].w};
+            float d0 = 0.0f, d1 = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t x = kw[i] ^ 0x80808080u;
+                const half2_t h01 = as_h2(__builtin_amdgcn_perm(K64, x, 0x04010400u));
+                const half2_t h23 = as_h2(__builtin_amdgcn_perm(K64, x, 0x04030402u));
+                d0 = fdot2(qh[0][2 * i], h01, d0);
+                d0 = fdot2(qh[0][2 * i + 1], h23, d0);
+                d1 = fdot2(qh[1][2 * i], h01, d1);
+                d1 = fdot2(qh[1][2 * i + 1], h23, d1);
+            }
+            d0 = sum8(d0);
+            d1 = sum8(d1);
+            s[u][0] = valid[u] ? (d0 - qsum[0]) * (ks[u] * kmul[0]) : -INFINITY;
+            s[u][1] = valid[u] ? (d1 - qsum[1]) * (ks[u] * kmul[1]) : -INFINITY;
+        }
+        // ---- online softmax per lane group ----
+        float msafe[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const float mt = fmaxf(fmaxf(s[0][h], s[1][h]), fmaxf(s[2][h], s[3][h]));
+            const float mn = fmaxf(m[h], mt);
+            if (mn > m[h]) {
+                const float alpha = exp2_safe(m[h] - mn);  // m = -inf -> 0
+#pragma unroll
+                for (int j = 0; j < 16; ++j) acc[h][j] *= alpha;
+                l[h] *= alpha;
+                ps[h] *= alpha;
+                m[h] = mn;
+            }
+            msafe[h] = m[h] == -INFINITY ? 0.0f : m[h];
+        }
+        _Float16 pv[DA_U][2];
+#pragma unroll
+        for (int u = 0; u < DA_U; ++u)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const float p = exp2_safe(s[u][h] - msafe[h]);
+                l[h] += p;
+                pv[u][h] = (_Float16)(p * vs[u]);
+                ps[h] += (float)pv[u][h];
+            }
+        // ---- PV over token pairs (u, u+1) ----
+#pragma unroll
+        for (int pr = 0; pr < DA_U / 2; ++pr) {
+            const int ua = 2 * pr, ub = ua + 1;
+            const half2_t p0 = half2_t{pv[ua][0], pv[ub][0]};
+            const half2_t p1 = half2_t{pv[ua][1], pv[ub][1]};
+            const uint32_t va[4] = {vr[ua].x, vr[ua].y, vr[ua].z, vr[ua].w};
+            const uint32_t vb4[4] = {vr[ub].x, vr[ub].y, vr[ub].z, vr[ub].w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t xa = va[i] ^ 0x80808080u, xb = vb4[i] ^ 0x80808080u;
+                const uint32_t t01 = __builtin_amdgcn_perm(xb, xa, 0x05010400u);
+                const uint32_t t23 = __builtin_amdgcn_perm(xb, xa, 0x07030602u);
+                const half2_t c0 = as_h2(__builtin_amdgcn_perm(K64, t01, 0x04010400u));
+                const half2_t c1 = as_h2(__builtin_amdgcn_perm(K64, t01, 0x04030402u));
+                const half2_t c2 = as_h2(__builtin_amdgcn_perm(K64, t23, 0x04010400u));
+                const half2_t c3 = as_h2(__builtin_amdgcn_perm(K64, t23, 0x04030402u));
+                acc[0][4 * i + 0] = fdot2(p0, c0, acc[0][4 * i + 0]);
+                acc[0][4 * i + 1] = fdot2(p0, c1, acc[0][4 * i + 1]);
+                acc[0][4 * i + 2] = fdot2(p0, c2, acc[0][4 * i + 2]);
+                acc[0][4 * i + 3] = fdot2(p0, c3, acc[0][4 * i + 3]);
+                acc[1][4 * i + 0] = fdot2(p1, c0, acc[1][4 * i + 0]);
+                acc[1][4 * i + 1] = fdot2(p1, c1, acc[1][4 * i + 1]);
+                acc[1][4 * i + 2] = fdot2(p1, c2, acc[1][4 * i + 2]);
+                acc[1][4 * i + 3] = fdot2(p1, c3, acc[1][4 * i + 3]);
+            }
+        }
+    }
+
+    // ---- merge the 8 lane groups of the wave ----
+    float mw[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        float mx = m[h];
+        mx = fmaxf(mx, dpp<DPP_ROR8>(mx));
+        mx = fmaxf(mx, shfl_xor(mx, 16));
+        mx = fmaxf(mx, shfl_xor(mx, 32));
+        mw[h] = mx;
+        const float f = m[h] == -INFINITY ? 0.0f : exp2_safe(m[h] - mx);
+        float lf = l[h] * f;
+        lf += dpp<DPP_ROR8>(lf);
+        lf += shfl_xor(lf, 16);
+        lf += shfl_xor(lf, 32);
+        l[h] = lf;
+        const float off = ps[h] * OFFSET;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            float x = (acc[h][j] - off) * f;
+            x += dpp<DPP_ROR8>(x);
+            x += shfl_xor(x, 16);
+            x += shfl_xor(x, 32);
+            acc[h][j] = x;
+        }
+    }
+
+    // ---- merge the 4 waves through LDS ----
+    __shared__ float s_acc[DA_WAVES][2][DA_D];
+    __shared__ float s_m[DA_WAVES][2], s_l[DA_WAVES][2];
+    if (g == 0) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) s_acc[wave][h][16 * cc + j] = acc[h][j];
+            if (cc == 0) {
+                s_m[wave][h] = mw[h];
+                s_l[wave][h] = l[h];
+            }
+        }
+    }
+    __syncthreads();
+    const int h = threadIdx.x >> 7, d = threadIdx.x & 127;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < DA_WAVES; ++w) mx = fmaxf(mx, s_m[w][h]);
+    float num = 0.0f, den = 0.0f;
+#pragma unroll
+    for (int w = 0; w < DA_WAVES; ++w) {
+        const float mwv = s_m[w][h];
+        const float f = mwv == -INFINITY ? 0.0f : exp2_safe(mwv - mx);
+        num += s_acc[w][h][d] * f;
+        den += s_l[w][h] * f;
+    }
+    const int qh_idx = 2 * hk + h;
+    if (wk.needed == 1) {
+        a.out[b * a.o_sb + qh_idx * a.o_sh + d] = (uint16_t)f32_to_bf16_rne(num / den);
+    } else {
+        const int64_t row = ((int64_t)b * a.hq + qh_idx) * a.max_splits + wk.split;
+        a.part_acc[row * DA_D + d] = num;
+        if (d == 0) {
+            a.part_m[row] = mx;
+            a.part_l[row] = den;
+        }
+    }
+}
+
+// grid (B, Hq), block 128: merge the pieces of sequences that had more than one
+// (kernels.py:216-264), in base 2.
+__global__ __launch_bounds__(128) void decode_combine_kernel(
+    const float* __restrict__ part_acc, const float* __restrict__ part_m,
+    const float* __restrict__ part_l, const int32_t* __restrict__ cached_lens,
+    const int32_t* __restrict__ num_decoding, uint16_t* __restrict__ out, int64_t o_sb,
+    int64_t o_sh, int hq, int max_splits, int target) {
+    const int nd = num_decoding[0];
+    const int b = blockIdx.x, h = blockIdx.y;
+    if (b >= nd) return;
+    const int piece = decode_piece(cached_lens, nd, target);
+    const int needed = cdiv_i(cached_lens[b] + 1, piece);
+    if (needed <= 1) return;
+    const int d = threadIdx.x;
+    const int64_t row0 = ((int64_t)b * hq + h) * max_splits;
+    float mx = -INFINITY;
+    for (int s = 0; s < needed; ++s) mx = fmaxf(mx, part_m[row0 + s]);
+    float num = 0.0f, den = 0.0f;
+    for (int s = 0; s < needed; ++s) {
+        const float ms = part_m[row0 + s];
+        const float f = ms == -INFINITY ? 0.0f : exp2_safe(ms - mx);
+        num += part_acc[(row0 + s) * DA_D + d] * f;
+        den += part_l[row0 + s] * f;
+    }
+    out[b * o_sb + h * o_sh + d] = (uint16_t)f32_to_bf16_rne(num / den);
+}
+
+struct Layout {
+    int target, max_splits;
+    size_t acc_off, m_off, l_off, bytes;
+};
+
+static Layout workspace_layout(int batch, int hq, int hkv) {
+    Layout L;
+    L.target = decode_target(hkv);
+    L.max_splits = L.target;
+    const size_t rows = (size_t)std::max(batch, 0) * hq * L.max_splits;
+    L.acc_off = 0;
+    L.m_off = rows * DA_D * sizeof(float);
+    L.l_off = L.m_off + rows * sizeof(float);
+    L.bytes = L.l_off + rows * sizeof(float);
+    return L;
+}
+
+}  // namespace ie
+
+using namespace ie;
+
+extern "C" int32_t ie_decode_attention_max_splits(int32_t num_kv_heads) {
+    return decode_target(num_kv_heads);
+}
+
+extern "C" size_t ie_decode_attention_workspace_size(int32_t batch, int32_t num_q_heads,
+                                                     int32_t head_dim) {
+    (void)head_dim;
+    // Hkv = Hq / 2 is the only geometry the kernels take.
+    return workspace_layout(batch, num_q_heads, std::max(1, num_q_heads / 2)).bytes;
+}
+
+static hipError_t check_decode(const ie_bf16* q, int32_t batch, int32_t num_q_heads,
+                               const ie_kv_cache* cache, const int32_t* cached_lens,
+                               const int32_t* slot_ids, const int32_t* num_decoding,
+                               const ie_bf16* out, int64_t q_sb, int64_t q_sh, void* workspace,
+                               size_t workspace_bytes, Layout* L) {
+    hipError_t e = check_cache(cache);
+    if (e != hipSuccess) return e;
+    IE_REQUIRE(batch >= 0, "negative batch");
+    IE_REQUIRE(num_q_heads == 2 * cache->num_kv_heads, "num_q_heads must be 2 * num_kv_heads");
+    if (batch == 0) return hipSuccess;
+    IE_REQUIRE(q && cached_lens && slot_ids && num_decoding && out, "null pointer");
+    IE_REQUIRE((reinterpret_cast<uintptr_t>(q) & 15) == 0 && q_sb % 8 == 0 && q_sh % 8 == 0,
+               "q rows must be 16-byte aligned with contiguous head_dim");
+    *L = workspace_layout(batch, num_q_heads, (int)cache->num_kv_heads);
+    IE_REQUIRE(workspace != nullptr && workspace_bytes >= L->bytes, "workspace too small");
+    IE_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 15) == 0, "workspace must be aligned");
+    return hipSuccess;
+}
+
+extern "C" hipError_t ie_decode_attention_split(
+    const ie_bf16* q, int64_t q_stride_b, int64_t q_stride_h, int32_t batch, int32_t num_q_heads,
+    const ie_kv_cache* cache, const int32_t* cached_lens, const int32_t* slot_ids,
+    const int32_t* num_decoding, float scale, ie_bf16* out, int64_t out_stride_b,
+    int64_t out_stride_h, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    Layout L{};
+    hipError_t e = check_decode(q, batch, num_q_heads, cache, cached_lens, slot_ids, num_decoding,
+                                out, q_stride_b, q_stride_h, workspace, workspace_bytes, &L);
+    if (e != hipSuccess || batch == 0) return e;
+    DecodeArgs a;
+    a.q = (const uint16_t*)q;
+    a.q_sb = q_stride_b;
+    a.q_sh = q_stride_h;
+    a.c = *cache;
+    a.cached_lens = cached_lens;
+    a.slot_ids = slot_ids;
+    a.num_decoding = num_decoding;
+    a.scale_log2 = scale * 1.4426950408889634f;
+    a.out = (uint16_t*)out;
+    a.o_sb = out_stride_b;
+    a.o_sh = out_stride_h;
+    char* ws = (char*)workspace;
+    a.part_acc = (float*)(ws + L.acc_off);
+    a.part_m = (float*)(ws + L.m_off);
+    a.part_l = (float*)(ws + L.l_off);
+    a.target = L.target;
+    a.max_splits = L.max_splits;
+    a.hq = num_q_heads;
+    dim3 grid(L.target + batch, (unsigned)cache->num_kv_heads);
+    hipLaunchKernelGGL(decode_split_kernel, grid, dim3(DA_THREADS), 0, stream, a);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t ie_decode_attention_combine(int32_t batch, int32_t num_q_heads,
+                                                  int32_t head_dim, int32_t num_kv_heads,
+                                                  const int32_t* cached_lens,
+                                                  const int32_t* num_decoding, ie_bf16* out,
+                                                  int64_t out_stride_b, int64_t out_stride_h,
+                                                  void* workspace, size_t workspace_bytes,
+                                                  hipStream_t stream) {
+    IE_REQUIRE(batch >= 0, "negative batch");
+    if (batch == 0) return hipSuccess;
+    IE_REQUIRE(head_dim == DA_D && num_q_heads == 2 * num_kv_heads, "unsupported geometry");
+    IE_REQUIRE(cached_lens && num_decoding && out && workspace, "null pointer");
+    const Layout L = workspace_layout(batch, num_q_heads, num_kv_heads);
+    IE_REQUIRE(workspace_bytes >= L.bytes, "workspace too small");
+    char* ws = (char*)workspace;
+    dim3 grid(batch, num_q_heads);
+    hipLaunchKernelGGL(decode_combine_kernel, grid, dim3(DA_D), 0, stream,
+                       (const float*)(ws + L.acc_off), (const float*)(ws + L.m_off),
+                       (const float*)(ws + L.l_off), cached_lens, num_decoding, (uint16_t*)out,
+                       out_stride_b, out_stride_h, num_q_heads, L.max_splits, L.target);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t ie_decode_attention(const ie_bf16* q, int64_t q_stride_b,
+                                          int64_t q_stride_h, int32_t batch, int32_t num_q_heads,
+                                          const ie_kv_cache* cache, const int32_t* cached_lens,
+                                          const int32_t* slot_ids, const int32_t* num_decoding,
+                                          float scale, ie_bf16* out, int64_t out_stride_b,
+                                          int64_t out_stride_h, void* workspace,
+                                          size_t workspace_bytes, hipStream_t stream) {
+    hipError_t e = ie_decode_attention_split(q, q_stride_b, q_stride_h, batch, num_q_heads, cache,
+                                             cached_lens, slot_ids, num_decoding, scale, out,
+                                             out_stride_b, out_stride_h, workspace,
+                                             workspace_bytes, stream);
+    if (e != hipSuccess || batch == 0) return e;
+    return ie_decode_attention_combine(batch, num_q_heads, (int)cache->head_dim,
+                                       (int)cache->num_kv_heads, cached_lens, num_decoding, out,
+                                       out_stride_b, out_stride_h, workspace, workspace_bytes,
+                                       stream);
+}

@@ -1,0 +1,107 @@
+// Device helpers shared by the gfx950 attention kernels: bf16 conversion, DPP lane exchange,
+// wave reductions with a fixed order, and host-side argument checking for the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/ie_attn.h"
+
+#define IE_WAVE 64
+
+namespace ie {
+
+// ---------------------------------------------------------------------------------------------
+// bf16 <-> fp32
+// ---------------------------------------------------------------------------------------------
+__device__ __forceinline__ float bf16_to_f32(uint32_t bits16) {
+    return __uint_as_float(bits16 << 16);
+}
+__device__ __forceinline__ float bf16lo(uint32_t packed) { return __uint_as_float(packed << 16); }
+__device__ __forceinline__ float bf16hi(uint32_t packed) {
+    return __uint_as_float(packed & 0xffff0000u);
+}
+
+// Round-to-nearest-even fp32 -> bf16 bits (NaN stays NaN).
+__device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    return f32_to_bf16_rne(lo) | (f32_to_bf16_rne(hi) << 16);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Lane exchange. DPP controls (GFX9): quad_perm = sel0 | sel1<<2 | sel2<<4 | sel3<<6,
+// row_mirror = 0x140, row_half_mirror = 0x141, row_ror:n = 0x120 + n.
+// ---------------------------------------------------------------------------------------------
+enum : int {
+    DPP_XOR1 = 0xB1,        // quad_perm [1,0,3,2]
+    DPP_XOR2 = 0x4E,        // quad_perm [2,3,0,1]
+    DPP_HALF_MIRROR = 0x141,  // lane i <- lane 7-i within each 8 lanes
+    DPP_MIRROR = 0x140,       // lane i <- lane 15-i within each 16 lanes
+    DPP_ROR8 = 0x128,         // lane i <- lane (i+8)%16 within each 16 lanes
+};
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int dppi(int x) {
+    return __builtin_amdgcn_update_dpp(0, x, CTRL, 0xf, 0xf, false);
+}
+
+__device__ __forceinline__ float shfl_xor(float x, int m) {
+    return __shfl_xor(x, m, IE_WAVE);
+}
+
+// Sum over each group of 8 consecutive lanes; every lane of the group gets the sum.
+__device__ __forceinline__ float sum8(float x) {
+    x += dpp<DPP_XOR1>(x);
+    x += dpp<DPP_XOR2>(x);
+    x += dpp<DPP_HALF_MIRROR>(x);
+    return x;
+}
+// Max over each group of 16 consecutive lanes; every lane of the group gets the max.
+__device__ __forceinline__ float max16(float x) {
+    x = fmaxf(x, dpp<DPP_XOR1>(x));
+    x = fmaxf(x, dpp<DPP_XOR2>(x));
+    x = fmaxf(x, dpp<DPP_HALF_MIRROR>(x));
+    x = fmaxf(x, dpp<DPP_MIRROR>(x));
+    return x;
+}
+// Max over the 64 lanes of the wave.
+__device__ __forceinline__ float wave_max(float x) {
+    x = max16(x);
+    x = fmaxf(x, shfl_xor(x, 16));
+    x = fmaxf(x, shfl_xor(x, 32));
+    return x;
+}
+// Sum over the 64 lanes in the fixed butterfly order: lane i adds lane i^32, i^16, ..., i^1.
+// fp32 addition is commutative, so after each step lanes i and i^m hold the same bits and the
+// result is identical in every lane.
+__device__ __forceinline__ float wave_sum_butterfly(float x) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) x = x + shfl_xor(x, m);
+    return x;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Host-side checks.
+// ---------------------------------------------------------------------------------------------
+void set_error(const char* msg);
+hipError_t check_cache(const ie_kv_cache* c);
+int device_cu_count();
+
+}  // namespace ie
+
+#define IE_REQUIRE(cond, msg)                      \
+    do {                                           \
+        if (!(cond)) {                             \
+            ::ie::set_error(msg);                  \
+            return hipErrorInvalidValue;           \
+        }                                          \
+    } while (0)

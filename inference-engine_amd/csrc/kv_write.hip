@@ -1,0 +1,343 @@
+// int8 KV cache writes and reads for gfx950.
+//
+//   quantize_kv_prefill_kernel   prefill quantize-on-write (+ K calibration on a first chunk)
+//   fused_rope_kv_decode_kernel  decode q/k RMSNorm + RoPE, q * calibration, K/V quantize
+//   dequantize_kv_prefix_kernel  int8 prefix -> bf16
+//
+// Bit-level contract: every value written is produced by IEEE round-to-nearest-even fp32
+// operations in the order stated at each step (no contraction into fused multiply-add), so it
+// is reproducible on the host. Each row of 128 channels is handled by 16 lanes x 8 channels
+// (prefill) or by one wave, 2 channels per lane (decode).
+#include "ie_common.h"
+
+namespace ie {
+
+constexpr int HEAD_DIM = 128;
+constexpr int QP_THREADS = 256;
+constexpr int QP_ROWS = QP_THREADS / 16;   // token rows per pass of a workgroup
+constexpr int QP_MIN_TOKENS = 128;         // fewest tokens a prefill-write workgroup takes
+constexpr int QP_MAX_SPLITS = 8;           // workgroups per (entry, kv head) at most
+
+struct Row8 {
+    float x[8];
+};
+
+// 8 consecutive bf16 (16 bytes) -> fp32.
+__device__ __forceinline__ Row8 load_bf16x8(const uint16_t* p) {
+    const uint4 u = *reinterpret_cast<const uint4*>(p);
+    Row8 r;
+    r.x[0] = bf16lo(u.x); r.x[1] = bf16hi(u.x);
+    r.x[2] = bf16lo(u.y); r.x[3] = bf16hi(u.y);
+    r.x[4] = bf16lo(u.z); r.x[5] = bf16hi(u.z);
+    r.x[6] = bf16lo(u.w); r.x[7] = bf16hi(u.w);
+    return r;
+}
+
+__device__ __forceinline__ int32_t quant1(float x, float s) {
+    // clamp(rint(x / s), -127, 127); x / s is an IEEE division, rint rounds half to even.
+    float r = rintf(x / s);
+    r = fminf(fmaxf(r, -127.0f), 127.0f);
+    return static_cast<int32_t>(r);
+}
+
+__device__ __forceinline__ uint2 pack_i8x8(const int32_t* q) {
+    uint2 o;
+    o.x = (q[0] & 0xff) | ((q[1] & 0xff) << 8) | ((q[2] & 0xff) << 16) | ((uint32_t)q[3] << 24);
+    o.y = (q[4] & 0xff) | ((q[5] & 0xff) << 8) | ((q[6] & 0xff) << 16) | ((uint32_t)q[7] << 24);
+    return o;
+}
+
+// Quantize 8 channels held by this lane of a 16-lane row group; returns the row scale.
+__device__ __forceinline__ float quantize_row8(const float* x, int32_t* q) {
+    float a = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) a = fmaxf(a, fabsf(x[j]));
+    a = max16(a);
+    const float s = fmaxf(a, 1e-6f) / 127.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) q[j] = quant1(x[j], s);
+    return s;
+}
+
+// grid (num_entries, Hkv, splits), block 256. Workgroup (b, h, z) quantizes its share of entry
+// b's chunk for kv head h (kernels.py:786-823). When cached_len == 0 every workgroup of (b, h)
+// computes the chunk's calibration (kernels.py:764-780) itself and split 0 stores it.
+__global__ __launch_bounds__(QP_THREADS) void quantize_kv_prefill_kernel(
+    const uint16_t* __restrict__ k, int64_t k_st, int64_t k_sh,
+    const uint16_t* __restrict__ v, int64_t v_st, int64_t v_sh,
+    const int32_t* __restrict__ cu_seqlens, const int32_t* __restrict__ slot_ids,
+    const int32_t* __restrict__ cached_lens, const int32_t* __restrict__ num_decoding,
+    ie_kv_cache c) {
+#pragma clang fp contract(off)
+    const int b = blockIdx.x, h = blockIdx.y, z = blockIdx.z;
+    if (b < num_decoding[0]) return;
+    const int start = cu_seqlens[b];
+    const int len = cu_seqlens[b + 1] - start;
+    if (len <= 0) return;
+    const int nsplit = min((int)gridDim.z, (len + QP_MIN_TOKENS - 1) / QP_MIN_TOKENS);
+    if (z >= nsplit) return;
+    const int per = (len + nsplit - 1) / nsplit;
+    const int t0 = z * per;
+    const int t1 = min(len, t0 + per);
+    if (t0 >= t1) return;
+
+    const int slot = slot_ids[b];
+    const int c0 = cached_lens[b];
+    const int tid = threadIdx.x;
+    const int c16 = tid & 15;  // channels [8*c16, 8*c16+8)
+    const int r = tid >> 4;    // row within a pass
+
+    __shared__ float s_red[QP_ROWS][HEAD_DIM];
+    __shared__ float s_cal[HEAD_DIM];
+
+    float* calp = c.k_calibration + slot * c.cal_stride_slot + h * c.cal_stride_head;
+    const uint16_t* kh = k + (int64_t)start * k_st + h * k_sh + 8 * c16;
+    const uint16_t* vh = v + (int64_t)start * v_st + h * v_sh + 8 * c16;
+
+    if (c0 == 0) {
+        float mx[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) mx[j] = 0.0f;
+        for (int t = r; t < len; t += QP_ROWS) {
+            const Row8 x = load_bf16x8(kh + (int64_t)t * k_st);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) mx[j] = fmaxf(mx[j], fabsf(x.x[j]));
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) s_red[r][8 * c16 + j] = mx[j];
+        __syncthreads();
+        if (tid < HEAD_DIM) {
+            float m = 1e-3f;
+#pragma unroll
+            for (int rr = 0; rr < QP_ROWS; ++rr) m = fmaxf(m, s_red[rr][tid]);
+            s_cal[tid] = m;
+            if (z == 0) calp[tid] = m;
+        }
+    } else {
+        if (tid < HEAD_DIM) s_cal[tid] = calp[tid];
+    }
+    __syncthreads();
+    float cal[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) cal[j] = s_cal[8 * c16 + j];
+
+    int8_t* kc = c.k + slot * c.stride_slot + h * c.stride_head + 8 * c16;
+    int8_t* vc = c.v + slot * c.stride_slot + h * c.stride_head + 8 * c16;
+    float* ks = c.k_scale + slot * c.scale_stride_slot + h * c.scale_stride_head;
+    float* vs = c.v_scale + slot * c.scale_stride_slot + h * c.scale_stride_head;
+
+    for (int t = t0 + r; t < t1; t += QP_ROWS) {
+        const int64_t col = (int64_t)(c0 + t);
+        int32_t q[8];
+        Row8 x = load_bf16x8(kh + (int64_t)t * k_st);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x.x[j] = x.x[j] / cal[j];
+        float s = quantize_row8(x.x, q);
+        *reinterpret_cast<uint2*>(kc + col * c.stride_tok) = pack_i8x8(q);
+        if (c16 == 0) ks[col] = s;
+
+        Row8 y = load_bf16x8(vh + (int64_t)t * v_st);
+        s = quantize_row8(y.x, q);
+        *reinterpret_cast<uint2*>(vc + col * c.stride_tok) = pack_i8x8(q);
+        if (c16 == 0) vs[col] = s;
+    }
+}
+
+// grid (B, ceil((Hq + Hkv) / 4)), block 256: wave w of workgroup y handles head row
+// r = 4y + w; r < Hq is query head r, else kv head r - Hq (its K and V). Lane i holds channels
+// i and i + 64 (the two halves RoPE pairs, kernels.py:410-436).
+__global__ __launch_bounds__(256) void fused_rope_kv_decode_kernel(
+    const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_sh,
+    const uint16_t* __restrict__ k, int64_t k_sb, int64_t k_sh,
+    const uint16_t* __restrict__ v, int64_t v_sb, int64_t v_sh,
+    const uint16_t* __restrict__ qw, const uint16_t* __restrict__ kw,
+    const uint16_t* __restrict__ cosp, int64_t cos_sb,
+    const uint16_t* __restrict__ sinp, int64_t sin_sb,
+    const int32_t* __restrict__ slot_ids, const int32_t* __restrict__ cached_lens,
+    const int32_t* __restrict__ num_decoding, int hq, int ratio, float eps, ie_kv_cache c,
+    uint16_t* __restrict__ out, int64_t o_sb, int64_t o_sh) {
+#pragma clang fp contract(off)
+    const int b = blockIdx.x;
+    if (b >= num_decoding[0]) return;
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.y * 4 + (threadIdx.x >> 6);
+    const int hkv = (int)c.num_kv_heads;
+    if (row >= hq + hkv) return;
+    const bool is_q = row < hq;
+    const int j = is_q ? row / ratio : row - hq;  // kv head whose calibration applies
+
+    const uint16_t* src = is_q ? q + b * q_sb + row * q_sh : k + b * k_sb + j * k_sh;
+    const uint16_t* w = is_q ? qw : kw;
+    float x1 = bf16_to_f32(src[lane]);
+    float x2 = bf16_to_f32(src[lane + 64]);
+
+    // RMSNorm (kernels.py:417-419 / :426-428) in the fixed butterfly order.
+    const float ss = wave_sum_butterfly(x1 * x1) + wave_sum_butterfly(x2 * x2);
+    const float var = ss / 128.0f + eps;
+    const float rstd = 1.0f / sqrtf(var);
+    x1 = (x1 * rstd) * bf16_to_f32(w[lane]);
+    x2 = (x2 * rstd) * bf16_to_f32(w[lane + 64]);
+
+    // RoPE with bf16 cos/sin (kernels.py:430-436).
+    const float cs = bf16_to_f32(cosp[b * cos_sb + lane]);
+    const float sn = bf16_to_f32(sinp[b * sin_sb + lane]);
+    const float o1 = (x1 * cs) - (x2 * sn);
+    const float o2 = (x1 * sn) + (x2 * cs);
+
+    const int slot = slot_ids[b];
+    const float* cal = c.k_calibration + slot * c.cal_stride_slot + j * c.cal_stride_head;
+    const float c1 = cal[lane], c2 = cal[lane + 64];
+    if (is_q) {
+        // q folded with the channel calibration, stored bf16 (kernels.py:440-447).
+        uint16_t* o = out + b * o_sb + row * o_sh;
+        o[lane] = (uint16_t)f32_to_bf16_rne(o1 * c1);
+        o[lane + 64] = (uint16_t)f32_to_bf16_rne(o2 * c2);
+        return;
+    }
+    // K: rope(norm(k)) / cal -> int8 at column cached_len (kernels.py:449-470).
+    const int64_t col = cached_lens[b];
+    const int64_t base = slot * c.stride_slot + j * c.stride_head + col * c.stride_tok;
+    const int64_t sidx = slot * c.scale_stride_slot + j * c.scale_stride_head + col;
+    {
+        const float k1 = o1 / c1, k2 = o2 / c2;
+        const float a = wave_max(fmaxf(fabsf(k1), fabsf(k2)));
+        const float s = fmaxf(a, 1e-6f) / 127.0f;
+        c.k[base + lane] = (int8_t)quant1(k1, s);
+        c.k[base + lane + 64] = (int8_t)quant1(k2, s);
+        if (lane == 0) c.k_scale[sidx] = s;
+    }
+    // V: int8 with its own scale (kernels.py:472-480).
+    {
+        const uint16_t* vp = v + b * v_sb + j * v_sh;
+        const float v1 = bf16_to_f32(vp[lane]), v2 = bf16_to_f32(vp[lane + 64]);
+        const float a = wave_max(fmaxf(fabsf(v1), fabsf(v2)));
+        const float s = fmaxf(a, 1e-6f) / 127.0f;
+        c.v[base + lane] = (int8_t)quant1(v1, s);
+        c.v[base + lane + 64] = (int8_t)quant1(v2, s);
+        if (lane == 0) c.v_scale[sidx] = s;
+    }
+}
+
+constexpr int DQ_TOKENS = 64;
+
+// grid (num_entries, Hkv, ceil(max_len / 64)), block 256 (kernels.py:868-932): 16 lanes x 8
+// channels per token, 16 tokens per pass.
+__global__ __launch_bounds__(256) void dequantize_kv_prefix_kernel(
+    ie_kv_cache c, const int32_t* __restrict__ cu_cached, const int32_t* __restrict__ slot_ids,
+    uint16_t* __restrict__ k_out, uint16_t* __restrict__ v_out, int64_t o_sh, int64_t o_st) {
+#pragma clang fp contract(off)
+    const int b = blockIdx.x, h = blockIdx.y;
+    const int out_start = cu_cached[b];
+    const int n = cu_cached[b + 1] - out_start;
+    const int tbase = blockIdx.z * DQ_TOKENS;
+    if (tbase >= n) return;
+    const int slot = slot_ids[b];
+    const int c16 = threadIdx.x & 15, r = threadIdx.x >> 4;
+    const float* calp = c.k_calibration + slot * c.cal_stride_slot + h * c.cal_stride_head;
+    float cal[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) cal[j] = calp[8 * c16 + j];
+    const int8_t* kc = c.k + slot * c.stride_slot + h * c.stride_head + 8 * c16;
+    const int8_t* vc = c.v + slot * c.stride_slot + h * c.stride_head + 8 * c16;
+    const float* ks = c.k_scale + slot * c.scale_stride_slot + h * c.scale_stride_head;
+    const float* vs = c.v_scale + slot * c.scale_stride_slot + h * c.scale_stride_head;
+    for (int t = tbase + r; t < min(n, tbase + DQ_TOKENS); t += 16) {
+        const uint2 kq = *reinterpret_cast<const uint2*>(kc + (int64_t)t * c.stride_tok);
+        const uint2 vq = *reinterpret_cast<const uint2*>(vc + (int64_t)t * c.stride_tok);
+        const float sk = ks[t], sv = vs[t];
+        uint32_t ko[4], vo[4];
+#pragma unroll
+        for (int j = 0; j < 8; j += 2) {
+            const uint32_t kw = j < 4 ? kq.x : kq.y, vw = j < 4 ? vq.x : vq.y;
+            const int sh = (j & 3) * 8;
+            const float k0 = (float)(int8_t)(kw >> sh), k1 = (float)(int8_t)(kw >> (sh + 8));
+            const float v0 = (float)(int8_t)(vw >> sh), v1 = (float)(int8_t)(vw >> (sh + 8));
+            ko[j / 2] = pack_bf16x2((k0 * sk) * cal[j], (k1 * sk) * cal[j + 1]);
+            vo[j / 2] = pack_bf16x2(v0 * sv, v1 * sv);
+        }
+        const int64_t o = h * o_sh + (int64_t)(out_start + t) * o_st + 8 * c16;
+        *reinterpret_cast<uint4*>(k_out + o) = make_uint4(ko[0], ko[1], ko[2], ko[3]);
+        *reinterpret_cast<uint4*>(v_out + o) = make_uint4(vo[0], vo[1], vo[2], vo[3]);
+    }
+}
+
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+}  // namespace ie
+
+using namespace ie;
+
+extern "C" hipError_t ie_quantize_kv_prefill(
+    const ie_bf16* k, int64_t k_stride_tok, int64_t k_stride_head, const ie_bf16* v,
+    int64_t v_stride_tok, int64_t v_stride_head, int64_t num_tokens, const int32_t* cu_seqlens,
+    const int32_t* slot_ids, const int32_t* cached_lens, const int32_t* num_decoding,
+    int32_t num_entries, const ie_kv_cache* cache, hipStream_t stream) {
+    hipError_t e = check_cache(cache);
+    if (e != hipSuccess) return e;
+    IE_REQUIRE(num_entries >= 0 && num_tokens >= 0, "negative sizes");
+    if (num_entries == 0) return hipSuccess;
+    IE_REQUIRE(k && v && cu_seqlens && slot_ids && cached_lens && num_decoding, "null pointer");
+    IE_REQUIRE(aligned16(k) && aligned16(v) && k_stride_tok % 8 == 0 && k_stride_head % 8 == 0 &&
+                   v_stride_tok % 8 == 0 && v_stride_head % 8 == 0,
+               "k/v rows must be 16-byte aligned with contiguous head_dim");
+    const int splits =
+        (int)std::max<int64_t>(1, std::min<int64_t>(QP_MAX_SPLITS, (num_tokens + QP_MIN_TOKENS - 1) /
+                                                                       QP_MIN_TOKENS));
+    dim3 grid(num_entries, (unsigned)cache->num_kv_heads, splits);
+    hipLaunchKernelGGL(quantize_kv_prefill_kernel, grid, dim3(QP_THREADS), 0, stream,
+                       (const uint16_t*)k, k_stride_tok, k_stride_head, (const uint16_t*)v,
+                       v_stride_tok, v_stride_head, cu_seqlens, slot_ids, cached_lens,
+                       num_decoding, *cache);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t ie_fused_rope_kv_decode(
+    const ie_bf16* q, int64_t q_stride_b, int64_t q_stride_h, const ie_bf16* k,
+    int64_t k_stride_b, int64_t k_stride_h, const ie_bf16* v, int64_t v_stride_b,
+    int64_t v_stride_h, const ie_bf16* q_norm_weight, const ie_bf16* k_norm_weight,
+    const ie_bf16* cos, int64_t cos_stride_b, const ie_bf16* sin, int64_t sin_stride_b,
+    const int32_t* slot_ids, const int32_t* cached_lens, const int32_t* num_decoding,
+    int32_t batch, int32_t num_q_heads, float eps, const ie_kv_cache* cache, ie_bf16* q_out,
+    int64_t q_out_stride_b, int64_t q_out_stride_h, hipStream_t stream) {
+    hipError_t e = check_cache(cache);
+    if (e != hipSuccess) return e;
+    IE_REQUIRE(batch >= 0, "negative batch");
+    if (batch == 0) return hipSuccess;
+    IE_REQUIRE(q && k && v && q_norm_weight && k_norm_weight && cos && sin && slot_ids &&
+                   cached_lens && num_decoding && q_out,
+               "null pointer");
+    IE_REQUIRE(num_q_heads > 0 && num_q_heads % cache->num_kv_heads == 0,
+               "num_q_heads must be a multiple of num_kv_heads");
+    const int rows = num_q_heads + (int)cache->num_kv_heads;
+    dim3 grid(batch, (rows + 3) / 4);
+    hipLaunchKernelGGL(fused_rope_kv_decode_kernel, grid, dim3(256), 0, stream,
+                       (const uint16_t*)q, q_stride_b, q_stride_h, (const uint16_t*)k,
+                       k_stride_b, k_stride_h, (const uint16_t*)v, v_stride_b, v_stride_h,
+                       (const uint16_t*)q_norm_weight, (const uint16_t*)k_norm_weight,
+                       (const uint16_t*)cos, cos_stride_b, (const uint16_t*)sin, sin_stride_b,
+                       slot_ids, cached_lens, num_decoding, num_q_heads,
+                       num_q_heads / (int)cache->num_kv_heads, eps, *cache, (uint16_t*)q_out,
+                       q_out_stride_b, q_out_stride_h);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t ie_dequantize_kv_prefix(const ie_kv_cache* cache, const int32_t* cu_cached,
+                                              const int32_t* slot_ids, int32_t num_entries,
+                                              ie_bf16* k_out, ie_bf16* v_out,
+                                              int64_t out_stride_head, int64_t out_stride_tok,
+                                              hipStream_t stream) {
+    hipError_t e = check_cache(cache);
+    if (e != hipSuccess) return e;
+    IE_REQUIRE(num_entries >= 0, "negative sizes");
+    if (num_entries == 0) return hipSuccess;
+    IE_REQUIRE(cu_cached && slot_ids && k_out && v_out, "null pointer");
+    IE_REQUIRE(aligned16(k_out) && aligned16(v_out) && out_stride_head % 8 == 0 &&
+                   out_stride_tok % 8 == 0,
+               "prefix rows must be 16-byte aligned with contiguous head_dim");
+    dim3 grid(num_entries, (unsigned)cache->num_kv_heads,
+              (unsigned)((cache->max_len + DQ_TOKENS - 1) / DQ_TOKENS));
+    hipLaunchKernelGGL(dequantize_kv_prefix_kernel, grid, dim3(256), 0, stream, *cache, cu_cached,
+                       slot_ids, (uint16_t*)k_out, (uint16_t*)v_out, out_stride_head,
+                       out_stride_tok);
+    return hipGetLastError();
+}

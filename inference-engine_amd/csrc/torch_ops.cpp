@@ -1,0 +1,319 @@
+// torch.ops.ie.* registration: validates tensors, turns them into the plain pointers, strides and
+// sizes of the C ABI (include/ie_attn.h), and enqueues on the current HIP stream. No kernel
+// code lives here and nothing is computed on the host; workspaces come from the PyTorch
+// caching allocator (the graph pool while a hipGraph is being captured).
+#include <ATen/ATen.h>
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+#include <torch/library.h>
+
+#include "../../include/ie_attn.h"
+
+namespace {
+
+void ok(hipError_t e, const char* what) {
+    TORCH_CHECK(e == hipSuccess, "ie.", what, ": ", hipGetErrorString(e), " (",
+                ie_attn_last_error(), ")");
+}
+
+hipStream_t stream_of(const at::Tensor& t) {
+    return c10::hip::getCurrentHIPStream(t.device().index()).stream();
+}
+
+void check_dev(const at::Tensor& t, const char* name) {
+    TORCH_CHECK(t.is_cuda(), "ie: ", name, " must be a GPU tensor");
+}
+
+void check_i32(const at::Tensor& t, const char* name) {
+    check_dev(t, name);
+    TORCH_CHECK(t.scalar_type() == at::kInt, "ie: ", name, " must be int32");
+    TORCH_CHECK(t.dim() == 1 && t.stride(0) == 1, "ie: ", name, " must be a contiguous vector");
+}
+
+void check_bf16_rows(const at::Tensor& t, const char* name, int64_t dim) {
+    check_dev(t, name);
+    TORCH_CHECK(t.scalar_type() == at::kBFloat16, "ie: ", name, " must be bfloat16");
+    TORCH_CHECK(t.dim() == dim, "ie: ", name, " must have ", dim, " dims");
+    TORCH_CHECK(t.stride(-1) == 1, "ie: ", name, " needs a contiguous last dim");
+}
+
+const ie_bf16* bf(const at::Tensor& t) {
+    return reinterpret_cast<const ie_bf16*>(t.data_ptr());
+}
+ie_bf16* bfm(const at::Tensor& t) { return reinterpret_cast<ie_bf16*>(t.data_ptr()); }
+const int32_t* i32(const at::Tensor& t) { return t.data_ptr<int32_t>(); }
+
+// LayerKVCache (qwen3-1.7b/kernels.py:11-17) -> descriptor; same stride asserts as
+// kernels.py:284-287.
+ie_kv_cache cache_desc(const at::Tensor& k, const at::Tensor& v, const at::Tensor& ks,
+                       const at::Tensor& vs, const at::Tensor& cal) {
+    check_dev(k, "k_cache");
+    TORCH_CHECK(k.scalar_type() == at::kChar && v.scalar_type() == at::kChar,
+                "ie: k/v cache must be int8");
+    TORCH_CHECK(ks.scalar_type() == at::kFloat && vs.scalar_type() == at::kFloat &&
+                    cal.scalar_type() == at::kFloat,
+                "ie: scales and calibration must be float32");
+    TORCH_CHECK(k.dim() == 4 && v.sizes() == k.sizes(), "ie: k/v cache must be [pool,Hkv,L,D]");
+    TORCH_CHECK(k.strides() == v.strides(), "kernel uses one set of strides for k and v");
+    TORCH_CHECK(ks.dim() == 3 && vs.sizes() == ks.sizes() && ks.strides() == vs.strides(),
+                "ie: k_scale/v_scale must be [pool,Hkv,L] with equal strides");
+    TORCH_CHECK(ks.size(0) == k.size(0) && ks.size(1) == k.size(1) && ks.size(2) == k.size(2) &&
+                    ks.stride(2) == 1,
+                "ie: scale shape/stride mismatch");
+    TORCH_CHECK(cal.dim() == 4 && cal.size(0) == k.size(0) && cal.size(1) == k.size(1) &&
+                    cal.size(3) == k.size(3) && cal.stride(3) == 1,
+                "ie: k_calibration must be [pool,Hkv,1,D]");
+    ie_kv_cache c;
+    c.k = k.data_ptr<int8_t>();
+    c.v = v.data_ptr<int8_t>();
+    c.k_scale = ks.data_ptr<float>();
+    c.v_scale = vs.data_ptr<float>();
+    c.k_calibration = cal.data_ptr<float>();
+    c.pool = k.size(0);
+    c.num_kv_heads = k.size(1);
+    c.max_len = k.size(2);
+    c.head_dim = k.size(3);
+    c.stride_slot = k.stride(0);
+    c.stride_head = k.stride(1);
+    c.stride_tok = k.stride(2);
+    c.scale_stride_slot = ks.stride(0);
+    c.scale_stride_head = ks.stride(1);
+    c.cal_stride_slot = cal.stride(0);
+    c.cal_stride_head = cal.stride(1);
+    TORCH_CHECK(k.stride(3) == 1, "ie: cache head_dim must be contiguous");
+    return c;
+}
+
+void quantize_kv_prefill(const at::Tensor& k, const at::Tensor& v, const at::Tensor& cu_seqlens,
+                         const at::Tensor& slot_ids, const at::Tensor& cached_lens,
+                         const at::Tensor& num_decoding, const at::Tensor& k_cache,
+                         const at::Tensor& v_cache, const at::Tensor& k_scale,
+                         const at::Tensor& v_scale, const at::Tensor& k_calibration) {
+    check_bf16_rows(k, "k", 3);
+    check_bf16_rows(v, "v", 3);
+    for (auto* t : {&cu_seqlens, &slot_ids, &cached_lens, &num_decoding}) check_i32(*t, "index");
+    const c10::DeviceGuard guard(k.device());
+    ie_kv_cache c = cache_desc(k_cache, v_cache, k_scale, v_scale, k_calibration);
+    TORCH_CHECK(k.size(1) == c.num_kv_heads && k.size(2) == c.head_dim && v.sizes() == k.sizes(),
+                "ie: k/v shape mismatch");
+    const int32_t entries = (int32_t)cu_seqlens.size(0) - 1;
+    TORCH_CHECK(slot_ids.size(0) >= entries && cached_lens.size(0) >= entries,
+                "ie: slot_ids/cached_lens shorter than the entry count");
+    ok(ie_quantize_kv_prefill(bf(k), k.stride(0), k.stride(1), bf(v), v.stride(0), v.stride(1),
+                              k.size(0), i32(cu_seqlens), i32(slot_ids), i32(cached_lens),
+                              i32(num_decoding), entries, &c, stream_of(k)),
+       "quantize_kv_prefill");
+}
+
+at::Tensor fused_rope_kv_decode(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
+                                const at::Tensor& q_norm_weight,
+                                const at::Tensor& k_norm_weight, const at::Tensor& cos,
+                                const at::Tensor& sin, const at::Tensor& slot_ids,
+                                const at::Tensor& k_cache, const at::Tensor& v_cache,
+                                const at::Tensor& k_scale, const at::Tensor& v_scale,
+                                const at::Tensor& k_calibration, const at::Tensor& cached_lens,
+                                const at::Tensor& num_decoding, double eps) {
+    check_bf16_rows(q, "q", 3);
+    check_bf16_rows(k, "k", 3);
+    check_bf16_rows(v, "v", 3);
+    check_bf16_rows(q_norm_weight, "q_norm_weight", 1);
+    check_bf16_rows(k_norm_weight, "k_norm_weight", 1);
+    check_bf16_rows(cos, "cos", 3);
+    check_bf16_rows(sin, "sin", 3);
+    for (auto* t : {&slot_ids, &cached_lens, &num_decoding}) check_i32(*t, "index");
+    const c10::DeviceGuard guard(q.device());
+    ie_kv_cache c = cache_desc(k_cache, v_cache, k_scale, v_scale, k_calibration);
+    const int64_t B = q.size(0), hq = q.size(1);
+    TORCH_CHECK(q.size(2) == 128 && k.size(2) == 128 && v.size(2) == 128, "ie: head_dim 128");
+    TORCH_CHECK(k.size(0) >= B && v.size(0) >= B && k.size(1) == c.num_kv_heads &&
+                    v.size(1) == c.num_kv_heads,
+                "ie: k/v shape mismatch");
+    TORCH_CHECK(cos.size(0) >= B && sin.size(0) >= B && cos.size(2) == 64 && sin.size(2) == 64,
+                "ie: cos/sin must be [B,1,64]");
+    TORCH_CHECK(slot_ids.size(0) >= B && cached_lens.size(0) >= B, "ie: index tensors too short");
+    at::Tensor out = at::empty({B, hq, 128}, q.options());
+    ok(ie_fused_rope_kv_decode(bf(q), q.stride(0), q.stride(1), bf(k), k.stride(0), k.stride(1),
+                               bf(v), v.stride(0), v.stride(1), bf(q_norm_weight),
+                               bf(k_norm_weight), bf(cos), cos.stride(0), bf(sin), sin.stride(0),
+                               i32(slot_ids), i32(cached_lens), i32(num_decoding), (int32_t)B,
+                               (int32_t)hq, (float)eps, &c, bfm(out), out.stride(0),
+                               out.stride(1), stream_of(q)),
+       "fused_rope_kv_decode");
+    return out;
+}
+
+struct DecodeCall {
+    ie_kv_cache c;
+    int32_t B, hq;
+    size_t ws_bytes;
+};
+
+DecodeCall decode_prep(const at::Tensor& q, const at::Tensor& k_cache, const at::Tensor& v_cache,
+                       const at::Tensor& k_scale, const at::Tensor& v_scale,
+                       const at::Tensor& k_calibration, const at::Tensor& cached_lens,
+                       const at::Tensor& slot_ids, const at::Tensor& num_decoding,
+                       const at::Tensor& out) {
+    check_bf16_rows(q, "q", 3);
+    check_bf16_rows(out, "out", 3);
+    for (auto* t : {&slot_ids, &cached_lens, &num_decoding}) check_i32(*t, "index");
+    DecodeCall d;
+    d.c = cache_desc(k_cache, v_cache, k_scale, v_scale, k_calibration);
+    d.B = (int32_t)q.size(0);
+    d.hq = (int32_t)q.size(1);
+    // kernels.py:292
+    TORCH_CHECK(out.size(0) >= d.B && out.size(1) == d.hq && out.size(2) == q.size(2),
+                "ie: out must be [>=B, Hq, D]");
+    TORCH_CHECK(cached_lens.size(0) >= d.B && slot_ids.size(0) >= d.B,
+                "ie: index tensors too short");
+    d.ws_bytes = ie_decode_attention_workspace_size(d.B, d.hq, (int32_t)q.size(2));
+    return d;
+}
+
+at::Tensor workspace_for(const at::Tensor& q, size_t bytes) {
+    return at::empty({(int64_t)std::max<size_t>(bytes, 16)}, q.options().dtype(at::kByte));
+}
+
+void decode_attention(const at::Tensor& q, const at::Tensor& k_cache, const at::Tensor& v_cache,
+                      const at::Tensor& k_scale, const at::Tensor& v_scale,
+                      const at::Tensor& k_calibration, const at::Tensor& cached_lens,
+                      const at::Tensor& slot_ids, const at::Tensor& num_decoding, double scale,
+                      const at::Tensor& out) {
+    const c10::DeviceGuard guard(q.device());
+    DecodeCall d = decode_prep(q, k_cache, v_cache, k_scale, v_scale, k_calibration, cached_lens,
+                               slot_ids, num_decoding, out);
+    at::Tensor ws = workspace_for(q, d.ws_bytes);
+    ok(ie_decode_attention(bf(q), q.stride(0), q.stride(1), d.B, d.hq, &d.c, i32(cached_lens),
+                           i32(slot_ids), i32(num_decoding), (float)scale, bfm(out),
+                           out.stride(0), out.stride(1), ws.data_ptr(), d.ws_bytes, stream_of(q)),
+       "decode_attention");
+}
+
+// The two launches of decode_attention with a caller-owned workspace (profiling harnesses).
+void decode_attention_split(const at::Tensor& q, const at::Tensor& k_cache,
+                            const at::Tensor& v_cache, const at::Tensor& k_scale,
+                            const at::Tensor& v_scale, const at::Tensor& k_calibration,
+                            const at::Tensor& cached_lens, const at::Tensor& slot_ids,
+                            const at::Tensor& num_decoding, double scale, const at::Tensor& out,
+                            const at::Tensor& workspace) {
+    const c10::DeviceGuard guard(q.device());
+    DecodeCall d = decode_prep(q, k_cache, v_cache, k_scale, v_scale, k_calibration, cached_lens,
+                               slot_ids, num_decoding, out);
+    TORCH_CHECK((size_t)workspace.numel() * workspace.element_size() >= d.ws_bytes,
+                "ie: workspace too small");
+    ok(ie_decode_attention_split(bf(q), q.stride(0), q.stride(1), d.B, d.hq, &d.c,
+                                 i32(cached_lens), i32(slot_ids), i32(num_decoding), (float)scale,
+                                 bfm(out), out.stride(0), out.stride(1), workspace.data_ptr(),
+                                 d.ws_bytes, stream_of(q)),
+       "decode_attention_split");
+}
+
+void decode_attention_combine(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
+                              const at::Tensor& cached_lens, const at::Tensor& num_decoding,
+                              const at::Tensor& out, const at::Tensor& workspace) {
+    check_bf16_rows(out, "out", 3);
+    const c10::DeviceGuard guard(out.device());
+    const size_t bytes =
+        ie_decode_attention_workspace_size((int32_t)batch, (int32_t)num_q_heads, 128);
+    TORCH_CHECK((size_t)workspace.numel() * workspace.element_size() >= bytes,
+                "ie: workspace too small");
+    ok(ie_decode_attention_combine((int32_t)batch, (int32_t)num_q_heads, 128,
+                                   (int32_t)num_kv_heads, i32(cached_lens), i32(num_decoding),
+                                   bfm(out), out.stride(0), out.stride(1), workspace.data_ptr(),
+                                   bytes, stream_of(out)),
+       "decode_attention_combine");
+}
+
+int64_t decode_attention_workspace_size(int64_t batch, int64_t num_q_heads) {
+    return (int64_t)ie_decode_attention_workspace_size((int32_t)batch, (int32_t)num_q_heads, 128);
+}
+
+void dequantize_kv_prefix(const at::Tensor& k_cache, const at::Tensor& v_cache,
+                          const at::Tensor& k_scale, const at::Tensor& v_scale,
+                          const at::Tensor& k_calibration, const at::Tensor& cu_cached,
+                          const at::Tensor& slot_ids, const at::Tensor& k_out,
+                          const at::Tensor& v_out) {
+    check_i32(cu_cached, "cu_cached");
+    check_i32(slot_ids, "slot_ids");
+    check_bf16_rows(k_out, "k_out", 3);
+    check_bf16_rows(v_out, "v_out", 3);
+    TORCH_CHECK(k_out.strides() == v_out.strides(), "ie: k_out/v_out strides differ");
+    const c10::DeviceGuard guard(k_cache.device());
+    ie_kv_cache c = cache_desc(k_cache, v_cache, k_scale, v_scale, k_calibration);
+    const int32_t entries = (int32_t)cu_cached.size(0) - 1;
+    ok(ie_dequantize_kv_prefix(&c, i32(cu_cached), i32(slot_ids), entries, bfm(k_out), bfm(v_out),
+                               k_out.stride(0), k_out.stride(1), stream_of(k_cache)),
+       "dequantize_kv_prefix");
+}
+
+at::Tensor prefill_attention(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
+                             const at::Tensor& seq_ids, const at::Tensor& cu_seqlens,
+                             const at::Tensor& tile_start, const at::Tensor& k_cache,
+                             const at::Tensor& v_cache, const at::Tensor& k_scale,
+                             const at::Tensor& v_scale, const at::Tensor& k_calibration,
+                             const at::Tensor& slot_ids, const at::Tensor& cu_cached,
+                             int64_t block_m) {
+    check_bf16_rows(q, "q", 3);
+    check_bf16_rows(k, "k", 3);
+    check_bf16_rows(v, "v", 3);
+    for (auto* t : {&seq_ids, &cu_seqlens, &tile_start, &slot_ids, &cu_cached})
+        check_i32(*t, "index");
+    const c10::DeviceGuard guard(q.device());
+    ie_kv_cache c = cache_desc(k_cache, v_cache, k_scale, v_scale, k_calibration);
+    const int64_t N = q.size(0);
+    TORCH_CHECK(k.size(0) == N && v.size(0) == N && k.size(1) == c.num_kv_heads &&
+                    v.size(1) == c.num_kv_heads,
+                "ie: k/v shape mismatch");
+    at::Tensor out = at::empty({N, q.size(1), q.size(2)}, q.options());
+    ok(ie_prefill_attention(bf(q), q.stride(0), q.stride(1), bf(k), k.stride(0), k.stride(1),
+                            bf(v), v.stride(0), v.stride(1), N, (int32_t)q.size(1), i32(seq_ids),
+                            i32(cu_seqlens), i32(tile_start), (int32_t)tile_start.size(0),
+                            (int32_t)block_m, &c, i32(slot_ids), i32(cu_cached), bfm(out),
+                            out.stride(0), out.stride(1), stream_of(q)),
+       "prefill_attention");
+    return out;
+}
+
+}  // namespace
+
+TORCH_LIBRARY(ie, m) {
+    m.def(
+        "quantize_kv_prefill(Tensor k, Tensor v, Tensor cu_seqlens, Tensor slot_ids, "
+        "Tensor cached_lens, Tensor num_decoding, Tensor(a!) k_cache, Tensor(b!) v_cache, "
+        "Tensor(c!) k_scale, Tensor(d!) v_scale, Tensor(e!) k_calibration) -> ()");
+    m.def(
+        "fused_rope_kv_decode(Tensor q, Tensor k, Tensor v, Tensor q_norm_weight, "
+        "Tensor k_norm_weight, Tensor cos, Tensor sin, Tensor slot_ids, Tensor(a!) k_cache, "
+        "Tensor(b!) v_cache, Tensor(c!) k_scale, Tensor(d!) v_scale, Tensor k_calibration, "
+        "Tensor cached_lens, Tensor num_decoding, float eps) -> Tensor");
+    m.def(
+        "decode_attention(Tensor q, Tensor k_cache, Tensor v_cache, Tensor k_scale, "
+        "Tensor v_scale, Tensor k_calibration, Tensor cached_lens, Tensor slot_ids, "
+        "Tensor num_decoding, float scale, Tensor(a!) out) -> ()");
+    m.def(
+        "decode_attention_split(Tensor q, Tensor k_cache, Tensor v_cache, Tensor k_scale, "
+        "Tensor v_scale, Tensor k_calibration, Tensor cached_lens, Tensor slot_ids, "
+        "Tensor num_decoding, float scale, Tensor(a!) out, Tensor(b!) workspace) -> ()");
+    m.def(
+        "decode_attention_combine(int batch, int num_q_heads, int num_kv_heads, "
+        "Tensor cached_lens, Tensor num_decoding, Tensor(a!) out, Tensor workspace) -> ()");
+    m.def("decode_attention_workspace_size(int batch, int num_q_heads) -> int");
+    m.def(
+        "dequantize_kv_prefix(Tensor k_cache, Tensor v_cache, Tensor k_scale, Tensor v_scale, "
+        "Tensor k_calibration, Tensor cu_cached, Tensor slot_ids, Tensor(a!) k_out, "
+        "Tensor(b!) v_out) -> ()");
+    m.def(
+        "prefill_attention(Tensor q, Tensor k, Tensor v, Tensor seq_ids, Tensor cu_seqlens, "
+        "Tensor tile_start, Tensor k_cache, Tensor v_cache, Tensor k_scale, Tensor v_scale, "
+        "Tensor k_calibration, Tensor slot_ids, Tensor cu_cached, int block_m) -> Tensor");
+    m.impl("decode_attention_workspace_size", &decode_attention_workspace_size);
+}
+
+TORCH_LIBRARY_IMPL(ie, CUDA, m) {
+    m.impl("quantize_kv_prefill", &quantize_kv_prefill);
+    m.impl("fused_rope_kv_decode", &fused_rope_kv_decode);
+    m.impl("decode_attention", &decode_attention);
+    m.impl("decode_attention_split", &decode_attention_split);
+    m.impl("decode_attention_combine", &decode_attention_combine);
+    m.impl("dequantize_kv_prefix", &dequantize_kv_prefix);
+    m.impl("prefill_attention", &prefill_attention);
+}

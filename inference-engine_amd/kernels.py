@@ -1,0 +1,165 @@
+"""The attention kernel API of kbwal/inference-engine (qwen3-1.7b/kernels.py), on MI355X.
+
+Same names, argument tensors, cache layout and host-side assertions as the reference's Python
+wrappers; each call forwards to a torch.ops.ie op (lib/_ie_torch_ops.so), which forwards to the
+C ABI of include/ie_attn.h (lib/libie_attn.so, hand-written gfx950 HIP). Nothing here computes on
+the host, and there is no other code path: if the native libraries are missing the first call
+raises.
+
+Only one signature differs from the reference: `prefill_attention` reads each entry's cached
+prefix straight from the int8 cache, so it takes (kv_cache, slot_ids, cu_cached) where the
+reference took the bf16 prefix scratch (k_prefix, v_prefix, cu_cached) that
+`dequantize_kv_prefix` filled (qwen3-1.7b/architecture.py:151-170). `dequantize_kv_prefix`
+itself is still provided with the reference's signature.
+"""
+
+from dataclasses import dataclass
+
+import torch
+
+from ._native import ops
+
+
+@dataclass
+class LayerKVCache:
+    """qwen3-1.7b/kernels.py:11-17."""
+
+    k: torch.Tensor  # int8  [pool, Hkv, max_len, D]
+    v: torch.Tensor  # int8  [pool, Hkv, max_len, D]
+    k_scale: torch.Tensor  # fp32  [pool, Hkv, max_len]
+    v_scale: torch.Tensor  # fp32  [pool, Hkv, max_len]
+    k_calibration: torch.Tensor  # fp32  [pool, Hkv, 1, D]
+
+
+def make_layer_cache(pool: int, num_kv_heads: int, max_len: int, head_dim: int,
+                     device="cuda") -> LayerKVCache:
+    """Zeroed cache with calibration ones (qwen3-1.7b/engine.py:472-492)."""
+    return LayerKVCache(
+        k=torch.zeros(pool, num_kv_heads, max_len, head_dim, device=device, dtype=torch.int8),
+        v=torch.zeros(pool, num_kv_heads, max_len, head_dim, device=device, dtype=torch.int8),
+        k_scale=torch.zeros(pool, num_kv_heads, max_len, device=device, dtype=torch.float32),
+        v_scale=torch.zeros(pool, num_kv_heads, max_len, device=device, dtype=torch.float32),
+        k_calibration=torch.ones(pool, num_kv_heads, 1, head_dim, device=device,
+                                 dtype=torch.float32),
+    )
+
+
+def _cache_args(c: LayerKVCache):
+    return c.k, c.v, c.k_scale, c.v_scale, c.k_calibration
+
+
+def decode_attention(
+    q: torch.Tensor,  # [B, Hq, D], one new token per sequence
+    kv_cache: LayerKVCache,
+    cached_lens: torch.Tensor,  # [B], tokens already cached per sequence
+    slot_ids: torch.Tensor,  # [B], kv cache row of each sequence
+    num_decoding: torch.Tensor,  # int32 [1], how many entries are decoding
+    scale,
+    out: torch.Tensor | None = None,  # [>= B, Hq, D]; decoding entry b's output goes to row b
+):
+    """qwen3-1.7b/kernels.py:272-361. Split-K kernel + reduce kernel on the current stream."""
+    k_cache, v_cache = kv_cache.k, kv_cache.v
+    assert k_cache.stride() == v_cache.stride(), "kernel uses one set of strides for k and v"
+    assert kv_cache.k_scale.stride() == kv_cache.v_scale.stride()
+    B, Hq, D = q.shape
+    if out is None:
+        out = torch.empty(B, Hq, D, device=q.device, dtype=q.dtype)
+    assert out.shape[0] >= B and out.shape[1:] == (Hq, D) and out.stride(-1) == 1
+    ops().decode_attention(q, *_cache_args(kv_cache), cached_lens, slot_ids, num_decoding,
+                           float(scale), out)
+    return out
+
+
+def decode_attention_workspace(q: torch.Tensor) -> torch.Tensor:
+    """Workspace for `decode_attention_split`/`_combine` (fp32 split-K partials)."""
+    n = ops().decode_attention_workspace_size(q.shape[0], q.shape[1])
+    return torch.empty(max(int(n), 16), device=q.device, dtype=torch.uint8)
+
+
+def decode_attention_split(q, kv_cache, cached_lens, slot_ids, num_decoding, scale, out,
+                           workspace):
+    """First launch of `decode_attention` (split-K partials / single-piece outputs)."""
+    ops().decode_attention_split(q, *_cache_args(kv_cache), cached_lens, slot_ids, num_decoding,
+                                 float(scale), out, workspace)
+    return out
+
+
+def decode_attention_combine(q, kv_cache, cached_lens, num_decoding, out, workspace):
+    """Second launch of `decode_attention` (merge of the pieces, kernels.py:216-264)."""
+    ops().decode_attention_combine(q.shape[0], q.shape[1], kv_cache.k.shape[1], cached_lens,
+                                   num_decoding, out, workspace)
+    return out
+
+
+def fused_rope_kv_decode(
+    q: torch.Tensor,  # (B, Hq, D), one new token per sequence
+    k: torch.Tensor,  # (B, Hkv, D)
+    v: torch.Tensor,
+    q_norm_weight: torch.Tensor,  # (D,)
+    k_norm_weight: torch.Tensor,
+    cos: torch.Tensor,  # (B, 1, D // 2)
+    sin: torch.Tensor,
+    slot_ids: torch.Tensor,  # [B]
+    kv_cache: LayerKVCache,
+    cached_lens: torch.Tensor,  # [B]
+    num_decoding: torch.Tensor,
+    eps: float,
+):
+    """qwen3-1.7b/kernels.py:483-544: returns normed + roped q (x calibration), writes K/V."""
+    assert kv_cache.k.stride() == kv_cache.v.stride(), "kernel uses one set of strides for both caches"
+    assert kv_cache.k_scale.stride() == kv_cache.v_scale.stride()
+    return ops().fused_rope_kv_decode(q, k, v, q_norm_weight, k_norm_weight, cos, sin, slot_ids,
+                                      *_cache_args(kv_cache), cached_lens, num_decoding,
+                                      float(eps))
+
+
+def quantize_kv_prefill(
+    k: torch.Tensor,  # bf16 [N, Hkv, D], all sequences packed along N
+    v: torch.Tensor,  # bf16 [N, Hkv, D]
+    cu_seqlens: torch.Tensor,  # int32 [B + 1]
+    slot_ids: torch.Tensor,  # [B]
+    cached_lens: torch.Tensor,  # [B]
+    num_decoding: torch.Tensor,
+    cache: LayerKVCache,
+):
+    """qwen3-1.7b/kernels.py:826-865."""
+    N, Hkv, D = k.shape
+    assert k.stride(-1) == 1 and v.stride(-1) == 1, "kernel assumes contiguous head_dim"
+    assert cache.k.stride() == cache.v.stride()
+    assert cache.k_scale.stride() == cache.v_scale.stride()
+    ops().quantize_kv_prefill(k, v, cu_seqlens, slot_ids, cached_lens, num_decoding,
+                              *_cache_args(cache))
+
+
+def dequantize_kv_prefix(
+    cache: LayerKVCache,
+    cu_cached: torch.Tensor,  # int32 [B + 1]
+    slot_ids: torch.Tensor,  # [B]
+    k_out: torch.Tensor,  # bf16 [Hkv, >= total_cached, D]
+    v_out: torch.Tensor,
+):
+    """qwen3-1.7b/kernels.py:935-970."""
+    assert cache.k.stride() == cache.v.stride()
+    assert cache.k_scale.stride() == cache.v_scale.stride()
+    assert k_out.stride() == v_out.stride() and k_out.stride(-1) == 1
+    ops().dequantize_kv_prefix(*_cache_args(cache), cu_cached, slot_ids, k_out, v_out)
+
+
+def prefill_attention(
+    q: torch.Tensor,  # bf16 [N, Hq, D], all sequences packed along N
+    k: torch.Tensor,  # bf16 [N, Hkv, D]
+    v: torch.Tensor,  # bf16 [N, Hkv, D]
+    seq_ids: torch.Tensor,  # [N] which entry each packed token belongs to
+    cu_seqlens: torch.Tensor,  # [B + 1] int32
+    tile_start: torch.Tensor,  # [num_tiles] int32, first packed row of each tile
+    kv_cache: LayerKVCache,  # entry b's prefix is cache row slot_ids[b]
+    slot_ids: torch.Tensor,  # [B]
+    cu_cached: torch.Tensor,  # [B + 1] int32, prefix lengths of every entry, cumulative
+    PREFILL_BLOCK_M: int,  # must be the value tile_start was built with
+) -> torch.Tensor:
+    """qwen3-1.7b/kernels.py:1129-1175 fused with the prefix dequantize (architecture.py:151-170)."""
+    N, Hq, D = q.shape
+    assert q.stride(-1) == 1 and k.stride(-1) == 1 and v.stride(-1) == 1
+    return ops().prefill_attention(q, k, v, seq_ids, cu_seqlens, tile_start,
+                                   *_cache_args(kv_cache), slot_ids, cu_cached,
+                                   int(PREFILL_BLOCK_M))

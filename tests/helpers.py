@@ -1,0 +1,49 @@
+"""Shared test helpers: moving caches between torch and the numpy oracle, tolerance checks."""
+
+import sys
+
+import numpy as np
+import torch
+
+from oracle import kv_cache as okv
+
+TOL_MAX, TOL_MEAN = 2e-2, 2e-3  # bf16 attention tolerance of the north star
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def cache_np(c) -> okv.CacheArrays:
+    return okv.CacheArrays(*(t.detach().cpu().numpy().copy() for t in
+                             (c.k, c.v, c.k_scale, c.v_scale, c.k_calibration)))
+
+
+def cache_to(c, device, LayerKVCache):
+    return LayerKVCache(*(t.to(device).clone() for t in
+                          (c.k, c.v, c.k_scale, c.v_scale, c.k_calibration)))
+
+
+def assert_cache_bitwise(gpu_cache, ref: okv.CacheArrays, what=""):
+    got = cache_np(gpu_cache)
+    for name in ("k", "v", "k_scale", "v_scale", "k_calibration"):
+        a, b = getattr(got, name), getattr(ref, name)
+        if a.dtype == np.float32:
+            a, b = a.view(np.uint32), b.view(np.uint32)
+        bad = np.argwhere(a != b)
+        assert bad.size == 0, f"{what} {name}: {len(bad)} mismatches, first at {bad[:4].tolist()}"
+
+
+def assert_attn_close(got, ref, what=""):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    assert got.shape == ref.shape
+    assert np.isfinite(got).all(), f"{what}: non-finite output"
+    err = np.abs(got - ref)
+    say(f"{what}: max abs err {err.max():.3e} mean {err.mean():.3e}")
+    assert err.max() <= TOL_MAX and err.mean() <= TOL_MEAN, what
+
+
+def bf16_np(t: torch.Tensor) -> np.ndarray:
+    return t.detach().float().cpu().numpy()

@@ -1,0 +1,67 @@
+"""The C ABI library loads, exports everything include/ie_attn.h declares, and rejects bad
+arguments on the host before touching a device (CPU only: no compute calls)."""
+
+import ctypes
+
+import pytest
+import torch
+
+HIP_ERROR_INVALID_VALUE = 1
+
+
+def test_library_exports_every_declared_symbol(native):
+    lib = native.cabi()
+    names = native.header_functions()
+    assert len(names) >= 11
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, f"declared but not exported: {missing}"
+    assert lib.ie_attn_version() >> 16 == 1
+
+
+def test_torch_ops_registered(ie):
+    ops = ie.kernels.ops()
+    for name in ["quantize_kv_prefill", "fused_rope_kv_decode", "decode_attention",
+                 "decode_attention_split", "decode_attention_combine", "dequantize_kv_prefix",
+                 "prefill_attention", "decode_attention_workspace_size"]:
+        assert hasattr(ops, name), name
+
+
+def test_null_cache_rejected_on_host(native):
+    lib = native.cabi()
+    fn = lib.ie_decode_attention
+    fn.restype = ctypes.c_int
+    null = ctypes.c_void_p(0)
+    rc = fn(null, ctypes.c_int64(128), ctypes.c_int64(128), ctypes.c_int32(1), ctypes.c_int32(16),
+            null, null, null, null, ctypes.c_float(0.1), null, ctypes.c_int64(2048),
+            ctypes.c_int64(128), null, ctypes.c_size_t(0), null)
+    assert rc == HIP_ERROR_INVALID_VALUE
+    assert b"null" in lib.ie_attn_last_error()
+
+
+def test_bad_geometry_rejected_on_host(native):
+    lib = native.cabi()
+    desc = native.KVCacheDesc(16, 16, 16, 16, 16, 2, 8, 64, 64, 8 * 64 * 64, 64 * 64, 64,
+                              8 * 64, 64, 8 * 64, 64)  # head_dim 64: unsupported
+    fn = lib.ie_quantize_kv_prefill
+    fn.restype = ctypes.c_int
+    null = ctypes.c_void_p(0)
+    rc = fn(null, ctypes.c_int64(0), ctypes.c_int64(0), null, ctypes.c_int64(0),
+            ctypes.c_int64(0), ctypes.c_int64(0), null, null, null, null, ctypes.c_int32(1),
+            ctypes.byref(desc), null)
+    assert rc == HIP_ERROR_INVALID_VALUE
+    assert b"head_dim" in lib.ie_attn_last_error()
+
+
+def test_workspace_size_formula(native):
+    lib = native.cabi()
+    splits = lib.ie_decode_attention_max_splits(8)
+    assert splits >= 1
+    assert lib.ie_decode_attention_workspace_size(64, 16, 128) == 64 * 16 * splits * 130 * 4
+
+
+def test_ops_refuse_cpu_tensors(ie):
+    c = ie.make_layer_cache(2, 8, 64, 128, device="cpu")
+    q = torch.zeros(1, 16, 128, dtype=torch.bfloat16)
+    i = torch.zeros(1, dtype=torch.int32)
+    with pytest.raises((RuntimeError, NotImplementedError)):
+        ie.decode_attention(q, c, i, i, i, 0.1)
