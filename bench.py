@@ -139,6 +139,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-sample", type=int, default=8)
     ap.add_argument("--sweep", action="store_true", help="also time the config-3 shape sweep")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="first run a plain device copy of MIB MiB 3 times (PMC calibration)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -152,6 +154,16 @@ def main():
     K = ie.kernels
     dev = "cuda:0"
     torch.cuda.set_device(0)
+
+    if args.copy_probe:
+        n = args.copy_probe << 20
+        src = torch.ones(n, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copy probe: 3 x {n} bytes read + written")
+        del src, dst
 
     ctx = [args.ctx] * args.batch
     log(f"building {args.rotate} cache sets B={args.batch} ctx={args.ctx}")

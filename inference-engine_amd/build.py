@@ -58,20 +58,22 @@ def _torch_paths():
     return ce.include_paths(), ce.library_paths(), Path(torch.__file__).parent
 
 
-def build_hip(extra_flags=(), verbose=False) -> Path:
-    """Compile every HIP source for gfx950 and link lib/libie_attn.so."""
-    BUILD.mkdir(exist_ok=True)
-    LIB.mkdir(exist_ok=True)
+def build_hip(extra_flags=(), verbose=False, out_dir=None) -> Path:
+    """Compile every HIP source for gfx950 and link libie_attn.so into `out_dir` (lib/)."""
+    lib = Path(out_dir) if out_dir else LIB
+    obj_dir = lib / "_obj" if out_dir else BUILD
+    obj_dir.mkdir(parents=True, exist_ok=True)
+    lib.mkdir(parents=True, exist_ok=True)
     hipcc = _hipcc()
     flags = HIPCC_FLAGS + [f"-I{INCLUDE}"] + list(extra_flags)
-    objs = [BUILD / (Path(s).stem + ".o") for s in HIP_SOURCES]
+    objs = [obj_dir / (Path(s).stem + ".o") for s in HIP_SOURCES]
     with cf.ThreadPoolExecutor(max_workers=min(8, len(HIP_SOURCES))) as ex:
         futs = [ex.submit(_run, [hipcc, *flags, "-c", CSRC / s, "-o", o], verbose)
                 for s, o in zip(HIP_SOURCES, objs)]
         for f in futs:
             f.result()
-    out = LIB / "libie_attn.so"
-    tmp = LIB / "libie_attn.so.tmp"
+    out = lib / "libie_attn.so"
+    tmp = lib / "libie_attn.so.tmp"
     _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", tmp],
          verbose)
     os.replace(tmp, out)

@@ -7,7 +7,7 @@
 // The grid is (TARGET + B, Hkv): it depends on shapes only, so the launch is graph-capturable,
 // and each workgroup finds its (sequence, piece) on the device from cached_lens.
 //
-// One workgroup = 4 waves = one (sequence, piece, kv head), i.e. both query heads of the GQA
+// One workgroup = 8 waves = one (sequence, piece, kv head), i.e. both query heads of the GQA
 // pair. Lane (g, c) of a wave (g = lane / 8, c = lane % 8) owns channels [16c, 16c+16) of the
 // four tokens 4g..4g+3 of the wave's 32-token block: each K and V row (128 int8) is read by 8
 // lanes with 16-byte loads, so one load instruction of a wave covers 8 full 128-byte rows.
@@ -23,19 +23,31 @@
 //   (m, l, acc) go to the workspace for the combine kernel (kernels.py:216-264).
 #include "ie_common.h"
 
+// Launch shape (measured on MI355X, B=64 ctx=4096): 8-wave workgroups, 2 per CU (the
+// register budget allows 4 waves per SIMD), so one piece covers a whole 4096-token row there.
 #ifndef IE_DECODE_WG_PER_CU
-#define IE_DECODE_WG_PER_CU 4
+#define IE_DECODE_WG_PER_CU 2
 #endif
 
 namespace ie {
 
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 
-constexpr int DA_THREADS = 256;
-constexpr int DA_WAVES = DA_THREADS / IE_WAVE;
+#ifndef IE_DECODE_WG_WAVES
+#define IE_DECODE_WG_WAVES 8
+#endif
+// K/V/scale loads carry the non-temporal cache policy (aux bit 1, "nt" on gfx94x/gfx950): every
+// byte is read once, and streaming it past the caches raised read bandwidth from ~6.0 to
+// ~7.0 TB/s in isolation.
+#ifndef IE_DECODE_LOAD_AUX
+#define IE_DECODE_LOAD_AUX 2
+#endif
+
+constexpr int DA_WAVES = IE_DECODE_WG_WAVES;
+constexpr int DA_THREADS = DA_WAVES * IE_WAVE;
 constexpr int DA_U = 4;                            // tokens per lane group per block
 constexpr int DA_TOK_WAVE = 8 * DA_U;              // 32 tokens per wave block
-constexpr int DA_TOK_WG = DA_WAVES * DA_TOK_WAVE;  // 128 tokens per workgroup step
+constexpr int DA_TOK_WG = DA_WAVES * DA_TOK_WAVE;  // tokens per workgroup step
 constexpr int DA_MIN_PIECE = 128;
 constexpr int DA_D = 128;
 constexpr uint32_t K64 = 0x64646464u;
@@ -101,6 +113,7 @@ __device__ Work decode_assign(const int32_t* __restrict__ cached_lens, int nd, i
     return r;
 }
 
+__device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
 __device__ __forceinline__ half2_t as_h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
 __device__ __forceinline__ float fdot2(half2_t a, half2_t b, float c) {
     return __builtin_amdgcn_fdot2(a, b, c, false);
@@ -123,19 +136,140 @@ struct DecodeArgs {
     int target, max_splits, hq;
 };
 
-__global__ __launch_bounds__(DA_THREADS) void decode_split_kernel(DecodeArgs a) {
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr int RSRC_WORD3 = 0x00020000;  // GFX9 buffer descriptor word 3 (32-bit raw data)
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, RSRC_WORD3);
+}
+__device__ __forceinline__ v4u ld128(rsrc_t r, int off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, IE_DECODE_LOAD_AUX);
+}
+
+// Running softmax state of one lane: query heads (2hk, 2hk+1), channels [16c, 16c+16).
+struct LaneState {
+    float m[2], l[2], ps[2];
+    float acc[2][16];
+};
+
+// Registers of one 32-token block of a wave: lane group g holds tokens t0+4g .. t0+4g+3,
+// channels [16c, 16c+16), plus their 4 K (or V) scales.
+struct KVRegs {
+    v4u x[DA_U];
+    v4u scale;
+};
+
+__device__ __forceinline__ void load_block(KVRegs& r, rsrc_t rows, rsrc_t scales, int tok,
+                                           int cc) {
+    const int off = tok * DA_D + 16 * cc;
+#pragma unroll
+    for (int u = 0; u < DA_U; ++u) r.x[u] = ld128(rows, off + u * DA_D);
+    r.scale = ld128(scales, tok * 4);
+}
+
+// Scores of the block in base 2, scaled: s = (q.k - 1152 sum q) * k_scale * scale*log2e / 2^e.
+// With MASKED, tokens at or past t_end score -inf (their loads returned zeros: buffer range).
+template <bool MASKED>
+__device__ __forceinline__ void block_scores(float (&s)[DA_U][2], const KVRegs& k,
+                                             const half2_t (&qh)[2][8], const float (&qsum)[2],
+                                             const float (&kmul)[2], int tok, int t_end) {
+#pragma unroll
+    for (int u = 0; u < DA_U; ++u) {
+        float d0 = 0.0f, d1 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t x = k.x[u][i] ^ 0x80808080u;
+            const half2_t h01 = as_h2(__builtin_amdgcn_perm(K64, x, 0x04010400u));
+            const half2_t h23 = as_h2(__builtin_amdgcn_perm(K64, x, 0x04030402u));
+            d0 = fdot2(qh[0][2 * i], h01, d0);
+            d0 = fdot2(qh[0][2 * i + 1], h23, d0);
+            d1 = fdot2(qh[1][2 * i], h01, d1);
+            d1 = fdot2(qh[1][2 * i + 1], h23, d1);
+        }
+        d0 = sum8(d0);
+        d1 = sum8(d1);
+        const float ks = __uint_as_float(k.scale[u]);
+        s[u][0] = (d0 - qsum[0]) * (ks * kmul[0]);
+        s[u][1] = (d1 - qsum[1]) * (ks * kmul[1]);
+        if (MASKED && tok + u >= t_end) s[u][0] = s[u][1] = -INFINITY;
+    }
+}
+
+// Online-softmax update of the lane group and the PV accumulation of the block.
+__device__ __forceinline__ void block_pv(LaneState& st, const float (&s)[DA_U][2],
+                                         const KVRegs& v) {
+    float msafe[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const float mt = fmaxf(fmaxf(s[0][h], s[1][h]), fmaxf(s[2][h], s[3][h]));
+        const float mn = fmaxf(st.m[h], mt);
+        if (mn > st.m[h]) {
+            const float alpha = exp2_safe(st.m[h] - mn);  // m = -inf -> 0
+#pragma unroll
+            for (int j = 0; j < 16; ++j) st.acc[h][j] *= alpha;
+            st.l[h] *= alpha;
+            st.ps[h] *= alpha;
+            st.m[h] = mn;
+        }
+        msafe[h] = st.m[h] == -INFINITY ? 0.0f : st.m[h];
+    }
+    half2_t pp[DA_U / 2][2];  // (p * v_scale) of token pairs, fp16
+#pragma unroll
+    for (int pr = 0; pr < DA_U / 2; ++pr)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const float pa = exp2_safe(s[2 * pr][h] - msafe[h]);
+            const float pb = exp2_safe(s[2 * pr + 1][h] - msafe[h]);
+            st.l[h] += pa + pb;
+            pp[pr][h] = half2_t{(_Float16)(pa * __uint_as_float(v.scale[2 * pr])),
+                                (_Float16)(pb * __uint_as_float(v.scale[2 * pr + 1]))};
+            st.ps[h] = fdot2(pp[pr][h], half2_t{(_Float16)1.0f, (_Float16)1.0f}, st.ps[h]);
+        }
+#pragma unroll
+    for (int pr = 0; pr < DA_U / 2; ++pr) {
+        const int ua = 2 * pr, ub = ua + 1;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t xa = v.x[ua][i] ^ 0x80808080u, xb = v.x[ub][i] ^ 0x80808080u;
+            const uint32_t t01 = __builtin_amdgcn_perm(xb, xa, 0x05010400u);
+            const uint32_t t23 = __builtin_amdgcn_perm(xb, xa, 0x07030602u);
+            const half2_t c[4] = {as_h2(__builtin_amdgcn_perm(K64, t01, 0x04010400u)),
+                                  as_h2(__builtin_amdgcn_perm(K64, t01, 0x04030402u)),
+                                  as_h2(__builtin_amdgcn_perm(K64, t23, 0x04010400u)),
+                                  as_h2(__builtin_amdgcn_perm(K64, t23, 0x04030402u))};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                st.acc[0][4 * i + j] = fdot2(pp[pr][0], c[j], st.acc[0][4 * i + j]);
+                st.acc[1][4 * i + j] = fdot2(pp[pr][1], c[j], st.acc[1][4 * i + j]);
+            }
+        }
+    }
+}
+
+#ifndef IE_DECODE_WAVES_PER_EU
+#define IE_DECODE_WAVES_PER_EU 4
+#endif
+
+__global__ __launch_bounds__(DA_THREADS)
+__attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_split_kernel(
+    DecodeArgs a) {
     const int nd = a.num_decoding[0];
     const int hk = blockIdx.y;
-    const Work wk = decode_assign(a.cached_lens, nd, blockIdx.x, a.target);
+    Work wk = decode_assign(a.cached_lens, nd, blockIdx.x, a.target);
+    // Wave-uniform by construction; readfirstlane lets the compiler keep them (and the buffer
+    // descriptors built from them) in SGPRs.
+    wk.needed = uniform(wk.needed);
     if (wk.needed == 0) return;
+    const int b = uniform(wk.b);
+    const int split = uniform(wk.split);
+    const int piece = uniform(wk.piece);
+    const int n_end = uniform(a.cached_lens[b] + 1);
+    const int t_begin = split * piece;
+    const int t_end = min(t_begin + piece, n_end);
+    const int slot = uniform(a.slot_ids[b]);
 
-    const int b = wk.b;
-    const int n_end = a.cached_lens[b] + 1;
-    const int t_begin = wk.split * wk.piece;
-    const int t_end = min(t_begin + wk.piece, n_end);
-    const int slot = a.slot_ids[b];
-
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = uniform(threadIdx.x >> 6);
     const int g = lane >> 3, cc = lane & 7;
 
     // ---- q of the two heads of this KV head, channels [16cc, 16cc + 16) ----
@@ -172,107 +306,50 @@ __global__ __launch_bounds__(DA_THREADS) void decode_split_kernel(DecodeArgs a) 
         kmul[h] = a.scale_log2 / sc;
     }
 
-    const int8_t* kb = a.c.k + slot * a.c.stride_slot + hk * a.c.stride_head + 16 * cc;
-    const int8_t* vb = a.c.v + slot * a.c.stride_slot + hk * a.c.stride_head + 16 * cc;
-    const float* ksb = a.c.k_scale + slot * a.c.scale_stride_slot + hk * a.c.scale_stride_head;
-    const float* vsb = a.c.v_scale + slot * a.c.scale_stride_slot + hk * a.c.scale_stride_head;
+    // Buffer resources over this (slot, kv head) row, bounded at the piece's end.
+    const int8_t* krow = a.c.k + slot * a.c.stride_slot + hk * a.c.stride_head;
+    const int8_t* vrow = a.c.v + slot * a.c.stride_slot + hk * a.c.stride_head;
+    const float* ksrow = a.c.k_scale + slot * a.c.scale_stride_slot + hk * a.c.scale_stride_head;
+    const float* vsrow = a.c.v_scale + slot * a.c.scale_stride_slot + hk * a.c.scale_stride_head;
+    const rsrc_t rk = make_rsrc(krow, (uint32_t)t_end * DA_D);
+    const rsrc_t rv = make_rsrc(vrow, (uint32_t)t_end * DA_D);
+    const rsrc_t rks = make_rsrc(ksrow, (uint32_t)t_end * 4);
+    const rsrc_t rvs = make_rsrc(vsrow, (uint32_t)t_end * 4);
 
-    float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.0f, 0.0f}, ps[2] = {0.0f, 0.0f};
-    float acc[2][16];
+    LaneState st;
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+    for (int h = 0; h < 2; ++h) {
+        st.m[h] = -INFINITY;
+        st.l[h] = 0.0f;
+        st.ps[h] = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 16; ++j) acc[h][j] = 0.0f;
-
-    for (int t0 = t_begin + wave * DA_TOK_WAVE; t0 < t_end; t0 += DA_TOK_WG) {
-        uint4 kr[DA_U], vr[DA_U];
-        float ks[DA_U], vs[DA_U];
-        bool valid[DA_U];
-#pragma unroll
-        for (int u = 0; u < DA_U; ++u) {
-            const int t = t0 + 4 * g + u;
-            valid[u] = t < t_end;
-            const int tl = valid[u] ? t : t_end - 1;  // masked tokens re-read a valid row
-            kr[u] = *reinterpret_cast<const uint4*>(kb + (int64_t)tl * DA_D);
-            vr[u] = *reinterpret_cast<const uint4*>(vb + (int64_t)tl * DA_D);
-            ks[u] = ksb[tl];
-            vs[u] = vsb[tl];
-        }
-        // ---- scores (base 2) ----
-        float s[DA_U][2];
-#pragma unroll
-        for (int u = 0; u < DA_U; ++u) {
-            const uint32_t kw[4] = {kr[u].x, kr[u].y, kr[u].z, kr[u].w};
-            float d0 = 0.0f, d1 = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t x = kw[i] ^ 0x80808080u;
-                const half2_t h01 = as_h2(__builtin_amdgcn_perm(K64, x, 0x04010400u));
-                const half2_t h23 = as_h2(__builtin_amdgcn_perm(K64, x, 0x04030402u));
-                d0 = fdot2(qh[0][2 * i], h01, d0);
-                d0 = fdot2(qh[0][2 * i + 1], h23, d0);
-                d1 = fdot2(qh[1][2 * i], h01, d1);
-                d1 = fdot2(qh[1][2 * i + 1], h23, d1);
-            }
-            d0 = sum8(d0);
-            d1 = sum8(d1);
-            s[u][0] = valid[u] ? (d0 - qsum[0]) * (ks[u] * kmul[0]) : -INFINITY;
-            s[u][1] = valid[u] ? (d1 - qsum[1]) * (ks[u] * kmul[1]) : -INFINITY;
-        }
-        // ---- online softmax per lane group ----
-        float msafe[2];
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const float mt = fmaxf(fmaxf(s[0][h], s[1][h]), fmaxf(s[2][h], s[3][h]));
-            const float mn = fmaxf(m[h], mt);
-            if (mn > m[h]) {
-                const float alpha = exp2_safe(m[h] - mn);  // m = -inf -> 0
-#pragma unroll
-                for (int j = 0; j < 16; ++j) acc[h][j] *= alpha;
-                l[h] *= alpha;
-                ps[h] *= alpha;
-                m[h] = mn;
-            }
-            msafe[h] = m[h] == -INFINITY ? 0.0f : m[h];
-        }
-        _Float16 pv[DA_U][2];
-#pragma unroll
-        for (int u = 0; u < DA_U; ++u)
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const float p = exp2_safe(s[u][h] - msafe[h]);
-                l[h] += p;
-                pv[u][h] = (_Float16)(p * vs[u]);
-                ps[h] += (float)pv[u][h];
-            }
-        // ---- PV over token pairs (u, u+1) ----
-#pragma unroll
-        for (int pr = 0; pr < DA_U / 2; ++pr) {
-            const int ua = 2 * pr, ub = ua + 1;
-            const half2_t p0 = half2_t{pv[ua][0], pv[ub][0]};
-            const half2_t p1 = half2_t{pv[ua][1], pv[ub][1]};
-            const uint32_t va[4] = {vr[ua].x, vr[ua].y, vr[ua].z, vr[ua].w};
-            const uint32_t vb4[4] = {vr[ub].x, vr[ub].y, vr[ub].z, vr[ub].w};
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t xa = va[i] ^ 0x80808080u, xb = vb4[i] ^ 0x80808080u;
-                const uint32_t t01 = __builtin_amdgcn_perm(xb, xa, 0x05010400u);
-                const uint32_t t23 = __builtin_amdgcn_perm(xb, xa, 0x07030602u);
-                const half2_t c0 = as_h2(__builtin_amdgcn_perm(K64, t01, 0x04010400u));
-                const half2_t c1 = as_h2(__builtin_amdgcn_perm(K64, t01, 0x04030402u));
-                const half2_t c2 = as_h2(__builtin_amdgcn_perm(K64, t23, 0x04010400u));
-                const half2_t c3 = as_h2(__builtin_amdgcn_perm(K64, t23, 0x04030402u));
-                acc[0][4 * i + 0] = fdot2(p0, c0, acc[0][4 * i + 0]);
-                acc[0][4 * i + 1] = fdot2(p0, c1, acc[0][4 * i + 1]);
-                acc[0][4 * i + 2] = fdot2(p0, c2, acc[0][4 * i + 2]);
-                acc[0][4 * i + 3] = fdot2(p0, c3, acc[0][4 * i + 3]);
-                acc[1][4 * i + 0] = fdot2(p1, c0, acc[1][4 * i + 0]);
-                acc[1][4 * i + 1] = fdot2(p1, c1, acc[1][4 * i + 1]);
-                acc[1][4 * i + 2] = fdot2(p1, c2, acc[1][4 * i + 2]);
-                acc[1][4 * i + 3] = fdot2(p1, c3, acc[1][4 * i + 3]);
-            }
-        }
+        for (int j = 0; j < 16; ++j) st.acc[h][j] = 0.0f;
     }
+
+    // Rolling pipeline: the next block's K is requested as soon as this block's scores are
+    // done and its V as soon as this block's PV is done, so every load has half a block of
+    // VALU work to hide behind without extra registers. Requests past the piece's end fall
+    // outside the buffer range and return zeros without touching memory.
+    int t0 = t_begin + wave * DA_TOK_WAVE;
+    KVRegs kr, vr;
+    load_block(kr, rk, rks, t0 + 4 * g, cc);
+    load_block(vr, rv, rvs, t0 + 4 * g, cc);
+    float s[DA_U][2];
+    for (; t0 + DA_TOK_WAVE <= t_end; t0 += DA_TOK_WG) {
+        block_scores<false>(s, kr, qh, qsum, kmul, t0 + 4 * g, t_end);
+        load_block(kr, rk, rks, t0 + DA_TOK_WG + 4 * g, cc);
+        block_pv(st, s, vr);
+        load_block(vr, rv, rvs, t0 + DA_TOK_WG + 4 * g, cc);
+    }
+    if (t0 < t_end) {
+        block_scores<true>(s, kr, qh, qsum, kmul, t0 + 4 * g, t_end);
+        block_pv(st, s, vr);
+    }
+
+    float (&m)[2] = st.m;
+    float (&l)[2] = st.l;
+    float (&ps)[2] = st.ps;
+    float (&acc)[2][16] = st.acc;
 
     // ---- merge the 8 lane groups of the wave ----
     float mw[2];
@@ -315,6 +392,7 @@ __global__ __launch_bounds__(DA_THREADS) void decode_split_kernel(DecodeArgs a) 
         }
     }
     __syncthreads();
+    if (threadIdx.x >= 2 * DA_D) return;  // one thread per (query head, channel)
     const int h = threadIdx.x >> 7, d = threadIdx.x & 127;
     float mx = -INFINITY;
 #pragma unroll
@@ -331,7 +409,7 @@ __global__ __launch_bounds__(DA_THREADS) void decode_split_kernel(DecodeArgs a) 
     if (wk.needed == 1) {
         a.out[b * a.o_sb + qh_idx * a.o_sh + d] = (uint16_t)f32_to_bf16_rne(num / den);
     } else {
-        const int64_t row = ((int64_t)b * a.hq + qh_idx) * a.max_splits + wk.split;
+        const int64_t row = ((int64_t)b * a.hq + qh_idx) * a.max_splits + split;
         a.part_acc[row * DA_D + d] = num;
         if (d == 0) {
             a.part_m[row] = mx;
