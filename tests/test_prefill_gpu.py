@@ -1,0 +1,58 @@
+"""Chunked-prefill attention on the GPU (int8 prefix dequantized in LDS, bf16 MFMA) against the
+oracle (reference rounding: bf16 prefix, bf16 P) within bf16 tolerance."""
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_attn_close, bf16_np, cache_np, say
+from oracle import attention as oat
+from oracle import kv_cache as okv
+
+pytestmark = pytest.mark.gpu
+
+
+def oracle_prefill(wl):
+    ins = {n: t.cpu().numpy() for n, t in wl.inputs.items()}
+    kp, vp = okv.dequantize_kv_prefix(cache_np(wl.cache), ins["cu_cached"], ins["slot_ids"])
+    return oat.prefill_attention(bf16_np(wl.q), bf16_np(wl.k), bf16_np(wl.v), ins["cu_seqlens"],
+                                 ins["tile_start"], wl.block_m, kp, vp, ins["cu_cached"])
+
+
+def run_gpu(ie, wl):
+    gi = wl.inputs
+    return ie.prefill_attention(wl.q, wl.k, wl.v, gi["seq_ids"], gi["cu_seqlens"],
+                                gi["tile_start"], wl.cache, gi["slot_ids"], gi["cu_cached"],
+                                wl.block_m)
+
+
+def check(ie, workloads, wl, dev, what):
+    ref = oracle_prefill(wl)
+    g = workloads.mixed_to(wl, dev)
+    out = run_gpu(ie, g)
+    torch.cuda.synchronize()
+    cov = ~np.isnan(ref[:, 0, 0])
+    assert cov.any()
+    assert_attn_close(bf16_np(out)[cov], ref[cov], what)
+
+
+def test_prefill_config4(ie, workloads, dev):
+    say("prefill config 4 (30 decoders, 512 new + 0 cached, 512 new + 1536 cached)")
+    check(ie, workloads, workloads.config4(seed=2), dev, "prefill config4")
+
+
+@pytest.mark.parametrize("block_m", [16, 32, 64, 128, 192])
+def test_prefill_tile_sizes(ie, workloads, dev, block_m):
+    say(f"prefill block_m={block_m}")
+    wl = workloads.mixed_workload([7, 300], [(100, 0), (65, 77), (1, 130), (129, 1)], seed=3,
+                                  block_m=block_m, max_len=1024)
+    check(ie, workloads, wl, dev, f"prefill block_m={block_m}")
+
+
+@pytest.mark.parametrize("chunks", [
+    [(1, 0)], [(64, 0)], [(63, 64)], [(200, 1000)], [(3, 0), (0, 0), (5, 5)], [(700, 2047)],
+])
+def test_prefill_edges(ie, workloads, dev, chunks):
+    say(f"prefill edge chunks {chunks}")
+    wl = workloads.mixed_workload([], chunks, seed=len(chunks), block_m=128, max_len=4096)
+    check(ie, workloads, wl, dev, f"prefill {chunks}")
