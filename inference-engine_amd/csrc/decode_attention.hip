@@ -137,12 +137,6 @@ struct DecodeArgs {
 };
 
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
-typedef __amdgpu_buffer_rsrc_t rsrc_t;
-constexpr int RSRC_WORD3 = 0x00020000;  // GFX9 buffer descriptor word 3 (32-bit raw data)
-
-__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, RSRC_WORD3);
-}
 __device__ __forceinline__ v4u ld128(rsrc_t r, int off) {
     return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, IE_DECODE_LOAD_AUX);
 }

@@ -22,16 +22,15 @@ __device__ __forceinline__ float bf16hi(uint32_t packed) {
     return __uint_as_float(packed & 0xffff0000u);
 }
 
-// Round-to-nearest-even fp32 -> bf16 bits (NaN stays NaN).
-__device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return u >> 16;
-}
+typedef __bf16 ie_bf16x2_t __attribute__((ext_vector_type(2)));
+
+// fp32 -> bf16 with round-to-nearest-even: the gfx950 v_cvt_pk_bf16_f32 conversion (one
+// instruction per pair, NaN stays NaN).
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-    return f32_to_bf16_rne(lo) | (f32_to_bf16_rne(hi) << 16);
+    const ie_bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+    return __builtin_bit_cast(uint32_t, v);
 }
+__device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) { return pack_bf16x2(f, 0.0f) & 0xffffu; }
 
 // ---------------------------------------------------------------------------------------------
 // Lane exchange. DPP controls (GFX9): quad_perm = sel0 | sel1<<2 | sel2<<4 | sel3<<6,
@@ -87,6 +86,17 @@ __device__ __forceinline__ float wave_sum_butterfly(float x) {
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) x = x + shfl_xor(x, m);
     return x;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Raw buffer loads: a descriptor over [base, base + bytes); lanes whose offset falls outside the
+// range read zeros, which is how the kernels mask rows past a sequence's end without branches.
+// ---------------------------------------------------------------------------------------------
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr int RSRC_WORD3 = 0x00020000;  // GFX9 buffer descriptor word 3 (32-bit raw data)
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, RSRC_WORD3);
 }
 
 // ---------------------------------------------------------------------------------------------
