@@ -184,9 +184,11 @@ hipError_t ie_dequantize_kv_prefix(const ie_kv_cache* cache, const int32_t* cu_c
  * e's prefix (cache row slot_ids[e], columns [0, cu_cached[e+1] - cu_cached[e])) and to its own
  * chunk rows [cu_seqlens[e], m]. Rows of out that no tile covers are left untouched.
  * Long key ranges are split across workgroups; `workspace` (fp32 partials) must hold
- * ie_prefill_attention_workspace_size(num_tokens, num_q_heads) bytes.
+ * ie_prefill_attention_workspace_size(num_tiles, block_m, num_kv_heads) bytes, a size that
+ * depends on the current device's CU count.
  */
-size_t ie_prefill_attention_workspace_size(int64_t num_tokens, int32_t num_q_heads);
+size_t ie_prefill_attention_workspace_size(int32_t num_tiles, int32_t block_m,
+                                           int32_t num_kv_heads);
 hipError_t ie_prefill_attention(const ie_bf16* q, int64_t q_stride_tok, int64_t q_stride_head,
                                 const ie_bf16* k, int64_t k_stride_tok, int64_t k_stride_head,
                                 const ie_bf16* v, int64_t v_stride_tok, int64_t v_stride_head,

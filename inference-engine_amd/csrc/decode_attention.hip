@@ -53,26 +53,11 @@ constexpr int DA_D = 128;
 constexpr uint32_t K64 = 0x64646464u;
 constexpr float OFFSET = 1152.0f;  // fp16(0x64xx) = 1024 + byte, byte = x + 128
 
-__host__ __device__ inline int cdiv_i(int a, int b) { return (a + b - 1) / b; }
 
 int decode_target(int num_kv_heads) {
     return std::max(1, device_cu_count() * IE_DECODE_WG_PER_CU / std::max(1, num_kv_heads));
 }
 
-__device__ __forceinline__ int wave_sum_i(int x) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m, IE_WAVE);
-    return x;
-}
-__device__ __forceinline__ int wave_incl_scan_i(int x) {
-    const int lane = threadIdx.x & 63;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const int y = __shfl_up(x, d, IE_WAVE);
-        if (lane >= d) x += y;
-    }
-    return x;
-}
 
 // Piece size for this step (kernels.py:20-37); wave-uniform, every lane returns it.
 __device__ int decode_piece(const int32_t* __restrict__ cached_lens, int nd, int target) {

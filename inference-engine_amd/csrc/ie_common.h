@@ -5,7 +5,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#include "../../include/ie_attn.h"
+#include "ie_attn.h"
 
 #define IE_WAVE 64
 
@@ -55,6 +55,44 @@ __device__ __forceinline__ int dppi(int x) {
 
 __device__ __forceinline__ float shfl_xor(float x, int m) {
     return __shfl_xor(x, m, IE_WAVE);
+}
+
+// gfx950 lane swaps (VALU, no LDS round trip). permlane16_swap(x, x) returns {x of rows 0,0,2,2;
+// x of rows 1,1,3,3} (rows of 16 lanes), permlane32_swap(x, x) returns {x of the low half twice;
+// x of the high half twice}: combining the pair gives lanes i and i^16 (i^32) the same result.
+__device__ __forceinline__ float max_xor16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_xor32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum_xor32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+__host__ __device__ inline int cdiv_i(int a, int b) { return (a + b - 1) / b; }
+
+// Integer sum over the wave (every lane gets it) and inclusive prefix sum in lane order.
+__device__ __forceinline__ int wave_sum_i(int x) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m, IE_WAVE);
+    return x;
+}
+__device__ __forceinline__ int wave_incl_scan_i(int x) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int y = __shfl_up(x, d, IE_WAVE);
+        if (lane >= d) x += y;
+    }
+    return x;
 }
 
 // Sum over each group of 8 consecutive lanes; every lane of the group gets the sum.

@@ -5,7 +5,7 @@
 // [0, P), P = cu_cached[e+1] - cu_cached[e], k = q_int8 * k_scale * cal, v = q_int8 * v_scale —
 // and to its own chunk rows [cu_seqlens[e], m] (bf16 k, v as given). Scores are
 // dot(q, k) * D^-0.5 * log2(e); softmax in base 2; P is rounded to bf16 before PV;
-// out = acc / l, or 0 when l == 0.
+// out = acc / l (as acc * (1 / l)), or 0 when l == 0.
 //
 // Dequantization with the scales folded out of the tiles: int8 -> bf16 is exact, so the
 // staged prefix tiles hold the raw integers and the scales go where they cost one multiply:
@@ -15,20 +15,25 @@
 // quantities, roundings in different places, well inside bf16 attention tolerance).
 //
 // Work: sub-blocks of up to 64 packed rows of one tile of `block_m` rows (tile_start, -1 = no
-// work), both query heads of one KV head per workgroup. A sub-block's key range (prefix then
-// chunk rows up to its last row) is cut into at most PF_MAXP pieces of >= PF_MIN_PIECE_TILES
-// 64-key tiles; workgroup (sub-block * PF_MAXP + piece, kv head) takes one piece. Single-piece
-// sub-blocks write `out` directly; the others write fp32 partials (acc, m, l) that
-// prefill_combine_kernel merges (log-sum-exp). The grid depends on shapes only.
+// work), both query heads of one KV head per workgroup. Every workgroup reads the tile metadata
+// (one wave, a few hundred sub-blocks at most) and derives the same work list: the key range of
+// a (sub-block, kv head) pair (prefix tiles, then chunk tiles up to its last row) is cut into
+// pieces of about T 64-key tiles, T chosen so that the pieces fill one resident wave of
+// workgroups (2 per CU). Workgroup w runs piece w of the list (largest sub-blocks first).
+// Unsplit pieces write `out`; split pieces write a bf16 partial O (normalized) and fp32 (m, l)
+// to their slot, and prefill_combine_kernel merges them (log-sum-exp) from the split list the
+// main kernel records.
 //
-// Per 64-key tile: the workgroup stages K as [key][d] and V transposed as [d][key] in LDS, and
-// the tile's score/probability scales; wave w (query head 2hk + (w & 1), rows 32 (w >> 1)..+32)
+// Per 64-key tile: the workgroup stages K as [key][d] and V transposed as [d][key] in LDS (two
+// buffers: the next tile is staged while this one is consumed, one barrier per tile), and the
+// tile's score/probability scales; wave w (query head 2hk + (w & 1), rows 32 (w >> 1)..+32)
 // computes
 //   S^T (64 keys x 32 rows) = K . Q^T   v_mfma_f32_16x16x32_bf16, A = K from LDS, B = Q^T in VGPRs
 //   online softmax on S^T (a lane holds one row's scores for 16 keys)
 //   O^T (128 d x 32 rows) += V^T . P^T  A = V^T from LDS, B = P^T straight from the S^T
 //                                       accumulators (same key permutation in A and B).
-// The next tile's global loads are issued before the current tile's MFMA work.
+// The next tile's global loads are issued before the current tile's MFMA work, and the tile
+// three ahead is prefetched into L2.
 #include "ie_common.h"
 
 namespace ie {
@@ -42,8 +47,14 @@ constexpr int PF_BM = 64;  // packed rows per sub-block
 constexpr int PF_BN = 64;  // keys per tile
 constexpr int PF_D = 128;
 constexpr int PF_THREADS = 256;
-constexpr int PF_MAXP = 4;             // key pieces per sub-block, at most
-constexpr int PF_MIN_PIECE_TILES = 4;  // tiles per piece, at least (when split)
+#ifndef IE_PREFILL_MAXP
+#define IE_PREFILL_MAXP 8
+#endif
+#ifndef IE_PREFILL_MIN_PIECE_TILES
+#define IE_PREFILL_MIN_PIECE_TILES 2
+#endif
+constexpr int PF_MAXP = IE_PREFILL_MAXP;                        // key pieces per sub-block, at most
+constexpr int PF_MIN_PIECE_TILES = IE_PREFILL_MIN_PIECE_TILES;  // tiles per piece, at least
 constexpr float RESCALE_SLACK = 8.0f;  // log2 units
 
 // LDS layouts (bytes), padded so that every fragment address is a per-lane base plus an
@@ -86,37 +97,160 @@ struct PrefillArgs {
     ie_kv_cache c;
     uint16_t* out;
     int64_t o_st, o_sh;
-    float* part_acc;  // [N, Hq, PF_MAXP, 128]
-    float* part_ml;   // [N, Hq, PF_MAXP, 2]
-    int block_m, sub_per_tile, hq;
+    uint16_t* part_o;  // [slot][64 rows][2 heads][128] bf16: normalized partial O of split items
+    float* part_ml;    // [slot][64 rows][2 heads][2]: their (m, l)
+    int* sched;  // [0] piece size T, [1] split sub-blocks n, [2 + 2i, 3 + 2i] (sub-block, first
+                 // item) of the i-th split sub-block in launch order
+    int block_m, sub_per_tile, hq, hkv;
+    int nsb;   // sub-blocks: num_tiles * sub_per_tile
+    int grid;  // partial slots (resident main-kernel workgroups); split items are numbered below it
     float qk_scale;  // D^-0.5 * log2(e)
 };
 
 __device__ __forceinline__ int uni(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
+// Sub-block `sb` (tile sb / sub_per_tile, 64-row slice sb % sub_per_tile) as seen by the calling
+// lane: rows [r0, r1) of the entry starting at packed row seq_start, its cache slot and prefix
+// length P, and its key tiles: cdiv(P, 64) prefix tiles then cdiv(r1 - seq_start, 64) chunk
+// tiles. ntiles = 0 when the sub-block has no rows.
+struct SbInfo {
+    int ntiles, r0, r1, seq_start, P, slot;
+};
+__device__ __forceinline__ SbInfo sb_info(const PrefillArgs& a, int sb) {
+    SbInfo z = {0, 0, 0, 0, 0, 0};
+    if (sb < 0 || sb >= a.nsb) return z;
+    const int tile = sb / a.sub_per_tile, sub = sb - tile * a.sub_per_tile;
+    const int row_start = a.tile_start[tile];
+    if (row_start < 0) return z;
+    const int seq = a.seq_ids[row_start];
+    const int seq_start = a.cu_seqlens[seq], seq_end = a.cu_seqlens[seq + 1];
+    const int c0 = a.cu_cached[seq], c1 = a.cu_cached[seq + 1], slot = a.slot_ids[seq];
+    const int r0 = row_start + sub * PF_BM;
+    const int r1 = min(min(r0 + PF_BM, row_start + a.block_m), seq_end);
+    if (r0 >= r1) return z;
+    z.P = c1 - c0;
+    z.ntiles = cdiv_i(z.P, PF_BN) + cdiv_i(r1 - seq_start, PF_BN);
+    z.r0 = r0;
+    z.r1 = r1;
+    z.seq_start = seq_start;
+    z.slot = slot;
+    return z;
+}
+
+__device__ __forceinline__ int piece_count(int ntiles, int T) {
+    return min(PF_MAXP, max(1, cdiv_i(ntiles, T)));
+}
+
+// The launch's work list, computed identically by every wave from the tile metadata:
+//  * piece size T (tiles): a (sub-block, kv head) pair with n tiles becomes cdiv(n, T) items (at
+//    most PF_MAXP). T is the smallest size for which the items fit the partial slots even in the
+//    worst rounding, sum(n / T + 1) * Hkv <= slots, so every split item owns a slot. With more
+//    (sub-block, head) pairs than slots there is enough parallelism without splitting.
+//  * items in launch order: sub-blocks from last to first (later sub-blocks of a sequence see
+//    more keys), then piece, then kv head.
+// schedule(target) finds the sub-block holding item `target`, the offset inside it and the
+// number of items before the sub-block. Sub-block sizes stay in registers between the two passes
+// for the first PF_SCHED_CHUNKS * 64 sub-blocks and are reloaded beyond that.
+constexpr int PF_SCHED_CHUNKS = 4;
+
 struct SubBlock {
     int r0, r1, seq_start, P, slot, npt, nct, ntiles, npieces;
 };
 
-// Rows and keys of sub-block `sb` (tile sb / sub_per_tile); false if it has no rows. Its keys
-// are npt prefix tiles covering [0, P) and then nct chunk tiles covering chunk rows
-// [seq_start, r1); a tile never mixes the two.
-__device__ __forceinline__ bool sub_block(const PrefillArgs& a, int sb, SubBlock& s) {
-    const int tile = sb / a.sub_per_tile, sub = sb - tile * a.sub_per_tile;
-    const int row_start = uni(a.tile_start[tile]);
-    if (row_start < 0) return false;
-    const int seq = uni(a.seq_ids[row_start]);
-    s.seq_start = uni(a.cu_seqlens[seq]);
-    const int seq_end = uni(a.cu_seqlens[seq + 1]);
-    s.r0 = row_start + sub * PF_BM;
-    s.r1 = min(min(s.r0 + PF_BM, row_start + a.block_m), seq_end);
-    if (s.r0 >= s.r1) return false;
-    s.P = uni(a.cu_cached[seq + 1] - a.cu_cached[seq]);
-    s.slot = uni(a.slot_ids[seq]);
-    s.npt = (s.P + PF_BN - 1) / PF_BN;
-    s.nct = (s.r1 - s.seq_start + PF_BN - 1) / PF_BN;
+__device__ __forceinline__ void fill_sub_block(SubBlock& s, int r0, int r1, int seq_start, int P,
+                                               int slot, int T) {
+    s.r0 = r0;
+    s.r1 = r1;
+    s.seq_start = seq_start;
+    s.P = P;
+    s.slot = slot;
+    s.npt = cdiv_i(P, PF_BN);
+    s.nct = cdiv_i(r1 - seq_start, PF_BN);
     s.ntiles = s.npt + s.nct;
-    s.npieces = min(PF_MAXP, max(1, s.ntiles / PF_MIN_PIECE_TILES));
+    s.npieces = piece_count(s.ntiles, T);
+}
+
+struct Loc {
+    int sb, off, item_base, T;
+    int nsplit;       // split sub-blocks in the launch
+    int split_index;  // rank of sub-block sb among them (launch order)
+    int found;
+    SubBlock s;       // sub-block sb
+};
+
+// One wave's pass over the tile metadata (every lane of the wave returns the same Loc).
+__device__ Loc schedule(const PrefillArgs& a, int target) {
+    const int lane = threadIdx.x & 63;
+    const int nchunks = cdiv_i(a.nsb, IE_WAVE);
+    auto sb_of = [&](int c) { return a.nsb - 1 - (c * IE_WAVE + lane); };
+    SbInfo zc[PF_SCHED_CHUNKS];
+    int tot = 0, nonempty = 0;
+#pragma unroll
+    for (int c = 0; c < PF_SCHED_CHUNKS; ++c) {
+        zc[c] = sb_info(a, c < nchunks ? sb_of(c) : -1);
+        tot += zc[c].ntiles;
+        nonempty += zc[c].ntiles > 0;
+    }
+    for (int c = PF_SCHED_CHUNKS; c < nchunks; ++c) {
+        const int nt = sb_info(a, sb_of(c)).ntiles;
+        tot += nt;
+        nonempty += nt > 0;
+    }
+    tot = uni(wave_sum_i(tot));
+    nonempty = uni(wave_sum_i(nonempty));
+    const int spare = a.grid - nonempty * a.hkv;
+    Loc L;
+    L.T = spare <= 0 ? (1 << 28) : max(PF_MIN_PIECE_TILES, cdiv_i(tot * a.hkv, spare));
+    L.found = 0;
+    L.sb = L.off = L.item_base = L.split_index = 0;
+    {
+        int ns = 0;
+#pragma unroll
+        for (int c = 0; c < PF_SCHED_CHUNKS; ++c)
+            ns += zc[c].ntiles > 0 && piece_count(zc[c].ntiles, L.T) > 1;
+        for (int c = PF_SCHED_CHUNKS; c < nchunks; ++c) {
+            const int nt = sb_info(a, sb_of(c)).ntiles;
+            ns += nt > 0 && piece_count(nt, L.T) > 1;
+        }
+        L.nsplit = uni(wave_sum_i(ns));
+    }
+    int items_before = 0, split_before = 0;
+    auto visit = [&](int c, const SbInfo& z) {
+        const int np = z.ntiles > 0 ? piece_count(z.ntiles, L.T) : 0;
+        const int items = np * a.hkv;
+        const int incl = wave_incl_scan_i(items) + items_before;
+        const int sincl = wave_incl_scan_i(np > 1) + split_before;
+        const unsigned long long hit = __ballot(target < incl && target >= incl - items);
+        if (hit) {
+            const int src = __builtin_ctzll(hit);  // the same lane in every wave: uniform
+            auto from = [&](int x) { return uni(__shfl(x, src, IE_WAVE)); };
+            L.sb = from(sb_of(c));
+            L.item_base = from(incl - items);
+            L.off = target - L.item_base;
+            L.split_index = from(sincl - (np > 1));
+            fill_sub_block(L.s, from(z.r0), from(z.r1), from(z.seq_start), from(z.P),
+                           from(z.slot), L.T);
+            L.found = 1;
+        }
+        items_before = uni(__shfl(incl, 63, IE_WAVE));
+        split_before = uni(__shfl(sincl, 63, IE_WAVE));
+        return L.found != 0;
+    };
+#pragma unroll
+    for (int c = 0; c < PF_SCHED_CHUNKS; ++c)
+        if (c < nchunks && visit(c, zc[c])) return L;
+    for (int c = PF_SCHED_CHUNKS; c < nchunks; ++c)
+        if (visit(c, sb_info(a, sb_of(c)))) return L;
+    return L;
+}
+
+// Rows and keys of sub-block `sb` (uniform across the workgroup); false if it has no rows. Its
+// keys are npt prefix tiles covering [0, P) and then nct chunk tiles covering chunk rows
+// [seq_start, r1); a tile never mixes the two.
+__device__ __forceinline__ bool sub_block(const PrefillArgs& a, int sb, int T, SubBlock& s) {
+    const SbInfo z = sb_info(a, sb);
+    if (uni(z.ntiles) == 0) return false;
+    fill_sub_block(s, uni(z.r0), uni(z.r1), uni(z.seq_start), uni(z.P), uni(z.slot), T);
     return true;
 }
 
@@ -124,8 +258,8 @@ __device__ __forceinline__ bool sub_block(const PrefillArgs& a, int sb, SubBlock
 struct TileRegs {
     uint32_t kw[16];    // K: key tid>>2, channels [32 (tid&3), +32): int8 (8 words) or bf16
     uint32_t vw[4][4];  // V: keys 4 (tid&15) + u, channels [8 (tid>>4), +8): int8 (2) or bf16 (4)
-    float kscale, kbias, vscale;  // prefix tiles, key tid (threads < 64): score scale, score
-                                  // bias (-inf past P), P scale
+    float kscale, kbias, vscale;  // prefix tiles, key tid & 63: k_scale, score bias (-inf past P),
+                                  // v_scale
 };
 
 // Buffer descriptors of one (sub-block, kv head): prefix K/V rows (128 B each, P rows) and scales
@@ -149,8 +283,7 @@ __device__ __forceinline__ float ldf(rsrc_t r, int off) {
 // Otherwise chunk keys: packed rows seq_start + [kbase, kbase + 64) (bf16; zeros at or past the
 // sub-block's last row). No branches: the buffer ranges do the masking.
 template <bool PREFIX>
-__device__ __forceinline__ void load_tile(TileRegs& r, const TileSrc& src, int kbase, int P,
-                                          float qk_scale) {
+__device__ __forceinline__ void load_tile(TileRegs& r, const TileSrc& src, int kbase, int P) {
     const int tid = threadIdx.x;
     {
         const int kk = kbase + (tid >> 2), q4 = tid & 3;
@@ -182,11 +315,11 @@ __device__ __forceinline__ void load_tile(TileRegs& r, const TileSrc& src, int k
             }
         }
     }
-    if (PREFIX && tid < PF_BN) {  // wave 0
-        const int kk = kbase + tid;
-        r.kscale = ldf(src.pks, 4 * kk) * qk_scale;
-        r.kbias = kk < P ? 0.f : -INFINITY;
+    if (PREFIX) {  // every wave loads the tile's 64 key scales; wave 0 stages them
+        const int kk = kbase + (tid & (PF_BN - 1));
+        r.kscale = ldf(src.pks, 4 * kk);
         r.vscale = ldf(src.pvs, 4 * kk);
+        r.kbias = kk < P ? 0.f : -INFINITY;
     }
 }
 
@@ -194,7 +327,8 @@ __device__ __forceinline__ void load_tile(TileRegs& r, const TileSrc& src, int k
 // exactly), and for prefix tiles the per-key scales.
 template <bool PREFIX>
 __device__ __forceinline__ void stage_tile(const TileRegs& r, uint8_t* s_k, uint8_t* s_vt,
-                                           float* s_ksc, float* s_kb, float* s_vsc) {
+                                           float* s_ksc, float* s_kb, float* s_vsc,
+                                           float qk_scale) {
     const int tid = threadIdx.x;
     {
         const int key = tid >> 2, q4 = tid & 3;
@@ -232,7 +366,7 @@ __device__ __forceinline__ void stage_tile(const TileRegs& r, uint8_t* s_k, uint
         }
     }
     if (PREFIX && tid < PF_BN) {
-        s_ksc[tid] = r.kscale;
+        s_ksc[tid] = r.kscale * qk_scale;
         s_kb[tid] = r.kbias;
         s_vsc[tid] = r.vscale;
     }
@@ -245,73 +379,101 @@ struct WaveState {
     float m[2], l[2];
 };
 
-// MFMA + softmax work of one staged 64-key tile for one wave. PREFIX tiles: scores scaled per
-// key, P scaled per key, keys past P masked (their scale is 0 and they are set to -inf).
-// Chunk tiles: scores scaled by qk_scale, causal mask (chunk key c visible to row m iff
-// seq_start + c <= m) and the range mask c < r1 - seq_start.
-template <bool PREFIX>
+// Tile kinds: prefix tiles (scores scaled per key, P scaled by v_scale per key) that are full or
+// hold keys past P (masked through the staged -inf bias); chunk tiles that every row of the wave
+// sees whole, or that cross the causal diagonal / the sub-block's last row (masked per key).
+enum : int { TILE_PREFIX = 0, TILE_PREFIX_PARTIAL = 1, TILE_CHUNK = 2, TILE_CHUNK_DIAG = 3 };
+
+// MFMA + softmax work of one staged 64-key tile for one wave. Chunk key c is visible to row m
+// iff seq_start + c <= m and c < r1 - seq_start (lim0 / lim1: last visible key of the lane's
+// two rows).
+template <int KIND>
 __device__ __forceinline__ void tile_compute(WaveState& w, const bf16x8 (&qf)[2][4],
                                              const uint8_t* s_k, const uint8_t* s_vt,
                                              const float* s_ksc, const float* s_kb,
                                              const float* s_vsc, int kbase, int lim0, int lim1,
                                              float qk_scale, int l16, int g) {
+    constexpr bool PREFIX = KIND == TILE_PREFIX || KIND == TILE_PREFIX_PARTIAL;
     // ---- S^T = K . Q^T (64 keys x 32 rows) ----
+    // Fragment reads run one 16-key step ahead of the MFMAs that consume them.
     const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
     f32x4 st[4][2];
     const uint8_t* kfrag = s_k + ks_off(l16, g);
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-        __builtin_amdgcn_sched_barrier(0);  // bound live fragment registers per step
-        bf16x8 kf[4];
+    auto read_k = [&](bf16x8 (&kf)[4], int mt) {
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks)
             kf[ks] = __builtin_bit_cast(
                 bf16x8, *reinterpret_cast<const u32x4*>(kfrag + 16 * mt * KS_STRIDE + 64 * ks));
+    };
+    bf16x8 kf[2][4];
+    read_k(kf[0], 0);
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+        __builtin_amdgcn_sched_barrier(0);
+        if (mt < 3) read_k(kf[(mt + 1) & 1], mt + 1);
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) {
-            f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[0], qf[nt][0], zero4, 0, 0, 0);
+            f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[mt & 1][0], qf[nt][0], zero4, 0, 0, 0);
 #pragma unroll
             for (int ks = 1; ks < 4; ++ks)
-                c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[ks], qf[nt][ks], c, 0, 0, 0);
+                c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[mt & 1][ks], qf[nt][ks], c, 0, 0, 0);
             st[mt][nt] = c;
         }
     }
+    // the first V^T fragments are read while the softmax runs
+    const uint8_t* vfrag = s_vt + l16 * VT_STRIDE + 16 * g;
+    auto read_v = [&](bf16x8 (&vf)[2], int mt) {
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2)
+            vf[s2] = __builtin_bit_cast(
+                bf16x8, *reinterpret_cast<const u32x4*>(vfrag + 16 * mt * VT_STRIDE + 64 * s2));
+    };
+    bf16x8 vf[2][2];
+    __builtin_amdgcn_sched_barrier(0);
+    read_v(vf[0], 0);
     // ---- scale, mask, online softmax (base 2) ----
+    // Scores are formed relative to the running max m in the scaling fma. The running max is lazy:
+    // it moves only when a row's tile max exceeds it by more than RESCALE_SLACK (or on the row's
+    // first visible key), so probabilities stay <= 2^RESCALE_SLACK; then the wave shifts its scores
+    // once more and rescales the accumulators.
     uint32_t pfrag[2][2][4];  // [32-key step][row tile] bf16x8 as 4 words
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
         __builtin_amdgcn_sched_barrier(0);
-        const int lim = nt ? lim1 : lim0;  // chunk tiles: last visible key index of this row
+        const int lim = nt ? lim1 : lim0;
+        const float mold = w.m[nt];
+        const float nmb = mold == -INFINITY ? 0.f : -mold;
         float mx = -INFINITY;
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) {
-            f32x4 ksv = {qk_scale, qk_scale, qk_scale, qk_scale}, kbv = {0.f, 0.f, 0.f, 0.f};
-            if (PREFIX) {
-                ksv = *reinterpret_cast<const f32x4*>(s_ksc + 16 * mt + 4 * g);
-                kbv = *reinterpret_cast<const f32x4*>(s_kb + 16 * mt + 4 * g);
-            }
+            f32x4 ksv = {qk_scale, qk_scale, qk_scale, qk_scale};
+            if (PREFIX) ksv = *reinterpret_cast<const f32x4*>(s_ksc + 16 * mt + 4 * g);
+            f32x4 kbv = zero4;
+            if (KIND == TILE_PREFIX_PARTIAL) kbv = *reinterpret_cast<const f32x4*>(s_kb + 16 * mt + 4 * g);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                float x;
-                if (PREFIX) {
-                    x = __builtin_fmaf(st[mt][nt][i], ksv[i], kbv[i]);  // -inf past P
-                } else {
-                    const int kk = kbase + 16 * mt + 4 * g + i;
-                    x = kk <= lim ? st[mt][nt][i] * ksv[i] : -INFINITY;
-                }
+                float x = __builtin_fmaf(st[mt][nt][i], ksv[i], nmb);
+                if (KIND == TILE_PREFIX_PARTIAL) x += kbv[i];  // -inf past P
+                if (KIND == TILE_CHUNK_DIAG) x = kbase + 16 * mt + 4 * g + i <= lim ? x : -INFINITY;
                 st[mt][nt][i] = x;
                 mx = fmaxf(mx, x);
             }
         }
-        mx = fmaxf(mx, shfl_xor(mx, 16));
-        mx = fmaxf(mx, shfl_xor(mx, 32));
-        // Lazy max: the running max only moves when the tile's max exceeds it by more than
-        // 2^RESCALE_SLACK, so probabilities stay <= 2^8 and the accumulators are rescaled rarely.
-        const float mold = w.m[nt];
-        const float mnew = mx > mold + RESCALE_SLACK ? mx : mold;
-        const float msafe = mnew == -INFINITY ? 0.f : mnew;
-        const float alpha = __builtin_amdgcn_exp2f(mold - msafe);  // 1 if unchanged, 0 from -inf
-        w.m[nt] = mnew;
+        mx = max_xor32(max_xor16(mx));
+        const bool move = mx != -INFINITY && (mold == -INFINITY || mx > RESCALE_SLACK);
+        const float shift = move ? mx : 0.f;
+        if (__ballot(move)) {
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) st[mt][nt] -= shift;
+            const float mnew = move ? -nmb + shift : mold;
+            const float alpha = __builtin_amdgcn_exp2f(mold - mnew);  // 1 unless moved; 0 from -inf
+            w.m[nt] = mnew;
+            w.l[nt] *= alpha;
+            if (__ballot(move && mold != -INFINITY)) {  // accumulators are 0 before any key
+#pragma unroll
+                for (int mt = 0; mt < 8; ++mt) w.acc[mt][nt] *= alpha;
+            }
+        }
         float lsum = 0.f;
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) {
@@ -319,35 +481,29 @@ __device__ __forceinline__ void tile_compute(WaveState& w, const bf16x8 (&qf)[2]
             if (PREFIX) vsv = *reinterpret_cast<const f32x4*>(s_vsc + 16 * mt + 4 * g);
 #pragma unroll
             for (int i = 0; i < 4; i += 2) {
-                const float p0 = __builtin_amdgcn_exp2f(st[mt][nt][i] - msafe);
-                const float p1 = __builtin_amdgcn_exp2f(st[mt][nt][i + 1] - msafe);
+                const float p0 = __builtin_amdgcn_exp2f(st[mt][nt][i]);
+                const float p1 = __builtin_amdgcn_exp2f(st[mt][nt][i + 1]);
                 lsum += p0 + p1;
                 pfrag[mt >> 1][nt][(mt & 1) * 2 + i / 2] =
                     PREFIX ? pack_bf16x2(p0 * vsv[i], p1 * vsv[i + 1]) : pack_bf16x2(p0, p1);
             }
         }
-        w.l[nt] = w.l[nt] * alpha + lsum;
-        if (__ballot(mnew != mold && mold != -INFINITY)) {  // accumulators are 0 before any key
-#pragma unroll
-            for (int mt = 0; mt < 8; ++mt) w.acc[mt][nt] *= alpha;
-        }
+        w.l[nt] += lsum;
     }
     // ---- O^T += V^T . P^T ----
-    const uint8_t* vfrag = s_vt + l16 * VT_STRIDE + 16 * g;
 #pragma unroll
     for (int mt = 0; mt < 8; ++mt) {
         __builtin_amdgcn_sched_barrier(0);
+        if (mt < 7) read_v(vf[(mt + 1) & 1], mt + 1);
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
-            const bf16x8 vf = __builtin_bit_cast(
-                bf16x8, *reinterpret_cast<const u32x4*>(vfrag + 16 * mt * VT_STRIDE + 64 * s2));
 #pragma unroll
             for (int nt = 0; nt < 2; ++nt) {
                 const bf16x8 pfv = __builtin_bit_cast(
                     bf16x8, u32x4{pfrag[s2][nt][0], pfrag[s2][nt][1], pfrag[s2][nt][2],
                                   pfrag[s2][nt][3]});
-                w.acc[mt][nt] =
-                    __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pfv, w.acc[mt][nt], 0, 0, 0);
+                w.acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[mt & 1][s2], pfv,
+                                                                       w.acc[mt][nt], 0, 0, 0);
             }
         }
     }
@@ -374,6 +530,9 @@ __device__ __forceinline__ void load_q(bf16x8 (&qf)[2][4], const PrefillArgs& a,
                           pack_bf16x2(bf16lo(w.z) * c1[0], bf16hi(w.z) * c1[1]),
                           pack_bf16x2(bf16lo(w.w) * c1[2], bf16hi(w.w) * c1[3])};
             }
+            // a register use here makes the compiler wait for the Q loads now, not inside the
+            // tile loop where the wait would also cover the next tile's prefetch
+            asm volatile("" : "+v"(w));
             qf[nt][ks] = __builtin_bit_cast(bf16x8, w);
         }
     }
@@ -383,12 +542,9 @@ __device__ __forceinline__ void load_q(bf16x8 (&qf)[2][4], const PrefillArgs& a,
 #define IE_PREFILL_WG_PER_CU 2
 #endif
 
-__global__ __launch_bounds__(PF_THREADS, IE_PREFILL_WG_PER_CU) void prefill_attention_kernel(
-    PrefillArgs a) {
-    const int sb = blockIdx.x / PF_MAXP, piece = blockIdx.x % PF_MAXP;
-    const int hk = blockIdx.y;
-    SubBlock s;
-    if (!sub_block(a, sb, s) || piece >= s.npieces) return;
+// One work item: tiles [kt_begin, kt_end) of piece `piece` of sub-block s for kv head hk.
+__device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBlock& s, int hk,
+                                             int piece, int item) {
     const int kt_begin = piece * s.ntiles / s.npieces;
     const int kt_end = (piece + 1) * s.ntiles / s.npieces;
 
@@ -427,13 +583,30 @@ __global__ __launch_bounds__(PF_THREADS, IE_PREFILL_WG_PER_CU) void prefill_atte
     const int lim0 = min(rowA - s.seq_start, clim), lim1 = min(rowB - s.seq_start, clim);
 
     // tile kt: prefix tile kt (keys [64kt, ..)) if kt < npt, else chunk tile kt - npt
+    // L2 prefetch of tile kt2 (no-op past the piece: the offsets fall outside the buffer range):
+    // one dword per lane and wave touches every 128-byte line of the tile's K rows, V rows and
+    // scales. The result is only consumed (never used) so the data lands in L2 for the real load.
+    const int wave_u = uni(wave);
+    auto prefetch = [&](int kt2) -> uint32_t {
+        const bool pre = kt2 < s.npt;
+        const int row = (pre ? kt2 : kt2 - s.npt) * PF_BN + lane;
+        const rsrc_t r = kt2 >= kt_end ? src.pks
+                       : pre ? (wave_u == 0 ? src.pk : wave_u == 1 ? src.pv : wave_u == 2 ? src.pks : src.pvs)
+                             : (wave_u < 2 ? src.ck : src.cv);
+        const int off = kt2 >= kt_end ? -1
+                      : pre ? row * (wave_u < 2 ? PF_D : 4)
+                            : row * (wave_u < 2 ? src.ck_stride : src.cv_stride) + 128 * (wave_u & 1);
+        return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+    };
+    auto consume = [](uint32_t x) { asm volatile("" ::"v"(x)); };
+
     auto load = [&](TileRegs& r, int kt) {
-        if (kt < s.npt) load_tile<true>(r, src, kt * PF_BN, s.P, a.qk_scale);
-        else load_tile<false>(r, src, (kt - s.npt) * PF_BN, s.P, a.qk_scale);
+        if (kt < s.npt) load_tile<true>(r, src, kt * PF_BN, s.P);
+        else load_tile<false>(r, src, (kt - s.npt) * PF_BN, s.P);
     };
     auto stage = [&](const TileRegs& r, int kt, int buf) {
-        if (kt < s.npt) stage_tile<true>(r, s_k[buf], s_vt[buf], s_ksc[buf], s_kb[buf], s_vsc[buf]);
-        else stage_tile<false>(r, s_k[buf], s_vt[buf], s_ksc[buf], s_kb[buf], s_vsc[buf]);
+        if (kt < s.npt) stage_tile<true>(r, s_k[buf], s_vt[buf], s_ksc[buf], s_kb[buf], s_vsc[buf], a.qk_scale);
+        else stage_tile<false>(r, s_k[buf], s_vt[buf], s_ksc[buf], s_kb[buf], s_vsc[buf], a.qk_scale);
     };
 
     WaveState ws;
@@ -444,37 +617,68 @@ __global__ __launch_bounds__(PF_THREADS, IE_PREFILL_WG_PER_CU) void prefill_atte
     ws.m[0] = ws.m[1] = -INFINITY;
     ws.l[0] = ws.l[1] = 0.f;
 
+    // the first tile's loads and the Q loads are in flight together
     TileRegs pf;
     load(pf, kt_begin);
-    stage(pf, kt_begin, 0);
+    uint32_t pfa = prefetch(kt_begin + 1), pfb = prefetch(kt_begin + 2);
     bf16x8 qf[2][4];
     int kt = kt_begin;
     const int prefix_end = min(kt_end, s.npt);
+    if (kt < prefix_end) load_q<true>(qf, a, wr0, s.r1, h, cal, l16, g);
+    else load_q<false>(qf, a, wr0, s.r1, h, cal, l16, g);
+    stage(pf, kt_begin, 0);
     if (kt < prefix_end) {
-        load_q<true>(qf, a, wr0, s.r1, h, cal, l16, g);
         __syncthreads();
-        for (; kt < prefix_end; ++kt) {
+        // prefix tiles followed by another prefix tile
+        for (; kt < prefix_end - 1; ++kt) {
             const int buf = (kt - kt_begin) & 1;
-            const bool has_next = kt + 1 < kt_end;
-            if (has_next) load(pf, kt + 1);  // in flight during this tile's MFMA work
-            tile_compute<true>(ws, qf, s_k[buf], s_vt[buf], s_ksc[buf], s_kb[buf], s_vsc[buf],
-                               kt * PF_BN, 0, 0, a.qk_scale, l16, g);
-            if (has_next) stage(pf, kt + 1, buf ^ 1);
+            load_tile<true>(pf, src, (kt + 1) * PF_BN, s.P);  // in flight during the MFMAs
+            consume(pfa);
+            pfa = pfb;
+            pfb = prefetch(kt + 3);
+            tile_compute<TILE_PREFIX>(ws, qf, s_k[buf], s_vt[buf], s_ksc[buf], s_kb[buf],
+                                      s_vsc[buf], kt * PF_BN, 0, 0, a.qk_scale, l16, g);
+            stage_tile<true>(pf, s_k[buf ^ 1], s_vt[buf ^ 1], s_ksc[buf ^ 1], s_kb[buf ^ 1],
+                             s_vsc[buf ^ 1], a.qk_scale);
             __syncthreads();  // next buffer staged; this buffer free for tile kt + 2
         }
+        // last prefix tile of the piece: followed by the first chunk tile, or by nothing
+        const int buf = (kt - kt_begin) & 1;
+        const bool has_next = kt + 1 < kt_end;
+        if (has_next) load_tile<false>(pf, src, 0, s.P);
+        consume(pfa);
+        pfa = pfb;
+        pfb = prefetch(kt + 3);
+        // the only prefix tile of the piece that can hold keys past P (one instance: a second
+        // one for full tiles here costs registers)
+        tile_compute<TILE_PREFIX_PARTIAL>(ws, qf, s_k[buf], s_vt[buf], s_ksc[buf], s_kb[buf],
+                                          s_vsc[buf], kt * PF_BN, 0, 0, a.qk_scale, l16, g);
+        if (has_next)
+            stage_tile<false>(pf, s_k[buf ^ 1], s_vt[buf ^ 1], s_ksc[buf ^ 1], s_kb[buf ^ 1],
+                              s_vsc[buf ^ 1], a.qk_scale);
+        __syncthreads();
+        ++kt;
     }
     if (kt < kt_end) {
-        load_q<false>(qf, a, wr0, s.r1, h, cal, l16, g);
         if (kt == kt_begin) __syncthreads();
+        else load_q<false>(qf, a, wr0, s.r1, h, cal, l16, g);
         for (; kt < kt_end; ++kt) {
             const int buf = (kt - kt_begin) & 1;
             const bool has_next = kt + 1 < kt_end;
             const int kc = (kt - s.npt) * PF_BN;
-            if (has_next) load_tile<false>(pf, src, kc + PF_BN, s.P, a.qk_scale);
-            tile_compute<false>(ws, qf, s_k[buf], s_vt[buf], s_ksc[buf], s_kb[buf], s_vsc[buf],
-                                kc, lim0, lim1, a.qk_scale, l16, g);
+            if (has_next) load_tile<false>(pf, src, kc + PF_BN, s.P);
+            consume(pfa);
+            pfa = pfb;
+            pfb = prefetch(kt + 3);
+            // the whole tile is visible to every row of this wave: no per-key mask
+            if (kc + PF_BN - 1 <= min(wr0 - s.seq_start, clim))
+                tile_compute<TILE_CHUNK>(ws, qf, s_k[buf], s_vt[buf], s_ksc[buf], s_kb[buf],
+                                         s_vsc[buf], kc, lim0, lim1, a.qk_scale, l16, g);
+            else
+                tile_compute<TILE_CHUNK_DIAG>(ws, qf, s_k[buf], s_vt[buf], s_ksc[buf], s_kb[buf],
+                                              s_vsc[buf], kc, lim0, lim1, a.qk_scale, l16, g);
             if (has_next) stage_tile<false>(pf, s_k[buf ^ 1], s_vt[buf ^ 1], s_ksc[buf ^ 1],
-                                            s_kb[buf ^ 1], s_vsc[buf ^ 1]);
+                                            s_kb[buf ^ 1], s_vsc[buf ^ 1], a.qk_scale);
             __syncthreads();
         }
     }
@@ -483,87 +687,152 @@ __global__ __launch_bounds__(PF_THREADS, IE_PREFILL_WG_PER_CU) void prefill_atte
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
         float l = ws.l[nt];
-        l += shfl_xor(l, 16);
-        l += shfl_xor(l, 32);
+        l = sum_xor32(sum_xor16(l));
         const int row = wr0 + 16 * nt + l16;
         if (row >= s.r1) continue;
+        const float rl = l != 0.f ? 1.f / l : 0.f;
         if (s.npieces == 1) {
             uint16_t* o = a.out + row * a.o_st + h * a.o_sh;
 #pragma unroll
             for (int mt = 0; mt < 8; ++mt) {
                 const f32x4 x = ws.acc[mt][nt];
-                float y[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) y[i] = l != 0.f ? x[i] / l : 0.f;
                 *reinterpret_cast<u32x2*>(o + 16 * mt + 4 * g) =
-                    u32x2{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
+                    u32x2{pack_bf16x2(x[0] * rl, x[1] * rl), pack_bf16x2(x[2] * rl, x[3] * rl)};
             }
-        } else {
-            const int64_t prow = ((int64_t)row * a.hq + h) * PF_MAXP + piece;
+        } else {  // normalized partial O in bf16 (a weighted mean of V rows) and fp32 (m, l)
+            const int64_t prow = ((int64_t)item * PF_BM + (row - s.r0)) * 2 + (wave & 1);
 #pragma unroll
-            for (int mt = 0; mt < 8; ++mt)
-                *reinterpret_cast<f32x4*>(a.part_acc + prow * PF_D + 16 * mt + 4 * g) = ws.acc[mt][nt];
+            for (int mt = 0; mt < 8; ++mt) {
+                const f32x4 x = ws.acc[mt][nt];
+                *reinterpret_cast<u32x2*>(a.part_o + prow * PF_D + 16 * mt + 4 * g) =
+                    u32x2{pack_bf16x2(x[0] * rl, x[1] * rl), pack_bf16x2(x[2] * rl, x[3] * rl)};
+            }
             if (g == 0)
                 *reinterpret_cast<float2*>(a.part_ml + prow * 2) = make_float2(ws.m[nt], l);
         }
     }
 }
 
-constexpr int PF_COMB_SPLIT = 16;  // combine workgroups per sub-block (8 (row, head) pairs each)
 
-// grid (num_tiles * sub_per_tile * PF_COMB_SPLIT, Hkv), block 256: merges the pieces of split
-// sub-blocks (log-sum-exp, base 2). 32 threads per (row, query head), 4 channels each; every
-// thread issues all of its loads up front.
-__global__ __launch_bounds__(PF_THREADS) void prefill_combine_kernel(PrefillArgs a) {
-    const int hk = blockIdx.y;
-    SubBlock s;
-    if (!sub_block(a, blockIdx.x / PF_COMB_SPLIT, s) || s.npieces <= 1) return;
-    const int tid = threadIdx.x;
-    const int pair = (blockIdx.x % PF_COMB_SPLIT) * 8 + (tid >> 5);  // 0..127
-    const int row = s.r0 + (pair >> 1);
-    if (row >= s.r1) return;
-    const int h = 2 * hk + (pair & 1);
-    const int d = 4 * (tid & 31);
-    const int64_t prow = ((int64_t)row * a.hq + h) * PF_MAXP;
-    float2 ml[PF_MAXP];
-    f32x4 acc[PF_MAXP];
-#pragma unroll
-    for (int p = 0; p < PF_MAXP; ++p) {
-        ml[p] = make_float2(-INFINITY, 0.f);
-        acc[p] = f32x4{0.f, 0.f, 0.f, 0.f};
-        if (p < s.npieces) {
-            ml[p] = *reinterpret_cast<const float2*>(a.part_ml + (prow + p) * 2);
-            acc[p] = *reinterpret_cast<const f32x4*>(a.part_acc + (prow + p) * PF_D + d);
-        }
+// grid (max(slots, sub-blocks * Hkv)), block 256: workgroup w runs item w of the launch's item
+// list (there are never more items than that), or nothing.
+__global__ __launch_bounds__(PF_THREADS, IE_PREFILL_WG_PER_CU) void prefill_attention_kernel(
+    PrefillArgs a) {
+    // wave 0 reads the tile metadata and hands the workgroup its item through LDS
+    __shared__ Loc s_loc;
+    if (threadIdx.x < IE_WAVE) {
+        const Loc l = schedule(a, blockIdx.x);
+        if (threadIdx.x == 0) s_loc = l;
     }
-    float mx = -INFINITY;
+    __syncthreads();
+    Loc loc;
+    {
+        const int* src = reinterpret_cast<const int*>(&s_loc);
+        int* dst = reinterpret_cast<int*>(&loc);
 #pragma unroll
-    for (int p = 0; p < PF_MAXP; ++p) mx = fmaxf(mx, ml[p].x);
-    f32x4 num = {0.f, 0.f, 0.f, 0.f};
-    float den = 0.f;
-#pragma unroll
-    for (int p = 0; p < PF_MAXP; ++p) {
-        const float w = ml[p].x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ml[p].x - mx);
-        num += acc[p] * w;
-        den += ml[p].y * w;
+        for (int i = 0; i < (int)(sizeof(Loc) / sizeof(int)); ++i) dst[i] = uni(src[i]);
     }
-    float y[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) y[i] = den != 0.f ? num[i] / den : 0.f;
-    *reinterpret_cast<u32x2*>(a.out + row * a.o_st + h * a.o_sh + d) =
-        u32x2{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        a.sched[0] = loc.T;
+        a.sched[1] = loc.nsplit;
+    }
+    if (!loc.found) return;
+    const SubBlock& s = loc.s;
+    if (loc.off == 0 && s.npieces > 1 && threadIdx.x == 0) {
+        a.sched[2 + 2 * loc.split_index] = loc.sb;
+        a.sched[3 + 2 * loc.split_index] = loc.item_base;
+    }
+    prefill_item(a, s, loc.off % a.hkv, loc.off / a.hkv, blockIdx.x);
 }
 
-static size_t prefill_workspace_bytes(int64_t num_tokens, int hq) {
-    return (size_t)num_tokens * hq * PF_MAXP * (PF_D + 2) * sizeof(float);
+constexpr int PF_COMB_GROUPS = 4;  // combine units per (split sub-block, kv head): 32 pairs each
+
+// grid (slots), block 256: merges the pieces of split sub-blocks (log-sum-exp, base 2) from the
+// list the main kernel recorded. Unit u: split sub-block u / (Hkv * 4), kv head, and 32 of its
+// 128 (row, query head) pairs; 8 threads per pair, 16 channels each, all loads issued up front.
+__global__ __launch_bounds__(PF_THREADS) void prefill_combine_kernel(PrefillArgs a) {
+    const int T = uni(a.sched[0]), nsplit = uni(a.sched[1]);
+    const int tid = threadIdx.x, d = 16 * (tid & 7);
+    const int units = nsplit * a.hkv * PF_COMB_GROUPS;
+    for (int u = blockIdx.x; u < units; u += gridDim.x) {
+        const int k = u / (a.hkv * PF_COMB_GROUPS);
+        const int hk = (u / PF_COMB_GROUPS) % a.hkv, grp = u % PF_COMB_GROUPS;
+        const int sb = uni(a.sched[2 + 2 * k]), item_base = uni(a.sched[3 + 2 * k]);
+        SubBlock s;
+        sub_block(a, sb, T, s);
+        const int pr = grp * (PF_THREADS / 8) + (tid >> 3);
+        const int row = s.r0 + (pr >> 1), hh = pr & 1;
+        if (row >= s.r1) continue;
+        float2 ml[PF_MAXP];
+        u32x4 o[PF_MAXP][2];
+#pragma unroll
+        for (int p = 0; p < PF_MAXP; ++p) {
+            ml[p] = make_float2(-INFINITY, 0.f);
+            o[p][0] = o[p][1] = u32x4{0u, 0u, 0u, 0u};
+            if (p < s.npieces) {
+                const int item = item_base + p * a.hkv + hk;
+                const int64_t prow = ((int64_t)item * PF_BM + (row - s.r0)) * 2 + hh;
+                ml[p] = *reinterpret_cast<const float2*>(a.part_ml + prow * 2);
+                o[p][0] = *reinterpret_cast<const u32x4*>(a.part_o + prow * PF_D + d);
+                o[p][1] = *reinterpret_cast<const u32x4*>(a.part_o + prow * PF_D + d + 8);
+            }
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int p = 0; p < PF_MAXP; ++p) mx = fmaxf(mx, ml[p].x);
+        float num[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) num[j] = 0.f;
+        float den = 0.f;
+#pragma unroll
+        for (int p = 0; p < PF_MAXP; ++p) {
+            // piece weight: its softmax mass l * 2^(m - mx) (0 for pieces with no visible key)
+            const float w =
+                ml[p].x == -INFINITY ? 0.f : ml[p].y * __builtin_amdgcn_exp2f(ml[p].x - mx);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t word = o[p][j >> 2][j & 3];
+                num[2 * j] += bf16lo(word) * w;
+                num[2 * j + 1] += bf16hi(word) * w;
+            }
+            den += w;
+        }
+        const float rd = den != 0.f ? 1.f / den : 0.f;
+        uint32_t y[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) y[j] = pack_bf16x2(num[2 * j] * rd, num[2 * j + 1] * rd);
+        uint16_t* dst = a.out + row * a.o_st + (2 * hk + hh) * a.o_sh + d;
+        *reinterpret_cast<u32x4*>(dst) = u32x4{y[0], y[1], y[2], y[3]};
+        *reinterpret_cast<u32x4*>(dst + 8) = u32x4{y[4], y[5], y[6], y[7]};
+    }
+}
+
+// Partial slots: one resident wave of main-kernel workgroups (split items never outnumber it).
+static int prefill_slots() { return std::max(1, device_cu_count() * IE_PREFILL_WG_PER_CU); }
+
+// Workspace: schedule record (2 + 2 ints per sub-block, padded to 256 B), then per partial
+// slot 64 rows x 2 query heads of (m, l) fp32 and 128 bf16 channels.
+struct PrefillWs {
+    size_t sched_bytes, ml_off, o_off, bytes;
+};
+static PrefillWs prefill_ws(int64_t nsb, int slots) {
+    PrefillWs w;
+    w.sched_bytes = (size_t)((4 * (2 * nsb + 2) + 255) / 256 * 256);
+    w.ml_off = w.sched_bytes;
+    w.o_off = w.ml_off + (size_t)slots * PF_BM * 2 * 2 * sizeof(float);
+    w.bytes = w.o_off + (size_t)slots * PF_BM * 2 * PF_D * sizeof(uint16_t);
+    return w;
 }
 
 }  // namespace ie
 
 using namespace ie;
 
-extern "C" size_t ie_prefill_attention_workspace_size(int64_t num_tokens, int32_t num_q_heads) {
-    return prefill_workspace_bytes(std::max<int64_t>(num_tokens, 0), std::max(num_q_heads, 0));
+extern "C" size_t ie_prefill_attention_workspace_size(int32_t num_tiles, int32_t block_m,
+                                                      int32_t num_kv_heads) {
+    if (num_tiles <= 0 || block_m <= 0 || num_kv_heads <= 0) return 0;
+    const int64_t nsb = (int64_t)num_tiles * ((block_m + PF_BM - 1) / PF_BM);
+    return prefill_ws(nsb, prefill_slots()).bytes;
 }
 
 extern "C" hipError_t ie_prefill_attention(
@@ -596,7 +865,11 @@ extern "C" hipError_t ie_prefill_attention(
     IE_REQUIRE((reinterpret_cast<uintptr_t>(cache->k_calibration) & 15) == 0 &&
                    cache->cal_stride_head % 4 == 0 && cache->cal_stride_slot % 4 == 0,
                "k_calibration rows must be 16-byte aligned");
-    const size_t need = prefill_workspace_bytes(num_tokens, num_q_heads);
+    const int64_t nsb = (int64_t)num_tiles * ((block_m + PF_BM - 1) / PF_BM);
+    IE_REQUIRE(nsb < (1 << 24), "too many tiles");
+    const int slots = prefill_slots();
+    const PrefillWs wsl = prefill_ws(nsb, slots);
+    const size_t need = wsl.bytes;
     IE_REQUIRE(workspace != nullptr && workspace_bytes >= need && al16(workspace),
                "workspace too small");
     PrefillArgs a;
@@ -618,18 +891,21 @@ extern "C" hipError_t ie_prefill_attention(
     a.out = (uint16_t*)out;
     a.o_st = out_stride_tok;
     a.o_sh = out_stride_head;
-    a.part_acc = (float*)workspace;
-    a.part_ml = a.part_acc + (size_t)num_tokens * num_q_heads * PF_MAXP * PF_D;
+    a.sched = (int*)workspace;
+    a.part_ml = (float*)((char*)workspace + wsl.ml_off);
+    a.part_o = (uint16_t*)((char*)workspace + wsl.o_off);
     a.block_m = block_m;
     a.sub_per_tile = (block_m + PF_BM - 1) / PF_BM;
     a.hq = num_q_heads;
+    a.hkv = cache->num_kv_heads;
+    a.nsb = (int)nsb;
+    a.grid = slots;
     a.qk_scale = (float)(0.08838834764831845 * 1.4426950408889634);  // D^-0.5 * log2(e), D = 128
-    const unsigned nsb = (unsigned)num_tiles * a.sub_per_tile;
-    hipLaunchKernelGGL(prefill_attention_kernel, dim3(nsb * PF_MAXP, cache->num_kv_heads),
-                       dim3(PF_THREADS), 0, stream, a);
+    const unsigned grid = (unsigned)std::max<int64_t>(slots, nsb * cache->num_kv_heads);
+    hipLaunchKernelGGL(prefill_attention_kernel, dim3(grid), dim3(PF_THREADS), 0, stream, a);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(prefill_combine_kernel, dim3(nsb * PF_COMB_SPLIT, cache->num_kv_heads),
-                       dim3(PF_THREADS), 0, stream, a);
+    hipLaunchKernelGGL(prefill_combine_kernel, dim3((unsigned)slots), dim3(PF_THREADS), 0, stream,
+                       a);
     return hipGetLastError();
 }

@@ -264,7 +264,8 @@ at::Tensor prefill_attention(const at::Tensor& q, const at::Tensor& k, const at:
                     v.size(1) == c.num_kv_heads,
                 "ie: k/v shape mismatch");
     at::Tensor out = at::empty({N, q.size(1), q.size(2)}, q.options());
-    const size_t ws_bytes = ie_prefill_attention_workspace_size(N, (int32_t)q.size(1));
+    const size_t ws_bytes = ie_prefill_attention_workspace_size(
+        (int32_t)tile_start.size(0), (int32_t)block_m, c.num_kv_heads);
     at::Tensor ws = workspace_for(q, ws_bytes);
     ok(ie_prefill_attention(bf(q), q.stride(0), q.stride(1), bf(k), k.stride(0), k.stride(1),
                             bf(v), v.stride(0), v.stride(1), N, (int32_t)q.size(1), i32(seq_ids),
