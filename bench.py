@@ -6,9 +6,12 @@ D=128 — µs per layer and achieved HBM GB/s against the 8 TB/s peak. One step 
 HBM. Distinct cache sets are rotated between steps so the 256 MB MALL cannot serve a repeat.
 
 Also reported beside it (extra keys): config-4 KV quantize-on-write and chunked-prefill
-attention, each timed with HIP events on the stream the kernels run on.
+attention, each timed with HIP events on the stream the kernels run on, and config 5: a whole
+greedy decode step of a Qwen3-1.7B-shaped model (28 layers, random weights, B=32, ctx ~
+U[128, 4096)) replayed as a hipGraph, with the share of the step spent in the attention kernels
+(the same kernels captured alone).
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--sweep]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--no-step] [--sweep]
 """
 
 import argparse
@@ -92,29 +95,75 @@ def time_op(fn, steps, warmup):
     return sum(ev[2 * i].elapsed_time(ev[2 * i + 1]) for i in range(steps)) / steps
 
 
-def cpu_baseline(wl_gpu, sample_seqs):
-    """The numpy oracle (the reference math restated) on `sample_seqs` sequences of the
-    headline batch, one thread, scaled to the whole batch."""
+def cpu_baseline(wl_gpu, min_seconds):
+    """The numpy oracle (the reference math restated, fp32 dequant/scores/softmax/PV) on the
+    whole headline batch, one thread, repeated until `min_seconds` of CPU work have run."""
     import numpy as np
     from threadpoolctl import threadpool_limits
 
     from oracle import attention as oat
     from oracle import kv_cache as okv
 
-    idx = list(range(sample_seqs))
-    slots = wl_gpu.slot_ids[idx].long()
+    B = len(wl_gpu.ctx)
+    slots = wl_gpu.slot_ids.long()
     c = wl_gpu.cache
     cache = okv.CacheArrays(*(t[slots].cpu().numpy() for t in
                               (c.k, c.v, c.k_scale, c.v_scale, c.k_calibration)))
-    q = wl_gpu.q[idx].float().cpu().numpy()
-    lens = wl_gpu.cached_lens[idx].cpu().numpy()
+    q = wl_gpu.q.float().cpu().numpy()
+    lens = wl_gpu.cached_lens.cpu().numpy()
+    reps = 0
     with threadpool_limits(1):
         t0 = time.perf_counter()
-        oat.decode_attention(q, cache, lens, np.arange(sample_seqs), sample_seqs, SCALE)
-        dt = time.perf_counter() - t0
-    B = len(wl_gpu.ctx)
-    us_layer = dt * 1e6 * B / sample_seqs
-    return us_layer, dt
+        while True:
+            oat.decode_attention(q, cache, lens, np.arange(B), B, SCALE)
+            reps += 1
+            dt = time.perf_counter() - t0
+            if dt >= min_seconds and reps >= 2:
+                break
+    return dt * 1e6 / reps, dt, reps
+
+
+def bench_step(steps, warmup, dev):
+    """Config 5: graph replays of the whole decode step and of its attention kernels alone."""
+    ds = importlib.import_module("inference-engine_amd.decode_step")
+    B = 32
+    step = ds.make_decode_step(batch=B, ctx_lo=128, ctx_hi=4096, device=dev, seed=0)
+    g_step, _ = step.capture()
+    g_attn, _ = step.capture(step.attention_only)
+
+    def t(graph):
+        for _ in range(warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = _events(2)
+        e0.record()
+        for _ in range(steps):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps
+
+    ms_step, ms_attn = t(g_step), t(g_attn)
+    res = {"tokens_per_s": round(B / (ms_step * 1e-3), 1), "ms_per_step": round(ms_step, 4),
+           "attention_ms": round(ms_attn, 4), "attention_share": round(ms_attn / ms_step, 4),
+           "batch": B, "layers": step.shape.layers, "ctx_mean": round(
+               float(step.cached_lens.float().mean().item()) + 1, 1),
+           "graph": "torch.cuda.CUDAGraph (hipGraph) of the full step; attention share = replay "
+                    "time of the step's fused_rope_kv_decode + decode_attention kernels captured "
+                    "alone / step replay time"}
+    del g_step, g_attn, step
+    torch.cuda.empty_cache()
+    return res
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return os.uname().machine
 
 
 def read_traffic():
@@ -137,7 +186,9 @@ def main():
     ap.add_argument("--ctx", type=int, default=4096)
     ap.add_argument("--rotate", type=int, default=2, help="distinct cache sets cycled per step")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-sample", type=int, default=8)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="minimum CPU-baseline work (whole batch, repeated)")
+    ap.add_argument("--no-step", action="store_true", help="skip the config-5 decode step")
     ap.add_argument("--sweep", action="store_true", help="also time the config-3 shape sweep")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run a plain device copy of MIB MiB 3 times (PMC calibration)")
@@ -207,6 +258,14 @@ def main():
     except Exception as e:  # reported, never silently replaced
         extra["config4_error"] = str(e).splitlines()[0][:200]
 
+    if not args.no_step:
+        log("config 5: Qwen3-1.7B-shaped decode step (hipGraph)")
+        try:
+            extra["decode_step_config5"] = bench_step(max(10, args.steps // 2), 3, dev)
+            log(f"config5 {extra['decode_step_config5']}")
+        except Exception as e:  # reported, never silently replaced
+            extra["decode_step_config5"] = {"error": str(e).splitlines()[0][:200]}
+
     if args.sweep:
         sweep = {}
         for b in (16, 64, 256):
@@ -224,12 +283,11 @@ def main():
     cpu = None
     if not args.no_cpu:
         log("cpu baseline (numpy oracle, 1 thread)")
-        us_cpu, dt = cpu_baseline(wls[0], args.cpu_sample)
+        us_cpu, dt, reps = cpu_baseline(wls[0], args.cpu_seconds)
         cpu = {"value": round(alg_bytes / (us_cpu * 1e-6) / 1e9, 3), "unit": "GB/s",
                "us_per_layer": round(us_cpu, 1), "cores": 1, "kind": "port",
-               "sample": f"{args.cpu_sample} of {args.batch} sequences at ctx {args.ctx} "
-                         f"({dt:.2f} s), scaled x{args.batch / args.cpu_sample:g}",
-               "cpu": os.uname().machine}
+               "sample": f"the whole batch ({args.batch} sequences at ctx {args.ctx}), "
+                         f"{reps} passes in {dt:.1f} s", "cpu": _cpu_model()}
     traffic = read_traffic()
     line = {
         "metric": METRIC,

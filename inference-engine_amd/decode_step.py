@@ -1,0 +1,222 @@
+"""One greedy decode step of a Qwen3-1.7B-shaped model with the int8-KV attention path, captured
+as a hipGraph: the harness for the whole-step measurement (tokens/s and the attention share).
+
+Mirrors the decode branch of the reference's model (qwen3-1.7b/architecture.py:98-122 inside
+TransformerBlock.forward :299-330 and Qwen3Model.forward :403-446) and its graph capture and
+replay (qwen3-1.7b/engine.py:376-470): per layer, residual add + RMSNorm, QKV projection,
+`fused_rope_kv_decode` (norm + RoPE + int8 KV write), `decode_attention`, output projection,
+residual add + RMSNorm, gate/up projection, SiLU * up, down projection; then the final norm, the
+tied-embedding LM head and greedy argmax. The attention ops are this package's HIP kernels; the
+projections, norms and argmax are plain PyTorch (hipBLASLt GEMMs), which the reference also
+leaves to its linear/add_rms_norm/silu_mul/sample kernels outside the attention path.
+
+Weights are random (bf16, std 0.02) and the caches hold random int8 K/V: there is no checkpoint
+here, and the step's cost does not depend on the values.
+"""
+
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+
+from .kernels import LayerKVCache, decode_attention, fused_rope_kv_decode, make_layer_cache
+
+
+@dataclass(frozen=True)
+class Qwen3Shape:
+    """qwen3-1.7b/architecture.py:492-500."""
+
+    model_dim: int = 2048
+    intermediate: int = 6144
+    head_dim: int = 128
+    num_q_heads: int = 16
+    num_kv_heads: int = 8
+    vocab: int = 151936
+    layers: int = 28
+    rope_base: float = 1e6
+    eps: float = 1e-6
+
+
+@dataclass
+class LayerWeights:
+    input_norm: torch.Tensor  # [model_dim]
+    qkv: torch.Tensor  # [(Hq + 2 Hkv) D, model_dim]
+    q_norm: torch.Tensor  # [D]
+    k_norm: torch.Tensor  # [D]
+    o_proj: torch.Tensor  # [model_dim, Hq D]
+    post_norm: torch.Tensor  # [model_dim]
+    gate_up: torch.Tensor  # [2 intermediate, model_dim]
+    down: torch.Tensor  # [model_dim, intermediate]
+
+
+def random_weights(shape: Qwen3Shape, device, seed=0, std=0.02):
+    g = torch.Generator(device=device).manual_seed(seed)
+
+    def w(*dims):
+        return (torch.randn(*dims, generator=g, device=device, dtype=torch.float32) * std).bfloat16()
+
+    def ones(n):
+        return torch.ones(n, device=device, dtype=torch.bfloat16)
+
+    D, H = shape.head_dim, shape.model_dim
+    layers = [
+        LayerWeights(
+            input_norm=ones(H),
+            qkv=w((shape.num_q_heads + 2 * shape.num_kv_heads) * D, H),
+            q_norm=ones(D),
+            k_norm=ones(D),
+            o_proj=w(H, shape.num_q_heads * D),
+            post_norm=ones(H),
+            gate_up=w(2 * shape.intermediate, H),
+            down=w(H, shape.intermediate),
+        )
+        for _ in range(shape.layers)
+    ]
+    embed = w(shape.vocab, H)
+    return layers, embed, ones(H)
+
+
+def random_caches(shape: Qwen3Shape, pool: int, max_len: int, device, seed=0):
+    """Per-layer int8 caches with random content in every column (scales ~0.02)."""
+    g = torch.Generator(device=device).manual_seed(seed + 1)
+    caches = []
+    for _ in range(shape.layers):
+        c = make_layer_cache(pool, shape.num_kv_heads, max_len, shape.head_dim, device=device)
+        c.k.copy_(torch.randint(-127, 128, c.k.shape, generator=g, device=device, dtype=torch.int8))
+        c.v.copy_(torch.randint(-127, 128, c.v.shape, generator=g, device=device, dtype=torch.int8))
+        c.k_scale.copy_(torch.rand(c.k_scale.shape, generator=g, device=device) * 0.04)
+        c.v_scale.copy_(torch.rand(c.v_scale.shape, generator=g, device=device) * 0.04)
+        caches.append(c)
+    return caches
+
+
+class DecodeStep:
+    """Static-address decode step for B sequences (engine.py:376-412): the graph reads ids,
+    cached_lens and slot_ids from fixed tensors, which the caller rewrites between replays."""
+
+    def __init__(self, shape: Qwen3Shape, layers, embed, final_norm, caches: list[LayerKVCache],
+                 batch: int, device):
+        self.shape, self.layers, self.embed, self.final_norm = shape, layers, embed, final_norm
+        self.caches = caches
+        self.B = batch
+        pool = caches[0].k.shape[0]
+        assert batch <= pool
+        self.ids = torch.zeros(batch, device=device, dtype=torch.int64)
+        self.cached_lens = torch.zeros(batch, device=device, dtype=torch.int32)
+        self.slot_ids = torch.arange(batch, device=device, dtype=torch.int32)
+        self.num_decoding = torch.full((1,), batch, device=device, dtype=torch.int32)
+        D = shape.head_dim
+        self.inv_freq = shape.rope_base ** (
+            -torch.arange(0, D, 2, dtype=torch.float32, device=device) / D)
+        self.graph = None
+        self.graph_out = None
+
+    def _rope(self):
+        # decode: a token's position is the number of tokens before it (architecture.py:413-422)
+        ang = self.cached_lens[:, None, None].float() * self.inv_freq[None, None, :]
+        return ang.cos().bfloat16(), ang.sin().bfloat16()
+
+    def _rms(self, x, w):
+        return F.rms_norm(x.float(), (x.shape[-1],), w.float(), self.shape.eps).bfloat16()
+
+    def attention(self, li, normed, cos, sin):
+        """AttentionLayer.forward, pure-decode branch (architecture.py:85-122)."""
+        s, lw, B = self.shape, self.layers[li], self.B
+        qkv = F.linear(normed, lw.qkv)
+        q, k, v = qkv.split([s.num_q_heads * s.head_dim, s.num_kv_heads * s.head_dim,
+                             s.num_kv_heads * s.head_dim], dim=-1)
+        q = q.view(B, s.num_q_heads, s.head_dim)
+        k = k.view(B, s.num_kv_heads, s.head_dim)
+        v = v.view(B, s.num_kv_heads, s.head_dim)
+        q = fused_rope_kv_decode(q, k, v, lw.q_norm, lw.k_norm, cos, sin, self.slot_ids,
+                                 self.caches[li], self.cached_lens, self.num_decoding, s.eps)
+        out = decode_attention(q, self.caches[li], self.cached_lens, self.slot_ids,
+                               self.num_decoding, s.head_dim ** -0.5)
+        return F.linear(out.view(B, -1), lw.o_proj)
+
+    def forward(self) -> torch.Tensor:
+        """One step: returns the greedy next token of every sequence, int64 [B, 1]."""
+        cos, sin = self._rope()
+        x = F.embedding(self.ids, self.embed)
+        residual = None
+        for li, lw in enumerate(self.layers):
+            residual = x if residual is None else residual + x
+            attn = self.attention(li, self._rms(residual, lw.input_norm), cos, sin)
+            residual = residual + attn
+            gate, up = F.linear(self._rms(residual, lw.post_norm), lw.gate_up).chunk(2, dim=-1)
+            x = F.linear(F.silu(gate) * up, lw.down)
+        h = self._rms(residual + x, self.final_norm)
+        logits = F.linear(h, self.embed)
+        return torch.argmax(logits, dim=-1, keepdim=True)
+
+    def attention_only(self) -> torch.Tensor:
+        """The step's attention kernels alone (per layer: fused_rope_kv_decode and
+        decode_attention on fixed activations), for the attention share of a step."""
+        s, B = self.shape, self.B
+        cos, sin = self._rope()
+        if not hasattr(self, "_qkv_fixed"):
+            g = torch.Generator(device=self.ids.device).manual_seed(7)
+            self._qkv_fixed = torch.randn(B, (s.num_q_heads + 2 * s.num_kv_heads) * s.head_dim,
+                                          generator=g, device=self.ids.device).bfloat16()
+        q, k, v = self._qkv_fixed.split([s.num_q_heads * s.head_dim, s.num_kv_heads * s.head_dim,
+                                         s.num_kv_heads * s.head_dim], dim=-1)
+        q = q.view(B, s.num_q_heads, s.head_dim)
+        k = k.view(B, s.num_kv_heads, s.head_dim)
+        v = v.view(B, s.num_kv_heads, s.head_dim)
+        out = None
+        for li, lw in enumerate(self.layers):
+            qo = fused_rope_kv_decode(q, k, v, lw.q_norm, lw.k_norm, cos, sin, self.slot_ids,
+                                      self.caches[li], self.cached_lens, self.num_decoding,
+                                      s.eps)
+            out = decode_attention(qo, self.caches[li], self.cached_lens, self.slot_ids,
+                                   self.num_decoding, s.head_dim ** -0.5)
+        return out
+
+    def capture(self, fn=None):
+        """Warm up twice on a side stream, then capture `fn` (default: forward) into a hipGraph
+        (engine.py:432-449). Returns (graph, output tensor the replays overwrite)."""
+        fn = fn or self.forward
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for _ in range(2):
+                fn()
+        torch.cuda.current_stream().wait_stream(s)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            out = fn()
+        return graph, out
+
+
+def make_decode_step(batch=32, ctx_lo=128, ctx_hi=4096, shape=Qwen3Shape(), device="cuda",
+                     seed=0):
+    """Config-5 step: B sequences with cached lengths ~ U[ctx_lo, ctx_hi) - 1 (the new token is
+    the ctx-th), slots 0..B-1 of a pool of B + 1 (the last row is the engine's scratch slot)."""
+    layers, embed, final_norm = random_weights(shape, device, seed)
+    caches = random_caches(shape, batch + 1, ctx_hi, device, seed)
+    step = DecodeStep(shape, layers, embed, final_norm, caches, batch, device)
+    g = torch.Generator().manual_seed(seed)
+    ctx = torch.randint(ctx_lo, ctx_hi, (batch,), generator=g)
+    step.cached_lens.copy_((ctx - 1).to(torch.int32))
+    step.ids.copy_(torch.randint(0, shape.vocab, (batch,), generator=g))
+    return step
+
+
+def _main():
+    """Replay the config-5 step graph (for kernel traces): python -m <package>.decode_step"""
+    import argparse
+
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--replays", type=int, default=20)
+    ap.add_argument("--attention-only", action="store_true")
+    args = ap.parse_args()
+    step = make_decode_step(device="cuda:0")
+    graph, out = step.capture(step.attention_only if args.attention_only else None)
+    for _ in range(args.replays):
+        graph.replay()
+    torch.cuda.synchronize()
+    print(f"replayed {args.replays} steps; first tokens {out.view(-1)[:4].tolist()}", flush=True)
+
+
+if __name__ == "__main__":
+    _main()
