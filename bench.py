@@ -83,16 +83,18 @@ def time_decode(ie, wls, steps, warmup):
 
 
 def time_op(fn, steps, warmup):
+    """Average time of back-to-back calls between two events: events around every call of a
+    microsecond-scale kernel would add several microseconds of their own per call."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
-    ev = _events(2 * steps)
-    for i in range(steps):
-        ev[2 * i].record()
+    e0, e1 = _events(2)
+    e0.record()
+    for _ in range(steps):
         fn()
-        ev[2 * i + 1].record()
+    e1.record()
     torch.cuda.synchronize()
-    return sum(ev[2 * i].elapsed_time(ev[2 * i + 1]) for i in range(steps)) / steps
+    return e0.elapsed_time(e1) / steps
 
 
 def cpu_baseline(wl_gpu, min_seconds):

@@ -15,8 +15,8 @@ namespace ie {
 constexpr int HEAD_DIM = 128;
 constexpr int QP_THREADS = 256;
 constexpr int QP_ROWS = QP_THREADS / 16;   // token rows per pass of a workgroup
-constexpr int QP_MIN_TOKENS = 128;         // fewest tokens a prefill-write workgroup takes
-constexpr int QP_MAX_SPLITS = 8;           // workgroups per (entry, kv head) at most
+constexpr int QP_BLOCK = 32;               // chunk rows per workgroup
+constexpr int QP_CAL_BATCH = 32;           // calibration rows in flight per thread
 
 struct Row8 {
     float x[8];
@@ -59,30 +59,53 @@ __device__ __forceinline__ float quantize_row8(const float* x, int32_t* q) {
     return s;
 }
 
-// grid (num_entries, Hkv, splits), block 256. Workgroup (b, h, z) quantizes its share of entry
-// b's chunk for kv head h (kernels.py:786-823). When cached_len == 0 every workgroup of (b, h)
-// computes the chunk's calibration (kernels.py:764-780) itself and split 0 stores it.
+// grid (cdiv(N, 32) + num_entries, Hkv), block 256. The prefilling entries' chunks are cut into
+// blocks of QP_BLOCK rows, numbered entry by entry; workgroup (u, h) quantizes block u for kv
+// head h (kernels.py:786-823), or exits when there are fewer blocks. When cached_len == 0 every
+// block of the entry computes the chunk's calibration (kernels.py:764-780) itself and block 0
+// stores it.
 __global__ __launch_bounds__(QP_THREADS) void quantize_kv_prefill_kernel(
     const uint16_t* __restrict__ k, int64_t k_st, int64_t k_sh,
     const uint16_t* __restrict__ v, int64_t v_st, int64_t v_sh,
     const int32_t* __restrict__ cu_seqlens, const int32_t* __restrict__ slot_ids,
     const int32_t* __restrict__ cached_lens, const int32_t* __restrict__ num_decoding,
-    ie_kv_cache c) {
+    int num_entries, ie_kv_cache c) {
 #pragma clang fp contract(off)
-    const int b = blockIdx.x, h = blockIdx.y, z = blockIdx.z;
-    if (b < num_decoding[0]) return;
-    const int start = cu_seqlens[b];
-    const int len = cu_seqlens[b + 1] - start;
-    if (len <= 0) return;
-    const int nsplit = min((int)gridDim.z, (len + QP_MIN_TOKENS - 1) / QP_MIN_TOKENS);
-    if (z >= nsplit) return;
-    const int per = (len + nsplit - 1) / nsplit;
-    const int t0 = z * per;
-    const int t1 = min(len, t0 + per);
-    if (t0 >= t1) return;
+    const int h = blockIdx.y, u = blockIdx.x;
+    // Locate block u: every wave scans the entries' block counts (identical result). The
+    // entry's start, length, slot and cached length come from the same (independent) loads, so
+    // the data loads below are the second round trip to memory.
+    const int lane = threadIdx.x & 63;
+    const int nd = __builtin_amdgcn_readfirstlane(num_decoding[0]);
+    int b = -1, z = 0, before = 0, start = 0, len = 0, slot = 0, c0 = 0;
+    for (int base = 0; base < num_entries && b < 0; base += IE_WAVE) {
+        const int e = base + lane;
+        int s0 = 0, s1 = 0, sl = 0, cl = 0;
+        if (e < num_entries) {
+            s0 = cu_seqlens[e];
+            s1 = cu_seqlens[e + 1];
+            sl = slot_ids[e];
+            cl = cached_lens[e];
+        }
+        const int nb = e >= nd && e < num_entries ? cdiv_i(s1 - s0, QP_BLOCK) : 0;
+        const int incl = wave_incl_scan_i(nb) + before;
+        const unsigned long long hit = __ballot(u < incl && u >= incl - nb);
+        if (hit) {
+            const int src = __builtin_ctzll(hit);
+            auto from = [&](int x) { return __builtin_amdgcn_readfirstlane(__shfl(x, src, IE_WAVE)); };
+            b = from(e);
+            z = u - from(incl - nb);
+            start = from(s0);
+            len = from(s1 - s0);
+            slot = from(sl);
+            c0 = from(cl);
+        }
+        before = __builtin_amdgcn_readfirstlane(__shfl(incl, 63, IE_WAVE));
+    }
+    if (b < 0) return;
+    const int t0 = z * QP_BLOCK;
+    const int t1 = min(len, t0 + QP_BLOCK);
 
-    const int slot = slot_ids[b];
-    const int c0 = cached_lens[b];
     const int tid = threadIdx.x;
     const int c16 = tid & 15;  // channels [8*c16, 8*c16+8)
     const int r = tid >> 4;    // row within a pass
@@ -94,14 +117,41 @@ __global__ __launch_bounds__(QP_THREADS) void quantize_kv_prefill_kernel(
     const uint16_t* kh = k + (int64_t)start * k_st + h * k_sh + 8 * c16;
     const uint16_t* vh = v + (int64_t)start * v_st + h * v_sh + 8 * c16;
 
+    // this workgroup's rows, two passes at a time: the first pair is loaded before the
+    // calibration pass so both sets of loads are in flight together
+    Row8 xk[2], xv[2];
+    auto load_pair = [&](int t) {
+        xk[0] = load_bf16x8(kh + (int64_t)t * k_st);
+        xv[0] = load_bf16x8(vh + (int64_t)t * v_st);
+        if (t + QP_ROWS < t1) {
+            xk[1] = load_bf16x8(kh + (int64_t)(t + QP_ROWS) * k_st);
+            xv[1] = load_bf16x8(vh + (int64_t)(t + QP_ROWS) * v_st);
+        }
+    };
+    if (t0 + r < t1) load_pair(t0 + r);
+
     if (c0 == 0) {
+        // max |k| per channel over the whole chunk, QP_CAL_BATCH rows per thread in flight
         float mx[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) mx[j] = 0.0f;
-        for (int t = r; t < len; t += QP_ROWS) {
-            const Row8 x = load_bf16x8(kh + (int64_t)t * k_st);
+        for (int t = r; t < len; t += QP_ROWS * QP_CAL_BATCH) {
+            uint4 u[QP_CAL_BATCH];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) mx[j] = fmaxf(mx[j], fabsf(x.x[j]));
+            for (int i = 0; i < QP_CAL_BATCH; ++i) {
+                const int ti = t + i * QP_ROWS;
+                u[i] = ti < len ? *reinterpret_cast<const uint4*>(kh + (int64_t)ti * k_st)
+                                : make_uint4(0u, 0u, 0u, 0u);
+            }
+#pragma unroll
+            for (int i = 0; i < QP_CAL_BATCH; ++i) {
+                const uint32_t w[4] = {u[i].x, u[i].y, u[i].z, u[i].w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    mx[2 * j] = fmaxf(mx[2 * j], fabsf(bf16lo(w[j])));
+                    mx[2 * j + 1] = fmaxf(mx[2 * j + 1], fabsf(bf16hi(w[j])));
+                }
+            }
         }
 #pragma unroll
         for (int j = 0; j < 8; ++j) s_red[r][8 * c16 + j] = mx[j];
@@ -126,20 +176,24 @@ __global__ __launch_bounds__(QP_THREADS) void quantize_kv_prefill_kernel(
     float* ks = c.k_scale + slot * c.scale_stride_slot + h * c.scale_stride_head;
     float* vs = c.v_scale + slot * c.scale_stride_slot + h * c.scale_stride_head;
 
-    for (int t = t0 + r; t < t1; t += QP_ROWS) {
-        const int64_t col = (int64_t)(c0 + t);
-        int32_t q[8];
-        Row8 x = load_bf16x8(kh + (int64_t)t * k_st);
+    for (int t = t0 + r; t < t1; t += 2 * QP_ROWS) {
+        const bool two = t + QP_ROWS < t1;
+        Row8 ck[2] = {xk[0], xk[1]}, cv[2] = {xv[0], xv[1]};
+        if (t + 2 * QP_ROWS < t1) load_pair(t + 2 * QP_ROWS);  // next pair in flight
 #pragma unroll
-        for (int j = 0; j < 8; ++j) x.x[j] = x.x[j] / cal[j];
-        float s = quantize_row8(x.x, q);
-        *reinterpret_cast<uint2*>(kc + col * c.stride_tok) = pack_i8x8(q);
-        if (c16 == 0) ks[col] = s;
-
-        Row8 y = load_bf16x8(vh + (int64_t)t * v_st);
-        s = quantize_row8(y.x, q);
-        *reinterpret_cast<uint2*>(vc + col * c.stride_tok) = pack_i8x8(q);
-        if (c16 == 0) vs[col] = s;
+        for (int p = 0; p < 2; ++p) {
+            if (p == 1 && !two) break;
+            const int64_t col = (int64_t)(c0 + t + p * QP_ROWS);
+            int32_t q[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) ck[p].x[j] = ck[p].x[j] / cal[j];
+            float s = quantize_row8(ck[p].x, q);
+            *reinterpret_cast<uint2*>(kc + col * c.stride_tok) = pack_i8x8(q);
+            if (c16 == 0) ks[col] = s;
+            s = quantize_row8(cv[p].x, q);
+            *reinterpret_cast<uint2*>(vc + col * c.stride_tok) = pack_i8x8(q);
+            if (c16 == 0) vs[col] = s;
+        }
     }
 }
 
@@ -280,14 +334,14 @@ extern "C" hipError_t ie_quantize_kv_prefill(
     IE_REQUIRE(aligned16(k) && aligned16(v) && k_stride_tok % 8 == 0 && k_stride_head % 8 == 0 &&
                    v_stride_tok % 8 == 0 && v_stride_head % 8 == 0,
                "k/v rows must be 16-byte aligned with contiguous head_dim");
-    const int splits =
-        (int)std::max<int64_t>(1, std::min<int64_t>(QP_MAX_SPLITS, (num_tokens + QP_MIN_TOKENS - 1) /
-                                                                       QP_MIN_TOKENS));
-    dim3 grid(num_entries, (unsigned)cache->num_kv_heads, splits);
+    // sum over entries of cdiv(len, 32) <= cdiv(N, 32) + num_entries
+    const int64_t blocks = (num_tokens + QP_BLOCK - 1) / QP_BLOCK + num_entries;
+    IE_REQUIRE(blocks < (1LL << 31), "too many tokens");
+    dim3 grid((unsigned)std::max<int64_t>(1, blocks), (unsigned)cache->num_kv_heads);
     hipLaunchKernelGGL(quantize_kv_prefill_kernel, grid, dim3(QP_THREADS), 0, stream,
                        (const uint16_t*)k, k_stride_tok, k_stride_head, (const uint16_t*)v,
                        v_stride_tok, v_stride_head, cu_seqlens, slot_ids, cached_lens,
-                       num_decoding, *cache);
+                       num_decoding, num_entries, *cache);
     return hipGetLastError();
 }
 
