@@ -183,7 +183,10 @@ hipError_t ie_dequantize_kv_prefix(const ie_kv_cache* cache, const int32_t* cu_c
  * block_m rows, -1 = no work; every tile lies inside one entry. Row m of entry e attends to the
  * e's prefix (cache row slot_ids[e], columns [0, cu_cached[e+1] - cu_cached[e])) and to its own
  * chunk rows [cu_seqlens[e], m]. Rows of out that no tile covers are left untouched.
- * Long key ranges are split across workgroups; `workspace` (fp32 partials) must hold
+ * num_entries = the length of slot_ids (cu_seqlens and cu_cached hold num_entries + 1), at most
+ * 512. A row's entry is found from cu_seqlens; seq_ids is accepted for the reference's
+ * signature and not read.
+ * Long key ranges are split across workgroups; `workspace` (partials) must hold
  * ie_prefill_attention_workspace_size(num_tiles, block_m, num_kv_heads) bytes, a size that
  * depends on the current device's CU count.
  */
@@ -196,7 +199,8 @@ hipError_t ie_prefill_attention(const ie_bf16* q, int64_t q_stride_tok, int64_t 
                                 const int32_t* seq_ids, const int32_t* cu_seqlens,
                                 const int32_t* tile_start, int32_t num_tiles, int32_t block_m,
                                 const ie_kv_cache* cache, const int32_t* slot_ids,
-                                const int32_t* cu_cached, ie_bf16* out, int64_t out_stride_tok,
+                                const int32_t* cu_cached, int32_t num_entries, ie_bf16* out,
+                                int64_t out_stride_tok,
                                 int64_t out_stride_head, void* workspace, size_t workspace_bytes,
                                 hipStream_t stream);
 

@@ -99,9 +99,10 @@ struct PrefillArgs {
     int64_t o_st, o_sh;
     uint16_t* part_o;  // [slot][64 rows][2 heads][128] bf16: normalized partial O of split items
     float* part_ml;    // [slot][64 rows][2 heads][2]: their (m, l)
-    int* sched;  // [0] piece size T, [1] split sub-blocks n, [2 + 2i, 3 + 2i] (sub-block, first
-                 // item) of the i-th split sub-block in launch order
+    int* sched;  // [0] piece size T, [1] split sub-blocks n, then per split sub-block i (launch
+                 // order) 4 ints at 4 + 4i: first item, r0, r1, pieces
     int block_m, sub_per_tile, hq, hkv;
+    int nent;  // entries (length of slot_ids; cu_seqlens and cu_cached hold nent + 1)
     int nsb;   // sub-blocks: num_tiles * sub_per_tile
     int grid;  // partial slots (resident main-kernel workgroups); split items are numbered below it
     float qk_scale;  // D^-0.5 * log2(e)
@@ -116,32 +117,12 @@ __device__ __forceinline__ int uni(int x) { return __builtin_amdgcn_readfirstlan
 struct SbInfo {
     int ntiles, r0, r1, seq_start, P, slot;
 };
-__device__ __forceinline__ SbInfo sb_info(const PrefillArgs& a, int sb) {
-    SbInfo z = {0, 0, 0, 0, 0, 0};
-    if (sb < 0 || sb >= a.nsb) return z;
-    const int tile = sb / a.sub_per_tile, sub = sb - tile * a.sub_per_tile;
-    const int row_start = a.tile_start[tile];
-    if (row_start < 0) return z;
-    const int seq = a.seq_ids[row_start];
-    const int seq_start = a.cu_seqlens[seq], seq_end = a.cu_seqlens[seq + 1];
-    const int c0 = a.cu_cached[seq], c1 = a.cu_cached[seq + 1], slot = a.slot_ids[seq];
-    const int r0 = row_start + sub * PF_BM;
-    const int r1 = min(min(r0 + PF_BM, row_start + a.block_m), seq_end);
-    if (r0 >= r1) return z;
-    z.P = c1 - c0;
-    z.ntiles = cdiv_i(z.P, PF_BN) + cdiv_i(r1 - seq_start, PF_BN);
-    z.r0 = r0;
-    z.r1 = r1;
-    z.seq_start = seq_start;
-    z.slot = slot;
-    return z;
-}
 
 __device__ __forceinline__ int piece_count(int ntiles, int T) {
     return min(PF_MAXP, max(1, cdiv_i(ntiles, T)));
 }
 
-// The launch's work list, computed identically by every wave from the tile metadata:
+// The launch's work list, computed identically by every workgroup from the tile metadata:
 //  * piece size T (tiles): a (sub-block, kv head) pair with n tiles becomes cdiv(n, T) items (at
 //    most PF_MAXP). T is the smallest size for which the items fit the partial slots even in the
 //    worst rounding, sum(n / T + 1) * Hkv <= slots, so every split item owns a slot. With more
@@ -149,9 +130,13 @@ __device__ __forceinline__ int piece_count(int ntiles, int T) {
 //  * items in launch order: sub-blocks from last to first (later sub-blocks of a sequence see
 //    more keys), then piece, then kv head.
 // schedule(target) finds the sub-block holding item `target`, the offset inside it and the
-// number of items before the sub-block. Sub-block sizes stay in registers between the two passes
-// for the first PF_SCHED_CHUNKS * 64 sub-blocks and are reloaded beyond that.
+// number of items before the sub-block. All metadata comes in one memory round trip: the tile
+// starts of the wave's sub-blocks (PF_SCHED_CHUNKS * 64 in registers, reloaded beyond) and the
+// per-entry tables (cu_seqlens, cu_cached, slot_ids) staged in LDS, where each sub-block finds
+// its entry by binary search (an entry owns the rows [cu_seqlens[e], cu_seqlens[e + 1]); the
+// largest e with cu_seqlens[e] <= row is that row's entry, empty entries included).
 constexpr int PF_SCHED_CHUNKS = 4;
+constexpr int PF_MAX_ENTRIES = 512;
 
 struct SubBlock {
     int r0, r1, seq_start, P, slot, npt, nct, ntiles, npieces;
@@ -178,21 +163,57 @@ struct Loc {
     SubBlock s;       // sub-block sb
 };
 
-// One wave's pass over the tile metadata (every lane of the wave returns the same Loc).
+// One wave's pass over the tile metadata (every lane of the wave returns the same Loc). Only
+// one wave of the workgroup may call it (it owns the entry tables in LDS).
 __device__ Loc schedule(const PrefillArgs& a, int target) {
+    __shared__ int s_cu[PF_MAX_ENTRIES + 1], s_cc[PF_MAX_ENTRIES + 1], s_sl[PF_MAX_ENTRIES];
     const int lane = threadIdx.x & 63;
     const int nchunks = cdiv_i(a.nsb, IE_WAVE);
     auto sb_of = [&](int c) { return a.nsb - 1 - (c * IE_WAVE + lane); };
+    auto row_start_of = [&](int sb) {
+        return sb >= 0 && sb < a.nsb ? a.tile_start[sb / a.sub_per_tile] : -1;
+    };
+    // the round trip: tile starts first, then the entry tables (all independent loads)
+    int rs[PF_SCHED_CHUNKS];
+#pragma unroll
+    for (int c = 0; c < PF_SCHED_CHUNKS; ++c) rs[c] = row_start_of(c < nchunks ? sb_of(c) : -1);
+    for (int e = lane; e <= a.nent; e += IE_WAVE) {
+        s_cu[e] = a.cu_seqlens[e];
+        s_cc[e] = a.cu_cached[e];
+        if (e < a.nent) s_sl[e] = a.slot_ids[e];
+    }
+    auto info = [&](int sb, int row_start) {
+        SbInfo z = {0, 0, 0, 0, 0, 0};
+        if (row_start < 0) return z;
+        int lo = 0, hi = a.nent - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (s_cu[mid] <= row_start) lo = mid;
+            else hi = mid - 1;
+        }
+        const int seq_start = s_cu[lo], seq_end = s_cu[lo + 1];
+        const int sub = sb - (sb / a.sub_per_tile) * a.sub_per_tile;
+        const int r0 = row_start + sub * PF_BM;
+        const int r1 = min(min(r0 + PF_BM, row_start + a.block_m), seq_end);
+        if (r0 >= r1) return z;
+        z.P = s_cc[lo + 1] - s_cc[lo];
+        z.ntiles = cdiv_i(z.P, PF_BN) + cdiv_i(r1 - seq_start, PF_BN);
+        z.r0 = r0;
+        z.r1 = r1;
+        z.seq_start = seq_start;
+        z.slot = s_sl[lo];
+        return z;
+    };
     SbInfo zc[PF_SCHED_CHUNKS];
     int tot = 0, nonempty = 0;
 #pragma unroll
     for (int c = 0; c < PF_SCHED_CHUNKS; ++c) {
-        zc[c] = sb_info(a, c < nchunks ? sb_of(c) : -1);
+        zc[c] = info(c < nchunks ? sb_of(c) : -1, rs[c]);
         tot += zc[c].ntiles;
         nonempty += zc[c].ntiles > 0;
     }
     for (int c = PF_SCHED_CHUNKS; c < nchunks; ++c) {
-        const int nt = sb_info(a, sb_of(c)).ntiles;
+        const int nt = info(sb_of(c), row_start_of(sb_of(c))).ntiles;
         tot += nt;
         nonempty += nt > 0;
     }
@@ -209,7 +230,7 @@ __device__ Loc schedule(const PrefillArgs& a, int target) {
         for (int c = 0; c < PF_SCHED_CHUNKS; ++c)
             ns += zc[c].ntiles > 0 && piece_count(zc[c].ntiles, L.T) > 1;
         for (int c = PF_SCHED_CHUNKS; c < nchunks; ++c) {
-            const int nt = sb_info(a, sb_of(c)).ntiles;
+            const int nt = info(sb_of(c), row_start_of(sb_of(c))).ntiles;
             ns += nt > 0 && piece_count(nt, L.T) > 1;
         }
         L.nsplit = uni(wave_sum_i(ns));
@@ -240,18 +261,8 @@ __device__ Loc schedule(const PrefillArgs& a, int target) {
     for (int c = 0; c < PF_SCHED_CHUNKS; ++c)
         if (c < nchunks && visit(c, zc[c])) return L;
     for (int c = PF_SCHED_CHUNKS; c < nchunks; ++c)
-        if (visit(c, sb_info(a, sb_of(c)))) return L;
+        if (visit(c, info(sb_of(c), row_start_of(sb_of(c))))) return L;
     return L;
-}
-
-// Rows and keys of sub-block `sb` (uniform across the workgroup); false if it has no rows. Its
-// keys are npt prefix tiles covering [0, P) and then nct chunk tiles covering chunk rows
-// [seq_start, r1); a tile never mixes the two.
-__device__ __forceinline__ bool sub_block(const PrefillArgs& a, int sb, int T, SubBlock& s) {
-    const SbInfo z = sb_info(a, sb);
-    if (uni(z.ntiles) == 0) return false;
-    fill_sub_block(s, uni(z.r0), uni(z.r1), uni(z.seq_start), uni(z.P), uni(z.slot), T);
-    return true;
 }
 
 // Global data of one tile, held in registers between its load and its LDS staging.
@@ -739,8 +750,8 @@ __global__ __launch_bounds__(PF_THREADS, IE_PREFILL_WG_PER_CU) void prefill_atte
     if (!loc.found) return;
     const SubBlock& s = loc.s;
     if (loc.off == 0 && s.npieces > 1 && threadIdx.x == 0) {
-        a.sched[2 + 2 * loc.split_index] = loc.sb;
-        a.sched[3 + 2 * loc.split_index] = loc.item_base;
+        *reinterpret_cast<int4*>(a.sched + 4 + 4 * loc.split_index) =
+            make_int4(loc.item_base, s.r0, s.r1, s.npieces);
     }
     prefill_item(a, s, loc.off % a.hkv, loc.off / a.hkv, blockIdx.x);
 }
@@ -751,15 +762,18 @@ constexpr int PF_COMB_GROUPS = 4;  // combine units per (split sub-block, kv hea
 // list the main kernel recorded. Unit u: split sub-block u / (Hkv * 4), kv head, and 32 of its
 // 128 (row, query head) pairs; 8 threads per pair, 16 channels each, all loads issued up front.
 __global__ __launch_bounds__(PF_THREADS) void prefill_combine_kernel(PrefillArgs a) {
-    const int T = uni(a.sched[0]), nsplit = uni(a.sched[1]);
+    const int nsplit = uni(a.sched[1]);
     const int tid = threadIdx.x, d = 16 * (tid & 7);
     const int units = nsplit * a.hkv * PF_COMB_GROUPS;
     for (int u = blockIdx.x; u < units; u += gridDim.x) {
         const int k = u / (a.hkv * PF_COMB_GROUPS);
         const int hk = (u / PF_COMB_GROUPS) % a.hkv, grp = u % PF_COMB_GROUPS;
-        const int sb = uni(a.sched[2 + 2 * k]), item_base = uni(a.sched[3 + 2 * k]);
+        const int4 rec = *reinterpret_cast<const int4*>(a.sched + 4 + 4 * k);
+        const int item_base = uni(rec.x);
         SubBlock s;
-        sub_block(a, sb, T, s);
+        s.r0 = uni(rec.y);
+        s.r1 = uni(rec.z);
+        s.npieces = uni(rec.w);
         const int pr = grp * (PF_THREADS / 8) + (tid >> 3);
         const int row = s.r0 + (pr >> 1), hh = pr & 1;
         if (row >= s.r1) continue;
@@ -810,14 +824,14 @@ __global__ __launch_bounds__(PF_THREADS) void prefill_combine_kernel(PrefillArgs
 // Partial slots: one resident wave of main-kernel workgroups (split items never outnumber it).
 static int prefill_slots() { return std::max(1, device_cu_count() * IE_PREFILL_WG_PER_CU); }
 
-// Workspace: schedule record (2 + 2 ints per sub-block, padded to 256 B), then per partial
+// Workspace: schedule record (4 + 4 ints per sub-block, padded to 256 B), then per partial
 // slot 64 rows x 2 query heads of (m, l) fp32 and 128 bf16 channels.
 struct PrefillWs {
     size_t sched_bytes, ml_off, o_off, bytes;
 };
 static PrefillWs prefill_ws(int64_t nsb, int slots) {
     PrefillWs w;
-    w.sched_bytes = (size_t)((4 * (2 * nsb + 2) + 255) / 256 * 256);
+    w.sched_bytes = (size_t)((4 * (4 * nsb + 4) + 255) / 256 * 256);
     w.ml_off = w.sched_bytes;
     w.o_off = w.ml_off + (size_t)slots * PF_BM * 2 * 2 * sizeof(float);
     w.bytes = w.o_off + (size_t)slots * PF_BM * 2 * PF_D * sizeof(uint16_t);
@@ -840,7 +854,8 @@ extern "C" hipError_t ie_prefill_attention(
     int64_t k_stride_tok, int64_t k_stride_head, const ie_bf16* v, int64_t v_stride_tok,
     int64_t v_stride_head, int64_t num_tokens, int32_t num_q_heads, const int32_t* seq_ids,
     const int32_t* cu_seqlens, const int32_t* tile_start, int32_t num_tiles, int32_t block_m,
-    const ie_kv_cache* cache, const int32_t* slot_ids, const int32_t* cu_cached, ie_bf16* out,
+    const ie_kv_cache* cache, const int32_t* slot_ids, const int32_t* cu_cached,
+    int32_t num_entries, ie_bf16* out,
     int64_t out_stride_tok, int64_t out_stride_head, void* workspace, size_t workspace_bytes,
     hipStream_t stream) {
     hipError_t e = check_cache(cache);
@@ -848,6 +863,8 @@ extern "C" hipError_t ie_prefill_attention(
     IE_REQUIRE(num_tokens >= 0 && num_tiles >= 0, "negative sizes");
     IE_REQUIRE(block_m > 0, "block_m must be positive");
     IE_REQUIRE(num_q_heads == 2 * cache->num_kv_heads, "num_q_heads must be 2 * num_kv_heads");
+    IE_REQUIRE(num_entries >= 1 && num_entries <= PF_MAX_ENTRIES,
+               "num_entries (the length of slot_ids) must be in [1, 512]");
     if (num_tokens == 0 || num_tiles == 0) return hipSuccess;
     IE_REQUIRE(q && k && v && seq_ids && cu_seqlens && tile_start && slot_ids && cu_cached && out,
                "null pointer");
@@ -898,6 +915,7 @@ extern "C" hipError_t ie_prefill_attention(
     a.sub_per_tile = (block_m + PF_BM - 1) / PF_BM;
     a.hq = num_q_heads;
     a.hkv = cache->num_kv_heads;
+    a.nent = num_entries;
     a.nsb = (int)nsb;
     a.grid = slots;
     a.qk_scale = (float)(0.08838834764831845 * 1.4426950408889634);  // D^-0.5 * log2(e), D = 128

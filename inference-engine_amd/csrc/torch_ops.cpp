@@ -270,7 +270,8 @@ at::Tensor prefill_attention(const at::Tensor& q, const at::Tensor& k, const at:
     ok(ie_prefill_attention(bf(q), q.stride(0), q.stride(1), bf(k), k.stride(0), k.stride(1),
                             bf(v), v.stride(0), v.stride(1), N, (int32_t)q.size(1), i32(seq_ids),
                             i32(cu_seqlens), i32(tile_start), (int32_t)tile_start.size(0),
-                            (int32_t)block_m, &c, i32(slot_ids), i32(cu_cached), bfm(out),
+                            (int32_t)block_m, &c, i32(slot_ids), i32(cu_cached),
+                            (int32_t)slot_ids.size(0), bfm(out),
                             out.stride(0), out.stride(1), ws.data_ptr(), ws_bytes, stream_of(q)),
        "prefill_attention");
     return out;
