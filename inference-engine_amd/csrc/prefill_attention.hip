@@ -47,6 +47,9 @@ constexpr int PF_BM = 64;  // packed rows per sub-block
 constexpr int PF_BN = 64;  // keys per tile
 constexpr int PF_D = 128;
 constexpr int PF_THREADS = 256;
+#ifndef IE_PREFILL_PIPELINE
+#define IE_PREFILL_PIPELINE 1
+#endif
 #ifndef IE_PREFILL_MAXP
 #define IE_PREFILL_MAXP 8
 #endif
@@ -383,6 +386,66 @@ __device__ __forceinline__ void stage_tile(const TileRegs& r, uint8_t* s_k, uint
     }
 }
 
+// Prefix tiles, K and V handled separately (the pipelined prefix loop stages K two tiles and V
+// one tile ahead of the MFMAs): the int8 rows and per-key scales of one tile, in registers
+// between load and staging. Same lane mappings as load_tile / stage_tile.
+struct PfxK {
+    uint32_t kw[8];
+    float kscale, kbias;
+};
+struct PfxV {
+    u32x2 vw[4];
+    float vscale;
+};
+__device__ __forceinline__ void load_pk(PfxK& r, const TileSrc& src, int kbase, int P) {
+    const int tid = threadIdx.x;
+    const int off = (kbase + (tid >> 2)) * PF_D + 32 * (tid & 3);
+    const u32x4 b0 = ld128(src.pk, off), b1 = ld128(src.pk, off + 16);
+    r.kw[0] = b0.x; r.kw[1] = b0.y; r.kw[2] = b0.z; r.kw[3] = b0.w;
+    r.kw[4] = b1.x; r.kw[5] = b1.y; r.kw[6] = b1.z; r.kw[7] = b1.w;
+    const int kk = kbase + (tid & (PF_BN - 1));
+    r.kscale = ldf(src.pks, 4 * kk);
+    r.kbias = kk < P ? 0.f : -INFINITY;
+}
+__device__ __forceinline__ void load_pv(PfxV& r, const TileSrc& src, int kbase) {
+    const int tid = threadIdx.x;
+    const int kg = tid & 15, dg = tid >> 4;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) r.vw[u] = ld64(src.pv, (kbase + 4 * kg + u) * PF_D + 8 * dg);
+    r.vscale = ldf(src.pvs, 4 * (kbase + (tid & (PF_BN - 1))));
+}
+__device__ __forceinline__ void stage_pk(const PfxK& r, uint8_t* s_k, float* s_ksc, float* s_kb,
+                                         float qk_scale) {
+    const int tid = threadIdx.x;
+    uint32_t w[16];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        w[2 * i] = hi16pair(sbyte(r.kw[i], 0), sbyte(r.kw[i], 1));
+        w[2 * i + 1] = hi16pair(sbyte(r.kw[i], 2), sbyte(r.kw[i], 3));
+    }
+    uint8_t* dst = s_k + ks_off(tid >> 2, 4 * (tid & 3));
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        *reinterpret_cast<u32x4*>(dst + 16 * i) = u32x4{w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]};
+    if (tid < PF_BN) {
+        s_ksc[tid] = r.kscale * qk_scale;
+        s_kb[tid] = r.kbias;
+    }
+}
+__device__ __forceinline__ void stage_pv(const PfxV& r, uint8_t* s_vt, float* s_vsc) {
+    const int tid = threadIdx.x;
+    const int kg = tid & 15, dg = tid >> 4;
+    uint8_t* dst = s_vt + vt_off4(8 * dg, kg);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int wj = j >> 2, bj = j & 3;
+        const uint32_t p01 = hi16pair(sbyte(r.vw[0][wj], bj), sbyte(r.vw[1][wj], bj));
+        const uint32_t p23 = hi16pair(sbyte(r.vw[2][wj], bj), sbyte(r.vw[3][wj], bj));
+        *reinterpret_cast<u32x2*>(dst + j * VT_STRIDE) = u32x2{p01, p23};
+    }
+    if (tid < PF_BN) s_vsc[tid] = r.vscale;
+}
+
 // Per-wave running state: O^T accumulators (lane: d = 16mt + 4g + i, row = 16nt + l16) and the
 // base-2 running max / sum of the lane's two rows.
 struct WaveState {
@@ -395,20 +458,36 @@ struct WaveState {
 // sees whole, or that cross the causal diagonal / the sub-block's last row (masked per key).
 enum : int { TILE_PREFIX = 0, TILE_PREFIX_PARTIAL = 1, TILE_CHUNK = 2, TILE_CHUNK_DIAG = 3 };
 
-// MFMA + softmax work of one staged 64-key tile for one wave. Chunk key c is visible to row m
-// iff seq_start + c <= m and c < r1 - seq_start (lim0 / lim1: last visible key of the lane's
-// two rows).
-template <int KIND>
-__device__ __forceinline__ void tile_compute(WaveState& w, const bf16x8 (&qf)[2][4],
-                                             const uint8_t* s_k, const uint8_t* s_vt,
-                                             const float* s_ksc, const float* s_kb,
-                                             const float* s_vsc, int kbase, int lim0, int lim1,
-                                             float qk_scale, int l16, int g) {
-    constexpr bool PREFIX = KIND == TILE_PREFIX || KIND == TILE_PREFIX_PARTIAL;
-    // ---- S^T = K . Q^T (64 keys x 32 rows) ----
-    // Fragment reads run one 16-key step ahead of the MFMAs that consume them.
+// The three parts of one wave's work on a staged 64-key tile (the sum is tile_compute):
+//   tile_scores   S^T = K . Q^T, 64 keys x 32 rows, 32 MFMAs (4 steps of 16 keys)
+//   softmax       scale, mask, online softmax (base 2) -> P^T as bf16 MFMA B fragments
+//   tile_pv       O^T += V^T . P^T, 32 MFMAs
+// Chunk key c is visible to row m iff seq_start + c <= m and c < r1 - seq_start (lim0 / lim1:
+// last visible key of the lane's two rows).
+
+// One 16-key step of S^T: reads the step's K fragments and runs the two 4-MFMA chains.
+__device__ __forceinline__ void score_step(f32x4 (&st)[4][2], const bf16x8 (&qf)[2][4],
+                                           const uint8_t* kfrag, int mt) {
     const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
-    f32x4 st[4][2];
+    bf16x8 kf[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+        kf[ks] = __builtin_bit_cast(
+            bf16x8, *reinterpret_cast<const u32x4*>(kfrag + 16 * mt * KS_STRIDE + 64 * ks));
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+        f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[0], qf[nt][0], zero4, 0, 0, 0);
+#pragma unroll
+        for (int ks = 1; ks < 4; ++ks)
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[ks], qf[nt][ks], c, 0, 0, 0);
+        st[mt][nt] = c;
+    }
+}
+
+__device__ __forceinline__ void tile_scores(f32x4 (&st)[4][2], const bf16x8 (&qf)[2][4],
+                                            const uint8_t* s_k, int l16, int g) {
+    // fragment reads run one 16-key step ahead of the MFMAs that consume them
+    const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
     const uint8_t* kfrag = s_k + ks_off(l16, g);
     auto read_k = [&](bf16x8 (&kf)[4], int mt) {
 #pragma unroll
@@ -431,7 +510,84 @@ __device__ __forceinline__ void tile_compute(WaveState& w, const bf16x8 (&qf)[2]
             st[mt][nt] = c;
         }
     }
-    // the first V^T fragments are read while the softmax runs
+}
+
+// Softmax part 1 for row tile nt: scale (relative to the running max), mask, tile max of the
+// lane's row. Branch-free.
+template <int KIND>
+__device__ __forceinline__ float softmax_scale(f32x4 (&st)[4][2], int nt, float mold,
+                                               const float* s_ksc, const float* s_kb, int kbase,
+                                               int lim, float qk_scale, int g) {
+    constexpr bool PREFIX = KIND == TILE_PREFIX || KIND == TILE_PREFIX_PARTIAL;
+    const float nmb = mold == -INFINITY ? 0.f : -mold;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+        f32x4 ksv = {qk_scale, qk_scale, qk_scale, qk_scale};
+        if (PREFIX) ksv = *reinterpret_cast<const f32x4*>(s_ksc + 16 * mt + 4 * g);
+        f32x4 kbv = {0.f, 0.f, 0.f, 0.f};
+        if (KIND == TILE_PREFIX_PARTIAL) kbv = *reinterpret_cast<const f32x4*>(s_kb + 16 * mt + 4 * g);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float x = __builtin_fmaf(st[mt][nt][i], ksv[i], nmb);
+            if (KIND == TILE_PREFIX_PARTIAL) x += kbv[i];  // -inf past P
+            if (KIND == TILE_CHUNK_DIAG) x = kbase + 16 * mt + 4 * g + i <= lim ? x : -INFINITY;
+            st[mt][nt][i] = x;
+            mx = fmaxf(mx, x);
+        }
+    }
+    return max_xor32(max_xor16(mx));
+}
+
+// Softmax part 2 for row tile nt: the lazy running max. It moves only when the row's tile max
+// exceeds it by more than RESCALE_SLACK (or on the row's first visible key), so probabilities
+// stay <= 2^RESCALE_SLACK; then the wave shifts its scores once more and rescales the
+// accumulators. A rare, wave-uniform branch.
+__device__ __forceinline__ void softmax_rescale(WaveState& w, f32x4 (&st)[4][2], int nt,
+                                                float mx) {
+    const float mold = w.m[nt];
+    const bool move = mx != -INFINITY && (mold == -INFINITY || mx > RESCALE_SLACK);
+    if (__ballot(move)) {
+        const float shift = move ? mx : 0.f;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) st[mt][nt] -= shift;
+        const float nmb = mold == -INFINITY ? 0.f : -mold;
+        const float mnew = move ? -nmb + shift : mold;
+        const float alpha = __builtin_amdgcn_exp2f(mold - mnew);  // 1 unless moved; 0 from -inf
+        w.m[nt] = mnew;
+        w.l[nt] *= alpha;
+        if (__ballot(move && mold != -INFINITY)) {  // accumulators are 0 before any key
+#pragma unroll
+            for (int mt = 0; mt < 8; ++mt) w.acc[mt][nt] *= alpha;
+        }
+    }
+}
+
+// Softmax part 3 for row tile nt: probabilities, row sum, bf16 P^T fragments (prefix tiles:
+// P x v_scale). Branch-free.
+template <bool PREFIX>
+__device__ __forceinline__ void softmax_p(WaveState& w, const f32x4 (&st)[4][2], int nt,
+                                          uint32_t (&pfrag)[2][2][4], const float* s_vsc,
+                                          int g) {
+    float lsum = 0.f;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+        f32x4 vsv = {1.f, 1.f, 1.f, 1.f};
+        if (PREFIX) vsv = *reinterpret_cast<const f32x4*>(s_vsc + 16 * mt + 4 * g);
+#pragma unroll
+        for (int i = 0; i < 4; i += 2) {
+            const float p0 = __builtin_amdgcn_exp2f(st[mt][nt][i]);
+            const float p1 = __builtin_amdgcn_exp2f(st[mt][nt][i + 1]);
+            lsum += p0 + p1;
+            pfrag[mt >> 1][nt][(mt & 1) * 2 + i / 2] =
+                PREFIX ? pack_bf16x2(p0 * vsv[i], p1 * vsv[i + 1]) : pack_bf16x2(p0, p1);
+        }
+    }
+    w.l[nt] += lsum;
+}
+
+__device__ __forceinline__ void tile_pv(WaveState& w, const uint32_t (&pfrag)[2][2][4],
+                                        const uint8_t* s_vt, int l16, int g) {
     const uint8_t* vfrag = s_vt + l16 * VT_STRIDE + 16 * g;
     auto read_v = [&](bf16x8 (&vf)[2], int mt) {
 #pragma unroll
@@ -440,68 +596,7 @@ __device__ __forceinline__ void tile_compute(WaveState& w, const bf16x8 (&qf)[2]
                 bf16x8, *reinterpret_cast<const u32x4*>(vfrag + 16 * mt * VT_STRIDE + 64 * s2));
     };
     bf16x8 vf[2][2];
-    __builtin_amdgcn_sched_barrier(0);
     read_v(vf[0], 0);
-    // ---- scale, mask, online softmax (base 2) ----
-    // Scores are formed relative to the running max m in the scaling fma. The running max is lazy:
-    // it moves only when a row's tile max exceeds it by more than RESCALE_SLACK (or on the row's
-    // first visible key), so probabilities stay <= 2^RESCALE_SLACK; then the wave shifts its scores
-    // once more and rescales the accumulators.
-    uint32_t pfrag[2][2][4];  // [32-key step][row tile] bf16x8 as 4 words
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-        __builtin_amdgcn_sched_barrier(0);
-        const int lim = nt ? lim1 : lim0;
-        const float mold = w.m[nt];
-        const float nmb = mold == -INFINITY ? 0.f : -mold;
-        float mx = -INFINITY;
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-            f32x4 ksv = {qk_scale, qk_scale, qk_scale, qk_scale};
-            if (PREFIX) ksv = *reinterpret_cast<const f32x4*>(s_ksc + 16 * mt + 4 * g);
-            f32x4 kbv = zero4;
-            if (KIND == TILE_PREFIX_PARTIAL) kbv = *reinterpret_cast<const f32x4*>(s_kb + 16 * mt + 4 * g);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                float x = __builtin_fmaf(st[mt][nt][i], ksv[i], nmb);
-                if (KIND == TILE_PREFIX_PARTIAL) x += kbv[i];  // -inf past P
-                if (KIND == TILE_CHUNK_DIAG) x = kbase + 16 * mt + 4 * g + i <= lim ? x : -INFINITY;
-                st[mt][nt][i] = x;
-                mx = fmaxf(mx, x);
-            }
-        }
-        mx = max_xor32(max_xor16(mx));
-        const bool move = mx != -INFINITY && (mold == -INFINITY || mx > RESCALE_SLACK);
-        const float shift = move ? mx : 0.f;
-        if (__ballot(move)) {
-#pragma unroll
-            for (int mt = 0; mt < 4; ++mt) st[mt][nt] -= shift;
-            const float mnew = move ? -nmb + shift : mold;
-            const float alpha = __builtin_amdgcn_exp2f(mold - mnew);  // 1 unless moved; 0 from -inf
-            w.m[nt] = mnew;
-            w.l[nt] *= alpha;
-            if (__ballot(move && mold != -INFINITY)) {  // accumulators are 0 before any key
-#pragma unroll
-                for (int mt = 0; mt < 8; ++mt) w.acc[mt][nt] *= alpha;
-            }
-        }
-        float lsum = 0.f;
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-            f32x4 vsv = {1.f, 1.f, 1.f, 1.f};
-            if (PREFIX) vsv = *reinterpret_cast<const f32x4*>(s_vsc + 16 * mt + 4 * g);
-#pragma unroll
-            for (int i = 0; i < 4; i += 2) {
-                const float p0 = __builtin_amdgcn_exp2f(st[mt][nt][i]);
-                const float p1 = __builtin_amdgcn_exp2f(st[mt][nt][i + 1]);
-                lsum += p0 + p1;
-                pfrag[mt >> 1][nt][(mt & 1) * 2 + i / 2] =
-                    PREFIX ? pack_bf16x2(p0 * vsv[i], p1 * vsv[i + 1]) : pack_bf16x2(p0, p1);
-            }
-        }
-        w.l[nt] += lsum;
-    }
-    // ---- O^T += V^T . P^T ----
 #pragma unroll
     for (int mt = 0; mt < 8; ++mt) {
         __builtin_amdgcn_sched_barrier(0);
@@ -518,6 +613,27 @@ __device__ __forceinline__ void tile_compute(WaveState& w, const bf16x8 (&qf)[2]
             }
         }
     }
+}
+
+template <int KIND>
+__device__ __forceinline__ void tile_compute(WaveState& w, const bf16x8 (&qf)[2][4],
+                                             const uint8_t* s_k, const uint8_t* s_vt,
+                                             const float* s_ksc, const float* s_kb,
+                                             const float* s_vsc, int kbase, int lim0, int lim1,
+                                             float qk_scale, int l16, int g) {
+    constexpr bool PREFIX = KIND == TILE_PREFIX || KIND == TILE_PREFIX_PARTIAL;
+    f32x4 st[4][2];
+    tile_scores(st, qf, s_k, l16, g);
+    uint32_t pfrag[2][2][4];  // [32-key step][row tile] bf16x8 as 4 words
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+        __builtin_amdgcn_sched_barrier(0);
+        const float mx = softmax_scale<KIND>(st, nt, w.m[nt], s_ksc, s_kb, kbase,
+                                             nt ? lim1 : lim0, qk_scale, g);
+        softmax_rescale(w, st, nt, mx);
+        softmax_p<PREFIX>(w, st, nt, pfrag, s_vsc, g);
+    }
+    tile_pv(w, pfrag, s_vt, l16, g);
 }
 
 // Q^T fragments of this wave: lane holds q[row = wr0 + 16nt + l16][d = 32ks + 8g .. +7], as
@@ -568,8 +684,8 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBloc
     // two tile buffers: tile i is staged into buffer i & 1 while the other one is computed on
     __shared__ __attribute__((aligned(16))) uint8_t s_k[2][PF_BN * KS_STRIDE];
     __shared__ __attribute__((aligned(16))) uint8_t s_vt[2][PF_D * VT_STRIDE];
-    __shared__ __attribute__((aligned(16))) float s_ksc[2][PF_BN];
-    __shared__ __attribute__((aligned(16))) float s_kb[2][PF_BN];
+    __shared__ __attribute__((aligned(16))) float s_ksc[3][PF_BN];  // 3 slots: the pipelined
+    __shared__ __attribute__((aligned(16))) float s_kb[3][PF_BN];   // prefix loop rotates them
     __shared__ __attribute__((aligned(16))) float s_vsc[2][PF_BN];
 
     const float* cal = a.c.k_calibration + s.slot * a.c.cal_stride_slot + hk * a.c.cal_stride_head;
@@ -628,6 +744,111 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBloc
     ws.m[0] = ws.m[1] = -INFINITY;
     ws.l[0] = ws.l[1] = 0.f;
 
+#if IE_PREFILL_PIPELINE
+    bf16x8 qf[2][4];
+    int kt = kt_begin;
+    const int prefix_end = min(kt_end, s.npt);
+    TileRegs pf;
+    if (kt < prefix_end) {
+        // Prefix tiles, software-pipelined per wave: in step j the MFMAs of S_{j+1} run beside
+        // the softmax of tile j, and the PV MFMAs of tile j beside the staging of K_{j+2} and
+        // V_{j+1}, whose loads were issued one step earlier. K data buffers alternate (K_j is
+        // last read by S_j one step earlier), V buffers alternate, the K scales rotate over
+        // three slots (tile j's are read by its softmax while K_{j+2}'s are written).
+        const int n = prefix_end - kt, kb0 = kt * PF_BN;
+        PfxK pk;
+        PfxV pv;
+        {
+            PfxK pk1;
+            load_pk(pk, src, kb0, s.P);
+            load_pv(pv, src, kb0);
+            if (n > 1) load_pk(pk1, src, kb0 + PF_BN, s.P);
+            load_q<true>(qf, a, wr0, s.r1, h, cal, l16, g);
+            stage_pk(pk, s_k[0], s_ksc[0], s_kb[0], a.qk_scale);
+            stage_pv(pv, s_vt[0], s_vsc[0]);
+            if (n > 1) stage_pk(pk1, s_k[1], s_ksc[1], s_kb[1], a.qk_scale);
+        }
+        if (n > 2) load_pk(pk, src, kb0 + 2 * PF_BN, s.P);
+        if (n > 1) load_pv(pv, src, kb0 + PF_BN);
+        __syncthreads();
+        f32x4 sc[4][2];
+        tile_scores(sc, qf, s_k[0], l16, g);
+        __syncthreads();  // every wave has read K_0 before step 0 stages K_2 over it
+        uint32_t pfrag[2][2][4];
+        int slot = 0;  // K-scale slot of tile j
+        for (int j = 0; j < n - 1; ++j) {
+            const int nslot = slot == 2 ? 0 : slot + 1, fslot = nslot == 2 ? 0 : nslot + 1;
+            const uint8_t* kfrag = s_k[(j + 1) & 1] + ks_off(l16, g);
+            f32x4 sn[4][2];
+            score_step(sn, qf, kfrag, 0);
+            score_step(sn, qf, kfrag, 1);
+            const float mx0 = softmax_scale<TILE_PREFIX>(sc, 0, ws.m[0], s_ksc[slot], s_kb[slot], 0,
+                                                         0, a.qk_scale, g);
+            const float mx1 = softmax_scale<TILE_PREFIX>(sc, 1, ws.m[1], s_ksc[slot], s_kb[slot], 0,
+                                                         0, a.qk_scale, g);
+            softmax_rescale(ws, sc, 0, mx0);
+            softmax_rescale(ws, sc, 1, mx1);
+            score_step(sn, qf, kfrag, 2);
+            score_step(sn, qf, kfrag, 3);
+            softmax_p<true>(ws, sc, 0, pfrag, s_vsc[j & 1], g);
+            softmax_p<true>(ws, sc, 1, pfrag, s_vsc[j & 1], g);
+            tile_pv(ws, pfrag, s_vt[j & 1], l16, g);
+            if (j + 2 < n) stage_pk(pk, s_k[j & 1], s_ksc[fslot], s_kb[fslot], a.qk_scale);
+            stage_pv(pv, s_vt[(j + 1) & 1], s_vsc[(j + 1) & 1]);
+            if (j + 3 < n) load_pk(pk, src, kb0 + (j + 3) * PF_BN, s.P);
+            if (j + 2 < n) load_pv(pv, src, kb0 + (j + 2) * PF_BN);
+            __syncthreads();
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) {
+                sc[mt][0] = sn[mt][0];
+                sc[mt][1] = sn[mt][1];
+            }
+            slot = nslot;
+        }
+        // the last prefix tile of the piece (the only one that can hold keys past P)
+        const int j = n - 1;
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+            const float mx = softmax_scale<TILE_PREFIX_PARTIAL>(sc, nt, ws.m[nt], s_ksc[slot],
+                                                                s_kb[slot], 0, 0, a.qk_scale, g);
+            softmax_rescale(ws, sc, nt, mx);
+            softmax_p<true>(ws, sc, nt, pfrag, s_vsc[j & 1], g);
+        }
+        tile_pv(ws, pfrag, s_vt[j & 1], l16, g);
+        __syncthreads();  // the chunk tiles reuse the buffers
+        kt = prefix_end;
+    }
+    uint32_t pfa = 0, pfb = 0;
+    if (kt < kt_end) {
+        load_tile<false>(pf, src, (kt - s.npt) * PF_BN, s.P);
+        pfa = prefetch(kt + 1);
+        pfb = prefetch(kt + 2);
+        load_q<false>(qf, a, wr0, s.r1, h, cal, l16, g);
+        stage_tile<false>(pf, s_k[(kt - kt_begin) & 1], s_vt[(kt - kt_begin) & 1],
+                          s_ksc[(kt - kt_begin) & 1], s_kb[(kt - kt_begin) & 1],
+                          s_vsc[(kt - kt_begin) & 1], a.qk_scale);
+        __syncthreads();
+        for (; kt < kt_end; ++kt) {
+            const int buf = (kt - kt_begin) & 1;
+            const bool has_next = kt + 1 < kt_end;
+            const int kc = (kt - s.npt) * PF_BN;
+            if (has_next) load_tile<false>(pf, src, kc + PF_BN, s.P);
+            consume(pfa);
+            pfa = pfb;
+            pfb = prefetch(kt + 3);
+            // the whole tile is visible to every row of this wave: no per-key mask
+            if (kc + PF_BN - 1 <= min(wr0 - s.seq_start, clim))
+                tile_compute<TILE_CHUNK>(ws, qf, s_k[buf], s_vt[buf], s_ksc[buf], s_kb[buf],
+                                         s_vsc[buf], kc, lim0, lim1, a.qk_scale, l16, g);
+            else
+                tile_compute<TILE_CHUNK_DIAG>(ws, qf, s_k[buf], s_vt[buf], s_ksc[buf], s_kb[buf],
+                                              s_vsc[buf], kc, lim0, lim1, a.qk_scale, l16, g);
+            if (has_next) stage_tile<false>(pf, s_k[buf ^ 1], s_vt[buf ^ 1], s_ksc[buf ^ 1],
+                                            s_kb[buf ^ 1], s_vsc[buf ^ 1], a.qk_scale);
+            __syncthreads();
+        }
+    }
+#else
     // the first tile's loads and the Q loads are in flight together
     TileRegs pf;
     load(pf, kt_begin);
@@ -694,6 +915,7 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBloc
         }
     }
 
+#endif
     // ---- results: lane holds row = wr0 + 16nt + l16, channels d = 16mt + 4g + i ----
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
