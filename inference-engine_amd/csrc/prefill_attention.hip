@@ -414,8 +414,7 @@ __device__ __forceinline__ void load_pv(PfxV& r, const TileSrc& src, int kbase) 
     for (int u = 0; u < 4; ++u) r.vw[u] = ld64(src.pv, (kbase + 4 * kg + u) * PF_D + 8 * dg);
     r.vscale = ldf(src.pvs, 4 * (kbase + (tid & (PF_BN - 1))));
 }
-__device__ __forceinline__ void stage_pk(const PfxK& r, uint8_t* s_k, float* s_ksc, float* s_kb,
-                                         float qk_scale) {
+__device__ __forceinline__ void stage_pk(const PfxK& r, uint8_t* s_k) {
     const int tid = threadIdx.x;
     uint32_t w[16];
 #pragma unroll
@@ -427,12 +426,16 @@ __device__ __forceinline__ void stage_pk(const PfxK& r, uint8_t* s_k, float* s_k
 #pragma unroll
     for (int i = 0; i < 4; ++i)
         *reinterpret_cast<u32x4*>(dst + 16 * i) = u32x4{w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]};
+}
+__device__ __forceinline__ void stage_pk_scales(const PfxK& r, float* s_ksc, float* s_kb,
+                                                float qk_scale) {
+    const int tid = threadIdx.x;
     if (tid < PF_BN) {
         s_ksc[tid] = r.kscale * qk_scale;
         s_kb[tid] = r.kbias;
     }
 }
-__device__ __forceinline__ void stage_pv(const PfxV& r, uint8_t* s_vt, float* s_vsc) {
+__device__ __forceinline__ void stage_pv(const PfxV& r, uint8_t* s_vt) {
     const int tid = threadIdx.x;
     const int kg = tid & 15, dg = tid >> 4;
     uint8_t* dst = s_vt + vt_off4(8 * dg, kg);
@@ -443,7 +446,9 @@ __device__ __forceinline__ void stage_pv(const PfxV& r, uint8_t* s_vt, float* s_
         const uint32_t p23 = hi16pair(sbyte(r.vw[2][wj], bj), sbyte(r.vw[3][wj], bj));
         *reinterpret_cast<u32x2*>(dst + j * VT_STRIDE) = u32x2{p01, p23};
     }
-    if (tid < PF_BN) s_vsc[tid] = r.vscale;
+}
+__device__ __forceinline__ void stage_pv_scales(const PfxV& r, float* s_vsc) {
+    if (threadIdx.x < PF_BN) s_vsc[threadIdx.x] = r.vscale;
 }
 
 // Per-wave running state: O^T accumulators (lane: d = 16mt + 4g + i, row = 16nt + l16) and the
@@ -586,6 +591,7 @@ __device__ __forceinline__ void softmax_p(WaveState& w, const f32x4 (&st)[4][2],
     w.l[nt] += lsum;
 }
 
+template <bool FENCE = true>
 __device__ __forceinline__ void tile_pv(WaveState& w, const uint32_t (&pfrag)[2][2][4],
                                         const uint8_t* s_vt, int l16, int g) {
     const uint8_t* vfrag = s_vt + l16 * VT_STRIDE + 16 * g;
@@ -599,7 +605,7 @@ __device__ __forceinline__ void tile_pv(WaveState& w, const uint32_t (&pfrag)[2]
     read_v(vf[0], 0);
 #pragma unroll
     for (int mt = 0; mt < 8; ++mt) {
-        __builtin_amdgcn_sched_barrier(0);
+        if (FENCE) __builtin_amdgcn_sched_barrier(0);
         if (mt < 7) read_v(vf[(mt + 1) & 1], mt + 1);
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
@@ -764,9 +770,14 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBloc
             load_pv(pv, src, kb0);
             if (n > 1) load_pk(pk1, src, kb0 + PF_BN, s.P);
             load_q<true>(qf, a, wr0, s.r1, h, cal, l16, g);
-            stage_pk(pk, s_k[0], s_ksc[0], s_kb[0], a.qk_scale);
-            stage_pv(pv, s_vt[0], s_vsc[0]);
-            if (n > 1) stage_pk(pk1, s_k[1], s_ksc[1], s_kb[1], a.qk_scale);
+            stage_pk(pk, s_k[0]);
+            stage_pk_scales(pk, s_ksc[0], s_kb[0], a.qk_scale);
+            stage_pv(pv, s_vt[0]);
+            stage_pv_scales(pv, s_vsc[0]);
+            if (n > 1) {
+                stage_pk(pk1, s_k[1]);
+                stage_pk_scales(pk1, s_ksc[1], s_kb[1], a.qk_scale);
+            }
         }
         if (n > 2) load_pk(pk, src, kb0 + 2 * PF_BN, s.P);
         if (n > 1) load_pv(pv, src, kb0 + PF_BN);
@@ -792,9 +803,13 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBloc
             score_step(sn, qf, kfrag, 3);
             softmax_p<true>(ws, sc, 0, pfrag, s_vsc[j & 1], g);
             softmax_p<true>(ws, sc, 1, pfrag, s_vsc[j & 1], g);
-            tile_pv(ws, pfrag, s_vt[j & 1], l16, g);
-            if (j + 2 < n) stage_pk(pk, s_k[j & 1], s_ksc[fslot], s_kb[fslot], a.qk_scale);
-            stage_pv(pv, s_vt[(j + 1) & 1], s_vsc[(j + 1) & 1]);
+            // PV and the staging of the next tiles in one scheduling region (no fences, no
+            // branches), so the conversions fill the MFMA issue gaps
+            tile_pv<false>(ws, pfrag, s_vt[j & 1], l16, g);
+            stage_pk(pk, s_k[j & 1]);  // K_{j+2}; a harmless copy of stale data if j + 2 == n
+            stage_pv(pv, s_vt[(j + 1) & 1]);
+            if (j + 2 < n) stage_pk_scales(pk, s_ksc[fslot], s_kb[fslot], a.qk_scale);
+            stage_pv_scales(pv, s_vsc[(j + 1) & 1]);
             if (j + 3 < n) load_pk(pk, src, kb0 + (j + 3) * PF_BN, s.P);
             if (j + 2 < n) load_pv(pv, src, kb0 + (j + 2) * PF_BN);
             __syncthreads();
