@@ -453,9 +453,11 @@ __device__ __forceinline__ void stage_pv_scales(const PfxV& r, float* s_vsc) {
 
 // Per-wave running state: O^T accumulators (lane: d = 16mt + 4g + i, row = 16nt + l16) and the
 // base-2 running max / sum of the lane's two rows.
+// Per row tile nt (the lane's row l16 of it): the running max m, kept as nmb = -m (0 while the
+// row has seen no key), and the running sum l.
 struct WaveState {
     f32x4 acc[8][2];
-    float m[2], l[2];
+    float nmb[2], l[2];
 };
 
 // Tile kinds: prefix tiles (scores scaled per key, P scaled by v_scale per key) that are full or
@@ -517,14 +519,14 @@ __device__ __forceinline__ void tile_scores(f32x4 (&st)[4][2], const bf16x8 (&qf
     }
 }
 
-// Softmax part 1 for row tile nt: scale (relative to the running max), mask, tile max of the
-// lane's row. Branch-free.
+// Softmax part 1 for row tile nt: scale (relative to the running max), mask, and the max over
+// the lane's own 16 keys of the tile (the row's max needs the other three lanes of the row only
+// when the running max moves). Branch-free.
 template <int KIND>
-__device__ __forceinline__ float softmax_scale(f32x4 (&st)[4][2], int nt, float mold,
+__device__ __forceinline__ float softmax_scale(f32x4 (&st)[4][2], int nt, float nmb,
                                                const float* s_ksc, const float* s_kb, int kbase,
                                                int lim, float qk_scale, int g) {
     constexpr bool PREFIX = KIND == TILE_PREFIX || KIND == TILE_PREFIX_PARTIAL;
-    const float nmb = mold == -INFINITY ? 0.f : -mold;
     float mx = -INFINITY;
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
@@ -541,29 +543,33 @@ __device__ __forceinline__ float softmax_scale(f32x4 (&st)[4][2], int nt, float 
             mx = fmaxf(mx, x);
         }
     }
-    return max_xor32(max_xor16(mx));
+    return mx;
 }
 
 // Softmax part 2 for row tile nt: the lazy running max. It moves only when the row's tile max
-// exceeds it by more than RESCALE_SLACK (or on the row's first visible key), so probabilities
-// stay <= 2^RESCALE_SLACK; then the wave shifts its scores once more and rescales the
-// accumulators. A rare, wave-uniform branch.
+// exceeds it by more than RESCALE_SLACK, so probabilities stay <= 2^RESCALE_SLACK, and it is set
+// on the first tile of a work item. A row that sees no key of an item's first tile sees none of
+// its later tiles either (prefix tiles are visible to every row and chunk tiles come in causal
+// order), so that first tile (`first`, wave-uniform) is the only place where a row's first key
+// can appear. The common path is one compare of the lane's own max; in the rare, wave-uniform
+// branch the row's max is reduced over its four lanes (every lane of a row takes the same
+// decision), the wave shifts its scores once more and rescales the accumulators.
 __device__ __forceinline__ void softmax_rescale(WaveState& w, f32x4 (&st)[4][2], int nt,
-                                                float mx) {
-    const float mold = w.m[nt];
-    const bool move = mx != -INFINITY && (mold == -INFINITY || mx > RESCALE_SLACK);
-    if (__ballot(move)) {
-        const float shift = move ? mx : 0.f;
+                                                float mx, bool first) {
+    if (first || __ballot(mx > RESCALE_SLACK)) {
+        const float rmx = max_xor32(max_xor16(mx));
+        const bool move = first ? rmx != -INFINITY : rmx > RESCALE_SLACK;
+        const float shift = move ? rmx : 0.f;
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) st[mt][nt] -= shift;
-        const float nmb = mold == -INFINITY ? 0.f : -mold;
-        const float mnew = move ? -nmb + shift : mold;
-        const float alpha = __builtin_amdgcn_exp2f(mold - mnew);  // 1 unless moved; 0 from -inf
-        w.m[nt] = mnew;
-        w.l[nt] *= alpha;
-        if (__ballot(move && mold != -INFINITY)) {  // accumulators are 0 before any key
+        w.nmb[nt] -= shift;
+        if (!first) {  // before the first tile, l and the accumulators are 0
+            const float alpha = __builtin_amdgcn_exp2f(-shift);  // 1 unless moved
+            w.l[nt] *= alpha;
+            if (__ballot(move)) {
 #pragma unroll
-            for (int mt = 0; mt < 8; ++mt) w.acc[mt][nt] *= alpha;
+                for (int mt = 0; mt < 8; ++mt) w.acc[mt][nt] *= alpha;
+            }
         }
     }
 }
@@ -626,7 +632,7 @@ __device__ __forceinline__ void tile_compute(WaveState& w, const bf16x8 (&qf)[2]
                                              const uint8_t* s_k, const uint8_t* s_vt,
                                              const float* s_ksc, const float* s_kb,
                                              const float* s_vsc, int kbase, int lim0, int lim1,
-                                             float qk_scale, int l16, int g) {
+                                             float qk_scale, int l16, int g, bool first) {
     constexpr bool PREFIX = KIND == TILE_PREFIX || KIND == TILE_PREFIX_PARTIAL;
     f32x4 st[4][2];
     tile_scores(st, qf, s_k, l16, g);
@@ -634,9 +640,9 @@ __device__ __forceinline__ void tile_compute(WaveState& w, const bf16x8 (&qf)[2]
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
         __builtin_amdgcn_sched_barrier(0);
-        const float mx = softmax_scale<KIND>(st, nt, w.m[nt], s_ksc, s_kb, kbase,
+        const float mx = softmax_scale<KIND>(st, nt, w.nmb[nt], s_ksc, s_kb, kbase,
                                              nt ? lim1 : lim0, qk_scale, g);
-        softmax_rescale(w, st, nt, mx);
+        softmax_rescale(w, st, nt, mx, first);
         softmax_p<PREFIX>(w, st, nt, pfrag, s_vsc, g);
     }
     tile_pv(w, pfrag, s_vt, l16, g);
@@ -747,7 +753,7 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBloc
     for (int mt = 0; mt < 8; ++mt)
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) ws.acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    ws.m[0] = ws.m[1] = -INFINITY;
+    ws.nmb[0] = ws.nmb[1] = 0.f;
     ws.l[0] = ws.l[1] = 0.f;
 
 #if IE_PREFILL_PIPELINE
@@ -793,12 +799,12 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBloc
             f32x4 sn[4][2];
             score_step(sn, qf, kfrag, 0);
             score_step(sn, qf, kfrag, 1);
-            const float mx0 = softmax_scale<TILE_PREFIX>(sc, 0, ws.m[0], s_ksc[slot], s_kb[slot], 0,
+            const float mx0 = softmax_scale<TILE_PREFIX>(sc, 0, ws.nmb[0], s_ksc[slot], s_kb[slot], 0,
                                                          0, a.qk_scale, g);
-            const float mx1 = softmax_scale<TILE_PREFIX>(sc, 1, ws.m[1], s_ksc[slot], s_kb[slot], 0,
+            const float mx1 = softmax_scale<TILE_PREFIX>(sc, 1, ws.nmb[1], s_ksc[slot], s_kb[slot], 0,
                                                          0, a.qk_scale, g);
-            softmax_rescale(ws, sc, 0, mx0);
-            softmax_rescale(ws, sc, 1, mx1);
+            softmax_rescale(ws, sc, 0, mx0, j == 0);
+            softmax_rescale(ws, sc, 1, mx1, j == 0);
             score_step(sn, qf, kfrag, 2);
             score_step(sn, qf, kfrag, 3);
             softmax_p<true>(ws, sc, 0, pfrag, s_vsc[j & 1], g);
@@ -824,9 +830,9 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBloc
         const int j = n - 1;
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) {
-            const float mx = softmax_scale<TILE_PREFIX_PARTIAL>(sc, nt, ws.m[nt], s_ksc[slot],
+            const float mx = softmax_scale<TILE_PREFIX_PARTIAL>(sc, nt, ws.nmb[nt], s_ksc[slot],
                                                                 s_kb[slot], 0, 0, a.qk_scale, g);
-            softmax_rescale(ws, sc, nt, mx);
+            softmax_rescale(ws, sc, nt, mx, n == 1);
             softmax_p<true>(ws, sc, nt, pfrag, s_vsc[j & 1], g);
         }
         tile_pv(ws, pfrag, s_vt[j & 1], l16, g);
@@ -854,10 +860,12 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBloc
             // the whole tile is visible to every row of this wave: no per-key mask
             if (kc + PF_BN - 1 <= min(wr0 - s.seq_start, clim))
                 tile_compute<TILE_CHUNK>(ws, qf, s_k[buf], s_vt[buf], s_ksc[buf], s_kb[buf],
-                                         s_vsc[buf], kc, lim0, lim1, a.qk_scale, l16, g);
+                                         s_vsc[buf], kc, lim0, lim1, a.qk_scale, l16, g,
+                                         kt == kt_begin);
             else
                 tile_compute<TILE_CHUNK_DIAG>(ws, qf, s_k[buf], s_vt[buf], s_ksc[buf], s_kb[buf],
-                                              s_vsc[buf], kc, lim0, lim1, a.qk_scale, l16, g);
+                                              s_vsc[buf], kc, lim0, lim1, a.qk_scale, l16, g,
+                                              kt == kt_begin);
             if (has_next) stage_tile<false>(pf, s_k[buf ^ 1], s_vt[buf ^ 1], s_ksc[buf ^ 1],
                                             s_kb[buf ^ 1], s_vsc[buf ^ 1], a.qk_scale);
             __syncthreads();
@@ -884,7 +892,8 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBloc
             pfa = pfb;
             pfb = prefetch(kt + 3);
             tile_compute<TILE_PREFIX>(ws, qf, s_k[buf], s_vt[buf], s_ksc[buf], s_kb[buf],
-                                      s_vsc[buf], kt * PF_BN, 0, 0, a.qk_scale, l16, g);
+                                      s_vsc[buf], kt * PF_BN, 0, 0, a.qk_scale, l16, g,
+                                      kt == kt_begin);
             stage_tile<true>(pf, s_k[buf ^ 1], s_vt[buf ^ 1], s_ksc[buf ^ 1], s_kb[buf ^ 1],
                              s_vsc[buf ^ 1], a.qk_scale);
             __syncthreads();  // next buffer staged; this buffer free for tile kt + 2
@@ -899,7 +908,8 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBloc
         // the only prefix tile of the piece that can hold keys past P (one instance: a second
         // one for full tiles here costs registers)
         tile_compute<TILE_PREFIX_PARTIAL>(ws, qf, s_k[buf], s_vt[buf], s_ksc[buf], s_kb[buf],
-                                          s_vsc[buf], kt * PF_BN, 0, 0, a.qk_scale, l16, g);
+                                          s_vsc[buf], kt * PF_BN, 0, 0, a.qk_scale, l16, g,
+                                          kt == kt_begin);
         if (has_next)
             stage_tile<false>(pf, s_k[buf ^ 1], s_vt[buf ^ 1], s_ksc[buf ^ 1], s_kb[buf ^ 1],
                               s_vsc[buf ^ 1], a.qk_scale);
@@ -920,10 +930,12 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBloc
             // the whole tile is visible to every row of this wave: no per-key mask
             if (kc + PF_BN - 1 <= min(wr0 - s.seq_start, clim))
                 tile_compute<TILE_CHUNK>(ws, qf, s_k[buf], s_vt[buf], s_ksc[buf], s_kb[buf],
-                                         s_vsc[buf], kc, lim0, lim1, a.qk_scale, l16, g);
+                                         s_vsc[buf], kc, lim0, lim1, a.qk_scale, l16, g,
+                                         kt == kt_begin);
             else
                 tile_compute<TILE_CHUNK_DIAG>(ws, qf, s_k[buf], s_vt[buf], s_ksc[buf], s_kb[buf],
-                                              s_vsc[buf], kc, lim0, lim1, a.qk_scale, l16, g);
+                                              s_vsc[buf], kc, lim0, lim1, a.qk_scale, l16, g,
+                                              kt == kt_begin);
             if (has_next) stage_tile<false>(pf, s_k[buf ^ 1], s_vt[buf ^ 1], s_ksc[buf ^ 1],
                                             s_kb[buf ^ 1], s_vsc[buf ^ 1], a.qk_scale);
             __syncthreads();
@@ -956,7 +968,7 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBloc
                     u32x2{pack_bf16x2(x[0] * rl, x[1] * rl), pack_bf16x2(x[2] * rl, x[3] * rl)};
             }
             if (g == 0)
-                *reinterpret_cast<float2*>(a.part_ml + prow * 2) = make_float2(ws.m[nt], l);
+                *reinterpret_cast<float2*>(a.part_ml + prow * 2) = make_float2(l != 0.f ? -ws.nmb[nt] : -INFINITY, l);
         }
     }
 }
