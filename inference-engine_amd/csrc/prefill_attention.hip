@@ -47,9 +47,6 @@ constexpr int PF_BM = 64;  // packed rows per sub-block
 constexpr int PF_BN = 64;  // keys per tile
 constexpr int PF_D = 128;
 constexpr int PF_THREADS = 256;
-#ifndef IE_PREFILL_PIPELINE
-#define IE_PREFILL_PIPELINE 1
-#endif
 #ifndef IE_PREFILL_MAXP
 #define IE_PREFILL_MAXP 8
 #endif
@@ -269,11 +266,10 @@ __device__ Loc schedule(const PrefillArgs& a, int target) {
 }
 
 // Global data of one tile, held in registers between its load and its LDS staging.
+// Chunk tiles (bf16 rows of the packed chunk), in registers between load and staging.
 struct TileRegs {
-    uint32_t kw[16];    // K: key tid>>2, channels [32 (tid&3), +32): int8 (8 words) or bf16
-    uint32_t vw[4][4];  // V: keys 4 (tid&15) + u, channels [8 (tid>>4), +8): int8 (2) or bf16 (4)
-    float kscale, kbias, vscale;  // prefix tiles, key tid & 63: k_scale, score bias (-inf past P),
-                                  // v_scale
+    uint32_t kw[16];    // K: key tid>>2, channels [32 (tid&3), +32)
+    uint32_t vw[4][4];  // V: keys 4 (tid&15) + u, channels [8 (tid>>4), +8)
 };
 
 // Buffer descriptors of one (sub-block, kv head): prefix K/V rows (128 B each, P rows) and scales
@@ -293,109 +289,63 @@ __device__ __forceinline__ float ldf(rsrc_t r, int off) {
     return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
 }
 
-// Issue the loads of a tile. PREFIX: cache keys [kbase, kbase + 64) (int8; zeros at or past P).
-// Otherwise chunk keys: packed rows seq_start + [kbase, kbase + 64) (bf16; zeros at or past the
-// sub-block's last row). No branches: the buffer ranges do the masking.
-template <bool PREFIX>
-__device__ __forceinline__ void load_tile(TileRegs& r, const TileSrc& src, int kbase, int P) {
+// Issue the loads of a chunk tile: packed rows seq_start + [kbase, kbase + 64) (zeros at or past
+// the sub-block's last row: the buffer range does the masking, no branches).
+__device__ __forceinline__ void load_tile(TileRegs& r, const TileSrc& src, int kbase) {
     const int tid = threadIdx.x;
     {
-        const int kk = kbase + (tid >> 2), q4 = tid & 3;
-        if (PREFIX) {
-            const int off = kk * PF_D + 32 * q4;
-            const u32x4 b0 = ld128(src.pk, off), b1 = ld128(src.pk, off + 16);
-            r.kw[0] = b0.x; r.kw[1] = b0.y; r.kw[2] = b0.z; r.kw[3] = b0.w;
-            r.kw[4] = b1.x; r.kw[5] = b1.y; r.kw[6] = b1.z; r.kw[7] = b1.w;
-        } else {
-            const int off = kk * src.ck_stride + 64 * q4;
+        const int off = (kbase + (tid >> 2)) * src.ck_stride + 64 * (tid & 3);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const u32x4 x = ld128(src.ck, off + 16 * i);
-                r.kw[4 * i] = x.x; r.kw[4 * i + 1] = x.y; r.kw[4 * i + 2] = x.z; r.kw[4 * i + 3] = x.w;
-            }
+        for (int i = 0; i < 4; ++i) {
+            const u32x4 x = ld128(src.ck, off + 16 * i);
+            r.kw[4 * i] = x.x; r.kw[4 * i + 1] = x.y; r.kw[4 * i + 2] = x.z; r.kw[4 * i + 3] = x.w;
         }
     }
     {
         const int kg = tid & 15, dg = tid >> 4;
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            const int kk = kbase + 4 * kg + u;
-            if (PREFIX) {
-                const u32x2 b = ld64(src.pv, kk * PF_D + 8 * dg);
-                r.vw[u][0] = b.x; r.vw[u][1] = b.y; r.vw[u][2] = 0u; r.vw[u][3] = 0u;
-            } else {
-                const u32x4 x = ld128(src.cv, kk * src.cv_stride + 16 * dg);
-                r.vw[u][0] = x.x; r.vw[u][1] = x.y; r.vw[u][2] = x.z; r.vw[u][3] = x.w;
-            }
+            const u32x4 x = ld128(src.cv, (kbase + 4 * kg + u) * src.cv_stride + 16 * dg);
+            r.vw[u][0] = x.x; r.vw[u][1] = x.y; r.vw[u][2] = x.z; r.vw[u][3] = x.w;
         }
-    }
-    if (PREFIX) {  // every wave loads the tile's 64 key scales; wave 0 stages them
-        const int kk = kbase + (tid & (PF_BN - 1));
-        r.kscale = ldf(src.pks, 4 * kk);
-        r.vscale = ldf(src.pvs, 4 * kk);
-        r.kbias = kk < P ? 0.f : -INFINITY;
     }
 }
 
-// Write a loaded tile to LDS: K as [key][d] bf16, V as [d][key] bf16 (int8 keys converted
-// exactly), and for prefix tiles the per-key scales.
-template <bool PREFIX>
-__device__ __forceinline__ void stage_tile(const TileRegs& r, uint8_t* s_k, uint8_t* s_vt,
-                                           float* s_ksc, float* s_kb, float* s_vsc,
-                                           float qk_scale) {
+// Write a loaded chunk tile to LDS: K as [key][d], V as [d][key] (bf16).
+__device__ __forceinline__ void stage_tile(const TileRegs& r, uint8_t* s_k, uint8_t* s_vt) {
     const int tid = threadIdx.x;
     {
-        const int key = tid >> 2, q4 = tid & 3;
-        uint32_t w[16];
-        if (PREFIX) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                w[2 * i] = hi16pair(sbyte(r.kw[i], 0), sbyte(r.kw[i], 1));
-                w[2 * i + 1] = hi16pair(sbyte(r.kw[i], 2), sbyte(r.kw[i], 3));
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) w[i] = r.kw[i];
-        }
-        uint8_t* dst = s_k + ks_off(key, 4 * q4);
+        uint8_t* dst = s_k + ks_off(tid >> 2, 4 * (tid & 3));
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            *reinterpret_cast<u32x4*>(dst + 16 * i) = u32x4{w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]};
+            *reinterpret_cast<u32x4*>(dst + 16 * i) =
+                u32x4{r.kw[4 * i], r.kw[4 * i + 1], r.kw[4 * i + 2], r.kw[4 * i + 3]};
     }
     {
         const int kg = tid & 15, dg = tid >> 4;
         uint8_t* dst = s_vt + vt_off4(8 * dg, kg);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            uint32_t p01, p23;
-            if (PREFIX) {  // channel j of key u: byte j of the key's 8 bytes
-                p01 = hi16pair(sbyte(r.vw[0][j >> 2], j & 3), sbyte(r.vw[1][j >> 2], j & 3));
-                p23 = hi16pair(sbyte(r.vw[2][j >> 2], j & 3), sbyte(r.vw[3][j >> 2], j & 3));
-            } else {  // channel j of key u: bf16 half (j & 1) of word j >> 1
-                const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
-                p01 = __builtin_amdgcn_perm(r.vw[1][j >> 1], r.vw[0][j >> 1], sel);
-                p23 = __builtin_amdgcn_perm(r.vw[3][j >> 1], r.vw[2][j >> 1], sel);
-            }
+        for (int j = 0; j < 8; ++j) {  // channel j of key u: bf16 half (j & 1) of word j >> 1
+            const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+            const uint32_t p01 = __builtin_amdgcn_perm(r.vw[1][j >> 1], r.vw[0][j >> 1], sel);
+            const uint32_t p23 = __builtin_amdgcn_perm(r.vw[3][j >> 1], r.vw[2][j >> 1], sel);
             *reinterpret_cast<u32x2*>(dst + j * VT_STRIDE) = u32x2{p01, p23};
         }
     }
-    if (PREFIX && tid < PF_BN) {
-        s_ksc[tid] = r.kscale * qk_scale;
-        s_kb[tid] = r.kbias;
-        s_vsc[tid] = r.vscale;
-    }
 }
 
-// Prefix tiles, K and V handled separately (the pipelined prefix loop stages K two tiles and V
-// one tile ahead of the MFMAs): the int8 rows and per-key scales of one tile, in registers
-// between load and staging. Same lane mappings as load_tile / stage_tile.
+// Prefix tiles, K and V handled separately (the prefix loop stages K two tiles and V one tile
+// ahead of the MFMAs): the int8 rows and per-key scales of one tile, in registers between load
+// and staging. Same lane mappings as load_tile / stage_tile. K is staged as exact bf16 integers
+// (its scale multiplies the scores); V is staged dequantized, bf16(v * v_scale), the rounding
+// the reference's dequantization applies, so P needs no per-key factor.
 struct PfxK {
     uint32_t kw[8];
     float kscale, kbias;
 };
 struct PfxV {
     u32x2 vw[4];
-    float vscale;
+    f32x4 vs;  // v_scale of the lane's four keys (0 past P: out of the buffer range)
 };
 __device__ __forceinline__ void load_pk(PfxK& r, const TileSrc& src, int kbase, int P) {
     const int tid = threadIdx.x;
@@ -412,7 +362,7 @@ __device__ __forceinline__ void load_pv(PfxV& r, const TileSrc& src, int kbase) 
     const int kg = tid & 15, dg = tid >> 4;
 #pragma unroll
     for (int u = 0; u < 4; ++u) r.vw[u] = ld64(src.pv, (kbase + 4 * kg + u) * PF_D + 8 * dg);
-    r.vscale = ldf(src.pvs, 4 * (kbase + (tid & (PF_BN - 1))));
+    r.vs = __builtin_bit_cast(f32x4, ld128(src.pvs, 4 * (kbase + 4 * kg)));
 }
 __device__ __forceinline__ void stage_pk(const PfxK& r, uint8_t* s_k) {
     const int tid = threadIdx.x;
@@ -442,22 +392,21 @@ __device__ __forceinline__ void stage_pv(const PfxV& r, uint8_t* s_vt) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
         const int wj = j >> 2, bj = j & 3;
-        const uint32_t p01 = hi16pair(sbyte(r.vw[0][wj], bj), sbyte(r.vw[1][wj], bj));
-        const uint32_t p23 = hi16pair(sbyte(r.vw[2][wj], bj), sbyte(r.vw[3][wj], bj));
+        const uint32_t p01 = pack_bf16x2(sbyte(r.vw[0][wj], bj) * r.vs[0], sbyte(r.vw[1][wj], bj) * r.vs[1]);
+        const uint32_t p23 = pack_bf16x2(sbyte(r.vw[2][wj], bj) * r.vs[2], sbyte(r.vw[3][wj], bj) * r.vs[3]);
         *reinterpret_cast<u32x2*>(dst + j * VT_STRIDE) = u32x2{p01, p23};
     }
-}
-__device__ __forceinline__ void stage_pv_scales(const PfxV& r, float* s_vsc) {
-    if (threadIdx.x < PF_BN) s_vsc[threadIdx.x] = r.vscale;
 }
 
 // Per-wave running state: O^T accumulators (lane: d = 16mt + 4g + i, row = 16nt + l16) and the
 // base-2 running max / sum of the lane's two rows.
 // Per row tile nt (the lane's row l16 of it): the running max m, kept as nmb = -m (0 while the
-// row has seen no key), and the running sum l.
+// row has seen no key), and the running sum l of the bf16 probabilities, accumulated by an MFMA
+// of a ones matrix with P^T (every element of lsum[nt] holds the lane's row sum).
 struct WaveState {
     f32x4 acc[8][2];
-    float nmb[2], l[2];
+    f32x4 lsum[2];
+    float nmb[2];
 };
 
 // Tile kinds: prefix tiles (scores scaled per key, P scaled by v_scale per key) that are full or
@@ -565,7 +514,7 @@ __device__ __forceinline__ void softmax_rescale(WaveState& w, f32x4 (&st)[4][2],
         w.nmb[nt] -= shift;
         if (!first) {  // before the first tile, l and the accumulators are 0
             const float alpha = __builtin_amdgcn_exp2f(-shift);  // 1 unless moved
-            w.l[nt] *= alpha;
+            w.lsum[nt] *= alpha;
             if (__ballot(move)) {
 #pragma unroll
                 for (int mt = 0; mt < 8; ++mt) w.acc[mt][nt] *= alpha;
@@ -574,29 +523,21 @@ __device__ __forceinline__ void softmax_rescale(WaveState& w, f32x4 (&st)[4][2],
     }
 }
 
-// Softmax part 3 for row tile nt: probabilities, row sum, bf16 P^T fragments (prefix tiles:
-// P x v_scale). Branch-free.
-template <bool PREFIX>
-__device__ __forceinline__ void softmax_p(WaveState& w, const f32x4 (&st)[4][2], int nt,
-                                          uint32_t (&pfrag)[2][2][4], const float* s_vsc,
-                                          int g) {
-    float lsum = 0.f;
+// Softmax part 3 for row tile nt: probabilities as bf16 P^T fragments. Branch-free.
+__device__ __forceinline__ void softmax_p(const f32x4 (&st)[4][2], int nt,
+                                          uint32_t (&pfrag)[2][2][4]) {
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-        f32x4 vsv = {1.f, 1.f, 1.f, 1.f};
-        if (PREFIX) vsv = *reinterpret_cast<const f32x4*>(s_vsc + 16 * mt + 4 * g);
+    for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-        for (int i = 0; i < 4; i += 2) {
-            const float p0 = __builtin_amdgcn_exp2f(st[mt][nt][i]);
-            const float p1 = __builtin_amdgcn_exp2f(st[mt][nt][i + 1]);
-            lsum += p0 + p1;
+        for (int i = 0; i < 4; i += 2)
             pfrag[mt >> 1][nt][(mt & 1) * 2 + i / 2] =
-                PREFIX ? pack_bf16x2(p0 * vsv[i], p1 * vsv[i + 1]) : pack_bf16x2(p0, p1);
-        }
-    }
-    w.l[nt] += lsum;
+                pack_bf16x2(__builtin_amdgcn_exp2f(st[mt][nt][i]),
+                            __builtin_amdgcn_exp2f(st[mt][nt][i + 1]));
 }
 
+// O^T += V^T . P^T (32 MFMAs) and the row sums l += ones . P^T (4 MFMAs: the row sum lands in
+// all four elements of lsum[nt], and it is the sum of the bf16 probabilities the PV product
+// weights, so O / l stays a weighted mean of V rows).
 template <bool FENCE = true>
 __device__ __forceinline__ void tile_pv(WaveState& w, const uint32_t (&pfrag)[2][2][4],
                                         const uint8_t* s_vt, int l16, int g) {
@@ -607,6 +548,12 @@ __device__ __forceinline__ void tile_pv(WaveState& w, const uint32_t (&pfrag)[2]
             vf[s2] = __builtin_bit_cast(
                 bf16x8, *reinterpret_cast<const u32x4*>(vfrag + 16 * mt * VT_STRIDE + 64 * s2));
     };
+    auto pfv = [&](int s2, int nt) {
+        return __builtin_bit_cast(bf16x8, u32x4{pfrag[s2][nt][0], pfrag[s2][nt][1],
+                                                pfrag[s2][nt][2], pfrag[s2][nt][3]});
+    };
+    const bf16x8 ones = __builtin_bit_cast(
+        bf16x8, u32x4{0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u});
     bf16x8 vf[2][2];
     read_v(vf[0], 0);
 #pragma unroll
@@ -614,36 +561,38 @@ __device__ __forceinline__ void tile_pv(WaveState& w, const uint32_t (&pfrag)[2]
         if (FENCE) __builtin_amdgcn_sched_barrier(0);
         if (mt < 7) read_v(vf[(mt + 1) & 1], mt + 1);
 #pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
+        for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
-            for (int nt = 0; nt < 2; ++nt) {
-                const bf16x8 pfv = __builtin_bit_cast(
-                    bf16x8, u32x4{pfrag[s2][nt][0], pfrag[s2][nt][1], pfrag[s2][nt][2],
-                                  pfrag[s2][nt][3]});
-                w.acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[mt & 1][s2], pfv,
+            for (int nt = 0; nt < 2; ++nt)
+                w.acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[mt & 1][s2], pfv(s2, nt),
                                                                        w.acc[mt][nt], 0, 0, 0);
-            }
+        if (mt == 0) {
+#pragma unroll
+            for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt)
+                    w.lsum[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pfv(s2, nt),
+                                                                        w.lsum[nt], 0, 0, 0);
         }
     }
 }
 
+// One chunk tile (TILE_CHUNK or TILE_CHUNK_DIAG) of one wave, staged in s_k / s_vt.
 template <int KIND>
 __device__ __forceinline__ void tile_compute(WaveState& w, const bf16x8 (&qf)[2][4],
-                                             const uint8_t* s_k, const uint8_t* s_vt,
-                                             const float* s_ksc, const float* s_kb,
-                                             const float* s_vsc, int kbase, int lim0, int lim1,
-                                             float qk_scale, int l16, int g, bool first) {
-    constexpr bool PREFIX = KIND == TILE_PREFIX || KIND == TILE_PREFIX_PARTIAL;
+                                             const uint8_t* s_k, const uint8_t* s_vt, int kbase,
+                                             int lim0, int lim1, float qk_scale, int l16, int g,
+                                             bool first) {
     f32x4 st[4][2];
     tile_scores(st, qf, s_k, l16, g);
     uint32_t pfrag[2][2][4];  // [32-key step][row tile] bf16x8 as 4 words
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
         __builtin_amdgcn_sched_barrier(0);
-        const float mx = softmax_scale<KIND>(st, nt, w.nmb[nt], s_ksc, s_kb, kbase,
+        const float mx = softmax_scale<KIND>(st, nt, w.nmb[nt], nullptr, nullptr, kbase,
                                              nt ? lim1 : lim0, qk_scale, g);
         softmax_rescale(w, st, nt, mx, first);
-        softmax_p<PREFIX>(w, st, nt, pfrag, s_vsc, g);
+        softmax_p(st, nt, pfrag);
     }
     tile_pv(w, pfrag, s_vt, l16, g);
 }
@@ -696,9 +645,8 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBloc
     // two tile buffers: tile i is staged into buffer i & 1 while the other one is computed on
     __shared__ __attribute__((aligned(16))) uint8_t s_k[2][PF_BN * KS_STRIDE];
     __shared__ __attribute__((aligned(16))) uint8_t s_vt[2][PF_D * VT_STRIDE];
-    __shared__ __attribute__((aligned(16))) float s_ksc[3][PF_BN];  // 3 slots: the pipelined
-    __shared__ __attribute__((aligned(16))) float s_kb[3][PF_BN];   // prefix loop rotates them
-    __shared__ __attribute__((aligned(16))) float s_vsc[2][PF_BN];
+    __shared__ __attribute__((aligned(16))) float s_ksc[3][PF_BN];  // 3 slots: the prefix loop
+    __shared__ __attribute__((aligned(16))) float s_kb[3][PF_BN];   // rotates them
 
     const float* cal = a.c.k_calibration + s.slot * a.c.cal_stride_slot + hk * a.c.cal_stride_head;
     TileSrc src;
@@ -739,28 +687,17 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBloc
     };
     auto consume = [](uint32_t x) { asm volatile("" ::"v"(x)); };
 
-    auto load = [&](TileRegs& r, int kt) {
-        if (kt < s.npt) load_tile<true>(r, src, kt * PF_BN, s.P);
-        else load_tile<false>(r, src, (kt - s.npt) * PF_BN, s.P);
-    };
-    auto stage = [&](const TileRegs& r, int kt, int buf) {
-        if (kt < s.npt) stage_tile<true>(r, s_k[buf], s_vt[buf], s_ksc[buf], s_kb[buf], s_vsc[buf], a.qk_scale);
-        else stage_tile<false>(r, s_k[buf], s_vt[buf], s_ksc[buf], s_kb[buf], s_vsc[buf], a.qk_scale);
-    };
-
     WaveState ws;
 #pragma unroll
     for (int mt = 0; mt < 8; ++mt)
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) ws.acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    ws.lsum[0] = ws.lsum[1] = f32x4{0.f, 0.f, 0.f, 0.f};
     ws.nmb[0] = ws.nmb[1] = 0.f;
-    ws.l[0] = ws.l[1] = 0.f;
 
-#if IE_PREFILL_PIPELINE
     bf16x8 qf[2][4];
     int kt = kt_begin;
     const int prefix_end = min(kt_end, s.npt);
-    TileRegs pf;
     if (kt < prefix_end) {
         // Prefix tiles, software-pipelined per wave: in step j the MFMAs of S_{j+1} run beside
         // the softmax of tile j, and the PV MFMAs of tile j beside the staging of K_{j+2} and
@@ -779,7 +716,6 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBloc
             stage_pk(pk, s_k[0]);
             stage_pk_scales(pk, s_ksc[0], s_kb[0], a.qk_scale);
             stage_pv(pv, s_vt[0]);
-            stage_pv_scales(pv, s_vsc[0]);
             if (n > 1) {
                 stage_pk(pk1, s_k[1]);
                 stage_pk_scales(pk1, s_ksc[1], s_kb[1], a.qk_scale);
@@ -807,15 +743,14 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBloc
             softmax_rescale(ws, sc, 1, mx1, j == 0);
             score_step(sn, qf, kfrag, 2);
             score_step(sn, qf, kfrag, 3);
-            softmax_p<true>(ws, sc, 0, pfrag, s_vsc[j & 1], g);
-            softmax_p<true>(ws, sc, 1, pfrag, s_vsc[j & 1], g);
+            softmax_p(sc, 0, pfrag);
+            softmax_p(sc, 1, pfrag);
             // PV and the staging of the next tiles in one scheduling region (no fences, no
             // branches), so the conversions fill the MFMA issue gaps
             tile_pv<false>(ws, pfrag, s_vt[j & 1], l16, g);
             stage_pk(pk, s_k[j & 1]);  // K_{j+2}; a harmless copy of stale data if j + 2 == n
             stage_pv(pv, s_vt[(j + 1) & 1]);
             if (j + 2 < n) stage_pk_scales(pk, s_ksc[fslot], s_kb[fslot], a.qk_scale);
-            stage_pv_scales(pv, s_vsc[(j + 1) & 1]);
             if (j + 3 < n) load_pk(pk, src, kb0 + (j + 3) * PF_BN, s.P);
             if (j + 2 < n) load_pv(pv, src, kb0 + (j + 2) * PF_BN);
             __syncthreads();
@@ -833,121 +768,44 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBloc
             const float mx = softmax_scale<TILE_PREFIX_PARTIAL>(sc, nt, ws.nmb[nt], s_ksc[slot],
                                                                 s_kb[slot], 0, 0, a.qk_scale, g);
             softmax_rescale(ws, sc, nt, mx, n == 1);
-            softmax_p<true>(ws, sc, nt, pfrag, s_vsc[j & 1], g);
+            softmax_p(sc, nt, pfrag);
         }
         tile_pv(ws, pfrag, s_vt[j & 1], l16, g);
         __syncthreads();  // the chunk tiles reuse the buffers
         kt = prefix_end;
     }
-    uint32_t pfa = 0, pfb = 0;
     if (kt < kt_end) {
-        load_tile<false>(pf, src, (kt - s.npt) * PF_BN, s.P);
-        pfa = prefetch(kt + 1);
-        pfb = prefetch(kt + 2);
+        // chunk tiles: double-buffered, the next tile's loads in flight during this tile's
+        // MFMAs, an L2 prefetch three tiles ahead
+        TileRegs pf;
+        load_tile(pf, src, (kt - s.npt) * PF_BN);
+        uint32_t pfa = prefetch(kt + 1), pfb = prefetch(kt + 2);
         load_q<false>(qf, a, wr0, s.r1, h, cal, l16, g);
-        stage_tile<false>(pf, s_k[(kt - kt_begin) & 1], s_vt[(kt - kt_begin) & 1],
-                          s_ksc[(kt - kt_begin) & 1], s_kb[(kt - kt_begin) & 1],
-                          s_vsc[(kt - kt_begin) & 1], a.qk_scale);
+        stage_tile(pf, s_k[(kt - kt_begin) & 1], s_vt[(kt - kt_begin) & 1]);
         __syncthreads();
         for (; kt < kt_end; ++kt) {
             const int buf = (kt - kt_begin) & 1;
             const bool has_next = kt + 1 < kt_end;
             const int kc = (kt - s.npt) * PF_BN;
-            if (has_next) load_tile<false>(pf, src, kc + PF_BN, s.P);
+            if (has_next) load_tile(pf, src, kc + PF_BN);
             consume(pfa);
             pfa = pfb;
             pfb = prefetch(kt + 3);
             // the whole tile is visible to every row of this wave: no per-key mask
             if (kc + PF_BN - 1 <= min(wr0 - s.seq_start, clim))
-                tile_compute<TILE_CHUNK>(ws, qf, s_k[buf], s_vt[buf], s_ksc[buf], s_kb[buf],
-                                         s_vsc[buf], kc, lim0, lim1, a.qk_scale, l16, g,
-                                         kt == kt_begin);
+                tile_compute<TILE_CHUNK>(ws, qf, s_k[buf], s_vt[buf], kc, lim0, lim1, a.qk_scale,
+                                         l16, g, kt == kt_begin);
             else
-                tile_compute<TILE_CHUNK_DIAG>(ws, qf, s_k[buf], s_vt[buf], s_ksc[buf], s_kb[buf],
-                                              s_vsc[buf], kc, lim0, lim1, a.qk_scale, l16, g,
-                                              kt == kt_begin);
-            if (has_next) stage_tile<false>(pf, s_k[buf ^ 1], s_vt[buf ^ 1], s_ksc[buf ^ 1],
-                                            s_kb[buf ^ 1], s_vsc[buf ^ 1], a.qk_scale);
+                tile_compute<TILE_CHUNK_DIAG>(ws, qf, s_k[buf], s_vt[buf], kc, lim0, lim1,
+                                              a.qk_scale, l16, g, kt == kt_begin);
+            if (has_next) stage_tile(pf, s_k[buf ^ 1], s_vt[buf ^ 1]);
             __syncthreads();
         }
     }
-#else
-    // the first tile's loads and the Q loads are in flight together
-    TileRegs pf;
-    load(pf, kt_begin);
-    uint32_t pfa = prefetch(kt_begin + 1), pfb = prefetch(kt_begin + 2);
-    bf16x8 qf[2][4];
-    int kt = kt_begin;
-    const int prefix_end = min(kt_end, s.npt);
-    if (kt < prefix_end) load_q<true>(qf, a, wr0, s.r1, h, cal, l16, g);
-    else load_q<false>(qf, a, wr0, s.r1, h, cal, l16, g);
-    stage(pf, kt_begin, 0);
-    if (kt < prefix_end) {
-        __syncthreads();
-        // prefix tiles followed by another prefix tile
-        for (; kt < prefix_end - 1; ++kt) {
-            const int buf = (kt - kt_begin) & 1;
-            load_tile<true>(pf, src, (kt + 1) * PF_BN, s.P);  // in flight during the MFMAs
-            consume(pfa);
-            pfa = pfb;
-            pfb = prefetch(kt + 3);
-            tile_compute<TILE_PREFIX>(ws, qf, s_k[buf], s_vt[buf], s_ksc[buf], s_kb[buf],
-                                      s_vsc[buf], kt * PF_BN, 0, 0, a.qk_scale, l16, g,
-                                      kt == kt_begin);
-            stage_tile<true>(pf, s_k[buf ^ 1], s_vt[buf ^ 1], s_ksc[buf ^ 1], s_kb[buf ^ 1],
-                             s_vsc[buf ^ 1], a.qk_scale);
-            __syncthreads();  // next buffer staged; this buffer free for tile kt + 2
-        }
-        // last prefix tile of the piece: followed by the first chunk tile, or by nothing
-        const int buf = (kt - kt_begin) & 1;
-        const bool has_next = kt + 1 < kt_end;
-        if (has_next) load_tile<false>(pf, src, 0, s.P);
-        consume(pfa);
-        pfa = pfb;
-        pfb = prefetch(kt + 3);
-        // the only prefix tile of the piece that can hold keys past P (one instance: a second
-        // one for full tiles here costs registers)
-        tile_compute<TILE_PREFIX_PARTIAL>(ws, qf, s_k[buf], s_vt[buf], s_ksc[buf], s_kb[buf],
-                                          s_vsc[buf], kt * PF_BN, 0, 0, a.qk_scale, l16, g,
-                                          kt == kt_begin);
-        if (has_next)
-            stage_tile<false>(pf, s_k[buf ^ 1], s_vt[buf ^ 1], s_ksc[buf ^ 1], s_kb[buf ^ 1],
-                              s_vsc[buf ^ 1], a.qk_scale);
-        __syncthreads();
-        ++kt;
-    }
-    if (kt < kt_end) {
-        if (kt == kt_begin) __syncthreads();
-        else load_q<false>(qf, a, wr0, s.r1, h, cal, l16, g);
-        for (; kt < kt_end; ++kt) {
-            const int buf = (kt - kt_begin) & 1;
-            const bool has_next = kt + 1 < kt_end;
-            const int kc = (kt - s.npt) * PF_BN;
-            if (has_next) load_tile<false>(pf, src, kc + PF_BN, s.P);
-            consume(pfa);
-            pfa = pfb;
-            pfb = prefetch(kt + 3);
-            // the whole tile is visible to every row of this wave: no per-key mask
-            if (kc + PF_BN - 1 <= min(wr0 - s.seq_start, clim))
-                tile_compute<TILE_CHUNK>(ws, qf, s_k[buf], s_vt[buf], s_ksc[buf], s_kb[buf],
-                                         s_vsc[buf], kc, lim0, lim1, a.qk_scale, l16, g,
-                                         kt == kt_begin);
-            else
-                tile_compute<TILE_CHUNK_DIAG>(ws, qf, s_k[buf], s_vt[buf], s_ksc[buf], s_kb[buf],
-                                              s_vsc[buf], kc, lim0, lim1, a.qk_scale, l16, g,
-                                              kt == kt_begin);
-            if (has_next) stage_tile<false>(pf, s_k[buf ^ 1], s_vt[buf ^ 1], s_ksc[buf ^ 1],
-                                            s_kb[buf ^ 1], s_vsc[buf ^ 1], a.qk_scale);
-            __syncthreads();
-        }
-    }
-
-#endif
     // ---- results: lane holds row = wr0 + 16nt + l16, channels d = 16mt + 4g + i ----
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
-        float l = ws.l[nt];
-        l = sum_xor32(sum_xor16(l));
+        const float l = ws.lsum[nt][0];
         const int row = wr0 + 16 * nt + l16;
         if (row >= s.r1) continue;
         const float rl = l != 0.f ? 1.f / l : 0.f;
@@ -968,7 +826,8 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBloc
                     u32x2{pack_bf16x2(x[0] * rl, x[1] * rl), pack_bf16x2(x[2] * rl, x[3] * rl)};
             }
             if (g == 0)
-                *reinterpret_cast<float2*>(a.part_ml + prow * 2) = make_float2(l != 0.f ? -ws.nmb[nt] : -INFINITY, l);
+                *reinterpret_cast<float2*>(a.part_ml + prow * 2) =
+                    make_float2(l != 0.f ? -ws.nmb[nt] : -INFINITY, l);
         }
     }
 }
