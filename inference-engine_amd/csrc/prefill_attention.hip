@@ -867,17 +867,26 @@ __global__ __launch_bounds__(PF_THREADS, IE_PREFILL_WG_PER_CU) void prefill_atte
 constexpr int PF_COMB_GROUPS = 4;  // combine units per (split sub-block, kv head): 32 pairs each
 
 // grid (slots), block 256: merges the pieces of split sub-blocks (log-sum-exp, base 2) from the
-// list the main kernel recorded. Unit u: split sub-block u / (Hkv * 4), kv head, and 32 of its
-// 128 (row, query head) pairs; 8 threads per pair, 16 channels each, all loads issued up front.
+// list the main kernel recorded. Unit: split sub-block k, kv head hk, and 32 of its 128 (row,
+// query head) pairs; 8 threads per pair, 16 channels each, all loads issued up front.
+// Workgroups are dealt to the 8 XCDs round-robin (workgroup w runs on XCD w % 8), and the pieces
+// of (k, hk) ran as workgroups item_base + p * Hkv + hk: with Hkv a multiple of 8 they all ran
+// on XCD (item_base + hk) % 8, and the unit is given to a workgroup of that XCD, whose L2 holds
+// the partials.
 __global__ __launch_bounds__(PF_THREADS) void prefill_combine_kernel(PrefillArgs a) {
     const int nsplit = uni(a.sched[1]);
     const int tid = threadIdx.x, d = 16 * (tid & 7);
-    const int units = nsplit * a.hkv * PF_COMB_GROUPS;
-    for (int u = blockIdx.x; u < units; u += gridDim.x) {
-        const int k = u / (a.hkv * PF_COMB_GROUPS);
-        const int hk = (u / PF_COMB_GROUPS) % a.hkv, grp = u % PF_COMB_GROUPS;
+    const bool by_xcd = (a.hkv & 7) == 0 && (gridDim.x & 7) == 0;
+    const int hk8 = a.hkv >> 3;
+    const int units = by_xcd ? nsplit * hk8 * PF_COMB_GROUPS : nsplit * a.hkv * PF_COMB_GROUPS;
+    const int u0 = by_xcd ? blockIdx.x >> 3 : blockIdx.x;
+    const int ustep = by_xcd ? gridDim.x >> 3 : gridDim.x;
+    for (int u = u0; u < units; u += ustep) {
+        const int per_k = (by_xcd ? hk8 : a.hkv) * PF_COMB_GROUPS;
+        const int k = u / per_k, hr = (u % per_k) / PF_COMB_GROUPS, grp = u % PF_COMB_GROUPS;
         const int4 rec = *reinterpret_cast<const int4*>(a.sched + 4 + 4 * k);
         const int item_base = uni(rec.x);
+        const int hk = by_xcd ? 8 * hr + (((int)(blockIdx.x & 7) - item_base) & 7) : hr;
         SubBlock s;
         s.r0 = uni(rec.y);
         s.r1 = uni(rec.z);
