@@ -113,20 +113,35 @@ __device__ __forceinline__ int uni(int x) { return __builtin_amdgcn_readfirstlan
 // Sub-block `sb` (tile sb / sub_per_tile, 64-row slice sb % sub_per_tile) as seen by the calling
 // lane: rows [r0, r1) of the entry starting at packed row seq_start, its cache slot and prefix
 // length P, and its key tiles: cdiv(P, 64) prefix tiles then cdiv(r1 - seq_start, 64) chunk
-// tiles. ntiles = 0 when the sub-block has no rows.
+// tiles (npt, nct; both 0 when the sub-block has no rows).
 struct SbInfo {
-    int ntiles, r0, r1, seq_start, P, slot;
+    int npt, nct, r0, r1, seq_start, P, slot;
 };
 
-__device__ __forceinline__ int piece_count(int ntiles, int T) {
-    return min(PF_MAXP, max(1, cdiv_i(ntiles, T)));
+constexpr int PF_UNSPLIT = 1 << 28;  // piece size that never splits a pair
+
+// Pieces of a pair with npt prefix and nct chunk tiles at piece size T. A pair of at most T
+// tiles is one piece; a longer one is split into prefix pieces and chunk pieces separately (no
+// piece mixes the two loops, so none pays two pipeline prologues), evenly within each part, at
+// most PF_MAXP pieces in all.
+__device__ __forceinline__ int prefix_pieces(int npt, int nct, int T) {
+    if (npt + nct <= T) return 0;
+    return npt == 0 ? 0 : min(PF_MAXP - 1, cdiv_i(npt, T));
+}
+__device__ __forceinline__ int piece_count(int npt, int nct, int T) {
+    if (npt + nct == 0) return 0;
+    if (npt + nct <= T) return 1;
+    const int pp = prefix_pieces(npt, nct, T);
+    return pp + min(PF_MAXP - pp, cdiv_i(nct, T));
 }
 
 // The launch's work list, computed identically by every workgroup from the tile metadata:
-//  * piece size T (tiles): a (sub-block, kv head) pair with n tiles becomes cdiv(n, T) items (at
-//    most PF_MAXP). T is the smallest size for which the items fit the partial slots even in the
-//    worst rounding, sum(n / T + 1) * Hkv <= slots, so every split item owns a slot. With more
-//    (sub-block, head) pairs than slots there is enough parallelism without splitting.
+//  * piece size T (tiles): a (sub-block, kv head) pair becomes piece_count items. T is the
+//    smallest size (at least PF_MIN_PIECE_TILES) whose item count fits the partial slots, so
+//    that every split item owns a slot: the search runs from the lower bound
+//    cdiv(sum(n) * Hkv, slots) up to the worst-rounding bound, where every part rounds up by a
+//    whole piece (sum(n / T) + parts) * Hkv <= slots, which always fits. With more (sub-block
+//    part, head) pairs than slots there is enough parallelism without splitting.
 //  * items in launch order: sub-blocks from last to first (later sub-blocks of a sequence see
 //    more keys), then piece, then kv head.
 // schedule(target) finds the sub-block holding item `target`, the offset inside it and the
@@ -139,7 +154,7 @@ constexpr int PF_SCHED_CHUNKS = 4;
 constexpr int PF_MAX_ENTRIES = 512;
 
 struct SubBlock {
-    int r0, r1, seq_start, P, slot, npt, nct, ntiles, npieces;
+    int r0, r1, seq_start, P, slot, npt, nct, ntiles, npieces, npp;  // npp: prefix pieces
 };
 
 __device__ __forceinline__ void fill_sub_block(SubBlock& s, int r0, int r1, int seq_start, int P,
@@ -152,7 +167,8 @@ __device__ __forceinline__ void fill_sub_block(SubBlock& s, int r0, int r1, int 
     s.npt = cdiv_i(P, PF_BN);
     s.nct = cdiv_i(r1 - seq_start, PF_BN);
     s.ntiles = s.npt + s.nct;
-    s.npieces = piece_count(s.ntiles, T);
+    s.npieces = piece_count(s.npt, s.nct, T);
+    s.npp = prefix_pieces(s.npt, s.nct, T);
 }
 
 struct Loc {
@@ -183,7 +199,7 @@ __device__ Loc schedule(const PrefillArgs& a, int target) {
         if (e < a.nent) s_sl[e] = a.slot_ids[e];
     }
     auto info = [&](int sb, int row_start) {
-        SbInfo z = {0, 0, 0, 0, 0, 0};
+        SbInfo z = {0, 0, 0, 0, 0, 0, 0};
         if (row_start < 0) return z;
         int lo = 0, hi = a.nent - 1;
         while (lo < hi) {
@@ -197,7 +213,8 @@ __device__ Loc schedule(const PrefillArgs& a, int target) {
         const int r1 = min(min(r0 + PF_BM, row_start + a.block_m), seq_end);
         if (r0 >= r1) return z;
         z.P = s_cc[lo + 1] - s_cc[lo];
-        z.ntiles = cdiv_i(z.P, PF_BN) + cdiv_i(r1 - seq_start, PF_BN);
+        z.npt = cdiv_i(z.P, PF_BN);
+        z.nct = cdiv_i(r1 - seq_start, PF_BN);
         z.r0 = r0;
         z.r1 = r1;
         z.seq_start = seq_start;
@@ -205,39 +222,46 @@ __device__ Loc schedule(const PrefillArgs& a, int target) {
         return z;
     };
     SbInfo zc[PF_SCHED_CHUNKS];
-    int tot = 0, nonempty = 0;
+    int tot = 0, parts = 0;
 #pragma unroll
     for (int c = 0; c < PF_SCHED_CHUNKS; ++c) {
         zc[c] = info(c < nchunks ? sb_of(c) : -1, rs[c]);
-        tot += zc[c].ntiles;
-        nonempty += zc[c].ntiles > 0;
+        tot += zc[c].npt + zc[c].nct;
+        parts += (zc[c].npt > 0) + (zc[c].nct > 0);
     }
     for (int c = PF_SCHED_CHUNKS; c < nchunks; ++c) {
-        const int nt = info(sb_of(c), row_start_of(sb_of(c))).ntiles;
-        tot += nt;
-        nonempty += nt > 0;
+        const SbInfo z = info(sb_of(c), row_start_of(sb_of(c)));
+        tot += z.npt + z.nct;
+        parts += (z.npt > 0) + (z.nct > 0);
     }
     tot = uni(wave_sum_i(tot));
-    nonempty = uni(wave_sum_i(nonempty));
-    const int spare = a.grid - nonempty * a.hkv;
+    parts = uni(wave_sum_i(parts));
+    // f(z) summed over the launch's sub-blocks (every lane gets the sum)
+    auto launch_sum = [&](auto f) {
+        int n = 0;
+#pragma unroll
+        for (int c = 0; c < PF_SCHED_CHUNKS; ++c) n += f(zc[c]);
+        for (int c = PF_SCHED_CHUNKS; c < nchunks; ++c) n += f(info(sb_of(c), row_start_of(sb_of(c))));
+        return uni(wave_sum_i(n));
+    };
+    const int spare = a.grid - parts * a.hkv;
     Loc L;
-    L.T = spare <= 0 ? (1 << 28) : max(PF_MIN_PIECE_TILES, cdiv_i(tot * a.hkv, spare));
+    L.T = PF_UNSPLIT;
+    if (spare > 0) {
+        L.T = max(PF_MIN_PIECE_TILES, cdiv_i(tot * a.hkv, spare));
+        for (int T = max(PF_MIN_PIECE_TILES, cdiv_i(tot * a.hkv, a.grid)); T < L.T; ++T)
+            if (launch_sum([&](const SbInfo& z) { return piece_count(z.npt, z.nct, T); }) * a.hkv <=
+                a.grid) {
+                L.T = T;
+                break;
+            }
+    }
     L.found = 0;
     L.sb = L.off = L.item_base = L.split_index = 0;
-    {
-        int ns = 0;
-#pragma unroll
-        for (int c = 0; c < PF_SCHED_CHUNKS; ++c)
-            ns += zc[c].ntiles > 0 && piece_count(zc[c].ntiles, L.T) > 1;
-        for (int c = PF_SCHED_CHUNKS; c < nchunks; ++c) {
-            const int nt = info(sb_of(c), row_start_of(sb_of(c))).ntiles;
-            ns += nt > 0 && piece_count(nt, L.T) > 1;
-        }
-        L.nsplit = uni(wave_sum_i(ns));
-    }
+    L.nsplit = launch_sum([&](const SbInfo& z) { return piece_count(z.npt, z.nct, L.T) > 1; });
     int items_before = 0, split_before = 0;
     auto visit = [&](int c, const SbInfo& z) {
-        const int np = z.ntiles > 0 ? piece_count(z.ntiles, L.T) : 0;
+        const int np = piece_count(z.npt, z.nct, L.T);
         const int items = np * a.hkv;
         const int incl = wave_incl_scan_i(items) + items_before;
         const int sincl = wave_incl_scan_i(np > 1) + split_before;
@@ -266,12 +290,6 @@ __device__ Loc schedule(const PrefillArgs& a, int target) {
 }
 
 // Global data of one tile, held in registers between its load and its LDS staging.
-// Chunk tiles (bf16 rows of the packed chunk), in registers between load and staging.
-struct TileRegs {
-    uint32_t kw[16];    // K: key tid>>2, channels [32 (tid&3), +32)
-    uint32_t vw[4][4];  // V: keys 4 (tid&15) + u, channels [8 (tid>>4), +8)
-};
-
 // Buffer descriptors of one (sub-block, kv head): prefix K/V rows (128 B each, P rows) and scales
 // of the cache, and the chunk's bf16 K/V rows [seq_start, r1). Reads past those ranges return 0.
 struct TileSrc {
@@ -287,51 +305,6 @@ __device__ __forceinline__ u32x2 ld64(rsrc_t r, int off) {
 }
 __device__ __forceinline__ float ldf(rsrc_t r, int off) {
     return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
-}
-
-// Issue the loads of a chunk tile: packed rows seq_start + [kbase, kbase + 64) (zeros at or past
-// the sub-block's last row: the buffer range does the masking, no branches).
-__device__ __forceinline__ void load_tile(TileRegs& r, const TileSrc& src, int kbase) {
-    const int tid = threadIdx.x;
-    {
-        const int off = (kbase + (tid >> 2)) * src.ck_stride + 64 * (tid & 3);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const u32x4 x = ld128(src.ck, off + 16 * i);
-            r.kw[4 * i] = x.x; r.kw[4 * i + 1] = x.y; r.kw[4 * i + 2] = x.z; r.kw[4 * i + 3] = x.w;
-        }
-    }
-    {
-        const int kg = tid & 15, dg = tid >> 4;
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const u32x4 x = ld128(src.cv, (kbase + 4 * kg + u) * src.cv_stride + 16 * dg);
-            r.vw[u][0] = x.x; r.vw[u][1] = x.y; r.vw[u][2] = x.z; r.vw[u][3] = x.w;
-        }
-    }
-}
-
-// Write a loaded chunk tile to LDS: K as [key][d], V as [d][key] (bf16).
-__device__ __forceinline__ void stage_tile(const TileRegs& r, uint8_t* s_k, uint8_t* s_vt) {
-    const int tid = threadIdx.x;
-    {
-        uint8_t* dst = s_k + ks_off(tid >> 2, 4 * (tid & 3));
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            *reinterpret_cast<u32x4*>(dst + 16 * i) =
-                u32x4{r.kw[4 * i], r.kw[4 * i + 1], r.kw[4 * i + 2], r.kw[4 * i + 3]};
-    }
-    {
-        const int kg = tid & 15, dg = tid >> 4;
-        uint8_t* dst = s_vt + vt_off4(8 * dg, kg);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {  // channel j of key u: bf16 half (j & 1) of word j >> 1
-            const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
-            const uint32_t p01 = __builtin_amdgcn_perm(r.vw[1][j >> 1], r.vw[0][j >> 1], sel);
-            const uint32_t p23 = __builtin_amdgcn_perm(r.vw[3][j >> 1], r.vw[2][j >> 1], sel);
-            *reinterpret_cast<u32x2*>(dst + j * VT_STRIDE) = u32x2{p01, p23};
-        }
-    }
 }
 
 // Prefix tiles, K and V handled separately (the prefix loop stages K two tiles and V one tile
@@ -398,6 +371,45 @@ __device__ __forceinline__ void stage_pv(const PfxV& r, uint8_t* s_vt) {
     }
 }
 
+// Chunk tiles: bf16 rows seq_start + [kbase, kbase + 64) of the packed chunk (zeros at or past
+// the sub-block's last row: the buffer range does the masking), K and V in registers between
+// load and staging. Same lane mappings as the prefix tiles.
+struct ChkK {
+    u32x4 w[4];  // key tid >> 2, channels [32 (tid & 3), +32)
+};
+struct ChkV {
+    u32x4 w[4];  // keys 4 (tid & 15) + u, channels [8 (tid >> 4), +8)
+};
+__device__ __forceinline__ void load_ck(ChkK& r, const TileSrc& src, int kbase) {
+    const int tid = threadIdx.x;
+    const int off = (kbase + (tid >> 2)) * src.ck_stride + 64 * (tid & 3);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r.w[i] = ld128(src.ck, off + 16 * i);
+}
+__device__ __forceinline__ void load_cv(ChkV& r, const TileSrc& src, int kbase) {
+    const int tid = threadIdx.x;
+    const int kg = tid & 15, dg = tid >> 4;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) r.w[u] = ld128(src.cv, (kbase + 4 * kg + u) * src.cv_stride + 16 * dg);
+}
+__device__ __forceinline__ void stage_ck(const ChkK& r, uint8_t* s_k) {
+    const int tid = threadIdx.x;
+    uint8_t* dst = s_k + ks_off(tid >> 2, 4 * (tid & 3));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(dst + 16 * i) = r.w[i];
+}
+__device__ __forceinline__ void stage_cv(const ChkV& r, uint8_t* s_vt) {
+    const int tid = threadIdx.x;
+    uint8_t* dst = s_vt + vt_off4(8 * (tid >> 4), tid & 15);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {  // channel j of key u: bf16 half (j & 1) of word j >> 1
+        const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+        const uint32_t p01 = __builtin_amdgcn_perm(r.w[1][j >> 1], r.w[0][j >> 1], sel);
+        const uint32_t p23 = __builtin_amdgcn_perm(r.w[3][j >> 1], r.w[2][j >> 1], sel);
+        *reinterpret_cast<u32x2*>(dst + j * VT_STRIDE) = u32x2{p01, p23};
+    }
+}
+
 // Per-wave running state: O^T accumulators (lane: d = 16mt + 4g + i, row = 16nt + l16) and the
 // base-2 running max / sum of the lane's two rows.
 // Per row tile nt (the lane's row l16 of it): the running max m, kept as nmb = -m (0 while the
@@ -409,10 +421,10 @@ struct WaveState {
     float nmb[2];
 };
 
-// Tile kinds: prefix tiles (scores scaled per key, P scaled by v_scale per key) that are full or
-// hold keys past P (masked through the staged -inf bias); chunk tiles that every row of the wave
-// sees whole, or that cross the causal diagonal / the sub-block's last row (masked per key).
-enum : int { TILE_PREFIX = 0, TILE_PREFIX_PARTIAL = 1, TILE_CHUNK = 2, TILE_CHUNK_DIAG = 3 };
+// Tile kinds for the score scaling: prefix tiles (scores scaled per key) that are full or hold
+// keys past P (masked through the staged -inf bias); chunk tiles (one scale; the causal mask is
+// applied in softmax_rescale).
+enum : int { TILE_PREFIX = 0, TILE_PREFIX_PARTIAL = 1, TILE_CHUNK = 2 };
 
 // The three parts of one wave's work on a staged 64-key tile (the sum is tile_compute):
 //   tile_scores   S^T = K . Q^T, 64 keys x 32 rows, 32 MFMAs (4 steps of 16 keys)
@@ -468,13 +480,13 @@ __device__ __forceinline__ void tile_scores(f32x4 (&st)[4][2], const bf16x8 (&qf
     }
 }
 
-// Softmax part 1 for row tile nt: scale (relative to the running max), mask, and the max over
-// the lane's own 16 keys of the tile (the row's max needs the other three lanes of the row only
-// when the running max moves). Branch-free.
+// Softmax part 1 for row tile nt: scale (relative to the running max), the prefix-partial mask,
+// and the max over the lane's own 16 keys of the tile (the row's max needs the other three lanes
+// of the row only when the running max moves). Branch-free.
 template <int KIND>
 __device__ __forceinline__ float softmax_scale(f32x4 (&st)[4][2], int nt, float nmb,
-                                               const float* s_ksc, const float* s_kb, int kbase,
-                                               int lim, float qk_scale, int g) {
+                                               const float* s_ksc, const float* s_kb,
+                                               float qk_scale, int g) {
     constexpr bool PREFIX = KIND == TILE_PREFIX || KIND == TILE_PREFIX_PARTIAL;
     float mx = -INFINITY;
 #pragma unroll
@@ -487,7 +499,6 @@ __device__ __forceinline__ float softmax_scale(f32x4 (&st)[4][2], int nt, float 
         for (int i = 0; i < 4; ++i) {
             float x = __builtin_fmaf(st[mt][nt][i], ksv[i], nmb);
             if (KIND == TILE_PREFIX_PARTIAL) x += kbv[i];  // -inf past P
-            if (KIND == TILE_CHUNK_DIAG) x = kbase + 16 * mt + 4 * g + i <= lim ? x : -INFINITY;
             st[mt][nt][i] = x;
             mx = fmaxf(mx, x);
         }
@@ -503,9 +514,24 @@ __device__ __forceinline__ float softmax_scale(f32x4 (&st)[4][2], int nt, float 
 // can appear. The common path is one compare of the lane's own max; in the rare, wave-uniform
 // branch the row's max is reduced over its four lanes (every lane of a row takes the same
 // decision), the wave shifts its scores once more and rescales the accumulators.
+// Chunk tiles on the causal diagonal or past the sub-block's last row (`diag`, wave-uniform: at
+// most two per wave and item) take the rare branch too, which masks them first (chunk key
+// kbase + 16mt + 4g + i is visible to the lane's row iff it is <= lim).
 __device__ __forceinline__ void softmax_rescale(WaveState& w, f32x4 (&st)[4][2], int nt,
-                                                float mx, bool first) {
-    if (first || __ballot(mx > RESCALE_SLACK)) {
+                                                float mx, bool first, bool diag = false,
+                                                int kbase = 0, int lim = 0, int g = 0) {
+    if (first || diag || __ballot(mx > RESCALE_SLACK)) {
+        if (diag) {
+            mx = -INFINITY;
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float x = kbase + 16 * mt + 4 * g + i <= lim ? st[mt][nt][i] : -INFINITY;
+                    st[mt][nt][i] = x;
+                    mx = fmaxf(mx, x);
+                }
+        }
         const float rmx = max_xor32(max_xor16(mx));
         const bool move = first ? rmx != -INFINITY : rmx > RESCALE_SLACK;
         const float shift = move ? rmx : 0.f;
@@ -577,26 +603,6 @@ __device__ __forceinline__ void tile_pv(WaveState& w, const uint32_t (&pfrag)[2]
     }
 }
 
-// One chunk tile (TILE_CHUNK or TILE_CHUNK_DIAG) of one wave, staged in s_k / s_vt.
-template <int KIND>
-__device__ __forceinline__ void tile_compute(WaveState& w, const bf16x8 (&qf)[2][4],
-                                             const uint8_t* s_k, const uint8_t* s_vt, int kbase,
-                                             int lim0, int lim1, float qk_scale, int l16, int g,
-                                             bool first) {
-    f32x4 st[4][2];
-    tile_scores(st, qf, s_k, l16, g);
-    uint32_t pfrag[2][2][4];  // [32-key step][row tile] bf16x8 as 4 words
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-        __builtin_amdgcn_sched_barrier(0);
-        const float mx = softmax_scale<KIND>(st, nt, w.nmb[nt], nullptr, nullptr, kbase,
-                                             nt ? lim1 : lim0, qk_scale, g);
-        softmax_rescale(w, st, nt, mx, first);
-        softmax_p(st, nt, pfrag);
-    }
-    tile_pv(w, pfrag, s_vt, l16, g);
-}
-
 // Q^T fragments of this wave: lane holds q[row = wr0 + 16nt + l16][d = 32ks + 8g .. +7], as
 // bf16(q * cal) for prefix tiles or bf16 q for chunk tiles; zero rows past the sub-block.
 template <bool PREFIX>
@@ -633,8 +639,13 @@ __device__ __forceinline__ void load_q(bf16x8 (&qf)[2][4], const PrefillArgs& a,
 // One work item: tiles [kt_begin, kt_end) of piece `piece` of sub-block s for kv head hk.
 __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBlock& s, int hk,
                                              int piece, int item) {
-    const int kt_begin = piece * s.ntiles / s.npieces;
-    const int kt_end = (piece + 1) * s.ntiles / s.npieces;
+    // tiles [kt_begin, kt_end): the whole pair, a prefix piece or a chunk piece
+    int kt_begin = 0, kt_end = s.ntiles;
+    if (s.npieces > 1) {
+        const int q = piece - s.npp, nc = s.npieces - s.npp;
+        kt_begin = q < 0 ? piece * s.npt / s.npp : s.npt + q * s.nct / nc;
+        kt_end = q < 0 ? (piece + 1) * s.npt / s.npp : s.npt + (q + 1) * s.nct / nc;
+    }
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -669,24 +680,7 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBloc
     const int clim = s.r1 - s.seq_start - 1;
     const int lim0 = min(rowA - s.seq_start, clim), lim1 = min(rowB - s.seq_start, clim);
 
-    // tile kt: prefix tile kt (keys [64kt, ..)) if kt < npt, else chunk tile kt - npt
-    // L2 prefetch of tile kt2 (no-op past the piece: the offsets fall outside the buffer range):
-    // one dword per lane and wave touches every 128-byte line of the tile's K rows, V rows and
-    // scales. The result is only consumed (never used) so the data lands in L2 for the real load.
-    const int wave_u = uni(wave);
-    auto prefetch = [&](int kt2) -> uint32_t {
-        const bool pre = kt2 < s.npt;
-        const int row = (pre ? kt2 : kt2 - s.npt) * PF_BN + lane;
-        const rsrc_t r = kt2 >= kt_end ? src.pks
-                       : pre ? (wave_u == 0 ? src.pk : wave_u == 1 ? src.pv : wave_u == 2 ? src.pks : src.pvs)
-                             : (wave_u < 2 ? src.ck : src.cv);
-        const int off = kt2 >= kt_end ? -1
-                      : pre ? row * (wave_u < 2 ? PF_D : 4)
-                            : row * (wave_u < 2 ? src.ck_stride : src.cv_stride) + 128 * (wave_u & 1);
-        return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
-    };
-    auto consume = [](uint32_t x) { asm volatile("" ::"v"(x)); };
-
+    // tile kt of the item: prefix tile kt (keys [64kt, ..)) if kt < npt, else chunk tile kt - npt
     WaveState ws;
 #pragma unroll
     for (int mt = 0; mt < 8; ++mt)
@@ -735,10 +729,10 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBloc
             f32x4 sn[4][2];
             score_step(sn, qf, kfrag, 0);
             score_step(sn, qf, kfrag, 1);
-            const float mx0 = softmax_scale<TILE_PREFIX>(sc, 0, ws.nmb[0], s_ksc[slot], s_kb[slot], 0,
-                                                         0, a.qk_scale, g);
-            const float mx1 = softmax_scale<TILE_PREFIX>(sc, 1, ws.nmb[1], s_ksc[slot], s_kb[slot], 0,
-                                                         0, a.qk_scale, g);
+            const float mx0 =
+                softmax_scale<TILE_PREFIX>(sc, 0, ws.nmb[0], s_ksc[slot], s_kb[slot], a.qk_scale, g);
+            const float mx1 =
+                softmax_scale<TILE_PREFIX>(sc, 1, ws.nmb[1], s_ksc[slot], s_kb[slot], a.qk_scale, g);
             softmax_rescale(ws, sc, 0, mx0, j == 0);
             softmax_rescale(ws, sc, 1, mx1, j == 0);
             score_step(sn, qf, kfrag, 2);
@@ -766,7 +760,7 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBloc
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) {
             const float mx = softmax_scale<TILE_PREFIX_PARTIAL>(sc, nt, ws.nmb[nt], s_ksc[slot],
-                                                                s_kb[slot], 0, 0, a.qk_scale, g);
+                                                                s_kb[slot], a.qk_scale, g);
             softmax_rescale(ws, sc, nt, mx, n == 1);
             softmax_p(sc, nt, pfrag);
         }
@@ -775,32 +769,70 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBloc
         kt = prefix_end;
     }
     if (kt < kt_end) {
-        // chunk tiles: double-buffered, the next tile's loads in flight during this tile's
-        // MFMAs, an L2 prefetch three tiles ahead
-        TileRegs pf;
-        load_tile(pf, src, (kt - s.npt) * PF_BN);
-        uint32_t pfa = prefetch(kt + 1), pfb = prefetch(kt + 2);
-        load_q<false>(qf, a, wr0, s.r1, h, cal, l16, g);
-        stage_tile(pf, s_k[(kt - kt_begin) & 1], s_vt[(kt - kt_begin) & 1]);
-        __syncthreads();
-        for (; kt < kt_end; ++kt) {
-            const int buf = (kt - kt_begin) & 1;
-            const bool has_next = kt + 1 < kt_end;
-            const int kc = (kt - s.npt) * PF_BN;
-            if (has_next) load_tile(pf, src, kc + PF_BN);
-            consume(pfa);
-            pfa = pfb;
-            pfb = prefetch(kt + 3);
-            // the whole tile is visible to every row of this wave: no per-key mask
-            if (kc + PF_BN - 1 <= min(wr0 - s.seq_start, clim))
-                tile_compute<TILE_CHUNK>(ws, qf, s_k[buf], s_vt[buf], kc, lim0, lim1, a.qk_scale,
-                                         l16, g, kt == kt_begin);
-            else
-                tile_compute<TILE_CHUNK_DIAG>(ws, qf, s_k[buf], s_vt[buf], kc, lim0, lim1,
-                                              a.qk_scale, l16, g, kt == kt_begin);
-            if (has_next) stage_tile(pf, s_k[buf ^ 1], s_vt[buf ^ 1]);
-            __syncthreads();
+        // Chunk tiles, pipelined like the prefix tiles (K_{j+2} and V_{j+1} staged in step j).
+        // Tiles that every row of the wave sees whole take the common softmax path; the wave's
+        // diagonal tiles (and a last tile past the sub-block's rows) are masked in the rare one.
+        const int n = kt_end - kt, kb0 = (kt - s.npt) * PF_BN;
+        const int wlim = min(wr0 - s.seq_start, clim);  // keys <= wlim: visible to all rows
+        const bool item_start = kt == kt_begin;
+        ChkK ck;
+        ChkV cv;
+        {
+            ChkK ck1;
+            load_ck(ck, src, kb0);
+            load_cv(cv, src, kb0);
+            if (n > 1) load_ck(ck1, src, kb0 + PF_BN);
+            load_q<false>(qf, a, wr0, s.r1, h, cal, l16, g);
+            stage_ck(ck, s_k[0]);
+            stage_cv(cv, s_vt[0]);
+            if (n > 1) stage_ck(ck1, s_k[1]);
         }
+        if (n > 2) load_ck(ck, src, kb0 + 2 * PF_BN);
+        if (n > 1) load_cv(cv, src, kb0 + PF_BN);
+        __syncthreads();
+        f32x4 sc[4][2];
+        tile_scores(sc, qf, s_k[0], l16, g);
+        __syncthreads();  // every wave has read K_0 before step 0 stages K_2 over it
+        uint32_t pfrag[2][2][4];
+        for (int j = 0; j < n - 1; ++j) {
+            const int kc = kb0 + j * PF_BN;
+            const bool diag = kc + PF_BN - 1 > wlim, first = item_start && j == 0;
+            const uint8_t* kfrag = s_k[(j + 1) & 1] + ks_off(l16, g);
+            f32x4 sn[4][2];
+            score_step(sn, qf, kfrag, 0);
+            score_step(sn, qf, kfrag, 1);
+            const float mx0 = softmax_scale<TILE_CHUNK>(sc, 0, ws.nmb[0], nullptr, nullptr,
+                                                        a.qk_scale, g);
+            const float mx1 = softmax_scale<TILE_CHUNK>(sc, 1, ws.nmb[1], nullptr, nullptr,
+                                                        a.qk_scale, g);
+            softmax_rescale(ws, sc, 0, mx0, first, diag, kc, lim0, g);
+            softmax_rescale(ws, sc, 1, mx1, first, diag, kc, lim1, g);
+            score_step(sn, qf, kfrag, 2);
+            score_step(sn, qf, kfrag, 3);
+            softmax_p(sc, 0, pfrag);
+            softmax_p(sc, 1, pfrag);
+            tile_pv<false>(ws, pfrag, s_vt[j & 1], l16, g);
+            stage_ck(ck, s_k[j & 1]);  // K_{j+2}; a harmless copy of stale data if j + 2 == n
+            stage_cv(cv, s_vt[(j + 1) & 1]);
+            if (j + 3 < n) load_ck(ck, src, kb0 + (j + 3) * PF_BN);
+            if (j + 2 < n) load_cv(cv, src, kb0 + (j + 2) * PF_BN);
+            __syncthreads();
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) {
+                sc[mt][0] = sn[mt][0];
+                sc[mt][1] = sn[mt][1];
+            }
+        }
+        const int kc = kb0 + (n - 1) * PF_BN;
+        const bool diag = kc + PF_BN - 1 > wlim, first = item_start && n == 1;
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+            const float mx = softmax_scale<TILE_CHUNK>(sc, nt, ws.nmb[nt], nullptr, nullptr,
+                                                       a.qk_scale, g);
+            softmax_rescale(ws, sc, nt, mx, first, diag, kc, nt ? lim1 : lim0, g);
+            softmax_p(sc, nt, pfrag);
+        }
+        tile_pv(ws, pfrag, s_vt[(n - 1) & 1], l16, g);
     }
     // ---- results: lane holds row = wr0 + 16nt + l16, channels d = 16mt + 4g + i ----
 #pragma unroll
