@@ -120,19 +120,34 @@ struct SbInfo {
 
 constexpr int PF_UNSPLIT = 1 << 28;  // piece size that never splits a pair
 
+// Division by a wave-uniform divisor d >= 1 of numerators 0 <= x < 2^22: the float estimate
+// x * (1/d) is within one of floor(x / d), and one compare each way makes it exact.
+struct Divisor {
+    int d;
+    float r;
+};
+__device__ __forceinline__ Divisor divisor(int d) { return Divisor{d, 1.0f / (float)d}; }
+__device__ __forceinline__ int div_floor(int x, const Divisor& D) {
+    int q = (int)((float)x * D.r);
+    q += (q + 1) * D.d <= x;
+    q -= q * D.d > x;
+    return q;
+}
+__device__ __forceinline__ int div_ceil(int x, const Divisor& D) { return div_floor(x + D.d - 1, D); }
+
 // Pieces of a pair with npt prefix and nct chunk tiles at piece size T. A pair of at most T
 // tiles is one piece; a longer one is split into prefix pieces and chunk pieces separately (no
 // piece mixes the two loops, so none pays two pipeline prologues), evenly within each part, at
 // most PF_MAXP pieces in all.
-__device__ __forceinline__ int prefix_pieces(int npt, int nct, int T) {
-    if (npt + nct <= T) return 0;
-    return npt == 0 ? 0 : min(PF_MAXP - 1, cdiv_i(npt, T));
+__device__ __forceinline__ int prefix_pieces(int npt, int nct, const Divisor& T) {
+    if (npt + nct <= T.d) return 0;
+    return npt == 0 ? 0 : min(PF_MAXP - 1, div_ceil(npt, T));
 }
-__device__ __forceinline__ int piece_count(int npt, int nct, int T) {
+__device__ __forceinline__ int piece_count(int npt, int nct, const Divisor& T) {
     if (npt + nct == 0) return 0;
-    if (npt + nct <= T) return 1;
+    if (npt + nct <= T.d) return 1;
     const int pp = prefix_pieces(npt, nct, T);
-    return pp + min(PF_MAXP - pp, cdiv_i(nct, T));
+    return pp + min(PF_MAXP - pp, div_ceil(nct, T));
 }
 
 // The launch's work list, computed identically by every workgroup from the tile metadata:
@@ -158,7 +173,7 @@ struct SubBlock {
 };
 
 __device__ __forceinline__ void fill_sub_block(SubBlock& s, int r0, int r1, int seq_start, int P,
-                                               int slot, int T) {
+                                               int slot, const Divisor& T) {
     s.r0 = r0;
     s.r1 = r1;
     s.seq_start = seq_start;
@@ -185,9 +200,10 @@ __device__ Loc schedule(const PrefillArgs& a, int target) {
     __shared__ int s_cu[PF_MAX_ENTRIES + 1], s_cc[PF_MAX_ENTRIES + 1], s_sl[PF_MAX_ENTRIES];
     const int lane = threadIdx.x & 63;
     const int nchunks = cdiv_i(a.nsb, IE_WAVE);
+    const Divisor spt = divisor(a.sub_per_tile);
     auto sb_of = [&](int c) { return a.nsb - 1 - (c * IE_WAVE + lane); };
     auto row_start_of = [&](int sb) {
-        return sb >= 0 && sb < a.nsb ? a.tile_start[sb / a.sub_per_tile] : -1;
+        return sb >= 0 && sb < a.nsb ? a.tile_start[div_floor(sb, spt)] : -1;
     };
     // the round trip: tile starts first, then the entry tables (all independent loads)
     int rs[PF_SCHED_CHUNKS];
@@ -208,7 +224,7 @@ __device__ Loc schedule(const PrefillArgs& a, int target) {
             else hi = mid - 1;
         }
         const int seq_start = s_cu[lo], seq_end = s_cu[lo + 1];
-        const int sub = sb - (sb / a.sub_per_tile) * a.sub_per_tile;
+        const int sub = sb - div_floor(sb, spt) * a.sub_per_tile;
         const int r0 = row_start + sub * PF_BM;
         const int r1 = min(min(r0 + PF_BM, row_start + a.block_m), seq_end);
         if (r0 >= r1) return z;
@@ -249,19 +265,33 @@ __device__ Loc schedule(const PrefillArgs& a, int target) {
     L.T = PF_UNSPLIT;
     if (spare > 0) {
         L.T = max(PF_MIN_PIECE_TILES, cdiv_i(tot * a.hkv, spare));
-        for (int T = max(PF_MIN_PIECE_TILES, cdiv_i(tot * a.hkv, a.grid)); T < L.T; ++T)
-            if (launch_sum([&](const SbInfo& z) { return piece_count(z.npt, z.nct, T); }) * a.hkv <=
+        for (int T = max(PF_MIN_PIECE_TILES, cdiv_i(tot * a.hkv, a.grid)); T < L.T; ++T) {
+            const Divisor D = divisor(T);
+            if (launch_sum([&](const SbInfo& z) { return piece_count(z.npt, z.nct, D); }) * a.hkv <=
                 a.grid) {
                 L.T = T;
                 break;
             }
+        }
     }
+    const Divisor DT = divisor(L.T);
+    int np[PF_SCHED_CHUNKS];  // pieces of the lane's sub-blocks
+#pragma unroll
+    for (int c = 0; c < PF_SCHED_CHUNKS; ++c) np[c] = piece_count(zc[c].npt, zc[c].nct, DT);
     L.found = 0;
     L.sb = L.off = L.item_base = L.split_index = 0;
-    L.nsplit = launch_sum([&](const SbInfo& z) { return piece_count(z.npt, z.nct, L.T) > 1; });
+    {
+        int ns = 0;
+#pragma unroll
+        for (int c = 0; c < PF_SCHED_CHUNKS; ++c) ns += np[c] > 1;
+        for (int c = PF_SCHED_CHUNKS; c < nchunks; ++c) {
+            const SbInfo z = info(sb_of(c), row_start_of(sb_of(c)));
+            ns += piece_count(z.npt, z.nct, DT) > 1;
+        }
+        L.nsplit = uni(wave_sum_i(ns));
+    }
     int items_before = 0, split_before = 0;
-    auto visit = [&](int c, const SbInfo& z) {
-        const int np = piece_count(z.npt, z.nct, L.T);
+    auto visit = [&](int c, const SbInfo& z, int np) {
         const int items = np * a.hkv;
         const int incl = wave_incl_scan_i(items) + items_before;
         const int sincl = wave_incl_scan_i(np > 1) + split_before;
@@ -274,7 +304,7 @@ __device__ Loc schedule(const PrefillArgs& a, int target) {
             L.off = target - L.item_base;
             L.split_index = from(sincl - (np > 1));
             fill_sub_block(L.s, from(z.r0), from(z.r1), from(z.seq_start), from(z.P),
-                           from(z.slot), L.T);
+                           from(z.slot), DT);
             L.found = 1;
         }
         items_before = uni(__shfl(incl, 63, IE_WAVE));
@@ -283,9 +313,11 @@ __device__ Loc schedule(const PrefillArgs& a, int target) {
     };
 #pragma unroll
     for (int c = 0; c < PF_SCHED_CHUNKS; ++c)
-        if (c < nchunks && visit(c, zc[c])) return L;
-    for (int c = PF_SCHED_CHUNKS; c < nchunks; ++c)
-        if (visit(c, info(sb_of(c), row_start_of(sb_of(c))))) return L;
+        if (c < nchunks && visit(c, zc[c], np[c])) return L;
+    for (int c = PF_SCHED_CHUNKS; c < nchunks; ++c) {
+        const SbInfo z = info(sb_of(c), row_start_of(sb_of(c)));
+        if (visit(c, z, piece_count(z.npt, z.nct, DT))) return L;
+    }
     return L;
 }
 
