@@ -171,8 +171,9 @@ hipError_t ie_dequantize_kv_prefix(const ie_kv_cache* cache, const int32_t* cu_c
 
 /*
  * Causal chunked-prefill attention that reads each entry's cached prefix straight from the int8
- * cache (dequantized in LDS with the same rounding as ie_dequantize_kv_prefix) and runs QK^T and
- * PV on bf16 MFMA.
+ * cache and runs QK^T and PV on bf16 MFMA: prefix V is dequantized in LDS with the rounding of
+ * ie_dequantize_kv_prefix, prefix K is staged as exact integers with its scale and calibration
+ * folded into the scores and into q.
  * Replaces qwen3-1.7b/kernels.py:1129-1175 `prefill_attention(q, k, v, seq_ids, cu_seqlens,
  * tile_start, k_prefix, v_prefix, cu_cached, PREFILL_BLOCK_M)` (kernel kernels.py:987-1126)
  * together with the dequantize_kv_prefix call that fed it (qwen3-1.7b/architecture.py:151-170):

@@ -7,33 +7,32 @@
 // dot(q, k) * D^-0.5 * log2(e); softmax in base 2; P is rounded to bf16 before PV;
 // out = acc / l (as acc * (1 / l)), or 0 when l == 0.
 //
-// Dequantization with the scales folded out of the tiles: int8 -> bf16 is exact, so the
-// staged prefix tiles hold the raw integers and the scales go where they cost one multiply:
+// Prefix K with its scales folded out of the tile: int8 -> bf16 is exact, so the staged K tiles
+// hold the raw integers and the scales go where they cost nothing extra:
 //   S(row, key) = (sum_d bf16(q[d] * cal[d]) * k_int8[key][d]) * (k_scale[key] * D^-0.5 log2 e)
-//   PV          = sum_key bf16(p[key] * v_scale[key]) * v_int8[key][d]
-// (the reference rounds bf16((k_int8 * k_scale) * cal) and bf16(v_int8 * v_scale) instead: same
-// quantities, roundings in different places, well inside bf16 attention tolerance).
+// (the reference rounds bf16((k_int8 * k_scale) * cal) instead: same quantity, the rounding in
+// another place, well inside bf16 attention tolerance). Prefix V is staged dequantized,
+// bf16(v_int8 * v_scale), exactly as the reference rounds it.
 //
 // Work: sub-blocks of up to 64 packed rows of one tile of `block_m` rows (tile_start, -1 = no
 // work), both query heads of one KV head per workgroup. Every workgroup reads the tile metadata
 // (one wave, a few hundred sub-blocks at most) and derives the same work list: the key range of
-// a (sub-block, kv head) pair (prefix tiles, then chunk tiles up to its last row) is cut into
-// pieces of about T 64-key tiles, T chosen so that the pieces fill one resident wave of
-// workgroups (2 per CU). Workgroup w runs piece w of the list (largest sub-blocks first).
-// Unsplit pieces write `out`; split pieces write a bf16 partial O (normalized) and fp32 (m, l)
-// to their slot, and prefill_combine_kernel merges them (log-sum-exp) from the split list the
-// main kernel records.
+// a (sub-block, kv head) pair (prefix tiles, then chunk tiles up to its last row) is one piece,
+// or, when longer than T 64-key tiles, prefix pieces and chunk pieces of at most T tiles, T the
+// smallest size whose pieces fit one resident wave of workgroups (2 per CU). Workgroup w runs
+// piece w of the list (largest sub-blocks first). Unsplit pieces write `out`; split pieces
+// write a bf16 partial O (normalized) and fp32 (m, l) to their slot, and prefill_combine_kernel
+// merges them (log-sum-exp) from the split list the main kernel records.
 //
-// Per 64-key tile: the workgroup stages K as [key][d] and V transposed as [d][key] in LDS (two
-// buffers: the next tile is staged while this one is consumed, one barrier per tile), and the
-// tile's score/probability scales; wave w (query head 2hk + (w & 1), rows 32 (w >> 1)..+32)
-// computes
+// Per 64-key tile: the workgroup stages K as [key][d] and V transposed as [d][key] in LDS, and
+// the tile's score scales; wave w (query head 2hk + (w & 1), rows 32 (w >> 1)..+32) computes
 //   S^T (64 keys x 32 rows) = K . Q^T   v_mfma_f32_16x16x32_bf16, A = K from LDS, B = Q^T in VGPRs
 //   online softmax on S^T (a lane holds one row's scores for 16 keys)
 //   O^T (128 d x 32 rows) += V^T . P^T  A = V^T from LDS, B = P^T straight from the S^T
-//                                       accumulators (same key permutation in A and B).
-// The next tile's global loads are issued before the current tile's MFMA work, and the tile
-// three ahead is prefetched into L2.
+//                                       accumulators (same key permutation in A and B)
+//   l += ones . P^T                     the row sums, on the MFMA as well
+// software-pipelined: the QK^T of tile j+1 beside the softmax of tile j, the PV of tile j beside
+// the staging of the next K and V tiles, whose global loads were issued a step earlier.
 #include "ie_common.h"
 
 namespace ie {
