@@ -5,8 +5,9 @@ D=128 — µs per layer and achieved HBM GB/s against the 8 TB/s peak. One step 
 `decode_attention` call (split kernel + reduce kernel) over the whole batch, inputs resident in
 HBM. Distinct cache sets are rotated between steps so the 256 MB MALL cannot serve a repeat.
 
-Also reported beside it (extra keys): config-4 KV quantize-on-write and chunked-prefill
-attention, each timed with HIP events on the stream the kernels run on, and config 5: a whole
+Also reported beside it (extra keys): config-4 KV quantize-on-write, chunked-prefill attention
+and the prefill q/k RMSNorm + RoPE of its 1,024 packed tokens, each timed with HIP events on the
+stream the kernels run on, and config 5: a whole
 greedy decode step of a Qwen3-1.7B-shaped model (28 layers, random weights, B=32, ctx ~
 U[128, 4096)) replayed as a hipGraph, with the share of the step spent in the attention kernels
 (the same kernels captured alone).
@@ -95,6 +96,23 @@ def time_op(fn, steps, warmup):
     e1.record()
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / steps
+
+
+def bench_norm_rope(K, N, steps, warmup, dev):
+    """fused_norm_rope_prefill over N packed tokens whose q/k are strided views of a fused qkv
+    row (Qwen3-1.7B: 16 + 8 + 8 heads of 128). Algorithmic bytes: q and k read and written once
+    (bf16), plus the per-token cos/sin rows."""
+    g = torch.Generator().manual_seed(0)
+    qkv = torch.randn(N, 32 * 128, generator=g).bfloat16().to(dev)
+    w = (1 + 0.1 * torch.randn(2, 128, generator=g)).bfloat16().to(dev)
+    ang = torch.rand(N, 1, 64, generator=g) * 1000
+    cos, sin = ang.cos().bfloat16().to(dev), ang.sin().bfloat16().to(dev)
+    q, k = qkv[:, :2048].view(N, 16, 128), qkv[:, 2048:3072].view(N, 8, 128)
+    ms = time_op(lambda: K.fused_norm_rope_prefill(q, k, w[0], w[1], cos, sin, 1e-6), steps,
+                 warmup)
+    nbytes = N * 24 * 128 * 2 * 2 + N * 64 * 2 * 2
+    return {"us": round(ms * 1e3, 3), "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "bytes": nbytes, "tokens": N}
 
 
 def cpu_baseline(wl_gpu, min_seconds):
@@ -259,6 +277,13 @@ def main():
             extra["prefill_config4"] = {"error": str(e).splitlines()[0][:200]}
     except Exception as e:  # reported, never silently replaced
         extra["config4_error"] = str(e).splitlines()[0][:200]
+    # ---- config 4: prefill q/k RMSNorm + RoPE of the 1,024 packed prefill tokens ----
+    try:
+        extra["norm_rope_prefill_config4"] = bench_norm_rope(K, 1024, args.steps, args.warmup,
+                                                             dev)
+        log(f"norm rope prefill config4 {extra['norm_rope_prefill_config4']}")
+    except Exception as e:  # reported, never silently replaced
+        extra["norm_rope_prefill_config4"] = {"error": str(e).splitlines()[0][:200]}
 
     if not args.no_step:
         log("config 5: Qwen3-1.7B-shaped decode step (hipGraph)")

@@ -158,6 +158,30 @@ hipError_t ie_decode_attention_combine(int32_t batch, int32_t num_q_heads, int32
                                        hipStream_t stream);
 
 /*
+ * Prefill-side q/k RMSNorm + RoPE over packed tokens.
+ * Replaces qwen3-1.7b/kernels.py:665-714 `fused_norm_rope_prefill(q, k, q_norm_weight,
+ * k_norm_weight, cos, sin, eps) -> (q_out, k_out)` (kernel kernels.py:547-662).
+ *
+ * q: bf16 [N, num_q_heads, head_dim], k: bf16 [N, num_kv_heads, head_dim], any token/head
+ * strides with unit channel stride (views of the fused qkv output); weights bf16 [head_dim];
+ * cos, sin: bf16 [N, 1, head_dim / 2] with unit channel stride. For every token and head row x:
+ * x <- x * rstd * w with rstd exactly as in ie_fused_rope_kv_decode (butterfly sum of squares,
+ * IEEE 1 / sqrt), then (x1, x2) <- (x1 c - x2 s, x1 s + x2 c) over the two halves; q_out /
+ * k_out get the bf16 result (round to nearest even). head_dim must be 128.
+ */
+hipError_t ie_fused_norm_rope_prefill(const ie_bf16* q, int64_t q_stride_tok, int64_t q_stride_head,
+                                      const ie_bf16* k, int64_t k_stride_tok, int64_t k_stride_head,
+                                      const ie_bf16* q_norm_weight, const ie_bf16* k_norm_weight,
+                                      const ie_bf16* cos, int64_t cos_stride_tok,
+                                      const ie_bf16* sin, int64_t sin_stride_tok,
+                                      int64_t num_tokens, int32_t num_q_heads,
+                                      int32_t num_kv_heads, int32_t head_dim, float eps,
+                                      ie_bf16* q_out, int64_t q_out_stride_tok,
+                                      int64_t q_out_stride_head, ie_bf16* k_out,
+                                      int64_t k_out_stride_tok, int64_t k_out_stride_head,
+                                      hipStream_t stream);
+
+/*
  * int8 cache prefix -> bf16 (k = bf16((q * k_scale) * cal), v = bf16(q * v_scale)).
  * Replaces qwen3-1.7b/kernels.py:935-970 `dequantize_kv_prefix(cache, cu_cached, slot_ids,
  * k_out, v_out)` (kernel kernels.py:868-932). Entry b's prefix, cache row slot_ids[b] columns

@@ -1,8 +1,8 @@
 """MI355X-native int8-KV attention path of kbwal/inference-engine.
 
 Drop-in for the reference's attention kernel API (qwen3-1.7b/kernels.py): int8 quantize-on-write,
-split-K GQA decode attention, causal chunked-prefill attention on bf16 MFMA, and hipGraph capture
-of the decode step. The directory name is not a Python identifier, so import it with
+split-K GQA decode attention, causal chunked-prefill attention on bf16 MFMA, the prefill q/k
+RMSNorm + RoPE, and hipGraph capture of the decode step. The directory name is not a Python identifier, so import it with
 `importlib.import_module("inference-engine_amd")`.
 """
 
@@ -11,6 +11,7 @@ from .kernels import (  # noqa: F401
     LayerKVCache,
     decode_attention,
     dequantize_kv_prefix,
+    fused_norm_rope_prefill,
     fused_rope_kv_decode,
     make_layer_cache,
     prefill_attention,

@@ -39,6 +39,7 @@ __device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) { return pack_bf16x
 enum : int {
     DPP_XOR1 = 0xB1,        // quad_perm [1,0,3,2]
     DPP_XOR2 = 0x4E,        // quad_perm [2,3,0,1]
+    DPP_XOR3 = 0x1B,        // quad_perm [3,2,1,0]
     DPP_HALF_MIRROR = 0x141,  // lane i <- lane 7-i within each 8 lanes
     DPP_MIRROR = 0x140,       // lane i <- lane 15-i within each 16 lanes
     DPP_ROR8 = 0x128,         // lane i <- lane (i+8)%16 within each 16 lanes
@@ -110,19 +111,20 @@ __device__ __forceinline__ float max16(float x) {
     x = fmaxf(x, dpp<DPP_MIRROR>(x));
     return x;
 }
-// Max over the 64 lanes of the wave.
-__device__ __forceinline__ float wave_max(float x) {
-    x = max16(x);
-    x = fmaxf(x, shfl_xor(x, 16));
-    x = fmaxf(x, shfl_xor(x, 32));
-    return x;
-}
+// Max over the 64 lanes of the wave (all on the VALU: DPP within rows of 16, then the gfx950
+// lane swaps across rows).
+__device__ __forceinline__ float wave_max(float x) { return max_xor32(max_xor16(max16(x))); }
 // Sum over the 64 lanes in the fixed butterfly order: lane i adds lane i^32, i^16, ..., i^1.
 // fp32 addition is commutative, so after each step lanes i and i^m hold the same bits and the
-// result is identical in every lane.
+// result is identical in every lane. All on the VALU: the lane swaps for 32 and 16, row_ror:8
+// for 8, quad_perm [3,2,1,0] then row_half_mirror (lane i <- 7 - (i ^ 3) = i ^ 4) for 4, and
+// quad_perm for 2 and 1.
 __device__ __forceinline__ float wave_sum_butterfly(float x) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) x = x + shfl_xor(x, m);
+    x = sum_xor16(sum_xor32(x));
+    x = x + dpp<DPP_ROR8>(x);
+    x = x + dpp<DPP_HALF_MIRROR>(dpp<DPP_XOR3>(x));
+    x = x + dpp<DPP_XOR2>(x);
+    x = x + dpp<DPP_XOR1>(x);
     return x;
 }
 

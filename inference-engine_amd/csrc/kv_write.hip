@@ -197,6 +197,35 @@ __global__ __launch_bounds__(QP_THREADS) void quantize_kv_prefill_kernel(
     }
 }
 
+// RMSNorm then RoPE of one head row, shared by the decode write and the prefill norm/rope
+// (kernels.py:414-436 and :582-646 compute the same thing): lane i holds channels i and i + 64
+// (the pair RoPE rotates); the sum of squares in the fixed butterfly order,
+// rstd = 1 / sqrt(ss / 128 + eps), x * rstd * w, then the rotation with the row's cos/sin.
+// IEEE single-precision operations, no contraction.
+// The three parts: the row's sum of squares (every lane gets it), rstd from it, and the
+// normalization and rotation of the lane's two channels.
+__device__ __forceinline__ float row_sumsq(float x1, float x2) {
+#pragma clang fp contract(off)
+    return wave_sum_butterfly(x1 * x1) + wave_sum_butterfly(x2 * x2);
+}
+__device__ __forceinline__ float row_rstd(float ss, float eps) {
+#pragma clang fp contract(off)
+    const float var = ss / 128.0f + eps;
+    return 1.0f / sqrtf(var);
+}
+__device__ __forceinline__ void row_norm_rope(float x1, float x2, float rstd, float w1, float w2,
+                                              float cs, float sn, float& o1, float& o2) {
+#pragma clang fp contract(off)
+    x1 = (x1 * rstd) * w1;
+    x2 = (x2 * rstd) * w2;
+    o1 = (x1 * cs) - (x2 * sn);
+    o2 = (x1 * sn) + (x2 * cs);
+}
+__device__ __forceinline__ void norm_rope_row(float x1, float x2, float w1, float w2, float cs,
+                                              float sn, float eps, float& o1, float& o2) {
+    row_norm_rope(x1, x2, row_rstd(row_sumsq(x1, x2), eps), w1, w2, cs, sn, o1, o2);
+}
+
 // grid (B, ceil((Hq + Hkv) / 4)), block 256: wave w of workgroup y handles head row
 // r = 4y + w; r < Hq is query head r, else kv head r - Hq (its K and V). Lane i holds channels
 // i and i + 64 (the two halves RoPE pairs, kernels.py:410-436).
@@ -222,21 +251,11 @@ __global__ __launch_bounds__(256) void fused_rope_kv_decode_kernel(
 
     const uint16_t* src = is_q ? q + b * q_sb + row * q_sh : k + b * k_sb + j * k_sh;
     const uint16_t* w = is_q ? qw : kw;
-    float x1 = bf16_to_f32(src[lane]);
-    float x2 = bf16_to_f32(src[lane + 64]);
-
-    // RMSNorm (kernels.py:417-419 / :426-428) in the fixed butterfly order.
-    const float ss = wave_sum_butterfly(x1 * x1) + wave_sum_butterfly(x2 * x2);
-    const float var = ss / 128.0f + eps;
-    const float rstd = 1.0f / sqrtf(var);
-    x1 = (x1 * rstd) * bf16_to_f32(w[lane]);
-    x2 = (x2 * rstd) * bf16_to_f32(w[lane + 64]);
-
-    // RoPE with bf16 cos/sin (kernels.py:430-436).
-    const float cs = bf16_to_f32(cosp[b * cos_sb + lane]);
-    const float sn = bf16_to_f32(sinp[b * sin_sb + lane]);
-    const float o1 = (x1 * cs) - (x2 * sn);
-    const float o2 = (x1 * sn) + (x2 * cs);
+    // RMSNorm (kernels.py:417-419 / :426-428), RoPE with bf16 cos/sin (kernels.py:430-436)
+    float o1, o2;
+    norm_rope_row(bf16_to_f32(src[lane]), bf16_to_f32(src[lane + 64]), bf16_to_f32(w[lane]),
+                  bf16_to_f32(w[lane + 64]), bf16_to_f32(cosp[b * cos_sb + lane]),
+                  bf16_to_f32(sinp[b * sin_sb + lane]), eps, o1, o2);
 
     const int slot = slot_ids[b];
     const float* cal = c.k_calibration + slot * c.cal_stride_slot + j * c.cal_stride_head;
@@ -269,6 +288,66 @@ __global__ __launch_bounds__(256) void fused_rope_kv_decode_kernel(
         c.v[base + lane] = (int8_t)quant1(v1, s);
         c.v[base + lane + 64] = (int8_t)quant1(v2, s);
         if (lane == 0) c.v_scale[sidx] = s;
+    }
+}
+
+constexpr int NR_ROWS_PER_WAVE = 8;
+constexpr int NR_ROWS_PER_WG = 4 * NR_ROWS_PER_WAVE;
+
+// grid (N, ceil((Hq + Hkv) / 32)), block 256 (kernels.py:547-646): wave w of workgroup (t, y)
+// normalizes and rotates head rows r = 32y + w + 4i (i < 8) of packed token t; r < Hq is query
+// head r, else key head r - Hq. All of the wave's row loads are issued before the first row is
+// computed. Lane i holds channels i and i + 64. Every lane holds every row's sum of squares, so
+// lane i computes rstd of row i only (one IEEE sqrt and division per lane instead of one per
+// row) and the rows read it back with v_readlane.
+__global__ __launch_bounds__(256) void fused_norm_rope_prefill_kernel(
+    const uint16_t* __restrict__ q, int64_t q_st, int64_t q_sh,
+    const uint16_t* __restrict__ k, int64_t k_st, int64_t k_sh,
+    const uint16_t* __restrict__ qw, const uint16_t* __restrict__ kw,
+    const uint16_t* __restrict__ cosp, int64_t cos_st,
+    const uint16_t* __restrict__ sinp, int64_t sin_st, int hq, int hkv, float eps,
+    uint16_t* __restrict__ qo, int64_t qo_st, int64_t qo_sh,
+    uint16_t* __restrict__ ko, int64_t ko_st, int64_t ko_sh) {
+    const int64_t t = blockIdx.x;
+    const int lane = threadIdx.x & 63;
+    const int r0 = NR_ROWS_PER_WG * blockIdx.y + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int rows = hq + hkv;
+    uint16_t a[NR_ROWS_PER_WAVE], b[NR_ROWS_PER_WAVE];
+#pragma unroll
+    for (int i = 0; i < NR_ROWS_PER_WAVE; ++i) {
+        const int r = r0 + 4 * i;
+        if (r < rows) {
+            const uint16_t* src = r < hq ? q + t * q_st + r * q_sh : k + t * k_st + (r - hq) * k_sh;
+            a[i] = src[lane];
+            b[i] = src[lane + 64];
+        }
+    }
+    const float cs = bf16_to_f32(cosp[t * cos_st + lane]);
+    const float sn = bf16_to_f32(sinp[t * sin_st + lane]);
+    const float qw1 = bf16_to_f32(qw[lane]), qw2 = bf16_to_f32(qw[lane + 64]);
+    const float kw1 = bf16_to_f32(kw[lane]), kw2 = bf16_to_f32(kw[lane + 64]);
+    float my_ss = 0.f;  // lane i: the sum of squares of row i
+#pragma unroll
+    for (int i = 0; i < NR_ROWS_PER_WAVE; ++i) {
+        const int r = r0 + 4 * i;
+        if (r >= rows) break;
+        const float ss = row_sumsq(bf16_to_f32(a[i]), bf16_to_f32(b[i]));
+        my_ss = lane == i ? ss : my_ss;
+    }
+    const float my_rstd = row_rstd(my_ss, eps);
+#pragma unroll
+    for (int i = 0; i < NR_ROWS_PER_WAVE; ++i) {
+        const int r = r0 + 4 * i;
+        if (r >= rows) break;
+        const bool is_q = r < hq;
+        const float rstd = __builtin_bit_cast(
+            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_rstd), i));
+        float o1, o2;
+        row_norm_rope(bf16_to_f32(a[i]), bf16_to_f32(b[i]), rstd, is_q ? qw1 : kw1,
+                      is_q ? qw2 : kw2, cs, sn, o1, o2);
+        uint16_t* dst = is_q ? qo + t * qo_st + r * qo_sh : ko + t * ko_st + (r - hq) * ko_sh;
+        dst[lane] = (uint16_t)f32_to_bf16_rne(o1);
+        dst[lane + 64] = (uint16_t)f32_to_bf16_rne(o2);
     }
 }
 
@@ -372,6 +451,32 @@ extern "C" hipError_t ie_fused_rope_kv_decode(
                        slot_ids, cached_lens, num_decoding, num_q_heads,
                        num_q_heads / (int)cache->num_kv_heads, eps, *cache, (uint16_t*)q_out,
                        q_out_stride_b, q_out_stride_h);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t ie_fused_norm_rope_prefill(
+    const ie_bf16* q, int64_t q_stride_tok, int64_t q_stride_head, const ie_bf16* k,
+    int64_t k_stride_tok, int64_t k_stride_head, const ie_bf16* q_norm_weight,
+    const ie_bf16* k_norm_weight, const ie_bf16* cos, int64_t cos_stride_tok, const ie_bf16* sin,
+    int64_t sin_stride_tok, int64_t num_tokens, int32_t num_q_heads, int32_t num_kv_heads,
+    int32_t head_dim, float eps, ie_bf16* q_out, int64_t q_out_stride_tok,
+    int64_t q_out_stride_head, ie_bf16* k_out, int64_t k_out_stride_tok,
+    int64_t k_out_stride_head, hipStream_t stream) {
+    IE_REQUIRE(num_tokens >= 0 && num_q_heads >= 0 && num_kv_heads >= 0, "negative sizes");
+    IE_REQUIRE(head_dim == 128, "head_dim must be 128");
+    if (num_tokens == 0 || num_q_heads + num_kv_heads == 0) return hipSuccess;
+    IE_REQUIRE(q && k && q_norm_weight && k_norm_weight && cos && sin && q_out && k_out,
+               "null pointer");
+    IE_REQUIRE(num_tokens < (1LL << 31), "too many tokens");
+    const int rows = num_q_heads + num_kv_heads;
+    dim3 grid((unsigned)num_tokens, (unsigned)((rows + NR_ROWS_PER_WG - 1) / NR_ROWS_PER_WG));
+    hipLaunchKernelGGL(fused_norm_rope_prefill_kernel, grid, dim3(256), 0, stream,
+                       (const uint16_t*)q, q_stride_tok, q_stride_head, (const uint16_t*)k,
+                       k_stride_tok, k_stride_head, (const uint16_t*)q_norm_weight,
+                       (const uint16_t*)k_norm_weight, (const uint16_t*)cos, cos_stride_tok,
+                       (const uint16_t*)sin, sin_stride_tok, num_q_heads, num_kv_heads, eps,
+                       (uint16_t*)q_out, q_out_stride_tok, q_out_stride_head, (uint16_t*)k_out,
+                       k_out_stride_tok, k_out_stride_head);
     return hipGetLastError();
 }
 

@@ -142,6 +142,37 @@ at::Tensor fused_rope_kv_decode(const at::Tensor& q, const at::Tensor& k, const 
     return out;
 }
 
+std::tuple<at::Tensor, at::Tensor> fused_norm_rope_prefill(const at::Tensor& q,
+                                                           const at::Tensor& k,
+                                                           const at::Tensor& q_norm_weight,
+                                                           const at::Tensor& k_norm_weight,
+                                                           const at::Tensor& cos,
+                                                           const at::Tensor& sin, double eps) {
+    check_bf16_rows(q, "q", 3);
+    check_bf16_rows(k, "k", 3);
+    check_bf16_rows(q_norm_weight, "q_norm_weight", 1);
+    check_bf16_rows(k_norm_weight, "k_norm_weight", 1);
+    check_bf16_rows(cos, "cos", 3);
+    check_bf16_rows(sin, "sin", 3);
+    const c10::DeviceGuard guard(q.device());
+    const int64_t N = q.size(0), hq = q.size(1), hkv = k.size(1), D = q.size(2);
+    TORCH_CHECK(D == 128 && k.size(2) == D, "ie: head_dim 128");
+    TORCH_CHECK(k.size(0) == N && cos.size(0) >= N && sin.size(0) >= N && cos.size(2) == D / 2 &&
+                    sin.size(2) == D / 2,
+                "ie: k [N, Hkv, D], cos/sin [N, 1, D/2]");
+    TORCH_CHECK(q_norm_weight.size(0) == D && k_norm_weight.size(0) == D, "ie: norm weights [D]");
+    at::Tensor q_out = at::empty({N, hq, D}, q.options());
+    at::Tensor k_out = at::empty({N, hkv, D}, k.options());
+    ok(ie_fused_norm_rope_prefill(bf(q), q.stride(0), q.stride(1), bf(k), k.stride(0), k.stride(1),
+                                  bf(q_norm_weight), bf(k_norm_weight), bf(cos), cos.stride(0),
+                                  bf(sin), sin.stride(0), N, (int32_t)hq, (int32_t)hkv,
+                                  (int32_t)D, (float)eps, bfm(q_out), q_out.stride(0),
+                                  q_out.stride(1), bfm(k_out), k_out.stride(0), k_out.stride(1),
+                                  stream_of(q)),
+       "fused_norm_rope_prefill");
+    return {q_out, k_out};
+}
+
 struct DecodeCall {
     ie_kv_cache c;
     int32_t B, hq;
@@ -290,6 +321,9 @@ TORCH_LIBRARY(ie, m) {
         "Tensor(b!) v_cache, Tensor(c!) k_scale, Tensor(d!) v_scale, Tensor k_calibration, "
         "Tensor cached_lens, Tensor num_decoding, float eps) -> Tensor");
     m.def(
+        "fused_norm_rope_prefill(Tensor q, Tensor k, Tensor q_norm_weight, Tensor k_norm_weight, "
+        "Tensor cos, Tensor sin, float eps) -> (Tensor, Tensor)");
+    m.def(
         "decode_attention(Tensor q, Tensor k_cache, Tensor v_cache, Tensor k_scale, "
         "Tensor v_scale, Tensor k_calibration, Tensor cached_lens, Tensor slot_ids, "
         "Tensor num_decoding, float scale, Tensor(a!) out) -> ()");
@@ -315,6 +349,7 @@ TORCH_LIBRARY(ie, m) {
 TORCH_LIBRARY_IMPL(ie, CUDA, m) {
     m.impl("quantize_kv_prefill", &quantize_kv_prefill);
     m.impl("fused_rope_kv_decode", &fused_rope_kv_decode);
+    m.impl("fused_norm_rope_prefill", &fused_norm_rope_prefill);
     m.impl("decode_attention", &decode_attention);
     m.impl("decode_attention_split", &decode_attention_split);
     m.impl("decode_attention_combine", &decode_attention_combine);

@@ -113,6 +113,21 @@ def fused_rope_kv_decode(
                                       float(eps))
 
 
+def fused_norm_rope_prefill(
+    q: torch.Tensor,  # bf16 [N, Hq, D], the prefill rows only: q[num_seqs_decoding:]
+    k: torch.Tensor,  # bf16 [N, Hkv, D]
+    q_norm_weight: torch.Tensor,  # [D]
+    k_norm_weight: torch.Tensor,
+    cos: torch.Tensor,  # [N, 1, D // 2]
+    sin: torch.Tensor,
+    eps: float,
+) -> tuple:
+    """qwen3-1.7b/kernels.py:665-714: normed + roped (q, k), contiguous."""
+    assert q.stride(-1) == 1 and k.stride(-1) == 1, "kernel assumes contiguous head_dim"
+    assert cos.stride(-1) == 1 and sin.stride(-1) == 1
+    return ops().fused_norm_rope_prefill(q, k, q_norm_weight, k_norm_weight, cos, sin, float(eps))
+
+
 def quantize_kv_prefill(
     k: torch.Tensor,  # bf16 [N, Hkv, D], all sequences packed along N
     v: torch.Tensor,  # bf16 [N, Hkv, D]

@@ -1,9 +1,10 @@
 """Oracle for the int8 KV cache writes and reads (test infrastructure only; see oracle/__init__.py).
 
 Restates qwen3-1.7b/kernels.py:
-  quantize_kv_prefill   :717-865
-  fused_rope_kv_decode  :364-544
-  dequantize_kv_prefix  :868-970
+  quantize_kv_prefill      :717-865
+  fused_rope_kv_decode     :364-544
+  fused_norm_rope_prefill  :547-714 (the same RMSNorm + RoPE, without the cache write)
+  dequantize_kv_prefix     :868-970
 with the cache container of :11-17 and the allocation of qwen3-1.7b/engine.py:472-492.
 All arithmetic is numpy float32 (IEEE round-to-nearest-even, no fused multiply-add), in the
 operation order of the reference source.
@@ -151,6 +152,19 @@ def fused_rope_kv_decode(q, k, v, q_norm_weight, k_norm_weight, cos, sin, slot_i
             cache.v[slot, j, col] = vq
             cache.v_scale[slot, j, col] = vs
     return out
+
+
+def fused_norm_rope_prefill(q, k, q_norm_weight, k_norm_weight, cos, sin, eps):
+    """Prefill q/k RMSNorm + RoPE over packed tokens (kernels.py:547-662, wrapper :665-714).
+
+    q [N, Hq, D], k [N, Hkv, D], cos/sin [N, 1, D/2]: fp32 values of bf16 inputs; one cos/sin row
+    per token for all of its heads (:627-634). Returns (q_out, k_out) fp32 (bf16-rounded, the
+    bf16 store of :636-662).
+    """
+    q1, q2 = rmsnorm_rope(q, q_norm_weight, cos, sin, eps)
+    k1, k2 = rmsnorm_rope(k, k_norm_weight, cos, sin, eps)
+    return (bf16_round(np.concatenate([q1, q2], axis=-1)),
+            bf16_round(np.concatenate([k1, k2], axis=-1)))
 
 
 def dequantize_kv_prefix(cache: CacheArrays, cu_cached, slot_ids):

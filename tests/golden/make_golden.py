@@ -1,6 +1,6 @@
 """Writes the golden fixtures of tests/golden/*.npz from the numpy oracle on seeded inputs.
 
-    python tests/golden/make_golden.py
+    python tests/golden/make_golden.py [name ...]     # all fixtures, or the named ones
 
 The reference ships no test vectors, so these fixtures are this build's own pins: the CPU tests
 check that the oracle still reproduces them exactly (a regression guard on the restatement,
@@ -111,6 +111,29 @@ def rope_kv_decode():
             "after_v_scale": arr.v_scale}
 
 
+def norm_rope_prefill():
+    """fused_norm_rope_prefill for 19 packed prefill tokens of two chunks (positions 0..10 and
+    500..507): q/k are strided views of one fused qkv row, RoPE tables as the engine builds
+    them (architecture.py:343-354: inv_freq = 1e6^(-2i/128), angle = position * inv_freq)."""
+    g = torch.Generator().manual_seed(16)
+    N = 19
+    qkv = (2 * torch.randn(N, 32 * 128, generator=g)).bfloat16()
+    qw = (1 + 0.1 * torch.randn(128, generator=g)).bfloat16()
+    kw = (1 + 0.1 * torch.randn(128, generator=g)).bfloat16()
+    pos = torch.cat([torch.arange(0, 11), torch.arange(500, 508)]).float()
+    inv = 1e6 ** (-torch.arange(0, 128, 2, dtype=torch.float32) / 128)
+    ang = pos[:, None, None] * inv[None, None, :]
+    cos, sin = ang.cos().bfloat16(), ang.sin().bfloat16()
+    q = _bf16(qkv[:, :2048].view(N, 16, 128))
+    k = _bf16(qkv[:, 2048:3072].view(N, 8, 128))
+    q_out, k_out = okv.fused_norm_rope_prefill(q, k, _bf16(qw), _bf16(kw), _bf16(cos),
+                                               _bf16(sin), 1e-6)
+    return {"qkv_bits": bf16_bits(_bf16(qkv)), "qw_bits": bf16_bits(_bf16(qw)),
+            "kw_bits": bf16_bits(_bf16(kw)), "cos_bits": bf16_bits(_bf16(cos)),
+            "sin_bits": bf16_bits(_bf16(sin)), "q_out_bits": bf16_bits(q_out),
+            "k_out_bits": bf16_bits(k_out)}
+
+
 def decode_config1():
     """BASELINE config 1 (B=1, ctx=128) decode attention: inputs and the oracle's output."""
     wl = W.decode_workload([128], seed=14)
@@ -142,6 +165,7 @@ FIXTURES = {
     "quant_rows": quant_rows,
     "prefill_write": prefill_write,
     "rope_kv_decode": rope_kv_decode,
+    "norm_rope_prefill": norm_rope_prefill,
     "decode_config1": decode_config1,
     "prefill_small": prefill_small,
 }
@@ -152,7 +176,9 @@ def _np(d):
 
 
 def main():
-    for name, fn in FIXTURES.items():
+    names = sys.argv[1:] or list(FIXTURES)
+    for name in names:
+        fn = FIXTURES[name]
         path = HERE / f"{name}.npz"
         np.savez_compressed(path, **_np(fn()))
         print(f"wrote {path.relative_to(REPO)} ({path.stat().st_size} bytes)")

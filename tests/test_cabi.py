@@ -20,7 +20,8 @@ def test_library_exports_every_declared_symbol(native):
 
 def test_torch_ops_registered(ie):
     ops = ie.kernels.ops()
-    for name in ["quantize_kv_prefill", "fused_rope_kv_decode", "decode_attention",
+    for name in ["quantize_kv_prefill", "fused_rope_kv_decode", "fused_norm_rope_prefill",
+                 "decode_attention",
                  "decode_attention_split", "decode_attention_combine", "dequantize_kv_prefix",
                  "prefill_attention", "decode_attention_workspace_size"]:
         assert hasattr(ops, name), name

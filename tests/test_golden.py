@@ -3,8 +3,9 @@
 CPU: the oracle still reproduces every fixture (bit-exact for int8 values, scales and bf16 bits;
 1e-6 for fp32 attention outputs, whose BLAS summation order may differ between machines), and the
 attention fixtures agree with the float64 textbook forms within the bf16 tolerance.
-GPU: the HIP path, through the torch ops, on the fixtures' inputs: bit-exact for the cache writes
-and the decode q, within the attention tolerance for decode and prefill attention."""
+GPU: the HIP path, through the torch ops, on the fixtures' inputs: bit-exact for the cache writes,
+the decode q and the prefill q/k norm + rope, within the attention tolerance for decode and
+prefill attention."""
 
 from pathlib import Path
 
@@ -87,6 +88,18 @@ def test_fixture_rope_kv_decode():
     assert np.array_equal(bf16_bits(q_out), d["q_out_bits"])
     for n in ("k", "v", "k_scale", "v_scale"):
         assert bitwise_equal(getattr(c, n), d[f"after_{n}"]), n
+
+
+def test_fixture_norm_rope_prefill():
+    d = load("norm_rope_prefill")
+    qkv = f32(d["qkv_bits"])
+    N = qkv.shape[0]
+    qo, ko = okv.fused_norm_rope_prefill(qkv[:, :2048].reshape(N, 16, 128),
+                                         qkv[:, 2048:3072].reshape(N, 8, 128), f32(d["qw_bits"]),
+                                         f32(d["kw_bits"]), f32(d["cos_bits"]),
+                                         f32(d["sin_bits"]), 1e-6)
+    assert np.array_equal(bf16_bits(qo), d["q_out_bits"])
+    assert np.array_equal(bf16_bits(ko), d["k_out_bits"])
 
 
 def test_fixture_decode_config1():
@@ -187,6 +200,20 @@ def test_gpu_rope_kv_decode(ie, dev):
     got = cache_np(cache)
     for n in ("k", "v", "k_scale", "v_scale"):
         assert bitwise_equal(getattr(got, n), d[f"after_{n}"]), n
+
+
+@pytest.mark.gpu
+def test_gpu_norm_rope_prefill(ie, dev):
+    say("golden norm_rope_prefill")
+    d = load("norm_rope_prefill")
+    qkv = _t(d["qkv_bits"], dev)
+    N = qkv.shape[0]
+    q_out, k_out = ie.fused_norm_rope_prefill(
+        qkv[:, :2048].view(N, 16, 128), qkv[:, 2048:3072].view(N, 8, 128), _t(d["qw_bits"], dev),
+        _t(d["kw_bits"], dev), _t(d["cos_bits"], dev), _t(d["sin_bits"], dev), 1e-6)
+    torch.cuda.synchronize()
+    assert np.array_equal(bf16_bits(bf16_np(q_out)), d["q_out_bits"])
+    assert np.array_equal(bf16_bits(bf16_np(k_out)), d["k_out_bits"])
 
 
 @pytest.mark.gpu

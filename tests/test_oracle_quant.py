@@ -149,6 +149,73 @@ def test_decode_write_matches_float64_norm_rope():
         assert np.abs(cache.v[slot, :, lens[b]] - np.rint(v[b] / vs64[:, None])).max() <= 1
 
 
+def _norm_rope64(x, w, c, s):
+    """float64 textbook: torch RMSNorm, then RoPE as a complex rotation of the two halves."""
+    xn = torch.nn.functional.rms_norm(torch.tensor(x, dtype=torch.float64), (128,),
+                                      torch.tensor(w, dtype=torch.float64), eps=1e-6).numpy()
+    z = (xn[..., :64] + 1j * xn[..., 64:]) * (c + 1j * s)
+    return np.concatenate([z.real, z.imag], axis=-1)
+
+
+def test_prefill_norm_rope_matches_float64():
+    rng = np.random.default_rng(5)
+    gen = torch.Generator().manual_seed(1)
+    N, hq, hkv = 37, 16, 8
+    q = (3 * torch.randn(N, hq, 128, generator=gen)).bfloat16().float().numpy()
+    k = torch.randn(N, hkv, 128, generator=gen).bfloat16().float().numpy()
+    qw = (1 + 0.1 * torch.randn(128, generator=gen)).bfloat16().float().numpy()
+    kw = (1 + 0.1 * torch.randn(128, generator=gen)).bfloat16().float().numpy()
+    ang = rng.uniform(0, 1000, (N, 1, 64))
+    cos = torch.tensor(np.cos(ang)).bfloat16().float().numpy()
+    sin = torch.tensor(np.sin(ang)).bfloat16().float().numpy()
+    qo, ko = okv.fused_norm_rope_prefill(q, k, qw, kw, cos, sin, 1e-6)
+    assert qo.shape == q.shape and ko.shape == k.shape
+    # each output is one bf16 rounding (relative 2^-9) of the float64 value, up to the fp32
+    # steps before it
+    for out, x, w in ((qo, q, qw), (ko, k, kw)):
+        ref = _norm_rope64(x, w, cos, sin)
+        assert np.all(np.abs(out - ref) <= 2 ** -8 * np.abs(ref) + 1e-6)
+    assert np.array_equal(qo, bf16_round(qo))  # bf16-representable
+
+
+def test_prefill_norm_rope_known_answers():
+    # a constant row c normalizes to sign(c) (up to eps); zero angle is the identity and a
+    # quarter turn maps (x1, x2) to (-x2, x1)
+    N = 2
+    x = np.zeros((N, 1, 128), np.float32)
+    x[0, 0, :] = 3.0
+    x[1, 0, :64], x[1, 0, 64:] = 1.0, -2.0
+    w = np.full(128, 0.5, np.float32)
+    cos = np.zeros((N, 1, 64), np.float32)
+    sin = np.zeros((N, 1, 64), np.float32)
+    cos[0], sin[1] = 1.0, 1.0
+    qo, ko = okv.fused_norm_rope_prefill(x, x, w, w, cos, sin, 0.0)
+    assert np.array_equal(qo, ko)
+    assert np.all(qo[0, 0] == F32(0.5))
+    # token 1: rms = sqrt((1 + 4) / 2), x1n = 0.5 / rms, x2n = -1 / rms; rotated: (-x2n, x1n)
+    rms = np.sqrt(2.5)
+    assert np.allclose(qo[1, 0, :64], 1.0 / rms, rtol=2 ** -8)
+    assert np.allclose(qo[1, 0, 64:], 0.5 / rms, rtol=2 ** -8)
+
+
+def test_prefill_norm_rope_is_the_decode_rotation():
+    # the decode write's q (before the calibration fold) and the prefill op share the math: with
+    # calibration ones the decode q_out equals the prefill q_out for the same rows
+    gen = torch.Generator().manual_seed(2)
+    B, hq, hkv = 4, 16, 8
+    q = torch.randn(B, hq, 128, generator=gen).bfloat16().float().numpy()
+    k = torch.randn(B, hkv, 128, generator=gen).bfloat16().float().numpy()
+    w = (1 + 0.1 * torch.randn(128, generator=gen)).bfloat16().float().numpy()
+    ang = np.random.default_rng(6).uniform(0, 50, (B, 1, 64))
+    cos = torch.tensor(np.cos(ang)).bfloat16().float().numpy()
+    sin = torch.tensor(np.sin(ang)).bfloat16().float().numpy()
+    cache = okv.CacheArrays.empty(B, hkv, 4, 128)
+    qd = okv.fused_rope_kv_decode(q, k, k, w, w, cos, sin, np.arange(B), cache,
+                                  np.zeros(B, np.int64), B, 1e-6)
+    qp, _ = okv.fused_norm_rope_prefill(q, k, w, w, cos, sin, 1e-6)
+    assert np.array_equal(qd, qp)
+
+
 def test_butterfly_sum_is_a_sum():
     rng = np.random.default_rng(3)
     x = rng.standard_normal((100, 64)).astype(np.float32)
