@@ -108,11 +108,39 @@ def bench_norm_rope(K, N, steps, warmup, dev):
     ang = torch.rand(N, 1, 64, generator=g) * 1000
     cos, sin = ang.cos().bfloat16().to(dev), ang.sin().bfloat16().to(dev)
     q, k = qkv[:, :2048].view(N, 16, 128), qkv[:, 2048:3072].view(N, 8, 128)
-    ms = time_op(lambda: K.fused_norm_rope_prefill(q, k, w[0], w[1], cos, sin, 1e-6), steps,
-                 warmup)
+    op = lambda: K.fused_norm_rope_prefill(q, k, w[0], w[1], cos, sin, 1e-6)
+    ms = time_op(op, steps, warmup)
+    gms = time_graph(op)
     nbytes = N * 24 * 128 * 2 * 2 + N * 64 * 2 * 2
-    return {"us": round(ms * 1e3, 3), "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
-            "bytes": nbytes, "tokens": N}
+    return {"us": round(ms * 1e3, 3), "us_graph": round(gms * 1e3, 3),
+            "GBps_graph": round(nbytes / (gms * 1e-3) / 1e9, 1), "bytes": nbytes, "tokens": N}
+
+
+def time_graph(fn, calls=20, reps=5):
+    """Average time per call of `calls` back-to-back calls captured in one hipGraph and replayed:
+    the GPU-side time of a µs-scale op without the host's per-call launch cost (an eager loop
+    of such calls measures the host as much as the kernels)."""
+    fn()
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(calls):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = _events(2)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / (reps * calls)
 
 
 def cpu_baseline(wl_gpu, min_seconds):
@@ -209,6 +237,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="minimum CPU-baseline work (whole batch, repeated)")
     ap.add_argument("--no-step", action="store_true", help="skip the config-5 decode step")
+    ap.add_argument("--norm-rope-tokens", type=int, default=1024,
+                    help="packed tokens of the prefill norm/rope line (config 4: 1024)")
     ap.add_argument("--sweep", action="store_true", help="also time the config-3 shape sweep")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run a plain device copy of MIB MiB 3 times (PMC calibration)")
@@ -253,24 +283,30 @@ def main():
     try:
         mw = W.mixed_to(W.config4(seed=0), dev)
         gi = mw.inputs
-        kv_ms = time_op(lambda: K.quantize_kv_prefill(mw.k, mw.v, gi["cu_seqlens"],
-                                                      gi["slot_ids"], gi["cached_lens"],
-                                                      gi["num_decoding"], mw.cache),
-                        args.steps, args.warmup)
+        kv_op = lambda: K.quantize_kv_prefill(mw.k, mw.v, gi["cu_seqlens"], gi["slot_ids"],
+                                              gi["cached_lens"], gi["num_decoding"], mw.cache)
+        kv_ms = time_op(kv_op, args.steps, args.warmup)
+        kv_gms = time_graph(kv_op)
         n_new = sum(L for L, _ in mw.chunks)
         kv_bytes = n_new * 8 * (128 * 2 * 2 + 128 * 2 + 8)
         extra["kv_write_config4"] = {"us": round(kv_ms * 1e3, 3),
                                      "GBps": round(kv_bytes / (kv_ms * 1e-3) / 1e9, 1),
-                                     "bytes": kv_bytes}
+                                     "us_graph": round(kv_gms * 1e3, 3), "bytes": kv_bytes}
         log(f"kv write config4 {kv_ms*1e3:.2f} us")
         flops = W.prefill_flops(mw.chunks)
         try:
-            pf_ms = time_op(lambda: K.prefill_attention(
+            pf_op = lambda: K.prefill_attention(
                 mw.q, mw.k, mw.v, gi["seq_ids"], gi["cu_seqlens"], gi["tile_start"], mw.cache,
-                gi["slot_ids"], gi["cu_cached"], mw.block_m), args.steps, args.warmup)
+                gi["slot_ids"], gi["cu_cached"], mw.block_m)
+            pf_ms = time_op(pf_op, args.steps, args.warmup)
+            pf_gms = time_graph(pf_op)
             tf = flops / (pf_ms * 1e-3) / 1e12
             extra["prefill_config4"] = {"us": round(pf_ms * 1e3, 3), "TFLOPs": round(tf, 1),
                                         "mfma_frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
+                                        "us_graph": round(pf_gms * 1e3, 3),
+                                        "mfma_frac_graph": round(
+                                            flops / (pf_gms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
+                                            4),
                                         "flops": flops}
             log(f"prefill config4 {pf_ms*1e3:.2f} us {tf:.1f} TFLOP/s")
         except RuntimeError as e:
@@ -279,8 +315,8 @@ def main():
         extra["config4_error"] = str(e).splitlines()[0][:200]
     # ---- config 4: prefill q/k RMSNorm + RoPE of the 1,024 packed prefill tokens ----
     try:
-        extra["norm_rope_prefill_config4"] = bench_norm_rope(K, 1024, args.steps, args.warmup,
-                                                             dev)
+        extra["norm_rope_prefill_config4"] = bench_norm_rope(K, args.norm_rope_tokens, args.steps,
+                                                             args.warmup, dev)
         log(f"norm rope prefill config4 {extra['norm_rope_prefill_config4']}")
     except Exception as e:  # reported, never silently replaced
         extra["norm_rope_prefill_config4"] = {"error": str(e).splitlines()[0][:200]}
