@@ -6,8 +6,8 @@ D=128 — µs per layer and achieved HBM GB/s against the 8 TB/s peak. One step 
 HBM. Distinct cache sets are rotated between steps so the 256 MB MALL cannot serve a repeat.
 
 Also reported beside it (extra keys): config-4 KV quantize-on-write, chunked-prefill attention
-and the prefill q/k RMSNorm + RoPE of its 1,024 packed tokens, each timed with HIP events on the
-stream the kernels run on, and config 5: a whole
+and the prefill q/k RMSNorm + RoPE of its 1,024 packed tokens, token sampling at config 5's shape,
+each timed with HIP events on the stream the kernels run on, and config 5: a whole
 greedy decode step of a Qwen3-1.7B-shaped model (28 layers, random weights, B=32, ctx ~
 U[128, 4096)) replayed as a hipGraph, with the share of the step spent in the attention kernels
 (the same kernels captured alone).
@@ -141,6 +141,24 @@ def time_graph(fn, calls=20, reps=5):
     e1.record()
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / (reps * calls)
+
+
+def bench_sample(K, B, V, steps, warmup, dev):
+    """`sample` over bf16 logits [B, V] (Qwen3-1.7B: V = 151,936): greedy (tau 0, one read of
+    the logits: B * V * 2 bytes) and Gumbel-max at tau 1 (the same bytes plus a Philox draw and
+    two logarithms per entry)."""
+    g = torch.Generator().manual_seed(0)
+    logits = (2 * torch.randn(B, V, generator=g)).bfloat16().to(dev)
+    seed = torch.zeros(1, dtype=torch.int64, device=dev)
+    nbytes = B * V * 2
+    res = {"batch": B, "vocab": V, "bytes": nbytes}
+    for tau in (0.0, 1.0):
+        op = lambda: K.sample(logits, tau, seed)
+        ms = time_op(op, steps, warmup)
+        gms = time_graph(op)
+        res[f"tau{tau:g}"] = {"us": round(ms * 1e3, 3), "us_graph": round(gms * 1e3, 3),
+                              "GBps_graph": round(nbytes / (gms * 1e-3) / 1e9, 1)}
+    return res
 
 
 def cpu_baseline(wl_gpu, min_seconds):
@@ -320,6 +338,13 @@ def main():
         log(f"norm rope prefill config4 {extra['norm_rope_prefill_config4']}")
     except Exception as e:  # reported, never silently replaced
         extra["norm_rope_prefill_config4"] = {"error": str(e).splitlines()[0][:200]}
+
+    # ---- config 5's sampler: B = 32 rows of the 151,936-entry vocabulary ----
+    try:
+        extra["sample_config5"] = bench_sample(K, 32, 151_936, args.steps, args.warmup, dev)
+        log(f"sample config5 {extra['sample_config5']}")
+    except Exception as e:  # reported, never silently replaced
+        extra["sample_config5"] = {"error": str(e).splitlines()[0][:200]}
 
     if not args.no_step:
         log("config 5: Qwen3-1.7B-shaped decode step (hipGraph)")

@@ -30,6 +30,9 @@ extern "C" {
 /* bf16 values travel as their 16-bit patterns. */
 typedef uint16_t ie_bf16;
 
+/* Element types an entry point may take at run time. */
+enum { IE_DTYPE_BF16 = 0, IE_DTYPE_F32 = 1 };
+
 /*
  * One layer's int8 KV cache (qwen3-1.7b/kernels.py:11-17 `LayerKVCache`; allocated by
  * qwen3-1.7b/engine.py:472-492). Layout, unchanged from the reference:
@@ -228,6 +231,26 @@ hipError_t ie_prefill_attention(const ie_bf16* q, int64_t q_stride_tok, int64_t 
                                 int64_t out_stride_tok,
                                 int64_t out_stride_head, void* workspace, size_t workspace_bytes,
                                 hipStream_t stream);
+
+/*
+ * Token sampling: Gumbel-max over the vocabulary, greedy argmax at tau = 0.
+ * Replaces qwen3-1.7b/kernels.py:1343-1370 `sample(logits, tau, seed) -> [B, 1] int64`
+ * (kernels sampling_kernel :1286-1318 and combine_partial_samples_kernel :1321-1340).
+ *
+ * logits: [batch, vocab] of logits_dtype (IE_DTYPE_BF16 or IE_DTYPE_F32), unit stride along the
+ * vocabulary, row stride logits_stride_row elements. out[b * out_stride_row] = the first v that
+ * maximizes logits[b, v] + tau * -log(-log(clamp(u, 1e-10, 1 - 1e-7))), where u is Triton's
+ * tl.rand(seed, b * vocab + v): Philox4x32-10 on counter (b * vocab + v as int32, 0, 0, 0) and
+ * key (low, high 32 bits of *seed), first output word x as int32,
+ * u = float(x < 0 ? -x - 1 : x) * 4.6566127342e-10. At tau = 0 no uniform is drawn. *seed (a
+ * device int64) is incremented once per call, after every row has read it, also when batch is
+ * 0. `workspace` must hold ie_sample_workspace_size(batch, vocab) bytes.
+ */
+size_t ie_sample_workspace_size(int32_t batch, int64_t vocab);
+hipError_t ie_sample(const void* logits, int32_t logits_dtype, int64_t logits_stride_row,
+                     int32_t batch, int64_t vocab, float tau, int64_t* seed, int64_t* out,
+                     int64_t out_stride_row, void* workspace, size_t workspace_bytes,
+                     hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -2,7 +2,7 @@
 
 Drop-in for the reference's attention kernel API (qwen3-1.7b/kernels.py): int8 quantize-on-write,
 split-K GQA decode attention, causal chunked-prefill attention on bf16 MFMA, the prefill q/k
-RMSNorm + RoPE, and hipGraph capture of the decode step. The directory name is not a Python identifier, so import it with
+RMSNorm + RoPE, token sampling, and hipGraph capture of the decode step. The directory name is not a Python identifier, so import it with
 `importlib.import_module("inference-engine_amd")`.
 """
 
@@ -16,4 +16,5 @@ from .kernels import (  # noqa: F401
     make_layer_cache,
     prefill_attention,
     quantize_kv_prefill,
+    sample,
 )

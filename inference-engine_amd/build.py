@@ -20,7 +20,8 @@ LIB = PKG / "lib"
 BUILD = PKG / "_build"
 INCLUDE = REPO / "include"
 
-HIP_SOURCES = ["runtime.hip", "kv_write.hip", "decode_attention.hip", "prefill_attention.hip"]
+HIP_SOURCES = ["runtime.hip", "kv_write.hip", "decode_attention.hip", "prefill_attention.hip",
+               "sampling.hip"]
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [

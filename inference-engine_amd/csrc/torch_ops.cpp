@@ -173,6 +173,29 @@ std::tuple<at::Tensor, at::Tensor> fused_norm_rope_prefill(const at::Tensor& q,
     return {q_out, k_out};
 }
 
+at::Tensor sample(const at::Tensor& logits, double tau, const at::Tensor& seed) {
+    TORCH_CHECK(logits.is_cuda() && logits.dim() == 2 && logits.stride(1) == 1,
+                "ie: logits must be a [B, V] device tensor with unit vocab stride");
+    TORCH_CHECK(logits.scalar_type() == at::kBFloat16 || logits.scalar_type() == at::kFloat,
+                "ie: logits must be bf16 or fp32");
+    TORCH_CHECK(seed.is_cuda() && seed.scalar_type() == at::kLong && seed.numel() >= 1 &&
+                    seed.is_contiguous(),
+                "ie: seed must be an int64 device tensor");
+    const c10::DeviceGuard guard(logits.device());
+    const int64_t B = logits.size(0), V = logits.size(1);
+    at::Tensor out = at::empty({B, 1}, logits.options().dtype(at::kLong));
+    const size_t ws_bytes = ie_sample_workspace_size((int32_t)B, V);
+    at::Tensor ws = at::empty({(int64_t)std::max<size_t>(ws_bytes, 16)},
+                              logits.options().dtype(at::kByte));
+    ok(ie_sample(logits.data_ptr(),
+                 logits.scalar_type() == at::kBFloat16 ? IE_DTYPE_BF16 : IE_DTYPE_F32,
+                 logits.stride(0), (int32_t)B, V, (float)tau, seed.data_ptr<int64_t>(),
+                 out.data_ptr<int64_t>(), out.stride(0), ws.data_ptr(), ws_bytes,
+                 stream_of(logits)),
+       "sample");
+    return out;
+}
+
 struct DecodeCall {
     ie_kv_cache c;
     int32_t B, hq;
@@ -323,6 +346,7 @@ TORCH_LIBRARY(ie, m) {
     m.def(
         "fused_norm_rope_prefill(Tensor q, Tensor k, Tensor q_norm_weight, Tensor k_norm_weight, "
         "Tensor cos, Tensor sin, float eps) -> (Tensor, Tensor)");
+    m.def("sample(Tensor logits, float tau, Tensor(a!) seed) -> Tensor");
     m.def(
         "decode_attention(Tensor q, Tensor k_cache, Tensor v_cache, Tensor k_scale, "
         "Tensor v_scale, Tensor k_calibration, Tensor cached_lens, Tensor slot_ids, "
@@ -350,6 +374,7 @@ TORCH_LIBRARY_IMPL(ie, CUDA, m) {
     m.impl("quantize_kv_prefill", &quantize_kv_prefill);
     m.impl("fused_rope_kv_decode", &fused_rope_kv_decode);
     m.impl("fused_norm_rope_prefill", &fused_norm_rope_prefill);
+    m.impl("sample", &sample);
     m.impl("decode_attention", &decode_attention);
     m.impl("decode_attention_split", &decode_attention_split);
     m.impl("decode_attention_combine", &decode_attention_combine);

@@ -6,9 +6,10 @@ TransformerBlock.forward :299-330 and Qwen3Model.forward :403-446) and its graph
 replay (qwen3-1.7b/engine.py:376-470): per layer, residual add + RMSNorm, QKV projection,
 `fused_rope_kv_decode` (norm + RoPE + int8 KV write), `decode_attention`, output projection,
 residual add + RMSNorm, gate/up projection, SiLU * up, down projection; then the final norm, the
-tied-embedding LM head and greedy argmax. The attention ops are this package's HIP kernels; the
-projections, norms and argmax are plain PyTorch (hipBLASLt GEMMs), which the reference also
-leaves to its linear/add_rms_norm/silu_mul/sample kernels outside the attention path.
+tied-embedding LM head and greedy sampling (`sample` at tau 0, kernels.py:1343-1370). The
+attention ops and the sampler are this package's HIP kernels; the projections and norms are
+plain PyTorch (hipBLASLt GEMMs), which the reference leaves to its linear/add_rms_norm/silu_mul
+kernels outside the attention path.
 
 Weights are random (bf16, std 0.02) and the caches hold random int8 K/V: there is no checkpoint
 here, and the step's cost does not depend on the values.
@@ -19,7 +20,8 @@ from dataclasses import dataclass
 import torch
 import torch.nn.functional as F
 
-from .kernels import LayerKVCache, decode_attention, fused_rope_kv_decode, make_layer_cache
+from .kernels import (LayerKVCache, decode_attention, fused_rope_kv_decode, make_layer_cache,
+                      sample)
 
 
 @dataclass(frozen=True)
@@ -105,6 +107,7 @@ class DecodeStep:
         self.cached_lens = torch.zeros(batch, device=device, dtype=torch.int32)
         self.slot_ids = torch.arange(batch, device=device, dtype=torch.int32)
         self.num_decoding = torch.full((1,), batch, device=device, dtype=torch.int32)
+        self.seed = torch.zeros(1, device=device, dtype=torch.int64)  # the engine's sampling seed
         D = shape.head_dim
         self.inv_freq = shape.rope_base ** (
             -torch.arange(0, D, 2, dtype=torch.float32, device=device) / D)
@@ -147,7 +150,7 @@ class DecodeStep:
             x = F.linear(F.silu(gate) * up, lw.down)
         h = self._rms(residual + x, self.final_norm)
         logits = F.linear(h, self.embed)
-        return torch.argmax(logits, dim=-1, keepdim=True)
+        return sample(logits, 0.0, self.seed)
 
     def attention_only(self) -> torch.Tensor:
         """The step's attention kernels alone (per layer: fused_rope_kv_decode and

@@ -178,3 +178,11 @@ def prefill_attention(
     return ops().prefill_attention(q, k, v, seq_ids, cu_seqlens, tile_start,
                                    *_cache_args(kv_cache), slot_ids, cu_cached,
                                    int(PREFILL_BLOCK_M))
+
+
+def sample(logits: torch.Tensor, tau: float, seed: torch.Tensor) -> torch.Tensor:
+    """qwen3-1.7b/kernels.py:1343-1370: [B, 1] int64 tokens (Gumbel-max; greedy at tau = 0);
+    increments the int64 device `seed` by one."""
+    B, V = logits.shape
+    assert logits.stride(-1) == 1, "kernel assumes contiguous vocab dim"
+    return ops().sample(logits, float(tau), seed)

@@ -7,7 +7,9 @@ and only as the checker: the product package never imports, links or runs anythi
 
 Modules
   numerics   bf16 rounding, the fixed-order wave butterfly sum
-  kv_cache   quantize-on-write (prefill and decode), prefix dequantize, cache containers
+  kv_cache   quantize-on-write (prefill and decode), prefix dequantize, cache containers,
+             the prefill q/k RMSNorm + RoPE
+  sampling   Gumbel-max token sampling with Triton's Philox4x32-10 uniforms (greedy at tau 0)
   attention  decode attention (reference rounding points, split-K form, float64 textbook)
              and causal chunked-prefill attention
   work_split the split-K work partition of the decode kernel (integer restatement)
@@ -17,6 +19,11 @@ Pinning (what checks each function independently of this restatement; see tests/
                                 calibration floor), brute-force round-trip bound |x - q*s| <= s/2
   fused_rope_kv_decode          RMSNorm against torch.nn.RMSNorm in float64, RoPE against complex
                                 multiplication in float64, quantize pinned as above
+  fused_norm_rope_prefill       the same float64 forms, known answers (constant rows, zero and
+                                quarter-turn angles), equality with the decode rotation
+  sampling                      Philox4x32-10 against the Random123 known-answer vectors, the
+                                uniform map's closed forms, greedy = first argmax, tau > 0
+                                frequencies against softmax(logits / tau)
   dequantize_kv_prefix          closed form on hand-built int8 rows
   decode_attention              float64 torch scaled_dot_product_attention on the dequantized
                                 cache; split-K merge equal to the unsplit form
