@@ -59,16 +59,37 @@ int decode_target(int num_kv_heads) {
 }
 
 
-// Piece size for this step (kernels.py:20-37); wave-uniform, every lane returns it.
+// Piece size for this step; wave-uniform, every lane returns it. The reference's rule
+// (kernels.py:20-37) gives p0 = roundup(max(128, cdiv(total, target)), 128), but every sequence
+// rounds its own split count up, so its pieces can number up to target + nd and spill past the
+// one resident wave of workgroups that target sizes. When nd <= target the piece is instead the
+// smallest multiple of 128, at least p0, whose pieces number at most target: a binary search,
+// since the count falls as the piece grows and is nd at the longest sequence's length.
 __device__ int decode_piece(const int32_t* __restrict__ cached_lens, int nd, int target) {
     const int lane = threadIdx.x & 63;
-    int total = 0;
+    const int n0 = lane < nd ? cached_lens[lane] + 1 : 0;  // the first 64 sequences stay in registers
+    auto n_of = [&](int b0) { return b0 == 0 ? n0 : (b0 + lane < nd ? cached_lens[b0 + lane] + 1 : 0); };
+    int total = 0, longest = 0;
     for (int b0 = 0; b0 < nd; b0 += 64) {
-        const int b = b0 + lane;
-        total += wave_sum_i(b < nd ? cached_lens[b] + 1 : 0);
+        const int n = n_of(b0);
+        total += wave_sum_i(n);
+        longest = max(longest, (int)wave_max((float)n));
     }
-    int piece = max(DA_MIN_PIECE, cdiv_i(total, target));
-    return cdiv_i(piece, DA_MIN_PIECE) * DA_MIN_PIECE;
+    const int k0 = max(1, cdiv_i(cdiv_i(total, target), DA_MIN_PIECE));
+    if (nd > target) return k0 * DA_MIN_PIECE;
+    auto pieces = [&](int k) {
+        const Divisor p = divisor(k * DA_MIN_PIECE);
+        int c = 0;
+        for (int b0 = 0; b0 < nd; b0 += 64) c += wave_sum_i(div_ceil(n_of(b0), p));
+        return c;
+    };
+    int lo = k0, hi = max(k0, cdiv_i(longest, DA_MIN_PIECE));  // pieces(hi) <= nd <= target
+    while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (pieces(mid) <= target) hi = mid;
+        else lo = mid + 1;
+    }
+    return lo * DA_MIN_PIECE;
 }
 
 struct Work {

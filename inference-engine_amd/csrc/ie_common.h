@@ -81,11 +81,6 @@ __device__ __forceinline__ float sum_xor32(float x) {
 __host__ __device__ inline int cdiv_i(int a, int b) { return (a + b - 1) / b; }
 
 // Integer sum over the wave (every lane gets it) and inclusive prefix sum in lane order.
-__device__ __forceinline__ int wave_sum_i(int x) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m, IE_WAVE);
-    return x;
-}
 __device__ __forceinline__ int wave_incl_scan_i(int x) {
     const int lane = threadIdx.x & 63;
 #pragma unroll
@@ -111,6 +106,39 @@ __device__ __forceinline__ float max16(float x) {
     x = fmaxf(x, dpp<DPP_MIRROR>(x));
     return x;
 }
+// Integer sum over the wave, every lane gets it (VALU only: the lane swaps for 32 and 16, DPP
+// within rows of 16).
+__device__ __forceinline__ int wave_sum_i(int x) {
+    {
+        const auto r = __builtin_amdgcn_permlane32_swap((uint32_t)x, (uint32_t)x, false, false);
+        x = (int)(r[0] + r[1]);
+    }
+    {
+        const auto r = __builtin_amdgcn_permlane16_swap((uint32_t)x, (uint32_t)x, false, false);
+        x = (int)(r[0] + r[1]);
+    }
+    x += dppi<DPP_ROR8>(x);
+    x += dppi<DPP_HALF_MIRROR>(dppi<DPP_XOR3>(x));
+    x += dppi<DPP_XOR2>(x);
+    x += dppi<DPP_XOR1>(x);
+    return x;
+}
+
+// Division by a wave-uniform divisor d >= 1 of numerators 0 <= x < 2^22: the float estimate
+// x * (1/d) is within one of floor(x / d), and one compare each way makes it exact.
+struct Divisor {
+    int d;
+    float r;
+};
+__device__ __forceinline__ Divisor divisor(int d) { return Divisor{d, 1.0f / (float)d}; }
+__device__ __forceinline__ int div_floor(int x, const Divisor& D) {
+    int q = (int)((float)x * D.r);
+    q += (q + 1) * D.d <= x;
+    q -= q * D.d > x;
+    return q;
+}
+__device__ __forceinline__ int div_ceil(int x, const Divisor& D) { return div_floor(x + D.d - 1, D); }
+
 // Max over the 64 lanes of the wave (all on the VALU: DPP within rows of 16, then the gfx950
 // lane swaps across rows).
 __device__ __forceinline__ float wave_max(float x) { return max_xor32(max_xor16(max16(x))); }

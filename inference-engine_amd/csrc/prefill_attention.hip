@@ -119,20 +119,6 @@ struct SbInfo {
 
 constexpr int PF_UNSPLIT = 1 << 28;  // piece size that never splits a pair
 
-// Division by a wave-uniform divisor d >= 1 of numerators 0 <= x < 2^22: the float estimate
-// x * (1/d) is within one of floor(x / d), and one compare each way makes it exact.
-struct Divisor {
-    int d;
-    float r;
-};
-__device__ __forceinline__ Divisor divisor(int d) { return Divisor{d, 1.0f / (float)d}; }
-__device__ __forceinline__ int div_floor(int x, const Divisor& D) {
-    int q = (int)((float)x * D.r);
-    q += (q + 1) * D.d <= x;
-    q -= q * D.d > x;
-    return q;
-}
-__device__ __forceinline__ int div_ceil(int x, const Divisor& D) { return div_floor(x + D.d - 1, D); }
 
 // Pieces of a pair with npt prefix and nct chunk tiles at piece size T. A pair of at most T
 // tiles is one piece; a longer one is split into prefix pieces and chunk pieces separately (no

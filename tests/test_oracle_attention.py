@@ -143,3 +143,27 @@ def test_work_plan_covers_every_token_once(seed):
     for b in range(nd):
         assert seen.get(("n", b), 0) == int(lens[b]) + 1
     assert len(rows) == target + B
+    # the build's rule: at least the reference's piece, and the list fits target items whenever
+    # nd <= target, with the smallest such piece
+    p0 = ows.reference_piece(lens, nd, target, 64)
+    assert piece >= p0
+    items = sum(1 for r in rows if r[2] > 0)
+    if 0 < nd <= target:
+        assert items <= target
+        if piece > p0:
+            n_end = np.asarray(lens[:nd], np.int64) + 1
+            assert int(ows.cdiv(n_end, piece - 64).sum()) > target
+    else:
+        assert piece == p0
+
+
+def test_work_plan_fits_one_wave_at_config5():
+    # 32 sequences of U[128, 4096) tokens: the reference's piece gives 75 pieces per KV head
+    # for 64 resident workgroups; the build's piece fits them
+    rng = np.random.default_rng(0)
+    lens = rng.integers(128, 4096, 32) - 1
+    p0 = ows.reference_piece(lens, 32, 64, 128)
+    n_end = lens.astype(np.int64) + 1
+    assert int(ows.cdiv(n_end, p0).sum()) > 64
+    piece, rows = ows.decode_work_plan(lens, 32, 32, 64, 128)
+    assert piece > p0 and sum(1 for r in rows if r[2] > 0) <= 64
