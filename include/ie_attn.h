@@ -252,6 +252,33 @@ hipError_t ie_sample(const void* logits, int32_t logits_dtype, int64_t logits_st
                      int64_t out_stride_row, void* workspace, size_t workspace_bytes,
                      hipStream_t stream);
 
+/*
+ * Residual add + RMSNorm of token rows.
+ * Replaces qwen3-1.7b/kernels.py:1260-1283 `add_rms_norm(residual, delta, rms_norm, eps) ->
+ * (new_residual, new_normed_residual)` (kernel kernels.py:1216-1257).
+ *
+ * residual, delta, new_residual, normed: bf16 [num_tokens, dim] rows (any row strides, 16-byte
+ * aligned rows); weight: bf16 [dim]; dim a multiple of 8, at most 8192. new_residual =
+ * bf16(residual + delta); normed = bf16((r * rstd) * w) with r = new_residual and
+ * rstd = 1 / sqrt(sum(r^2) / dim + eps) (IEEE). Sum order: thread t of 256 adds the squares of
+ * elements 8t + 2048j + i in order, the wave's 64 sums combine by the xor butterfly (lane
+ * distance 32 ... 1), the four wave sums are added in order.
+ */
+hipError_t ie_add_rms_norm(const ie_bf16* residual, int64_t residual_stride, const ie_bf16* delta,
+                           int64_t delta_stride, const ie_bf16* weight, int64_t num_tokens,
+                           int32_t dim, float eps, ie_bf16* new_residual,
+                           int64_t new_residual_stride, ie_bf16* normed, int64_t normed_stride,
+                           hipStream_t stream);
+
+/*
+ * SiLU-gated product. Replaces qwen3-1.7b/kernels.py:1204-1213 `silu_mul(gate_up) -> out`
+ * (kernel kernels.py:1178-1201): gate_up bf16 [num_tokens, 2 * dim] (gate then up), out bf16
+ * [num_tokens, dim] = bf16((g * sigmoid(g)) * u), sigmoid(g) = 1 / (1 + exp(-g)) in fp32.
+ * dim a multiple of 8, rows 16-byte aligned.
+ */
+hipError_t ie_silu_mul(const ie_bf16* gate_up, int64_t gate_up_stride, int64_t num_tokens,
+                       int32_t dim, ie_bf16* out, int64_t out_stride, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

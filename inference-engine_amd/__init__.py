@@ -2,13 +2,15 @@
 
 Drop-in for the reference's attention kernel API (qwen3-1.7b/kernels.py): int8 quantize-on-write,
 split-K GQA decode attention, causal chunked-prefill attention on bf16 MFMA, the prefill q/k
-RMSNorm + RoPE, token sampling, and hipGraph capture of the decode step. The directory name is not a Python identifier, so import it with
+RMSNorm + RoPE, token sampling, the per-layer add_rms_norm / silu_mul, and hipGraph capture of
+the decode step. The directory name is not a Python identifier, so import it with
 `importlib.import_module("inference-engine_amd")`.
 """
 
 from . import kernels, step_inputs  # noqa: F401
 from .kernels import (  # noqa: F401
     LayerKVCache,
+    add_rms_norm,
     decode_attention,
     dequantize_kv_prefix,
     fused_norm_rope_prefill,
@@ -17,4 +19,5 @@ from .kernels import (  # noqa: F401
     prefill_attention,
     quantize_kv_prefill,
     sample,
+    silu_mul,
 )

@@ -196,6 +196,37 @@ at::Tensor sample(const at::Tensor& logits, double tau, const at::Tensor& seed) 
     return out;
 }
 
+std::tuple<at::Tensor, at::Tensor> add_rms_norm(const at::Tensor& residual,
+                                                const at::Tensor& delta,
+                                                const at::Tensor& weight, double eps) {
+    check_bf16_rows(residual, "residual", 2);
+    check_bf16_rows(delta, "delta", 2);
+    check_bf16_rows(weight, "weight", 1);
+    const c10::DeviceGuard guard(residual.device());
+    const int64_t N = residual.size(0), D = residual.size(1);
+    TORCH_CHECK(delta.size(0) == N && delta.size(1) == D && weight.size(0) == D,
+                "ie: residual/delta [N, D], weight [D]");
+    at::Tensor nres = at::empty({N, D}, residual.options());
+    at::Tensor normed = at::empty({N, D}, residual.options());
+    ok(ie_add_rms_norm(bf(residual), residual.stride(0), bf(delta), delta.stride(0), bf(weight), N,
+                       (int32_t)D, (float)eps, bfm(nres), nres.stride(0), bfm(normed),
+                       normed.stride(0), stream_of(residual)),
+       "add_rms_norm");
+    return {nres, normed};
+}
+
+at::Tensor silu_mul(const at::Tensor& gate_up) {
+    check_bf16_rows(gate_up, "gate_up", 2);
+    const c10::DeviceGuard guard(gate_up.device());
+    const int64_t N = gate_up.size(0), D = gate_up.size(1) / 2;
+    TORCH_CHECK(gate_up.size(1) % 2 == 0, "ie: gate_up must be [N, 2D]");
+    at::Tensor out = at::empty({N, D}, gate_up.options());
+    ok(ie_silu_mul(bf(gate_up), gate_up.stride(0), N, (int32_t)D, bfm(out), out.stride(0),
+                   stream_of(gate_up)),
+       "silu_mul");
+    return out;
+}
+
 struct DecodeCall {
     ie_kv_cache c;
     int32_t B, hq;
@@ -347,6 +378,8 @@ TORCH_LIBRARY(ie, m) {
         "fused_norm_rope_prefill(Tensor q, Tensor k, Tensor q_norm_weight, Tensor k_norm_weight, "
         "Tensor cos, Tensor sin, float eps) -> (Tensor, Tensor)");
     m.def("sample(Tensor logits, float tau, Tensor(a!) seed) -> Tensor");
+    m.def("add_rms_norm(Tensor residual, Tensor delta, Tensor weight, float eps) -> (Tensor, Tensor)");
+    m.def("silu_mul(Tensor gate_up) -> Tensor");
     m.def(
         "decode_attention(Tensor q, Tensor k_cache, Tensor v_cache, Tensor k_scale, "
         "Tensor v_scale, Tensor k_calibration, Tensor cached_lens, Tensor slot_ids, "
@@ -375,6 +408,8 @@ TORCH_LIBRARY_IMPL(ie, CUDA, m) {
     m.impl("fused_rope_kv_decode", &fused_rope_kv_decode);
     m.impl("fused_norm_rope_prefill", &fused_norm_rope_prefill);
     m.impl("sample", &sample);
+    m.impl("add_rms_norm", &add_rms_norm);
+    m.impl("silu_mul", &silu_mul);
     m.impl("decode_attention", &decode_attention);
     m.impl("decode_attention_split", &decode_attention_split);
     m.impl("decode_attention_combine", &decode_attention_combine);

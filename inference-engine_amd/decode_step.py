@@ -2,14 +2,14 @@
 as a hipGraph: the harness for the whole-step measurement (tokens/s and the attention share).
 
 Mirrors the decode branch of the reference's model (qwen3-1.7b/architecture.py:98-122 inside
-TransformerBlock.forward :299-330 and Qwen3Model.forward :403-446) and its graph capture and
-replay (qwen3-1.7b/engine.py:376-470): per layer, residual add + RMSNorm, QKV projection,
-`fused_rope_kv_decode` (norm + RoPE + int8 KV write), `decode_attention`, output projection,
-residual add + RMSNorm, gate/up projection, SiLU * up, down projection; then the final norm, the
-tied-embedding LM head and greedy sampling (`sample` at tau 0, kernels.py:1343-1370). The
-attention ops and the sampler are this package's HIP kernels; the projections and norms are
-plain PyTorch (hipBLASLt GEMMs), which the reference leaves to its linear/add_rms_norm/silu_mul
-kernels outside the attention path.
+TransformerBlock.forward :262-304 and Qwen3Model.forward :395-413) and its graph capture and
+replay (qwen3-1.7b/engine.py:376-470): per layer, `add_rms_norm` (the first layer: RMSNorm),
+QKV projection, `fused_rope_kv_decode` (norm + RoPE + int8 KV write), `decode_attention`,
+output projection, `add_rms_norm`, gate/up projection, `silu_mul`, down projection; then the
+final `add_rms_norm`, the tied-embedding LM head and greedy sampling (`sample` at tau 0,
+kernels.py:1343-1370). All of these but the projections are this package's HIP kernels; the
+projections are PyTorch linear layers (hipBLASLt GEMMs), as the reference leaves them to its
+`linear` (kernels.py:1373-1485).
 
 Weights are random (bf16, std 0.02) and the caches hold random int8 K/V: there is no checkpoint
 here, and the step's cost does not depend on the values.
@@ -20,8 +20,8 @@ from dataclasses import dataclass
 import torch
 import torch.nn.functional as F
 
-from .kernels import (LayerKVCache, decode_attention, fused_rope_kv_decode, make_layer_cache,
-                      sample)
+from .kernels import (LayerKVCache, add_rms_norm, decode_attention, fused_rope_kv_decode,
+                      make_layer_cache, sample, silu_mul)
 
 
 @dataclass(frozen=True)
@@ -142,13 +142,16 @@ class DecodeStep:
         cos, sin = self._rope()
         x = F.embedding(self.ids, self.embed)
         residual = None
+        eps = self.shape.eps
         for li, lw in enumerate(self.layers):
-            residual = x if residual is None else residual + x
-            attn = self.attention(li, self._rms(residual, lw.input_norm), cos, sin)
-            residual = residual + attn
-            gate, up = F.linear(self._rms(residual, lw.post_norm), lw.gate_up).chunk(2, dim=-1)
-            x = F.linear(F.silu(gate) * up, lw.down)
-        h = self._rms(residual + x, self.final_norm)
+            if residual is None:  # architecture.py:280-281: the first block norms its input
+                residual, normed = x, self._rms(x, lw.input_norm)
+            else:
+                residual, normed = add_rms_norm(residual, x, lw.input_norm, eps)
+            attn = self.attention(li, normed, cos, sin)
+            residual, normed = add_rms_norm(residual, attn, lw.post_norm, eps)
+            x = F.linear(silu_mul(F.linear(normed, lw.gate_up)), lw.down)
+        _, h = add_rms_norm(residual, x, self.final_norm, eps)
         logits = F.linear(h, self.embed)
         return sample(logits, 0.0, self.seed)
 

@@ -186,3 +186,15 @@ def sample(logits: torch.Tensor, tau: float, seed: torch.Tensor) -> torch.Tensor
     B, V = logits.shape
     assert logits.stride(-1) == 1, "kernel assumes contiguous vocab dim"
     return ops().sample(logits, float(tau), seed)
+
+
+def add_rms_norm(residual: torch.Tensor, delta: torch.Tensor, rms_norm: torch.Tensor, eps: float):
+    """qwen3-1.7b/kernels.py:1260-1283: (bf16(residual + delta), its RMSNorm x weight)."""
+    N, D = residual.shape
+    assert residual.stride(-1) == 1 and delta.stride(-1) == 1
+    return ops().add_rms_norm(residual, delta, rms_norm, float(eps))
+
+
+def silu_mul(gate_up: torch.Tensor) -> torch.Tensor:
+    """qwen3-1.7b/kernels.py:1204-1213: [N, 2D] -> [N, D], silu(gate) * up."""
+    return ops().silu_mul(gate_up)
