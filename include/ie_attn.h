@@ -279,6 +279,20 @@ hipError_t ie_add_rms_norm(const ie_bf16* residual, int64_t residual_stride, con
 hipError_t ie_silu_mul(const ie_bf16* gate_up, int64_t gate_up_stride, int64_t num_tokens,
                        int32_t dim, ie_bf16* out, int64_t out_stride, hipStream_t stream);
 
+/*
+ * y = x . weight^T for few rows (decode). Replaces qwen3-1.7b/kernels.py:1406-1443
+ * `skinny_matmul(x, weight) -> y` (kernel kernels.py:1373-1403), which `linear`
+ * (kernels.py:1451-1458) picks per (N, K, M) over the library GEMM after `tune_linear` timed both.
+ * x: bf16 [m, k] (m <= 64), weight: bf16 [n, k] (nn.Linear layout), y: bf16 [m, n]; fp32
+ * accumulation, y rounded to nearest even. n_tiles (1, 2 or 4): weight rows per workgroup / 16,
+ * the shape-dependent launch choice (more rows per workgroup re-read x less often, fewer
+ * workgroups fill fewer CUs). n a multiple of 16 n_tiles, k of 256; rows 16-byte aligned (y
+ * 8-byte).
+ */
+hipError_t ie_skinny_gemm(const ie_bf16* x, int64_t x_stride, int32_t m, const ie_bf16* weight,
+                          int64_t weight_stride, int32_t n, int32_t k, int32_t n_tiles, ie_bf16* y,
+                          int64_t y_stride, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

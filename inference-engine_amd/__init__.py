@@ -20,4 +20,7 @@ from .kernels import (  # noqa: F401
     quantize_kv_prefill,
     sample,
     silu_mul,
+    skinny_matmul,
+    linear,
+    tune_linear,
 )

@@ -21,7 +21,7 @@ BUILD = PKG / "_build"
 INCLUDE = REPO / "include"
 
 HIP_SOURCES = ["runtime.hip", "kv_write.hip", "decode_attention.hip", "prefill_attention.hip",
-               "sampling.hip", "norm_act.hip"]
+               "sampling.hip", "norm_act.hip", "skinny_gemm.hip"]
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [

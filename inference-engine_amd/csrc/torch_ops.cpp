@@ -227,6 +227,19 @@ at::Tensor silu_mul(const at::Tensor& gate_up) {
     return out;
 }
 
+at::Tensor skinny_matmul(const at::Tensor& x, const at::Tensor& weight, int64_t n_tiles) {
+    check_bf16_rows(x, "x", 2);
+    check_bf16_rows(weight, "weight", 2);
+    const c10::DeviceGuard guard(x.device());
+    const int64_t M = x.size(0), K = x.size(1), N = weight.size(0);
+    TORCH_CHECK(weight.size(1) == K, "ie: weight must be [N, K]");
+    at::Tensor y = at::empty({M, N}, x.options());
+    ok(ie_skinny_gemm(bf(x), x.stride(0), (int32_t)M, bf(weight), weight.stride(0), (int32_t)N,
+                      (int32_t)K, (int32_t)n_tiles, bfm(y), y.stride(0), stream_of(x)),
+       "skinny_matmul");
+    return y;
+}
+
 struct DecodeCall {
     ie_kv_cache c;
     int32_t B, hq;
@@ -380,6 +393,7 @@ TORCH_LIBRARY(ie, m) {
     m.def("sample(Tensor logits, float tau, Tensor(a!) seed) -> Tensor");
     m.def("add_rms_norm(Tensor residual, Tensor delta, Tensor weight, float eps) -> (Tensor, Tensor)");
     m.def("silu_mul(Tensor gate_up) -> Tensor");
+    m.def("skinny_matmul(Tensor x, Tensor weight, int n_tiles=1) -> Tensor");
     m.def(
         "decode_attention(Tensor q, Tensor k_cache, Tensor v_cache, Tensor k_scale, "
         "Tensor v_scale, Tensor k_calibration, Tensor cached_lens, Tensor slot_ids, "
@@ -410,6 +424,7 @@ TORCH_LIBRARY_IMPL(ie, CUDA, m) {
     m.impl("sample", &sample);
     m.impl("add_rms_norm", &add_rms_norm);
     m.impl("silu_mul", &silu_mul);
+    m.impl("skinny_matmul", &skinny_matmul);
     m.impl("decode_attention", &decode_attention);
     m.impl("decode_attention_split", &decode_attention_split);
     m.impl("decode_attention_combine", &decode_attention_combine);

@@ -7,9 +7,10 @@ replay (qwen3-1.7b/engine.py:376-470): per layer, `add_rms_norm` (the first laye
 QKV projection, `fused_rope_kv_decode` (norm + RoPE + int8 KV write), `decode_attention`,
 output projection, `add_rms_norm`, gate/up projection, `silu_mul`, down projection; then the
 final `add_rms_norm`, the tied-embedding LM head and greedy sampling (`sample` at tau 0,
-kernels.py:1343-1370). All of these but the projections are this package's HIP kernels; the
-projections are PyTorch linear layers (hipBLASLt GEMMs), as the reference leaves them to its
-`linear` (kernels.py:1373-1485).
+kernels.py:1343-1370). All of these are this package's HIP kernels except the projections where
+`linear` (kernels.py:1451-1458) picks the library GEMM (hipBLASLt): `tune_linear` times this
+package's skinny GEMM against it for every weight shape at the step's row count before
+capture, as the reference's engine does (engine.py:352-374).
 
 Weights are random (bf16, std 0.02) and the caches hold random int8 K/V: there is no checkpoint
 here, and the step's cost does not depend on the values.
@@ -20,8 +21,8 @@ from dataclasses import dataclass
 import torch
 import torch.nn.functional as F
 
-from .kernels import (LayerKVCache, add_rms_norm, decode_attention, fused_rope_kv_decode,
-                      make_layer_cache, sample, silu_mul)
+from .kernels import (LayerKVCache, add_rms_norm, decode_attention, fused_rope_kv_decode, linear,
+                      make_layer_cache, sample, silu_mul, tune_linear)
 
 
 @dataclass(frozen=True)
@@ -125,7 +126,7 @@ class DecodeStep:
     def attention(self, li, normed, cos, sin):
         """AttentionLayer.forward, pure-decode branch (architecture.py:85-122)."""
         s, lw, B = self.shape, self.layers[li], self.B
-        qkv = F.linear(normed, lw.qkv)
+        qkv = linear(normed, lw.qkv)
         q, k, v = qkv.split([s.num_q_heads * s.head_dim, s.num_kv_heads * s.head_dim,
                              s.num_kv_heads * s.head_dim], dim=-1)
         q = q.view(B, s.num_q_heads, s.head_dim)
@@ -135,7 +136,7 @@ class DecodeStep:
                                  self.caches[li], self.cached_lens, self.num_decoding, s.eps)
         out = decode_attention(q, self.caches[li], self.cached_lens, self.slot_ids,
                                self.num_decoding, s.head_dim ** -0.5)
-        return F.linear(out.view(B, -1), lw.o_proj)
+        return linear(out.view(B, -1), lw.o_proj)
 
     def forward(self) -> torch.Tensor:
         """One step: returns the greedy next token of every sequence, int64 [B, 1]."""
@@ -150,9 +151,9 @@ class DecodeStep:
                 residual, normed = add_rms_norm(residual, x, lw.input_norm, eps)
             attn = self.attention(li, normed, cos, sin)
             residual, normed = add_rms_norm(residual, attn, lw.post_norm, eps)
-            x = F.linear(silu_mul(F.linear(normed, lw.gate_up)), lw.down)
+            x = linear(silu_mul(linear(normed, lw.gate_up)), lw.down)
         _, h = add_rms_norm(residual, x, self.final_norm, eps)
-        logits = F.linear(h, self.embed)
+        logits = linear(h, self.embed)
         return sample(logits, 0.0, self.seed)
 
     def attention_only(self) -> torch.Tensor:
@@ -195,7 +196,7 @@ class DecodeStep:
 
 
 def make_decode_step(batch=32, ctx_lo=128, ctx_hi=4096, shape=Qwen3Shape(), device="cuda",
-                     seed=0):
+                     seed=0, tune=True):
     """Config-5 step: B sequences with cached lengths ~ U[ctx_lo, ctx_hi) - 1 (the new token is
     the ctx-th), slots 0..B-1 of a pool of B + 1 (the last row is the engine's scratch slot)."""
     layers, embed, final_norm = random_weights(shape, device, seed)
@@ -205,6 +206,9 @@ def make_decode_step(batch=32, ctx_lo=128, ctx_hi=4096, shape=Qwen3Shape(), devi
     ctx = torch.randint(ctx_lo, ctx_hi, (batch,), generator=g)
     step.cached_lens.copy_((ctx - 1).to(torch.int32))
     step.ids.copy_(torch.randint(0, shape.vocab, (batch,), generator=g))
+    if tune:  # one weight of every shape (the table is keyed by shape)
+        lw = layers[0]
+        tune_linear([lw.qkv, lw.o_proj, lw.gate_up, lw.down, embed], [batch])
     return step
 
 

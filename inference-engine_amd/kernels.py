@@ -198,3 +198,84 @@ def add_rms_norm(residual: torch.Tensor, delta: torch.Tensor, rms_norm: torch.Te
 def silu_mul(gate_up: torch.Tensor) -> torch.Tensor:
     """qwen3-1.7b/kernels.py:1204-1213: [N, 2D] -> [N, D], silu(gate) * up."""
     return ops().silu_mul(gate_up)
+
+
+def skinny_matmul(x: torch.Tensor, weight: torch.Tensor, n_tiles: int = 1) -> torch.Tensor:
+    """qwen3-1.7b/kernels.py:1406-1443: [M, K] bf16 @ [N, K].T bf16 -> [M, N] bf16 for M <= 64.
+    `n_tiles` (1, 2, 4): weight rows per workgroup / 16, the launch shape tune_linear picks."""
+    M, K = x.shape
+    N = weight.shape[0]
+    assert x.stride(-1) == 1 and weight.stride(-1) == 1
+    assert M <= 64, "big M is compute bound, the library GEMM is faster there"
+    assert N % (16 * n_tiles) == 0 and K % 256 == 0
+    return ops().skinny_matmul(x, weight, int(n_tiles))
+
+
+# (N, K, M) -> the n_tiles of skinny_matmul when it beat the library GEMM for that weight shape
+# and row count, else 0 (qwen3-1.7b/kernels.py:1446-1448). Filled by tune_linear before graph
+# capture; anything it never measured uses the library.
+use_skinny: dict = {}
+
+
+def linear(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """qwen3-1.7b/kernels.py:1451-1458: [M, K] @ [N, K].T -> [M, N], with whichever measured
+    faster."""
+    nt = use_skinny.get((weight.shape[0], weight.shape[1], x.shape[0]), 0)
+    if nt:
+        return skinny_matmul(x, weight, nt)
+    return torch.nn.functional.linear(x, weight)
+
+
+def tune_linear(weights: list, rows: list, calls: int = 20) -> None:
+    """qwen3-1.7b/kernels.py:1461-1485: times skinny_matmul (each n_tiles) against the library
+    GEMM for every weight shape at every row count and records the faster; the skinny kernel
+    needs a 2 % win. Each candidate runs `calls` back-to-back launches captured in one hipGraph
+    (the way the engine replays a step), cycling through copies of the weight that together
+    exceed the 256 MB last-level cache, so the weights come from HBM as every layer's do in a
+    step (the reference clears the cache before each timing for the same reason)."""
+    for weight in weights:
+        N, K = weight.shape
+        todo = [M for M in rows if M <= 64 and (N, K, M) not in use_skinny]
+        if not todo:
+            continue
+        nbytes = weight.numel() * weight.element_size()
+        copies = [weight] + [weight.clone() for _ in range(max(0, -(-(512 << 20) // nbytes) - 1))]
+        for M in todo:
+            x = torch.randn(M, K, device=weight.device, dtype=weight.dtype)
+            cycle = lambda f: [lambda w=w: f(w) for w in copies] * max(1, calls // len(copies))
+            lib = _graph_time(cycle(lambda w: torch.nn.functional.linear(x, w)))
+            best, choice = 0.98 * lib, 0
+            if K % 256 == 0:
+                for nt in (1, 2, 4):
+                    if N % (16 * nt):
+                        continue
+                    t = _graph_time(cycle(lambda w, nt=nt: skinny_matmul(x, w, nt)))
+                    if t < best:
+                        best, choice = t, nt
+            use_skinny[(N, K, M)] = choice
+        del copies
+
+
+def _graph_time(fns: list) -> float:
+    """Average time per call of the calls `fns`, captured in order in one hipGraph."""
+    for f in fns[:2]:
+        f()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fns[0]()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for f in fns:
+            f()
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(3):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / (3 * len(fns))

@@ -45,13 +45,13 @@ def test_decode_step_attention_matches_parts(ie, dev):
     x = torch.randn(4, shape.model_dim, device=dev).bfloat16()
     got = step.attention(0, x, cos, sin)  # the second call below rewrites the same cache column
     lw = step.layers[0]
-    qkv = torch.nn.functional.linear(x, lw.qkv)
+    qkv = ie.kernels.linear(x, lw.qkv)  # the step's projection (tuned: skinny or library)
     q, k, v = qkv.split([2048, 1024, 1024], dim=-1)
     qo = ie.fused_rope_kv_decode(q.view(4, 16, 128), k.view(4, 8, 128), v.view(4, 8, 128),
                                  lw.q_norm, lw.k_norm, cos, sin, step.slot_ids, step.caches[0],
                                  step.cached_lens, step.num_decoding, 1e-6)
     o = ie.decode_attention(qo, step.caches[0], step.cached_lens, step.slot_ids,
                             step.num_decoding, 128 ** -0.5)
-    want = torch.nn.functional.linear(o.view(4, -1), lw.o_proj)
+    want = ie.kernels.linear(o.view(4, -1), lw.o_proj)
     torch.cuda.synchronize()
     assert torch.equal(got, want)

@@ -1,0 +1,61 @@
+"""skinny_matmul / linear / tune_linear (qwen3-1.7b/kernels.py:1373-1485) on the GPU: y = x W^T
+for decode row counts against a float32 matmul (each output within one bf16 rounding of the
+fp32 value, up to fp32 summation-order noise), for every n_tiles launch shape, Qwen3-1.7B's
+projection shapes and ragged row counts; linear follows the table tune_linear fills."""
+
+import pytest
+import torch
+
+from helpers import say
+
+SHAPES = [(4096, 2048), (2048, 2048), (12288, 2048), (2048, 6144), (512, 256)]
+
+
+def _check(y, x, w, what):
+    ref = x.float() @ w.float().T
+    # one bf16 rounding of the exact value: |y - ref| <= 2^-8 |ref| (+ fp32 summation noise)
+    err = (y.float() - ref).abs()
+    bound = ref.abs() * 2 ** -8 + 1e-3 * ref.abs().max()
+    assert torch.all(err <= bound), f"{what}: max err {err.max().item():.3e}"
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("N,K", SHAPES)
+@pytest.mark.parametrize("M", [1, 8, 17, 32, 64])
+def test_skinny_matmul(ie, dev, N, K, M):
+    g = torch.Generator().manual_seed(N + K + M)
+    w = (0.02 * torch.randn(N, K, generator=g)).bfloat16().to(dev)
+    x = torch.randn(M, K, generator=g).bfloat16().to(dev)
+    for nt in (1, 2, 4):
+        if N % (16 * nt):
+            continue
+        y = ie.skinny_matmul(x, w, nt)
+        torch.cuda.synchronize()
+        assert y.shape == (M, N) and y.dtype == torch.bfloat16
+        _check(y, x, w, f"N={N} K={K} M={M} n_tiles={nt}")
+    say(f"skinny_matmul N={N} K={K} M={M}: ok")
+
+
+@pytest.mark.gpu
+def test_strided_x_rows(ie, dev):
+    g = torch.Generator().manual_seed(1)
+    w = (0.02 * torch.randn(2048, 2048, generator=g)).bfloat16().to(dev)
+    wide = torch.randn(16, 4096, generator=g).bfloat16().to(dev)
+    x = wide[:, 1024:3072]  # row stride 4096
+    _check(ie.skinny_matmul(x, w), x, w, "strided x")
+
+
+@pytest.mark.gpu
+def test_linear_follows_tuning_table(ie, dev):
+    g = torch.Generator().manual_seed(2)
+    w = (0.02 * torch.randn(4096, 2048, generator=g)).bfloat16().to(dev)
+    K = ie.kernels
+    K.use_skinny.clear()
+    K.tune_linear([w], [8, 32, 100])
+    assert (4096, 2048, 100) not in K.use_skinny  # > 64 rows: always the library
+    assert K.use_skinny[(4096, 2048, 8)] in (0, 1, 2, 4)
+    say(f"tuned: {K.use_skinny}")
+    for M in (8, 32, 100):
+        x = torch.randn(M, 2048, generator=g).bfloat16().to(dev)
+        _check(K.linear(x, w), x, w, f"linear M={M}")
+    K.use_skinny.clear()
