@@ -6,8 +6,9 @@ D=128 — µs per layer and achieved HBM GB/s against the 8 TB/s peak. One step 
 HBM. Distinct cache sets are rotated between steps so the 256 MB MALL cannot serve a repeat.
 
 Also reported beside it (extra keys): config-4 KV quantize-on-write, chunked-prefill attention
-and the prefill q/k RMSNorm + RoPE of its 1,024 packed tokens, token sampling at config 5's shape,
-each timed with HIP events on the stream the kernels run on, and config 5: a whole
+and the prefill q/k RMSNorm + RoPE of its 1,024 packed tokens, token sampling and the projection
+GEMMs at config 5's shape, each timed with HIP events on the stream the kernels run on, and
+config 5: a whole
 greedy decode step of a Qwen3-1.7B-shaped model (28 layers, random weights, B=32, ctx ~
 U[128, 4096)) replayed as a hipGraph, with the share of the step spent in the attention kernels
 (the same kernels captured alone).
@@ -159,6 +160,61 @@ def bench_sample(K, B, V, steps, warmup, dev):
         res[f"tau{tau:g}"] = {"us": round(ms * 1e3, 3), "us_graph": round(gms * 1e3, 3),
                               "GBps_graph": round(nbytes / (gms * 1e-3) / 1e9, 1)}
     return res
+
+
+def bench_linear(K, M, dev):
+    """skinny_matmul (best n_tiles) and the library GEMM on Qwen3-1.7B's projection shapes at M
+    rows, each timed over weight copies that together exceed the 256 MB last-level cache (the
+    weights come from HBM, as every layer's do in a step). Algorithmic bytes: the weight."""
+    import math
+    shapes = {"qkv": (4096, 2048), "o_proj": (2048, 2048), "gate_up": (12288, 2048),
+              "down": (2048, 6144), "lm_head": (151_936, 2048)}
+    res = {"rows": M}
+    g = torch.Generator().manual_seed(0)
+    for name, (N, Kd) in shapes.items():
+        nbytes = N * Kd * 2
+        ws = [(0.02 * torch.randn(N, Kd, generator=g)).bfloat16().to(dev)
+              for _ in range(max(1, math.ceil((512 << 20) / nbytes)))]
+        x = torch.randn(M, Kd, generator=g).bfloat16().to(dev)
+        calls = lambda f: [lambda w=w: f(w) for w in ws] * max(1, 16 // len(ws))
+        lib_ms = time_graph_calls(calls(lambda w: torch.nn.functional.linear(x, w)))
+        best = None
+        for nt in (1, 2, 4):
+            if N % (16 * nt) == 0:
+                t = time_graph_calls(calls(lambda w, nt=nt: K.skinny_matmul(x, w, nt)))
+                best = (t, nt) if best is None or t < best[0] else best
+        res[name] = {"bytes": nbytes, "skinny_us": round(best[0] * 1e3, 2), "n_tiles": best[1],
+                     "skinny_GBps": round(nbytes / (best[0] * 1e-3) / 1e9, 1),
+                     "library_us": round(lib_ms * 1e3, 2),
+                     "library_GBps": round(nbytes / (lib_ms * 1e-3) / 1e9, 1)}
+        del ws
+    return res
+
+
+def time_graph_calls(fns, reps=3):
+    """Average time per call of the calls `fns` captured in order in one hipGraph."""
+    for f in fns[:2]:
+        f()
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fns[0]()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for f in fns:
+            f()
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = _events(2)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / (reps * len(fns))
 
 
 def cpu_baseline(wl_gpu, min_seconds):
@@ -345,6 +401,13 @@ def main():
         log(f"sample config5 {extra['sample_config5']}")
     except Exception as e:  # reported, never silently replaced
         extra["sample_config5"] = {"error": str(e).splitlines()[0][:200]}
+
+    # ---- config 5's projections: 32 rows ----
+    try:
+        extra["linear_config5"] = bench_linear(K, 32, dev)
+        log(f"linear config5 {extra['linear_config5']}")
+    except Exception as e:  # reported, never silently replaced
+        extra["linear_config5"] = {"error": str(e).splitlines()[0][:200]}
 
     if not args.no_step:
         log("config 5: Qwen3-1.7B-shaped decode step (hipGraph)")
