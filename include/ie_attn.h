@@ -117,7 +117,8 @@ hipError_t ie_fused_rope_kv_decode(const ie_bf16* q, int64_t q_stride_b, int64_t
 
 /*
  * Bytes of device workspace ie_decode_attention needs for `batch` sequences on the current
- * device (fp32 split-K partials [batch, num_q_heads, max_splits, head_dim + 2]).
+ * device: a 256-byte plan record (the split launch writes the step's piece size there for the
+ * combine launch), then fp32 split-K partials [batch, num_q_heads, max_splits, head_dim + 2].
  */
 size_t ie_decode_attention_workspace_size(int32_t batch, int32_t num_q_heads, int32_t head_dim);
 

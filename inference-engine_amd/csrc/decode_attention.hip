@@ -139,6 +139,7 @@ struct DecodeArgs {
     float* part_acc;  // [B, Hq, max_splits, 128]
     float* part_m;    // [B, Hq, max_splits]
     float* part_l;    // [B, Hq, max_splits]
+    int* plan;        // [0]: this step's piece size, for the combine kernel
     int target, max_splits, hq;
 };
 
@@ -257,6 +258,7 @@ __attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_split_k
     const int nd = a.num_decoding[0];
     const int hk = blockIdx.y;
     Work wk = decode_assign(a.cached_lens, nd, blockIdx.x, a.target);
+    if (blockIdx.x == 0 && hk == 0 && threadIdx.x == 0) a.plan[0] = wk.piece;
     // Wave-uniform by construction; readfirstlane lets the compiler keep them (and the buffer
     // descriptors built from them) in SGPRs.
     wk.needed = uniform(wk.needed);
@@ -419,17 +421,19 @@ __attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_split_k
 }
 
 // grid (B, Hq), block 128: merge the pieces of sequences that had more than one
-// (kernels.py:216-264), in base 2.
+// (kernels.py:216-264), in base 2. The piece size is the one the split kernel recorded in the
+// workspace (one load, together with the sequence's length, instead of a pass over all
+// lengths); a value the split kernel did not write (no split launch before this one) is
+// rejected or clamped, so the reads stay inside the workspace.
 __global__ __launch_bounds__(128) void decode_combine_kernel(
     const float* __restrict__ part_acc, const float* __restrict__ part_m,
-    const float* __restrict__ part_l, const int32_t* __restrict__ cached_lens,
-    const int32_t* __restrict__ num_decoding, uint16_t* __restrict__ out, int64_t o_sb,
-    int64_t o_sh, int hq, int max_splits, int target) {
-    const int nd = num_decoding[0];
+    const float* __restrict__ part_l, const int* __restrict__ plan,
+    const int32_t* __restrict__ cached_lens, const int32_t* __restrict__ num_decoding,
+    uint16_t* __restrict__ out, int64_t o_sb, int64_t o_sh, int hq, int max_splits) {
     const int b = blockIdx.x, h = blockIdx.y;
-    if (b >= nd) return;
-    const int piece = decode_piece(cached_lens, nd, target);
-    const int needed = cdiv_i(cached_lens[b] + 1, piece);
+    const int nd = num_decoding[0], piece = plan[0], len = cached_lens[b];
+    if (b >= nd || piece < DA_MIN_PIECE) return;
+    const int needed = min(cdiv_i(len + 1, piece), max_splits);
     if (needed <= 1) return;
     const int d = threadIdx.x;
     const int64_t row0 = ((int64_t)b * hq + h) * max_splits;
@@ -447,7 +451,7 @@ __global__ __launch_bounds__(128) void decode_combine_kernel(
 
 struct Layout {
     int target, max_splits;
-    size_t acc_off, m_off, l_off, bytes;
+    size_t plan_off, acc_off, m_off, l_off, bytes;
 };
 
 static Layout workspace_layout(int batch, int hq, int hkv) {
@@ -455,8 +459,9 @@ static Layout workspace_layout(int batch, int hq, int hkv) {
     L.target = decode_target(hkv);
     L.max_splits = L.target;
     const size_t rows = (size_t)std::max(batch, 0) * hq * L.max_splits;
-    L.acc_off = 0;
-    L.m_off = rows * DA_D * sizeof(float);
+    L.plan_off = 0;
+    L.acc_off = 256;  // the plan record, padded
+    L.m_off = L.acc_off + rows * DA_D * sizeof(float);
     L.l_off = L.m_off + rows * sizeof(float);
     L.bytes = L.l_off + rows * sizeof(float);
     return L;
@@ -521,6 +526,7 @@ extern "C" hipError_t ie_decode_attention_split(
     a.part_acc = (float*)(ws + L.acc_off);
     a.part_m = (float*)(ws + L.m_off);
     a.part_l = (float*)(ws + L.l_off);
+    a.plan = (int*)(ws + L.plan_off);
     a.target = L.target;
     a.max_splits = L.max_splits;
     a.hq = num_q_heads;
@@ -546,8 +552,9 @@ extern "C" hipError_t ie_decode_attention_combine(int32_t batch, int32_t num_q_h
     dim3 grid(batch, num_q_heads);
     hipLaunchKernelGGL(decode_combine_kernel, grid, dim3(DA_D), 0, stream,
                        (const float*)(ws + L.acc_off), (const float*)(ws + L.m_off),
-                       (const float*)(ws + L.l_off), cached_lens, num_decoding, (uint16_t*)out,
-                       out_stride_b, out_stride_h, num_q_heads, L.max_splits, L.target);
+                       (const float*)(ws + L.l_off), (const int*)(ws + L.plan_off), cached_lens,
+                       num_decoding, (uint16_t*)out, out_stride_b, out_stride_h, num_q_heads,
+                       L.max_splits);
     return hipGetLastError();
 }
 

@@ -57,13 +57,15 @@ constexpr int PF_MIN_PIECE_TILES = IE_PREFILL_MIN_PIECE_TILES;  // tiles per pie
 constexpr float RESCALE_SLACK = 8.0f;  // log2 units
 
 // LDS layouts (bytes), padded so that every fragment address is a per-lane base plus an
-// immediate and the accesses are bank-conflict-free:
-//   K tile: row = key, 256 B + 16 B pad; 16-byte unit c (8 channels) at c * 16.
-//   V^T tile: row = channel d, 128 B (64 keys) + 16 B pad. Keys are stored in the order the PV
+// immediate. A fragment read (ds_read_b128, lane (l16, g) at row l16, 16-byte column g) is free of
+// bank conflicts on gfx950 when the row stride is 32 mod 64 bytes (measured: strides of 16, 48
+// or 0 mod 64 take two passes), hence the 32-byte pads:
+//   K tile: row = key, 256 B + 32 B pad; 16-byte unit c (8 channels) at c * 16.
+//   V^T tile: row = channel d, 128 B (64 keys) + 32 B pad. Keys are stored in the order the PV
 //   MFMA consumes them: within each 32-key half, position 8g + j holds key 4g + j (j < 4) and
 //   key 16 + 4g + (j - 4) (j >= 4), so a lane's 8 keys for one 32-key step are one 16-byte read.
-constexpr int KS_STRIDE = 272;
-constexpr int VT_STRIDE = 144;
+constexpr int KS_STRIDE = 288;
+constexpr int VT_STRIDE = 160;
 __device__ __forceinline__ int ks_off(int key, int c) { return key * KS_STRIDE + (c << 4); }
 // byte offset of keys [4kg, 4kg + 4) of channel d
 __device__ __forceinline__ int vt_off4(int d, int kg) {
@@ -80,6 +82,16 @@ __device__ __forceinline__ float sbyte(uint32_t w, int j) {
 __device__ __forceinline__ uint32_t hi16pair(float lo, float hi) {
     return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
 }
+
+// The workgroup's LDS: two K and two V^T tile buffers and three K-scale slots. Before the tile
+// loop the second V^T buffer holds the schedule's entry tables (cu_seqlens, cu_cached and
+// slot_ids of up to PF_MAX_ENTRIES entries). 79,360 bytes: two workgroups fit a CU's 160 KB.
+struct PfLds {
+    uint8_t k[2][PF_BN * KS_STRIDE];
+    uint8_t vt[2][PF_D * VT_STRIDE];
+    float ksc[3][PF_BN];
+    float kb[3][PF_BN];
+};
 
 struct PrefillArgs {
     const uint16_t* q;
@@ -180,9 +192,13 @@ struct Loc {
 };
 
 // One wave's pass over the tile metadata (every lane of the wave returns the same Loc). Only
-// one wave of the workgroup may call it (it owns the entry tables in LDS).
-__device__ Loc schedule(const PrefillArgs& a, int target) {
-    __shared__ int s_cu[PF_MAX_ENTRIES + 1], s_cc[PF_MAX_ENTRIES + 1], s_sl[PF_MAX_ENTRIES];
+// one wave of the workgroup may call it (it owns the entry tables in LDS, `tables`).
+__device__ Loc schedule(const PrefillArgs& a, int target, int* tables) {
+    static_assert((3 * PF_MAX_ENTRIES + 2) * sizeof(int) <= sizeof(PfLds::vt[1]),
+                  "entry tables must fit one V^T buffer");
+    int* s_cu = tables;
+    int* s_cc = tables + PF_MAX_ENTRIES + 1;
+    int* s_sl = tables + 2 * (PF_MAX_ENTRIES + 1);
     const int lane = threadIdx.x & 63;
     const int nchunks = cdiv_i(a.nsb, IE_WAVE);
     const Divisor spt = divisor(a.sub_per_tile);
@@ -655,7 +671,7 @@ __device__ __forceinline__ void load_q(bf16x8 (&qf)[2][4], const PrefillArgs& a,
 
 // One work item: tiles [kt_begin, kt_end) of piece `piece` of sub-block s for kv head hk.
 __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBlock& s, int hk,
-                                             int piece, int item) {
+                                             int piece, int item, PfLds& lds) {
     // tiles [kt_begin, kt_end): the whole pair, a prefix piece or a chunk piece
     int kt_begin = 0, kt_end = s.ntiles;
     if (s.npieces > 1) {
@@ -670,11 +686,12 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBloc
     const int h = 2 * hk + (wave & 1);
     const int wr0 = s.r0 + 32 * (wave >> 1);  // first row of this wave
 
-    // two tile buffers: tile i is staged into buffer i & 1 while the other one is computed on
-    __shared__ __attribute__((aligned(16))) uint8_t s_k[2][PF_BN * KS_STRIDE];
-    __shared__ __attribute__((aligned(16))) uint8_t s_vt[2][PF_D * VT_STRIDE];
-    __shared__ __attribute__((aligned(16))) float s_ksc[3][PF_BN];  // 3 slots: the prefix loop
-    __shared__ __attribute__((aligned(16))) float s_kb[3][PF_BN];   // rotates them
+    // two tile buffers: tile i is staged into buffer i & 1 while the other one is computed on;
+    // 3 K-scale slots: the prefix loop rotates them
+    auto& s_k = lds.k;
+    auto& s_vt = lds.vt;
+    auto& s_ksc = lds.ksc;
+    auto& s_kb = lds.kb;
 
     const float* cal = a.c.k_calibration + s.slot * a.c.cal_stride_slot + hk * a.c.cal_stride_head;
     TileSrc src;
@@ -888,8 +905,9 @@ __global__ __launch_bounds__(PF_THREADS, IE_PREFILL_WG_PER_CU) void prefill_atte
     PrefillArgs a) {
     // wave 0 reads the tile metadata and hands the workgroup its item through LDS
     __shared__ Loc s_loc;
+    __shared__ __attribute__((aligned(16))) PfLds lds;
     if (threadIdx.x < IE_WAVE) {
-        const Loc l = schedule(a, blockIdx.x);
+        const Loc l = schedule(a, blockIdx.x, reinterpret_cast<int*>(lds.vt[1]));
         if (threadIdx.x == 0) s_loc = l;
     }
     __syncthreads();
@@ -910,7 +928,7 @@ __global__ __launch_bounds__(PF_THREADS, IE_PREFILL_WG_PER_CU) void prefill_atte
         *reinterpret_cast<int4*>(a.sched + 4 + 4 * loc.split_index) =
             make_int4(loc.item_base, s.r0, s.r1, s.npieces);
     }
-    prefill_item(a, s, loc.off % a.hkv, loc.off / a.hkv, blockIdx.x);
+    prefill_item(a, s, loc.off % a.hkv, loc.off / a.hkv, blockIdx.x, lds);
 }
 
 constexpr int PF_COMB_GROUPS = 4;  // combine units per (split sub-block, kv head): 32 pairs each
@@ -923,17 +941,22 @@ constexpr int PF_COMB_GROUPS = 4;  // combine units per (split sub-block, kv hea
 // on XCD (item_base + hk) % 8, and the unit is given to a workgroup of that XCD, whose L2 holds
 // the partials.
 __global__ __launch_bounds__(PF_THREADS) void prefill_combine_kernel(PrefillArgs a) {
-    const int nsplit = uni(a.sched[1]);
     const int tid = threadIdx.x, d = 16 * (tid & 7);
     const bool by_xcd = (a.hkv & 7) == 0 && (gridDim.x & 7) == 0;
     const int hk8 = a.hkv >> 3;
-    const int units = by_xcd ? nsplit * hk8 * PF_COMB_GROUPS : nsplit * a.hkv * PF_COMB_GROUPS;
+    const int per_k = (by_xcd ? hk8 : a.hkv) * PF_COMB_GROUPS;
     const int u0 = by_xcd ? blockIdx.x >> 3 : blockIdx.x;
     const int ustep = by_xcd ? gridDim.x >> 3 : gridDim.x;
+    // the split count and the first unit's record in one memory round trip (records exist for
+    // k < nsb; the count decides which of them are this launch's)
+    const int k0 = u0 / per_k;
+    int4 rec0 = {0, 0, 0, 0};
+    if (k0 < a.nsb) rec0 = *reinterpret_cast<const int4*>(a.sched + 4 + 4 * k0);
+    const int nsplit = uni(a.sched[1]);
+    const int units = nsplit * per_k;
     for (int u = u0; u < units; u += ustep) {
-        const int per_k = (by_xcd ? hk8 : a.hkv) * PF_COMB_GROUPS;
         const int k = u / per_k, hr = (u % per_k) / PF_COMB_GROUPS, grp = u % PF_COMB_GROUPS;
-        const int4 rec = *reinterpret_cast<const int4*>(a.sched + 4 + 4 * k);
+        const int4 rec = u == u0 ? rec0 : *reinterpret_cast<const int4*>(a.sched + 4 + 4 * k);
         const int item_base = uni(rec.x);
         const int hk = by_xcd ? 8 * hr + (((int)(blockIdx.x & 7) - item_base) & 7) : hr;
         SubBlock s;

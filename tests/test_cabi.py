@@ -57,7 +57,8 @@ def test_workspace_size_formula(native):
     lib = native.cabi()
     splits = lib.ie_decode_attention_max_splits(8)
     assert splits >= 1
-    assert lib.ie_decode_attention_workspace_size(64, 16, 128) == 64 * 16 * splits * 130 * 4
+    # a 256-byte plan record (the step's piece size), then the fp32 partials
+    assert lib.ie_decode_attention_workspace_size(64, 16, 128) == 256 + 64 * 16 * splits * 130 * 4
 
 
 def test_ops_refuse_cpu_tensors(ie):
