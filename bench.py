@@ -179,8 +179,8 @@ def bench_linear(K, M, dev):
         calls = lambda f: [lambda w=w: f(w) for w in ws] * max(1, 16 // len(ws))
         lib_ms = time_graph_calls(calls(lambda w: torch.nn.functional.linear(x, w)))
         best = None
-        for nt in (1, 2, 4):
-            if N % (16 * nt) == 0:
+        for nt in (0, 1, 2, 4):
+            if N % (16 * max(1, nt)) == 0:
                 t = time_graph_calls(calls(lambda w, nt=nt: K.skinny_matmul(x, w, nt)))
                 best = (t, nt) if best is None or t < best[0] else best
         res[name] = {"bytes": nbytes, "skinny_us": round(best[0] * 1e3, 2), "n_tiles": best[1],

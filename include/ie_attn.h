@@ -286,9 +286,10 @@ hipError_t ie_silu_mul(const ie_bf16* gate_up, int64_t gate_up_stride, int64_t n
  * (kernels.py:1451-1458) picks per (N, K, M) over the library GEMM after `tune_linear` timed both.
  * x: bf16 [m, k] (m <= 64), weight: bf16 [n, k] (nn.Linear layout), y: bf16 [m, n]; fp32
  * accumulation, y rounded to nearest even. n_tiles (1, 2 or 4): weight rows per workgroup / 16,
- * the shape-dependent launch choice (more rows per workgroup re-read x less often, fewer
- * workgroups fill fewer CUs). n a multiple of 16 n_tiles, k of 256; rows 16-byte aligned (y
- * 8-byte).
+ * or 0 for 8 rows per workgroup, the shape-dependent launch choice (more rows per workgroup
+ * re-read x less often, fewer workgroups fill fewer CUs; it is lowered where m leaves too little
+ * LDS for it, which can change the rounding of the k summation, not the result's tolerance).
+ * n a multiple of 16 max(1, n_tiles), k of 256; rows 16-byte aligned (y 8-byte).
  */
 hipError_t ie_skinny_gemm(const ie_bf16* x, int64_t x_stride, int32_t m, const ie_bf16* weight,
                           int64_t weight_stride, int32_t n, int32_t k, int32_t n_tiles, ie_bf16* y,

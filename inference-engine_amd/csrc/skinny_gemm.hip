@@ -4,90 +4,153 @@
 //
 // At decode row counts the weight read is the whole cost (one byte of W feeds 2M flops), so the
 // kernel streams every weight byte once from HBM and keeps x, which every workgroup needs, in the
-// caches. Workgroup n-tile t (grid N / 16, 512 threads) owns W rows [16t, 16t + 16); its eight
-// waves split K into eight contiguous slices. Per 32-wide k step a wave issues
-// v_mfma_f32_16x16x32_bf16 with A = 16 W rows x 32 k (lane (r, g) holds row 16t + r, k 8g..8g+7:
-// one 16-byte load) and B = x^T, 32 k x 16 rows of x per m-tile (the same lane mapping over x's
-// rows), so D = y^T (16 n x 16 m). Loads run SG_UNROLL steps ahead of the MFMAs. The eight
-// partial D tiles are summed through LDS in wave order and written as bf16.
+// caches. Workgroup n-tile t (grid N / (16 NT), 512 threads) owns W rows [16 NT t, +16 NT); its
+// eight waves split K into eight contiguous slices. Per 32-wide k step a wave issues
+// v_mfma_f32_16x16x32_bf16 with A = 16 W rows x 32 k (lane (r, g): row r, k 8g..8g+7) and
+// B = x^T, 32 k x 16 rows of x per m-tile (the same lane mapping over x's rows), so
+// D = y^T (16 n x 16 m).
+//
+// Loads do not use that lane mapping: a wave load in it touches 16 rows x 64 bytes, and such
+// loads moved 15 bytes per clock per CU on this part against 44 for 8 rows x 128 bytes and 50
+// for 1 KB contiguous (measured, L2-resident data). So each wave loads a batch of 64 k as
+// 8-row x 128-byte pieces (lane (row L / 8, 16-byte chunk L % 8)), stores them in its own LDS
+// region (rows of 160 bytes: both the row-wise stores and the fragment reads are free of bank
+// conflicts) and reads the MFMA fragments back. Batch b + 1 is loaded into registers while
+// batch b goes through LDS and the MFMAs. The eight partial D tiles are summed through LDS in
+// wave order and written as bf16.
 #include "ie_common.h"
 
 namespace ie {
 
 typedef __bf16 sg_bf16x8 __attribute__((ext_vector_type(8)));
 typedef float sg_f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t sg_u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int SG_WAVES = 8;
 constexpr int SG_THREADS = SG_WAVES * IE_WAVE;
-constexpr int SG_UNROLL = 4;  // k steps of 32 in flight per wave
+constexpr int SG_BK = 64;      // k per batch: 128 bytes of a row, one 8-lane load group
+constexpr int SG_LROW = 160;   // LDS row stride (bytes)
+constexpr int SG_MAX_TILES = 6;  // NT + MT, at most (LDS: 8 waves x 16 (NT + MT) rows x 160 B)
 
-__device__ __forceinline__ sg_bf16x8 ld_frag(rsrc_t r, int off) {
-    return __builtin_bit_cast(sg_bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
-}
+template <int NT, int MT>
+struct SgLds {
+    union {
+        uint8_t t[SG_WAVES][16 * (NT + MT) * SG_LROW];  // per-wave transpose regions
+        sg_f32x4 acc[SG_WAVES][NT * MT][IE_WAVE];       // partial D tiles (after the loop)
+    };
+};
 
 // MT m-tiles of 16 rows (M <= 16 MT), NT n-tiles of 16 weight rows per workgroup (every x
-// fragment feeds NT MFMAs). K a multiple of 8 * 32 = 256 (each wave's slice is a multiple of 32).
-template <int MT, int NT>
+// fragment feeds NT MFMAs), or with HALF one n-tile of 8 rows (NT = 1: twice the workgroups for
+// narrow weights; the MFMA's other 8 rows compute outputs that are not stored). K a multiple of
+// 8 * 32 = 256 (each wave's slice is a multiple of 32).
+template <int MT, int NT, bool HALF>
 __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
     const uint16_t* __restrict__ x, int64_t xs, int M, const uint16_t* __restrict__ w, int64_t ws,
     int K, uint16_t* __restrict__ y, int64_t ys) {
+    static_assert(NT + MT <= SG_MAX_TILES, "LDS transpose region too large");
+    static_assert(!HALF || NT == 1, "8-row n-tiles come one per workgroup");
+    constexpr int WROWS = HALF ? 8 : 16 * NT;  // weight rows per workgroup
+    constexpr int TILES = NT + MT;  // W tiles 0..NT-1, then x tiles
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l16 = lane & 15, g = lane >> 4;
-    const int n0 = blockIdx.x * 16 * NT;
+    const int lr = lane >> 3, lc = lane & 7;  // load mapping: row lr of 8, 16-byte chunk lc
+    const int n0 = blockIdx.x * WROWS;
     // wave w of workgroup b takes K slice (w + b) mod 8: neighbouring workgroups read different
     // parts of x at any moment instead of all hitting the same L2 lines
     const int kw = K / SG_WAVES, k_begin = (int)((wave + blockIdx.x) % SG_WAVES) * kw;
     // W rows [n0, n0 + 16 NT) and x rows [0, M): the buffer ranges zero the rows of x past M
-    const rsrc_t rw = make_rsrc(w + (int64_t)n0 * ws, (uint32_t)(16 * NT * ws * 2));
+    const rsrc_t rw = make_rsrc(w + (int64_t)n0 * ws, (uint32_t)(WROWS * ws * 2));
     const rsrc_t rx = make_rsrc(x, (uint32_t)(M * xs * 2));
-    int woff[NT], xoff[MT];
+    // byte offsets of this lane's two 8-row halves of every tile at the slice start
+    int loff[TILES][2];
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) woff[nt] = ((16 * nt + l16) * (int)ws + k_begin + 8 * g) * 2;
+    for (int i = 0; i < TILES; ++i)
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) xoff[mt] = ((16 * mt + l16) * (int)xs + k_begin + 8 * g) * 2;
+        for (int h = 0; h < 2; ++h) {
+            const int row = 16 * (i < NT ? i : i - NT) + 8 * h + lr;
+            loff[i][h] = (row * (int)(i < NT ? ws : xs) + k_begin + 8 * lc) * 2;
+        }
+
+    __shared__ __attribute__((aligned(16))) SgLds<NT, MT> lds;
+    uint8_t* reg = lds.t[wave];
+    uint8_t* wdst = reg + lr * SG_LROW + 16 * lc;          // + (16 i + 8 h) rows
+    const uint8_t* rsrc = reg + l16 * SG_LROW + 16 * g;   // + 16 i rows + 64 t
 
     sg_f32x4 acc[NT][MT];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = sg_f32x4{0.f, 0.f, 0.f, 0.f};
-    const int steps = kw / 32;
-    for (int s = 0; s < steps; s += SG_UNROLL) {
-        sg_bf16x8 wf[SG_UNROLL][NT], xf[SG_UNROLL][MT];
+
+    typedef sg_u32x4 Batch[TILES][2];
+    // batch b: k [64 b, 64 b + 64) of the slice; chunks past the slice (or past the last batch)
+    // load out of range, i.e. zeros without a memory access
+    auto load = [&](Batch& r, int b) {
+        const bool in = SG_BK * b + 8 * lc < kw;
 #pragma unroll
-        for (int u = 0; u < SG_UNROLL; ++u) {
-            const int o = (s + u < steps ? s + u : steps) * 64;  // past the slice: out of range
+        for (int i = 0; i < TILES; ++i)
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt) wf[u][nt] = ld_frag(rw, s + u < steps ? woff[nt] + o : -1);
+            for (int h = 0; h < 2; ++h) {
+                if (HALF && i < NT && h == 1) continue;
+                r[i][h] = __builtin_amdgcn_raw_buffer_load_b128(i < NT ? rw : rx,
+                                                                in ? loff[i][h] + 128 * b : -1, 0, 0);
+            }
+    };
+    auto compute = [&](const Batch& r) {
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt) xf[u][mt] = ld_frag(rx, s + u < steps ? xoff[mt] + o : -1);
-        }
+        for (int i = 0; i < TILES; ++i)
 #pragma unroll
-        for (int u = 0; u < SG_UNROLL; ++u)
+            for (int h = 0; h < 2; ++h) {
+                if (HALF && i < NT && h == 1) continue;  // weight rows 8..15: not stored
+                *reinterpret_cast<sg_u32x4*>(wdst + (16 * i + 8 * h) * SG_LROW) = r[i][h];
+            }
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            sg_bf16x8 f[TILES];
+#pragma unroll
+            for (int i = 0; i < TILES; ++i)
+                f[i] = __builtin_bit_cast(
+                    sg_bf16x8, *reinterpret_cast<const sg_u32x4*>(rsrc + 16 * i * SG_LROW + 64 * t));
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt)
-                    acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[u][nt], xf[u][mt],
+                    acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f[nt], f[NT + mt],
                                                                          acc[nt][mt], 0, 0, 0);
+        }
+    };
+    // The batch loads are unconditional and each is pinned ahead of the work it overlaps with a
+    // sched_barrier: loads under a branch make the compiler's wait counts assume the worst at the
+    // join, and left alone the scheduler sinks them below the MFMAs.
+    const int nb = (kw + SG_BK - 1) / SG_BK;
+    Batch ra, rb;
+    load(ra, 0);
+    for (int b = 0; b < nb; b += 2) {
+        load(rb, b + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(ra);
+        load(ra, b + 2);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(rb);
     }
 
     // D lane (l16, g) element i: n = n0 + 16 nt + 4g + i, m = 16 mt + l16. The waves' partial
     // tiles are summed in wave order, one (nt, mt) tile per wave.
-    __shared__ sg_f32x4 s_acc[SG_WAVES][NT * MT][IE_WAVE];
+    __syncthreads();  // every wave is done with its transpose region (the partial tiles alias it)
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) s_acc[wave][nt * MT + mt][lane] = acc[nt][mt];
+        for (int mt = 0; mt < MT; ++mt) lds.acc[wave][nt * MT + mt][lane] = acc[nt][mt];
     __syncthreads();
     for (int tile = wave; tile < NT * MT; tile += SG_WAVES) {
-        sg_f32x4 t = s_acc[0][tile][lane];
+        sg_f32x4 t = lds.acc[0][tile][lane];
 #pragma unroll
-        for (int v = 1; v < SG_WAVES; ++v) t += s_acc[v][tile][lane];
+        for (int v = 1; v < SG_WAVES; ++v) t += lds.acc[v][tile][lane];
         const int nt = tile / MT, mt = tile % MT;
         const int m = 16 * mt + l16;
-        if (m < M) {
+        if (m < M && (!HALF || g < 2)) {
             uint16_t* dst = y + (int64_t)m * ys + n0 + 16 * nt + 4 * g;
             *reinterpret_cast<uint2*>(dst) =
                 make_uint2(pack_bf16x2(t[0], t[1]), pack_bf16x2(t[2], t[3]));
@@ -109,35 +172,52 @@ extern "C" hipError_t ie_skinny_gemm(const ie_bf16* x, int64_t x_stride, int32_t
     IE_REQUIRE(m <= 64, "at most 64 rows");
     IE_REQUIRE(n % 16 == 0 && k % (SG_WAVES * 32) == 0 && k > 0,
                "n must be a multiple of 16 and k of 256");
-    IE_REQUIRE(n_tiles == 1 || n_tiles == 2 || n_tiles == 4, "n_tiles must be 1, 2 or 4");
-    IE_REQUIRE(n % (16 * n_tiles) == 0, "n must be a multiple of 16 n_tiles");
+    IE_REQUIRE(n_tiles == 0 || n_tiles == 1 || n_tiles == 2 || n_tiles == 4,
+               "n_tiles must be 0 (8-row tiles), 1, 2 or 4");
+    IE_REQUIRE(n % (16 * std::max(1, n_tiles)) == 0, "n must be a multiple of 16 n_tiles");
     IE_REQUIRE(x_stride % 8 == 0 && weight_stride % 8 == 0 && y_stride % 4 == 0 &&
                    (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
                    (reinterpret_cast<uintptr_t>(weight) & 15) == 0 &&
                    (reinterpret_cast<uintptr_t>(y) & 7) == 0,
                "rows must be 16-byte aligned (8-byte for y)");
     IE_REQUIRE((int64_t)m * x_stride * 2 < (1LL << 31) &&
-                   16LL * n_tiles * weight_stride * 2 < (1LL << 31),
+                   16LL * std::max(1, n_tiles) * weight_stride * 2 < (1LL << 31),
                "operands too large for 32-bit buffer offsets");
-    const dim3 grid((unsigned)(n / (16 * n_tiles)));
     const int mt = (m + 15) / 16;
+    // n_tiles is a performance choice: it is lowered until the LDS transpose region fits
+    while (n_tiles > 1 && n_tiles + mt > SG_MAX_TILES) n_tiles >>= 1;
+    const bool half = n_tiles == 0;
+    const dim3 grid((unsigned)(half ? n / 8 : n / (16 * n_tiles)));
 #define IE_SG_LAUNCH(MT, NT)                                                                   \
-    hipLaunchKernelGGL((skinny_gemm_kernel<MT, NT>), grid, dim3(SG_THREADS), 0, stream,        \
+    hipLaunchKernelGGL((skinny_gemm_kernel<MT, NT, false>), grid, dim3(SG_THREADS), 0, stream, \
                        (const uint16_t*)x, x_stride, m, (const uint16_t*)weight, weight_stride, \
                        k, (uint16_t*)y, y_stride)
-#define IE_SG_NT(MT)                                 \
+#define IE_SG_LAUNCH_HALF(MT)                                                                   \
+    hipLaunchKernelGGL((skinny_gemm_kernel<MT, 1, true>), grid, dim3(SG_THREADS), 0, stream,     \
+                       (const uint16_t*)x, x_stride, m, (const uint16_t*)weight, weight_stride,  \
+                       k, (uint16_t*)y, y_stride)
+#define IE_SG_NT4(MT)                                \
     switch (n_tiles) {                               \
+        case 0: IE_SG_LAUNCH_HALF(MT); break;        \
         case 1: IE_SG_LAUNCH(MT, 1); break;          \
         case 2: IE_SG_LAUNCH(MT, 2); break;          \
         default: IE_SG_LAUNCH(MT, 4); break;         \
     }
-    switch (mt) {
-        case 1: IE_SG_NT(1); break;
-        case 2: IE_SG_NT(2); break;
-        case 3: IE_SG_NT(3); break;
-        default: IE_SG_NT(4); break;
+#define IE_SG_NT2(MT)                                \
+    switch (n_tiles) {                               \
+        case 0: IE_SG_LAUNCH_HALF(MT); break;        \
+        case 1: IE_SG_LAUNCH(MT, 1); break;          \
+        default: IE_SG_LAUNCH(MT, 2); break;         \
     }
-#undef IE_SG_NT
+    switch (mt) {  // (MT, NT) pairs within SG_MAX_TILES
+        case 1: IE_SG_NT4(1); break;
+        case 2: IE_SG_NT4(2); break;
+        case 3: IE_SG_NT2(3); break;
+        default: IE_SG_NT2(4); break;
+    }
+#undef IE_SG_NT4
+#undef IE_SG_NT2
+#undef IE_SG_LAUNCH_HALF
 #undef IE_SG_LAUNCH
     return hipGetLastError();
 }

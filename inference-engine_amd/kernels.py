@@ -202,17 +202,18 @@ def silu_mul(gate_up: torch.Tensor) -> torch.Tensor:
 
 def skinny_matmul(x: torch.Tensor, weight: torch.Tensor, n_tiles: int = 1) -> torch.Tensor:
     """qwen3-1.7b/kernels.py:1406-1443: [M, K] bf16 @ [N, K].T bf16 -> [M, N] bf16 for M <= 64.
-    `n_tiles` (1, 2, 4): weight rows per workgroup / 16, the launch shape tune_linear picks."""
+    `n_tiles` (1, 2, 4; 0 = 8 rows): weight rows per workgroup / 16, the launch shape tune_linear
+    picks."""
     M, K = x.shape
     N = weight.shape[0]
     assert x.stride(-1) == 1 and weight.stride(-1) == 1
     assert M <= 64, "big M is compute bound, the library GEMM is faster there"
-    assert N % (16 * n_tiles) == 0 and K % 256 == 0
+    assert n_tiles in (0, 1, 2, 4) and N % (16 * max(1, n_tiles)) == 0 and K % 256 == 0
     return ops().skinny_matmul(x, weight, int(n_tiles))
 
 
 # (N, K, M) -> the n_tiles of skinny_matmul when it beat the library GEMM for that weight shape
-# and row count, else 0 (qwen3-1.7b/kernels.py:1446-1448). Filled by tune_linear before graph
+# and row count, else None (qwen3-1.7b/kernels.py:1446-1448). Filled by tune_linear before graph
 # capture; anything it never measured uses the library.
 use_skinny: dict = {}
 
@@ -220,8 +221,8 @@ use_skinny: dict = {}
 def linear(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     """qwen3-1.7b/kernels.py:1451-1458: [M, K] @ [N, K].T -> [M, N], with whichever measured
     faster."""
-    nt = use_skinny.get((weight.shape[0], weight.shape[1], x.shape[0]), 0)
-    if nt:
+    nt = use_skinny.get((weight.shape[0], weight.shape[1], x.shape[0]))
+    if nt is not None:
         return skinny_matmul(x, weight, nt)
     return torch.nn.functional.linear(x, weight)
 
@@ -244,10 +245,10 @@ def tune_linear(weights: list, rows: list, calls: int = 20) -> None:
             x = torch.randn(M, K, device=weight.device, dtype=weight.dtype)
             cycle = lambda f: [lambda w=w: f(w) for w in copies] * max(1, calls // len(copies))
             lib = _graph_time(cycle(lambda w: torch.nn.functional.linear(x, w)))
-            best, choice = 0.98 * lib, 0
+            best, choice = 0.98 * lib, None
             if K % 256 == 0:
-                for nt in (1, 2, 4):
-                    if N % (16 * nt):
+                for nt in (0, 1, 2, 4):
+                    if N % (16 * max(1, nt)):
                         continue
                     t = _graph_time(cycle(lambda w, nt=nt: skinny_matmul(x, w, nt)))
                     if t < best:
