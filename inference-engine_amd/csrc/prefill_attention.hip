@@ -342,11 +342,14 @@ __device__ __forceinline__ float ldf(rsrc_t r, int off) {
 
 // Prefix tiles, K and V handled separately (the prefix loop stages K two tiles and V one tile
 // ahead of the MFMAs): the int8 rows and per-key scales of one tile, in registers between load
-// and staging. Same lane mappings as load_tile / stage_tile. K is staged as exact bf16 integers
-// (its scale multiplies the scores); V is staged dequantized, bf16(v * v_scale), the rounding
-// the reference's dequantization applies, so P needs no per-key factor.
+// and staging. K is staged as exact bf16 integers (its scale multiplies the scores); V is staged
+// dequantized, bf16(v * v_scale), the rounding the reference's dequantization applies, so P
+// needs no per-key factor.
+// K rows are loaded 8 lanes per 128-byte row (thread: keys (tid >> 3) and (tid >> 3) + 32,
+// channels [16 (tid & 7), +16)): wave loads that cover few lanes per row moved a third of the
+// bytes per clock on this part.
 struct PfxK {
-    uint32_t kw[8];
+    u32x4 kw[2];
     float kscale, kbias;
 };
 struct PfxV {
@@ -355,10 +358,9 @@ struct PfxV {
 };
 __device__ __forceinline__ void load_pk(PfxK& r, const TileSrc& src, int kbase, int P) {
     const int tid = threadIdx.x;
-    const int off = (kbase + (tid >> 2)) * PF_D + 32 * (tid & 3);
-    const u32x4 b0 = ld128(src.pk, off), b1 = ld128(src.pk, off + 16);
-    r.kw[0] = b0.x; r.kw[1] = b0.y; r.kw[2] = b0.z; r.kw[3] = b0.w;
-    r.kw[4] = b1.x; r.kw[5] = b1.y; r.kw[6] = b1.z; r.kw[7] = b1.w;
+    const int off = (kbase + (tid >> 3)) * PF_D + 16 * (tid & 7);
+    r.kw[0] = ld128(src.pk, off);
+    r.kw[1] = ld128(src.pk, off + 32 * PF_D);
     const int kk = kbase + (tid & (PF_BN - 1));
     r.kscale = ldf(src.pks, 4 * kk);
     r.kbias = kk < P ? 0.f : -INFINITY;
@@ -370,18 +372,23 @@ __device__ __forceinline__ void load_pv(PfxV& r, const TileSrc& src, int kbase) 
     for (int u = 0; u < 4; ++u) r.vw[u] = ld64(src.pv, (kbase + 4 * kg + u) * PF_D + 8 * dg);
     r.vs = __builtin_bit_cast(f32x4, ld128(src.pvs, 4 * (kbase + 4 * kg)));
 }
+// 16 int8 channels -> two 16-byte bf16 units 2c and 2c + 1 of the key's row, the one written
+// first alternating with c / 4 so that each 8-lane store group covers distinct banks.
 __device__ __forceinline__ void stage_pk(const PfxK& r, uint8_t* s_k) {
-    const int tid = threadIdx.x;
-    uint32_t w[16];
+    const int tid = threadIdx.x, c = tid & 7, sw = (c >> 2) & 1;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        w[2 * i] = hi16pair(sbyte(r.kw[i], 0), sbyte(r.kw[i], 1));
-        w[2 * i + 1] = hi16pair(sbyte(r.kw[i], 2), sbyte(r.kw[i], 3));
+    for (int i = 0; i < 2; ++i) {
+        uint32_t w[8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            w[2 * j] = hi16pair(sbyte(r.kw[i][j], 0), sbyte(r.kw[i][j], 1));
+            w[2 * j + 1] = hi16pair(sbyte(r.kw[i][j], 2), sbyte(r.kw[i][j], 3));
+        }
+        uint8_t* row = s_k + ks_off((tid >> 3) + 32 * i, 2 * c);
+        const u32x4 lo = {w[0], w[1], w[2], w[3]}, hi = {w[4], w[5], w[6], w[7]};
+        *reinterpret_cast<u32x4*>(row + 16 * sw) = sw ? hi : lo;
+        *reinterpret_cast<u32x4*>(row + 16 * (1 - sw)) = sw ? lo : hi;
     }
-    uint8_t* dst = s_k + ks_off(tid >> 2, 4 * (tid & 3));
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-        *reinterpret_cast<u32x4*>(dst + 16 * i) = u32x4{w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]};
 }
 __device__ __forceinline__ void stage_pk_scales(const PfxK& r, float* s_ksc, float* s_kb,
                                                 float qk_scale) {
@@ -406,18 +413,18 @@ __device__ __forceinline__ void stage_pv(const PfxV& r, uint8_t* s_vt) {
 
 // Chunk tiles: bf16 rows seq_start + [kbase, kbase + 64) of the packed chunk (zeros at or past
 // the sub-block's last row: the buffer range does the masking), K and V in registers between
-// load and staging. Same lane mappings as the prefix tiles.
+// load and staging. V has the prefix tiles' lane mapping.
 struct ChkK {
-    u32x4 w[4];  // key tid >> 2, channels [32 (tid & 3), +32)
+    u32x4 w[4];  // keys (tid >> 4) + 16 i, channels [8 (tid & 15), +8): 16 lanes per 256-byte row
 };
 struct ChkV {
     u32x4 w[4];  // keys 4 (tid & 15) + u, channels [8 (tid >> 4), +8)
 };
 __device__ __forceinline__ void load_ck(ChkK& r, const TileSrc& src, int kbase) {
     const int tid = threadIdx.x;
-    const int off = (kbase + (tid >> 2)) * src.ck_stride + 64 * (tid & 3);
+    const int off = (kbase + (tid >> 4)) * src.ck_stride + 16 * (tid & 15);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) r.w[i] = ld128(src.ck, off + 16 * i);
+    for (int i = 0; i < 4; ++i) r.w[i] = ld128(src.ck, off + 16 * i * src.ck_stride);
 }
 __device__ __forceinline__ void load_cv(ChkV& r, const TileSrc& src, int kbase) {
     const int tid = threadIdx.x;
@@ -427,9 +434,9 @@ __device__ __forceinline__ void load_cv(ChkV& r, const TileSrc& src, int kbase) 
 }
 __device__ __forceinline__ void stage_ck(const ChkK& r, uint8_t* s_k) {
     const int tid = threadIdx.x;
-    uint8_t* dst = s_k + ks_off(tid >> 2, 4 * (tid & 3));
+    uint8_t* dst = s_k + ks_off(tid >> 4, tid & 15);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(dst + 16 * i) = r.w[i];
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(dst + 16 * i * KS_STRIDE) = r.w[i];
 }
 __device__ __forceinline__ void stage_cv(const ChkV& r, uint8_t* s_vt) {
     const int tid = threadIdx.x;
