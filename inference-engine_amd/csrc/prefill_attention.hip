@@ -645,17 +645,37 @@ __device__ __forceinline__ void tile_pv(WaveState& w, const uint32_t (&pfrag)[2]
 
 // Q^T fragments of this wave: lane holds q[row = wr0 + 16nt + l16][d = 32ks + 8g .. +7], as
 // bf16(q * cal) for prefix tiles or bf16 q for chunk tiles; zero rows past the sub-block.
+// The 32 rows x 256 bytes are loaded 16 lanes per row (loads in the fragment layout, 16 rows x
+// 64 bytes per wave instruction, moved a third of the bytes per clock) into the wave's own LDS
+// region `qreg` (rows of QS_STRIDE bytes, 32 mod 64: conflict-free fragment reads) and read back
+// in the fragment layout. The region lies in the V^T buffers: the caller keeps them unstaged
+// until every wave has passed a barrier after this call.
+constexpr int QS_STRIDE = 288;
+static_assert(4 * 32 * QS_STRIDE <= 2 * PF_D * VT_STRIDE, "Q regions must fit the V^T buffers");
 template <bool PREFIX>
 __device__ __forceinline__ void load_q(bf16x8 (&qf)[2][4], const PrefillArgs& a, int wr0, int r1,
-                                       int h, const float* cal, int l16, int g) {
+                                       int h, const float* cal, int l16, int g, uint8_t* qreg) {
+    const int lane = threadIdx.x & 63, qr = lane >> 4, qc = lane & 15;
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {  // 16 rows at a time: fewer registers in flight
+        u32x4 raw[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int row = wr0 + 16 * half + 4 * j + qr;
+            raw[j] = u32x4{0u, 0u, 0u, 0u};
+            if (row < r1)
+                raw[j] = *reinterpret_cast<const u32x4*>(a.q + row * a.q_st + h * a.q_sh + 8 * qc);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            *reinterpret_cast<u32x4*>(qreg + (16 * half + 4 * j + qr) * QS_STRIDE + 16 * qc) = raw[j];
+    }
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
-        const int row = wr0 + 16 * nt + l16;
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-            u32x4 w = {0u, 0u, 0u, 0u};
-            if (row < r1)
-                w = *reinterpret_cast<const u32x4*>(a.q + row * a.q_st + h * a.q_sh + 32 * ks + 8 * g);
+            u32x4 w = *reinterpret_cast<const u32x4*>(qreg + (16 * nt + l16) * QS_STRIDE +
+                                                      16 * (4 * ks + g));
             if (PREFIX) {
                 const f32x4 c0 = *reinterpret_cast<const f32x4*>(cal + 32 * ks + 8 * g);
                 const f32x4 c1 = *reinterpret_cast<const f32x4*>(cal + 32 * ks + 8 * g + 4);
@@ -664,9 +684,6 @@ __device__ __forceinline__ void load_q(bf16x8 (&qf)[2][4], const PrefillArgs& a,
                           pack_bf16x2(bf16lo(w.z) * c1[0], bf16hi(w.z) * c1[1]),
                           pack_bf16x2(bf16lo(w.w) * c1[2], bf16hi(w.w) * c1[3])};
             }
-            // a register use here makes the compiler wait for the Q loads now, not inside the
-            // tile loop where the wait would also cover the next tile's prefetch
-            asm volatile("" : "+v"(w));
             qf[nt][ks] = __builtin_bit_cast(bf16x8, w);
         }
     }
@@ -697,6 +714,7 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBloc
     // 3 K-scale slots: the prefix loop rotates them
     auto& s_k = lds.k;
     auto& s_vt = lds.vt;
+    uint8_t* qreg = &lds.vt[0][0] + wave * 32 * QS_STRIDE;  // this wave's Q staging region
     auto& s_ksc = lds.ksc;
     auto& s_kb = lds.kb;
 
@@ -747,9 +765,10 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBloc
             load_pk(pk, src, kb0, s.P);
             load_pv(pv, src, kb0);
             if (n > 1) load_pk(pk1, src, kb0 + PF_BN, s.P);
-            load_q<true>(qf, a, wr0, s.r1, h, cal, l16, g);
+            load_q<true>(qf, a, wr0, s.r1, h, cal, l16, g, qreg);
             stage_pk(pk, s_k[0]);
             stage_pk_scales(pk, s_ksc[0], s_kb[0], a.qk_scale);
+            __syncthreads();  // every wave has read its Q region (in the V^T buffers)
             stage_pv(pv, s_vt[0]);
             if (n > 1) {
                 stage_pk(pk1, s_k[1]);
@@ -823,8 +842,9 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBloc
             load_ck(ck, src, kb0);
             load_cv(cv, src, kb0);
             if (n > 1) load_ck(ck1, src, kb0 + PF_BN);
-            load_q<false>(qf, a, wr0, s.r1, h, cal, l16, g);
+            load_q<false>(qf, a, wr0, s.r1, h, cal, l16, g, qreg);
             stage_ck(ck, s_k[0]);
+            __syncthreads();  // every wave has read its Q region (in the V^T buffers)
             stage_cv(cv, s_vt[0]);
             if (n > 1) stage_ck(ck1, s_k[1]);
         }
