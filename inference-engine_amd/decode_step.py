@@ -7,10 +7,10 @@ replay (qwen3-1.7b/engine.py:376-470): per layer, `add_rms_norm` (the first laye
 QKV projection, `fused_rope_kv_decode` (norm + RoPE + int8 KV write), `decode_attention`,
 output projection, `add_rms_norm`, gate/up projection, `silu_mul`, down projection; then the
 final `add_rms_norm`, the tied-embedding LM head and greedy sampling (`sample` at tau 0,
-kernels.py:1343-1370). All of these are this package's HIP kernels except the projections where
-`linear` (kernels.py:1451-1458) picks the library GEMM (hipBLASLt): `tune_linear` times this
-package's skinny GEMM against it for every weight shape at the step's row count before
-capture, as the reference's engine does (engine.py:352-374).
+kernels.py:1343-1370). All of these are this package's HIP kernels; for each projection
+`linear` (kernels.py:1451-1458) runs this package's skinny GEMM or the library GEMM
+(hipBLASLt), whichever `tune_linear` measured faster for that weight shape at the step's row
+count before capture, as the reference's engine does (engine.py:352-374).
 
 Weights are random (bf16, std 0.02) and the caches hold random int8 K/V: there is no checkpoint
 here, and the step's cost does not depend on the values.
