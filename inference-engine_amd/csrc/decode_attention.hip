@@ -49,6 +49,7 @@ constexpr int DA_U = 4;                            // tokens per lane group per 
 constexpr int DA_TOK_WAVE = 8 * DA_U;              // 32 tokens per wave block
 constexpr int DA_TOK_WG = DA_WAVES * DA_TOK_WAVE;  // tokens per workgroup step
 constexpr int DA_MIN_PIECE = 128;
+constexpr int DA_MAX_SPLITS = 1024;  // pieces per sequence the combine kernel merges, at most
 constexpr int DA_D = 128;
 constexpr uint32_t K64 = 0x64646464u;
 constexpr float OFFSET = 1152.0f;  // fp16(0x64xx) = 1024 + byte, byte = x + 128
@@ -437,14 +438,44 @@ __global__ __launch_bounds__(128) void decode_combine_kernel(
     if (needed <= 1) return;
     const int d = threadIdx.x;
     const int64_t row0 = ((int64_t)b * hq + h) * max_splits;
-    float mx = -INFINITY;
-    for (int s = 0; s < needed; ++s) mx = fmaxf(mx, part_m[row0 + s]);
+    // One memory round trip for all of it: lane s of wave 0 loads split s's (m, l) while every
+    // thread loads its first batch of partial outputs; the weights 2^(m_s - max m) go through
+    // LDS, and each thread then adds the splits in order (the same sums as one thread alone).
+    constexpr int CB = 8;  // partial outputs per load batch
+    __shared__ float s_f[DA_MAX_SPLITS], s_l[DA_MAX_SPLITS];
+    float av[CB];
+#pragma unroll
+    for (int u = 0; u < CB; ++u) av[u] = u < needed ? part_acc[(row0 + u) * DA_D + d] : 0.0f;
+    if (d < IE_WAVE) {  // splits d, d + 64, ...: one pass when there are at most 64
+        const float m0 = d < needed ? part_m[row0 + d] : -INFINITY;
+        const float l0 = d < needed ? part_l[row0 + d] : 0.0f;
+        float mx = m0;
+        for (int s = d + IE_WAVE; s < needed; s += IE_WAVE) mx = fmaxf(mx, part_m[row0 + s]);
+        mx = wave_max(mx);
+        s_f[d] = m0 == -INFINITY ? 0.0f : exp2_safe(m0 - mx);
+        s_l[d] = l0;
+        for (int s = d + IE_WAVE; s < needed; s += IE_WAVE) {
+            const float m = part_m[row0 + s];
+            s_f[s] = m == -INFINITY ? 0.0f : exp2_safe(m - mx);
+            s_l[s] = part_l[row0 + s];
+        }
+    }
+    __syncthreads();
     float num = 0.0f, den = 0.0f;
-    for (int s = 0; s < needed; ++s) {
-        const float ms = part_m[row0 + s];
-        const float f = ms == -INFINITY ? 0.0f : exp2_safe(ms - mx);
-        num += part_acc[(row0 + s) * DA_D + d] * f;
-        den += part_l[row0 + s] * f;
+    for (int s0 = 0; s0 < needed; s0 += CB) {
+        if (s0 > 0) {
+#pragma unroll
+            for (int u = 0; u < CB; ++u)
+                av[u] = s0 + u < needed ? part_acc[(row0 + s0 + u) * DA_D + d] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < CB; ++u) {
+            if (s0 + u < needed) {
+                const float f = s_f[s0 + u];
+                num += av[u] * f;
+                den += s_l[s0 + u] * f;
+            }
+        }
     }
     out[b * o_sb + h * o_sh + d] = (uint16_t)f32_to_bf16_rne(num / den);
 }
@@ -456,7 +487,7 @@ struct Layout {
 
 static Layout workspace_layout(int batch, int hq, int hkv) {
     Layout L;
-    L.target = decode_target(hkv);
+    L.target = std::min(decode_target(hkv), DA_MAX_SPLITS);
     L.max_splits = L.target;
     const size_t rows = (size_t)std::max(batch, 0) * hq * L.max_splits;
     L.plan_off = 0;
@@ -472,7 +503,7 @@ static Layout workspace_layout(int batch, int hq, int hkv) {
 using namespace ie;
 
 extern "C" int32_t ie_decode_attention_max_splits(int32_t num_kv_heads) {
-    return decode_target(num_kv_heads);
+    return std::min(decode_target(num_kv_heads), DA_MAX_SPLITS);
 }
 
 extern "C" size_t ie_decode_attention_workspace_size(int32_t batch, int32_t num_q_heads,

@@ -40,7 +40,13 @@ __global__ __launch_bounds__(NA_THREADS) void add_rms_norm_kernel(
     const int tid = threadIdx.x;
     const int passes = (D + NA_STEP - 1) / NA_STEP;
     float r[NA_MAX_PASSES][NA_VEC];
+    uint4 wraw[NA_MAX_PASSES];  // the weight, loaded with the row (not after the reduction)
     float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NA_MAX_PASSES; ++j) {
+        const int c = j * NA_STEP + NA_VEC * tid;
+        if (j < passes && c < D) wraw[j] = *reinterpret_cast<const uint4*>(w + c);
+    }
 #pragma unroll
     for (int j = 0; j < NA_MAX_PASSES; ++j) {
         const int c = j * NA_STEP + NA_VEC * tid;
@@ -68,7 +74,7 @@ __global__ __launch_bounds__(NA_THREADS) void add_rms_norm_kernel(
         const int c = j * NA_STEP + NA_VEC * tid;
         if (j < passes && c < D) {
             float wv[NA_VEC], y[NA_VEC];
-            unpack8(*reinterpret_cast<const uint4*>(w + c), wv);
+            unpack8(wraw[j], wv);
 #pragma unroll
             for (int i = 0; i < NA_VEC; ++i) y[i] = (r[j][i] * rstd) * wv[i];
             *reinterpret_cast<uint4*>(normed + t * ns + c) = pack8(y);
