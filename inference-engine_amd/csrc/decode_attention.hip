@@ -3,9 +3,11 @@
 // Work split (same rule as qwen3-1.7b/kernels.py:20-70): every decoding sequence's tokens
 // [0, cached_len + 1) are cut into pieces of `piece` tokens, piece = roundup(max(MIN_PIECE,
 // cdiv(total_tokens, TARGET)), MIN_PIECE) with TARGET = CUs * WG_PER_CU / Hkv workgroups per KV
-// head. The pieces of all sequences form one work list; workgroup (w, kv head) takes entry w.
-// The grid is (TARGET + B, Hkv): it depends on shapes only, so the launch is graph-capturable,
-// and each workgroup finds its (sequence, piece) on the device from cached_lens.
+// head (when B <= TARGET the piece is grown until the pieces fit TARGET, see decode_piece). The
+// pieces of all sequences form one work list; workgroup (w, kv head) takes entry w. The grid is
+// (TARGET, Hkv) when B <= TARGET, else (TARGET + B, Hkv): it depends on shapes only, so the
+// launch is graph-capturable, and each workgroup finds its (sequence, piece) on the device from
+// cached_lens.
 //
 // One workgroup = 8 waves = one (sequence, piece, kv head), i.e. both query heads of the GQA
 // pair. Lane (g, c) of a wave (g = lane / 8, c = lane % 8) owns channels [16c, 16c+16) of the
@@ -561,7 +563,10 @@ extern "C" hipError_t ie_decode_attention_split(
     a.target = L.target;
     a.max_splits = L.max_splits;
     a.hq = num_q_heads;
-    dim3 grid(L.target + batch, (unsigned)cache->num_kv_heads);
+    // pieces number at most target + nd, and at most target when nd <= target (decode_piece):
+    // with batch <= target the grid needs no spare workgroups, which would otherwise hold
+    // resident slots while they find out that they are idle
+    dim3 grid(batch <= L.target ? L.target : L.target + batch, (unsigned)cache->num_kv_heads);
     hipLaunchKernelGGL(decode_split_kernel, grid, dim3(DA_THREADS), 0, stream, a);
     return hipGetLastError();
 }
