@@ -299,7 +299,7 @@ __device__ Loc schedule(const PrefillArgs& a, int target, int* tables) {
         const unsigned long long hit = __ballot(target < incl && target >= incl - items);
         if (hit) {
             const int src = __builtin_ctzll(hit);  // the same lane in every wave: uniform
-            auto from = [&](int x) { return uni(__shfl(x, src, IE_WAVE)); };
+            auto from = [&](int x) { return __builtin_amdgcn_readlane(x, src); };
             L.sb = from(sb_of(c));
             L.item_base = from(incl - items);
             L.off = target - L.item_base;
@@ -308,8 +308,8 @@ __device__ Loc schedule(const PrefillArgs& a, int target, int* tables) {
                            from(z.slot), DT);
             L.found = 1;
         }
-        items_before = uni(__shfl(incl, 63, IE_WAVE));
-        split_before = uni(__shfl(sincl, 63, IE_WAVE));
+        items_before = __builtin_amdgcn_readlane(incl, 63);
+        split_before = __builtin_amdgcn_readlane(sincl, 63);
         return L.found != 0;
     };
 #pragma unroll
@@ -977,13 +977,13 @@ __global__ __launch_bounds__(PF_THREADS) void prefill_combine_kernel(PrefillArgs
     // the split count and the first unit's record in one memory round trip (records exist for
     // k < nsb; the count decides which of them are this launch's)
     const int k0 = u0 / per_k;
-    int4 rec0 = {0, 0, 0, 0};
-    if (k0 < a.nsb) rec0 = *reinterpret_cast<const int4*>(a.sched + 4 + 4 * k0);
+    int4 rec = {0, 0, 0, 0};  // the record of unit u's split sub-block
+    if (k0 < a.nsb) rec = *reinterpret_cast<const int4*>(a.sched + 4 + 4 * k0);
     const int nsplit = uni(a.sched[1]);
     const int units = nsplit * per_k;
     for (int u = u0; u < units; u += ustep) {
         const int k = u / per_k, hr = (u % per_k) / PF_COMB_GROUPS, grp = u % PF_COMB_GROUPS;
-        const int4 rec = u == u0 ? rec0 : *reinterpret_cast<const int4*>(a.sched + 4 + 4 * k);
+        if (u != u0) rec = *reinterpret_cast<const int4*>(a.sched + 4 + 4 * k);
         const int item_base = uni(rec.x);
         const int hk = by_xcd ? 8 * hr + (((int)(blockIdx.x & 7) - item_base) & 7) : hr;
         SubBlock s;
