@@ -84,8 +84,10 @@ __device__ __forceinline__ uint32_t hi16pair(float lo, float hi) {
 }
 
 // The workgroup's LDS: two K and two V^T tile buffers and three K-scale slots. Before the tile
-// loop the second V^T buffer holds the schedule's entry tables (cu_seqlens, cu_cached and
-// slot_ids of up to PF_MAX_ENTRIES entries). 79,360 bytes: two workgroups fit a CU's 160 KB.
+// loop the second K buffer holds the schedule's entry tables (cu_seqlens, cu_cached and
+// slot_ids of up to PF_MAX_ENTRIES entries): no wave writes it before the first barrier of the
+// item, which every wave reaches only after its schedule. 79,360 bytes: two workgroups fit a
+// CU's 160 KB.
 struct PfLds {
     uint8_t k[2][PF_BN * KS_STRIDE];
     uint8_t vt[2][PF_D * VT_STRIDE];
@@ -191,11 +193,12 @@ struct Loc {
     SubBlock s;       // sub-block sb
 };
 
-// One wave's pass over the tile metadata (every lane of the wave returns the same Loc). Only
-// one wave of the workgroup may call it (it owns the entry tables in LDS, `tables`).
+// One wave's pass over the tile metadata (every lane of the wave returns the same Loc). Every
+// wave of the workgroup runs it: each writes the same values into the entry tables in LDS
+// (`tables`) before reading them, so no wave waits for another.
 __device__ Loc schedule(const PrefillArgs& a, int target, int* tables) {
-    static_assert((3 * PF_MAX_ENTRIES + 2) * sizeof(int) <= sizeof(PfLds::vt[1]),
-                  "entry tables must fit one V^T buffer");
+    static_assert((3 * PF_MAX_ENTRIES + 2) * sizeof(int) <= sizeof(PfLds::k[1]),
+                  "entry tables must fit one K buffer");
     int* s_cu = tables;
     int* s_cc = tables + PF_MAX_ENTRIES + 1;
     int* s_sl = tables + 2 * (PF_MAX_ENTRIES + 1);
@@ -930,20 +933,13 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBloc
 // list (there are never more items than that), or nothing.
 __global__ __launch_bounds__(PF_THREADS, IE_PREFILL_WG_PER_CU) void prefill_attention_kernel(
     PrefillArgs a) {
-    // wave 0 reads the tile metadata and hands the workgroup its item through LDS
-    __shared__ Loc s_loc;
+    // every wave reads the tile metadata and derives the workgroup's item itself
     __shared__ __attribute__((aligned(16))) PfLds lds;
-    if (threadIdx.x < IE_WAVE) {
-        const Loc l = schedule(a, blockIdx.x, reinterpret_cast<int*>(lds.vt[1]));
-        if (threadIdx.x == 0) s_loc = l;
-    }
-    __syncthreads();
-    Loc loc;
+    Loc loc = schedule(a, blockIdx.x, reinterpret_cast<int*>(lds.k[1]));
     {
-        const int* src = reinterpret_cast<const int*>(&s_loc);
-        int* dst = reinterpret_cast<int*>(&loc);
+        int* f = reinterpret_cast<int*>(&loc);
 #pragma unroll
-        for (int i = 0; i < (int)(sizeof(Loc) / sizeof(int)); ++i) dst[i] = uni(src[i]);
+        for (int i = 0; i < (int)(sizeof(Loc) / sizeof(int)); ++i) f[i] = uni(f[i]);
     }
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         a.sched[0] = loc.T;
