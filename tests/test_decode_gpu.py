@@ -35,6 +35,11 @@ def test_decode_configs(ie, workloads, dev, cfg):
 @pytest.mark.parametrize("ctx", [
     [1], [2, 1, 3], [5, 127, 128, 129, 255, 256, 257], [33000], [64] * 40 + [9000],
     list(range(1, 300, 7)),
+    # batches at and just under the per-head workgroup target (64 on 256 CUs), where the grid
+    # has no spare workgroups and the fitted piece must keep every piece inside it
+    [int(x) for x in np.random.default_rng(7).integers(1, 3000, 64)],
+    [int(x) for x in np.random.default_rng(8).integers(100, 5000, 63)],
+    [4096] * 63 + [1],
 ])
 def test_decode_ragged(ie, workloads, dev, ctx):
     say(f"decode ragged B={len(ctx)} max ctx {max(ctx)}")
