@@ -295,6 +295,21 @@ hipError_t ie_skinny_gemm(const ie_bf16* x, int64_t x_stride, int32_t m, const i
                           int64_t weight_stride, int32_t n, int32_t k, int32_t n_tiles, ie_bf16* y,
                           int64_t y_stride, hipStream_t stream);
 
+/*
+ * y = silu_mul(x . weight^T) in one launch: the MLP's gate/up projection followed by the
+ * SiLU-gated product, i.e. qwen3-1.7b/kernels.py:1451-1458 `linear(x, w_gate_up)` then
+ * kernels.py:1178-1213 `silu_mul` (called in sequence at architecture.py:282-300). weight: bf16
+ * [n, k], the n / 2 gate rows then the n / 2 up rows; y: bf16 [m, n / 2] =
+ * bf16((g * (1 / (1 + e^-g))) * u) with g, u the bf16-rounded products, as the two-step path
+ * computes them (the products' fp32 summation order may differ from ie_skinny_gemm's, within
+ * its tolerance). n_tiles (1 or 2): gate (and up) rows per workgroup / 16, lowered to 1 where m
+ * leaves too little LDS. n / 2 a multiple of 16 n_tiles, k of 256; m <= 64.
+ */
+hipError_t ie_skinny_gemm_silu_mul(const ie_bf16* x, int64_t x_stride, int32_t m,
+                                   const ie_bf16* weight, int64_t weight_stride, int32_t n,
+                                   int32_t k, int32_t n_tiles, ie_bf16* y, int64_t y_stride,
+                                   hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

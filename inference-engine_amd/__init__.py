@@ -21,6 +21,8 @@ from .kernels import (  # noqa: F401
     sample,
     silu_mul,
     skinny_matmul,
+    skinny_matmul_silu_mul,
     linear,
+    linear_silu_mul,
     tune_linear,
 )

@@ -32,11 +32,17 @@ constexpr int SG_BK = 64;      // k per batch: 128 bytes of a row, one 8-lane lo
 constexpr int SG_LROW = 160;   // LDS row stride (bytes)
 constexpr int SG_MAX_TILES = 6;  // NT + MT, at most (LDS: 8 waves x 16 (NT + MT) rows x 160 B)
 
-template <int NT, int MT>
+// Launch modes: plain n-tiles of 16 rows; one n-tile of 8 rows (HALF); GLU, the gate/up
+// projection with the SiLU-gated product fused: n-tile t pairs gate rows [16 NT t, +16 NT) with
+// the up rows nh further (the weight is [gate; up], 2 nh rows) and the workgroup writes
+// bf16(silu(g) * u) from the bf16-rounded g and u, as silu_mul does with the GEMM's output.
+enum : int { SG_PLAIN = 0, SG_HALF = 1, SG_GLU = 2 };
+
+template <int WT, int MT, int PT>
 struct SgLds {
     union {
-        uint8_t t[SG_WAVES][16 * (NT + MT) * SG_LROW];  // per-wave transpose regions
-        sg_f32x4 acc[SG_WAVES][NT * MT][IE_WAVE];       // partial D tiles (after the loop)
+        uint8_t t[SG_WAVES][16 * (WT + MT) * SG_LROW];  // per-wave transpose regions
+        sg_f32x4 acc[SG_WAVES][PT * MT][IE_WAVE];       // partial D tiles (after the loop)
     };
 };
 
@@ -44,14 +50,17 @@ struct SgLds {
 // fragment feeds NT MFMAs), or with HALF one n-tile of 8 rows (NT = 1: twice the workgroups for
 // narrow weights; the MFMA's other 8 rows compute outputs that are not stored). K a multiple of
 // 8 * 32 = 256 (each wave's slice is a multiple of 32).
-template <int MT, int NT, bool HALF>
+template <int MT, int NT, int MODE>
 __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
     const uint16_t* __restrict__ x, int64_t xs, int M, const uint16_t* __restrict__ w, int64_t ws,
-    int K, uint16_t* __restrict__ y, int64_t ys) {
-    static_assert(NT + MT <= SG_MAX_TILES, "LDS transpose region too large");
+    int K, uint16_t* __restrict__ y, int64_t ys, int nh) {
+    constexpr bool HALF = MODE == SG_HALF, GLU = MODE == SG_GLU;
+    constexpr int WT = GLU ? 2 * NT : NT;  // weight tiles: NT (GLU: NT gate, then NT up tiles)
+    static_assert(WT + MT <= SG_MAX_TILES, "LDS transpose region too large");
     static_assert(!HALF || NT == 1, "8-row n-tiles come one per workgroup");
-    constexpr int WROWS = HALF ? 8 : 16 * NT;  // weight rows per workgroup
-    constexpr int TILES = NT + MT;  // W tiles 0..NT-1, then x tiles
+    static_assert(!GLU || NT * MT <= SG_WAVES, "GLU: at most one output tile per wave");
+    constexpr int WROWS = HALF ? 8 : 16 * NT;  // weight rows per workgroup (per half in GLU)
+    constexpr int TILES = WT + MT;  // W tiles 0..WT-1, then x tiles
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l16 = lane & 15, g = lane >> 4;
@@ -60,8 +69,10 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
     // wave w of workgroup b takes K slice (w + b) mod 8: neighbouring workgroups read different
     // parts of x at any moment instead of all hitting the same L2 lines
     const int kw = K / SG_WAVES, k_begin = (int)((wave + blockIdx.x) % SG_WAVES) * kw;
-    // W rows [n0, n0 + 16 NT) and x rows [0, M): the buffer ranges zero the rows of x past M
+    // W rows [n0, n0 + WROWS) (GLU: and the up rows [nh + n0, +WROWS)) and x rows [0, M): the
+    // buffer ranges zero the rows of x past M
     const rsrc_t rw = make_rsrc(w + (int64_t)n0 * ws, (uint32_t)(WROWS * ws * 2));
+    const rsrc_t ru = make_rsrc(w + ((int64_t)nh + n0) * ws, (uint32_t)(GLU ? WROWS * ws * 2 : 0));
     const rsrc_t rx = make_rsrc(x, (uint32_t)(M * xs * 2));
     // byte offsets of this lane's two 8-row halves of every tile at the slice start
     int loff[TILES][2];
@@ -69,18 +80,18 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
     for (int i = 0; i < TILES; ++i)
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            const int row = 16 * (i < NT ? i : i - NT) + 8 * h + lr;
-            loff[i][h] = (row * (int)(i < NT ? ws : xs) + k_begin + 8 * lc) * 2;
+            const int row = 16 * (i < WT ? i % NT : i - WT) + 8 * h + lr;
+            loff[i][h] = (row * (int)(i < WT ? ws : xs) + k_begin + 8 * lc) * 2;
         }
 
-    __shared__ __attribute__((aligned(16))) SgLds<NT, MT> lds;
+    __shared__ __attribute__((aligned(16))) SgLds<WT, MT, NT> lds;
     uint8_t* reg = lds.t[wave];
     uint8_t* wdst = reg + lr * SG_LROW + 16 * lc;          // + (16 i + 8 h) rows
     const uint8_t* rsrc = reg + l16 * SG_LROW + 16 * g;   // + 16 i rows + 64 t
 
-    sg_f32x4 acc[NT][MT];
+    sg_f32x4 acc[WT][MT];
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt)
+    for (int nt = 0; nt < WT; ++nt)
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = sg_f32x4{0.f, 0.f, 0.f, 0.f};
 
@@ -94,8 +105,8 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 if (HALF && i < NT && h == 1) continue;
-                r[i][h] = __builtin_amdgcn_raw_buffer_load_b128(i < NT ? rw : rx,
-                                                                in ? loff[i][h] + 128 * b : -1, 0, 0);
+                r[i][h] = __builtin_amdgcn_raw_buffer_load_b128(
+                    i < NT ? rw : (i < WT ? ru : rx), in ? loff[i][h] + 128 * b : -1, 0, 0);
             }
     };
     auto compute = [&](const Batch& r) {
@@ -114,10 +125,10 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
                 f[i] = __builtin_bit_cast(
                     sg_bf16x8, *reinterpret_cast<const sg_u32x4*>(rsrc + 16 * i * SG_LROW + 64 * t));
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt)
+            for (int nt = 0; nt < WT; ++nt)
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt)
-                    acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f[nt], f[NT + mt],
+                    acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f[nt], f[WT + mt],
                                                                          acc[nt][mt], 0, 0, 0);
         }
     };
@@ -137,23 +148,44 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
     }
 
     // D lane (l16, g) element i: n = n0 + 16 nt + 4g + i, m = 16 mt + l16. The waves' partial
-    // tiles are summed in wave order, one (nt, mt) tile per wave.
-    __syncthreads();  // every wave is done with its transpose region (the partial tiles alias it)
+    // tiles are summed in wave order, one (nt, mt) tile per wave; in GLU the gate tiles go
+    // through LDS first and the up tiles second, and the wave holding gate tile (nt, mt) keeps
+    // its bf16-rounded values for the product with up tile (nt, mt) of the second round.
+    float gate[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt)
+    for (int round = 0; round < (GLU ? 2 : 1); ++round) {
+        __syncthreads();  // every wave is done with its transpose region / the previous round
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) lds.acc[wave][nt * MT + mt][lane] = acc[nt][mt];
-    __syncthreads();
-    for (int tile = wave; tile < NT * MT; tile += SG_WAVES) {
-        sg_f32x4 t = lds.acc[0][tile][lane];
+        for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-        for (int v = 1; v < SG_WAVES; ++v) t += lds.acc[v][tile][lane];
-        const int nt = tile / MT, mt = tile % MT;
-        const int m = 16 * mt + l16;
-        if (m < M && (!HALF || g < 2)) {
-            uint16_t* dst = y + (int64_t)m * ys + n0 + 16 * nt + 4 * g;
-            *reinterpret_cast<uint2*>(dst) =
-                make_uint2(pack_bf16x2(t[0], t[1]), pack_bf16x2(t[2], t[3]));
+            for (int mt = 0; mt < MT; ++mt)
+                lds.acc[wave][nt * MT + mt][lane] = acc[round * NT + nt][mt];
+        __syncthreads();
+        for (int tile = wave; tile < NT * MT; tile += SG_WAVES) {
+            sg_f32x4 t = lds.acc[0][tile][lane];
+#pragma unroll
+            for (int v = 1; v < SG_WAVES; ++v) t += lds.acc[v][tile][lane];
+            const int nt = tile / MT, mt = tile % MT;
+            const int m = 16 * mt + l16;
+            if (GLU) {
+#pragma clang fp contract(off)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float v = bf16_to_f32(f32_to_bf16_rne(t[i]));
+                    if (round == 0) {
+                        gate[i] = v;
+                    } else {  // silu_mul's arithmetic: (g * (1 / (1 + e^-g))) * u
+                        const float sg = 1.0f / (1.0f + expf(-gate[i]));
+                        t[i] = (gate[i] * sg) * v;
+                    }
+                }
+                if (round == 0) continue;
+            }
+            if (m < M && (!HALF || g < 2)) {
+                uint16_t* dst = y + (int64_t)m * ys + n0 + 16 * nt + 4 * g;
+                *reinterpret_cast<uint2*>(dst) =
+                    make_uint2(pack_bf16x2(t[0], t[1]), pack_bf16x2(t[2], t[3]));
+            }
         }
     }
 }
@@ -162,12 +194,10 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
 
 using namespace ie;
 
-extern "C" hipError_t ie_skinny_gemm(const ie_bf16* x, int64_t x_stride, int32_t m,
-                                     const ie_bf16* weight, int64_t weight_stride, int32_t n,
-                                     int32_t k, int32_t n_tiles, ie_bf16* y, int64_t y_stride,
-                                     hipStream_t stream) {
-    IE_REQUIRE(m >= 0 && n >= 0 && k >= 0, "negative sizes");
-    if (m == 0 || n == 0) return hipSuccess;
+// Shared argument checks of the two entry points (n: weight rows).
+static hipError_t skinny_check(const ie_bf16* x, int64_t x_stride, int32_t m, const ie_bf16* weight,
+                               int64_t weight_stride, int32_t n, int32_t k, int32_t n_tiles,
+                               const ie_bf16* y, int64_t y_stride) {
     IE_REQUIRE(x && weight && y, "null pointer");
     IE_REQUIRE(m <= 64, "at most 64 rows");
     IE_REQUIRE(n % 16 == 0 && k % (SG_WAVES * 32) == 0 && k > 0,
@@ -183,31 +213,40 @@ extern "C" hipError_t ie_skinny_gemm(const ie_bf16* x, int64_t x_stride, int32_t
     IE_REQUIRE((int64_t)m * x_stride * 2 < (1LL << 31) &&
                    16LL * std::max(1, n_tiles) * weight_stride * 2 < (1LL << 31),
                "operands too large for 32-bit buffer offsets");
-    const int mt = (m + 15) / 16;
+    return hipSuccess;
+}
+
+#define IE_SG_ARGS                                                                          \
+    (const uint16_t*)x, x_stride, m, (const uint16_t*)weight, weight_stride, k, (uint16_t*)y, \
+        y_stride, nh
+
+extern "C" hipError_t ie_skinny_gemm(const ie_bf16* x, int64_t x_stride, int32_t m,
+                                     const ie_bf16* weight, int64_t weight_stride, int32_t n,
+                                     int32_t k, int32_t n_tiles, ie_bf16* y, int64_t y_stride,
+                                     hipStream_t stream) {
+    IE_REQUIRE(m >= 0 && n >= 0 && k >= 0, "negative sizes");
+    if (m == 0 || n == 0) return hipSuccess;
+    hipError_t e = skinny_check(x, x_stride, m, weight, weight_stride, n, k, n_tiles, y, y_stride);
+    if (e != hipSuccess) return e;
+    const int mt = (m + 15) / 16, nh = 0;
     // n_tiles is a performance choice: it is lowered until the LDS transpose region fits
     while (n_tiles > 1 && n_tiles + mt > SG_MAX_TILES) n_tiles >>= 1;
     const bool half = n_tiles == 0;
     const dim3 grid((unsigned)(half ? n / 8 : n / (16 * n_tiles)));
-#define IE_SG_LAUNCH(MT, NT)                                                                   \
-    hipLaunchKernelGGL((skinny_gemm_kernel<MT, NT, false>), grid, dim3(SG_THREADS), 0, stream, \
-                       (const uint16_t*)x, x_stride, m, (const uint16_t*)weight, weight_stride, \
-                       k, (uint16_t*)y, y_stride)
-#define IE_SG_LAUNCH_HALF(MT)                                                                   \
-    hipLaunchKernelGGL((skinny_gemm_kernel<MT, 1, true>), grid, dim3(SG_THREADS), 0, stream,     \
-                       (const uint16_t*)x, x_stride, m, (const uint16_t*)weight, weight_stride,  \
-                       k, (uint16_t*)y, y_stride)
-#define IE_SG_NT4(MT)                                \
-    switch (n_tiles) {                               \
-        case 0: IE_SG_LAUNCH_HALF(MT); break;        \
-        case 1: IE_SG_LAUNCH(MT, 1); break;          \
-        case 2: IE_SG_LAUNCH(MT, 2); break;          \
-        default: IE_SG_LAUNCH(MT, 4); break;         \
+#define IE_SG_LAUNCH(MT, NT, MODE) \
+    hipLaunchKernelGGL((skinny_gemm_kernel<MT, NT, MODE>), grid, dim3(SG_THREADS), 0, stream, IE_SG_ARGS)
+#define IE_SG_NT4(MT)                                   \
+    switch (n_tiles) {                                  \
+        case 0: IE_SG_LAUNCH(MT, 1, SG_HALF); break;    \
+        case 1: IE_SG_LAUNCH(MT, 1, SG_PLAIN); break;   \
+        case 2: IE_SG_LAUNCH(MT, 2, SG_PLAIN); break;   \
+        default: IE_SG_LAUNCH(MT, 4, SG_PLAIN); break;  \
     }
-#define IE_SG_NT2(MT)                                \
-    switch (n_tiles) {                               \
-        case 0: IE_SG_LAUNCH_HALF(MT); break;        \
-        case 1: IE_SG_LAUNCH(MT, 1); break;          \
-        default: IE_SG_LAUNCH(MT, 2); break;         \
+#define IE_SG_NT2(MT)                                   \
+    switch (n_tiles) {                                  \
+        case 0: IE_SG_LAUNCH(MT, 1, SG_HALF); break;    \
+        case 1: IE_SG_LAUNCH(MT, 1, SG_PLAIN); break;   \
+        default: IE_SG_LAUNCH(MT, 2, SG_PLAIN); break;  \
     }
     switch (mt) {  // (MT, NT) pairs within SG_MAX_TILES
         case 1: IE_SG_NT4(1); break;
@@ -217,7 +256,31 @@ extern "C" hipError_t ie_skinny_gemm(const ie_bf16* x, int64_t x_stride, int32_t
     }
 #undef IE_SG_NT4
 #undef IE_SG_NT2
-#undef IE_SG_LAUNCH_HALF
+    return hipGetLastError();
+}
+
+extern "C" hipError_t ie_skinny_gemm_silu_mul(const ie_bf16* x, int64_t x_stride, int32_t m,
+                                              const ie_bf16* weight, int64_t weight_stride,
+                                              int32_t n, int32_t k, int32_t n_tiles, ie_bf16* y,
+                                              int64_t y_stride, hipStream_t stream) {
+    IE_REQUIRE(m >= 0 && n >= 0 && k >= 0, "negative sizes");
+    if (m == 0 || n == 0) return hipSuccess;
+    IE_REQUIRE(n_tiles == 1 || n_tiles == 2, "n_tiles must be 1 or 2");
+    IE_REQUIRE(n % 2 == 0 && (n / 2) % (16 * n_tiles) == 0,
+               "n must be even and n / 2 a multiple of 16 n_tiles");
+    hipError_t e = skinny_check(x, x_stride, m, weight, weight_stride, n, k, n_tiles, y, y_stride);
+    if (e != hipSuccess) return e;
+    const int mt = (m + 15) / 16, nh = n / 2;
+    // gate and up tiles: lowered to one n-tile where m leaves too little LDS for two
+    if (2 * n_tiles + mt > SG_MAX_TILES) n_tiles = 1;
+    const dim3 grid((unsigned)(nh / (16 * n_tiles)));
+    switch (mt) {
+        case 1: if (n_tiles == 2) IE_SG_LAUNCH(1, 2, SG_GLU); else IE_SG_LAUNCH(1, 1, SG_GLU); break;
+        case 2: if (n_tiles == 2) IE_SG_LAUNCH(2, 2, SG_GLU); else IE_SG_LAUNCH(2, 1, SG_GLU); break;
+        case 3: IE_SG_LAUNCH(3, 1, SG_GLU); break;
+        default: IE_SG_LAUNCH(4, 1, SG_GLU); break;
+    }
 #undef IE_SG_LAUNCH
     return hipGetLastError();
 }
+#undef IE_SG_ARGS

@@ -240,6 +240,21 @@ at::Tensor skinny_matmul(const at::Tensor& x, const at::Tensor& weight, int64_t 
     return y;
 }
 
+at::Tensor skinny_matmul_silu_mul(const at::Tensor& x, const at::Tensor& weight, int64_t n_tiles) {
+    check_bf16_rows(x, "x", 2);
+    check_bf16_rows(weight, "weight", 2);
+    const c10::DeviceGuard guard(x.device());
+    const int64_t M = x.size(0), K = x.size(1), N = weight.size(0);
+    TORCH_CHECK(weight.size(1) == K, "ie: weight must be [N, K]");
+    TORCH_CHECK(N % 2 == 0, "ie: weight must hold the gate rows then the up rows");
+    at::Tensor y = at::empty({M, N / 2}, x.options());
+    ok(ie_skinny_gemm_silu_mul(bf(x), x.stride(0), (int32_t)M, bf(weight), weight.stride(0),
+                               (int32_t)N, (int32_t)K, (int32_t)n_tiles, bfm(y), y.stride(0),
+                               stream_of(x)),
+       "skinny_matmul_silu_mul");
+    return y;
+}
+
 struct DecodeCall {
     ie_kv_cache c;
     int32_t B, hq;
@@ -394,6 +409,7 @@ TORCH_LIBRARY(ie, m) {
     m.def("add_rms_norm(Tensor residual, Tensor delta, Tensor weight, float eps) -> (Tensor, Tensor)");
     m.def("silu_mul(Tensor gate_up) -> Tensor");
     m.def("skinny_matmul(Tensor x, Tensor weight, int n_tiles=1) -> Tensor");
+    m.def("skinny_matmul_silu_mul(Tensor x, Tensor weight, int n_tiles=1) -> Tensor");
     m.def(
         "decode_attention(Tensor q, Tensor k_cache, Tensor v_cache, Tensor k_scale, "
         "Tensor v_scale, Tensor k_calibration, Tensor cached_lens, Tensor slot_ids, "
@@ -425,6 +441,7 @@ TORCH_LIBRARY_IMPL(ie, CUDA, m) {
     m.impl("add_rms_norm", &add_rms_norm);
     m.impl("silu_mul", &silu_mul);
     m.impl("skinny_matmul", &skinny_matmul);
+    m.impl("skinny_matmul_silu_mul", &skinny_matmul_silu_mul);
     m.impl("decode_attention", &decode_attention);
     m.impl("decode_attention_split", &decode_attention_split);
     m.impl("decode_attention_combine", &decode_attention_combine);

@@ -5,7 +5,8 @@ Mirrors the decode branch of the reference's model (qwen3-1.7b/architecture.py:9
 TransformerBlock.forward :262-304 and Qwen3Model.forward :395-413) and its graph capture and
 replay (qwen3-1.7b/engine.py:376-470): per layer, `add_rms_norm` (the first layer: RMSNorm),
 QKV projection, `fused_rope_kv_decode` (norm + RoPE + int8 KV write), `decode_attention`,
-output projection, `add_rms_norm`, gate/up projection, `silu_mul`, down projection; then the
+output projection, `add_rms_norm`, gate/up projection and `silu_mul` (one launch,
+`linear_silu_mul`, where the skinny GEMM serves that shape), down projection; then the
 final `add_rms_norm`, the tied-embedding LM head and greedy sampling (`sample` at tau 0,
 kernels.py:1343-1370). All of these are this package's HIP kernels; for each projection
 `linear` (kernels.py:1451-1458) runs this package's skinny GEMM or the library GEMM
@@ -22,7 +23,7 @@ import torch
 import torch.nn.functional as F
 
 from .kernels import (LayerKVCache, add_rms_norm, decode_attention, fused_rope_kv_decode, linear,
-                      make_layer_cache, sample, silu_mul, tune_linear)
+                      linear_silu_mul, make_layer_cache, sample, tune_linear)
 
 
 @dataclass(frozen=True)
@@ -151,7 +152,7 @@ class DecodeStep:
                 residual, normed = add_rms_norm(residual, x, lw.input_norm, eps)
             attn = self.attention(li, normed, cos, sin)
             residual, normed = add_rms_norm(residual, attn, lw.post_norm, eps)
-            x = linear(silu_mul(linear(normed, lw.gate_up)), lw.down)
+            x = linear(linear_silu_mul(normed, lw.gate_up), lw.down)
         _, h = add_rms_norm(residual, x, self.final_norm, eps)
         logits = linear(h, self.embed)
         return sample(logits, 0.0, self.seed)

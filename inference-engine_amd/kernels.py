@@ -218,6 +218,26 @@ def skinny_matmul(x: torch.Tensor, weight: torch.Tensor, n_tiles: int = 1) -> to
 use_skinny: dict = {}
 
 
+def skinny_matmul_silu_mul(x: torch.Tensor, weight: torch.Tensor, n_tiles: int = 1) -> torch.Tensor:
+    """silu_mul(skinny_matmul(x, weight)) in one launch (qwen3-1.7b/kernels.py:1451-1458 then
+    :1178-1213): weight [2D, K] holds the gate rows then the up rows, result [M, D]."""
+    M, K = x.shape
+    N = weight.shape[0]
+    assert x.stride(-1) == 1 and weight.stride(-1) == 1
+    assert M <= 64 and N % 2 == 0 and n_tiles in (1, 2)
+    assert (N // 2) % (16 * n_tiles) == 0 and K % 256 == 0
+    return ops().skinny_matmul_silu_mul(x, weight, int(n_tiles))
+
+
+def linear_silu_mul(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """silu_mul(linear(x, weight)): the fused launch wherever tune_linear chose the skinny GEMM
+    for this weight shape and row count, else the library GEMM then silu_mul."""
+    nt = use_skinny.get((weight.shape[0], weight.shape[1], x.shape[0]))
+    if nt is not None and weight.shape[0] % 64 == 0:
+        return skinny_matmul_silu_mul(x, weight, 2 if nt in (2, 4) else 1)
+    return silu_mul(torch.nn.functional.linear(x, weight))
+
+
 def linear(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     """qwen3-1.7b/kernels.py:1451-1458: [M, K] @ [N, K].T -> [M, N], with whichever measured
     faster."""

@@ -23,7 +23,8 @@ def test_torch_ops_registered(ie):
     for name in ["quantize_kv_prefill", "fused_rope_kv_decode", "fused_norm_rope_prefill",
                  "decode_attention",
                  "decode_attention_split", "decode_attention_combine", "dequantize_kv_prefix",
-                 "prefill_attention", "decode_attention_workspace_size", "sample", "add_rms_norm", "silu_mul", "skinny_matmul"]:
+                 "prefill_attention", "decode_attention_workspace_size", "sample", "add_rms_norm",
+                 "silu_mul", "skinny_matmul", "skinny_matmul_silu_mul"]:
         assert hasattr(ops, name), name
 
 

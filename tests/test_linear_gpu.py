@@ -59,3 +59,46 @@ def test_linear_follows_tuning_table(ie, dev):
         x = torch.randn(M, 2048, generator=g).bfloat16().to(dev)
         _check(K.linear(x, w), x, w, f"linear M={M}")
     K.use_skinny.clear()
+
+
+def _check_glu(y, x, w, what):
+    D = w.shape[0] // 2
+    gu = x.float() @ w.float().T
+    g, u = gu[:, :D].bfloat16().float(), gu[:, D:].bfloat16().float()
+    ref = (g * torch.sigmoid(g)) * u
+    # one bf16 rounding of the product, plus the bf16 roundings of g and u when the fp32 sums
+    # land on the other side of a rounding boundary
+    err = (y.float() - ref).abs()
+    bound = ref.abs() * 2 ** -7 + 2e-3 * ref.abs().max()
+    assert torch.all(err <= bound), f"{what}: max err {err.max().item():.3e}"
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("N,K", [(12288, 2048), (1024, 512)])
+@pytest.mark.parametrize("M", [1, 17, 32, 64])
+def test_skinny_matmul_silu_mul(ie, dev, N, K, M):
+    g = torch.Generator().manual_seed(N + K + M + 1)
+    w = (0.02 * torch.randn(N, K, generator=g)).bfloat16().to(dev)
+    x = torch.randn(M, K, generator=g).bfloat16().to(dev)
+    for nt in (1, 2):
+        y = ie.skinny_matmul_silu_mul(x, w, nt)
+        torch.cuda.synchronize()
+        assert y.shape == (M, N // 2) and y.dtype == torch.bfloat16
+        _check_glu(y, x, w, f"fused N={N} K={K} M={M} n_tiles={nt}")
+        # the two-launch path it replaces
+        two = ie.silu_mul(ie.skinny_matmul(x, w, nt))
+        torch.cuda.synchronize()
+        _check_glu(two, x, w, f"two-step N={N} K={K} M={M}")
+    say(f"skinny_matmul_silu_mul N={N} K={K} M={M}: ok")
+
+
+@pytest.mark.gpu
+def test_linear_silu_mul_follows_tuning_table(ie, dev):
+    g = torch.Generator().manual_seed(4)
+    w = (0.02 * torch.randn(1024, 512, generator=g)).bfloat16().to(dev)
+    x = torch.randn(8, 512, generator=g).bfloat16().to(dev)
+    K = ie.kernels
+    for choice in (None, 1, 4):  # library, then the fused skinny launch
+        K.use_skinny[(1024, 512, 8)] = choice
+        _check_glu(K.linear_silu_mul(x, w), x, w, f"linear_silu_mul table={choice}")
+    K.use_skinny.pop((1024, 512, 8))
