@@ -17,7 +17,8 @@
 // region (rows of 160 bytes: both the row-wise stores and the fragment reads are free of bank
 // conflicts) and reads the MFMA fragments back. Batch b + 1 is loaded into registers while
 // batch b goes through LDS and the MFMAs. The eight partial D tiles are summed through LDS in
-// wave order and written as bf16.
+// wave order and written as bf16. Launch modes below: 8-row n-tiles for narrow weights, and the
+// gate/up projection with the SiLU-gated product fused (ie_skinny_gemm_silu_mul).
 #include "ie_common.h"
 
 namespace ie {
@@ -30,7 +31,7 @@ constexpr int SG_WAVES = 8;
 constexpr int SG_THREADS = SG_WAVES * IE_WAVE;
 constexpr int SG_BK = 64;      // k per batch: 128 bytes of a row, one 8-lane load group
 constexpr int SG_LROW = 160;   // LDS row stride (bytes)
-constexpr int SG_MAX_TILES = 6;  // NT + MT, at most (LDS: 8 waves x 16 (NT + MT) rows x 160 B)
+constexpr int SG_MAX_TILES = 6;  // weight + x tiles, at most (LDS: 8 waves x 16 tiles' rows x 160 B)
 
 // Launch modes: plain n-tiles of 16 rows; one n-tile of 8 rows (HALF); GLU, the gate/up
 // projection with the SiLU-gated product fused: n-tile t pairs gate rows [16 NT t, +16 NT) with
