@@ -68,9 +68,9 @@ int decode_target(int num_kv_heads) {
 // one resident wave of workgroups that target sizes. When nd <= target the piece is instead the
 // smallest multiple of 128, at least p0, whose pieces number at most target: a binary search,
 // since the count falls as the piece grows and is nd at the longest sequence's length.
-__device__ int decode_piece(const int32_t* __restrict__ cached_lens, int nd, int target) {
+// n0: this lane's n_b of the first 64 sequences (0 past nd).
+__device__ int decode_piece(const int32_t* __restrict__ cached_lens, int nd, int target, int n0) {
     const int lane = threadIdx.x & 63;
-    const int n0 = lane < nd ? cached_lens[lane] + 1 : 0;  // the first 64 sequences stay in registers
     auto n_of = [&](int b0) { return b0 == 0 ? n0 : (b0 + lane < nd ? cached_lens[b0 + lane] + 1 : 0); };
     int total = 0, longest = 0;
     for (int b0 = 0; b0 < nd; b0 += 64) {
@@ -99,14 +99,18 @@ struct Work {
     int b, split, needed, piece;
 };
 
-// Entry `w` of the work list (kernels.py:40-70); needed == 0 for idle workgroups.
-__device__ Work decode_assign(const int32_t* __restrict__ cached_lens, int nd, int w, int target) {
-    Work r{0, 0, 0, decode_piece(cached_lens, nd, target)};
+// Entry `w` of the work list (kernels.py:40-70); needed == 0 for idle workgroups. `raw0`: this
+// lane's cached_lens entry of the first 64 sequences, loaded by the caller bounded by the batch
+// size instead of num_decoding, so that it shares one memory round trip with num_decoding.
+__device__ Work decode_assign(const int32_t* __restrict__ cached_lens, int nd, int w, int target,
+                              int raw0) {
     const int lane = threadIdx.x & 63;
+    const int n0 = lane < nd ? raw0 + 1 : 0;
+    Work r{0, 0, 0, decode_piece(cached_lens, nd, target, n0)};
     int before = 0;
     for (int b0 = 0; b0 < nd; b0 += 64) {
         const int b = b0 + lane;
-        const int s = b < nd ? cdiv_i(cached_lens[b] + 1, r.piece) : 0;
+        const int s = b < nd ? cdiv_i(b0 == 0 ? n0 : cached_lens[b] + 1, r.piece) : 0;
         const int incl = wave_incl_scan_i(s) + before;
         const int excl = incl - s;
         const unsigned long long hit = __ballot(s > 0 && excl <= w && w < incl);
@@ -144,6 +148,7 @@ struct DecodeArgs {
     float* part_l;    // [B, Hq, max_splits]
     int* plan;        // [0]: this step's piece size, for the combine kernel
     int target, max_splits, hq;
+    int batch;        // rows of q / cached_lens (num_decoding[0] <= batch)
 };
 
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
@@ -258,9 +263,11 @@ __device__ __forceinline__ void block_pv(LaneState& st, const float (&s)[DA_U][2
 __global__ __launch_bounds__(DA_THREADS)
 __attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_split_kernel(
     DecodeArgs a) {
+    const int lane0 = threadIdx.x & 63;
+    const int raw0 = lane0 < a.batch ? a.cached_lens[lane0] : 0;  // issued beside num_decoding
     const int nd = a.num_decoding[0];
     const int hk = blockIdx.y;
-    Work wk = decode_assign(a.cached_lens, nd, blockIdx.x, a.target);
+    Work wk = decode_assign(a.cached_lens, nd, blockIdx.x, a.target, raw0);
     if (blockIdx.x == 0 && hk == 0 && threadIdx.x == 0) a.plan[0] = wk.piece;
     // Wave-uniform by construction; readfirstlane lets the compiler keep them (and the buffer
     // descriptors built from them) in SGPRs.
@@ -563,6 +570,7 @@ extern "C" hipError_t ie_decode_attention_split(
     a.target = L.target;
     a.max_splits = L.max_splits;
     a.hq = num_q_heads;
+    a.batch = batch;
     // pieces number at most target + nd, and at most target when nd <= target (decode_piece):
     // with batch <= target the grid needs no spare workgroups, which would otherwise hold
     // resident slots while they find out that they are idle
