@@ -240,8 +240,7 @@ __global__ __launch_bounds__(256) void fused_rope_kv_decode_kernel(
     const int32_t* __restrict__ num_decoding, int hq, int ratio, float eps, ie_kv_cache c,
     uint16_t* __restrict__ out, int64_t o_sb, int64_t o_sh) {
 #pragma clang fp contract(off)
-    const int b = blockIdx.x;
-    if (b >= num_decoding[0]) return;
+    const int b = blockIdx.x;  // < batch: every per-sequence load below is in bounds
     const int lane = threadIdx.x & 63;
     const int row = blockIdx.y * 4 + (threadIdx.x >> 6);
     const int hkv = (int)c.num_kv_heads;
@@ -249,17 +248,29 @@ __global__ __launch_bounds__(256) void fused_rope_kv_decode_kernel(
     const bool is_q = row < hq;
     const int j = is_q ? row / ratio : row - hq;  // kv head whose calibration applies
 
+    // Every load that does not depend on another is issued before the first wait: the step's
+    // count, the sequence's slot and length, and the row data (the calibration row, which
+    // needs the slot, is the only second round trip).
+    const int nd = num_decoding[0];
+    const int slot = slot_ids[b];
+    const int64_t col = cached_lens[b];
     const uint16_t* src = is_q ? q + b * q_sb + row * q_sh : k + b * k_sb + j * k_sh;
     const uint16_t* w = is_q ? qw : kw;
-    // RMSNorm (kernels.py:417-419 / :426-428), RoPE with bf16 cos/sin (kernels.py:430-436)
-    float o1, o2;
-    norm_rope_row(bf16_to_f32(src[lane]), bf16_to_f32(src[lane + 64]), bf16_to_f32(w[lane]),
-                  bf16_to_f32(w[lane + 64]), bf16_to_f32(cosp[b * cos_sb + lane]),
-                  bf16_to_f32(sinp[b * sin_sb + lane]), eps, o1, o2);
-
-    const int slot = slot_ids[b];
+    const uint16_t x1 = src[lane], x2 = src[lane + 64], w1 = w[lane], w2 = w[lane + 64];
+    const uint16_t cv = cosp[b * cos_sb + lane], sv = sinp[b * sin_sb + lane];
+    uint16_t vr1 = 0, vr2 = 0;
+    if (!is_q) {
+        const uint16_t* vp = v + b * v_sb + j * v_sh;
+        vr1 = vp[lane];
+        vr2 = vp[lane + 64];
+    }
+    if (b >= nd) return;
     const float* cal = c.k_calibration + slot * c.cal_stride_slot + j * c.cal_stride_head;
     const float c1 = cal[lane], c2 = cal[lane + 64];
+    // RMSNorm (kernels.py:417-419 / :426-428), RoPE with bf16 cos/sin (kernels.py:430-436)
+    float o1, o2;
+    norm_rope_row(bf16_to_f32(x1), bf16_to_f32(x2), bf16_to_f32(w1), bf16_to_f32(w2),
+                  bf16_to_f32(cv), bf16_to_f32(sv), eps, o1, o2);
     if (is_q) {
         // q folded with the channel calibration, stored bf16 (kernels.py:440-447).
         uint16_t* o = out + b * o_sb + row * o_sh;
@@ -268,7 +279,6 @@ __global__ __launch_bounds__(256) void fused_rope_kv_decode_kernel(
         return;
     }
     // K: rope(norm(k)) / cal -> int8 at column cached_len (kernels.py:449-470).
-    const int64_t col = cached_lens[b];
     const int64_t base = slot * c.stride_slot + j * c.stride_head + col * c.stride_tok;
     const int64_t sidx = slot * c.scale_stride_slot + j * c.scale_stride_head + col;
     {
@@ -281,8 +291,7 @@ __global__ __launch_bounds__(256) void fused_rope_kv_decode_kernel(
     }
     // V: int8 with its own scale (kernels.py:472-480).
     {
-        const uint16_t* vp = v + b * v_sb + j * v_sh;
-        const float v1 = bf16_to_f32(vp[lane]), v2 = bf16_to_f32(vp[lane + 64]);
+        const float v1 = bf16_to_f32(vr1), v2 = bf16_to_f32(vr2);
         const float a = wave_max(fmaxf(fabsf(v1), fabsf(v2)));
         const float s = fmaxf(a, 1e-6f) / 127.0f;
         c.v[base + lane] = (int8_t)quant1(v1, s);
