@@ -367,6 +367,20 @@ def main():
                                      "GBps": round(kv_bytes / (kv_ms * 1e-3) / 1e9, 1),
                                      "us_graph": round(kv_gms * 1e3, 3), "bytes": kv_bytes}
         log(f"kv write config4 {kv_ms*1e3:.2f} us")
+        # a long step: a first chunk of 8192 tokens (with its calibration) and 4096 new tokens
+        # after 4096 cached, where the write is bandwidth-bound rather than latency-bound
+        lw = W.mixed_to(W.mixed_workload([], [(8192, 0), (4096, 4096)], seed=1, block_m=128,
+                                         max_len=8192), dev)
+        li = lw.inputs
+        kvl_op = lambda: K.quantize_kv_prefill(lw.k, lw.v, li["cu_seqlens"], li["slot_ids"],
+                                               li["cached_lens"], li["num_decoding"], lw.cache)
+        kvl_ms = time_op(kvl_op, args.steps, args.warmup)
+        kvl_bytes = (8192 + 4096) * 8 * (128 * 2 * 2 + 128 * 2 + 8)
+        extra["kv_write_long"] = {"tokens": 8192 + 4096, "us": round(kvl_ms * 1e3, 3),
+                                  "GBps": round(kvl_bytes / (kvl_ms * 1e-3) / 1e9, 1),
+                                  "bytes": kvl_bytes}
+        log(f"kv write long {kvl_ms*1e3:.2f} us")
+        del lw, li
         flops = W.prefill_flops(mw.chunks)
         try:
             pf_op = lambda: K.prefill_attention(

@@ -1,6 +1,7 @@
 // int8 KV cache writes and reads for gfx950.
 //
 //   quantize_kv_prefill_kernel   prefill quantize-on-write (+ K calibration on a first chunk)
+//   kcal_init/kcal_max_kernel    first-chunk K calibration ahead of it, for long steps
 //   fused_rope_kv_decode_kernel  decode q/k RMSNorm + RoPE, q * calibration, K/V quantize
 //   dequantize_kv_prefix_kernel  int8 prefix -> bf16
 //
@@ -17,6 +18,11 @@ constexpr int QP_THREADS = 256;
 constexpr int QP_ROWS = QP_THREADS / 16;   // token rows per pass of a workgroup
 constexpr int QP_BLOCK = 32;               // chunk rows per workgroup
 constexpr int QP_CAL_BATCH = 32;           // calibration rows in flight per thread
+// Steps of at most this many packed tokens compute a first chunk's calibration inside the
+// quantize launch (every block re-reads the chunk's K: (len / 32) x len x 256 B per KV head);
+// longer steps compute it in two launches of linear cost first.
+constexpr int64_t QP_INLINE_CAL_MAX_TOKENS = 1536;
+constexpr int QP_CAL_BLOCK = 256;  // chunk rows per workgroup of the separate calibration launch
 
 struct Row8 {
     float x[8];
@@ -59,22 +65,20 @@ __device__ __forceinline__ float quantize_row8(const float* x, int32_t* q) {
     return s;
 }
 
-// grid (cdiv(N, 32) + num_entries, Hkv), block 256. The prefilling entries' chunks are cut into
-// blocks of QP_BLOCK rows, numbered entry by entry; workgroup (u, h) quantizes block u for kv
-// head h (kernels.py:786-823), or exits when there are fewer blocks. When cached_len == 0 every
-// block of the entry computes the chunk's calibration (kernels.py:764-780) itself and block 0
-// stores it.
-__global__ __launch_bounds__(QP_THREADS) void quantize_kv_prefill_kernel(
-    const uint16_t* __restrict__ k, int64_t k_st, int64_t k_sh,
-    const uint16_t* __restrict__ v, int64_t v_st, int64_t v_sh,
-    const int32_t* __restrict__ cu_seqlens, const int32_t* __restrict__ slot_ids,
-    const int32_t* __restrict__ cached_lens, const int32_t* __restrict__ num_decoding,
-    int num_entries, ie_kv_cache c) {
-#pragma clang fp contract(off)
-    const int h = blockIdx.y, u = blockIdx.x;
-    // Locate block u: every wave scans the entries' block counts (identical result). The
-    // entry's start, length, slot and cached length come from the same (independent) loads, so
-    // the data loads below are the second round trip to memory.
+// The prefilling entries' chunks are cut into blocks of ROWS rows, numbered entry by entry.
+// Block u's entry b (-1 past the last block), its index z within the entry, and the entry's
+// chunk start, length, cache slot and cached length. Every wave scans the entries' block counts
+// (identical result); the entry fields come from the same independent loads, so the data loads
+// that follow are the second round trip to memory.
+struct QpBlock {
+    int b, z, start, len, slot, c0;
+};
+template <int ROWS>
+__device__ __forceinline__ QpBlock qp_locate(int u, const int32_t* __restrict__ cu_seqlens,
+                                             const int32_t* __restrict__ slot_ids,
+                                             const int32_t* __restrict__ cached_lens,
+                                             const int32_t* __restrict__ num_decoding,
+                                             int num_entries) {
     const int lane = threadIdx.x & 63;
     const int nd = __builtin_amdgcn_readfirstlane(num_decoding[0]);
     int b = -1, z = 0, before = 0, start = 0, len = 0, slot = 0, c0 = 0;
@@ -87,7 +91,7 @@ __global__ __launch_bounds__(QP_THREADS) void quantize_kv_prefill_kernel(
             sl = slot_ids[e];
             cl = cached_lens[e];
         }
-        const int nb = e >= nd && e < num_entries ? cdiv_i(s1 - s0, QP_BLOCK) : 0;
+        const int nb = e >= nd && e < num_entries ? cdiv_i(s1 - s0, ROWS) : 0;
         const int incl = wave_incl_scan_i(nb) + before;
         const unsigned long long hit = __ballot(u < incl && u >= incl - nb);
         if (hit) {
@@ -102,9 +106,91 @@ __global__ __launch_bounds__(QP_THREADS) void quantize_kv_prefill_kernel(
         }
         before = __builtin_amdgcn_readfirstlane(__shfl(incl, 63, IE_WAVE));
     }
-    if (b < 0) return;
-    const int t0 = z * QP_BLOCK;
-    const int t1 = min(len, t0 + QP_BLOCK);
+    return QpBlock{b, z, start, len, slot, c0};
+}
+
+// Calibration rows longer than a few blocks are computed ahead of the quantize launch, in
+// linear time: kcal_init_kernel sets the calibration row of every entry with cached_len == 0
+// to the floor 1e-3, then kcal_max_kernel's workgroups (one per block of QP_CAL_BLOCK rows)
+// raise it to their rows' max |k| per channel with atomic max on the float bits (max is exact
+// and order-free, so the result equals the sequential one). Blocks of 256 rows keep the atomics
+// per calibration word few (they serialize at the memory side).
+// grid (num_entries, Hkv), block HEAD_DIM.
+__global__ __launch_bounds__(HEAD_DIM) void kcal_init_kernel(
+    const int32_t* __restrict__ cu_seqlens, const int32_t* __restrict__ slot_ids,
+    const int32_t* __restrict__ cached_lens, const int32_t* __restrict__ num_decoding,
+    ie_kv_cache c) {
+    const int e = blockIdx.x, h = blockIdx.y;
+    if (e < num_decoding[0] || cached_lens[e] != 0 || cu_seqlens[e + 1] == cu_seqlens[e]) return;
+    c.k_calibration[slot_ids[e] * c.cal_stride_slot + h * c.cal_stride_head + threadIdx.x] = 1e-3f;
+}
+
+// grid (cdiv(N, QP_CAL_BLOCK) + num_entries, Hkv), block 256.
+__global__ __launch_bounds__(QP_THREADS) void kcal_max_kernel(
+    const uint16_t* __restrict__ k, int64_t k_st, int64_t k_sh,
+    const int32_t* __restrict__ cu_seqlens, const int32_t* __restrict__ slot_ids,
+    const int32_t* __restrict__ cached_lens, const int32_t* __restrict__ num_decoding,
+    int num_entries, ie_kv_cache c) {
+    const int h = blockIdx.y;
+    const QpBlock q = qp_locate<QP_CAL_BLOCK>(blockIdx.x, cu_seqlens, slot_ids, cached_lens,
+                                              num_decoding, num_entries);
+    if (q.b < 0 || q.c0 != 0) return;
+    const int tid = threadIdx.x, c16 = tid & 15, r = tid >> 4;
+    const int t0 = q.z * QP_CAL_BLOCK, t1 = min(q.len, t0 + QP_CAL_BLOCK);
+    const uint16_t* kh = k + (int64_t)q.start * k_st + h * k_sh + 8 * c16;
+    float mx[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) mx[j] = 0.0f;
+    uint4 w[QP_CAL_BLOCK / QP_ROWS];  // all of the thread's rows in flight at once
+#pragma unroll
+    for (int i = 0; i < QP_CAL_BLOCK / QP_ROWS; ++i) {
+        const int t = t0 + r + i * QP_ROWS;
+        w[i] = t < t1 ? *reinterpret_cast<const uint4*>(kh + (int64_t)t * k_st)
+                      : make_uint4(0u, 0u, 0u, 0u);
+    }
+#pragma unroll
+    for (int i = 0; i < QP_CAL_BLOCK / QP_ROWS; ++i) {
+        const uint32_t x[4] = {w[i].x, w[i].y, w[i].z, w[i].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            mx[2 * j] = fmaxf(mx[2 * j], fabsf(bf16lo(x[j])));
+            mx[2 * j + 1] = fmaxf(mx[2 * j + 1], fabsf(bf16hi(x[j])));
+        }
+    }
+    __shared__ float s_red[QP_ROWS][HEAD_DIM];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s_red[r][8 * c16 + j] = mx[j];
+    __syncthreads();
+    if (tid < HEAD_DIM) {
+        float m = 0.0f;
+#pragma unroll
+        for (int rr = 0; rr < QP_ROWS; ++rr) m = fmaxf(m, s_red[rr][tid]);
+        float* calp = c.k_calibration + q.slot * c.cal_stride_slot + h * c.cal_stride_head;
+        atomicMax(reinterpret_cast<unsigned int*>(calp + tid), __float_as_uint(m));
+    }
+}
+
+// grid (cdiv(N, ROWS) + num_entries, Hkv), block 256: workgroup (u, h) quantizes block u of ROWS
+// rows for kv head h (kernels.py:786-823), or exits when there are fewer blocks. With INLINE_CAL, every
+// block of an entry with cached_len == 0 computes the chunk's calibration (kernels.py:764-780)
+// itself and block 0 stores it (one launch; each block reads the whole chunk's K, so the host
+// takes this form only for short steps); otherwise the calibration row was computed by the two
+// launches above and every block reads it.
+template <bool INLINE_CAL, int ROWS>
+__global__ __launch_bounds__(QP_THREADS) void quantize_kv_prefill_kernel(
+    const uint16_t* __restrict__ k, int64_t k_st, int64_t k_sh,
+    const uint16_t* __restrict__ v, int64_t v_st, int64_t v_sh,
+    const int32_t* __restrict__ cu_seqlens, const int32_t* __restrict__ slot_ids,
+    const int32_t* __restrict__ cached_lens, const int32_t* __restrict__ num_decoding,
+    int num_entries, ie_kv_cache c) {
+#pragma clang fp contract(off)
+    const int h = blockIdx.y;
+    const QpBlock q = qp_locate<ROWS>(blockIdx.x, cu_seqlens, slot_ids, cached_lens,
+                                      num_decoding, num_entries);
+    if (q.b < 0) return;
+    const int z = q.z, start = q.start, len = q.len, slot = q.slot, c0 = q.c0;
+    const int t0 = z * ROWS;
+    const int t1 = min(len, t0 + ROWS);
 
     const int tid = threadIdx.x;
     const int c16 = tid & 15;  // channels [8*c16, 8*c16+8)
@@ -130,7 +216,7 @@ __global__ __launch_bounds__(QP_THREADS) void quantize_kv_prefill_kernel(
     };
     if (t0 + r < t1) load_pair(t0 + r);
 
-    if (c0 == 0) {
+    if (INLINE_CAL && c0 == 0) {
         // max |k| per channel over the whole chunk, QP_CAL_BATCH rows per thread in flight
         float mx[8];
 #pragma unroll
@@ -426,7 +512,24 @@ extern "C" hipError_t ie_quantize_kv_prefill(
     const int64_t blocks = (num_tokens + QP_BLOCK - 1) / QP_BLOCK + num_entries;
     IE_REQUIRE(blocks < (1LL << 31), "too many tokens");
     dim3 grid((unsigned)std::max<int64_t>(1, blocks), (unsigned)cache->num_kv_heads);
-    hipLaunchKernelGGL(quantize_kv_prefill_kernel, grid, dim3(QP_THREADS), 0, stream,
+    if (num_tokens <= QP_INLINE_CAL_MAX_TOKENS) {
+        hipLaunchKernelGGL((quantize_kv_prefill_kernel<true, QP_BLOCK>), grid, dim3(QP_THREADS),
+                           0, stream,
+                           (const uint16_t*)k, k_stride_tok, k_stride_head, (const uint16_t*)v,
+                           v_stride_tok, v_stride_head, cu_seqlens, slot_ids, cached_lens,
+                           num_decoding, num_entries, *cache);
+        return hipGetLastError();
+    }
+    hipLaunchKernelGGL(kcal_init_kernel, dim3(num_entries, cache->num_kv_heads), dim3(HEAD_DIM),
+                       0, stream, cu_seqlens, slot_ids, cached_lens, num_decoding, *cache);
+    const int64_t cal_blocks = (num_tokens + QP_CAL_BLOCK - 1) / QP_CAL_BLOCK + num_entries;
+    hipLaunchKernelGGL(kcal_max_kernel, dim3((unsigned)cal_blocks, cache->num_kv_heads),
+                       dim3(QP_THREADS), 0, stream, (const uint16_t*)k,
+                       k_stride_tok, k_stride_head, cu_seqlens, slot_ids, cached_lens,
+                       num_decoding, num_entries, *cache);
+    // (blocks of 16, 64 or 128 rows were measured slower than 32 on a 12,288-token step)
+    hipLaunchKernelGGL((quantize_kv_prefill_kernel<false, QP_BLOCK>), grid, dim3(QP_THREADS), 0,
+                       stream,
                        (const uint16_t*)k, k_stride_tok, k_stride_head, (const uint16_t*)v,
                        v_stride_tok, v_stride_head, cu_seqlens, slot_ids, cached_lens,
                        num_decoding, num_entries, *cache);

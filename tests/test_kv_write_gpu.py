@@ -20,8 +20,11 @@ def _prefill_case(workloads, decode_ctx, chunks, seed, max_len=2048):
     ("config4", None),
     ([3, 70], [(1, 0), (17, 0), (0, 0), (33, 5), (1000, 0)]),
     ([], [(2100, 0), (129, 300)]),
+    ([5, 9], [(4000, 0), (64, 0), (1, 0), (300, 700)]),
 ])
 def test_quantize_kv_prefill_bitwise(ie, workloads, dev, decode_ctx, chunks):
+    # steps of more than 1536 packed tokens compute a first chunk's calibration in two launches
+    # ahead of the quantize launch (the last two cases), shorter ones inside it
     say(f"quantize_kv_prefill case {decode_ctx if chunks is None else chunks}")
     if decode_ctx == "config4":
         wl = workloads.config4(seed=3)
