@@ -353,6 +353,31 @@ def main():
         f"({split_gbs:.0f} GB/s), combine {comb_ms*1e3:.2f} us")
 
     extra = {}
+    # ---- the attainable read rate on this device: a pure 16-byte read stream (ie_hbm_read_probe)
+    # over as many bytes as one decode launch reads, past the 256 MB last-level cache, two
+    # buffers alternating; and torch's own sum over the same bytes ----
+    import ctypes
+    lib = importlib.import_module("inference-engine_amd._native").cabi()
+    probes = [torch.ones(alg_bytes // 4, dtype=torch.float32, device=dev) for _ in range(2)]
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    turn = [0]
+
+    def read_probe():
+        t = probes[turn[0]]
+        turn[0] ^= 1
+        rc = lib.ie_hbm_read_probe(ctypes.c_void_p(t.data_ptr()), ctypes.c_size_t(alg_bytes),
+                                   ctypes.c_uint32(0x9E3779B9), ctypes.c_void_p(sink.data_ptr()),
+                                   stream)
+        assert rc == 0, lib.ie_attn_last_error()
+    rp_ms = time_op(read_probe, args.steps, args.warmup)
+    ts_ms = time_op(lambda: probes[0].sum(), args.steps, args.warmup)
+    extra["read_probe"] = {"bytes": alg_bytes,
+                           "stream_us": round(rp_ms * 1e3, 2),
+                           "stream_GBps": round(alg_bytes / (rp_ms * 1e-3) / 1e9, 1),
+                           "torch_sum_GBps": round(alg_bytes / (ts_ms * 1e-3) / 1e9, 1)}
+    log(f"read probe {rp_ms*1e3:.2f} us, torch.sum {ts_ms*1e3:.2f} us")
+    del probes, sink
     # ---- config 4: KV write + chunked prefill ----
     try:
         mw = W.mixed_to(W.config4(seed=0), dev)

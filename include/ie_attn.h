@@ -69,6 +69,17 @@ int32_t ie_attn_version(void);
 const char* ie_attn_last_error(void);
 
 /*
+ * Measurement helper, no counterpart in the reference: reads `bytes` (a multiple of 16, 16-byte
+ * aligned) from device memory p once, at the device's attainable rate (8 workgroups of 256
+ * per CU, each streaming a contiguous 1/G of the buffer with 16-byte loads, eight in flight).
+ * Each thread XORs the 32-bit words it read and writes that value to out[0] only if it equals
+ * `never`. Used to put the decode kernel's HBM rate beside what a pure read stream reaches on
+ * the same device.
+ */
+hipError_t ie_hbm_read_probe(const void* p, size_t bytes, uint32_t never, uint32_t* out,
+                             hipStream_t stream);
+
+/*
  * Quantize-on-write for prefilling entries.
  * Replaces qwen3-1.7b/kernels.py:826-865 `quantize_kv_prefill(k, v, cu_seqlens, slot_ids,
  * cached_lens, num_decoding, cache)` (kernel kernels.py:717-823).

@@ -47,7 +47,47 @@ int device_cu_count() {
     return counts[dev];
 }
 
+// Attainable HBM read rate on this device: workgroup w streams its own contiguous 1/G of the
+// buffer (as a decode workgroup streams its rows), 4 KB per workgroup step with 16-byte loads,
+// eight steps in flight, and each thread XORs the words it read. A thread stores only when its
+// XOR equals `never`, a value the caller picks, so the compiler keeps every load and the kernel
+// writes nothing in practice.
+__global__ __launch_bounds__(256) void hbm_read_probe_kernel(const uint4* __restrict__ p,
+                                                             int64_t n16, uint32_t never,
+                                                             uint32_t* out) {
+    const int64_t per = (n16 + gridDim.x - 1) / gridDim.x;
+    const int64_t end = min(n16, per * (blockIdx.x + 1));
+    int64_t i = per * blockIdx.x + threadIdx.x;
+    uint4 acc = make_uint4(0u, 0u, 0u, 0u);
+    for (; i + 7 * 256 < end; i += 8 * 256) {
+        uint4 w[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) w[j] = p[i + j * 256];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            acc.x ^= w[j].x; acc.y ^= w[j].y; acc.z ^= w[j].z; acc.w ^= w[j].w;
+        }
+    }
+    for (; i < end; i += 256) {
+        const uint4 w = p[i];
+        acc.x ^= w.x; acc.y ^= w.y; acc.z ^= w.z; acc.w ^= w.w;
+    }
+    const uint32_t r = acc.x ^ acc.y ^ acc.z ^ acc.w;
+    if (r == never) out[0] = r;
+}
+
 }  // namespace ie
+
+extern "C" hipError_t ie_hbm_read_probe(const void* p, size_t bytes, uint32_t never,
+                                        uint32_t* out, hipStream_t stream) {
+    IE_REQUIRE(p && out, "null pointer");
+    IE_REQUIRE((reinterpret_cast<uintptr_t>(p) & 15) == 0 && bytes % 16 == 0,
+               "buffer must be 16-byte aligned and a multiple of 16 bytes");
+    const int wg = 8 * ie::device_cu_count();
+    hipLaunchKernelGGL(ie::hbm_read_probe_kernel, dim3(wg), dim3(256), 0, stream,
+                       static_cast<const uint4*>(p), (int64_t)(bytes / 16), never, out);
+    return hipGetLastError();
+}
 
 extern "C" int32_t ie_attn_version(void) { return (1 << 16) | 0; }
 
