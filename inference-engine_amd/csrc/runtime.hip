@@ -48,30 +48,27 @@ int device_cu_count() {
 }
 
 // Attainable HBM read rate on this device: workgroup w streams its own contiguous 1/G of the
-// buffer (as a decode workgroup streams its rows), 4 KB per workgroup step with 16-byte loads,
-// eight steps in flight, and each thread XORs the words it read. A thread stores only when its
+// buffer (as a decode workgroup streams its rows), 4 KB per workgroup step with 16-byte
+// non-temporal loads (the decode kernel's cache policy), eight steps in flight, and each thread
+// XORs the words it read. A thread stores only when its
 // XOR equals `never`, a value the caller picks, so the compiler keeps every load and the kernel
 // writes nothing in practice.
-__global__ __launch_bounds__(256) void hbm_read_probe_kernel(const uint4* __restrict__ p,
+typedef uint32_t probe_u32x4 __attribute__((ext_vector_type(4)));
+__global__ __launch_bounds__(256) void hbm_read_probe_kernel(const probe_u32x4* __restrict__ p,
                                                              int64_t n16, uint32_t never,
                                                              uint32_t* out) {
     const int64_t per = (n16 + gridDim.x - 1) / gridDim.x;
     const int64_t end = min(n16, per * (blockIdx.x + 1));
     int64_t i = per * blockIdx.x + threadIdx.x;
-    uint4 acc = make_uint4(0u, 0u, 0u, 0u);
+    probe_u32x4 acc = {0u, 0u, 0u, 0u};
     for (; i + 7 * 256 < end; i += 8 * 256) {
-        uint4 w[8];
+        probe_u32x4 w[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) w[j] = p[i + j * 256];
+        for (int j = 0; j < 8; ++j) w[j] = __builtin_nontemporal_load(p + i + j * 256);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            acc.x ^= w[j].x; acc.y ^= w[j].y; acc.z ^= w[j].z; acc.w ^= w[j].w;
-        }
+        for (int j = 0; j < 8; ++j) acc ^= w[j];
     }
-    for (; i < end; i += 256) {
-        const uint4 w = p[i];
-        acc.x ^= w.x; acc.y ^= w.y; acc.z ^= w.z; acc.w ^= w.w;
-    }
+    for (; i < end; i += 256) acc ^= __builtin_nontemporal_load(p + i);
     const uint32_t r = acc.x ^ acc.y ^ acc.z ^ acc.w;
     if (r == never) out[0] = r;
 }
@@ -85,7 +82,8 @@ extern "C" hipError_t ie_hbm_read_probe(const void* p, size_t bytes, uint32_t ne
                "buffer must be 16-byte aligned and a multiple of 16 bytes");
     const int wg = 8 * ie::device_cu_count();
     hipLaunchKernelGGL(ie::hbm_read_probe_kernel, dim3(wg), dim3(256), 0, stream,
-                       static_cast<const uint4*>(p), (int64_t)(bytes / 16), never, out);
+                       static_cast<const ie::probe_u32x4*>(p), (int64_t)(bytes / 16), never,
+                       out);
     return hipGetLastError();
 }
 
