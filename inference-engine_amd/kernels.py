@@ -216,6 +216,9 @@ def skinny_matmul(x: torch.Tensor, weight: torch.Tensor, n_tiles: int = 1) -> to
 # and row count, else None (qwen3-1.7b/kernels.py:1446-1448). Filled by tune_linear before graph
 # capture; anything it never measured uses the library.
 use_skinny: dict = {}
+# (N, K, M) -> n_tiles of the fused gate/up + SiLU-gated launch, timed by tune_linear beside the
+# plain choice (the fused launch's best tile width can differ from the plain GEMM's).
+use_skinny_glu: dict = {}
 
 
 def skinny_matmul_silu_mul(x: torch.Tensor, weight: torch.Tensor, n_tiles: int = 1) -> torch.Tensor:
@@ -232,7 +235,10 @@ def skinny_matmul_silu_mul(x: torch.Tensor, weight: torch.Tensor, n_tiles: int =
 def linear_silu_mul(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     """silu_mul(linear(x, weight)): the fused launch wherever tune_linear chose the skinny GEMM
     for this weight shape and row count, else the library GEMM then silu_mul."""
-    nt = use_skinny.get((weight.shape[0], weight.shape[1], x.shape[0]))
+    key = (weight.shape[0], weight.shape[1], x.shape[0])
+    if key in use_skinny_glu:
+        return skinny_matmul_silu_mul(x, weight, use_skinny_glu[key])
+    nt = use_skinny.get(key)
     if nt is not None and weight.shape[0] % 64 == 0:
         return skinny_matmul_silu_mul(x, weight, 2 if nt in (2, 4) else 1)
     return silu_mul(torch.nn.functional.linear(x, weight))
@@ -253,7 +259,9 @@ def tune_linear(weights: list, rows: list, calls: int = 20) -> None:
     needs a 2 % win. Each candidate runs `calls` back-to-back launches captured in one hipGraph
     (the way the engine replays a step), cycling through copies of the weight that together
     exceed the 256 MB last-level cache, so the weights come from HBM as every layer's do in a
-    step (the reference clears the cache before each timing for the same reason)."""
+    step (the reference clears the cache before each timing for the same reason). Where the
+    skinny kernel wins and N allows it, the fused gate/up + SiLU-gated launch is timed at each
+    tile width as well, for linear_silu_mul."""
     for weight in weights:
         N, K = weight.shape
         todo = [M for M in rows if M <= 64 and (N, K, M) not in use_skinny]
@@ -274,6 +282,10 @@ def tune_linear(weights: list, rows: list, calls: int = 20) -> None:
                     if t < best:
                         best, choice = t, nt
             use_skinny[(N, K, M)] = choice
+            if choice is not None and N % 64 == 0:
+                glu = {nt: _graph_time(cycle(lambda w, nt=nt: skinny_matmul_silu_mul(x, w, nt)))
+                       for nt in (1, 2) if (N // 2) % (16 * nt) == 0}
+                use_skinny_glu[(N, K, M)] = min(glu, key=glu.get)
         del copies
 
 

@@ -51,14 +51,18 @@ def test_linear_follows_tuning_table(ie, dev):
     w = (0.02 * torch.randn(4096, 2048, generator=g)).bfloat16().to(dev)
     K = ie.kernels
     K.use_skinny.clear()
+    K.use_skinny_glu.clear()
     K.tune_linear([w], [8, 32, 100])
     assert (4096, 2048, 100) not in K.use_skinny  # > 64 rows: always the library
     assert K.use_skinny[(4096, 2048, 8)] in (None, 0, 1, 2, 4)
+    if K.use_skinny[(4096, 2048, 8)] is not None:
+        assert K.use_skinny_glu[(4096, 2048, 8)] in (1, 2)
     say(f"tuned: {K.use_skinny}")
     for M in (8, 32, 100):
         x = torch.randn(M, 2048, generator=g).bfloat16().to(dev)
         _check(K.linear(x, w), x, w, f"linear M={M}")
     K.use_skinny.clear()
+    K.use_skinny_glu.clear()
 
 
 def _check_glu(y, x, w, what):
@@ -101,4 +105,8 @@ def test_linear_silu_mul_follows_tuning_table(ie, dev):
     for choice in (None, 1, 4):  # library, then the fused skinny launch
         K.use_skinny[(1024, 512, 8)] = choice
         _check_glu(K.linear_silu_mul(x, w), x, w, f"linear_silu_mul table={choice}")
+    for nt in (1, 2):  # the fused launch's own tuned width takes precedence
+        K.use_skinny_glu[(1024, 512, 8)] = nt
+        _check_glu(K.linear_silu_mul(x, w), x, w, f"linear_silu_mul glu table={nt}")
     K.use_skinny.pop((1024, 512, 8))
+    K.use_skinny_glu.pop((1024, 512, 8))
