@@ -302,8 +302,10 @@ def read_traffic():
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    # the warm-up also brings the device's clocks up from idle: 300 decode steps (~27 ms) do;
+    # 10 measured 3-5 % slower on the same box
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=300)
     ap.add_argument("--batch", type=int, default=64)
     ap.add_argument("--ctx", type=int, default=4096)
     ap.add_argument("--rotate", type=int, default=2, help="distinct cache sets cycled per step")
@@ -426,6 +428,28 @@ def main():
             extra["prefill_config4"] = {"error": str(e).splitlines()[0][:200]}
     except Exception as e:  # reported, never silently replaced
         extra["config4_error"] = str(e).splitlines()[0][:200]
+    # ---- long prefills, where the tile loop rather than the per-launch latency sets the time:
+    # 4 x 2048 new tokens after 2048 cached, and 4 x 1024 new after 7168 cached ----
+    try:
+        longs = {}
+        for name, chunks, max_len in (("4x2048_after_2048", [(2048, 2048)] * 4, 4096),
+                                      ("4x1024_after_7168", [(1024, 7168)] * 4, 8192)):
+            pw = W.mixed_to(W.mixed_workload([], chunks, seed=2, block_m=128, max_len=max_len),
+                            dev)
+            pi = pw.inputs
+            op = lambda: K.prefill_attention(
+                pw.q, pw.k, pw.v, pi["seq_ids"], pi["cu_seqlens"], pi["tile_start"], pw.cache,
+                pi["slot_ids"], pi["cu_cached"], pw.block_m)
+            ms = time_op(op, args.steps, args.warmup)
+            fl = W.prefill_flops(pw.chunks)
+            tf = fl / (ms * 1e-3) / 1e12
+            longs[name] = {"us": round(ms * 1e3, 2), "TFLOPs": round(tf, 1),
+                           "mfma_frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4), "flops": fl}
+            log(f"prefill {name} {ms*1e3:.2f} us {tf:.1f} TFLOP/s")
+            del pw, pi, op
+        extra["prefill_long"] = longs
+    except Exception as e:  # reported, never silently replaced
+        extra["prefill_long"] = {"error": str(e).splitlines()[0][:200]}
     # ---- config 4: prefill q/k RMSNorm + RoPE of the 1,024 packed prefill tokens ----
     try:
         extra["norm_rope_prefill_config4"] = bench_norm_rope(K, args.norm_rope_tokens, args.steps,
