@@ -93,7 +93,8 @@ hipError_t ie_hbm_read_probe(const void* p, size_t bytes, uint32_t never, uint32
  * V uses the same formula with cal = 1.
  * One launch when num_tokens <= 1536 (each workgroup derives the calibration itself); three
  * launches otherwise (calibration floor, per-channel max, quantize), so the cost stays linear in
- * the chunk length. Both forms write identical bytes.
+ * the chunk length. Both forms write identical bytes. cdiv(num_tokens, 32) + num_entries must
+ * not exceed 65535 (about two million tokens per step).
  */
 hipError_t ie_quantize_kv_prefill(const ie_bf16* k, int64_t k_stride_tok, int64_t k_stride_head,
                                   const ie_bf16* v, int64_t v_stride_tok, int64_t v_stride_head,

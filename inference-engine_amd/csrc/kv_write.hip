@@ -125,14 +125,14 @@ __global__ __launch_bounds__(HEAD_DIM) void kcal_init_kernel(
     c.k_calibration[slot_ids[e] * c.cal_stride_slot + h * c.cal_stride_head + threadIdx.x] = 1e-3f;
 }
 
-// grid (cdiv(N, QP_CAL_BLOCK) + num_entries, Hkv), block 256.
+// grid (Hkv, cdiv(N, QP_CAL_BLOCK) + num_entries), block 256.
 __global__ __launch_bounds__(QP_THREADS) void kcal_max_kernel(
     const uint16_t* __restrict__ k, int64_t k_st, int64_t k_sh,
     const int32_t* __restrict__ cu_seqlens, const int32_t* __restrict__ slot_ids,
     const int32_t* __restrict__ cached_lens, const int32_t* __restrict__ num_decoding,
     int num_entries, ie_kv_cache c) {
-    const int h = blockIdx.y;
-    const QpBlock q = qp_locate<QP_CAL_BLOCK>(blockIdx.x, cu_seqlens, slot_ids, cached_lens,
+    const int h = blockIdx.x;
+    const QpBlock q = qp_locate<QP_CAL_BLOCK>(blockIdx.y, cu_seqlens, slot_ids, cached_lens,
                                               num_decoding, num_entries);
     if (q.b < 0 || q.c0 != 0) return;
     const int tid = threadIdx.x, c16 = tid & 15, r = tid >> 4;
@@ -170,7 +170,7 @@ __global__ __launch_bounds__(QP_THREADS) void kcal_max_kernel(
     }
 }
 
-// grid (cdiv(N, ROWS) + num_entries, Hkv), block 256: workgroup (u, h) quantizes block u of ROWS
+// grid (Hkv, cdiv(N, ROWS) + num_entries), block 256: workgroup (h, u) quantizes block u of ROWS
 // rows for kv head h (kernels.py:786-823), or exits when there are fewer blocks. With INLINE_CAL, every
 // block of an entry with cached_len == 0 computes the chunk's calibration (kernels.py:764-780)
 // itself and block 0 stores it (one launch; each block reads the whole chunk's K, so the host
@@ -184,8 +184,8 @@ __global__ __launch_bounds__(QP_THREADS) void quantize_kv_prefill_kernel(
     const int32_t* __restrict__ cached_lens, const int32_t* __restrict__ num_decoding,
     int num_entries, ie_kv_cache c) {
 #pragma clang fp contract(off)
-    const int h = blockIdx.y;
-    const QpBlock q = qp_locate<ROWS>(blockIdx.x, cu_seqlens, slot_ids, cached_lens,
+    const int h = blockIdx.x;
+    const QpBlock q = qp_locate<ROWS>(blockIdx.y, cu_seqlens, slot_ids, cached_lens,
                                       num_decoding, num_entries);
     if (q.b < 0) return;
     const int z = q.z, start = q.start, len = q.len, slot = q.slot, c0 = q.c0;
@@ -510,8 +510,10 @@ extern "C" hipError_t ie_quantize_kv_prefill(
                "k/v rows must be 16-byte aligned with contiguous head_dim");
     // sum over entries of cdiv(len, 32) <= cdiv(N, 32) + num_entries
     const int64_t blocks = (num_tokens + QP_BLOCK - 1) / QP_BLOCK + num_entries;
-    IE_REQUIRE(blocks < (1LL << 31), "too many tokens");
-    dim3 grid((unsigned)std::max<int64_t>(1, blocks), (unsigned)cache->num_kv_heads);
+    IE_REQUIRE(blocks <= 65535, "too many tokens (at most 65535 blocks of 32 rows per step)");
+    // kv head fastest: the workgroups in flight together cover whole 2 KB token rows of k and v
+    // (measured 5-6 % faster than block fastest at config 4 and on a 12,288-token step)
+    dim3 grid((unsigned)cache->num_kv_heads, (unsigned)std::max<int64_t>(1, blocks));
     if (num_tokens <= QP_INLINE_CAL_MAX_TOKENS) {
         hipLaunchKernelGGL((quantize_kv_prefill_kernel<true, QP_BLOCK>), grid, dim3(QP_THREADS),
                            0, stream,
@@ -523,7 +525,7 @@ extern "C" hipError_t ie_quantize_kv_prefill(
     hipLaunchKernelGGL(kcal_init_kernel, dim3(num_entries, cache->num_kv_heads), dim3(HEAD_DIM),
                        0, stream, cu_seqlens, slot_ids, cached_lens, num_decoding, *cache);
     const int64_t cal_blocks = (num_tokens + QP_CAL_BLOCK - 1) / QP_CAL_BLOCK + num_entries;
-    hipLaunchKernelGGL(kcal_max_kernel, dim3((unsigned)cal_blocks, cache->num_kv_heads),
+    hipLaunchKernelGGL(kcal_max_kernel, dim3(cache->num_kv_heads, (unsigned)cal_blocks),
                        dim3(QP_THREADS), 0, stream, (const uint16_t*)k,
                        k_stride_tok, k_stride_head, cu_seqlens, slot_ids, cached_lens,
                        num_decoding, num_entries, *cache);
