@@ -68,3 +68,18 @@ def test_ops_refuse_cpu_tensors(ie):
     i = torch.zeros(1, dtype=torch.int32)
     with pytest.raises((RuntimeError, NotImplementedError)):
         ie.decode_attention(q, c, i, i, i, 0.1)
+
+
+def test_quantize_too_many_tokens_rejected_on_host(native):
+    lib = native.cabi()
+    # a well-formed descriptor (head_dim 128) over fake aligned addresses: rejected before launch
+    desc = native.KVCacheDesc(256, 256, 256, 256, 256, 2, 8, 64, 128, 8 * 64 * 128, 64 * 128, 128,
+                              8 * 64, 64, 8 * 128, 128)
+    fn = lib.ie_quantize_kv_prefill
+    fn.restype = ctypes.c_int
+    p = ctypes.c_void_p(256)
+    rc = fn(p, ctypes.c_int64(1024), ctypes.c_int64(128), p, ctypes.c_int64(1024),
+            ctypes.c_int64(128), ctypes.c_int64(65535 * 32), p, p, p, p, ctypes.c_int32(2),
+            ctypes.byref(desc), ctypes.c_void_p(0))
+    assert rc == HIP_ERROR_INVALID_VALUE
+    assert b"too many tokens" in lib.ie_attn_last_error()
