@@ -42,7 +42,7 @@ typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 // byte is read once, and streaming it past the caches raised read bandwidth from ~6.0 to
 // ~7.0 TB/s in isolation.
 #ifndef IE_DECODE_HEAD_FAST_MIN_BATCH
-#define IE_DECODE_HEAD_FAST_MIN_BATCH 64
+#define IE_DECODE_HEAD_FAST_MIN_BATCH 0
 #endif
 #ifndef IE_DECODE_LOAD_AUX
 #define IE_DECODE_LOAD_AUX 2
@@ -580,10 +580,11 @@ extern "C" hipError_t ie_decode_attention_split(
     // with batch <= target the grid needs no spare workgroups, which would otherwise hold
     // resident slots while they find out that they are idle
     const unsigned pieces = batch <= L.target ? L.target : L.target + batch;
-    // The order in which the dispatcher hands out workgroups: from 64 sequences up, the KV heads
-    // of one piece side by side, 9 % faster at B=64 ctx=1024 and within +-1 % at B=64 ctx=4096,
-    // B=128 ctx=2048 and B=256 ctx=1024; below, the pieces of one head side by side, 3-4 %
-    // faster at config 5 (B=32). Either order gives the same results.
+    // The order in which the dispatcher hands out workgroups (same results either way): the KV
+    // heads of one piece side by side measured 9 % faster at B=64 ctx=1024, but 0.4-0.8 %
+    // slower at B=64 ctx=4096 and 3-4 % slower at config 5 (B=32); the host cannot tell the
+    // context lengths apart, so the pieces of one head go side by side unless
+    // IE_DECODE_HEAD_FAST_MIN_BATCH (0: never) is set.
     a.head_fast = IE_DECODE_HEAD_FAST_MIN_BATCH > 0 && batch >= IE_DECODE_HEAD_FAST_MIN_BATCH;
     const dim3 grid = a.head_fast ? dim3((unsigned)cache->num_kv_heads, pieces)
                                   : dim3(pieces, (unsigned)cache->num_kv_heads);
