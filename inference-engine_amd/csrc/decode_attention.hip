@@ -585,7 +585,8 @@ extern "C" hipError_t ie_decode_attention_split(
     // slower at B=64 ctx=4096 and 3-4 % slower at config 5 (B=32); the host cannot tell the
     // context lengths apart, so the pieces of one head go side by side unless
     // IE_DECODE_HEAD_FAST_MIN_BATCH (0: never) is set.
-    a.head_fast = IE_DECODE_HEAD_FAST_MIN_BATCH > 0 && batch >= IE_DECODE_HEAD_FAST_MIN_BATCH;
+    a.head_fast = IE_DECODE_HEAD_FAST_MIN_BATCH > 0 && batch >= IE_DECODE_HEAD_FAST_MIN_BATCH &&
+                  pieces <= 65535;  // the grid's y dimension holds at most 65535
     const dim3 grid = a.head_fast ? dim3((unsigned)cache->num_kv_heads, pieces)
                                   : dim3(pieces, (unsigned)cache->num_kv_heads);
     hipLaunchKernelGGL(decode_split_kernel, grid, dim3(DA_THREADS), 0, stream, a);
