@@ -347,18 +347,24 @@ __attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_split_k
     // done and its V as soon as this block's PV is done, so every load has half a block of
     // VALU work to hide behind without extra registers. Requests past the piece's end fall
     // outside the buffer range and return zeros without touching memory.
+    // this wave's blocks: w, w + 8, ... of the piece's 32-token blocks, counted up front
+    const int nb = (t_end - t_begin + DA_TOK_WAVE - 1) / DA_TOK_WAVE;
+    const int cw = wave < nb ? (nb - wave + DA_WAVES - 1) / DA_WAVES : 0;
+    int nfull = cw;
+    if (cw > 0 && t_begin + DA_TOK_WAVE * (wave + DA_WAVES * (cw - 1)) + DA_TOK_WAVE > t_end)
+        --nfull;  // the piece's last, partial block
     int t0 = t_begin + wave * DA_TOK_WAVE;
     KVRegs kr, vr;
     load_block(kr, rk, rks, t0 + 4 * g, cc);
     load_block(vr, rv, rvs, t0 + 4 * g, cc);
     float s[DA_U][2];
-    for (; t0 + DA_TOK_WAVE <= t_end; t0 += DA_TOK_WG) {
+    for (int j = 0; j < nfull; ++j, t0 += DA_TOK_WG) {
         block_scores<false>(s, kr, qh, qsum, kmul, t0 + 4 * g, t_end);
         load_block(kr, rk, rks, t0 + DA_TOK_WG + 4 * g, cc);
         block_pv(st, s, vr);
         load_block(vr, rv, rvs, t0 + DA_TOK_WG + 4 * g, cc);
     }
-    if (t0 < t_end) {
+    if (nfull < cw) {
         block_scores<true>(s, kr, qh, qsum, kmul, t0 + 4 * g, t_end);
         block_pv(st, s, vr);
     }
