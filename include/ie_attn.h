@@ -177,6 +177,19 @@ hipError_t ie_decode_attention_combine(int32_t batch, int32_t num_q_heads, int32
                                        hipStream_t stream);
 
 /*
+ * The split launch's work list, for tests and diagnostics: the work split of
+ * qwen3-1.7b/kernels.py:20-70 (`compute_piece`, `assign_work`) as the split kernel computes it
+ * on the device. ie_decode_attention_grid(batch, num_kv_heads) is the number of work entries
+ * (the split launch's workgroups per KV head); ie_decode_attention_plan writes, for each entry
+ * w, rows[4w .. 4w+3] = (sequence b, split index, splits of b, piece size in tokens), with
+ * splits = 0 for an entry that has no work. rows: int32 [grid, 4] device memory.
+ */
+int32_t ie_decode_attention_grid(int32_t batch, int32_t num_kv_heads);
+hipError_t ie_decode_attention_plan(const int32_t* cached_lens, const int32_t* num_decoding,
+                                    int32_t batch, int32_t num_kv_heads, int32_t* rows,
+                                    hipStream_t stream);
+
+/*
  * Prefill-side q/k RMSNorm + RoPE over packed tokens.
  * Replaces qwen3-1.7b/kernels.py:665-714 `fused_norm_rope_prefill(q, k, q_norm_weight,
  * k_norm_weight, cos, sin, eps) -> (q_out, k_out)` (kernel kernels.py:547-662).

@@ -161,9 +161,15 @@ __device__ __forceinline__ v4u ld128(rsrc_t r, int off) {
 }
 
 // Running softmax state of one lane: query heads (2hk, 2hk+1), channels [16c, 16c+16).
+// The PV products are fp16 values of p * v_scale * 2^ve: the exponent ve is chosen from the V
+// scales the lane group has seen so that the largest product stays inside fp16's normal range
+// whatever the magnitude of V (the reference rounds p * v_scale to bf16, whose exponent range
+// is fp32's). l, ps and acc all carry the factor 2^ve, so the state is an ordinary online
+// softmax whose running maximum m is kept as (max score - ve), and it merges as one.
 struct LaneState {
     float m[2], l[2], ps[2];
     float acc[2][16];
+    float ve;  // an integer
 };
 
 // Registers of one 32-token block of a wave: lane group g holds tokens t0+4g .. t0+4g+3,
@@ -212,22 +218,45 @@ __device__ __forceinline__ void block_scores(float (&s)[DA_U][2], const KVRegs& 
 // Online-softmax update of the lane group and the PV accumulation of the block.
 __device__ __forceinline__ void block_pv(LaneState& st, const float (&s)[DA_U][2],
                                          const KVRegs& v) {
+    // The block's largest V scale vmax lies in [2^(ex-1), 2^ex). With p <= 2^ve the products
+    // stay below 2^15 while ex + ve <= 15; the exponent is re-chosen (vmax * 2^ve in
+    // [2^14, 2^15)) when that fails, or when ex + ve < 9, i.e. the scales fell by 2^6 or more
+    // and small products would lose precision. The state is rescaled by the exact power of two
+    // and m moves with ve. Scales past the piece's end load as 0; a block of them changes
+    // nothing.
+    const float vmax = fmaxf(fmaxf(__uint_as_float(v.scale[0]), __uint_as_float(v.scale[1])),
+                             fmaxf(__uint_as_float(v.scale[2]), __uint_as_float(v.scale[3])));
+    const float ex = (float)__builtin_amdgcn_frexp_expf(vmax);
+    const float t = ex + st.ve;
+    if (!(t >= 9.0f && t <= 15.0f) && vmax > 0.0f) {
+        const float d = 15.0f - t;  // the new ve is 15 - ex
+        const float r = ldexpf(1.0f, (int)d);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) st.acc[h][j] *= r;
+            st.l[h] *= r;
+            st.ps[h] *= r;
+            st.m[h] -= d;  // -inf stays -inf
+        }
+        st.ve += d;
+    }
     float msafe[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-        const float mt = fmaxf(fmaxf(s[0][h], s[1][h]), fmaxf(s[2][h], s[3][h]));
-        const float mn = fmaxf(st.m[h], mt);
-        if (mn > st.m[h]) {
-            const float alpha = exp2_safe(st.m[h] - mn);  // m = -inf -> 0
+        const float mt = fmaxf(fmaxf(s[0][h], s[1][h]), fmaxf(s[2][h], s[3][h])) - st.ve;
+        if (mt > st.m[h]) {
+            const float alpha = exp2_safe(st.m[h] - mt);  // m = -inf -> 0
 #pragma unroll
             for (int j = 0; j < 16; ++j) st.acc[h][j] *= alpha;
             st.l[h] *= alpha;
             st.ps[h] *= alpha;
-            st.m[h] = mn;
+            st.m[h] = mt;
         }
+        // p = 2^(s - max + ve) <= 2^ve
         msafe[h] = st.m[h] == -INFINITY ? 0.0f : st.m[h];
     }
-    half2_t pp[DA_U / 2][2];  // (p * v_scale) of token pairs, fp16
+    half2_t pp[DA_U / 2][2];  // (p * v_scale * 2^ve) of token pairs, fp16
 #pragma unroll
     for (int pr = 0; pr < DA_U / 2; ++pr)
 #pragma unroll
@@ -342,6 +371,7 @@ __attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_split_k
 #pragma unroll
         for (int j = 0; j < 16; ++j) st.acc[h][j] = 0.0f;
     }
+    st.ve = 0.0f;
 
     // Rolling pipeline: the next block's K is requested as soon as this block's scores are
     // done and its V as soon as this block's PV is done, so every load has half a block of
@@ -500,6 +530,26 @@ __global__ __launch_bounds__(128) void decode_combine_kernel(
     out[b * o_sb + h * o_sh + d] = (uint16_t)f32_to_bf16_rne(num / den);
 }
 
+// grid (work entries), block 64: the split kernel's work list, one entry per workgroup index w
+// of its grid, computed by the same device code (decode_assign), written as
+// rows[w] = (b, split, needed, piece).
+__global__ __launch_bounds__(64) void decode_plan_kernel(const int32_t* __restrict__ cached_lens,
+                                                         const int32_t* __restrict__ num_decoding,
+                                                         int batch, int target,
+                                                         int32_t* __restrict__ rows) {
+    const int lane = threadIdx.x;
+    const int raw0 = lane < batch ? cached_lens[lane] : 0;
+    const int nd = num_decoding[0];
+    const Work wk = decode_assign(cached_lens, nd, blockIdx.x, target, raw0);
+    if (lane == 0) {
+        int32_t* r = rows + 4 * blockIdx.x;
+        r[0] = wk.b;
+        r[1] = wk.split;
+        r[2] = wk.needed;
+        r[3] = wk.piece;
+    }
+}
+
 struct Layout {
     int target, max_splits;
     size_t plan_off, acc_off, m_off, l_off, bytes;
@@ -596,6 +646,25 @@ extern "C" hipError_t ie_decode_attention_split(
     const dim3 grid = a.head_fast ? dim3((unsigned)cache->num_kv_heads, pieces)
                                   : dim3(pieces, (unsigned)cache->num_kv_heads);
     hipLaunchKernelGGL(decode_split_kernel, grid, dim3(DA_THREADS), 0, stream, a);
+    return hipGetLastError();
+}
+
+extern "C" int32_t ie_decode_attention_grid(int32_t batch, int32_t num_kv_heads) {
+    if (batch <= 0 || num_kv_heads <= 0) return 0;
+    const int target = std::min(decode_target(num_kv_heads), DA_MAX_SPLITS);
+    return batch <= target ? target : target + batch;
+}
+
+extern "C" hipError_t ie_decode_attention_plan(const int32_t* cached_lens,
+                                               const int32_t* num_decoding, int32_t batch,
+                                               int32_t num_kv_heads, int32_t* rows,
+                                               hipStream_t stream) {
+    IE_REQUIRE(batch >= 0 && num_kv_heads > 0, "bad sizes");
+    if (batch == 0) return hipSuccess;
+    IE_REQUIRE(cached_lens && num_decoding && rows, "null pointer");
+    const int target = std::min(decode_target(num_kv_heads), DA_MAX_SPLITS);
+    hipLaunchKernelGGL(decode_plan_kernel, dim3((unsigned)ie_decode_attention_grid(batch, num_kv_heads)),
+                       dim3(IE_WAVE), 0, stream, cached_lens, num_decoding, batch, target, rows);
     return hipGetLastError();
 }
 

@@ -41,14 +41,18 @@ def empty_cache(pool, max_len, device="cpu") -> LayerKVCache:
     )
 
 
-def fill_rows(cache: LayerKVCache, slot: int, n: int, gen, calibrate=False) -> None:
-    """Columns [0, n) of cache row `slot` from bf16 N(0,1) K/V; optional per-channel calibration
-    max(1e-3, max_t |k|) (the first-chunk rule) applied to K before quantizing."""
+def fill_rows(cache: LayerKVCache, slot: int, n: int, gen, calibrate=False,
+              v_mult: float = 1.0) -> None:
+    """Columns [0, n) of cache row `slot` from bf16 N(0,1) K/V (V times `v_mult`, rounded to
+    bf16); optional per-channel calibration max(1e-3, max_t |k|) (the first-chunk rule)
+    applied to K before quantizing."""
     if n <= 0:
         return
     dev = cache.k.device
     k = randn_bf16((HKV, n, D), gen, dev).float()
     v = randn_bf16((HKV, n, D), gen, dev).float()
+    if v_mult != 1.0:
+        v = (v * v_mult).to(torch.bfloat16).float()
     if calibrate:
         cal = k.abs().amax(dim=1).clamp_min(1e-3)  # [HKV, D]
         cache.k_calibration[slot, :, 0] = cal
@@ -98,8 +102,14 @@ def decode_ctx_lens(config: str, seed: int = 0) -> list:
 
 
 def decode_workload(ctx: list, seed: int = 0, device="cpu", max_len=None, pool=None,
-                    num_decoding=None) -> DecodeWorkload:
-    """Decode batch with the given per-sequence contexts; slots are a seeded permutation."""
+                    num_decoding=None, v_mult: float = 1.0,
+                    sink_alpha: float = 0.0) -> DecodeWorkload:
+    """Decode batch with the given per-sequence contexts; slots are a seeded permutation.
+
+    v_mult scales the V source (the V scales scale with it). sink_alpha > 0 makes token 0 of
+    every sequence an attention sink for the first query head of each KV head: its K is
+    sink_alpha * q of that head (quantized like every row), so that token's score stands
+    sink_alpha * |q|^2 / sqrt(D) above the N(0, 1) scores of the other tokens."""
     B = len(ctx)
     gen = torch.Generator(device=device).manual_seed(seed)
     max_len = max_len or int(math.ceil(max(ctx) / 64) * 64)
@@ -108,7 +118,13 @@ def decode_workload(ctx: list, seed: int = 0, device="cpu", max_len=None, pool=N
     perm = torch.randperm(pool, generator=torch.Generator().manual_seed(seed + 1))[:B]
     cache = empty_cache(pool, max_len, device)
     for b in range(B):
-        fill_rows(cache, int(perm[b]), ctx[b], gen)
+        fill_rows(cache, int(perm[b]), ctx[b], gen, v_mult=v_mult)
+        if sink_alpha:
+            slot = int(perm[b])
+            k0 = (q[b, 0::HQ // HKV].float() * sink_alpha).to(torch.bfloat16).float()  # [HKV, D]
+            kq, ks = quantize_rows(k0)
+            cache.k[slot, :, 0] = kq
+            cache.k_scale[slot, :, 0] = ks
     nd = B if num_decoding is None else num_decoding
     return DecodeWorkload(q, cache, torch.tensor([c - 1 for c in ctx], dtype=torch.int32,
                                                  device=device),

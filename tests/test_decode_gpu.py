@@ -7,8 +7,9 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import assert_attn_close, bf16_np, cache_np, say
+from helpers import TOL_MAX, TOL_MEAN, assert_attn_close, bf16_np, cache_np, rel_err, say
 from oracle import attention as oat
+from oracle import work_split as ows
 
 pytestmark = pytest.mark.gpu
 SCALE = 128 ** -0.5
@@ -65,24 +66,131 @@ def test_decode_partial_batch_and_out_rows(ie, workloads, dev):
     assert np.all(o[4:] == 7.0)
 
 
-def test_decode_full_size_sampled(ie, workloads, dev):
-    """B=64, ctx=4096 (the headline shape), generated on the GPU; 6 sampled sequences checked
-    against the oracle on their own rows, all outputs finite and bounded by max|v|."""
-    ctx = [4096] * 64
-    say("decode headline shape B=64 ctx=4096 (sampled)")
-    g = workloads.decode_workload(ctx, seed=1, device=dev)
+def sampled_check(ie, workloads, dev, ctx, pick, seed, what, **kw):
+    """The batch generated on the GPU, decoded whole; all outputs finite, and the sequences
+    `pick` checked against the oracle on their own cache rows."""
+    g = workloads.decode_workload(ctx, seed=seed, device=dev, **kw)
     out = ie.decode_attention(g.q, g.cache, g.cached_lens, g.slot_ids, g.num_decoding, SCALE)
     torch.cuda.synchronize()
+    nd = int(g.num_decoding[0])
     o = bf16_np(out)
-    assert np.isfinite(o).all()
-    pick = [0, 5, 17, 32, 50, 63]
+    assert np.isfinite(o[:nd]).all()
     sub = workloads.DecodeWorkload(
         g.q[pick].cpu(), type(g.cache)(*(t[g.slot_ids[pick].long()].cpu() for t in
                                           (g.cache.k, g.cache.v, g.cache.k_scale,
                                            g.cache.v_scale, g.cache.k_calibration))),
         g.cached_lens[pick].cpu(), torch.arange(len(pick), dtype=torch.int32),
         torch.tensor([len(pick)], dtype=torch.int32), [ctx[i] for i in pick])
-    assert_attn_close(o[pick], oracle_out(sub), "headline sampled")
+    assert_attn_close(o[pick], oracle_out(sub), what)
+    del g, out
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("B,ctx", [(64, 4096), (16, 4096), (256, 1024), (256, 4096)])
+def test_decode_config3_sampled(ie, workloads, dev, B, ctx):
+    """BASELINE config 3 points at full size, generated on the GPU (B=64 ctx=4096 is the
+    headline; B=256 runs the grid of TARGET + B workgroups, where pieces are not fitted):
+    8 sampled sequences checked against the oracle."""
+    say(f"decode config 3 B={B} ctx={ctx} (sampled)")
+    pick = sorted({0, 1, B // 4, B // 2 - 1, B // 2, 3 * B // 4, B - 2, B - 1})
+    sampled_check(ie, workloads, dev, [ctx] * B, pick, seed=B + ctx, what=f"config3 {B}x{ctx}")
+
+
+@pytest.mark.parametrize("B,nd,lo,hi,seed", [
+    (200, 170, 1, 3000, 31),  # more sequences than the per-head workgroup target
+    (300, 299, 1, 600, 32),   # one-split sequences filling the TARGET + B grid
+    (65, 65, 2000, 9000, 33),  # one past the target, several splits per sequence
+])
+def test_decode_ragged_large_batch(ie, workloads, dev, B, nd, lo, hi, seed):
+    """Batches above the per-head workgroup target (64 on 256 CUs) with num_decoding < B:
+    the reference's unfitted piece rule and the TARGET + B grid (kernels.py:294-314), every
+    decoding row against the oracle and the rows past num_decoding untouched."""
+    ctx = [int(x) for x in np.random.default_rng(seed).integers(lo, hi + 1, B)]
+    say(f"decode ragged B={B} num_decoding={nd} ctx {min(ctx)}..{max(ctx)}")
+    wl = workloads.decode_workload(ctx, seed=seed, num_decoding=nd)
+    ref = oracle_out(wl, nd=nd)
+    g = wl.to(dev)
+    out = torch.full((B, 16, 128), 3.0, dtype=torch.bfloat16, device=dev)
+    ie.decode_attention(g.q, g.cache, g.cached_lens, g.slot_ids, g.num_decoding, SCALE, out=out)
+    torch.cuda.synchronize()
+    o = bf16_np(out)
+    assert_attn_close(o[:nd], ref[:nd], f"ragged large B={B}")
+    assert np.all(o[nd:] == 3.0)
+
+
+def test_decode_long_and_short_mix_above_target(ie, workloads, dev):
+    """96 sequences, 6 of them 30-60K tokens long: above the target the long ones split into
+    many pieces merged by the combine kernel."""
+    rng = np.random.default_rng(41)
+    ctx = [int(x) for x in rng.integers(100, 500, 90)] + [int(x) for x in
+                                                          rng.integers(30000, 60000, 6)]
+    rng.shuffle(ctx)
+    say(f"decode long/short mix B={len(ctx)} max ctx {max(ctx)}")
+    wl = workloads.decode_workload(ctx, seed=41)
+    ref = oracle_out(wl)
+    g = wl.to(dev)
+    out = ie.decode_attention(g.q, g.cache, g.cached_lens, g.slot_ids, g.num_decoding, SCALE)
+    torch.cuda.synchronize()
+    assert_attn_close(bf16_np(out), ref, "long/short mix")
+
+
+@pytest.mark.parametrize("v_mult,sink", [(1e-2, 0.8), (1e-4, 0.8), (1e2, 0.8), (1e-2, 0.0),
+                                         (1.0, 0.8)])
+def test_decode_v_magnitude_and_sink(ie, workloads, dev, v_mult, sink):
+    """V far from unit scale, with an attention sink (one key scoring ~9 above the rest, so the
+    thousands of tail keys each weigh ~1e-4 and together about as much as the sink): the
+    products p * v_scale span many binades, and the scale-normalised error must stay within
+    the bf16 tolerance whatever V's magnitude."""
+    ctx = [8000, 6000, 9000, 3000]
+    wl = workloads.decode_workload(ctx, seed=51, v_mult=v_mult, sink_alpha=sink)
+    ref = oracle_out(wl)
+    g = wl.to(dev)
+    out = ie.decode_attention(g.q, g.cache, g.cached_lens, g.slot_ids, g.num_decoding, SCALE)
+    torch.cuda.synchronize()
+    o = bf16_np(out)
+    r = rel_err(o, ref)
+    say(f"v_mult {v_mult} sink {sink}: scaled max err {r.max():.3e} mean {r.mean():.3e}")
+    assert np.isfinite(o).all()
+    assert r.max() <= TOL_MAX and r.mean() <= TOL_MEAN
+
+
+@pytest.mark.parametrize("ctx,nd", [
+    ([4096] * 64, 64), ([4096] * 63 + [1], 64), ([7] * 10, 10), ([100, 3000, 5] * 7, 20),
+    ([int(x) for x in np.random.default_rng(3).integers(1, 5000, 64)], 64),
+    ([int(x) for x in np.random.default_rng(4).integers(1, 5000, 200)], 170),
+    ([1024] * 256, 256), ([200] * 90 + [50000] * 6, 96), ([33000], 1), ([5, 6], 0),
+])
+def test_decode_plan_matches_oracle(ie, native, dev, ctx, nd):
+    """The split launch's work list, as the device computes it (ie_decode_attention_plan runs
+    the split kernel's own assignment code), equals oracle/work_split.decode_work_plan entry
+    for entry, and no piece of the oracle's list falls outside the launch's grid."""
+    lib = native.cabi()
+    B = len(ctx)
+    hkv = 8
+    target = lib.ie_decode_attention_max_splits(hkv)
+    grid = lib.ie_decode_attention_grid(ctypes.c_int32(B), ctypes.c_int32(hkv))
+    assert grid == (target if B <= target else target + B)
+    cl = torch.tensor([c - 1 for c in ctx], dtype=torch.int32, device=dev)
+    ndt = torch.tensor([nd], dtype=torch.int32, device=dev)
+    rows = torch.full((grid, 4), -7, dtype=torch.int32, device=dev)
+    fn = lib.ie_decode_attention_plan
+    fn.restype = ctypes.c_int
+    rc = fn(ctypes.c_void_p(cl.data_ptr()), ctypes.c_void_p(ndt.data_ptr()), ctypes.c_int32(B),
+            ctypes.c_int32(hkv), ctypes.c_void_p(rows.data_ptr()),
+            ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert rc == 0, lib.ie_attn_last_error()
+    torch.cuda.synchronize()
+    got = rows.cpu().numpy()
+    piece, ref_rows = ows.decode_work_plan(np.array(ctx) - 1, nd, B, target, min_piece=128)
+    ref = np.array(ref_rows)
+    say(f"plan B={B} nd={nd}: piece {piece}, {int((ref[:, 2] > 0).sum())} work entries, "
+        f"grid {grid}")
+    assert np.all(ref[grid:, 2] == 0), "oracle pieces past the grid"
+    if nd > 0:
+        assert np.all(got[:, 3] == piece)
+    work = ref[:grid, 2] > 0
+    assert np.array_equal(got[:, 2] > 0, work)
+    assert np.array_equal(got[work, :3], ref[:grid][work])
 
 
 def test_decode_through_c_abi(ie, workloads, dev, native):
