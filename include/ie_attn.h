@@ -240,9 +240,10 @@ hipError_t ie_dequantize_kv_prefix(const ie_kv_cache* cache, const int32_t* cu_c
  * block_m rows, -1 = no work; every tile lies inside one entry. Row m of entry e attends to the
  * e's prefix (cache row slot_ids[e], columns [0, cu_cached[e+1] - cu_cached[e])) and to its own
  * chunk rows [cu_seqlens[e], m]. Rows of out that no tile covers are left untouched.
- * num_entries = the length of slot_ids (cu_seqlens and cu_cached hold num_entries + 1), at most
- * 512. A row's entry is found from cu_seqlens; seq_ids is accepted for the reference's
- * signature and not read.
+ * num_entries = the length of slot_ids (cu_seqlens and cu_cached hold num_entries + 1), any
+ * count >= 1. Up to 512 entries a tile's entry is found by binary search over cu_seqlens
+ * (the tables staged on chip) and seq_ids is not read; above 512 it is seq_ids[first row of the
+ * tile], as in the reference kernel (kernels.py:1029), and seq_ids must hold num_tokens values.
  * Long key ranges are split across workgroups; `workspace` (partials) must hold
  * ie_prefill_attention_workspace_size(num_tiles, block_m, num_kv_heads) bytes, a size that
  * depends on the current device's CU count.

@@ -7,7 +7,7 @@ the decode step. The directory name is not a Python identifier, so import it wit
 `importlib.import_module("inference-engine_amd")`.
 """
 
-from . import kernels, step_inputs  # noqa: F401
+from . import attention_layer, kernels, step_inputs  # noqa: F401
 from .kernels import (  # noqa: F401
     LayerKVCache,
     add_rms_norm,

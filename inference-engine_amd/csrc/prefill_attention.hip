@@ -85,7 +85,7 @@ __device__ __forceinline__ uint32_t hi16pair(float lo, float hi) {
 
 // The workgroup's LDS: two K and two V^T tile buffers and three K-scale slots. Before the tile
 // loop the second K buffer holds the schedule's entry tables (cu_seqlens, cu_cached and
-// slot_ids of up to PF_MAX_ENTRIES entries): no wave writes it before the first barrier of the
+// slot_ids of up to PF_LDS_ENTRIES entries): no wave writes it before the first barrier of the
 // item, which every wave reaches only after its schedule. 79,360 bytes: two workgroups fit a
 // CU's 160 KB.
 struct PfLds {
@@ -116,6 +116,7 @@ struct PrefillArgs {
                  // order) 4 ints at 4 + 4i: first item, r0, r1, pieces
     int block_m, sub_per_tile, hq, hkv;
     int nent;  // entries (length of slot_ids; cu_seqlens and cu_cached hold nent + 1)
+    int ntok;  // packed rows (length of seq_ids)
     int nsb;   // sub-blocks: num_tiles * sub_per_tile
     int grid;  // partial slots (resident main-kernel workgroups); split items are numbered below it
     float qk_scale;  // D^-0.5 * log2(e)
@@ -159,13 +160,17 @@ __device__ __forceinline__ int piece_count(int npt, int nct, const Divisor& T) {
 //  * items in launch order: sub-blocks from last to first (later sub-blocks of a sequence see
 //    more keys), then piece, then kv head.
 // schedule(target) finds the sub-block holding item `target`, the offset inside it and the
-// number of items before the sub-block. All metadata comes in one memory round trip: the tile
-// starts of the wave's sub-blocks (PF_SCHED_CHUNKS * 64 in registers, reloaded beyond) and the
-// per-entry tables (cu_seqlens, cu_cached, slot_ids) staged in LDS, where each sub-block finds
-// its entry by binary search (an entry owns the rows [cu_seqlens[e], cu_seqlens[e + 1]); the
-// largest e with cu_seqlens[e] <= row is that row's entry, empty entries included).
+// number of items before the sub-block. With up to PF_LDS_ENTRIES entries all metadata comes in
+// one memory round trip: the tile starts of the wave's sub-blocks (PF_SCHED_CHUNKS * 64 in
+// registers, reloaded beyond) and the per-entry tables (cu_seqlens, cu_cached, slot_ids) staged
+// in LDS, where each sub-block finds its entry by binary search (an entry owns the rows
+// [cu_seqlens[e], cu_seqlens[e + 1]); the largest e with cu_seqlens[e] <= row is that row's
+// entry, empty entries included). With more entries (engines with a large max_batch_size) a
+// sub-block reads its entry from seq_ids at its tile's first row, as the reference kernel does
+// (kernels.py:1029-1033), and that entry's table values from global memory: two more dependent
+// round trips, no limit on the entry count.
 constexpr int PF_SCHED_CHUNKS = 4;
-constexpr int PF_MAX_ENTRIES = 512;
+constexpr int PF_LDS_ENTRIES = 512;
 
 struct SubBlock {
     int r0, r1, seq_start, P, slot, npt, nct, ntiles, npieces, npp;  // npp: prefix pieces
@@ -197,11 +202,12 @@ struct Loc {
 // wave of the workgroup runs it: each writes the same values into the entry tables in LDS
 // (`tables`) before reading them, so no wave waits for another.
 __device__ Loc schedule(const PrefillArgs& a, int target, int* tables) {
-    static_assert((3 * PF_MAX_ENTRIES + 2) * sizeof(int) <= sizeof(PfLds::k[1]),
+    static_assert((3 * PF_LDS_ENTRIES + 2) * sizeof(int) <= sizeof(PfLds::k[1]),
                   "entry tables must fit one K buffer");
     int* s_cu = tables;
-    int* s_cc = tables + PF_MAX_ENTRIES + 1;
-    int* s_sl = tables + 2 * (PF_MAX_ENTRIES + 1);
+    int* s_cc = tables + PF_LDS_ENTRIES + 1;
+    int* s_sl = tables + 2 * (PF_LDS_ENTRIES + 1);
+    const bool in_lds = a.nent <= PF_LDS_ENTRIES;  // uniform
     const int lane = threadIdx.x & 63;
     const int nchunks = cdiv_i(a.nsb, IE_WAVE);
     const Divisor spt = divisor(a.sub_per_tile);
@@ -213,32 +219,48 @@ __device__ Loc schedule(const PrefillArgs& a, int target, int* tables) {
     int rs[PF_SCHED_CHUNKS];
 #pragma unroll
     for (int c = 0; c < PF_SCHED_CHUNKS; ++c) rs[c] = row_start_of(c < nchunks ? sb_of(c) : -1);
-    for (int e = lane; e <= a.nent; e += IE_WAVE) {
-        s_cu[e] = a.cu_seqlens[e];
-        s_cc[e] = a.cu_cached[e];
-        if (e < a.nent) s_sl[e] = a.slot_ids[e];
+    if (in_lds) {
+        for (int e = lane; e <= a.nent; e += IE_WAVE) {
+            s_cu[e] = a.cu_seqlens[e];
+            s_cc[e] = a.cu_cached[e];
+            if (e < a.nent) s_sl[e] = a.slot_ids[e];
+        }
     }
     auto info = [&](int sb, int row_start) {
         SbInfo z = {0, 0, 0, 0, 0, 0, 0};
         if (row_start < 0) return z;
-        int lo = 0, hi = a.nent - 1;
-        while (lo < hi) {
-            const int mid = (lo + hi + 1) >> 1;
-            if (s_cu[mid] <= row_start) lo = mid;
-            else hi = mid - 1;
+        int seq_start, seq_end, P, slot;
+        if (in_lds) {
+            int lo = 0, hi = a.nent - 1;
+            while (lo < hi) {
+                const int mid = (lo + hi + 1) >> 1;
+                if (s_cu[mid] <= row_start) lo = mid;
+                else hi = mid - 1;
+            }
+            seq_start = s_cu[lo];
+            seq_end = s_cu[lo + 1];
+            P = s_cc[lo + 1] - s_cc[lo];
+            slot = s_sl[lo];
+        } else {
+            // a tile start or entry id out of range reads nothing past the index arrays
+            if (row_start >= a.ntok) return z;
+            const int e = min(max(a.seq_ids[row_start], 0), a.nent - 1);
+            seq_start = a.cu_seqlens[e];
+            seq_end = a.cu_seqlens[e + 1];
+            P = a.cu_cached[e + 1] - a.cu_cached[e];
+            slot = a.slot_ids[e];
         }
-        const int seq_start = s_cu[lo], seq_end = s_cu[lo + 1];
         const int sub = sb - div_floor(sb, spt) * a.sub_per_tile;
         const int r0 = row_start + sub * PF_BM;
         const int r1 = min(min(r0 + PF_BM, row_start + a.block_m), seq_end);
         if (r0 >= r1) return z;
-        z.P = s_cc[lo + 1] - s_cc[lo];
+        z.P = P;
         z.npt = cdiv_i(z.P, PF_BN);
         z.nct = cdiv_i(r1 - seq_start, PF_BN);
         z.r0 = r0;
         z.r1 = r1;
         z.seq_start = seq_start;
-        z.slot = s_sl[lo];
+        z.slot = slot;
         return z;
     };
     SbInfo zc[PF_SCHED_CHUNKS];
@@ -1075,8 +1097,7 @@ extern "C" hipError_t ie_prefill_attention(
     IE_REQUIRE(num_tokens >= 0 && num_tiles >= 0, "negative sizes");
     IE_REQUIRE(block_m > 0, "block_m must be positive");
     IE_REQUIRE(num_q_heads == 2 * cache->num_kv_heads, "num_q_heads must be 2 * num_kv_heads");
-    IE_REQUIRE(num_entries >= 1 && num_entries <= PF_MAX_ENTRIES,
-               "num_entries (the length of slot_ids) must be in [1, 512]");
+    IE_REQUIRE(num_entries >= 1, "num_entries (the length of slot_ids) must be at least 1");
     if (num_tokens == 0 || num_tiles == 0) return hipSuccess;
     IE_REQUIRE(q && k && v && seq_ids && cu_seqlens && tile_start && slot_ids && cu_cached && out,
                "null pointer");
@@ -1128,6 +1149,7 @@ extern "C" hipError_t ie_prefill_attention(
     a.hq = num_q_heads;
     a.hkv = cache->num_kv_heads;
     a.nent = num_entries;
+    a.ntok = (int)num_tokens;
     a.nsb = (int)nsb;
     a.grid = slots;
     a.qk_scale = (float)(0.08838834764831845 * 1.4426950408889634);  // D^-0.5 * log2(e), D = 128

@@ -376,6 +376,11 @@ at::Tensor prefill_attention(const at::Tensor& q, const at::Tensor& k, const at:
     TORCH_CHECK(k.size(0) == N && v.size(0) == N && k.size(1) == c.num_kv_heads &&
                     v.size(1) == c.num_kv_heads,
                 "ie: k/v shape mismatch");
+    // the kernel reads cu_seqlens/cu_cached[0 .. entries] and seq_ids[0 .. N) on the device
+    TORCH_CHECK(slot_ids.size(0) >= 1 && cu_seqlens.size(0) == slot_ids.size(0) + 1 &&
+                    cu_cached.size(0) == slot_ids.size(0) + 1,
+                "ie: cu_seqlens and cu_cached must hold len(slot_ids) + 1 entries");
+    TORCH_CHECK(seq_ids.size(0) >= N, "ie: seq_ids must hold one entry per packed row");
     at::Tensor out = at::empty({N, q.size(1), q.size(2)}, q.options());
     const size_t ws_bytes = ie_prefill_attention_workspace_size(
         (int32_t)tile_start.size(0), (int32_t)block_m, c.num_kv_heads);

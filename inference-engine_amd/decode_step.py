@@ -22,6 +22,7 @@ from dataclasses import dataclass
 import torch
 import torch.nn.functional as F
 
+from .attention_layer import attention, rope_inv_freq, rope_tables
 from .kernels import (LayerKVCache, add_rms_norm, decode_attention, fused_rope_kv_decode, linear,
                       linear_silu_mul, make_layer_cache, sample, tune_linear)
 
@@ -110,22 +111,20 @@ class DecodeStep:
         self.slot_ids = torch.arange(batch, device=device, dtype=torch.int32)
         self.num_decoding = torch.full((1,), batch, device=device, dtype=torch.int32)
         self.seed = torch.zeros(1, device=device, dtype=torch.int64)  # the engine's sampling seed
-        D = shape.head_dim
-        self.inv_freq = shape.rope_base ** (
-            -torch.arange(0, D, 2, dtype=torch.float32, device=device) / D)
+        self.inv_freq = rope_inv_freq(shape.head_dim, shape.rope_base, device)
         self.graph = None
         self.graph_out = None
 
     def _rope(self):
-        # decode: a token's position is the number of tokens before it (architecture.py:413-422)
-        ang = self.cached_lens[:, None, None].float() * self.inv_freq[None, None, :]
-        return ang.cos().bfloat16(), ang.sin().bfloat16()
+        # decode: a token's position is the number of tokens before it (architecture.py:382-390)
+        return rope_tables(self.cached_lens, self.inv_freq)
 
     def _rms(self, x, w):
         return F.rms_norm(x.float(), (x.shape[-1],), w.float(), self.shape.eps).bfloat16()
 
     def attention(self, li, normed, cos, sin):
-        """AttentionLayer.forward, pure-decode branch (architecture.py:85-122)."""
+        """AttentionLayer.forward, pure-decode branch (architecture.py:85-122), through
+        attention_layer.attention."""
         s, lw, B = self.shape, self.layers[li], self.B
         qkv = linear(normed, lw.qkv)
         q, k, v = qkv.split([s.num_q_heads * s.head_dim, s.num_kv_heads * s.head_dim,
@@ -133,10 +132,9 @@ class DecodeStep:
         q = q.view(B, s.num_q_heads, s.head_dim)
         k = k.view(B, s.num_kv_heads, s.head_dim)
         v = v.view(B, s.num_kv_heads, s.head_dim)
-        q = fused_rope_kv_decode(q, k, v, lw.q_norm, lw.k_norm, cos, sin, self.slot_ids,
-                                 self.caches[li], self.cached_lens, self.num_decoding, s.eps)
-        out = decode_attention(q, self.caches[li], self.cached_lens, self.slot_ids,
-                               self.num_decoding, s.head_dim ** -0.5)
+        out = attention(q, k, v, None, None, cos, sin, self.caches[li], self.cached_lens,
+                        self.slot_ids, None, 0, None, self.num_decoding, lw.q_norm, lw.k_norm,
+                        s.eps)
         return linear(out.view(B, -1), lw.o_proj)
 
     def forward(self) -> torch.Tensor:

@@ -15,6 +15,7 @@ import itertools
 import math
 from dataclasses import dataclass
 
+import numpy as np
 import torch
 
 
@@ -67,27 +68,45 @@ def fill_inputs(plan: list, num_seqs_decoding: int, n_pad: int, num_entries: int
                 scratch_slot: int) -> StepInputs:
     """engine.py:297-350 for a plan of (cached_len, slot, token_ids) per entry.
 
-    Returns the packed fields; `cu_cached[-1]` is the number of prefix tokens the step reads.
+    Built per entry as arrays: S = num_entries entries of which the first len(plan) are the
+    plan's, then a padding entry of n_pad - N tokens, then empty entries (both on the scratch
+    slot with nothing cached). Per token: its entry and its position (the entry's cached length
+    plus the token's offset inside the chunk). Tiles: every prefilling entry (index >=
+    num_seqs_decoding, the padding entry included) contributes tiles at offsets 0, block_m,
+    ... of its own rows, then -1 up to ceil(n_pad / block_m) + S. Prefix lengths: the cached
+    lengths of the prefilling entries, 0 for decoders. `cu_cached[-1]` is the number of prefix
+    tokens the step reads.
     """
     S, B = num_entries, len(plan)
     assert B < S, "needs one spare entry for padding"
-    N = sum(len(toks) for _, _, toks in plan)
+    lens = np.zeros(S, np.int64)
+    lens[:B] = [len(toks) for _, _, toks in plan]
+    N = int(lens.sum())
     assert n_pad >= N
-    chunk_lens = [len(toks) for _, _, toks in plan] + [n_pad - N] + [0] * (S - B - 1)
-    cached_lens = [c for c, _, _ in plan] + [0] * (S - B)
-    slot_ids = [s for _, s, _ in plan] + [scratch_slot] * (S - B)
-    ids = [t for _, _, toks in plan for t in toks] + [0] * (n_pad - N)
-    cu_seqlens = [0, *itertools.accumulate(chunk_lens)]
-    positions, seq_ids, tile_start = [], [], []
-    for b, (start, L) in enumerate(zip(cu_seqlens, chunk_lens)):
-        positions += range(cached_lens[b], cached_lens[b] + L)
-        seq_ids += [b] * L
-        if b >= num_seqs_decoding:
-            tile_start += range(start, start + L, block_m)
-    tile_start += [-1] * (math.ceil(n_pad / block_m) + S - len(tile_start))
-    prefix_lens = [0] * num_seqs_decoding + cached_lens[num_seqs_decoding:]
-    cu_cached = [0, *itertools.accumulate(prefix_lens)]
-    out = StepInputs(ids, positions, seq_ids, cu_seqlens, cached_lens, slot_ids, cu_cached,
-                     tile_start, num_seqs_decoding)
+    lens[B] = n_pad - N
+    cached = np.zeros(S, np.int64)
+    cached[:B] = [c for c, _, _ in plan]
+    slots = np.full(S, scratch_slot, np.int64)
+    slots[:B] = [sl for _, sl, _ in plan]
+    ids = np.zeros(n_pad, np.int64)
+    ids[:N] = [t for _, _, toks in plan for t in toks]
+
+    cu = np.zeros(S + 1, np.int64)
+    np.cumsum(lens, out=cu[1:])
+    seq_ids = np.repeat(np.arange(S), lens)
+    offset = np.arange(n_pad) - cu[:-1][seq_ids]  # token's index inside its chunk
+    positions = cached[seq_ids] + offset
+    first_of_tile = (offset % block_m == 0) & (seq_ids >= num_seqs_decoding)
+    starts = np.flatnonzero(first_of_tile)
+    tile_start = np.full(-(-n_pad // block_m) + S, -1, np.int64)
+    tile_start[:len(starts)] = starts
+    prefix = np.where(np.arange(S) >= num_seqs_decoding, cached, 0)
+    cu_cached = np.zeros(S + 1, np.int64)
+    np.cumsum(prefix, out=cu_cached[1:])
+
+    as_list = lambda a: [int(x) for x in a]
+    out = StepInputs(as_list(ids), as_list(positions), as_list(seq_ids), as_list(cu),
+                     as_list(cached), as_list(slots), as_list(cu_cached), as_list(tile_start),
+                     num_seqs_decoding)
     assert [len(f) for f in out.fields()] == input_layout(n_pad, S, block_m)
     return out

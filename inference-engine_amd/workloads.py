@@ -147,16 +147,19 @@ class MixedWorkload:
 
 
 def mixed_workload(decode_ctx: list, chunks: list, seed: int = 0, block_m: int = 128,
-                   max_len: int = 4096, num_entries: int | None = None,
-                   device="cpu") -> MixedWorkload:
+                   max_len: int = 4096, num_entries: int | None = None, pool: int | None = None,
+                   n_pad: int | None = None, device="cpu") -> MixedWorkload:
     """Config-4-shaped step: decoders with `decode_ctx` tokens attended, then prefill chunks
     (chunk_len, cached_len). A prefilling entry's cached prefix is filled with calibration
-    (its first chunk computed one), decoders' rows without."""
+    (its first chunk computed one), decoders' rows without. Entry b uses cache slot b; the
+    last slot of the pool (default num_entries + 1 slots) is the scratch slot of the padding
+    and unused entries. n_pad (default: the token count) pads the step to a token bucket."""
     gen = torch.Generator().manual_seed(seed)
     nd = len(decode_ctx)
     B = nd + len(chunks)
     S = num_entries or B + 1
-    pool = S + 1
+    pool = pool or S + 1
+    assert pool > B
     scratch = pool - 1
     cache = empty_cache(pool, max_len)
     plan = []
@@ -167,7 +170,7 @@ def mixed_workload(decode_ctx: list, chunks: list, seed: int = 0, block_m: int =
         slot = nd + j
         fill_rows(cache, slot, cached, gen, calibrate=True)
         plan.append((cached, slot, [0] * L))
-    N = sum(len(t) for _, _, t in plan)
+    N = n_pad or sum(len(t) for _, _, t in plan)
     step = fill_inputs(plan, nd, N, S, block_m, scratch)
     qkv = randn_bf16((N, (HQ + 2 * HKV) * D), gen)
     q = qkv[:, : HQ * D].reshape(N, HQ, D).contiguous()

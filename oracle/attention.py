@@ -100,12 +100,14 @@ def prefill_rows(cu_seqlens, tile_start, block_m, n_tokens):
     return covered
 
 
-def prefill_attention(q, k, v, cu_seqlens, tile_start, block_m, k_prefix, v_prefix, cu_cached):
+def prefill_attention(q, k, v, cu_seqlens, tile_start, block_m, k_prefix, v_prefix, cu_cached,
+                      rows=None):
     """Reference-rounding chunked-prefill attention.
 
     q [N, Hq, D], k/v [N, Hkv, D]: fp32 values of bf16 inputs; k_prefix/v_prefix
     [Hkv, total_cached, D] bf16-rounded (from dequantize_kv_prefix). Returns fp32
-    (bf16-rounded) [N, Hq, D]; rows no tile covers are NaN.
+    (bf16-rounded) [N, Hq, D]; rows no tile covers are NaN. `rows`: compute only these packed
+    rows (the others stay NaN), for long prefills checked on a sample.
     """
     q = np.asarray(q, np.float32)
     N, hq, d = q.shape
@@ -114,6 +116,10 @@ def prefill_attention(q, k, v, cu_seqlens, tile_start, block_m, k_prefix, v_pref
     qk_scale = F32(d ** -0.5 * LOG2E)
     out = np.full(q.shape, np.nan, np.float32)
     covered = prefill_rows(cu_seqlens, tile_start, block_m, N)
+    if rows is not None:
+        keep = np.zeros(N, bool)
+        keep[np.asarray(rows)] = True
+        covered &= keep
     cu = np.asarray(cu_seqlens)
     for m in np.nonzero(covered)[0]:
         e = int(np.searchsorted(cu, m, side="right") - 1)

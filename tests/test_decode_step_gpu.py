@@ -55,3 +55,70 @@ def test_decode_step_attention_matches_parts(ie, dev):
     want = ie.kernels.linear(o.view(4, -1), lw.o_proj)
     torch.cuda.synchronize()
     assert torch.equal(got, want)
+
+
+def test_config5_full_size(ie, dev):
+    """BASELINE config 5 at full size: 28 layers, vocab 151,936, B=32, ctx ~ U[128, 4096), the
+    projections tuned as the benchmark runs them. The captured step replays equal to the eager
+    step (tokens, and the 28-layer attention-only graph's output bit for bit); layer 0's
+    fused_rope_kv_decode -> decode_attention on the step's own activations matches the oracle on
+    sampled sequences (q and the written cache column bit for bit, attention within
+    tolerance)."""
+    import numpy as np
+
+    from helpers import assert_attn_close, bf16_np, cache_np
+    from oracle import attention as oat
+    from oracle import kv_cache as okv
+
+    ds = importlib.import_module("inference-engine_amd.decode_step")
+    say("config 5 full size: 28 layers, vocab 151936, B=32")
+    step = ds.make_decode_step(batch=32, ctx_lo=128, ctx_hi=4096, device=dev, seed=11)
+    eager = step.forward().clone()
+    graph, out = step.capture()
+    for i in range(2):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"config 5 replay {i} differs from eager"
+    att_eager = step.attention_only().clone()
+    agraph, aout = step.capture(step.attention_only)
+    agraph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(aout, att_eager), "attention-only replay differs from eager"
+
+    # layer 0 on the step's own activations, against the oracle on sampled sequences
+    pick = [0, 7, 19, 31]
+    s, lw, B = step.shape, step.layers[0], step.B
+    cos, sin = step._rope()
+    x = torch.nn.functional.embedding(step.ids, step.embed)
+    normed = step._rms(x, lw.input_norm)
+    qkv = ie.kernels.linear(normed, lw.qkv)
+    q = qkv[:, :2048].view(B, 16, 128)
+    k = qkv[:, 2048:3072].view(B, 8, 128)
+    v = qkv[:, 3072:].view(B, 8, 128)
+    cache = step.caches[0]
+    slots = step.slot_ids[pick].long()
+    sub = okv.CacheArrays(*(t[slots].cpu().numpy().copy() for t in
+                            (cache.k, cache.v, cache.k_scale, cache.v_scale,
+                             cache.k_calibration)))
+    qo = ie.fused_rope_kv_decode(q, k, v, lw.q_norm, lw.k_norm, cos, sin, step.slot_ids, cache,
+                                 step.cached_lens, step.num_decoding, s.eps)
+    o = ie.decode_attention(qo, cache, step.cached_lens, step.slot_ids, step.num_decoding,
+                            128 ** -0.5)
+    torch.cuda.synchronize()
+    lens = step.cached_lens[pick].cpu().numpy()
+    qo_ref = okv.fused_rope_kv_decode(*(bf16_np(t[pick]) for t in (q, k, v)), bf16_np(lw.q_norm),
+                                      bf16_np(lw.k_norm), bf16_np(cos[pick]), bf16_np(sin[pick]),
+                                      np.arange(len(pick), dtype=np.int32), sub, lens, len(pick),
+                                      s.eps)
+    assert np.array_equal(bf16_np(qo[pick]), qo_ref), "layer 0 q_out differs from the oracle"
+    got = cache_np(type(cache)(*(t[slots] for t in (cache.k, cache.v, cache.k_scale,
+                                                      cache.v_scale, cache.k_calibration))))
+    for i, L in enumerate(lens):
+        assert np.array_equal(got.k[i, :, L], sub.k[i, :, L]), "written K column differs"
+        assert np.array_equal(got.v[i, :, L], sub.v[i, :, L]), "written V column differs"
+        assert np.array_equal(got.k_scale[i, :, L].view(np.uint32),
+                              sub.k_scale[i, :, L].view(np.uint32))
+        assert np.array_equal(got.v_scale[i, :, L].view(np.uint32),
+                              sub.v_scale[i, :, L].view(np.uint32))
+    ref = oat.decode_attention(qo_ref, sub, lens, np.arange(len(pick)), len(pick), 128 ** -0.5)
+    assert_attn_close(bf16_np(o[pick]), ref, "config 5 layer 0 attention")

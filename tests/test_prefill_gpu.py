@@ -56,3 +56,29 @@ def test_prefill_edges(ie, workloads, dev, chunks):
     say(f"prefill edge chunks {chunks}")
     wl = workloads.mixed_workload([], chunks, seed=len(chunks), block_m=128, max_len=4096)
     check(ie, workloads, wl, dev, f"prefill {chunks}")
+
+
+@pytest.mark.parametrize("chunks", [[(2048, 2048)] * 4, [(1024, 7168)] * 4])
+def test_prefill_long_sampled(ie, workloads, dev, chunks):
+    """The long-prefill shapes the benchmark times (4 x 2048 new after 2048 cached, 4 x 1024 new
+    after 7168): every row finite, and rows at the chunk edges, tile and sub-block boundaries
+    and inside checked against the oracle."""
+    say(f"prefill long {chunks} (sampled rows)")
+    max_len = max(L + c for L, c in chunks)
+    wl = workloads.mixed_workload([], chunks, seed=21, block_m=128, max_len=max_len)
+    cu = wl.inputs["cu_seqlens"].numpy()
+    rows = []
+    for e in range(len(chunks)):
+        L = chunks[e][0]
+        rows += [int(cu[e]) + o for o in (0, 1, 63, 64, 127, 128, 129, L // 2, L - 65, L - 1)]
+    ins = {n: t.numpy() for n, t in wl.inputs.items()}
+    kp, vp = okv.dequantize_kv_prefix(cache_np(wl.cache), ins["cu_cached"], ins["slot_ids"])
+    ref = oat.prefill_attention(bf16_np(wl.q), bf16_np(wl.k), bf16_np(wl.v), ins["cu_seqlens"],
+                                ins["tile_start"], wl.block_m, kp, vp, ins["cu_cached"],
+                                rows=rows)
+    g = workloads.mixed_to(wl, dev)
+    out = run_gpu(ie, g)
+    torch.cuda.synchronize()
+    o = bf16_np(out)
+    assert np.isfinite(o).all()
+    assert_attn_close(o[rows], ref[rows], f"prefill long {chunks[0]} x {len(chunks)}")
