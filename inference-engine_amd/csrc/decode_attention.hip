@@ -55,6 +55,7 @@ constexpr int DA_TOK_WAVE = 8 * DA_U;              // 32 tokens per wave block
 constexpr int DA_TOK_WG = DA_WAVES * DA_TOK_WAVE;  // tokens per workgroup step
 constexpr int DA_MIN_PIECE = 128;
 constexpr int DA_MAX_SPLITS = 1024;  // pieces per sequence the combine kernel merges, at most
+constexpr int DA_PLAN_FIRST = 64;    // plan record: sequence b's first work entry at int 64 + b
 constexpr int DA_D = 128;
 constexpr uint32_t K64 = 0x64646464u;
 constexpr float OFFSET = 1152.0f;  // fp16(0x64xx) = 1024 + byte, byte = x + 128
@@ -146,11 +147,12 @@ struct DecodeArgs {
     float scale_log2;  // softmax scale * log2(e)
     uint16_t* out;
     int64_t o_sb, o_sh;
-    float* part_acc;  // [B, Hq, max_splits, 128]
-    float* part_m;    // [B, Hq, max_splits]
-    float* part_l;    // [B, Hq, max_splits]
-    int* plan;        // [0]: this step's piece size, for the combine kernel
-    int target, max_splits, hq;
+    float* part_acc;  // [Hq, nwork, 128]: work entry w's partial output for query head h
+    float* part_m;    // [Hq, nwork]
+    float* part_l;    // [Hq, nwork]
+    int* plan;        // [0]: this step's piece size; [DA_PLAN_FIRST + b]: sequence b's first
+                      // work entry (written when b has more than one piece), for the combine
+    int target, nwork, hq;
     int batch;        // rows of q / cached_lens (num_decoding[0] <= batch)
     int head_fast;    // 1: grid (Hkv, pieces), the KV head in blockIdx.x; 0: grid (pieces, Hkv)
 };
@@ -309,6 +311,7 @@ __attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_split_k
     if (wk.needed == 0) return;
     const int b = uniform(wk.b);
     const int split = uniform(wk.split);
+    if (hk == 0 && split == 0 && wk.needed > 1 && threadIdx.x == 0) a.plan[DA_PLAN_FIRST + b] = item;
     const int piece = uniform(wk.piece);
     const int n_end = uniform(a.cached_lens[b] + 1);
     const int t_begin = split * piece;
@@ -462,7 +465,8 @@ __attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_split_k
     if (wk.needed == 1) {
         a.out[b * a.o_sb + qh_idx * a.o_sh + d] = (uint16_t)f32_to_bf16_rne(num / den);
     } else {
-        const int64_t row = ((int64_t)b * a.hq + qh_idx) * a.max_splits + split;
+        const int64_t row = (int64_t)qh_idx * a.nwork + item;  // the sequence's pieces are
+                                                               // consecutive work entries
         a.part_acc[row * DA_D + d] = num;
         if (d == 0) {
             a.part_m[row] = mx;
@@ -472,22 +476,25 @@ __attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_split_k
 }
 
 // grid (B, Hq), block 128: merge the pieces of sequences that had more than one
-// (kernels.py:216-264), in base 2. The piece size is the one the split kernel recorded in the
-// workspace (one load, together with the sequence's length, instead of a pass over all
-// lengths); a value the split kernel did not write (no split launch before this one) is
-// rejected or clamped, so the reads stay inside the workspace.
+// (kernels.py:216-264), in base 2. The piece size and the sequence's first work entry are the
+// ones the split kernel recorded in the workspace (loaded together with the sequence's length:
+// one memory round trip, no pass over all lengths); values the split kernel did not write (no
+// split launch before this one) are rejected or clamped, so the reads stay inside the
+// workspace.
 __global__ __launch_bounds__(128) void decode_combine_kernel(
     const float* __restrict__ part_acc, const float* __restrict__ part_m,
     const float* __restrict__ part_l, const int* __restrict__ plan,
     const int32_t* __restrict__ cached_lens, const int32_t* __restrict__ num_decoding,
-    uint16_t* __restrict__ out, int64_t o_sb, int64_t o_sh, int hq, int max_splits) {
+    uint16_t* __restrict__ out, int64_t o_sb, int64_t o_sh, int nwork) {
     const int b = blockIdx.x, h = blockIdx.y;
     const int nd = num_decoding[0], piece = plan[0], len = cached_lens[b];
+    const int first_raw = plan[DA_PLAN_FIRST + b];
     if (b >= nd || piece < DA_MIN_PIECE) return;
-    const int needed = min(cdiv_i(len + 1, piece), max_splits);
+    const int first = min(max(first_raw, 0), nwork - 1);
+    const int needed = min(min(cdiv_i(len + 1, piece), DA_MAX_SPLITS), nwork - first);
     if (needed <= 1) return;
     const int d = threadIdx.x;
-    const int64_t row0 = ((int64_t)b * hq + h) * max_splits;
+    const int64_t row0 = (int64_t)h * nwork + first;
     // One memory round trip for all of it: lane s of wave 0 loads split s's (m, l) while every
     // thread loads its first batch of partial outputs; the weights 2^(m_s - max m) go through
     // LDS, and each thread then adds the splits in order (the same sums as one thread alone).
@@ -550,18 +557,22 @@ __global__ __launch_bounds__(64) void decode_plan_kernel(const int32_t* __restri
     }
 }
 
+// Workspace: the plan record (piece size, then each sequence's first work entry; padded to
+// 256 bytes), then fp32 partials (acc, m, l) of every (query head, work entry): one per piece,
+// since pieces never outnumber the split launch's work entries per KV head.
 struct Layout {
-    int target, max_splits;
+    int target, nwork;
     size_t plan_off, acc_off, m_off, l_off, bytes;
 };
 
 static Layout workspace_layout(int batch, int hq, int hkv) {
     Layout L;
+    batch = std::max(batch, 0);
     L.target = std::min(decode_target(hkv), DA_MAX_SPLITS);
-    L.max_splits = L.target;
-    const size_t rows = (size_t)std::max(batch, 0) * hq * L.max_splits;
+    L.nwork = batch <= L.target ? L.target : L.target + batch;
+    const size_t rows = (size_t)hq * L.nwork;
     L.plan_off = 0;
-    L.acc_off = 256;  // the plan record, padded
+    L.acc_off = ((size_t)(DA_PLAN_FIRST + batch) * sizeof(int) + 255) / 256 * 256;
     L.m_off = L.acc_off + rows * DA_D * sizeof(float);
     L.l_off = L.m_off + rows * sizeof(float);
     L.bytes = L.l_off + rows * sizeof(float);
@@ -629,13 +640,13 @@ extern "C" hipError_t ie_decode_attention_split(
     a.part_l = (float*)(ws + L.l_off);
     a.plan = (int*)(ws + L.plan_off);
     a.target = L.target;
-    a.max_splits = L.max_splits;
+    a.nwork = L.nwork;
     a.hq = num_q_heads;
     a.batch = batch;
     // pieces number at most target + nd, and at most target when nd <= target (decode_piece):
     // with batch <= target the grid needs no spare workgroups, which would otherwise hold
     // resident slots while they find out that they are idle
-    const unsigned pieces = batch <= L.target ? L.target : L.target + batch;
+    const unsigned pieces = (unsigned)L.nwork;
     // The order in which the dispatcher hands out workgroups (same results either way): the KV
     // heads of one piece side by side measured 9 % faster at B=64 ctx=1024, but 0.4-0.8 %
     // slower at B=64 ctx=4096 and 3-4 % slower at config 5 (B=32); the host cannot tell the
@@ -686,8 +697,7 @@ extern "C" hipError_t ie_decode_attention_combine(int32_t batch, int32_t num_q_h
     hipLaunchKernelGGL(decode_combine_kernel, grid, dim3(DA_D), 0, stream,
                        (const float*)(ws + L.acc_off), (const float*)(ws + L.m_off),
                        (const float*)(ws + L.l_off), (const int*)(ws + L.plan_off), cached_lens,
-                       num_decoding, (uint16_t*)out, out_stride_b, out_stride_h, num_q_heads,
-                       L.max_splits);
+                       num_decoding, (uint16_t*)out, out_stride_b, out_stride_h, L.nwork);
     return hipGetLastError();
 }
 

@@ -55,11 +55,18 @@ def test_bad_geometry_rejected_on_host(native):
 
 
 def test_workspace_size_formula(native):
+    """The plan record (piece size and one first-entry index per sequence after 64 ints, padded
+    to 256 bytes), then one fp32 partial (128 outputs, m, l) per query head and work entry; the
+    work entries are the split launch's grid: the target, or target + B above it."""
     lib = native.cabi()
-    splits = lib.ie_decode_attention_max_splits(8)
-    assert splits >= 1
-    # a 256-byte plan record (the step's piece size), then the fp32 partials
-    assert lib.ie_decode_attention_workspace_size(64, 16, 128) == 256 + 64 * 16 * splits * 130 * 4
+    target = lib.ie_decode_attention_max_splits(8)
+    assert target >= 1
+    lib.ie_decode_attention_grid.restype = ctypes.c_int32
+    for B in (1, 64, target, target + 1, 300, 1024):
+        grid = lib.ie_decode_attention_grid(ctypes.c_int32(B), ctypes.c_int32(8))
+        assert grid == (target if B <= target else target + B)
+        plan = -(-(64 + B) * 4 // 256) * 256
+        assert lib.ie_decode_attention_workspace_size(B, 16, 128) == plan + 16 * grid * 130 * 4
 
 
 def test_ops_refuse_cpu_tensors(ie):
