@@ -132,12 +132,15 @@ hipError_t ie_fused_rope_kv_decode(const ie_bf16* q, int64_t q_stride_b, int64_t
 
 /*
  * Bytes of device workspace ie_decode_attention needs for `batch` sequences on the current
- * device: a 256-byte plan record (the split launch writes the step's piece size there for the
- * combine launch), then fp32 split-K partials [batch, num_q_heads, max_splits, head_dim + 2].
+ * device: the plan record (the split launch writes the step's piece size and each split
+ * sequence's first work entry there for the combine launch: (64 + batch) ints, padded to 256
+ * bytes), then fp32 split-K partials, head_dim + 2 values per (query head, work entry), where
+ * the work entries are ie_decode_attention_grid(batch, num_q_heads / 2).
  */
 size_t ie_decode_attention_workspace_size(int32_t batch, int32_t num_q_heads, int32_t head_dim);
 
-/* Upper bound on splits per sequence on the current device (the partial buffer stride). */
+/* Upper bound on splits per sequence on the current device (the per-KV-head workgroup target of
+ * the work split: CUs * 2 / num_kv_heads). */
 int32_t ie_decode_attention_max_splits(int32_t num_kv_heads);
 
 /*
@@ -175,6 +178,25 @@ hipError_t ie_decode_attention_combine(int32_t batch, int32_t num_q_heads, int32
                                        int64_t out_stride_b, int64_t out_stride_h,
                                        void* workspace, size_t workspace_bytes,
                                        hipStream_t stream);
+
+/*
+ * ie_decode_attention without a workspace argument, for callers that cannot allocate device
+ * memory (code under hipGraph capture, serving loops and harnesses that forbid allocation). No
+ * counterpart in the reference. The split-K partials and the plan record live in a static
+ * device array of ie_decode_attention_noalloc_max_bytes() bytes (16 MiB) that each device the
+ * library runs on holds until the process ends; a batch whose workspace
+ * (ie_decode_attention_workspace_size) exceeds it returns hipErrorInvalidValue. Allocates
+ * nothing; the first call on a device looks up the array's address there (make it outside
+ * graph capture). Every call on a device shares the array: calls that overlap on one device
+ * race. Same arguments, results and errors as ie_decode_attention otherwise.
+ */
+size_t ie_decode_attention_noalloc_max_bytes(void);
+hipError_t ie_decode_attention_noalloc(const ie_bf16* q, int64_t q_stride_b, int64_t q_stride_h,
+                                       int32_t batch, int32_t num_q_heads,
+                                       const ie_kv_cache* cache, const int32_t* cached_lens,
+                                       const int32_t* slot_ids, const int32_t* num_decoding,
+                                       float scale, ie_bf16* out, int64_t out_stride_b,
+                                       int64_t out_stride_h, hipStream_t stream);
 
 /*
  * The split launch's work list, for tests and diagnostics: the work split of

@@ -23,6 +23,8 @@
 //   with DPP. Online softmax in base 2 per lane group; groups and waves are merged at the end
 //   (log-sum-exp), then either the output is written (one piece) or fp32 partials
 //   (m, l, acc) go to the workspace for the combine kernel (kernels.py:216-264).
+#include <mutex>
+
 #include "ie_common.h"
 
 // Launch shape (measured on MI355X, B=64 ctx=4096): 8-wave workgroups, 2 per CU (the
@@ -717,4 +719,64 @@ extern "C" hipError_t ie_decode_attention(const ie_bf16* q, int64_t q_stride_b,
                                        (int)cache->num_kv_heads, cached_lens, num_decoding, out,
                                        out_stride_b, out_stride_h, workspace, workspace_bytes,
                                        stream);
+}
+
+// ---------------------------------------------------------------------------------------------
+// The entry point that allocates nothing: ie_decode_attention with its workspace in a static
+// device array of DA_SCRATCH_BYTES, which every device the library runs on holds until the
+// process ends (16 MiB: the plan and partials of up to 1,952 sequences at 16 query / 8 KV
+// heads on 256 CUs). The array's name is only a host-side stand-in for the device copy, so its
+// address on each device is looked up once, with that device current, and only that address
+// is passed to the kernels. The workspace needs no clearing: every call's split launch writes
+// the plan and the partials its combine launch reads. All calls on one device share the array,
+// so calls that overlap on one device (different streams, or threads without ordering) race.
+// ---------------------------------------------------------------------------------------------
+namespace {
+constexpr size_t DA_SCRATCH_BYTES = size_t(16) << 20;
+constexpr int DA_SCRATCH_DEVICES = 64;
+__device__ __align__(256) unsigned char scratch[DA_SCRATCH_BYTES];
+std::mutex scratch_mu;
+void* scratch_ptr[DA_SCRATCH_DEVICES];
+
+// This device's copy of `scratch` (resolved on the first call made with the device current).
+hipError_t scratch_address(void** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    IE_REQUIRE(dev >= 0 && dev < DA_SCRATCH_DEVICES, "device index out of range");
+    std::lock_guard<std::mutex> lock(scratch_mu);
+    if (scratch_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        IE_REQUIRE(p != nullptr, "no device address for the decode scratch");
+        scratch_ptr[dev] = p;
+    }
+    *out = scratch_ptr[dev];
+    return hipSuccess;
+}
+}  // namespace
+
+extern "C" size_t ie_decode_attention_noalloc_max_bytes(void) { return DA_SCRATCH_BYTES; }
+
+extern "C" hipError_t ie_decode_attention_noalloc(
+    const ie_bf16* q, int64_t q_stride_b, int64_t q_stride_h, int32_t batch, int32_t num_q_heads,
+    const ie_kv_cache* cache, const int32_t* cached_lens, const int32_t* slot_ids,
+    const int32_t* num_decoding, float scale, ie_bf16* out, int64_t out_stride_b,
+    int64_t out_stride_h, hipStream_t stream) {
+    hipError_t e = check_cache(cache);
+    if (e != hipSuccess) return e;
+    IE_REQUIRE(batch >= 0, "negative batch");
+    if (batch == 0) return hipSuccess;
+    IE_REQUIRE(num_q_heads == 2 * cache->num_kv_heads, "num_q_heads must be 2 * num_kv_heads");
+    const Layout L = workspace_layout(batch, num_q_heads, (int)cache->num_kv_heads);
+    IE_REQUIRE(L.bytes <= DA_SCRATCH_BYTES,
+               "batch too large for the no-alloc decode scratch (16 MiB; use ie_decode_attention "
+               "with a workspace)");
+    void* ws = nullptr;
+    e = scratch_address(&ws);
+    if (e != hipSuccess) return e;
+    return ie_decode_attention(q, q_stride_b, q_stride_h, batch, num_q_heads, cache, cached_lens,
+                               slot_ids, num_decoding, scale, out, out_stride_b, out_stride_h, ws,
+                               DA_SCRATCH_BYTES, stream);
 }
