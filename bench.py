@@ -5,10 +5,11 @@ D=128 — µs per layer and achieved HBM GB/s against the 8 TB/s peak. One step 
 `decode_attention` call (split kernel + reduce kernel) over the whole batch, inputs resident in
 HBM. Distinct cache sets are rotated between steps so the 256 MB MALL cannot serve a repeat.
 
-Also reported beside it (extra keys): config-4 KV quantize-on-write, chunked-prefill attention
-and the prefill q/k RMSNorm + RoPE of its 1,024 packed tokens, token sampling and the projection
-GEMMs at config 5's shape, each timed with HIP events on the stream the kernels run on, and
-config 5: a whole
+Also reported beside it (extra keys): config-4 KV quantize-on-write, chunked-prefill attention,
+the prefill q/k RMSNorm + RoPE of its 1,024 packed tokens and the whole config-4 attention step,
+token sampling and the projection GEMMs at config 5's shape, each timed with HIP events on the
+stream the kernels run on; the CPU baseline (the same math in PyTorch on the host cores) for
+the headline, the config-4 KV write and the config-4 prefill; and config 5: a whole
 greedy decode step of a Qwen3-1.7B-shaped model (28 layers, random weights, B=32, ctx ~
 U[128, 4096)) replayed as a hipGraph, with the share of the step spent in the attention kernels
 (the same kernels captured alone).
@@ -44,8 +45,9 @@ def _events(n):
 
 
 def time_decode(ie, wls, steps, warmup):
-    """Whole-step time (events at the ends) and the split kernel's own average duration
-    (events around each launch, separate pass)."""
+    """Whole-step time (split + combine, back to back between two events) and, in a separate
+    pass, the split kernel's average duration from back-to-back split-only launches between two
+    events (events around each launch of a ~90 us kernel would add their own microseconds)."""
     K = ie.kernels
     outs = [torch.empty_like(w.q) for w in wls]
     wss = [K.decode_attention_workspace(w.q) for w in wls]
@@ -68,20 +70,23 @@ def time_decode(ie, wls, steps, warmup):
     torch.cuda.synchronize()
     step_ms = e0.elapsed_time(e1) / steps
 
-    ev = _events(3 * steps)
-    for i in range(steps):
+    def split(i):
         w = wls[i % len(wls)]
-        o, ws = outs[i % len(wls)], wss[i % len(wls)]
-        ev[3 * i].record()
         K.decode_attention_split(w.q, w.cache, w.cached_lens, w.slot_ids, w.num_decoding, SCALE,
-                                 o, ws)
-        ev[3 * i + 1].record()
-        K.decode_attention_combine(w.q, w.cache, w.cached_lens, w.num_decoding, o, ws)
-        ev[3 * i + 2].record()
+                                 outs[i % len(wls)], wss[i % len(wls)])
+
+    for i in range(max(10, warmup // 10)):
+        split(i)
     torch.cuda.synchronize()
-    split_ms = sum(ev[3 * i].elapsed_time(ev[3 * i + 1]) for i in range(steps)) / steps
-    comb_ms = sum(ev[3 * i + 1].elapsed_time(ev[3 * i + 2]) for i in range(steps)) / steps
-    return step_ms, split_ms, comb_ms
+    e0, e1 = _events(2)
+    e0.record()
+    for i in range(steps):
+        split(i)
+    e1.record()
+    torch.cuda.synchronize()
+    split_ms = e0.elapsed_time(e1) / steps
+    # the combine's share: what the whole step takes beyond its split launch
+    return step_ms, split_ms, max(0.0, step_ms - split_ms)
 
 
 def time_op(fn, steps, warmup):
@@ -217,32 +222,96 @@ def time_graph_calls(fns, reps=3):
     return e0.elapsed_time(e1) / (reps * len(fns))
 
 
-def cpu_baseline(wl_gpu, min_seconds):
-    """The numpy oracle (the reference math restated, fp32 dequant/scores/softmax/PV) on the
-    whole headline batch, one thread, repeated until `min_seconds` of CPU work have run."""
-    import numpy as np
-    from threadpoolctl import threadpool_limits
+def cpu_threads() -> int:
+    """Host threads for the CPU baseline: the cores this process may run on, capped by the
+    box's OMP_NUM_THREADS share when one is set."""
+    n = len(os.sched_getaffinity(0))
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    return min(n, int(omp)) if omp.isdigit() and int(omp) > 0 else n
 
-    from oracle import attention as oat
-    from oracle import kv_cache as okv
 
+def _repeat(fn, min_seconds):
+    fn()  # first call: allocator and thread-pool warm-up, not timed
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        reps += 1
+        dt = time.perf_counter() - t0
+        if dt >= min_seconds and reps >= 2:
+            return dt / reps, dt, reps
+
+
+def cpu_baselines(wl_gpu, alg_bytes, W, min_seconds):
+    """The reference attention math restated in PyTorch (oracle/torch_cpu.py: fp32 dequant,
+    scores, softmax, PV; batches in slices of <= 16 sequences) on the host cores, on the same
+    kind of inputs: the headline decode batch (its 64 cache rows copied to host memory), and
+    config 4's KV write and chunked-prefill attention. Each is repeated for at least
+    `min_seconds` (the decode sample) or a third of it (the two config-4 ops)."""
+    from oracle import torch_cpu as otc
+
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
     B = len(wl_gpu.ctx)
     slots = wl_gpu.slot_ids.long()
     c = wl_gpu.cache
-    cache = okv.CacheArrays(*(t[slots].cpu().numpy() for t in
-                              (c.k, c.v, c.k_scale, c.v_scale, c.k_calibration)))
-    q = wl_gpu.q.float().cpu().numpy()
-    lens = wl_gpu.cached_lens.cpu().numpy()
-    reps = 0
-    with threadpool_limits(1):
-        t0 = time.perf_counter()
-        while True:
-            oat.decode_attention(q, cache, lens, np.arange(B), B, SCALE)
-            reps += 1
-            dt = time.perf_counter() - t0
-            if dt >= min_seconds and reps >= 2:
-                break
-    return dt * 1e6 / reps, dt, reps
+    k, v, ks, vs = (t[slots].cpu() for t in (c.k, c.v, c.k_scale, c.v_scale))
+    q = wl_gpu.q.cpu()
+    lens = wl_gpu.cached_lens.cpu()
+    rows = torch.arange(B, dtype=torch.int32)
+    per, dt, reps = _repeat(lambda: otc.decode_attention(q, k, v, ks, vs, lens, rows, B, SCALE),
+                            min_seconds)
+    res = {"value": round(alg_bytes / per / 1e9, 3), "unit": "GB/s",
+           "us_per_layer": round(per * 1e6, 1), "cores": threads, "kind": "port",
+           "sample": f"the whole headline batch ({B} sequences at ctx {wl_gpu.ctx[0]}, "
+                     f"slices of {otc.SLICE}), {reps} passes in {dt:.1f} s",
+           "cpu": _cpu_model(), "torch_threads": torch.get_num_threads()}
+    del k, v, ks, vs
+    mw = W.config4(seed=0)
+    gi = mw.inputs
+    nd = int(gi["num_decoding"][0])
+    cache = mw.cache
+    kv_per, kv_dt, kv_reps = _repeat(lambda: otc.quantize_kv_prefill(
+        mw.k, mw.v, gi["cu_seqlens"], gi["slot_ids"], gi["cached_lens"], nd, cache.k, cache.v,
+        cache.k_scale, cache.v_scale, cache.k_calibration), min_seconds / 3)
+    n_new = sum(L for L, _ in mw.chunks)
+    kv_bytes = n_new * 8 * (128 * 2 * 2 + 128 * 2 + 8)
+    res["kv_write_config4"] = {"us": round(kv_per * 1e6, 1),
+                               "GBps": round(kv_bytes / kv_per / 1e9, 3),
+                               "sample": f"{kv_reps} calls in {kv_dt:.1f} s"}
+    pf_per, pf_dt, pf_reps = _repeat(lambda: otc.prefill_attention(
+        mw.q, mw.k, mw.v, gi["cu_seqlens"], gi["slot_ids"], gi["cu_cached"], nd, cache.k,
+        cache.v, cache.k_scale, cache.v_scale, cache.k_calibration), min_seconds / 3)
+    flops = W.prefill_flops(mw.chunks)
+    res["prefill_config4"] = {"us": round(pf_per * 1e6, 1),
+                              "GFLOPs": round(flops / pf_per / 1e9, 1),
+                              "sample": f"{pf_reps} calls in {pf_dt:.1f} s"}
+    return res
+
+
+def bench_mixed_step(W, dev):
+    """Config 4 as one attention step (qwen3-1.7b/architecture.py:124-197 through
+    attention_layer.attention: prefill norm/RoPE of all 1,054 rows, KV quantize-on-write,
+    prefill attention over the int8 prefix, decode norm/RoPE/write and decode attention of the
+    30 decoders into the same output), captured as a hipGraph and replayed."""
+    al = importlib.import_module("inference-engine_amd.attention_layer")
+    wl = W.mixed_to(W.config4(seed=0), dev)
+    gi = wl.inputs
+    N = wl.q.shape[0]
+    g = torch.Generator().manual_seed(0)
+    qkv = torch.randn(N, 32 * 128, generator=g).bfloat16().to(dev)
+    q, k, v = qkv[:, :2048].view(N, 16, 128), qkv[:, 2048:3072].view(N, 8, 128), \
+        qkv[:, 3072:].view(N, 8, 128)
+    w = torch.ones(2, 128, dtype=torch.bfloat16, device=dev)
+    cos, sin = al.rope_tables(gi["positions"], al.rope_inv_freq(128, 1e6, dev))
+    ps = al.PrefixScratch(None, None, gi["cu_cached"])
+    op = lambda: al.attention(q, k, v, gi["seq_ids"], gi["cu_seqlens"], cos, sin, wl.cache,
+                              gi["cached_lens"], gi["slot_ids"], gi["tile_start"], wl.block_m, ps,
+                              gi["num_decoding"], w[0], w[1], 1e-6)
+    ms = time_graph(op)
+    return {"us_graph": round(ms * 1e3, 2), "rows": N, "decoders": len(wl.decode_ctx),
+            "prefill_tokens": sum(L for L, _ in wl.chunks),
+            "kernels": "fused_norm_rope_prefill, quantize_kv_prefill, prefill_attention "
+                       "(+ combine), fused_rope_kv_decode, decode_attention split + combine"}
 
 
 def bench_step(steps, warmup, dev):
@@ -299,61 +368,10 @@ def read_traffic():
     return None
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    # the warm-up also brings the device's clocks up from idle: 300 decode steps (~27 ms) do;
-    # 10 measured 3-5 % slower on the same box
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=300)
-    ap.add_argument("--batch", type=int, default=64)
-    ap.add_argument("--ctx", type=int, default=4096)
-    ap.add_argument("--rotate", type=int, default=2, help="distinct cache sets cycled per step")
-    ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0,
-                    help="minimum CPU-baseline work (whole batch, repeated)")
-    ap.add_argument("--no-step", action="store_true", help="skip the config-5 decode step")
-    ap.add_argument("--norm-rope-tokens", type=int, default=1024,
-                    help="packed tokens of the prefill norm/rope line (config 4: 1024)")
-    ap.add_argument("--sweep", action="store_true", help="also time the config-3 shape sweep")
-    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
-                    help="first run a plain device copy of MIB MiB 3 times (PMC calibration)")
-    args = ap.parse_args()
-
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(decode attention shards by sequence or KV head without exchange); "
-              "run with --gpus 1", file=sys.stderr)
-        sys.exit(2)
-
-    ie = importlib.import_module("inference-engine_amd")
-    W = importlib.import_module("inference-engine_amd.workloads")
-    K = ie.kernels
-    dev = "cuda:0"
-    torch.cuda.set_device(0)
-
-    if args.copy_probe:
-        n = args.copy_probe << 20
-        src = torch.ones(n, dtype=torch.uint8, device=dev)
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        log(f"copy probe: 3 x {n} bytes read + written")
-        del src, dst
-
-    ctx = [args.ctx] * args.batch
-    log(f"building {args.rotate} cache sets B={args.batch} ctx={args.ctx}")
-    wls = [W.decode_workload(ctx, seed=s, device=dev) for s in range(args.rotate)]
-    torch.cuda.synchronize()
-    alg_bytes = wls[0].algorithmic_bytes()
-    log("timing decode attention")
-    step_ms, split_ms, comb_ms = time_decode(ie, wls, args.steps, args.warmup)
-    gbs = alg_bytes / (step_ms * 1e-3) / 1e9
-    split_gbs = alg_bytes / (split_ms * 1e-3) / 1e9
-    log(f"decode step {step_ms*1e3:.2f} us ({gbs:.0f} GB/s); split kernel {split_ms*1e3:.2f} us "
-        f"({split_gbs:.0f} GB/s), combine {comb_ms*1e3:.2f} us")
-
+def extras(args, ie, W, K, dev, alg_bytes) -> dict:
+    """Every line beside the headline: the read probe, config 4 (KV write, prefill, the whole
+    mixed step), long prefills, the prefill norm/rope, config 5's sampler and projections, the
+    config-5 step and (with --sweep) the config-3 sweep."""
     extra = {}
     # ---- the attainable read rate on this device: a pure 16-byte read stream (ie_hbm_read_probe)
     # over as many bytes as one decode launch reads, past the 256 MB last-level cache, two
@@ -472,6 +490,12 @@ def main():
     except Exception as e:  # reported, never silently replaced
         extra["linear_config5"] = {"error": str(e).splitlines()[0][:200]}
 
+    try:
+        extra["mixed_step_config4"] = bench_mixed_step(W, dev)
+        log(f"mixed step config4 {extra['mixed_step_config4']}")
+    except Exception as e:  # reported, never silently replaced
+        extra["mixed_step_config4"] = {"error": str(e).splitlines()[0][:200]}
+
     if not args.no_step:
         log("config 5: Qwen3-1.7B-shaped decode step (hipGraph)")
         try:
@@ -494,15 +518,83 @@ def main():
                 torch.cuda.empty_cache()
         extra["decode_sweep"] = sweep
 
+    return extra
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    # the warm-up also brings the device's clocks up from idle: 300 decode steps (~27 ms) do;
+    # 10 measured 3-5 % slower on the same box
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=300)
+    ap.add_argument("--batch", type=int, default=64)
+    ap.add_argument("--ctx", type=int, default=4096)
+    ap.add_argument("--rotate", type=int, default=2, help="distinct cache sets cycled per step")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="minimum CPU-baseline decode work (whole batch, repeated); the config-4 "
+                         "KV write and prefill baselines run a third of it each")
+    ap.add_argument("--no-step", action="store_true", help="skip the config-5 decode step")
+    ap.add_argument("--norm-rope-tokens", type=int, default=1024,
+                    help="packed tokens of the prefill norm/rope line (config 4: 1024)")
+    ap.add_argument("--sweep", action="store_true", help="also time the config-3 shape sweep")
+    ap.add_argument("--headline-only", action="store_true",
+                    help="only the headline decode timing (for kernel traces and PMC passes: "
+                         "every decode launch of the run is then a headline launch)")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="first run a plain device copy of MIB MiB 3 times (PMC calibration)")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(decode attention shards by sequence or KV head without exchange); "
+              "run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    ie = importlib.import_module("inference-engine_amd")
+    W = importlib.import_module("inference-engine_amd.workloads")
+    K = ie.kernels
+    dev = "cuda:0"
+    torch.cuda.set_device(0)
+
+    if args.copy_probe:
+        n = args.copy_probe << 20
+        src = torch.ones(n, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copy probe: 3 x {n} bytes read + written")
+        del src, dst
+
+    ctx = [args.ctx] * args.batch
+    log(f"building {args.rotate} cache sets B={args.batch} ctx={args.ctx}")
+    wls = [W.decode_workload(ctx, seed=s, device=dev) for s in range(args.rotate)]
+    torch.cuda.synchronize()
+    alg_bytes = wls[0].algorithmic_bytes()
+    log("timing decode attention")
+    step_ms, split_ms, comb_ms = time_decode(ie, wls, args.steps, args.warmup)
+    gbs = alg_bytes / (step_ms * 1e-3) / 1e9
+    split_gbs = alg_bytes / (split_ms * 1e-3) / 1e9
+    log(f"decode step {step_ms*1e3:.2f} us ({gbs:.0f} GB/s); split kernel {split_ms*1e3:.2f} us "
+        f"({split_gbs:.0f} GB/s), combine {comb_ms*1e3:.2f} us")
+
+    extra = {}
+    if args.headline_only:
+        args.no_cpu = True
+    else:
+        extra.update(extras(args, ie, W, K, dev, alg_bytes))
+
     cpu = None
     if not args.no_cpu:
-        log("cpu baseline (numpy oracle, 1 thread)")
-        us_cpu, dt, reps = cpu_baseline(wls[0], args.cpu_seconds)
-        cpu = {"value": round(alg_bytes / (us_cpu * 1e-6) / 1e9, 3), "unit": "GB/s",
-               "us_per_layer": round(us_cpu, 1), "cores": 1, "kind": "port",
-               "sample": f"the whole batch ({args.batch} sequences at ctx {args.ctx}), "
-                         f"{reps} passes in {dt:.1f} s", "cpu": _cpu_model()}
+        log(f"cpu baseline (PyTorch on {cpu_threads()} host threads)")
+        cpu = cpu_baselines(wls[0], alg_bytes, W, args.cpu_seconds)
+        log(f"cpu baseline {cpu}")
     traffic = read_traffic()
+    if split_ms > step_ms:
+        log(f"warning: split-only launches ({split_ms*1e3:.2f} us) measured longer than the "
+            f"whole step ({step_ms*1e3:.2f} us)")
     line = {
         "metric": METRIC,
         "value": round(gbs, 1),
@@ -525,9 +617,11 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(split_gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(split_gbs / HBM_PEAK_GBS, 4),
                      "traffic": traffic, "kernel": "decode_split_kernel",
-                     "kernel_us": round(split_ms * 1e3, 2)},
+                     "kernel_us": round(split_ms * 1e3, 2),
+                     "kernel_us_from": "back-to-back split launches between two HIP events on "
+                                       "the launch stream"},
         "cpu_baseline": cpu,
-        "combine_us": round(comb_ms * 1e3, 2),
+        "step_minus_split_us": round(comb_ms * 1e3, 2),
         **extra,
     }
     print(json.dumps(line), flush=True)

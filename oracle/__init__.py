@@ -13,6 +13,8 @@ Modules
   attention  decode attention (reference rounding points, split-K form, float64 textbook)
              and causal chunked-prefill attention
   work_split the split-K work partition of the decode kernel (integer restatement)
+  torch_cpu  the same decode / KV write / prefill math in PyTorch fp32 on the host cores: the
+             benchmark's CPU baseline (bench.py's cpu_baseline leg only)
 
 Pinning (what checks each function independently of this restatement; see tests/test_oracle_*):
   quantize_rows / calibration   closed-form known answers (zero rows, one-hot, exact ties, clamp,
@@ -31,6 +33,8 @@ Pinning (what checks each function independently of this restatement; see tests/
                                 causal+prefix mask; brute-force per-row loop on tiny shapes
   decode_work_plan              brute-force coverage properties (every token of every decoding
                                 sequence covered exactly once, <= target+B work items)
+  torch_cpu                     decode and prefill against the float64 textbook forms (2e-5),
+                                the KV write bit for bit against quantize_kv_prefill
 The reference ships no tests, golden vectors or fixtures (it has no test suite at all), so no
 reference-held vector pins any function; the reference kernels need a GPU and Triton and are not
 run here.
