@@ -173,7 +173,8 @@ __device__ __forceinline__ v4u ld128(rsrc_t r, int off) {
 struct LaneState {
     float m[2], l[2], ps[2];
     float acc[2][16];
-    float ve;  // an integer
+    float ve;       // an integer
+    uint32_t vlo;   // bits of 2^(8 - ve): the V scales this ve serves are [2^(8-ve), 2^(15-ve))
 };
 
 // Registers of one 32-token block of a wave: lane group g holds tokens t0+4g .. t0+4g+3,
@@ -191,15 +192,18 @@ __device__ __forceinline__ void load_block(KVRegs& r, rsrc_t rows, rsrc_t scales
     r.scale = ld128(scales, tok * 4);
 }
 
-// Scores of the block in base 2, scaled: s = (q.k - 1152 sum q) * k_scale * scale*log2e / 2^e.
+// Scores of the block in base 2 up to the head's factor kmul (applied in block_pv):
+// t = (q.k - 1152 sum q) * k_scale, where q is q * 2^e in fp16 and kmul = scale * log2(e) / 2^e.
+// The 1152 sum q offset enters as the dot chain's starting value: qoff = -1152 sum q / 8 in
+// each of the 8 lanes of a row, which the row sum adds up. qoff and kmul are wave-uniform.
 // With MASKED, tokens at or past t_end score -inf (their loads returned zeros: buffer range).
 template <bool MASKED>
-__device__ __forceinline__ void block_scores(float (&s)[DA_U][2], const KVRegs& k,
-                                             const half2_t (&qh)[2][8], const float (&qsum)[2],
-                                             const float (&kmul)[2], int tok, int t_end) {
+__device__ __forceinline__ void block_scores(float (&t)[DA_U][2], const KVRegs& k,
+                                             const half2_t (&qh)[2][8], const float (&qoff)[2],
+                                             int tok, int t_end) {
 #pragma unroll
     for (int u = 0; u < DA_U; ++u) {
-        float d0 = 0.0f, d1 = 0.0f;
+        float d0 = qoff[0], d1 = qoff[1];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const uint32_t x = k.x[u][i] ^ 0x80808080u;
@@ -213,42 +217,47 @@ __device__ __forceinline__ void block_scores(float (&s)[DA_U][2], const KVRegs& 
         d0 = sum8(d0);
         d1 = sum8(d1);
         const float ks = __uint_as_float(k.scale[u]);
-        s[u][0] = (d0 - qsum[0]) * (ks * kmul[0]);
-        s[u][1] = (d1 - qsum[1]) * (ks * kmul[1]);
-        if (MASKED && tok + u >= t_end) s[u][0] = s[u][1] = -INFINITY;
+        t[u][0] = d0 * ks;
+        t[u][1] = d1 * ks;
+        if (MASKED && tok + u >= t_end) t[u][0] = t[u][1] = -INFINITY;
     }
 }
 
-// Online-softmax update of the lane group and the PV accumulation of the block.
-__device__ __forceinline__ void block_pv(LaneState& st, const float (&s)[DA_U][2],
-                                         const KVRegs& v) {
+// Online-softmax update of the lane group and the PV accumulation of the block; scores are
+// s = t * kmul (kmul > 0).
+__device__ __forceinline__ void block_pv(LaneState& st, const float (&t)[DA_U][2],
+                                         const KVRegs& v, const float (&kmul)[2]) {
     // The block's largest V scale vmax lies in [2^(ex-1), 2^ex). With p <= 2^ve the products
-    // stay below 2^15 while ex + ve <= 15; the exponent is re-chosen (vmax * 2^ve in
-    // [2^14, 2^15)) when that fails, or when ex + ve < 9, i.e. the scales fell by 2^6 or more
-    // and small products would lose precision. The state is rescaled by the exact power of two
-    // and m moves with ve. Scales past the piece's end load as 0; a block of them changes
-    // nothing.
+    // stay below 2^15 while vmax < 2^(15-ve); the exponent is re-chosen (ve = 15 - ex, so
+    // vmax * 2^ve lies in [2^14, 2^15)) when that fails, or when vmax < 2^(8-ve), i.e. the
+    // scales fell by 2^6 or more and small products would lose precision. Both bounds are one
+    // unsigned compare on the float bits. The state is rescaled by the exact power of two and
+    // m moves with ve. Scales past the piece's end load as 0 and change nothing.
     const float vmax = fmaxf(fmaxf(__uint_as_float(v.scale[0]), __uint_as_float(v.scale[1])),
                              fmaxf(__uint_as_float(v.scale[2]), __uint_as_float(v.scale[3])));
-    const float ex = (float)__builtin_amdgcn_frexp_expf(vmax);
-    const float t = ex + st.ve;
-    if (!(t >= 9.0f && t <= 15.0f) && vmax > 0.0f) {
-        const float d = 15.0f - t;  // the new ve is 15 - ex
-        const float r = ldexpf(1.0f, (int)d);
+    if (__float_as_uint(vmax) - st.vlo >= (7u << 23)) {
+        if (vmax > 0.0f) {
+            const int ex = __builtin_amdgcn_frexp_expf(vmax);
+            const float ve = (float)(15 - ex);
+            const float d = ve - st.ve;
+            const float r = ldexpf(1.0f, (int)d);
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
+            for (int h = 0; h < 2; ++h) {
 #pragma unroll
-            for (int j = 0; j < 16; ++j) st.acc[h][j] *= r;
-            st.l[h] *= r;
-            st.ps[h] *= r;
-            st.m[h] -= d;  // -inf stays -inf
+                for (int j = 0; j < 16; ++j) st.acc[h][j] *= r;
+                st.l[h] *= r;
+                st.ps[h] *= r;
+                st.m[h] -= d;  // -inf stays -inf
+            }
+            st.ve = ve;
+            st.vlo = (uint32_t)(ex - 7 + 127) << 23;
         }
-        st.ve += d;
     }
-    float msafe[2];
+    float nms[2];  // minus the effective running max, the exp2 argument's offset
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-        const float mt = fmaxf(fmaxf(s[0][h], s[1][h]), fmaxf(s[2][h], s[3][h])) - st.ve;
+        const float mt =
+            fmaxf(fmaxf(t[0][h], t[1][h]), fmaxf(t[2][h], t[3][h])) * kmul[h] - st.ve;
         if (mt > st.m[h]) {
             const float alpha = exp2_safe(st.m[h] - mt);  // m = -inf -> 0
 #pragma unroll
@@ -258,15 +267,15 @@ __device__ __forceinline__ void block_pv(LaneState& st, const float (&s)[DA_U][2
             st.m[h] = mt;
         }
         // p = 2^(s - max + ve) <= 2^ve
-        msafe[h] = st.m[h] == -INFINITY ? 0.0f : st.m[h];
+        nms[h] = st.m[h] == -INFINITY ? 0.0f : -st.m[h];
     }
     half2_t pp[DA_U / 2][2];  // (p * v_scale * 2^ve) of token pairs, fp16
 #pragma unroll
     for (int pr = 0; pr < DA_U / 2; ++pr)
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            const float pa = exp2_safe(s[2 * pr][h] - msafe[h]);
-            const float pb = exp2_safe(s[2 * pr + 1][h] - msafe[h]);
+            const float pa = exp2_safe(__builtin_fmaf(t[2 * pr][h], kmul[h], nms[h]));
+            const float pb = exp2_safe(__builtin_fmaf(t[2 * pr + 1][h], kmul[h], nms[h]));
             st.l[h] += pa + pb;
             pp[pr][h] = half2_t{(_Float16)(pa * __uint_as_float(v.scale[2 * pr])),
                                 (_Float16)(pb * __uint_as_float(v.scale[2 * pr + 1]))};
@@ -325,7 +334,7 @@ __attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_split_k
 
     // ---- q of the two heads of this KV head, channels [16cc, 16cc + 16) ----
     half2_t qh[2][8];
-    float qsum[2], kmul[2];
+    float qoff[2], kmul[2];  // wave-uniform (kept in SGPRs)
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         const uint16_t* qp = a.q + b * a.q_sb + (2 * hk + h) * a.q_sh + 16 * cc;
@@ -353,8 +362,8 @@ __attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_split_k
             qh[h][i] = half2_t{lo, hi};
             s += (float)lo + (float)hi;
         }
-        qsum[h] = sum8(s) * OFFSET;
-        kmul[h] = a.scale_log2 / sc;
+        qoff[h] = __int_as_float(uniform(__float_as_int(sum8(s) * (-OFFSET / 8.0f))));
+        kmul[h] = __int_as_float(uniform(__float_as_int(a.scale_log2 / sc)));
     }
 
     // Buffer resources over this (slot, kv head) row, bounded at the piece's end.
@@ -377,6 +386,7 @@ __attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_split_k
         for (int j = 0; j < 16; ++j) st.acc[h][j] = 0.0f;
     }
     st.ve = 0.0f;
+    st.vlo = (uint32_t)(8 + 127) << 23;
 
     // Rolling pipeline: the next block's K is requested as soon as this block's scores are
     // done and its V as soon as this block's PV is done, so every load has half a block of
@@ -394,14 +404,14 @@ __attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_split_k
     load_block(vr, rv, rvs, t0 + 4 * g, cc);
     float s[DA_U][2];
     for (int j = 0; j < nfull; ++j, t0 += DA_TOK_WG) {
-        block_scores<false>(s, kr, qh, qsum, kmul, t0 + 4 * g, t_end);
+        block_scores<false>(s, kr, qh, qoff, t0 + 4 * g, t_end);
         load_block(kr, rk, rks, t0 + DA_TOK_WG + 4 * g, cc);
-        block_pv(st, s, vr);
+        block_pv(st, s, vr, kmul);
         load_block(vr, rv, rvs, t0 + DA_TOK_WG + 4 * g, cc);
     }
     if (nfull < cw) {
-        block_scores<true>(s, kr, qh, qsum, kmul, t0 + 4 * g, t_end);
-        block_pv(st, s, vr);
+        block_scores<true>(s, kr, qh, qoff, t0 + 4 * g, t_end);
+        block_pv(st, s, vr, kmul);
     }
 
     float (&m)[2] = st.m;
@@ -435,15 +445,20 @@ __attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_split_k
         }
     }
 
-    // ---- merge the 4 waves through LDS ----
+    // ---- merge the 8 waves through LDS ----
     __shared__ float s_acc[DA_WAVES][2][DA_D];
     __shared__ float s_m[DA_WAVES][2], s_l[DA_WAVES][2];
+    // the lane's channel group, derived afresh from the thread index: keeping the prologue's copy
+    // alive across the loop costs a register the loop needs
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    const int ccm = tid & 7;
     if (g == 0) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
 #pragma unroll
-            for (int j = 0; j < 16; ++j) s_acc[wave][h][16 * cc + j] = acc[h][j];
-            if (cc == 0) {
+            for (int j = 0; j < 16; ++j) s_acc[wave][h][16 * ccm + j] = acc[h][j];
+            if (ccm == 0) {
                 s_m[wave][h] = mw[h];
                 s_l[wave][h] = l[h];
             }
