@@ -121,13 +121,13 @@ __device__ Work decode_assign(const int32_t* __restrict__ cached_lens, int nd, i
         const int excl = incl - s;
         const unsigned long long hit = __ballot(s > 0 && excl <= w && w < incl);
         if (hit) {
-            const int src = __ffsll((long long)hit) - 1;
+            const int src = __ffsll((long long)hit) - 1;  // wave-uniform
             r.b = b0 + src;
-            r.split = w - __shfl(excl, src, IE_WAVE);
-            r.needed = __shfl(s, src, IE_WAVE);
+            r.split = w - __builtin_amdgcn_readlane(excl, src);
+            r.needed = __builtin_amdgcn_readlane(s, src);
             return r;
         }
-        before = __shfl(incl, 63, IE_WAVE);
+        before = __builtin_amdgcn_readlane(incl, 63);
     }
     return r;
 }

@@ -80,14 +80,17 @@ __device__ __forceinline__ float sum_xor32(float x) {
 
 __host__ __device__ inline int cdiv_i(int a, int b) { return (a + b - 1) / b; }
 
-// Integer sum over the wave (every lane gets it) and inclusive prefix sum in lane order.
+// Inclusive prefix sum in lane order, on the VALU: shifts by 1, 2, 4 and 8 lanes inside each
+// row of 16 (row_shr; a lane whose source lies outside its row adds 0), then each row's total
+// carried into the rows after it with row_bcast:15 (rows 1 and 3) and row_bcast:31 (rows 2
+// and 3).
 __device__ __forceinline__ int wave_incl_scan_i(int x) {
-    const int lane = threadIdx.x & 63;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const int y = __shfl_up(x, d, IE_WAVE);
-        if (lane >= d) x += y;
-    }
+    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);
+    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);
+    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);
+    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);
+    x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);
+    x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);
     return x;
 }
 

@@ -96,7 +96,7 @@ __device__ __forceinline__ QpBlock qp_locate(int u, const int32_t* __restrict__ 
         const unsigned long long hit = __ballot(u < incl && u >= incl - nb);
         if (hit) {
             const int src = __builtin_ctzll(hit);
-            auto from = [&](int x) { return __builtin_amdgcn_readfirstlane(__shfl(x, src, IE_WAVE)); };
+            auto from = [&](int x) { return __builtin_amdgcn_readlane(x, src); };
             b = from(e);
             z = u - from(incl - nb);
             start = from(s0);
@@ -104,7 +104,7 @@ __device__ __forceinline__ QpBlock qp_locate(int u, const int32_t* __restrict__ 
             slot = from(sl);
             c0 = from(cl);
         }
-        before = __builtin_amdgcn_readfirstlane(__shfl(incl, 63, IE_WAVE));
+        before = __builtin_amdgcn_readlane(incl, 63);
     }
     return QpBlock{b, z, start, len, slot, c0};
 }
