@@ -42,10 +42,23 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int PF_BM = 64;  // packed rows per sub-block
-constexpr int PF_BN = 64;  // keys per tile
+// Workgroup shape: PF_WAVES waves of 32 rows x one query head each, i.e. PF_BM = 16 * PF_WAVES
+// packed rows x both query heads of a KV head. 8 waves (one workgroup per CU, 128 rows) halve
+// the staging work per MFMA against 4 waves (two workgroups per CU, 64 rows): one staged K/V
+// tile serves twice the rows.
+#ifndef IE_PREFILL_WAVES
+#define IE_PREFILL_WAVES 8
+#endif
+constexpr int PF_WAVES = IE_PREFILL_WAVES;
+static_assert(PF_WAVES == 4 || PF_WAVES == 8, "4 or 8 waves per workgroup");
+constexpr int PF_BM = 16 * PF_WAVES;  // packed rows per sub-block
+constexpr int PF_BN = 64;             // keys per tile
 constexpr int PF_D = 128;
-constexpr int PF_THREADS = 256;
+constexpr int PF_THREADS = 64 * PF_WAVES;
+constexpr int PF_KP = 512 / PF_THREADS;   // prefix K rows per thread (64 keys x 8 lanes)
+constexpr int PF_VK = 1024 / PF_THREADS;  // V keys per thread (64 keys x 16 channel groups)
+constexpr int PF_CK = 1024 / PF_THREADS;  // chunk K rows per thread (64 keys x 16 lanes)
+constexpr int PF_VG = 64 / PF_VK;         // V key groups (threads per channel group)
 #ifndef IE_PREFILL_MAXP
 #define IE_PREFILL_MAXP 8
 #endif
@@ -66,6 +79,7 @@ constexpr float RESCALE_SLACK = 8.0f;  // log2 units
 //   key 16 + 4g + (j - 4) (j >= 4), so a lane's 8 keys for one 32-key step are one 16-byte read.
 constexpr int KS_STRIDE = 288;
 constexpr int VT_STRIDE = 160;
+constexpr int QS_STRIDE = 288;  // per-wave Q staging rows (see load_q)
 __device__ __forceinline__ int ks_off(int key, int c) { return key * KS_STRIDE + (c << 4); }
 // byte offset of keys [4kg, 4kg + 4) of channel d
 __device__ __forceinline__ int vt_off4(int d, int kg) {
@@ -93,6 +107,9 @@ struct PfLds {
     uint8_t vt[2][PF_D * VT_STRIDE];
     float ksc[3][PF_BN];
     float kb[3][PF_BN];
+#if IE_PREFILL_WAVES == 8
+    uint8_t q[PF_WAVES][32 * QS_STRIDE];  // one workgroup per CU: room for separate Q regions
+#endif
 };
 
 struct PrefillArgs {
@@ -370,46 +387,61 @@ __device__ __forceinline__ float ldf(rsrc_t r, int off) {
 // and staging. K is staged as exact bf16 integers (its scale multiplies the scores); V is staged
 // dequantized, bf16(v * v_scale), the rounding the reference's dequantization applies, so P
 // needs no per-key factor.
-// K rows are loaded 8 lanes per 128-byte row (thread: keys (tid >> 3) and (tid >> 3) + 32,
+// K rows are loaded 8 lanes per 128-byte row (thread: keys (tid >> 3) + i * PF_THREADS / 8,
 // channels [16 (tid & 7), +16)): wave loads that cover few lanes per row moved a third of the
-// bytes per clock on this part.
+// bytes per clock on this part. V: thread (key group kg = tid % PF_VG, channel group
+// dg = tid / PF_VG) holds channels [8 dg, +8) of keys PF_VK kg + u.
 struct PfxK {
-    u32x4 kw[2];
+    u32x4 kw[PF_KP];
     float kscale, kbias;
 };
 struct PfxV {
-    u32x2 vw[4];
-    f32x4 vs;  // v_scale of the lane's four keys (0 past P: out of the buffer range)
+    u32x2 vw[PF_VK];
+    float vs[PF_VK];  // v_scale of the thread's keys (0 past P: out of the buffer range)
 };
 __device__ __forceinline__ void load_pk(PfxK& r, const TileSrc& src, int kbase, int P) {
     const int tid = threadIdx.x;
     const int off = (kbase + (tid >> 3)) * PF_D + 16 * (tid & 7);
-    r.kw[0] = ld128(src.pk, off);
-    r.kw[1] = ld128(src.pk, off + 32 * PF_D);
+#pragma unroll
+    for (int i = 0; i < PF_KP; ++i) r.kw[i] = ld128(src.pk, off + i * (PF_THREADS / 8) * PF_D);
     const int kk = kbase + (tid & (PF_BN - 1));
     r.kscale = ldf(src.pks, 4 * kk);
     r.kbias = kk < P ? 0.f : -INFINITY;
 }
 __device__ __forceinline__ void load_pv(PfxV& r, const TileSrc& src, int kbase) {
     const int tid = threadIdx.x;
-    const int kg = tid & 15, dg = tid >> 4;
+    const int kg = tid % PF_VG, dg = tid / PF_VG;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) r.vw[u] = ld64(src.pv, (kbase + 4 * kg + u) * PF_D + 8 * dg);
-    r.vs = __builtin_bit_cast(f32x4, ld128(src.pvs, 4 * (kbase + 4 * kg)));
+    for (int u = 0; u < PF_VK; ++u)
+        r.vw[u] = ld64(src.pv, (kbase + PF_VK * kg + u) * PF_D + 8 * dg);
+    if constexpr (PF_VK == 4) {
+        const f32x4 v = __builtin_bit_cast(f32x4, ld128(src.pvs, 4 * (kbase + 4 * kg)));
+#pragma unroll
+        for (int u = 0; u < 4; ++u) r.vs[u] = v[u];
+    } else {
+        const u32x2 v = ld64(src.pvs, 4 * (kbase + PF_VK * kg));
+        r.vs[0] = __uint_as_float(v[0]);
+        r.vs[1] = __uint_as_float(v[1]);
+    }
+}
+// byte offset in a V^T tile of the PF_VK keys [PF_VK kg, +PF_VK) of channel d (consecutive
+// positions of the MFMA key order)
+__device__ __forceinline__ int vt_off_keys(int d, int kg) {
+    return vt_off4(d, (PF_VK * kg) >> 2) + 2 * ((PF_VK * kg) & 3);
 }
 // 16 int8 channels -> two 16-byte bf16 units 2c and 2c + 1 of the key's row, the one written
 // first alternating with c / 4 so that each 8-lane store group covers distinct banks.
 __device__ __forceinline__ void stage_pk(const PfxK& r, uint8_t* s_k) {
     const int tid = threadIdx.x, c = tid & 7, sw = (c >> 2) & 1;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < PF_KP; ++i) {
         uint32_t w[8];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             w[2 * j] = hi16pair(sbyte(r.kw[i][j], 0), sbyte(r.kw[i][j], 1));
             w[2 * j + 1] = hi16pair(sbyte(r.kw[i][j], 2), sbyte(r.kw[i][j], 3));
         }
-        uint8_t* row = s_k + ks_off((tid >> 3) + 32 * i, 2 * c);
+        uint8_t* row = s_k + ks_off((tid >> 3) + i * (PF_THREADS / 8), 2 * c);
         const u32x4 lo = {w[0], w[1], w[2], w[3]}, hi = {w[4], w[5], w[6], w[7]};
         *reinterpret_cast<u32x4*>(row + 16 * sw) = sw ? hi : lo;
         *reinterpret_cast<u32x4*>(row + 16 * (1 - sw)) = sw ? lo : hi;
@@ -425,14 +457,18 @@ __device__ __forceinline__ void stage_pk_scales(const PfxK& r, float* s_ksc, flo
 }
 __device__ __forceinline__ void stage_pv(const PfxV& r, uint8_t* s_vt) {
     const int tid = threadIdx.x;
-    const int kg = tid & 15, dg = tid >> 4;
-    uint8_t* dst = s_vt + vt_off4(8 * dg, kg);
+    const int kg = tid % PF_VG, dg = tid / PF_VG;
+    uint8_t* dst = s_vt + vt_off_keys(8 * dg, kg);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
         const int wj = j >> 2, bj = j & 3;
         const uint32_t p01 = pack_bf16x2(sbyte(r.vw[0][wj], bj) * r.vs[0], sbyte(r.vw[1][wj], bj) * r.vs[1]);
-        const uint32_t p23 = pack_bf16x2(sbyte(r.vw[2][wj], bj) * r.vs[2], sbyte(r.vw[3][wj], bj) * r.vs[3]);
-        *reinterpret_cast<u32x2*>(dst + j * VT_STRIDE) = u32x2{p01, p23};
+        if constexpr (PF_VK == 4) {
+            const uint32_t p23 = pack_bf16x2(sbyte(r.vw[2][wj], bj) * r.vs[2], sbyte(r.vw[3][wj], bj) * r.vs[3]);
+            *reinterpret_cast<u32x2*>(dst + j * VT_STRIDE) = u32x2{p01, p23};
+        } else {
+            *reinterpret_cast<uint32_t*>(dst + j * VT_STRIDE) = p01;
+        }
     }
 }
 
@@ -440,38 +476,46 @@ __device__ __forceinline__ void stage_pv(const PfxV& r, uint8_t* s_vt) {
 // the sub-block's last row: the buffer range does the masking), K and V in registers between
 // load and staging. V has the prefix tiles' lane mapping.
 struct ChkK {
-    u32x4 w[4];  // keys (tid >> 4) + 16 i, channels [8 (tid & 15), +8): 16 lanes per 256-byte row
+    u32x4 w[PF_CK];  // keys (tid >> 4) + i PF_THREADS / 16, channels [8 (tid & 15), +8): 16 lanes
+                     // per 256-byte row
 };
 struct ChkV {
-    u32x4 w[4];  // keys 4 (tid & 15) + u, channels [8 (tid >> 4), +8)
+    u32x4 w[PF_VK];  // keys PF_VK (tid % PF_VG) + u, channels [8 (tid / PF_VG), +8)
 };
 __device__ __forceinline__ void load_ck(ChkK& r, const TileSrc& src, int kbase) {
     const int tid = threadIdx.x;
     const int off = (kbase + (tid >> 4)) * src.ck_stride + 16 * (tid & 15);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) r.w[i] = ld128(src.ck, off + 16 * i * src.ck_stride);
+    for (int i = 0; i < PF_CK; ++i)
+        r.w[i] = ld128(src.ck, off + i * (PF_THREADS / 16) * src.ck_stride);
 }
 __device__ __forceinline__ void load_cv(ChkV& r, const TileSrc& src, int kbase) {
     const int tid = threadIdx.x;
-    const int kg = tid & 15, dg = tid >> 4;
+    const int kg = tid % PF_VG, dg = tid / PF_VG;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) r.w[u] = ld128(src.cv, (kbase + 4 * kg + u) * src.cv_stride + 16 * dg);
+    for (int u = 0; u < PF_VK; ++u)
+        r.w[u] = ld128(src.cv, (kbase + PF_VK * kg + u) * src.cv_stride + 16 * dg);
 }
 __device__ __forceinline__ void stage_ck(const ChkK& r, uint8_t* s_k) {
     const int tid = threadIdx.x;
     uint8_t* dst = s_k + ks_off(tid >> 4, tid & 15);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(dst + 16 * i * KS_STRIDE) = r.w[i];
+    for (int i = 0; i < PF_CK; ++i)
+        *reinterpret_cast<u32x4*>(dst + i * (PF_THREADS / 16) * KS_STRIDE) = r.w[i];
 }
 __device__ __forceinline__ void stage_cv(const ChkV& r, uint8_t* s_vt) {
     const int tid = threadIdx.x;
-    uint8_t* dst = s_vt + vt_off4(8 * (tid >> 4), tid & 15);
+    uint8_t* dst = s_vt + vt_off_keys(8 * (tid / PF_VG), tid % PF_VG);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {  // channel j of key u: bf16 half (j & 1) of word j >> 1
         const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
         const uint32_t p01 = __builtin_amdgcn_perm(r.w[1][j >> 1], r.w[0][j >> 1], sel);
-        const uint32_t p23 = __builtin_amdgcn_perm(r.w[3][j >> 1], r.w[2][j >> 1], sel);
-        *reinterpret_cast<u32x2*>(dst + j * VT_STRIDE) = u32x2{p01, p23};
+        if constexpr (PF_VK == 4) {
+            const uint32_t p23 = __builtin_amdgcn_perm(r.w[3][j >> 1], r.w[2][j >> 1], sel);
+            *reinterpret_cast<u32x2*>(dst + j * VT_STRIDE) = u32x2{p01, p23};
+        } else {
+            *reinterpret_cast<uint32_t*>(dst + j * VT_STRIDE) = p01;
+        }
     }
 }
 
@@ -675,8 +719,8 @@ __device__ __forceinline__ void tile_pv(WaveState& w, const uint32_t (&pfrag)[2]
 // region `qreg` (rows of QS_STRIDE bytes, 32 mod 64: conflict-free fragment reads) and read back
 // in the fragment layout. The region lies in the V^T buffers: the caller keeps them unstaged
 // until every wave has passed a barrier after this call.
-constexpr int QS_STRIDE = 288;
-static_assert(4 * 32 * QS_STRIDE <= 2 * PF_D * VT_STRIDE, "Q regions must fit the V^T buffers");
+static_assert(PF_WAVES == 8 || PF_WAVES * 32 * QS_STRIDE <= 2 * PF_D * VT_STRIDE,
+              "Q regions must fit the V^T buffers");
 template <bool PREFIX>
 __device__ __forceinline__ void load_q(bf16x8 (&qf)[2][4], const PrefillArgs& a, int wr0, int r1,
                                        int h, const float* cal, int l16, int g, uint8_t* qreg) {
@@ -715,7 +759,7 @@ __device__ __forceinline__ void load_q(bf16x8 (&qf)[2][4], const PrefillArgs& a,
 }
 
 #ifndef IE_PREFILL_WG_PER_CU
-#define IE_PREFILL_WG_PER_CU 2
+#define IE_PREFILL_WG_PER_CU (8 / IE_PREFILL_WAVES)
 #endif
 
 // One work item: tiles [kt_begin, kt_end) of piece `piece` of sub-block s for kv head hk.
@@ -739,7 +783,11 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBloc
     // 3 K-scale slots: the prefix loop rotates them
     auto& s_k = lds.k;
     auto& s_vt = lds.vt;
+#if IE_PREFILL_WAVES == 8
+    uint8_t* qreg = lds.q[wave];  // this wave's Q staging region
+#else
     uint8_t* qreg = &lds.vt[0][0] + wave * 32 * QS_STRIDE;  // this wave's Q staging region
+#endif
     auto& s_ksc = lds.ksc;
     auto& s_kb = lds.kb;
 
@@ -979,7 +1027,8 @@ __global__ __launch_bounds__(PF_THREADS, IE_PREFILL_WG_PER_CU) void prefill_atte
     prefill_item(a, s, loc.off % a.hkv, loc.off / a.hkv, blockIdx.x, lds);
 }
 
-constexpr int PF_COMB_GROUPS = 4;  // combine units per (split sub-block, kv head): 32 pairs each
+constexpr int PF_COMB_GROUPS = 4;  // combine units per (split sub-block, kv head): PF_THREADS / 8
+                                   // (row, query head) pairs each
 
 // grid (slots), block 256: merges the pieces of split sub-blocks (log-sum-exp, base 2) from the
 // list the main kernel recorded. Unit: split sub-block k, kv head hk, and 32 of its 128 (row,
