@@ -368,14 +368,10 @@ def read_traffic():
     return None
 
 
-def extras(args, ie, W, K, dev, alg_bytes) -> dict:
-    """Every line beside the headline: the read probe, config 4 (KV write, prefill, the whole
-    mixed step), long prefills, the prefill norm/rope, config 5's sampler and projections, the
-    config-5 step and (with --sweep) the config-3 sweep."""
-    extra = {}
-    # ---- the attainable read rate on this device: a pure 16-byte read stream (ie_hbm_read_probe)
-    # over as many bytes as one decode launch reads, past the 256 MB last-level cache, two
-    # buffers alternating; and torch's own sum over the same bytes ----
+def line_read_probe(args, ie, W, K, dev, alg_bytes, extra):
+    """The attainable read rate on this device: a pure 16-byte read stream (ie_hbm_read_probe)
+    over as many bytes as one decode launch reads, past the 256 MB last-level cache, two buffers
+    alternating; and torch's own sum over the same bytes."""
     import ctypes
     lib = importlib.import_module("inference-engine_amd._native").cabi()
     probes = [torch.ones(alg_bytes // 4, dtype=torch.float32, device=dev) for _ in range(2)]
@@ -397,127 +393,142 @@ def extras(args, ie, W, K, dev, alg_bytes) -> dict:
                            "stream_GBps": round(alg_bytes / (rp_ms * 1e-3) / 1e9, 1),
                            "torch_sum_GBps": round(alg_bytes / (ts_ms * 1e-3) / 1e9, 1)}
     log(f"read probe {rp_ms*1e3:.2f} us, torch.sum {ts_ms*1e3:.2f} us")
-    del probes, sink
-    # ---- config 4: KV write + chunked prefill ----
-    try:
-        mw = W.mixed_to(W.config4(seed=0), dev)
-        gi = mw.inputs
-        kv_op = lambda: K.quantize_kv_prefill(mw.k, mw.v, gi["cu_seqlens"], gi["slot_ids"],
-                                              gi["cached_lens"], gi["num_decoding"], mw.cache)
-        kv_ms = time_op(kv_op, args.steps, args.warmup)
-        kv_gms = time_graph(kv_op)
-        n_new = sum(L for L, _ in mw.chunks)
-        kv_bytes = n_new * 8 * (128 * 2 * 2 + 128 * 2 + 8)
-        extra["kv_write_config4"] = {"us": round(kv_ms * 1e3, 3),
-                                     "GBps": round(kv_bytes / (kv_ms * 1e-3) / 1e9, 1),
-                                     "us_graph": round(kv_gms * 1e3, 3), "bytes": kv_bytes}
-        log(f"kv write config4 {kv_ms*1e3:.2f} us")
-        # a long step: a first chunk of 8192 tokens (with its calibration) and 4096 new tokens
-        # after 4096 cached, where the write is bandwidth-bound rather than latency-bound
-        lw = W.mixed_to(W.mixed_workload([], [(8192, 0), (4096, 4096)], seed=1, block_m=128,
-                                         max_len=8192), dev)
-        li = lw.inputs
-        kvl_op = lambda: K.quantize_kv_prefill(lw.k, lw.v, li["cu_seqlens"], li["slot_ids"],
-                                               li["cached_lens"], li["num_decoding"], lw.cache)
-        kvl_ms = time_op(kvl_op, args.steps, args.warmup)
-        kvl_bytes = (8192 + 4096) * 8 * (128 * 2 * 2 + 128 * 2 + 8)
-        extra["kv_write_long"] = {"tokens": 8192 + 4096, "us": round(kvl_ms * 1e3, 3),
-                                  "GBps": round(kvl_bytes / (kvl_ms * 1e-3) / 1e9, 1),
-                                  "bytes": kvl_bytes}
-        log(f"kv write long {kvl_ms*1e3:.2f} us")
-        del lw, li
-        flops = W.prefill_flops(mw.chunks)
+
+
+def line_kv_write(args, ie, W, K, dev, alg_bytes, extra):
+    """Config 4's KV quantize-on-write (1,024 new tokens), and a long step: a first chunk of 8192
+    tokens (with its calibration) and 4096 new tokens after 4096 cached, where the write is
+    bandwidth-bound rather than latency-bound."""
+    mw = W.mixed_to(W.config4(seed=0), dev)
+    gi = mw.inputs
+    kv_op = lambda: K.quantize_kv_prefill(mw.k, mw.v, gi["cu_seqlens"], gi["slot_ids"],
+                                          gi["cached_lens"], gi["num_decoding"], mw.cache)
+    kv_ms = time_op(kv_op, args.steps, args.warmup)
+    kv_gms = time_graph(kv_op)
+    n_new = sum(L for L, _ in mw.chunks)
+    kv_bytes = n_new * 8 * (128 * 2 * 2 + 128 * 2 + 8)
+    extra["kv_write_config4"] = {"us": round(kv_ms * 1e3, 3),
+                                 "GBps": round(kv_bytes / (kv_ms * 1e-3) / 1e9, 1),
+                                 "us_graph": round(kv_gms * 1e3, 3), "bytes": kv_bytes}
+    log(f"kv write config4 {kv_ms*1e3:.2f} us")
+    lw = W.mixed_to(W.mixed_workload([], [(8192, 0), (4096, 4096)], seed=1, block_m=128,
+                                     max_len=8192), dev)
+    li = lw.inputs
+    kvl_op = lambda: K.quantize_kv_prefill(lw.k, lw.v, li["cu_seqlens"], li["slot_ids"],
+                                           li["cached_lens"], li["num_decoding"], lw.cache)
+    kvl_ms = time_op(kvl_op, args.steps, args.warmup)
+    kvl_bytes = (8192 + 4096) * 8 * (128 * 2 * 2 + 128 * 2 + 8)
+    extra["kv_write_long"] = {"tokens": 8192 + 4096, "us": round(kvl_ms * 1e3, 3),
+                              "GBps": round(kvl_bytes / (kvl_ms * 1e-3) / 1e9, 1),
+                              "bytes": kvl_bytes}
+    log(f"kv write long {kvl_ms*1e3:.2f} us")
+
+
+def line_prefill_config4(args, ie, W, K, dev, alg_bytes, extra):
+    """Config 4's chunked-prefill attention (main kernel + combine), causal-exact flops."""
+    mw = W.mixed_to(W.config4(seed=0), dev)
+    gi = mw.inputs
+    flops = W.prefill_flops(mw.chunks)
+    pf_op = lambda: K.prefill_attention(
+        mw.q, mw.k, mw.v, gi["seq_ids"], gi["cu_seqlens"], gi["tile_start"], mw.cache,
+        gi["slot_ids"], gi["cu_cached"], mw.block_m)
+    pf_ms = time_op(pf_op, args.steps, args.warmup)
+    pf_gms = time_graph(pf_op)
+    tf = flops / (pf_ms * 1e-3) / 1e12
+    extra["prefill_config4"] = {"us": round(pf_ms * 1e3, 3), "TFLOPs": round(tf, 1),
+                                "mfma_frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
+                                "us_graph": round(pf_gms * 1e3, 3),
+                                "mfma_frac_graph": round(
+                                    flops / (pf_gms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+                                "flops": flops}
+    log(f"prefill config4 {pf_ms*1e3:.2f} us {tf:.1f} TFLOP/s")
+
+
+def line_prefill_long(args, ie, W, K, dev, alg_bytes, extra):
+    """Long prefills, where the tile loop rather than the per-launch latency sets the time:
+    4 x 2048 new tokens after 2048 cached, and 4 x 1024 new after 7168 cached."""
+    longs = {}
+    for name, chunks, max_len in (("4x2048_after_2048", [(2048, 2048)] * 4, 4096),
+                                  ("4x1024_after_7168", [(1024, 7168)] * 4, 8192)):
+        pw = W.mixed_to(W.mixed_workload([], chunks, seed=2, block_m=128, max_len=max_len), dev)
+        pi = pw.inputs
+        op = lambda: K.prefill_attention(
+            pw.q, pw.k, pw.v, pi["seq_ids"], pi["cu_seqlens"], pi["tile_start"], pw.cache,
+            pi["slot_ids"], pi["cu_cached"], pw.block_m)
+        ms = time_op(op, args.steps, args.warmup)
+        fl = W.prefill_flops(pw.chunks)
+        tf = fl / (ms * 1e-3) / 1e12
+        longs[name] = {"us": round(ms * 1e3, 2), "TFLOPs": round(tf, 1),
+                       "mfma_frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4), "flops": fl}
+        log(f"prefill {name} {ms*1e3:.2f} us {tf:.1f} TFLOP/s")
+        del pw, pi, op
+    extra["prefill_long"] = longs
+
+
+def line_norm_rope(args, ie, W, K, dev, alg_bytes, extra):
+    """Config 4: prefill q/k RMSNorm + RoPE of the 1,024 packed prefill tokens."""
+    extra["norm_rope_prefill_config4"] = bench_norm_rope(K, args.norm_rope_tokens, args.steps,
+                                                         args.warmup, dev)
+    log(f"norm rope prefill config4 {extra['norm_rope_prefill_config4']}")
+
+
+def line_sample(args, ie, W, K, dev, alg_bytes, extra):
+    """Config 5's sampler: B = 32 rows of the 151,936-entry vocabulary."""
+    extra["sample_config5"] = bench_sample(K, 32, 151_936, args.steps, args.warmup, dev)
+    log(f"sample config5 {extra['sample_config5']}")
+
+
+def line_linear(args, ie, W, K, dev, alg_bytes, extra):
+    """Config 5's projections at 32 rows."""
+    extra["linear_config5"] = bench_linear(K, 32, dev)
+    log(f"linear config5 {extra['linear_config5']}")
+
+
+def line_mixed_step(args, ie, W, K, dev, alg_bytes, extra):
+    extra["mixed_step_config4"] = bench_mixed_step(W, dev)
+    log(f"mixed step config4 {extra['mixed_step_config4']}")
+
+
+def line_step(args, ie, W, K, dev, alg_bytes, extra):
+    log("config 5: Qwen3-1.7B-shaped decode step (hipGraph)")
+    extra["decode_step_config5"] = bench_step(max(10, args.steps // 2), 3, dev)
+    log(f"config5 {extra['decode_step_config5']}")
+
+
+def line_sweep(args, ie, W, K, dev, alg_bytes, extra):
+    """The config-3 shape sweep: whole decode_attention steps, two rotated cache sets."""
+    sweep = {}
+    for b in (16, 64, 256):
+        for c in (1024, 4096):
+            ws = [W.decode_workload([c] * b, seed=s, device=dev) for s in range(2)]
+            sm, spm, _ = time_decode(ie, ws, 20, 5)
+            by = ws[0].algorithmic_bytes()
+            sweep[f"B{b}_ctx{c}"] = {"us": round(sm * 1e3, 2),
+                                     "GBps": round(by / (sm * 1e-3) / 1e9, 1)}
+            log(f"sweep B={b} ctx={c}: {sm*1e3:.2f} us")
+            del ws
+            torch.cuda.empty_cache()
+    extra["decode_sweep"] = sweep
+
+
+# the lines beside the headline, in the order they run (--lines picks a subset)
+LINES = {"read_probe": line_read_probe, "kv_write": line_kv_write,
+         "prefill_config4": line_prefill_config4, "prefill_long": line_prefill_long,
+         "norm_rope": line_norm_rope, "sample": line_sample, "linear": line_linear,
+         "mixed_step": line_mixed_step, "step": line_step, "sweep": line_sweep}
+DEFAULT_LINES = [n for n in LINES if n != "sweep"]
+
+
+def extras(args, ie, W, K, dev, alg_bytes) -> dict:
+    """Every line beside the headline that --lines selects; a line that fails reports its error
+    under its own key instead of its numbers."""
+    extra = {}
+    for name in args.lines:
+        torch.cuda.empty_cache()
         try:
-            pf_op = lambda: K.prefill_attention(
-                mw.q, mw.k, mw.v, gi["seq_ids"], gi["cu_seqlens"], gi["tile_start"], mw.cache,
-                gi["slot_ids"], gi["cu_cached"], mw.block_m)
-            pf_ms = time_op(pf_op, args.steps, args.warmup)
-            pf_gms = time_graph(pf_op)
-            tf = flops / (pf_ms * 1e-3) / 1e12
-            extra["prefill_config4"] = {"us": round(pf_ms * 1e3, 3), "TFLOPs": round(tf, 1),
-                                        "mfma_frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
-                                        "us_graph": round(pf_gms * 1e3, 3),
-                                        "mfma_frac_graph": round(
-                                            flops / (pf_gms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
-                                            4),
-                                        "flops": flops}
-            log(f"prefill config4 {pf_ms*1e3:.2f} us {tf:.1f} TFLOP/s")
-        except RuntimeError as e:
-            extra["prefill_config4"] = {"error": str(e).splitlines()[0][:200]}
-    except Exception as e:  # reported, never silently replaced
-        extra["config4_error"] = str(e).splitlines()[0][:200]
-    # ---- long prefills, where the tile loop rather than the per-launch latency sets the time:
-    # 4 x 2048 new tokens after 2048 cached, and 4 x 1024 new after 7168 cached ----
-    try:
-        longs = {}
-        for name, chunks, max_len in (("4x2048_after_2048", [(2048, 2048)] * 4, 4096),
-                                      ("4x1024_after_7168", [(1024, 7168)] * 4, 8192)):
-            pw = W.mixed_to(W.mixed_workload([], chunks, seed=2, block_m=128, max_len=max_len),
-                            dev)
-            pi = pw.inputs
-            op = lambda: K.prefill_attention(
-                pw.q, pw.k, pw.v, pi["seq_ids"], pi["cu_seqlens"], pi["tile_start"], pw.cache,
-                pi["slot_ids"], pi["cu_cached"], pw.block_m)
-            ms = time_op(op, args.steps, args.warmup)
-            fl = W.prefill_flops(pw.chunks)
-            tf = fl / (ms * 1e-3) / 1e12
-            longs[name] = {"us": round(ms * 1e3, 2), "TFLOPs": round(tf, 1),
-                           "mfma_frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4), "flops": fl}
-            log(f"prefill {name} {ms*1e3:.2f} us {tf:.1f} TFLOP/s")
-            del pw, pi, op
-        extra["prefill_long"] = longs
-    except Exception as e:  # reported, never silently replaced
-        extra["prefill_long"] = {"error": str(e).splitlines()[0][:200]}
-    # ---- config 4: prefill q/k RMSNorm + RoPE of the 1,024 packed prefill tokens ----
-    try:
-        extra["norm_rope_prefill_config4"] = bench_norm_rope(K, args.norm_rope_tokens, args.steps,
-                                                             args.warmup, dev)
-        log(f"norm rope prefill config4 {extra['norm_rope_prefill_config4']}")
-    except Exception as e:  # reported, never silently replaced
-        extra["norm_rope_prefill_config4"] = {"error": str(e).splitlines()[0][:200]}
-
-    # ---- config 5's sampler: B = 32 rows of the 151,936-entry vocabulary ----
-    try:
-        extra["sample_config5"] = bench_sample(K, 32, 151_936, args.steps, args.warmup, dev)
-        log(f"sample config5 {extra['sample_config5']}")
-    except Exception as e:  # reported, never silently replaced
-        extra["sample_config5"] = {"error": str(e).splitlines()[0][:200]}
-
-    # ---- config 5's projections: 32 rows ----
-    try:
-        extra["linear_config5"] = bench_linear(K, 32, dev)
-        log(f"linear config5 {extra['linear_config5']}")
-    except Exception as e:  # reported, never silently replaced
-        extra["linear_config5"] = {"error": str(e).splitlines()[0][:200]}
-
-    try:
-        extra["mixed_step_config4"] = bench_mixed_step(W, dev)
-        log(f"mixed step config4 {extra['mixed_step_config4']}")
-    except Exception as e:  # reported, never silently replaced
-        extra["mixed_step_config4"] = {"error": str(e).splitlines()[0][:200]}
-
-    if not args.no_step:
-        log("config 5: Qwen3-1.7B-shaped decode step (hipGraph)")
-        try:
-            extra["decode_step_config5"] = bench_step(max(10, args.steps // 2), 3, dev)
-            log(f"config5 {extra['decode_step_config5']}")
+            LINES[name](args, ie, W, K, dev, alg_bytes, extra)
         except Exception as e:  # reported, never silently replaced
-            extra["decode_step_config5"] = {"error": str(e).splitlines()[0][:200]}
-
-    if args.sweep:
-        sweep = {}
-        for b in (16, 64, 256):
-            for c in (1024, 4096):
-                ws = [W.decode_workload([c] * b, seed=s, device=dev) for s in range(2)]
-                sm, spm, _ = time_decode(ie, ws, 20, 5)
-                by = ws[0].algorithmic_bytes()
-                sweep[f"B{b}_ctx{c}"] = {"us": round(sm * 1e3, 2),
-                                         "GBps": round(by / (sm * 1e-3) / 1e9, 1)}
-                log(f"sweep B={b} ctx={c}: {sm*1e3:.2f} us")
-                del ws
-                torch.cuda.empty_cache()
-        extra["decode_sweep"] = sweep
-
+            extra[f"{name}_error"] = str(e).splitlines()[0][:200]
     return extra
 
 
@@ -536,6 +547,9 @@ def main():
                     help="minimum CPU-baseline decode work (whole batch, repeated); the config-4 "
                          "KV write and prefill baselines run a third of it each")
     ap.add_argument("--no-step", action="store_true", help="skip the config-5 decode step")
+    ap.add_argument("--lines", default=",".join(DEFAULT_LINES),
+                    help=f"comma-separated lines beside the headline, of {','.join(LINES)} "
+                         "(default: all but sweep)")
     ap.add_argument("--norm-rope-tokens", type=int, default=1024,
                     help="packed tokens of the prefill norm/rope line (config 4: 1024)")
     ap.add_argument("--sweep", action="store_true", help="also time the config-3 shape sweep")
@@ -545,6 +559,14 @@ def main():
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run a plain device copy of MIB MiB 3 times (PMC calibration)")
     args = ap.parse_args()
+    args.lines = [x for x in args.lines.split(",") if x]
+    bad = [x for x in args.lines if x not in LINES]
+    if bad:
+        ap.error(f"unknown lines {bad}; known: {list(LINES)}")
+    if args.no_step and "step" in args.lines:
+        args.lines.remove("step")
+    if args.sweep and "sweep" not in args.lines:
+        args.lines.append("sweep")
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "

@@ -305,6 +305,17 @@ __device__ Loc schedule(const PrefillArgs& a, int target, int* tables) {
     };
     const int spare = a.grid - parts * a.hkv;
     Loc L;
+    L.found = 0;
+    if (spare > 0 && target >= a.grid) {
+        // with spare slots the pairs are split and every item is numbered below a.grid: a
+        // workgroup past them has no item (these start late, once resident ones finish, and
+        // would otherwise spend the rest of the schedule finding that out)
+        L.T = 0;
+        L.nsplit = 0;
+        L.sb = L.off = L.item_base = L.split_index = 0;
+        L.s = SubBlock{};
+        return L;
+    }
     L.T = PF_UNSPLIT;
     if (spare > 0) {
         L.T = max(PF_MIN_PIECE_TILES, cdiv_i(tot * a.hkv, spare));
