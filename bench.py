@@ -2,8 +2,8 @@
 
 Headline (BASELINE metric): split-K int8-KV decode attention at B=64, ctx=4096, Hq=16, Hkv=8,
 D=128 — µs per layer and achieved HBM GB/s against the 8 TB/s peak. One step = one
-`decode_attention` call (split kernel + reduce kernel) over the whole batch, inputs resident in
-HBM. Distinct cache sets are rotated between steps so the 256 MB MALL cannot serve a repeat.
+`decode_attention` call over the whole batch (one launch: split-K pieces, the last piece of
+each sequence merging them), inputs resident in HBM. Distinct cache sets are rotated between steps so the 256 MB MALL cannot serve a repeat.
 
 Also reported beside it (extra keys): config-4 KV quantize-on-write, chunked-prefill attention,
 the prefill q/k RMSNorm + RoPE of its 1,024 packed tokens and the whole config-4 attention step,
@@ -45,19 +45,16 @@ def _events(n):
 
 
 def time_decode(ie, wls, steps, warmup):
-    """Whole-step time (split + combine, back to back between two events) and, in a separate
-    pass, the split kernel's average duration from back-to-back split-only launches between two
-    events (events around each launch of a ~90 us kernel would add their own microseconds)."""
+    """Whole-step time: `decode_attention` back to back between two events, cycling through the
+    cache sets. The op is one launch (decode_attention_kernel, whose last piece per sequence also
+    merges the pieces), so this is also that kernel's average duration."""
     K = ie.kernels
     outs = [torch.empty_like(w.q) for w in wls]
-    wss = [K.decode_attention_workspace(w.q) for w in wls]
 
     def run(i):
         w = wls[i % len(wls)]
-        K.decode_attention_split(w.q, w.cache, w.cached_lens, w.slot_ids, w.num_decoding, SCALE,
-                                 outs[i % len(wls)], wss[i % len(wls)])
-        K.decode_attention_combine(w.q, w.cache, w.cached_lens, w.num_decoding,
-                                   outs[i % len(wls)], wss[i % len(wls)])
+        K.decode_attention(w.q, w.cache, w.cached_lens, w.slot_ids, w.num_decoding, SCALE,
+                           out=outs[i % len(wls)])
 
     for i in range(warmup):
         run(i)
@@ -68,25 +65,7 @@ def time_decode(ie, wls, steps, warmup):
         run(i)
     e1.record()
     torch.cuda.synchronize()
-    step_ms = e0.elapsed_time(e1) / steps
-
-    def split(i):
-        w = wls[i % len(wls)]
-        K.decode_attention_split(w.q, w.cache, w.cached_lens, w.slot_ids, w.num_decoding, SCALE,
-                                 outs[i % len(wls)], wss[i % len(wls)])
-
-    for i in range(max(10, warmup // 10)):
-        split(i)
-    torch.cuda.synchronize()
-    e0, e1 = _events(2)
-    e0.record()
-    for i in range(steps):
-        split(i)
-    e1.record()
-    torch.cuda.synchronize()
-    split_ms = e0.elapsed_time(e1) / steps
-    # the combine's share: what the whole step takes beyond its split launch
-    return step_ms, split_ms, max(0.0, step_ms - split_ms)
+    return e0.elapsed_time(e1) / steps
 
 
 def time_op(fn, steps, warmup):
@@ -358,7 +337,7 @@ def _cpu_model():
 
 
 def read_traffic():
-    """HBM bytes per launch of the split kernel from the committed rocprofv3 PMC summary."""
+    """HBM bytes per launch of the decode kernel from the committed rocprofv3 PMC summary."""
     p = REPO / "profiles" / "decode_attention_B64_ctx4096_pmc.md"
     if not p.exists():
         return None
@@ -501,7 +480,7 @@ def line_sweep(args, ie, W, K, dev, alg_bytes, extra):
     for b in (16, 64, 256):
         for c in (1024, 4096):
             ws = [W.decode_workload([c] * b, seed=s, device=dev) for s in range(2)]
-            sm, spm, _ = time_decode(ie, ws, 20, 5)
+            sm = time_decode(ie, ws, 20, 5)
             by = ws[0].algorithmic_bytes()
             sweep[f"B{b}_ctx{c}"] = {"us": round(sm * 1e3, 2),
                                      "GBps": round(by / (sm * 1e-3) / 1e9, 1)}
@@ -596,11 +575,9 @@ def main():
     torch.cuda.synchronize()
     alg_bytes = wls[0].algorithmic_bytes()
     log("timing decode attention")
-    step_ms, split_ms, comb_ms = time_decode(ie, wls, args.steps, args.warmup)
+    step_ms = time_decode(ie, wls, args.steps, args.warmup)
     gbs = alg_bytes / (step_ms * 1e-3) / 1e9
-    split_gbs = alg_bytes / (split_ms * 1e-3) / 1e9
-    log(f"decode step {step_ms*1e3:.2f} us ({gbs:.0f} GB/s); split kernel {split_ms*1e3:.2f} us "
-        f"({split_gbs:.0f} GB/s), combine {comb_ms*1e3:.2f} us")
+    log(f"decode step (one launch of decode_attention_kernel) {step_ms*1e3:.2f} us ({gbs:.0f} GB/s)")
 
     extra = {}
     if args.headline_only:
@@ -614,9 +591,6 @@ def main():
         cpu = cpu_baselines(wls[0], alg_bytes, W, args.cpu_seconds)
         log(f"cpu baseline {cpu}")
     traffic = read_traffic()
-    if split_ms > step_ms:
-        log(f"warning: split-only launches ({split_ms*1e3:.2f} us) measured longer than the "
-            f"whole step ({step_ms*1e3:.2f} us)")
     line = {
         "metric": METRIC,
         "value": round(gbs, 1),
@@ -636,14 +610,13 @@ def main():
                    "batch": args.batch, "ctx": args.ctx, "q_heads": 16, "kv_heads": 8,
                    "head_dim": 128, "rotated_cache_sets": args.rotate,
                    "algorithmic_bytes": alg_bytes},
-        "roofline": {"bound": "hbm", "achieved": round(split_gbs, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(split_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": traffic, "kernel": "decode_split_kernel",
-                     "kernel_us": round(split_ms * 1e3, 2),
-                     "kernel_us_from": "back-to-back split launches between two HIP events on "
-                                       "the launch stream"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": traffic, "kernel": "decode_attention_kernel",
+                     "kernel_us": round(step_ms * 1e3, 2),
+                     "kernel_us_from": "back-to-back launches between two HIP events on the "
+                                       "launch stream (the op is this one kernel)"},
         "cpu_baseline": cpu,
-        "step_minus_split_us": round(comb_ms * 1e3, 2),
         **extra,
     }
     print(json.dumps(line), flush=True)

@@ -132,10 +132,13 @@ hipError_t ie_fused_rope_kv_decode(const ie_bf16* q, int64_t q_stride_b, int64_t
 
 /*
  * Bytes of device workspace ie_decode_attention needs for `batch` sequences on the current
- * device: the plan record (the split launch writes the step's piece size and each split
- * sequence's first work entry there for the combine launch: (64 + batch) ints, padded to 256
- * bytes), then fp32 split-K partials, head_dim + 2 values per (query head, work entry), where
- * the work entries are ie_decode_attention_grid(batch, num_q_heads / 2).
+ * device: the arrival counts (one uint32 per sequence and KV head, with room for max(batch,
+ * 1024) sequences, padded to 256 bytes), then fp32 split-K partials, head_dim + 2 values per
+ * (query head, work entry), where the work entries are ie_decode_attention_grid(batch,
+ * num_q_heads / 2). The arrival counts must be zero when a workspace is first used (allocate it
+ * zeroed); every call that completes leaves them zero again, so one workspace serves any number
+ * of calls in stream order, of any batch up to 1024 (they share one count region). A workspace
+ * used with a batch above 1024 serves that batch size only, unless zeroed again.
  */
 size_t ie_decode_attention_workspace_size(int32_t batch, int32_t num_q_heads, int32_t head_dim);
 
@@ -144,7 +147,8 @@ size_t ie_decode_attention_workspace_size(int32_t batch, int32_t num_q_heads, in
 int32_t ie_decode_attention_max_splits(int32_t num_kv_heads);
 
 /*
- * Split-K GQA decode attention over the int8 cache, then the partial-softmax reduce.
+ * Split-K GQA decode attention over the int8 cache, with the partial-softmax reduce folded into
+ * the same launch (the sequence's last piece to finish merges its pieces).
  * Replaces qwen3-1.7b/kernels.py:272-361 `decode_attention(q, kv_cache, cached_lens, slot_ids,
  * num_decoding, scale, out)` (kernels kernels.py:73-213 and 216-264, work split 20-70).
  *
@@ -152,7 +156,8 @@ int32_t ie_decode_attention_max_splits(int32_t num_kv_heads);
  * attends to tokens [0, cached_lens[b] + 1) of cache row slot_ids[b]:
  *   out[b, h] = sum_t softmax_t(scale * k_scale[t] * <q[b, h], k[t]>) * v_scale[t] * v[t].
  * Only rows b < num_decoding[0] of out are written. `workspace` must hold
- * ie_decode_attention_workspace_size(B, num_q_heads, head_dim) bytes.
+ * ie_decode_attention_workspace_size(B, num_q_heads, head_dim) bytes with its arrival counts
+ * zero (see there); calls that share a workspace must not overlap.
  */
 hipError_t ie_decode_attention(const ie_bf16* q, int64_t q_stride_b, int64_t q_stride_h,
                                int32_t batch, int32_t num_q_heads, const ie_kv_cache* cache,
@@ -162,30 +167,12 @@ hipError_t ie_decode_attention(const ie_bf16* q, int64_t q_stride_b, int64_t q_s
                                size_t workspace_bytes, hipStream_t stream);
 
 /*
- * The two launches of ie_decode_attention, exposed separately so a profiler harness can time
- * the split kernel on its own: ie_decode_attention == split followed by combine, same args.
- */
-hipError_t ie_decode_attention_split(const ie_bf16* q, int64_t q_stride_b, int64_t q_stride_h,
-                                     int32_t batch, int32_t num_q_heads,
-                                     const ie_kv_cache* cache, const int32_t* cached_lens,
-                                     const int32_t* slot_ids, const int32_t* num_decoding,
-                                     float scale, ie_bf16* out, int64_t out_stride_b,
-                                     int64_t out_stride_h, void* workspace,
-                                     size_t workspace_bytes, hipStream_t stream);
-hipError_t ie_decode_attention_combine(int32_t batch, int32_t num_q_heads, int32_t head_dim,
-                                       int32_t num_kv_heads, const int32_t* cached_lens,
-                                       const int32_t* num_decoding, ie_bf16* out,
-                                       int64_t out_stride_b, int64_t out_stride_h,
-                                       void* workspace, size_t workspace_bytes,
-                                       hipStream_t stream);
-
-/*
  * ie_decode_attention without a workspace argument, for callers that cannot allocate device
  * memory (code under hipGraph capture, serving loops and harnesses that forbid allocation). No
- * counterpart in the reference. The split-K partials and the plan record live in a static
- * device array of ie_decode_attention_noalloc_max_bytes() bytes (16 MiB) that each device the
- * library runs on holds until the process ends; a batch whose workspace
- * (ie_decode_attention_workspace_size) exceeds it returns hipErrorInvalidValue. Allocates
+ * counterpart in the reference. The arrival counts and split-K partials live in a static device
+ * array of ie_decode_attention_noalloc_max_bytes() bytes (16 MiB) that each device the library
+ * runs on holds until the process ends; a batch above 1024 sequences returns
+ * hipErrorInvalidValue. Allocates
  * nothing; the first call on a device looks up the array's address there (make it outside
  * graph capture). Every call on a device shares the array: calls that overlap on one device
  * race. Same arguments, results and errors as ie_decode_attention otherwise.
@@ -199,10 +186,10 @@ hipError_t ie_decode_attention_noalloc(const ie_bf16* q, int64_t q_stride_b, int
                                        int64_t out_stride_h, hipStream_t stream);
 
 /*
- * The split launch's work list, for tests and diagnostics: the work split of
- * qwen3-1.7b/kernels.py:20-70 (`compute_piece`, `assign_work`) as the split kernel computes it
+ * The decode launch's work list, for tests and diagnostics: the work split of
+ * qwen3-1.7b/kernels.py:20-70 (`compute_piece`, `assign_work`) as the decode kernel computes it
  * on the device. ie_decode_attention_grid(batch, num_kv_heads) is the number of work entries
- * (the split launch's workgroups per KV head); ie_decode_attention_plan writes, for each entry
+ * (the decode launch's workgroups per KV head); ie_decode_attention_plan writes, for each entry
  * w, rows[4w .. 4w+3] = (sequence b, split index, splits of b, piece size in tokens), with
  * splits = 0 for an entry that has no work. rows: int32 [grid, 4] device memory.
  */

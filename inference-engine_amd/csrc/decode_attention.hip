@@ -21,8 +21,9 @@
 //   q is scaled by a power of two per head so it is exact in fp16; QK^T and PV use the
 //   fp32-accumulating v_dot2_f32_f16. QK partial dots are reduced across the 8 lanes of a row
 //   with DPP. Online softmax in base 2 per lane group; groups and waves are merged at the end
-//   (log-sum-exp), then either the output is written (one piece) or fp32 partials
-//   (m, l, acc) go to the workspace for the combine kernel (kernels.py:216-264).
+//   (log-sum-exp), then either the output is written (one piece) or fp32 partials (m, l, acc)
+//   go to the workspace and the sequence's last piece to finish merges them (the reference's
+//   combine kernel, kernels.py:216-264, folded into the same launch).
 #include <mutex>
 
 #include "ie_common.h"
@@ -56,8 +57,7 @@ constexpr int DA_U = 4;                            // tokens per lane group per 
 constexpr int DA_TOK_WAVE = 8 * DA_U;              // 32 tokens per wave block
 constexpr int DA_TOK_WG = DA_WAVES * DA_TOK_WAVE;  // tokens per workgroup step
 constexpr int DA_MIN_PIECE = 128;
-constexpr int DA_MAX_SPLITS = 1024;  // pieces per sequence the combine kernel merges, at most
-constexpr int DA_PLAN_FIRST = 64;    // plan record: sequence b's first work entry at int 64 + b
+constexpr int DA_MAX_SPLITS = 1024;  // per-KV-head workgroup target, at most
 constexpr int DA_D = 128;
 constexpr uint32_t K64 = 0x64646464u;
 constexpr float OFFSET = 1152.0f;  // fp16(0x64xx) = 1024 + byte, byte = x + 128
@@ -139,6 +139,16 @@ __device__ __forceinline__ float fdot2(half2_t a, half2_t b, float c) {
 }
 __device__ __forceinline__ float exp2_safe(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Device-coherent float accesses (agent-scope relaxed atomics: global loads and stores with
+// the device scope bit, served at the level all XCDs share rather than from a possibly stale
+// per-XCD L2 line).
+__device__ __forceinline__ void st_dev(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_dev(const float* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 struct DecodeArgs {
     const uint16_t* q;
     int64_t q_sb, q_sh;
@@ -149,12 +159,11 @@ struct DecodeArgs {
     float scale_log2;  // softmax scale * log2(e)
     uint16_t* out;
     int64_t o_sb, o_sh;
-    float* part_acc;  // [Hq, nwork, 128]: work entry w's partial output for query head h
-    float* part_m;    // [Hq, nwork]
-    float* part_l;    // [Hq, nwork]
-    int* plan;        // [0]: this step's piece size; [DA_PLAN_FIRST + b]: sequence b's first
-                      // work entry (written when b has more than one piece), for the combine
-    int target, nwork, hq;
+    float* part_acc;     // [Hq, nwork, 128]: work entry w's partial output for query head h
+    float* part_m;       // [Hq, nwork]
+    float* part_l;       // [Hq, nwork]
+    uint32_t* arrivals;  // [B, Hkv]: pieces of the sequence done; 0 between calls
+    int target, nwork, hq, hkv;
     int batch;        // rows of q / cached_lens (num_decoding[0] <= batch)
     int head_fast;    // 1: grid (Hkv, pieces), the KV head in blockIdx.x; 0: grid (pieces, Hkv)
 };
@@ -307,7 +316,7 @@ __device__ __forceinline__ void block_pv(LaneState& st, const float (&t)[DA_U][2
 #endif
 
 __global__ __launch_bounds__(DA_THREADS)
-__attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_split_kernel(
+__attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_attention_kernel(
     DecodeArgs a) {
     const int lane0 = threadIdx.x & 63;
     const int raw0 = lane0 < a.batch ? a.cached_lens[lane0] : 0;  // issued beside num_decoding
@@ -315,14 +324,12 @@ __attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_split_k
     const int hk = a.head_fast ? blockIdx.x : blockIdx.y;
     const int item = a.head_fast ? blockIdx.y : blockIdx.x;
     Work wk = decode_assign(a.cached_lens, nd, item, a.target, raw0);
-    if (item == 0 && hk == 0 && threadIdx.x == 0) a.plan[0] = wk.piece;
     // Wave-uniform by construction; readfirstlane lets the compiler keep them (and the buffer
     // descriptors built from them) in SGPRs.
     wk.needed = uniform(wk.needed);
     if (wk.needed == 0) return;
     const int b = uniform(wk.b);
     const int split = uniform(wk.split);
-    if (hk == 0 && split == 0 && wk.needed > 1 && threadIdx.x == 0) a.plan[DA_PLAN_FIRST + b] = item;
     const int piece = uniform(wk.piece);
     const int n_end = uniform(a.cached_lens[b] + 1);
     const int t_begin = split * piece;
@@ -465,8 +472,9 @@ __attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_split_k
         }
     }
     __syncthreads();
-    if (threadIdx.x >= 2 * DA_D) return;  // one thread per (query head, channel)
-    const int h = threadIdx.x >> 7, d = threadIdx.x & 127;
+    // one thread per (query head, channel) from here on; the others stay for the barriers
+    const bool active = threadIdx.x < 2 * DA_D;
+    const int h = (threadIdx.x >> 7) & 1, d = threadIdx.x & 127;
     float mx = -INFINITY;
 #pragma unroll
     for (int w = 0; w < DA_WAVES; ++w) mx = fmaxf(mx, s_m[w][h]);
@@ -479,82 +487,66 @@ __attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_split_k
         den += s_l[w][h] * f;
     }
     const int qh_idx = 2 * hk + h;
+    uint16_t* const o = a.out + b * a.o_sb + qh_idx * a.o_sh + d;
     if (wk.needed == 1) {
-        a.out[b * a.o_sb + qh_idx * a.o_sh + d] = (uint16_t)f32_to_bf16_rne(num / den);
-    } else {
-        const int64_t row = (int64_t)qh_idx * a.nwork + item;  // the sequence's pieces are
-                                                               // consecutive work entries
-        a.part_acc[row * DA_D + d] = num;
+        if (active) *o = (uint16_t)f32_to_bf16_rne(num / den);
+        return;
+    }
+    // A sequence of several pieces: each piece publishes its partial (the sequence's pieces
+    // are consecutive work entries) and counts itself in; the piece that arrives last merges
+    // them all (kernels.py:216-264, in base 2, pieces in order) and resets the count for the
+    // next call. The partials are written and read with device-coherent accesses (ld_dev,
+    // st_dev), which the per-XCD L2s do not hold stale, and each wave waits for its stores to
+    // complete before the barrier that precedes the count: the ordering a device-scope
+    // release/acquire pair gives, without the L2 writeback and invalidate those fences cost on
+    // every workgroup.
+    uint32_t* const arrivals = a.arrivals + b * a.hkv + hk;
+    if (active) {
+        const int64_t row = (int64_t)qh_idx * a.nwork + item;
+        st_dev(a.part_acc + row * DA_D + d, num);
         if (d == 0) {
-            a.part_m[row] = mx;
-            a.part_l[row] = den;
+            st_dev(a.part_m + row, mx);
+            st_dev(a.part_l + row, den);
         }
     }
-}
-
-// grid (B, Hq), block 128: merge the pieces of sequences that had more than one
-// (kernels.py:216-264), in base 2. The piece size and the sequence's first work entry are the
-// ones the split kernel recorded in the workspace (loaded together with the sequence's length:
-// one memory round trip, no pass over all lengths); values the split kernel did not write (no
-// split launch before this one) are rejected or clamped, so the reads stay inside the
-// workspace.
-__global__ __launch_bounds__(128) void decode_combine_kernel(
-    const float* __restrict__ part_acc, const float* __restrict__ part_m,
-    const float* __restrict__ part_l, const int* __restrict__ plan,
-    const int32_t* __restrict__ cached_lens, const int32_t* __restrict__ num_decoding,
-    uint16_t* __restrict__ out, int64_t o_sb, int64_t o_sh, int nwork) {
-    const int b = blockIdx.x, h = blockIdx.y;
-    const int nd = num_decoding[0], piece = plan[0], len = cached_lens[b];
-    const int first_raw = plan[DA_PLAN_FIRST + b];
-    if (b >= nd || piece < DA_MIN_PIECE) return;
-    const int first = min(max(first_raw, 0), nwork - 1);
-    const int needed = min(min(cdiv_i(len + 1, piece), DA_MAX_SPLITS), nwork - first);
-    if (needed <= 1) return;
-    const int d = threadIdx.x;
-    const int64_t row0 = (int64_t)h * nwork + first;
-    // One memory round trip for all of it: lane s of wave 0 loads split s's (m, l) while every
-    // thread loads its first batch of partial outputs; the weights 2^(m_s - max m) go through
-    // LDS, and each thread then adds the splits in order (the same sums as one thread alone).
-    constexpr int CB = 8;  // partial outputs per load batch
-    __shared__ float s_f[DA_MAX_SPLITS], s_l[DA_MAX_SPLITS];
-    float av[CB];
-#pragma unroll
-    for (int u = 0; u < CB; ++u) av[u] = u < needed ? part_acc[(row0 + u) * DA_D + d] : 0.0f;
-    if (d < IE_WAVE) {  // splits d, d + 64, ...: one pass when there are at most 64
-        const float m0 = d < needed ? part_m[row0 + d] : -INFINITY;
-        const float l0 = d < needed ? part_l[row0 + d] : 0.0f;
-        float mx = m0;
-        for (int s = d + IE_WAVE; s < needed; s += IE_WAVE) mx = fmaxf(mx, part_m[row0 + s]);
-        mx = wave_max(mx);
-        s_f[d] = m0 == -INFINITY ? 0.0f : exp2_safe(m0 - mx);
-        s_l[d] = l0;
-        for (int s = d + IE_WAVE; s < needed; s += IE_WAVE) {
-            const float m = part_m[row0 + s];
-            s_f[s] = m == -INFINITY ? 0.0f : exp2_safe(m - mx);
-            s_l[s] = part_l[row0 + s];
-        }
-    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __shared__ uint32_t s_last;
     __syncthreads();
-    float num = 0.0f, den = 0.0f;
+    if (threadIdx.x == 0)
+        s_last = __hip_atomic_fetch_add(arrivals, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                 (uint32_t)(wk.needed - 1);
+    __syncthreads();
+    if (!s_last || !active) return;
+    const int needed = wk.needed;
+    const int64_t row0 = (int64_t)qh_idx * a.nwork + (item - split);
+    float pm = -INFINITY;
+    for (int sp = 0; sp < needed; ++sp) pm = fmaxf(pm, ld_dev(a.part_m + row0 + sp));
+    constexpr int CB = 8;  // partial outputs per load batch
+    num = 0.0f;
+    den = 0.0f;
     for (int s0 = 0; s0 < needed; s0 += CB) {
-        if (s0 > 0) {
+        float av[CB], ml[CB][2];
 #pragma unroll
-            for (int u = 0; u < CB; ++u)
-                av[u] = s0 + u < needed ? part_acc[(row0 + s0 + u) * DA_D + d] : 0.0f;
+        for (int u = 0; u < CB; ++u) {
+            const bool in = s0 + u < needed;
+            av[u] = in ? ld_dev(a.part_acc + (row0 + s0 + u) * DA_D + d) : 0.0f;
+            ml[u][0] = in ? ld_dev(a.part_m + row0 + s0 + u) : -INFINITY;
+            ml[u][1] = in ? ld_dev(a.part_l + row0 + s0 + u) : 0.0f;
         }
 #pragma unroll
         for (int u = 0; u < CB; ++u) {
             if (s0 + u < needed) {
-                const float f = s_f[s0 + u];
+                const float f = ml[u][0] == -INFINITY ? 0.0f : exp2_safe(ml[u][0] - pm);
                 num += av[u] * f;
-                den += s_l[s0 + u] * f;
+                den += ml[u][1] * f;
             }
         }
     }
-    out[b * o_sb + h * o_sh + d] = (uint16_t)f32_to_bf16_rne(num / den);
+    *o = (uint16_t)f32_to_bf16_rne(num / den);
+    if (threadIdx.x == 0) __hip_atomic_store(arrivals, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// grid (work entries), block 64: the split kernel's work list, one entry per workgroup index w
+// grid (work entries), block 64: the decode kernel's work list, one entry per workgroup index w
 // of its grid, computed by the same device code (decode_assign), written as
 // rows[w] = (b, split, needed, piece).
 __global__ __launch_bounds__(64) void decode_plan_kernel(const int32_t* __restrict__ cached_lens,
@@ -574,12 +566,16 @@ __global__ __launch_bounds__(64) void decode_plan_kernel(const int32_t* __restri
     }
 }
 
-// Workspace: the plan record (piece size, then each sequence's first work entry; padded to
-// 256 bytes), then fp32 partials (acc, m, l) of every (query head, work entry): one per piece,
-// since pieces never outnumber the split launch's work entries per KV head.
+// Workspace: the arrival counts (one per sequence and KV head; zero on entry, and every call
+// leaves them zero), then fp32 partials (acc, m, l) of every (query head, work entry): one per
+// piece, since pieces never outnumber the decode launch's work entries per KV head. The count
+// region has room for DA_COUNT_CAP sequences whatever the batch, so calls of any batch up to
+// that size agree on where the counts are and their partials never land on them: one workspace
+// serves them all. A larger batch gets a count region of its own size.
+constexpr int DA_COUNT_CAP = 1024;
 struct Layout {
     int target, nwork;
-    size_t plan_off, acc_off, m_off, l_off, bytes;
+    size_t arr_off, acc_off, m_off, l_off, bytes;
 };
 
 static Layout workspace_layout(int batch, int hq, int hkv) {
@@ -588,8 +584,8 @@ static Layout workspace_layout(int batch, int hq, int hkv) {
     L.target = std::min(decode_target(hkv), DA_MAX_SPLITS);
     L.nwork = batch <= L.target ? L.target : L.target + batch;
     const size_t rows = (size_t)hq * L.nwork;
-    L.plan_off = 0;
-    L.acc_off = ((size_t)(DA_PLAN_FIRST + batch) * sizeof(int) + 255) / 256 * 256;
+    L.arr_off = 0;
+    L.acc_off = ((size_t)std::max(batch, DA_COUNT_CAP) * hkv * sizeof(uint32_t) + 255) / 256 * 256;
     L.m_off = L.acc_off + rows * DA_D * sizeof(float);
     L.l_off = L.m_off + rows * sizeof(float);
     L.bytes = L.l_off + rows * sizeof(float);
@@ -630,7 +626,7 @@ static hipError_t check_decode(const ie_bf16* q, int32_t batch, int32_t num_q_he
     return hipSuccess;
 }
 
-extern "C" hipError_t ie_decode_attention_split(
+extern "C" hipError_t ie_decode_attention(
     const ie_bf16* q, int64_t q_stride_b, int64_t q_stride_h, int32_t batch, int32_t num_q_heads,
     const ie_kv_cache* cache, const int32_t* cached_lens, const int32_t* slot_ids,
     const int32_t* num_decoding, float scale, ie_bf16* out, int64_t out_stride_b,
@@ -655,10 +651,11 @@ extern "C" hipError_t ie_decode_attention_split(
     a.part_acc = (float*)(ws + L.acc_off);
     a.part_m = (float*)(ws + L.m_off);
     a.part_l = (float*)(ws + L.l_off);
-    a.plan = (int*)(ws + L.plan_off);
+    a.arrivals = (uint32_t*)(ws + L.arr_off);
     a.target = L.target;
     a.nwork = L.nwork;
     a.hq = num_q_heads;
+    a.hkv = (int)cache->num_kv_heads;
     a.batch = batch;
     // pieces number at most target + nd, and at most target when nd <= target (decode_piece):
     // with batch <= target the grid needs no spare workgroups, which would otherwise hold
@@ -673,7 +670,7 @@ extern "C" hipError_t ie_decode_attention_split(
                   pieces <= 65535;  // the grid's y dimension holds at most 65535
     const dim3 grid = a.head_fast ? dim3((unsigned)cache->num_kv_heads, pieces)
                                   : dim3(pieces, (unsigned)cache->num_kv_heads);
-    hipLaunchKernelGGL(decode_split_kernel, grid, dim3(DA_THREADS), 0, stream, a);
+    hipLaunchKernelGGL(decode_attention_kernel, grid, dim3(DA_THREADS), 0, stream, a);
     return hipGetLastError();
 }
 
@@ -696,54 +693,14 @@ extern "C" hipError_t ie_decode_attention_plan(const int32_t* cached_lens,
     return hipGetLastError();
 }
 
-extern "C" hipError_t ie_decode_attention_combine(int32_t batch, int32_t num_q_heads,
-                                                  int32_t head_dim, int32_t num_kv_heads,
-                                                  const int32_t* cached_lens,
-                                                  const int32_t* num_decoding, ie_bf16* out,
-                                                  int64_t out_stride_b, int64_t out_stride_h,
-                                                  void* workspace, size_t workspace_bytes,
-                                                  hipStream_t stream) {
-    IE_REQUIRE(batch >= 0, "negative batch");
-    if (batch == 0) return hipSuccess;
-    IE_REQUIRE(head_dim == DA_D && num_q_heads == 2 * num_kv_heads, "unsupported geometry");
-    IE_REQUIRE(cached_lens && num_decoding && out && workspace, "null pointer");
-    const Layout L = workspace_layout(batch, num_q_heads, num_kv_heads);
-    IE_REQUIRE(workspace_bytes >= L.bytes, "workspace too small");
-    char* ws = (char*)workspace;
-    dim3 grid(batch, num_q_heads);
-    hipLaunchKernelGGL(decode_combine_kernel, grid, dim3(DA_D), 0, stream,
-                       (const float*)(ws + L.acc_off), (const float*)(ws + L.m_off),
-                       (const float*)(ws + L.l_off), (const int*)(ws + L.plan_off), cached_lens,
-                       num_decoding, (uint16_t*)out, out_stride_b, out_stride_h, L.nwork);
-    return hipGetLastError();
-}
-
-extern "C" hipError_t ie_decode_attention(const ie_bf16* q, int64_t q_stride_b,
-                                          int64_t q_stride_h, int32_t batch, int32_t num_q_heads,
-                                          const ie_kv_cache* cache, const int32_t* cached_lens,
-                                          const int32_t* slot_ids, const int32_t* num_decoding,
-                                          float scale, ie_bf16* out, int64_t out_stride_b,
-                                          int64_t out_stride_h, void* workspace,
-                                          size_t workspace_bytes, hipStream_t stream) {
-    hipError_t e = ie_decode_attention_split(q, q_stride_b, q_stride_h, batch, num_q_heads, cache,
-                                             cached_lens, slot_ids, num_decoding, scale, out,
-                                             out_stride_b, out_stride_h, workspace,
-                                             workspace_bytes, stream);
-    if (e != hipSuccess || batch == 0) return e;
-    return ie_decode_attention_combine(batch, num_q_heads, (int)cache->head_dim,
-                                       (int)cache->num_kv_heads, cached_lens, num_decoding, out,
-                                       out_stride_b, out_stride_h, workspace, workspace_bytes,
-                                       stream);
-}
-
 // ---------------------------------------------------------------------------------------------
 // The entry point that allocates nothing: ie_decode_attention with its workspace in a static
 // device array of DA_SCRATCH_BYTES, which every device the library runs on holds until the
-// process ends (16 MiB: the plan and partials of up to 1,952 sequences at 16 query / 8 KV
-// heads on 256 CUs). The array's name is only a host-side stand-in for the device copy, so its
-// address on each device is looked up once, with that device current, and only that address
-// is passed to the kernels. The workspace needs no clearing: every call's split launch writes
-// the plan and the partials its combine launch reads. All calls on one device share the array,
+// process ends (16 MiB: the arrival counts and partials of up to 1,024 sequences, the batches
+// that share one count region). The array's name is only a host-side stand-in for the device copy, so
+// its address on each device is looked up once, with that device current, and only that
+// address is passed to the kernels. The array starts zeroed, as the workspace contract asks,
+// and every call leaves the arrival counts zeroed again. All calls on one device share the array,
 // so calls that overlap on one device (different streams, or threads without ordering) race.
 // ---------------------------------------------------------------------------------------------
 namespace {
@@ -785,9 +742,9 @@ extern "C" hipError_t ie_decode_attention_noalloc(
     if (batch == 0) return hipSuccess;
     IE_REQUIRE(num_q_heads == 2 * cache->num_kv_heads, "num_q_heads must be 2 * num_kv_heads");
     const Layout L = workspace_layout(batch, num_q_heads, (int)cache->num_kv_heads);
-    IE_REQUIRE(L.bytes <= DA_SCRATCH_BYTES,
-               "batch too large for the no-alloc decode scratch (16 MiB; use ie_decode_attention "
-               "with a workspace)");
+    IE_REQUIRE(batch <= DA_COUNT_CAP && L.bytes <= DA_SCRATCH_BYTES,
+               "batch too large for the no-alloc decode scratch (at most 1024 sequences in "
+               "16 MiB; use ie_decode_attention with a workspace)");
     void* ws = nullptr;
     e = scratch_address(&ws);
     if (e != hipSuccess) return e;

@@ -7,6 +7,11 @@
 #include <c10/hip/HIPStream.h>
 #include <torch/library.h>
 
+#include <map>
+#include <tuple>
+#include <mutex>
+#include <vector>
+
 #include "../../include/ie_attn.h"
 
 namespace {
@@ -286,6 +291,25 @@ at::Tensor workspace_for(const at::Tensor& q, size_t bytes) {
     return at::empty({(int64_t)std::max<size_t>(bytes, 16)}, q.options().dtype(at::kByte));
 }
 
+// The decode workspace carries arrival counts that must be zero on entry and that every call
+// leaves zero, so it is kept across calls: one per (device, stream), allocated zeroed on first
+// use and replaced by a larger one when a call needs more. Replaced buffers are kept too: a
+// graph captured with one still addresses it. Calls in stream order never overlap on a buffer.
+// Batches up to 1024 sequences share a buffer (their count regions coincide); a larger batch
+// has a buffer of its own.
+at::Tensor decode_workspace(const at::Tensor& q, size_t bytes, int32_t batch) {
+    static std::mutex mu;
+    static auto* cache =
+        new std::map<std::tuple<int, hipStream_t, int32_t>, std::vector<at::Tensor>>();  // kept
+    std::lock_guard<std::mutex> lock(mu);
+    auto& held = (*cache)[{q.device().index(), stream_of(q), batch <= 1024 ? 0 : batch}];
+    if (held.empty() || (size_t)held.back().numel() < bytes) {
+        const int64_t n = (int64_t)std::max<size_t>(bytes, 256);
+        held.push_back(at::zeros({n}, q.options().dtype(at::kByte)));
+    }
+    return held.back();
+}
+
 void decode_attention(const at::Tensor& q, const at::Tensor& k_cache, const at::Tensor& v_cache,
                       const at::Tensor& k_scale, const at::Tensor& v_scale,
                       const at::Tensor& k_calibration, const at::Tensor& cached_lens,
@@ -294,46 +318,11 @@ void decode_attention(const at::Tensor& q, const at::Tensor& k_cache, const at::
     const c10::DeviceGuard guard(q.device());
     DecodeCall d = decode_prep(q, k_cache, v_cache, k_scale, v_scale, k_calibration, cached_lens,
                                slot_ids, num_decoding, out);
-    at::Tensor ws = workspace_for(q, d.ws_bytes);
+    at::Tensor ws = decode_workspace(q, d.ws_bytes, d.B);
     ok(ie_decode_attention(bf(q), q.stride(0), q.stride(1), d.B, d.hq, &d.c, i32(cached_lens),
                            i32(slot_ids), i32(num_decoding), (float)scale, bfm(out),
                            out.stride(0), out.stride(1), ws.data_ptr(), d.ws_bytes, stream_of(q)),
        "decode_attention");
-}
-
-// The two launches of decode_attention with a caller-owned workspace (profiling harnesses).
-void decode_attention_split(const at::Tensor& q, const at::Tensor& k_cache,
-                            const at::Tensor& v_cache, const at::Tensor& k_scale,
-                            const at::Tensor& v_scale, const at::Tensor& k_calibration,
-                            const at::Tensor& cached_lens, const at::Tensor& slot_ids,
-                            const at::Tensor& num_decoding, double scale, const at::Tensor& out,
-                            const at::Tensor& workspace) {
-    const c10::DeviceGuard guard(q.device());
-    DecodeCall d = decode_prep(q, k_cache, v_cache, k_scale, v_scale, k_calibration, cached_lens,
-                               slot_ids, num_decoding, out);
-    TORCH_CHECK((size_t)workspace.numel() * workspace.element_size() >= d.ws_bytes,
-                "ie: workspace too small");
-    ok(ie_decode_attention_split(bf(q), q.stride(0), q.stride(1), d.B, d.hq, &d.c,
-                                 i32(cached_lens), i32(slot_ids), i32(num_decoding), (float)scale,
-                                 bfm(out), out.stride(0), out.stride(1), workspace.data_ptr(),
-                                 d.ws_bytes, stream_of(q)),
-       "decode_attention_split");
-}
-
-void decode_attention_combine(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
-                              const at::Tensor& cached_lens, const at::Tensor& num_decoding,
-                              const at::Tensor& out, const at::Tensor& workspace) {
-    check_bf16_rows(out, "out", 3);
-    const c10::DeviceGuard guard(out.device());
-    const size_t bytes =
-        ie_decode_attention_workspace_size((int32_t)batch, (int32_t)num_q_heads, 128);
-    TORCH_CHECK((size_t)workspace.numel() * workspace.element_size() >= bytes,
-                "ie: workspace too small");
-    ok(ie_decode_attention_combine((int32_t)batch, (int32_t)num_q_heads, 128,
-                                   (int32_t)num_kv_heads, i32(cached_lens), i32(num_decoding),
-                                   bfm(out), out.stride(0), out.stride(1), workspace.data_ptr(),
-                                   bytes, stream_of(out)),
-       "decode_attention_combine");
 }
 
 int64_t decode_attention_workspace_size(int64_t batch, int64_t num_q_heads) {
@@ -419,13 +408,6 @@ TORCH_LIBRARY(ie, m) {
         "decode_attention(Tensor q, Tensor k_cache, Tensor v_cache, Tensor k_scale, "
         "Tensor v_scale, Tensor k_calibration, Tensor cached_lens, Tensor slot_ids, "
         "Tensor num_decoding, float scale, Tensor(a!) out) -> ()");
-    m.def(
-        "decode_attention_split(Tensor q, Tensor k_cache, Tensor v_cache, Tensor k_scale, "
-        "Tensor v_scale, Tensor k_calibration, Tensor cached_lens, Tensor slot_ids, "
-        "Tensor num_decoding, float scale, Tensor(a!) out, Tensor(b!) workspace) -> ()");
-    m.def(
-        "decode_attention_combine(int batch, int num_q_heads, int num_kv_heads, "
-        "Tensor cached_lens, Tensor num_decoding, Tensor(a!) out, Tensor workspace) -> ()");
     m.def("decode_attention_workspace_size(int batch, int num_q_heads) -> int");
     m.def(
         "dequantize_kv_prefix(Tensor k_cache, Tensor v_cache, Tensor k_scale, Tensor v_scale, "
@@ -448,8 +430,6 @@ TORCH_LIBRARY_IMPL(ie, CUDA, m) {
     m.impl("skinny_matmul", &skinny_matmul);
     m.impl("skinny_matmul_silu_mul", &skinny_matmul_silu_mul);
     m.impl("decode_attention", &decode_attention);
-    m.impl("decode_attention_split", &decode_attention_split);
-    m.impl("decode_attention_combine", &decode_attention_combine);
     m.impl("dequantize_kv_prefix", &dequantize_kv_prefix);
     m.impl("prefill_attention", &prefill_attention);
 }

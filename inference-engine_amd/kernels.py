@@ -57,7 +57,8 @@ def decode_attention(
     scale,
     out: torch.Tensor | None = None,  # [>= B, Hq, D]; decoding entry b's output goes to row b
 ):
-    """qwen3-1.7b/kernels.py:272-361. Split-K kernel + reduce kernel on the current stream."""
+    """qwen3-1.7b/kernels.py:272-361. One launch on the current stream: the split-K kernel, whose
+    last piece per sequence also does the reference's reduce (kernels.py:216-264)."""
     k_cache, v_cache = kv_cache.k, kv_cache.v
     assert k_cache.stride() == v_cache.stride(), "kernel uses one set of strides for k and v"
     assert kv_cache.k_scale.stride() == kv_cache.v_scale.stride()
@@ -67,27 +68,6 @@ def decode_attention(
     assert out.shape[0] >= B and out.shape[1:] == (Hq, D) and out.stride(-1) == 1
     ops().decode_attention(q, *_cache_args(kv_cache), cached_lens, slot_ids, num_decoding,
                            float(scale), out)
-    return out
-
-
-def decode_attention_workspace(q: torch.Tensor) -> torch.Tensor:
-    """Workspace for `decode_attention_split`/`_combine` (fp32 split-K partials)."""
-    n = ops().decode_attention_workspace_size(q.shape[0], q.shape[1])
-    return torch.empty(max(int(n), 16), device=q.device, dtype=torch.uint8)
-
-
-def decode_attention_split(q, kv_cache, cached_lens, slot_ids, num_decoding, scale, out,
-                           workspace):
-    """First launch of `decode_attention` (split-K partials / single-piece outputs)."""
-    ops().decode_attention_split(q, *_cache_args(kv_cache), cached_lens, slot_ids, num_decoding,
-                                 float(scale), out, workspace)
-    return out
-
-
-def decode_attention_combine(q, kv_cache, cached_lens, num_decoding, out, workspace):
-    """Second launch of `decode_attention` (merge of the pieces, kernels.py:216-264)."""
-    ops().decode_attention_combine(q.shape[0], q.shape[1], kv_cache.k.shape[1], cached_lens,
-                                   num_decoding, out, workspace)
     return out
 
 

@@ -21,8 +21,7 @@ def test_library_exports_every_declared_symbol(native):
 def test_torch_ops_registered(ie):
     ops = ie.kernels.ops()
     for name in ["quantize_kv_prefill", "fused_rope_kv_decode", "fused_norm_rope_prefill",
-                 "decode_attention",
-                 "decode_attention_split", "decode_attention_combine", "dequantize_kv_prefix",
+                 "decode_attention", "dequantize_kv_prefix",
                  "prefill_attention", "decode_attention_workspace_size", "sample", "add_rms_norm",
                  "silu_mul", "skinny_matmul", "skinny_matmul_silu_mul"]:
         assert hasattr(ops, name), name
@@ -55,9 +54,10 @@ def test_bad_geometry_rejected_on_host(native):
 
 
 def test_workspace_size_formula(native):
-    """The plan record (piece size and one first-entry index per sequence after 64 ints, padded
-    to 256 bytes), then one fp32 partial (128 outputs, m, l) per query head and work entry; the
-    work entries are the split launch's grid: the target, or target + B above it."""
+    """The arrival counts (one uint32 per sequence and KV head, room for at least 1024 sequences,
+    padded to 256 bytes), then one
+    fp32 partial (128 outputs, m, l) per query head and work entry; the work entries are the
+    launch's grid: the target, or target + B above it."""
     lib = native.cabi()
     target = lib.ie_decode_attention_max_splits(8)
     assert target >= 1
@@ -65,7 +65,7 @@ def test_workspace_size_formula(native):
     for B in (1, 64, target, target + 1, 300, 1024):
         grid = lib.ie_decode_attention_grid(ctypes.c_int32(B), ctypes.c_int32(8))
         assert grid == (target if B <= target else target + B)
-        plan = -(-(64 + B) * 4 // 256) * 256
+        plan = -(-(max(B, 1024) * 8) * 4 // 256) * 256
         assert lib.ie_decode_attention_workspace_size(B, 16, 128) == plan + 16 * grid * 130 * 4
 
 

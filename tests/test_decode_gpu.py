@@ -52,6 +52,24 @@ def test_decode_ragged(ie, workloads, dev, ctx):
     assert_attn_close(bf16_np(out), ref, f"ragged {len(ctx)}")
 
 
+def test_decode_workspace_reuse_across_batches(ie, workloads, dev):
+    """The op keeps one zeroed workspace per stream whose arrival counts every call leaves at
+    zero: calls of growing, shrinking and above-1024 batches in a row, each against the oracle.
+    A count region that moved with the batch would let one call's partials land on the next
+    call's counts."""
+    rng = np.random.default_rng(17)
+    plan = [[20000], [3000] * 64, [64] * 40 + [9000], [int(x) for x in rng.integers(1, 200, 1100)],
+            [5, 4000, 70], [int(x) for x in rng.integers(1, 200, 1100)], [33000, 2]]
+    for i, ctx in enumerate(plan):
+        say(f"decode workspace reuse call {i}: B={len(ctx)} max ctx {max(ctx)}")
+        wl = workloads.decode_workload(ctx, seed=100 + i, pool=len(ctx) + 3)
+        ref = oracle_out(wl)
+        g = wl.to(dev)
+        out = ie.decode_attention(g.q, g.cache, g.cached_lens, g.slot_ids, g.num_decoding, SCALE)
+        torch.cuda.synchronize()
+        assert_attn_close(bf16_np(out), ref, f"reuse call {i} B={len(ctx)}")
+
+
 def test_decode_partial_batch_and_out_rows(ie, workloads, dev):
     """Rows >= num_decoding of `out` are untouched; out may be taller than B (mixed steps)."""
     ctx = [700, 40, 1500, 3, 64, 900]
@@ -194,28 +212,38 @@ def test_decode_plan_matches_oracle(ie, native, dev, ctx, nd):
 
 
 def test_decode_through_c_abi(ie, workloads, dev, native):
-    """The same computation driven through libie_attn.so's C entry point directly."""
+    """The same computation driven through libie_attn.so's C entry point directly, three times
+    on one workspace: the sequences of 300 and 2,000 tokens split into pieces that the last one
+    to finish merges, and every call leaves the workspace's arrival counts at zero again."""
     ctx = [300, 2000, 77]
     wl = workloads.decode_workload(ctx, seed=13)
     ref = oracle_out(wl)
     g = wl.to(dev)
     lib = native.cabi()
     ws_bytes = lib.ie_decode_attention_workspace_size(len(ctx), 16, 128)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)  # arrival counts start at 0
     out = torch.empty(len(ctx), 16, 128, dtype=torch.bfloat16, device=dev)
     desc = native.KVCacheDesc.of(g.cache)
     fn = lib.ie_decode_attention
     fn.restype = ctypes.c_int
     p = lambda t: ctypes.c_void_p(t.data_ptr())
-    rc = fn(p(g.q), ctypes.c_int64(g.q.stride(0)), ctypes.c_int64(g.q.stride(1)),
-            ctypes.c_int32(len(ctx)), ctypes.c_int32(16), ctypes.byref(desc), p(g.cached_lens),
-            p(g.slot_ids), p(g.num_decoding), ctypes.c_float(SCALE), p(out),
-            ctypes.c_int64(out.stride(0)), ctypes.c_int64(out.stride(1)), p(ws),
-            ctypes.c_size_t(ws_bytes),
-            ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
-    assert rc == 0, lib.ie_attn_last_error()
-    torch.cuda.synchronize()
-    assert_attn_close(bf16_np(out), ref, "c-abi decode")
+    first = None
+    for call in range(3):
+        out.fill_(9.0)
+        rc = fn(p(g.q), ctypes.c_int64(g.q.stride(0)), ctypes.c_int64(g.q.stride(1)),
+                ctypes.c_int32(len(ctx)), ctypes.c_int32(16), ctypes.byref(desc),
+                p(g.cached_lens), p(g.slot_ids), p(g.num_decoding), ctypes.c_float(SCALE),
+                p(out), ctypes.c_int64(out.stride(0)), ctypes.c_int64(out.stride(1)), p(ws),
+                ctypes.c_size_t(ws_bytes),
+                ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        assert rc == 0, lib.ie_attn_last_error()
+        torch.cuda.synchronize()
+        assert not ws[:len(ctx) * 8 * 4].any(), f"call {call} left arrival counts behind"
+        if first is None:
+            first = out.clone()
+            assert_attn_close(bf16_np(out), ref, "c-abi decode")
+        else:
+            assert torch.equal(out, first), f"call {call} differs from the first"
 
 
 def test_decode_split_count_invariance(ie, workloads, dev):

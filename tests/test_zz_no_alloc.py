@@ -1,7 +1,7 @@
 """ie_decode_attention_noalloc (the decode entry point that allocates nothing, its workspace
 in a static device array) against ie_decode_attention with a caller workspace, through the C
 ABI: identical bits on two calls in a row, the second with a smaller batch, and the host-side
-rejection of a batch whose workspace exceeds the array."""
+rejection of a batch above the 1024 sequences the array serves."""
 
 import ctypes
 
@@ -49,7 +49,7 @@ def test_noalloc_matches_workspace_entry(ie, workloads, native, dev):
         g = workloads.decode_workload(ctx, seed=seed, device=dev)
         ws_bytes = lib.ie_decode_attention_workspace_size(B, 16, 128)
         assert ws_bytes <= cap
-        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)  # arrival counts start at 0
         ref = torch.full((B, 16, 128), 5.0, dtype=torch.bfloat16, device=dev)
         got = torch.full((B, 16, 128), 6.0, dtype=torch.bfloat16, device=dev)
         _call(lib, native, g, ref, ws)
@@ -80,5 +80,15 @@ def test_noalloc_rejects_batch_beyond_scratch(ie, native, dev):
             p(out), ctypes.c_int64(2048), ctypes.c_int64(128),
             ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
     assert rc == 1 and b"no-alloc" in lib.ie_attn_last_error()
+    # a batch just above the 1024 sequences that share the array's count region
+    B = 1025
+    q = torch.zeros(B, 16, 128, dtype=torch.bfloat16, device=dev)
+    i = torch.zeros(B, dtype=torch.int32, device=dev)
+    out2 = torch.zeros_like(q)
+    rc = fn(p(q), ctypes.c_int64(2048), ctypes.c_int64(128), ctypes.c_int32(B),
+            ctypes.c_int32(16), ctypes.byref(desc), p(i), p(i), p(nd), ctypes.c_float(SCALE),
+            p(out2), ctypes.c_int64(2048), ctypes.c_int64(128),
+            ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert rc == 1 and b"no-alloc" in lib.ie_attn_last_error()
     torch.cuda.synchronize()
-    assert not out.any()
+    assert not out.any() and not out2.any()
