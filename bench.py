@@ -290,7 +290,7 @@ def bench_mixed_step(W, dev):
     return {"us_graph": round(ms * 1e3, 2), "rows": N, "decoders": len(wl.decode_ctx),
             "prefill_tokens": sum(L for L, _ in wl.chunks),
             "kernels": "fused_norm_rope_prefill, quantize_kv_prefill, prefill_attention "
-                       "(+ combine), fused_rope_kv_decode, decode_attention split + combine"}
+                       "(+ combine), fused_rope_kv_decode, decode_attention"}
 
 
 def bench_step(steps, warmup, dev):
