@@ -289,8 +289,8 @@ def bench_mixed_step(W, dev):
     ms = time_graph(op)
     return {"us_graph": round(ms * 1e3, 2), "rows": N, "decoders": len(wl.decode_ctx),
             "prefill_tokens": sum(L for L, _ in wl.chunks),
-            "kernels": "fused_norm_rope_prefill, quantize_kv_prefill, prefill_attention "
-                       "(+ combine), fused_rope_kv_decode, decode_attention"}
+            "kernels": "fused_norm_rope_prefill, quantize_kv_prefill, prefill_attention, "
+                       "fused_rope_kv_decode, decode_attention"}
 
 
 def bench_step(steps, warmup, dev):
@@ -404,7 +404,7 @@ def line_kv_write(args, ie, W, K, dev, alg_bytes, extra):
 
 
 def line_prefill_config4(args, ie, W, K, dev, alg_bytes, extra):
-    """Config 4's chunked-prefill attention (main kernel + combine), causal-exact flops."""
+    """Config 4's chunked-prefill attention (one launch; split pieces merge in it), causal-exact flops."""
     mw = W.mixed_to(W.config4(seed=0), dev)
     gi = mw.inputs
     flops = W.prefill_flops(mw.chunks)

@@ -253,9 +253,13 @@ hipError_t ie_dequantize_kv_prefix(const ie_kv_cache* cache, const int32_t* cu_c
  * count >= 1. Up to 512 entries a tile's entry is found by binary search over cu_seqlens
  * (the tables staged on chip) and seq_ids is not read; above 512 it is seq_ids[first row of the
  * tile], as in the reference kernel (kernels.py:1029), and seq_ids must hold num_tokens values.
- * Long key ranges are split across workgroups; `workspace` (partials) must hold
+ * Long key ranges are split across workgroups, and the last piece of a split range to finish
+ * merges the pieces in the same launch. `workspace` must hold
  * ie_prefill_attention_workspace_size(num_tiles, block_m, num_kv_heads) bytes, a size that
- * depends on the current device's CU count.
+ * depends on the current device's CU count only: one arrival count per resident workgroup
+ * (padded to 256 bytes), then the split pieces' partials. The counts must be zero the first
+ * time a workspace is used (allocate it zeroed); every launch leaves them zero, so one
+ * workspace serves every call in stream order. Calls that overlap on one workspace race.
  */
 size_t ie_prefill_attention_workspace_size(int32_t num_tiles, int32_t block_m,
                                            int32_t num_kv_heads);

@@ -139,16 +139,6 @@ __device__ __forceinline__ float fdot2(half2_t a, half2_t b, float c) {
 }
 __device__ __forceinline__ float exp2_safe(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Device-coherent float accesses (agent-scope relaxed atomics: global loads and stores with
-// the device scope bit, served at the level all XCDs share rather than from a possibly stale
-// per-XCD L2 line).
-__device__ __forceinline__ void st_dev(float* p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float ld_dev(const float* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 struct DecodeArgs {
     const uint16_t* q;
     int64_t q_sb, q_sh;
@@ -495,12 +485,7 @@ __attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_attenti
     // A sequence of several pieces: each piece publishes its partial (the sequence's pieces
     // are consecutive work entries) and counts itself in; the piece that arrives last merges
     // them all (kernels.py:216-264, in base 2, pieces in order) and resets the count for the
-    // next call. The partials are written and read with device-coherent accesses (ld_dev,
-    // st_dev), which the per-XCD L2s do not hold stale, and each wave waits for its stores to
-    // complete before the barrier that precedes the count: the ordering a device-scope
-    // release/acquire pair gives, without the L2 writeback and invalidate those fences cost on
-    // every workgroup.
-    uint32_t* const arrivals = a.arrivals + b * a.hkv + hk;
+    // next call. The partials are written and read with device-coherent accesses.
     if (active) {
         const int64_t row = (int64_t)qh_idx * a.nwork + item;
         st_dev(a.part_acc + row * DA_D + d, num);
@@ -509,14 +494,7 @@ __attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_attenti
             st_dev(a.part_l + row, den);
         }
     }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __shared__ uint32_t s_last;
-    __syncthreads();
-    if (threadIdx.x == 0)
-        s_last = __hip_atomic_fetch_add(arrivals, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                 (uint32_t)(wk.needed - 1);
-    __syncthreads();
-    if (!s_last || !active) return;
+    if (!arrive_last(a.arrivals + b * a.hkv + hk, wk.needed) || !active) return;
     const int needed = wk.needed;
     const int64_t row0 = (int64_t)qh_idx * a.nwork + (item - split);
     float pm = -INFINITY;
@@ -543,7 +521,6 @@ __attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_attenti
         }
     }
     *o = (uint16_t)f32_to_bf16_rne(num / den);
-    if (threadIdx.x == 0) __hip_atomic_store(arrivals, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // grid (work entries), block 64: the decode kernel's work list, one entry per workgroup index w

@@ -171,6 +171,50 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
 }
 
 // ---------------------------------------------------------------------------------------------
+// Device-coherent accesses, for partial results that one workgroup writes and another merges in
+// the same launch: loads and stores with the device scope bit (sc1), served at the level all
+// XCDs share rather than from a possibly stale per-XCD L2 line. The 4- and 8-byte forms are
+// agent-scope relaxed atomics; the 16-byte load is a buffer load with that cache policy. The
+// writer waits for its stores (wait_stores) before the barrier that precedes its arrival count,
+// and the merging workgroup reads only after that count: the order a device-scope release and
+// acquire give, without the whole-L2 writeback and invalidate those fences cost.
+// ---------------------------------------------------------------------------------------------
+constexpr int CPOL_SC1 = 16;  // buffer intrinsic cache policy: device scope
+__device__ __forceinline__ void st_dev(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_dev(const float* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_dev64(void* p, uint64_t v) {
+    __hip_atomic_store(reinterpret_cast<uint64_t*>(p), v, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t ld_dev64(const void* p) {
+    return __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+}
+// Every vector memory access of the wave, stores included, has completed.
+__device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// Counts the calling workgroup in at `count` (thread 0's device-scope atomic, after a barrier
+// that follows every wave's wait_stores) and returns, to every thread, whether it was the last
+// of `needed`; the last one resets the count to zero for the next launch.
+__device__ __forceinline__ bool arrive_last(uint32_t* count, int needed) {
+    __shared__ uint32_t s_last;
+    wait_stores();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const bool last =
+            __hip_atomic_fetch_add(count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+            (uint32_t)(needed - 1);
+        if (last) __hip_atomic_store(count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = last;
+    }
+    __syncthreads();
+    return s_last != 0;
+}
+
+// ---------------------------------------------------------------------------------------------
 // Host-side checks.
 // ---------------------------------------------------------------------------------------------
 void set_error(const char* msg);

@@ -21,8 +21,9 @@
 // or, when longer than T 64-key tiles, prefix pieces and chunk pieces of at most T tiles, T the
 // smallest size whose pieces fit one resident wave of workgroups (2 per CU). Workgroup w runs
 // piece w of the list (largest sub-blocks first). Unsplit pieces write `out`; split pieces
-// write a bf16 partial O (normalized) and fp32 (m, l) to their slot, and prefill_combine_kernel
-// merges them (log-sum-exp) from the split list the main kernel records.
+// write a bf16 partial O (normalized) and fp32 (m, l) to their slot and count themselves in,
+// and the piece of a (sub-block, kv head) that arrives last merges them all (log-sum-exp) into
+// `out` in the same launch.
 //
 // Per 64-key tile: the workgroup stages K as [key][d] and V transposed as [d][key] in LDS, and
 // the tile's score scales; wave w (query head 2hk + (w & 1), rows 32 (w >> 1)..+32) computes
@@ -33,6 +34,8 @@
 //   l += ones . P^T                     the row sums, on the MFMA as well
 // software-pipelined: the QK^T of tile j+1 beside the softmax of tile j, the PV of tile j beside
 // the staging of the next K and V tiles, whose global loads were issued a step earlier.
+#include <cstdlib>
+
 #include "ie_common.h"
 
 namespace ie {
@@ -127,10 +130,13 @@ struct PrefillArgs {
     ie_kv_cache c;
     uint16_t* out;
     int64_t o_st, o_sh;
-    uint16_t* part_o;  // [slot][64 rows][2 heads][128] bf16: normalized partial O of split items
-    float* part_ml;    // [slot][64 rows][2 heads][2]: their (m, l)
-    int* sched;  // [0] piece size T, [1] split sub-blocks n, then per split sub-block i (launch
-                 // order) 4 ints at 4 + 4i: first item, r0, r1, pieces
+    uint16_t* part_o;  // [slot][8 channel blocks][2 heads][PF_BM rows][16] bf16: normalized
+                       // partial O of split items, in the accumulators' order (a store of 16
+                       // rows x 16 channels is 512 contiguous bytes)
+    float* part_ml;    // [slot][2 heads][PF_BM rows][2]: their (m, l)
+    uint32_t* arrivals;  // [2][grid]: arrival and finish words of each split (sub-block, kv
+                         // head) pair, at the pair's first item; 0 between launches
+    uint64_t merge_wait_ticks;  // longest wait of a piece for its pair's others (100 MHz clock)
     int block_m, sub_per_tile, hq, hkv;
     int nent;  // entries (length of slot_ids; cu_seqlens and cu_cached hold nent + 1)
     int ntok;  // packed rows (length of seq_ids)
@@ -209,8 +215,6 @@ __device__ __forceinline__ void fill_sub_block(SubBlock& s, int r0, int r1, int 
 
 struct Loc {
     int sb, off, item_base, T;
-    int nsplit;       // split sub-blocks in the launch
-    int split_index;  // rank of sub-block sb among them (launch order)
     int found;
     SubBlock s;       // sub-block sb
 };
@@ -311,8 +315,7 @@ __device__ Loc schedule(const PrefillArgs& a, int target, int* tables) {
         // workgroup past them has no item (these start late, once resident ones finish, and
         // would otherwise spend the rest of the schedule finding that out)
         L.T = 0;
-        L.nsplit = 0;
-        L.sb = L.off = L.item_base = L.split_index = 0;
+        L.sb = L.off = L.item_base = 0;
         L.s = SubBlock{};
         return L;
     }
@@ -333,22 +336,11 @@ __device__ Loc schedule(const PrefillArgs& a, int target, int* tables) {
 #pragma unroll
     for (int c = 0; c < PF_SCHED_CHUNKS; ++c) np[c] = piece_count(zc[c].npt, zc[c].nct, DT);
     L.found = 0;
-    L.sb = L.off = L.item_base = L.split_index = 0;
-    {
-        int ns = 0;
-#pragma unroll
-        for (int c = 0; c < PF_SCHED_CHUNKS; ++c) ns += np[c] > 1;
-        for (int c = PF_SCHED_CHUNKS; c < nchunks; ++c) {
-            const SbInfo z = info(sb_of(c), row_start_of(sb_of(c)));
-            ns += piece_count(z.npt, z.nct, DT) > 1;
-        }
-        L.nsplit = uni(wave_sum_i(ns));
-    }
-    int items_before = 0, split_before = 0;
+    L.sb = L.off = L.item_base = 0;
+    int items_before = 0;
     auto visit = [&](int c, const SbInfo& z, int np) {
         const int items = np * a.hkv;
         const int incl = wave_incl_scan_i(items) + items_before;
-        const int sincl = wave_incl_scan_i(np > 1) + split_before;
         const unsigned long long hit = __ballot(target < incl && target >= incl - items);
         if (hit) {
             const int src = __builtin_ctzll(hit);  // the same lane in every wave: uniform
@@ -356,13 +348,11 @@ __device__ Loc schedule(const PrefillArgs& a, int target, int* tables) {
             L.sb = from(sb_of(c));
             L.item_base = from(incl - items);
             L.off = target - L.item_base;
-            L.split_index = from(sincl - (np > 1));
             fill_sub_block(L.s, from(z.r0), from(z.r1), from(z.seq_start), from(z.P),
                            from(z.slot), DT);
             L.found = 1;
         }
         items_before = __builtin_amdgcn_readlane(incl, 63);
-        split_before = __builtin_amdgcn_readlane(sincl, 63);
         return L.found != 0;
     };
 #pragma unroll
@@ -773,9 +763,12 @@ __device__ __forceinline__ void load_q(bf16x8 (&qf)[2][4], const PrefillArgs& a,
 #define IE_PREFILL_WG_PER_CU (8 / IE_PREFILL_WAVES)
 #endif
 
+__device__ __forceinline__ void merge_pieces(const PrefillArgs& a, const SubBlock& s, int hk,
+                                             int item_base);
+
 // One work item: tiles [kt_begin, kt_end) of piece `piece` of sub-block s for kv head hk.
 __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBlock& s, int hk,
-                                             int piece, int item, PfLds& lds) {
+                                             int piece, int item, int item_base, PfLds& lds) {
     // tiles [kt_begin, kt_end): the whole pair, a prefix piece or a chunk piece
     int kt_begin = 0, kt_end = s.ntiles;
     if (s.npieces > 1) {
@@ -995,18 +988,161 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBloc
                     u32x2{pack_bf16x2(x[0] * rl, x[1] * rl), pack_bf16x2(x[2] * rl, x[3] * rl)};
             }
         } else {  // normalized partial O in bf16 (a weighted mean of V rows) and fp32 (m, l)
-            const int64_t prow = ((int64_t)item * PF_BM + (row - s.r0)) * 2 + (wave & 1);
+            const int rr = (wave & 1) * PF_BM + (row - s.r0);  // the slot's row (head-major)
+            const int64_t prow = (int64_t)item * 2 * PF_BM + rr;
 #pragma unroll
             for (int mt = 0; mt < 8; ++mt) {
                 const f32x4 x = ws.acc[mt][nt];
-                *reinterpret_cast<u32x2*>(a.part_o + prow * PF_D + 16 * mt + 4 * g) =
-                    u32x2{pack_bf16x2(x[0] * rl, x[1] * rl), pack_bf16x2(x[2] * rl, x[3] * rl)};
+                st_dev64(a.part_o + (prow - rr) * PF_D + (mt * 2 * PF_BM + rr) * 16 + 4 * g,
+                         (uint64_t)pack_bf16x2(x[0] * rl, x[1] * rl) |
+                             ((uint64_t)pack_bf16x2(x[2] * rl, x[3] * rl) << 32));
             }
             if (g == 0)
-                *reinterpret_cast<float2*>(a.part_ml + prow * 2) =
-                    make_float2(l != 0.f ? -ws.nmb[nt] : -INFINITY, l);
+                st_dev64(a.part_ml + prow * 2,
+                         (uint64_t)__float_as_uint(l != 0.f ? -ws.nmb[nt] : -INFINITY) |
+                             ((uint64_t)__float_as_uint(l) << 32));
         }
     }
+    if (s.npieces == 1) return;
+    merge_pieces(a, s, hk, item_base);
+}
+
+// Merge of a split (sub-block, kv head) pair, in the launch that computed its pieces. Piece p ran
+// as item item_base + p * Hkv + hk and wrote its partial rows to that item's slot. The pair's
+// (row, query head) outputs are cut into npieces shares, and the merge of share k (log-sum-exp
+// in base 2, pieces in order) reads share k's rows of every piece's partial:
+//  * each piece counts itself in at arrivals[item_base + hk] (its arrival index k), then waits
+//    until all pieces have arrived, for at most a.merge_wait_ticks of the 100 MHz real-time
+//    clock, and merges share k; the last to arrive merges its share at once. The wait spreads
+//    the merge over the pair's workgroups (one workgroup alone reads device-coherent data at a
+//    fraction of the rate the pair's pieces reach together);
+//  * each then adds (1 << 16) | (merged ? 1 << k : 0) to the pair's finish word
+//    (arrivals[grid + item_base + hk]); the last to finish merges every share whose owner gave
+//    up waiting (none, unless a piece ran long after the others) and resets both words to zero.
+// Every wait ends; a piece that gives up costs time, not correctness. The pair's words sit at
+// its first item: split items are numbered below the slot count and no other pair's first item
+// is that one.
+__device__ __forceinline__ void merge_pieces(const PrefillArgs& a, const SubBlock& s, int hk,
+                                             int item_base) {
+    const int np = s.npieces, nrows = s.r1 - s.r0;
+    uint32_t* const arr = a.arrivals + item_base + hk;
+    uint32_t* const fin = a.arrivals + a.grid + item_base + hk;
+    __shared__ int s_k, s_go, s_missing;
+    wait_stores();  // this wave's partial is written
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int k = (int)__hip_atomic_fetch_add(arr, 1u, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT);
+        int go = k == np - 1;
+        if (!go) {
+            const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+            for (;;) {
+                if ((int)__hip_atomic_load(arr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= np) {
+                    go = 1;
+                    break;
+                }
+                if (__builtin_amdgcn_s_memrealtime() - t0 > a.merge_wait_ticks) break;
+                __builtin_amdgcn_s_sleep(2);
+            }
+        }
+        s_k = k;
+        s_go = go;
+    }
+    __syncthreads();
+    const int k = s_k;
+    const bool go = s_go != 0;
+
+    // 16 lanes per (row, query head), 8 channels each: a wave's load reads four consecutive slot
+    // rows, 128 contiguous bytes in each of the 8 channel blocks. Group G of 16 lanes merges the
+    // share's pairs G, G + GR, ...
+    constexpr int GR = PF_THREADS / 16;
+    const int G = threadIdx.x >> 4, c0 = 8 * (threadIdx.x & 15);
+    const rsrc_t po = make_rsrc(a.part_o, (uint32_t)a.grid * PF_BM * 2 * PF_D * 2);
+    const rsrc_t pml = make_rsrc(a.part_ml, (uint32_t)a.grid * PF_BM * 2 * 2 * 4);
+    // piece p's partial slot; the pair q of the share (head-major: head q / nrows, row q % nrows)
+    // is slot row rr = head * PF_BM + row
+    auto slot_of = [&](int p) { return item_base + p * a.hkv + hk; };
+    auto merge_share = [&](int share) {
+        const int npairs = 2 * nrows;
+        const int pb = share * npairs / np, pe = (share + 1) * npairs / np;
+        constexpr int U = 2;  // pairs per group whose loads are in flight together
+#pragma unroll 1
+        for (int q0 = pb; q0 < pe; q0 += U * GR) {
+            // (m, l) and the channels of every piece of U pairs in one round trip (an offset past
+            // a buffer's range reads zeros without a memory access)
+            u32x2 ml[U][PF_MAXP];
+            u32x4 o[U][PF_MAXP];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int q = q0 + u * GR + G;
+                const bool row_in = q < pe;
+                const int hh = q >= nrows, rr = hh * PF_BM + q - hh * nrows;
+#pragma unroll
+                for (int p = 0; p < PF_MAXP; ++p) {
+                    const bool in = row_in && p < np;
+                    const int sl = slot_of(p);
+                    ml[u][p] = __builtin_amdgcn_raw_buffer_load_b64(
+                        pml, in ? (sl * 2 * PF_BM + rr) * 8 : -64, 0, CPOL_SC1);
+                    // channels c0..c0 + 7: 16-channel block c0 / 16, half (c0 / 8) & 1
+                    o[u][p] = __builtin_amdgcn_raw_buffer_load_b128(
+                        po,
+                        in ? (sl * 2 * PF_BM * PF_D + ((c0 >> 4) * 2 * PF_BM + rr) * 16 + (c0 & 8)) * 2
+                           : -64,
+                        0, CPOL_SC1);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int q = q0 + u * GR + G;
+                if (q >= pe) continue;
+                const int hh = q >= nrows, row = s.r0 + q - hh * nrows;
+                float mx = -INFINITY;
+#pragma unroll
+                for (int p = 0; p < PF_MAXP; ++p)
+                    mx = fmaxf(mx, p < np ? __uint_as_float(ml[u][p][0]) : -INFINITY);
+                float num[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, den = 0.f;
+#pragma unroll
+                for (int p = 0; p < PF_MAXP; ++p) {
+                    // piece weight: its softmax mass l * 2^(m - mx) (0 for a piece with no
+                    // visible key)
+                    const float m = __uint_as_float(ml[u][p][0]);
+                    const float w =
+                        p >= np || m == -INFINITY
+                            ? 0.f
+                            : __uint_as_float(ml[u][p][1]) * __builtin_amdgcn_exp2f(m - mx);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        num[2 * j] += bf16lo(o[u][p][j]) * w;
+                        num[2 * j + 1] += bf16hi(o[u][p][j]) * w;
+                    }
+                    den += w;
+                }
+                const float rd = den != 0.f ? 1.f / den : 0.f;
+                uint16_t* dst = a.out + row * a.o_st + (2 * hk + hh) * a.o_sh + c0;
+                *reinterpret_cast<u32x4*>(dst) = u32x4{
+                    pack_bf16x2(num[0] * rd, num[1] * rd), pack_bf16x2(num[2] * rd, num[3] * rd),
+                    pack_bf16x2(num[4] * rd, num[5] * rd), pack_bf16x2(num[6] * rd, num[7] * rd)};
+            }
+        }
+    };
+    if (go) merge_share(k);
+    if (threadIdx.x == 0) {
+        const uint32_t mine = (1u << 16) | (go ? 1u << k : 0u);
+        const uint32_t old =
+            __hip_atomic_fetch_add(fin, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        int missing = -1;  // not the last to finish
+        if ((int)(old >> 16) == np - 1) {
+            missing = (int)(~(old | mine) & ((1u << np) - 1));
+            __hip_atomic_store(arr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(fin, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        s_missing = missing;
+    }
+    __syncthreads();
+    const int missing = s_missing;
+    if (missing > 0)
+        for (int share = 0; share < np; ++share)
+            if ((missing >> share) & 1) merge_share(share);
 }
 
 
@@ -1025,111 +1161,33 @@ __global__ __launch_bounds__(PF_THREADS, IE_PREFILL_WG_PER_CU) void prefill_atte
 #pragma unroll
         for (int i = 0; i < (int)(sizeof(Loc) / sizeof(int)); ++i) f[i] = uni(f[i]);
     }
-    if (blockIdx.x == 0 && threadIdx.x == 0) {
-        a.sched[0] = loc.T;
-        a.sched[1] = loc.nsplit;
-    }
     if (!loc.found) return;
-    const SubBlock& s = loc.s;
-    if (loc.off == 0 && s.npieces > 1 && threadIdx.x == 0) {
-        *reinterpret_cast<int4*>(a.sched + 4 + 4 * loc.split_index) =
-            make_int4(loc.item_base, s.r0, s.r1, s.npieces);
-    }
-    prefill_item(a, s, loc.off % a.hkv, loc.off / a.hkv, blockIdx.x, lds);
+    prefill_item(a, loc.s, loc.off % a.hkv, loc.off / a.hkv, blockIdx.x, loc.item_base, lds);
 }
 
-constexpr int PF_COMB_GROUPS = 4;  // combine units per (split sub-block, kv head): PF_THREADS / 8
-                                   // (row, query head) pairs each
-
-// grid (slots), block 256: merges the pieces of split sub-blocks (log-sum-exp, base 2) from the
-// list the main kernel recorded. Unit: split sub-block k, kv head hk, and 32 of its 128 (row,
-// query head) pairs; 8 threads per pair, 16 channels each, all loads issued up front.
-// Workgroups are dealt to the 8 XCDs round-robin (workgroup w runs on XCD w % 8), and the pieces
-// of (k, hk) ran as workgroups item_base + p * Hkv + hk: with Hkv a multiple of 8 they all ran
-// on XCD (item_base + hk) % 8, and the unit is given to a workgroup of that XCD, whose L2 holds
-// the partials.
-__global__ __launch_bounds__(PF_THREADS) void prefill_combine_kernel(PrefillArgs a) {
-    const int tid = threadIdx.x, d = 16 * (tid & 7);
-    const bool by_xcd = (a.hkv & 7) == 0 && (gridDim.x & 7) == 0;
-    const int hk8 = a.hkv >> 3;
-    const int per_k = (by_xcd ? hk8 : a.hkv) * PF_COMB_GROUPS;
-    const int u0 = by_xcd ? blockIdx.x >> 3 : blockIdx.x;
-    const int ustep = by_xcd ? gridDim.x >> 3 : gridDim.x;
-    // the split count and the first unit's record in one memory round trip (records exist for
-    // k < nsb; the count decides which of them are this launch's)
-    const int k0 = u0 / per_k;
-    int4 rec = {0, 0, 0, 0};  // the record of unit u's split sub-block
-    if (k0 < a.nsb) rec = *reinterpret_cast<const int4*>(a.sched + 4 + 4 * k0);
-    const int nsplit = uni(a.sched[1]);
-    const int units = nsplit * per_k;
-    for (int u = u0; u < units; u += ustep) {
-        const int k = u / per_k, hr = (u % per_k) / PF_COMB_GROUPS, grp = u % PF_COMB_GROUPS;
-        if (u != u0) rec = *reinterpret_cast<const int4*>(a.sched + 4 + 4 * k);
-        const int item_base = uni(rec.x);
-        const int hk = by_xcd ? 8 * hr + (((int)(blockIdx.x & 7) - item_base) & 7) : hr;
-        SubBlock s;
-        s.r0 = uni(rec.y);
-        s.r1 = uni(rec.z);
-        s.npieces = uni(rec.w);
-        const int pr = grp * (PF_THREADS / 8) + (tid >> 3);
-        const int row = s.r0 + (pr >> 1), hh = pr & 1;
-        if (row >= s.r1) continue;
-        float2 ml[PF_MAXP];
-        u32x4 o[PF_MAXP][2];
-#pragma unroll
-        for (int p = 0; p < PF_MAXP; ++p) {
-            ml[p] = make_float2(-INFINITY, 0.f);
-            o[p][0] = o[p][1] = u32x4{0u, 0u, 0u, 0u};
-            if (p < s.npieces) {
-                const int item = item_base + p * a.hkv + hk;
-                const int64_t prow = ((int64_t)item * PF_BM + (row - s.r0)) * 2 + hh;
-                ml[p] = *reinterpret_cast<const float2*>(a.part_ml + prow * 2);
-                o[p][0] = *reinterpret_cast<const u32x4*>(a.part_o + prow * PF_D + d);
-                o[p][1] = *reinterpret_cast<const u32x4*>(a.part_o + prow * PF_D + d + 8);
-            }
-        }
-        float mx = -INFINITY;
-#pragma unroll
-        for (int p = 0; p < PF_MAXP; ++p) mx = fmaxf(mx, ml[p].x);
-        float num[16];
-#pragma unroll
-        for (int j = 0; j < 16; ++j) num[j] = 0.f;
-        float den = 0.f;
-#pragma unroll
-        for (int p = 0; p < PF_MAXP; ++p) {
-            // piece weight: its softmax mass l * 2^(m - mx) (0 for pieces with no visible key)
-            const float w =
-                ml[p].x == -INFINITY ? 0.f : ml[p].y * __builtin_amdgcn_exp2f(ml[p].x - mx);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const uint32_t word = o[p][j >> 2][j & 3];
-                num[2 * j] += bf16lo(word) * w;
-                num[2 * j + 1] += bf16hi(word) * w;
-            }
-            den += w;
-        }
-        const float rd = den != 0.f ? 1.f / den : 0.f;
-        uint32_t y[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) y[j] = pack_bf16x2(num[2 * j] * rd, num[2 * j + 1] * rd);
-        uint16_t* dst = a.out + row * a.o_st + (2 * hk + hh) * a.o_sh + d;
-        *reinterpret_cast<u32x4*>(dst) = u32x4{y[0], y[1], y[2], y[3]};
-        *reinterpret_cast<u32x4*>(dst + 8) = u32x4{y[4], y[5], y[6], y[7]};
-    }
+// How long a split piece waits for its pair's other pieces before leaving its share of the
+// merge to the last one to finish, in ticks of the 100 MHz real-time clock: 100 us, or
+// IE_PREFILL_MERGE_WAIT_US (read at every call; 0 makes every piece but the last give up at
+// once, which tests the fallback).
+static uint64_t merge_wait_ticks() {
+    const char* e = std::getenv("IE_PREFILL_MERGE_WAIT_US");
+    const long us = e && *e ? std::strtol(e, nullptr, 10) : 100;
+    return (uint64_t)std::max(0L, std::min(us, 10000000L)) * 100;
 }
 
 // Partial slots: one resident wave of main-kernel workgroups (split items never outnumber it).
 static int prefill_slots() { return std::max(1, device_cu_count() * IE_PREFILL_WG_PER_CU); }
 
-// Workspace: schedule record (4 + 4 ints per sub-block, padded to 256 B), then per partial
-// slot 64 rows x 2 query heads of (m, l) fp32 and 128 bf16 channels.
+// Workspace: an arrival word and a finish word per partial slot (padded to 256 B; zero on entry,
+// and every launch leaves them zero), then per partial slot PF_BM rows x 2 query heads of (m, l)
+// fp32 and 128 bf16 channels. The layout depends on the device only, so one workspace serves
+// every launch.
 struct PrefillWs {
-    size_t sched_bytes, ml_off, o_off, bytes;
+    size_t ml_off, o_off, bytes;
 };
-static PrefillWs prefill_ws(int64_t nsb, int slots) {
+static PrefillWs prefill_ws(int slots) {
     PrefillWs w;
-    w.sched_bytes = (size_t)((4 * (4 * nsb + 4) + 255) / 256 * 256);
-    w.ml_off = w.sched_bytes;
+    w.ml_off = (2 * (size_t)slots * sizeof(uint32_t) + 255) / 256 * 256;
     w.o_off = w.ml_off + (size_t)slots * PF_BM * 2 * 2 * sizeof(float);
     w.bytes = w.o_off + (size_t)slots * PF_BM * 2 * PF_D * sizeof(uint16_t);
     return w;
@@ -1142,8 +1200,7 @@ using namespace ie;
 extern "C" size_t ie_prefill_attention_workspace_size(int32_t num_tiles, int32_t block_m,
                                                       int32_t num_kv_heads) {
     if (num_tiles <= 0 || block_m <= 0 || num_kv_heads <= 0) return 0;
-    const int64_t nsb = (int64_t)num_tiles * ((block_m + PF_BM - 1) / PF_BM);
-    return prefill_ws(nsb, prefill_slots()).bytes;
+    return prefill_ws(prefill_slots()).bytes;
 }
 
 extern "C" hipError_t ie_prefill_attention(
@@ -1181,7 +1238,7 @@ extern "C" hipError_t ie_prefill_attention(
     const int64_t nsb = (int64_t)num_tiles * ((block_m + PF_BM - 1) / PF_BM);
     IE_REQUIRE(nsb < (1 << 24), "too many tiles");
     const int slots = prefill_slots();
-    const PrefillWs wsl = prefill_ws(nsb, slots);
+    const PrefillWs wsl = prefill_ws(slots);
     const size_t need = wsl.bytes;
     IE_REQUIRE(workspace != nullptr && workspace_bytes >= need && al16(workspace),
                "workspace too small");
@@ -1204,7 +1261,7 @@ extern "C" hipError_t ie_prefill_attention(
     a.out = (uint16_t*)out;
     a.o_st = out_stride_tok;
     a.o_sh = out_stride_head;
-    a.sched = (int*)workspace;
+    a.arrivals = (uint32_t*)workspace;
     a.part_ml = (float*)((char*)workspace + wsl.ml_off);
     a.part_o = (uint16_t*)((char*)workspace + wsl.o_off);
     a.block_m = block_m;
@@ -1216,11 +1273,8 @@ extern "C" hipError_t ie_prefill_attention(
     a.nsb = (int)nsb;
     a.grid = slots;
     a.qk_scale = (float)(0.08838834764831845 * 1.4426950408889634);  // D^-0.5 * log2(e), D = 128
+    a.merge_wait_ticks = merge_wait_ticks();
     const unsigned grid = (unsigned)std::max<int64_t>(slots, nsb * cache->num_kv_heads);
     hipLaunchKernelGGL(prefill_attention_kernel, dim3(grid), dim3(PF_THREADS), 0, stream, a);
-    e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(prefill_combine_kernel, dim3((unsigned)slots), dim3(PF_THREADS), 0, stream,
-                       a);
     return hipGetLastError();
 }

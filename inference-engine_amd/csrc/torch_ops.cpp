@@ -287,22 +287,19 @@ DecodeCall decode_prep(const at::Tensor& q, const at::Tensor& k_cache, const at:
     return d;
 }
 
-at::Tensor workspace_for(const at::Tensor& q, size_t bytes) {
-    return at::empty({(int64_t)std::max<size_t>(bytes, 16)}, q.options().dtype(at::kByte));
-}
-
-// The decode workspace carries arrival counts that must be zero on entry and that every call
-// leaves zero, so it is kept across calls: one per (device, stream), allocated zeroed on first
-// use and replaced by a larger one when a call needs more. Replaced buffers are kept too: a
-// graph captured with one still addresses it. Calls in stream order never overlap on a buffer.
-// Batches up to 1024 sequences share a buffer (their count regions coincide); a larger batch
-// has a buffer of its own.
-at::Tensor decode_workspace(const at::Tensor& q, size_t bytes, int32_t batch) {
+// The decode and prefill workspaces carry arrival counts that must be zero on entry and that
+// every call leaves zero, so they are kept across calls: one per (device, stream, kind),
+// allocated zeroed on first use and replaced by a larger one when a call needs more. Replaced
+// buffers are kept too: a graph captured with one still addresses it. Calls in stream order
+// never overlap on a buffer. Kinds: prefill; decode of up to 1024 sequences (their count
+// regions coincide); decode of each larger batch size.
+constexpr int32_t WS_PREFILL = -1;
+at::Tensor persistent_workspace(const at::Tensor& q, size_t bytes, int32_t kind) {
     static std::mutex mu;
     static auto* cache =
         new std::map<std::tuple<int, hipStream_t, int32_t>, std::vector<at::Tensor>>();  // kept
     std::lock_guard<std::mutex> lock(mu);
-    auto& held = (*cache)[{q.device().index(), stream_of(q), batch <= 1024 ? 0 : batch}];
+    auto& held = (*cache)[{q.device().index(), stream_of(q), kind}];
     if (held.empty() || (size_t)held.back().numel() < bytes) {
         const int64_t n = (int64_t)std::max<size_t>(bytes, 256);
         held.push_back(at::zeros({n}, q.options().dtype(at::kByte)));
@@ -318,7 +315,7 @@ void decode_attention(const at::Tensor& q, const at::Tensor& k_cache, const at::
     const c10::DeviceGuard guard(q.device());
     DecodeCall d = decode_prep(q, k_cache, v_cache, k_scale, v_scale, k_calibration, cached_lens,
                                slot_ids, num_decoding, out);
-    at::Tensor ws = decode_workspace(q, d.ws_bytes, d.B);
+    at::Tensor ws = persistent_workspace(q, d.ws_bytes, d.B <= 1024 ? 0 : d.B);
     ok(ie_decode_attention(bf(q), q.stride(0), q.stride(1), d.B, d.hq, &d.c, i32(cached_lens),
                            i32(slot_ids), i32(num_decoding), (float)scale, bfm(out),
                            out.stride(0), out.stride(1), ws.data_ptr(), d.ws_bytes, stream_of(q)),
@@ -373,7 +370,7 @@ at::Tensor prefill_attention(const at::Tensor& q, const at::Tensor& k, const at:
     at::Tensor out = at::empty({N, q.size(1), q.size(2)}, q.options());
     const size_t ws_bytes = ie_prefill_attention_workspace_size(
         (int32_t)tile_start.size(0), (int32_t)block_m, c.num_kv_heads);
-    at::Tensor ws = workspace_for(q, ws_bytes);
+    at::Tensor ws = persistent_workspace(q, ws_bytes, WS_PREFILL);
     ok(ie_prefill_attention(bf(q), q.stride(0), q.stride(1), bf(k), k.stride(0), k.stride(1),
                             bf(v), v.stride(0), v.stride(1), N, (int32_t)q.size(1), i32(seq_ids),
                             i32(cu_seqlens), i32(tile_start), (int32_t)tile_start.size(0),

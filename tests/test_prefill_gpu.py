@@ -82,3 +82,25 @@ def test_prefill_long_sampled(ie, workloads, dev, chunks):
     o = bf16_np(out)
     assert np.isfinite(o).all()
     assert_attn_close(o[rows], ref[rows], f"prefill long {chunks[0]} x {len(chunks)}")
+
+
+@pytest.mark.parametrize("chunks", [[(512, 0), (512, 1536)], [(300, 5000), (64, 9000)]])
+def test_prefill_split_merge_fallback(ie, workloads, dev, monkeypatch, chunks):
+    """Split pieces wait a bounded time for their pair's other pieces and then merge a share
+    each; a piece that gives up leaves its share to the last one to finish. With the wait set to
+    zero every piece but the last gives up, so the last finisher merges every share: the output
+    must be bit-identical to the cooperative merge, and the next calls (the counters left at
+    zero) too."""
+    say(f"prefill split-merge fallback {chunks}")
+    wl = workloads.mixed_to(workloads.mixed_workload([], chunks, seed=5, block_m=128,
+                                                     max_len=10240), dev)
+    monkeypatch.delenv("IE_PREFILL_MERGE_WAIT_US", raising=False)
+    coop = run_gpu(ie, wl)
+    monkeypatch.setenv("IE_PREFILL_MERGE_WAIT_US", "0")
+    fall = [run_gpu(ie, wl) for _ in range(3)]
+    monkeypatch.delenv("IE_PREFILL_MERGE_WAIT_US")
+    again = run_gpu(ie, wl)
+    torch.cuda.synchronize()
+    for i, f in enumerate(fall):
+        assert torch.equal(f.view(torch.int16), coop.view(torch.int16)), f"fallback call {i}"
+    assert torch.equal(again.view(torch.int16), coop.view(torch.int16))
