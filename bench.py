@@ -404,7 +404,8 @@ def line_kv_write(args, ie, W, K, dev, alg_bytes, extra):
 
 
 def line_prefill_config4(args, ie, W, K, dev, alg_bytes, extra):
-    """Config 4's chunked-prefill attention (one launch; split pieces merge in it), causal-exact flops."""
+    """Config 4's chunked-prefill attention (one launch; split pieces merge in it),
+    causal-exact flops."""
     mw = W.mixed_to(W.config4(seed=0), dev)
     gi = mw.inputs
     flops = W.prefill_flops(mw.chunks)
