@@ -142,9 +142,18 @@ hipError_t ie_fused_rope_kv_decode(const ie_bf16* q, int64_t q_stride_b, int64_t
  */
 size_t ie_decode_attention_workspace_size(int32_t batch, int32_t num_q_heads, int32_t head_dim);
 
-/* Upper bound on splits per sequence on the current device (the per-KV-head workgroup target of
- * the work split: CUs * 2 / num_kv_heads). */
+/* Upper bound on splits per sequence on the current device: the largest per-KV-head workgroup
+ * target of any launch shape (CUs * 8 / num_kv_heads, 2-wave workgroups). */
 int32_t ie_decode_attention_max_splits(int32_t num_kv_heads);
+
+/*
+ * The per-KV-head workgroup target of the work split (qwen3-1.7b/kernels.py:20-37 TARGET) that
+ * ie_decode_attention uses for `batch` sequences on the current device. The launch fills the CUs
+ * with 16 waves each, as 8-wave workgroups (target CUs * 2 / num_kv_heads) while the batch fits
+ * that target, else as 4-wave (CUs * 4 / num_kv_heads) or 2-wave (CUs * 8 / num_kv_heads)
+ * workgroups, the first whose target holds the batch (the 2-wave one above that).
+ */
+int32_t ie_decode_attention_target(int32_t batch, int32_t num_kv_heads);
 
 /*
  * Split-K GQA decode attention over the int8 cache, with the partial-softmax reduce folded into

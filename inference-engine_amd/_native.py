@@ -50,6 +50,8 @@ def cabi() -> ctypes.CDLL:
         _cabi.ie_decode_attention_workspace_size.argtypes = [ctypes.c_int32] * 3
         _cabi.ie_decode_attention_max_splits.restype = ctypes.c_int32
         _cabi.ie_decode_attention_max_splits.argtypes = [ctypes.c_int32]
+        _cabi.ie_decode_attention_target.restype = ctypes.c_int32
+        _cabi.ie_decode_attention_target.argtypes = [ctypes.c_int32, ctypes.c_int32]
     return _cabi
 
 

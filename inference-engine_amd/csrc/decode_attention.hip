@@ -28,19 +28,18 @@
 
 #include "ie_common.h"
 
-// Launch shape (measured on MI355X, B=64 ctx=4096): 8-wave workgroups, 2 per CU (the
-// register budget allows 4 waves per SIMD), so one piece covers a whole 4096-token row there.
-#ifndef IE_DECODE_WG_PER_CU
-#define IE_DECODE_WG_PER_CU 2
-#endif
+// Launch shape: 16 waves per CU (the 128-register budget allows 4 waves per SIMD), as 8-wave
+// workgroups, 2 per CU, while the batch fits their per-head target, else 4-wave workgroups
+// (4 per CU) or 2-wave workgroups (8 per CU), whose targets are twice and four times as large
+// (decode_waves). Measured on MI355X: 8 waves are best up to B = 64 (one 4096-token piece per
+// row at B=64 ctx=4096); above, the smaller workgroups keep every sequence in one resident
+// round of fitted pieces instead of the reference rule's target + B pieces: B=96 ctx=1024
+// -15 % (4 waves), B=256 ctx=512 -31 % and ctx=1024 -11 % (2 waves), long contexts level.
 
 namespace ie {
 
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 
-#ifndef IE_DECODE_WG_WAVES
-#define IE_DECODE_WG_WAVES 8
-#endif
 // K/V/scale loads carry the non-temporal cache policy (aux bit 1, "nt" on gfx94x/gfx950): every
 // byte is read once, and streaming it past the caches raised read bandwidth from ~6.0 to
 // ~7.0 TB/s in isolation.
@@ -51,11 +50,9 @@ typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 #define IE_DECODE_LOAD_AUX 2
 #endif
 
-constexpr int DA_WAVES = IE_DECODE_WG_WAVES;
-constexpr int DA_THREADS = DA_WAVES * IE_WAVE;
-constexpr int DA_U = 4;                            // tokens per lane group per block
-constexpr int DA_TOK_WAVE = 8 * DA_U;              // 32 tokens per wave block
-constexpr int DA_TOK_WG = DA_WAVES * DA_TOK_WAVE;  // tokens per workgroup step
+constexpr int DA_WAVES_PER_CU = 16;
+constexpr int DA_U = 4;                // tokens per lane group per block
+constexpr int DA_TOK_WAVE = 8 * DA_U;  // 32 tokens per wave block
 constexpr int DA_MIN_PIECE = 128;
 constexpr int DA_MAX_SPLITS = 1024;  // per-KV-head workgroup target, at most
 constexpr int DA_D = 128;
@@ -63,8 +60,17 @@ constexpr uint32_t K64 = 0x64646464u;
 constexpr float OFFSET = 1152.0f;  // fp16(0x64xx) = 1024 + byte, byte = x + 128
 
 
-int decode_target(int num_kv_heads) {
-    return std::max(1, device_cu_count() * IE_DECODE_WG_PER_CU / std::max(1, num_kv_heads));
+// Per-KV-head workgroup target of workgroups of `waves` waves: one resident round.
+int decode_target(int num_kv_heads, int waves) {
+    return std::min(DA_MAX_SPLITS, std::max(1, device_cu_count() * (DA_WAVES_PER_CU / waves) /
+                                                   std::max(1, num_kv_heads)));
+}
+// Waves per workgroup for a batch: the largest workgroup whose target holds the batch, else
+// the smallest.
+int decode_waves(int batch, int num_kv_heads) {
+    for (int w = 8; w > 2; w /= 2)
+        if (batch <= decode_target(num_kv_heads, w)) return w;
+    return 2;
 }
 
 
@@ -305,9 +311,12 @@ __device__ __forceinline__ void block_pv(LaneState& st, const float (&t)[DA_U][2
 #define IE_DECODE_WAVES_PER_EU 4
 #endif
 
-__global__ __launch_bounds__(DA_THREADS)
+template <int WAVES>
+__global__ __launch_bounds__(WAVES * IE_WAVE)
 __attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_attention_kernel(
     DecodeArgs a) {
+    constexpr int THREADS = WAVES * IE_WAVE;
+    constexpr int TOK_WG = WAVES * DA_TOK_WAVE;  // tokens per workgroup step
     const int lane0 = threadIdx.x & 63;
     const int raw0 = lane0 < a.batch ? a.cached_lens[lane0] : 0;  // issued beside num_decoding
     const int nd = a.num_decoding[0];
@@ -391,20 +400,20 @@ __attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_attenti
     // outside the buffer range and return zeros without touching memory.
     // this wave's blocks: w, w + 8, ... of the piece's 32-token blocks, counted up front
     const int nb = (t_end - t_begin + DA_TOK_WAVE - 1) / DA_TOK_WAVE;
-    const int cw = wave < nb ? (nb - wave + DA_WAVES - 1) / DA_WAVES : 0;
+    const int cw = wave < nb ? (nb - wave + WAVES - 1) / WAVES : 0;
     int nfull = cw;
-    if (cw > 0 && t_begin + DA_TOK_WAVE * (wave + DA_WAVES * (cw - 1)) + DA_TOK_WAVE > t_end)
+    if (cw > 0 && t_begin + DA_TOK_WAVE * (wave + WAVES * (cw - 1)) + DA_TOK_WAVE > t_end)
         --nfull;  // the piece's last, partial block
     int t0 = t_begin + wave * DA_TOK_WAVE;
     KVRegs kr, vr;
     load_block(kr, rk, rks, t0 + 4 * g, cc);
     load_block(vr, rv, rvs, t0 + 4 * g, cc);
     float s[DA_U][2];
-    for (int j = 0; j < nfull; ++j, t0 += DA_TOK_WG) {
+    for (int j = 0; j < nfull; ++j, t0 += TOK_WG) {
         block_scores<false>(s, kr, qh, qoff, t0 + 4 * g, t_end);
-        load_block(kr, rk, rks, t0 + DA_TOK_WG + 4 * g, cc);
+        load_block(kr, rk, rks, t0 + TOK_WG + 4 * g, cc);
         block_pv(st, s, vr, kmul);
-        load_block(vr, rv, rvs, t0 + DA_TOK_WG + 4 * g, cc);
+        load_block(vr, rv, rvs, t0 + TOK_WG + 4 * g, cc);
     }
     if (nfull < cw) {
         block_scores<true>(s, kr, qh, qoff, t0 + 4 * g, t_end);
@@ -442,9 +451,9 @@ __attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_attenti
         }
     }
 
-    // ---- merge the 8 waves through LDS ----
-    __shared__ float s_acc[DA_WAVES][2][DA_D];
-    __shared__ float s_m[DA_WAVES][2], s_l[DA_WAVES][2];
+    // ---- merge the waves through LDS ----
+    __shared__ float s_acc[WAVES][2][DA_D];
+    __shared__ float s_m[WAVES][2], s_l[WAVES][2];
     // the lane's channel group, derived afresh from the thread index: keeping the prologue's copy
     // alive across the loop costs a register the loop needs
     int tid = threadIdx.x;
@@ -462,65 +471,87 @@ __attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_attenti
         }
     }
     __syncthreads();
-    // one thread per (query head, channel) from here on; the others stay for the barriers
-    const bool active = threadIdx.x < 2 * DA_D;
-    const int h = (threadIdx.x >> 7) & 1, d = threadIdx.x & 127;
-    float mx = -INFINITY;
+    // one (query head, channel) output per thread, or two with 2-wave workgroups; threads past
+    // the 256 outputs stay for the barriers
+    constexpr int PER = (2 * DA_D + THREADS - 1) / THREADS;
+    float num[PER], den[PER], mxo[PER];
 #pragma unroll
-    for (int w = 0; w < DA_WAVES; ++w) mx = fmaxf(mx, s_m[w][h]);
-    float num = 0.0f, den = 0.0f;
+    for (int u = 0; u < PER; ++u) {
+        const int idx = threadIdx.x + u * THREADS;
+        const int h = (idx >> 7) & 1, d = idx & 127;
+        float mx = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < DA_WAVES; ++w) {
-        const float mwv = s_m[w][h];
-        const float f = mwv == -INFINITY ? 0.0f : exp2_safe(mwv - mx);
-        num += s_acc[w][h][d] * f;
-        den += s_l[w][h] * f;
+        for (int w = 0; w < WAVES; ++w) mx = fmaxf(mx, s_m[w][h]);
+        num[u] = 0.0f;
+        den[u] = 0.0f;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) {
+            const float mwv = s_m[w][h];
+            const float f = mwv == -INFINITY ? 0.0f : exp2_safe(mwv - mx);
+            num[u] += s_acc[w][h][d] * f;
+            den[u] += s_l[w][h] * f;
+        }
+        mxo[u] = mx;
     }
-    const int qh_idx = 2 * hk + h;
-    uint16_t* const o = a.out + b * a.o_sb + qh_idx * a.o_sh + d;
+    auto out_of = [&](int u) {
+        const int idx = threadIdx.x + u * THREADS;
+        return a.out + b * a.o_sb + (2 * hk + ((idx >> 7) & 1)) * a.o_sh + (idx & 127);
+    };
+    auto active = [&](int u) { return threadIdx.x + u * THREADS < 2 * DA_D; };
     if (wk.needed == 1) {
-        if (active) *o = (uint16_t)f32_to_bf16_rne(num / den);
+#pragma unroll
+        for (int u = 0; u < PER; ++u)
+            if (active(u)) *out_of(u) = (uint16_t)f32_to_bf16_rne(num[u] / den[u]);
         return;
     }
     // A sequence of several pieces: each piece publishes its partial (the sequence's pieces
     // are consecutive work entries) and counts itself in; the piece that arrives last merges
     // them all (kernels.py:216-264, in base 2, pieces in order) and resets the count for the
     // next call. The partials are written and read with device-coherent accesses.
-    if (active) {
-        const int64_t row = (int64_t)qh_idx * a.nwork + item;
-        st_dev(a.part_acc + row * DA_D + d, num);
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+        if (!active(u)) continue;
+        const int idx = threadIdx.x + u * THREADS;
+        const int d = idx & 127;
+        const int64_t row = (int64_t)(2 * hk + ((idx >> 7) & 1)) * a.nwork + item;
+        st_dev(a.part_acc + row * DA_D + d, num[u]);
         if (d == 0) {
-            st_dev(a.part_m + row, mx);
-            st_dev(a.part_l + row, den);
+            st_dev(a.part_m + row, mxo[u]);
+            st_dev(a.part_l + row, den[u]);
         }
     }
-    if (!arrive_last(a.arrivals + b * a.hkv + hk, wk.needed) || !active) return;
+    if (!arrive_last(a.arrivals + b * a.hkv + hk, wk.needed)) return;
     const int needed = wk.needed;
-    const int64_t row0 = (int64_t)qh_idx * a.nwork + (item - split);
-    float pm = -INFINITY;
-    for (int sp = 0; sp < needed; ++sp) pm = fmaxf(pm, ld_dev(a.part_m + row0 + sp));
-    constexpr int CB = 8;  // partial outputs per load batch
-    num = 0.0f;
-    den = 0.0f;
-    for (int s0 = 0; s0 < needed; s0 += CB) {
-        float av[CB], ml[CB][2];
 #pragma unroll
-        for (int u = 0; u < CB; ++u) {
-            const bool in = s0 + u < needed;
-            av[u] = in ? ld_dev(a.part_acc + (row0 + s0 + u) * DA_D + d) : 0.0f;
-            ml[u][0] = in ? ld_dev(a.part_m + row0 + s0 + u) : -INFINITY;
-            ml[u][1] = in ? ld_dev(a.part_l + row0 + s0 + u) : 0.0f;
-        }
+    for (int u = 0; u < PER; ++u) {
+        if (!active(u)) continue;
+        const int idx = threadIdx.x + u * THREADS;
+        const int d = idx & 127;
+        const int64_t row0 = (int64_t)(2 * hk + ((idx >> 7) & 1)) * a.nwork + (item - split);
+        float pm = -INFINITY;
+        for (int sp = 0; sp < needed; ++sp) pm = fmaxf(pm, ld_dev(a.part_m + row0 + sp));
+        constexpr int CB = 8;  // partial outputs per load batch
+        float nm = 0.0f, dn = 0.0f;
+        for (int s0 = 0; s0 < needed; s0 += CB) {
+            float av[CB], ml[CB][2];
 #pragma unroll
-        for (int u = 0; u < CB; ++u) {
-            if (s0 + u < needed) {
-                const float f = ml[u][0] == -INFINITY ? 0.0f : exp2_safe(ml[u][0] - pm);
-                num += av[u] * f;
-                den += ml[u][1] * f;
+            for (int v = 0; v < CB; ++v) {
+                const bool in = s0 + v < needed;
+                av[v] = in ? ld_dev(a.part_acc + (row0 + s0 + v) * DA_D + d) : 0.0f;
+                ml[v][0] = in ? ld_dev(a.part_m + row0 + s0 + v) : -INFINITY;
+                ml[v][1] = in ? ld_dev(a.part_l + row0 + s0 + v) : 0.0f;
+            }
+#pragma unroll
+            for (int v = 0; v < CB; ++v) {
+                if (s0 + v < needed) {
+                    const float f = ml[v][0] == -INFINITY ? 0.0f : exp2_safe(ml[v][0] - pm);
+                    nm += av[v] * f;
+                    dn += ml[v][1] * f;
+                }
             }
         }
+        *out_of(u) = (uint16_t)f32_to_bf16_rne(nm / dn);
     }
-    *o = (uint16_t)f32_to_bf16_rne(num / den);
 }
 
 // grid (work entries), block 64: the decode kernel's work list, one entry per workgroup index w
@@ -551,14 +582,15 @@ __global__ __launch_bounds__(64) void decode_plan_kernel(const int32_t* __restri
 // serves them all. A larger batch gets a count region of its own size.
 constexpr int DA_COUNT_CAP = 1024;
 struct Layout {
-    int target, nwork;
+    int waves, target, nwork;
     size_t arr_off, acc_off, m_off, l_off, bytes;
 };
 
 static Layout workspace_layout(int batch, int hq, int hkv) {
     Layout L;
     batch = std::max(batch, 0);
-    L.target = std::min(decode_target(hkv), DA_MAX_SPLITS);
+    L.waves = decode_waves(batch, hkv);
+    L.target = decode_target(hkv, L.waves);
     L.nwork = batch <= L.target ? L.target : L.target + batch;
     const size_t rows = (size_t)hq * L.nwork;
     L.arr_off = 0;
@@ -574,7 +606,12 @@ static Layout workspace_layout(int batch, int hq, int hkv) {
 using namespace ie;
 
 extern "C" int32_t ie_decode_attention_max_splits(int32_t num_kv_heads) {
-    return std::min(decode_target(num_kv_heads), DA_MAX_SPLITS);
+    return decode_target(num_kv_heads, 2);  // the largest target of any launch shape
+}
+
+extern "C" int32_t ie_decode_attention_target(int32_t batch, int32_t num_kv_heads) {
+    if (batch <= 0 || num_kv_heads <= 0) return 0;
+    return decode_target(num_kv_heads, decode_waves(batch, num_kv_heads));
 }
 
 extern "C" size_t ie_decode_attention_workspace_size(int32_t batch, int32_t num_q_heads,
@@ -647,13 +684,17 @@ extern "C" hipError_t ie_decode_attention(
                   pieces <= 65535;  // the grid's y dimension holds at most 65535
     const dim3 grid = a.head_fast ? dim3((unsigned)cache->num_kv_heads, pieces)
                                   : dim3(pieces, (unsigned)cache->num_kv_heads);
-    hipLaunchKernelGGL(decode_attention_kernel, grid, dim3(DA_THREADS), 0, stream, a);
+    switch (L.waves) {
+        case 8: hipLaunchKernelGGL(decode_attention_kernel<8>, grid, dim3(512), 0, stream, a); break;
+        case 4: hipLaunchKernelGGL(decode_attention_kernel<4>, grid, dim3(256), 0, stream, a); break;
+        default: hipLaunchKernelGGL(decode_attention_kernel<2>, grid, dim3(128), 0, stream, a); break;
+    }
     return hipGetLastError();
 }
 
 extern "C" int32_t ie_decode_attention_grid(int32_t batch, int32_t num_kv_heads) {
     if (batch <= 0 || num_kv_heads <= 0) return 0;
-    const int target = std::min(decode_target(num_kv_heads), DA_MAX_SPLITS);
+    const int target = ie_decode_attention_target(batch, num_kv_heads);
     return batch <= target ? target : target + batch;
 }
 
@@ -664,7 +705,7 @@ extern "C" hipError_t ie_decode_attention_plan(const int32_t* cached_lens,
     IE_REQUIRE(batch >= 0 && num_kv_heads > 0, "bad sizes");
     if (batch == 0) return hipSuccess;
     IE_REQUIRE(cached_lens && num_decoding && rows, "null pointer");
-    const int target = std::min(decode_target(num_kv_heads), DA_MAX_SPLITS);
+    const int target = ie_decode_attention_target(batch, num_kv_heads);
     hipLaunchKernelGGL(decode_plan_kernel, dim3((unsigned)ie_decode_attention_grid(batch, num_kv_heads)),
                        dim3(IE_WAVE), 0, stream, cached_lens, num_decoding, batch, target, rows);
     return hipGetLastError();

@@ -59,10 +59,16 @@ def test_workspace_size_formula(native):
     fp32 partial (128 outputs, m, l) per query head and work entry; the work entries are the
     launch's grid: the target, or target + B above it."""
     lib = native.cabi()
-    target = lib.ie_decode_attention_max_splits(8)
-    assert target >= 1
+    t_max = lib.ie_decode_attention_max_splits(8)
+    assert t_max >= 1
     lib.ie_decode_attention_grid.restype = ctypes.c_int32
-    for B in (1, 64, target, target + 1, 300, 1024):
+    prev = 0
+    for B in (1, 64, 65, 96, 128, 129, 256, 257, 300, 1024):
+        # the target grows with the batch (8-, 4- then 2-wave workgroups) and holds it while
+        # any launch shape can
+        target = lib.ie_decode_attention_target(ctypes.c_int32(B), ctypes.c_int32(8))
+        assert prev <= target <= t_max and (B <= target or target == t_max)
+        prev = target
         grid = lib.ie_decode_attention_grid(ctypes.c_int32(B), ctypes.c_int32(8))
         assert grid == (target if B <= target else target + B)
         plan = -(-(max(B, 1024) * 8) * 4 // 256) * 256

@@ -107,22 +107,23 @@ def sampled_check(ie, workloads, dev, ctx, pick, seed, what, **kw):
 @pytest.mark.parametrize("B,ctx", [(64, 4096), (16, 4096), (256, 1024), (256, 4096)])
 def test_decode_config3_sampled(ie, workloads, dev, B, ctx):
     """BASELINE config 3 points at full size, generated on the GPU (B=64 ctx=4096 is the
-    headline; B=256 runs the grid of TARGET + B workgroups, where pieces are not fitted):
-    8 sampled sequences checked against the oracle."""
+    headline, 8-wave workgroups; B=256 runs 2-wave workgroups, whose per-head target of 256
+    holds the batch): 8 sampled sequences checked against the oracle."""
     say(f"decode config 3 B={B} ctx={ctx} (sampled)")
     pick = sorted({0, 1, B // 4, B // 2 - 1, B // 2, 3 * B // 4, B - 2, B - 1})
     sampled_check(ie, workloads, dev, [ctx] * B, pick, seed=B + ctx, what=f"config3 {B}x{ctx}")
 
 
 @pytest.mark.parametrize("B,nd,lo,hi,seed", [
-    (200, 170, 1, 3000, 31),  # more sequences than the per-head workgroup target
-    (300, 299, 1, 600, 32),   # one-split sequences filling the TARGET + B grid
-    (65, 65, 2000, 9000, 33),  # one past the target, several splits per sequence
+    (200, 170, 1, 3000, 31),  # 2-wave workgroups (target 256 on 256 CUs), fitted pieces
+    (300, 299, 1, 600, 32),   # above every target: the reference's TARGET + B grid
+    (65, 65, 2000, 9000, 33),  # one past the 8-wave target: 4-wave workgroups, several splits
 ])
 def test_decode_ragged_large_batch(ie, workloads, dev, B, nd, lo, hi, seed):
-    """Batches above the per-head workgroup target (64 on 256 CUs) with num_decoding < B:
-    the reference's unfitted piece rule and the TARGET + B grid (kernels.py:294-314), every
-    decoding row against the oracle and the rows past num_decoding untouched."""
+    """Batches above the 8-wave workgroups' per-head target (64 on 256 CUs) with
+    num_decoding < B: 4- and 2-wave workgroups with fitted pieces, and above every target the
+    reference's unfitted piece rule and TARGET + B grid (kernels.py:294-314); every decoding row
+    against the oracle and the rows past num_decoding untouched."""
     ctx = [int(x) for x in np.random.default_rng(seed).integers(lo, hi + 1, B)]
     say(f"decode ragged B={B} num_decoding={nd} ctx {min(ctx)}..{max(ctx)}")
     wl = workloads.decode_workload(ctx, seed=seed, num_decoding=nd)
@@ -137,8 +138,8 @@ def test_decode_ragged_large_batch(ie, workloads, dev, B, nd, lo, hi, seed):
 
 
 def test_decode_long_and_short_mix_above_target(ie, workloads, dev):
-    """96 sequences, 6 of them 30-60K tokens long: above the target the long ones split into
-    many pieces merged by the combine kernel."""
+    """96 sequences, 6 of them 30-60K tokens long (4-wave workgroups): the long ones split into
+    many pieces, merged by their last piece."""
     rng = np.random.default_rng(41)
     ctx = [int(x) for x in rng.integers(100, 500, 90)] + [int(x) for x in
                                                           rng.integers(30000, 60000, 6)]
@@ -177,15 +178,16 @@ def test_decode_v_magnitude_and_sink(ie, workloads, dev, v_mult, sink):
     ([int(x) for x in np.random.default_rng(3).integers(1, 5000, 64)], 64),
     ([int(x) for x in np.random.default_rng(4).integers(1, 5000, 200)], 170),
     ([1024] * 256, 256), ([200] * 90 + [50000] * 6, 96), ([33000], 1), ([5, 6], 0),
+    ([int(x) for x in np.random.default_rng(5).integers(1, 600, 300)], 299),
 ])
 def test_decode_plan_matches_oracle(ie, native, dev, ctx, nd):
-    """The split launch's work list, as the device computes it (ie_decode_attention_plan runs
-    the split kernel's own assignment code), equals oracle/work_split.decode_work_plan entry
+    """The decode launch's work list, as the device computes it (ie_decode_attention_plan runs
+    the decode kernel's own assignment code), equals oracle/work_split.decode_work_plan entry
     for entry, and no piece of the oracle's list falls outside the launch's grid."""
     lib = native.cabi()
     B = len(ctx)
     hkv = 8
-    target = lib.ie_decode_attention_max_splits(hkv)
+    target = lib.ie_decode_attention_target(ctypes.c_int32(B), ctypes.c_int32(hkv))
     grid = lib.ie_decode_attention_grid(ctypes.c_int32(B), ctypes.c_int32(hkv))
     assert grid == (target if B <= target else target + B)
     cl = torch.tensor([c - 1 for c in ctx], dtype=torch.int32, device=dev)
