@@ -373,6 +373,32 @@ def line_read_probe(args, ie, W, K, dev, alg_bytes, extra):
                            "torch_sum_GBps": round(alg_bytes / (ts_ms * 1e-3) / 1e9, 1)}
     log(f"read probe {rp_ms*1e3:.2f} us, torch.sum {ts_ms*1e3:.2f} us")
 
+    # Config 5's decode launch beside the same stream over its bytes: B=32, ctx ~ U[128, 4096)
+    # as decode_step draws it; the stream reads four regions in turn (past the 256 MB cache)
+    g = torch.Generator().manual_seed(0)
+    c5 = torch.randint(128, 4096, (32,), generator=g).tolist()
+    c5_wls = [W.decode_workload(c5, seed=s, device=dev) for s in range(2)]
+    c5_bytes = c5_wls[0].algorithmic_bytes() // 16 * 16
+    assert 2 * c5_bytes <= alg_bytes
+    regions = [(t, off) for t in probes for off in (0, alg_bytes // 2 // 16 * 16)]
+
+    def read_probe_c5():
+        t, off = regions[turn[0] % 4]
+        turn[0] += 1
+        rc = lib.ie_hbm_read_probe(ctypes.c_void_p(t.data_ptr() + off), ctypes.c_size_t(c5_bytes),
+                                   ctypes.c_uint32(0x9E3779B9), ctypes.c_void_p(sink.data_ptr()),
+                                   stream)
+        assert rc == 0, lib.ie_attn_last_error()
+    rp5_ms = time_op(read_probe_c5, args.steps, args.warmup)
+    dec5_ms = time_decode(ie, c5_wls, args.steps, args.warmup)
+    extra["read_probe"]["config5"] = {
+        "bytes": c5_bytes, "stream_us": round(rp5_ms * 1e3, 2),
+        "decode_us": round(dec5_ms * 1e3, 2),
+        "decode_GBps": round(c5_bytes / (dec5_ms * 1e-3) / 1e9, 1),
+        "decode_over_stream": round(rp5_ms / dec5_ms, 3)}
+    log(f"config 5 bytes {c5_bytes / 1e6:.1f} MB: read probe {rp5_ms*1e3:.2f} us, "
+        f"decode {dec5_ms*1e3:.2f} us")
+
 
 def line_kv_write(args, ie, W, K, dev, alg_bytes, extra):
     """Config 4's KV quantize-on-write (1,024 new tokens), and a long step: a first chunk of 8192
@@ -512,6 +538,89 @@ def extras(args, ie, W, K, dev, alg_bytes) -> dict:
     return extra
 
 
+def prefill_phase_stamps(W, dev, warmup):
+    """Config 4's prefill attention through the C ABI of the phase-stamp build
+    (inference-engine_amd/lib/stamps/libie_attn.so: the same kernel with a 100 MHz clock read
+    by thread 0 of every workgroup at each phase boundary). Per call: the time from the first
+    workgroup's start to each workgroup's phase boundaries; medians over five calls after
+    `warmup` calls that bring the clocks up."""
+    import ctypes
+    import numpy as np
+    path = REPO / "inference-engine_amd" / "lib" / "stamps" / "libie_attn.so"
+    if not path.exists():
+        raise SystemExit(f"{path} is missing: run python inference-engine_amd/build.py --stamps")
+    lib = ctypes.CDLL(str(path))
+    lib.ie_prefill_attention_workspace_size.restype = ctypes.c_size_t
+    lib.ie_attn_last_error.restype = ctypes.c_char_p
+    NT = importlib.import_module("inference-engine_amd._native")
+    mw = W.mixed_to(W.config4(seed=0), dev)
+    gi = mw.inputs
+    N, nt = mw.q.shape[0], gi["tile_start"].shape[0]
+    p = lambda t: ctypes.c_void_p(t.data_ptr())
+    desc = NT.KVCacheDesc.of(mw.cache)
+    wsb = lib.ie_prefill_attention_workspace_size(nt, mw.block_m, 8)
+    ws = torch.zeros(int(wsb), dtype=torch.uint8, device=dev)
+    out = torch.empty_like(mw.q)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def run():
+        i64, i32 = ctypes.c_int64, ctypes.c_int32
+        rc = lib.ie_prefill_attention(
+            p(mw.q), i64(mw.q.stride(0)), i64(mw.q.stride(1)), p(mw.k), i64(mw.k.stride(0)),
+            i64(mw.k.stride(1)), p(mw.v), i64(mw.v.stride(0)), i64(mw.v.stride(1)), i64(N),
+            i32(16), p(gi["seq_ids"]), p(gi["cu_seqlens"]), p(gi["tile_start"]), i32(nt),
+            i32(mw.block_m), ctypes.byref(desc), p(gi["slot_ids"]), p(gi["cu_cached"]),
+            i32(gi["slot_ids"].shape[0]), p(out), i64(out.stride(0)), i64(out.stride(1)), p(ws),
+            ctypes.c_size_t(wsb), stream)
+        assert rc == 0, lib.ie_attn_last_error()
+
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize()
+    nwg, words = 4096, 9
+    buf = (ctypes.c_ulonglong * (nwg * words))()
+    assert lib.ie_prefill_phase_stamps_copy(buf, ctypes.c_size_t(nwg * words), 1) == 0
+    calls = []
+    for _ in range(5):
+        for _ in range(20):  # the clocks stay up; these calls' stamps are cleared below
+            run()
+        torch.cuda.synchronize()
+        assert lib.ie_prefill_phase_stamps_copy(buf, ctypes.c_size_t(nwg * words), 1) == 0
+        run()
+        torch.cuda.synchronize()
+        assert lib.ie_prefill_phase_stamps_copy(buf, ctypes.c_size_t(nwg * words), 1) == 0
+        t = np.array(buf, dtype=np.int64).reshape(nwg, words)
+        t = t[t[:, 0] > 0]
+        calls.append(t)
+    names = ["start", "work_list", "first_scores", "tiles_done", "partial_written",
+             "wait_over", "share_merged", "end"]
+    res = {}
+    for i, nm in enumerate(names):
+        vals = []
+        for t in calls:
+            base = t[:, 0].min()
+            col = t[:, i]
+            vals.append((col[col > 0] - base) * 0.01)  # us
+        v = np.concatenate(vals)
+        if len(v):
+            res[nm] = {"p50_us": round(float(np.median(v)), 2),
+                       "p90_us": round(float(np.percentile(v, 90)), 2),
+                       "max_us": round(float(v.max()), 2), "workgroups": int(len(v) // 5)}
+    steps = {}
+    for a, b in ((0, 1), (1, 2), (2, 3), (3, 4), (4, 5), (5, 6), (6, 7), (3, 7)):
+        d = np.concatenate([(t[:, b] - t[:, a])[(t[:, a] > 0) & (t[:, b] > 0)] * 0.01
+                            for t in calls])
+        if len(d):
+            steps[f"{names[a]}->{names[b]}"] = {"p50_us": round(float(np.median(d)), 2),
+                                                "p90_us": round(float(np.percentile(d, 90)), 2)}
+    pieces = calls[0][:, 8]
+    return {"workload": "prefill_attention config 4 (phase-stamp build)",
+            "call_us_last_end": round(float(np.median([(t[:, 7].max() - t[:, 0].min()) * 0.01
+                                                       for t in calls])), 2),
+            "workgroups_with_work": int((pieces > 0).sum()),
+            "split_pieces": int((pieces > 1).sum()), "phases": res, "steps": steps}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -538,6 +647,10 @@ def main():
                          "every decode launch of the run is then a headline launch)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run a plain device copy of MIB MiB 3 times (PMC calibration)")
+    ap.add_argument("--prefill-stamps", action="store_true",
+                    help="instead of the bench line: config 4's prefill attention on the "
+                         "phase-stamp build (python inference-engine_amd/build.py --stamps), "
+                         "per-phase medians of its workgroups as one JSON line")
     args = ap.parse_args()
     args.lines = [x for x in args.lines.split(",") if x]
     bad = [x for x in args.lines if x not in LINES]
@@ -559,6 +672,10 @@ def main():
     K = ie.kernels
     dev = "cuda:0"
     torch.cuda.set_device(0)
+
+    if args.prefill_stamps:
+        print(json.dumps(prefill_phase_stamps(W, dev, args.warmup)), flush=True)
+        return
 
     if args.copy_probe:
         n = args.copy_probe << 20

@@ -109,5 +109,12 @@ def clean() -> None:
 
 
 if __name__ == "__main__":
-    build(verbose="-v" in sys.argv)
-    print("built", LIB / "libie_attn.so", LIB / "_ie_torch_ops.so")
+    if "--stamps" in sys.argv:
+        # the prefill kernel with its phase stamps compiled in (bench.py --prefill-stamps)
+        out = build_hip(["-DIE_PREFILL_PHASE_STAMPS"], verbose="-v" in sys.argv,
+                        out_dir=LIB / "stamps")
+        shutil.rmtree(LIB / "stamps" / "_obj", ignore_errors=True)
+        print("built", out)
+    else:
+        build(verbose="-v" in sys.argv)
+        print("built", LIB / "libie_attn.so", LIB / "_ie_torch_ops.so")

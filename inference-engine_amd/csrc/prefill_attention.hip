@@ -40,6 +40,30 @@
 
 namespace ie {
 
+// Phase stamps (diagnostic build only, -DIE_PREFILL_PHASE_STAMPS; the product build compiles
+// them out): thread 0 of workgroup w < PF_STAMP_WGS records the 100 MHz real-time clock at
+//   0 start, 1 work list known, 2 first tile's scores done, 3 last tile done,
+//   4 split piece: partial written and counted in, 5 wait for the pair's pieces over,
+//   6 share merged, 7 end
+// and in slot 8 its piece count (0: no work). Read with ie_prefill_phase_stamps_copy.
+#ifdef IE_PREFILL_PHASE_STAMPS
+constexpr int PF_STAMP_WGS = 4096;
+__device__ unsigned long long pf_phase_stamps[PF_STAMP_WGS * 9];
+#define PF_STAMP(i)                                                                            \
+    do {                                                                                       \
+        if (threadIdx.x == 0 && blockIdx.x < PF_STAMP_WGS)                                     \
+            pf_phase_stamps[blockIdx.x * 9 + (i)] = __builtin_amdgcn_s_memrealtime();          \
+    } while (0)
+#define PF_STAMP_VALUE(i, v)                                                                   \
+    do {                                                                                       \
+        if (threadIdx.x == 0 && blockIdx.x < PF_STAMP_WGS)                                     \
+            pf_phase_stamps[blockIdx.x * 9 + (i)] = (unsigned long long)(v);                   \
+    } while (0)
+#else
+#define PF_STAMP(i) do { } while (0)
+#define PF_STAMP_VALUE(i, v) do { } while (0)
+#endif
+
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -858,6 +882,7 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBloc
         f32x4 sc[4][2];
         tile_scores(sc, qf, s_k[0], l16, g);
         __syncthreads();  // every wave has read K_0 before step 0 stages K_2 over it
+        PF_STAMP(2);
         uint32_t pfrag[2][2][4];
         int slot = 0;  // K-scale slot of tile j
         for (int j = 0; j < n - 1; ++j) {
@@ -931,6 +956,7 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBloc
         f32x4 sc[4][2];
         tile_scores(sc, qf, s_k[0], l16, g);
         __syncthreads();  // every wave has read K_0 before step 0 stages K_2 over it
+        if (item_start) PF_STAMP(2);
         uint32_t pfrag[2][2][4];
         for (int j = 0; j < n - 1; ++j) {
             const int kc = kb0 + j * PF_BN;
@@ -972,6 +998,7 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBloc
         }
         tile_pv(ws, pfrag, s_vt[(n - 1) & 1], l16, g);
     }
+    PF_STAMP(3);
     // ---- results: lane holds row = wr0 + 16nt + l16, channels d = 16mt + 4g + i ----
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
@@ -1003,8 +1030,12 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBloc
                              ((uint64_t)__float_as_uint(l) << 32));
         }
     }
-    if (s.npieces == 1) return;
+    if (s.npieces == 1) {
+        PF_STAMP(7);
+        return;
+    }
     merge_pieces(a, s, hk, item_base);
+    PF_STAMP(7);
 }
 
 // Merge of a split (sub-block, kv head) pair, in the launch that computed its pieces. Piece p ran
@@ -1033,6 +1064,7 @@ __device__ __forceinline__ void merge_pieces(const PrefillArgs& a, const SubBloc
     if (threadIdx.x == 0) {
         const int k = (int)__hip_atomic_fetch_add(arr, 1u, __ATOMIC_RELAXED,
                                                   __HIP_MEMORY_SCOPE_AGENT);
+        PF_STAMP(4);
         int go = k == np - 1;
         if (!go) {
             const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
@@ -1047,6 +1079,7 @@ __device__ __forceinline__ void merge_pieces(const PrefillArgs& a, const SubBloc
         }
         s_k = k;
         s_go = go;
+        PF_STAMP(5);
     }
     __syncthreads();
     const int k = s_k;
@@ -1126,6 +1159,7 @@ __device__ __forceinline__ void merge_pieces(const PrefillArgs& a, const SubBloc
         }
     };
     if (go) merge_share(k);
+    PF_STAMP(6);
     if (threadIdx.x == 0) {
         const uint32_t mine = (1u << 16) | (go ? 1u << k : 0u);
         const uint32_t old =
@@ -1155,12 +1189,15 @@ __global__ __launch_bounds__(PF_THREADS, IE_PREFILL_WG_PER_CU) void prefill_atte
     PrefillArgs a) {
     // every wave reads the tile metadata and derives the workgroup's item itself
     __shared__ __attribute__((aligned(16))) PfLds lds;
+    PF_STAMP(0);
     Loc loc = schedule(a, blockIdx.x, reinterpret_cast<int*>(lds.k[1]));
     {
         int* f = reinterpret_cast<int*>(&loc);
 #pragma unroll
         for (int i = 0; i < (int)(sizeof(Loc) / sizeof(int)); ++i) f[i] = uni(f[i]);
     }
+    PF_STAMP(1);
+    PF_STAMP_VALUE(8, loc.found ? loc.s.npieces : 0);
     if (!loc.found) return;
     prefill_item(a, loc.s, loc.off % a.hkv, loc.off / a.hkv, blockIdx.x, loc.item_base, lds);
 }
@@ -1278,3 +1315,17 @@ extern "C" hipError_t ie_prefill_attention(
     hipLaunchKernelGGL(prefill_attention_kernel, dim3(grid), dim3(PF_THREADS), 0, stream, a);
     return hipGetLastError();
 }
+
+#ifdef IE_PREFILL_PHASE_STAMPS
+// Diagnostic build only: copies the first `count` words of the phase-stamp array to host memory
+// (clear: then zeroes the array).
+extern "C" hipError_t ie_prefill_phase_stamps_copy(unsigned long long* host, size_t count,
+                                                   int clear) {
+    IE_REQUIRE(count <= (size_t)PF_STAMP_WGS * 9, "count beyond the stamp array");
+    hipError_t e = hipMemcpyFromSymbol(host, HIP_SYMBOL(ie::pf_phase_stamps),
+                                       count * sizeof(unsigned long long));
+    if (e != hipSuccess || !clear) return e;
+    static unsigned long long zeros[PF_STAMP_WGS * 9];
+    return hipMemcpyToSymbol(HIP_SYMBOL(ie::pf_phase_stamps), zeros, sizeof(zeros));
+}
+#endif
