@@ -114,7 +114,7 @@ def time_graph(fn, calls=20, reps=5):
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
+    with torch.cuda.graph(g, stream=s):  # the warmed-up stream: its workspaces exist
         for _ in range(calls):
             fn()
     g.replay()
@@ -187,7 +187,7 @@ def time_graph_calls(fns, reps=3):
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
+    with torch.cuda.graph(g, stream=s):
         for f in fns:
             f()
     g.replay()

@@ -119,16 +119,20 @@ class GraphSet:
     def __init__(self):
         self.pool = torch.cuda.graph_pool_handle()
         self.graphs: dict = {}
+        # one side stream for every warm-up and capture: the ops' per-stream workspaces (zeroed
+        # arrival counts) are then allocated by the first warm-up, outside any capture, and the
+        # graphs share them as they share the pool (one replays at a time)
+        self.stream = torch.cuda.Stream()
 
     def capture(self, key, run: Callable[[], torch.Tensor]):
-        s = torch.cuda.Stream()
+        s = self.stream
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
             for _ in range(2):
                 run()
         torch.cuda.current_stream().wait_stream(s)
         graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, pool=self.pool):
+        with torch.cuda.graph(graph, pool=self.pool, stream=s):
             out = run()
         self.graphs[key] = (graph, out)
         return graph, out

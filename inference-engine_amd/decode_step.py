@@ -189,7 +189,7 @@ class DecodeStep:
                 fn()
         torch.cuda.current_stream().wait_stream(s)
         graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
+        with torch.cuda.graph(graph, stream=s):  # the warmed-up stream: its workspaces exist
             out = fn()
         return graph, out
 

@@ -280,7 +280,7 @@ def _graph_time(fns: list) -> float:
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
+    with torch.cuda.graph(g, stream=s):
         for f in fns:
             f()
     g.replay()
