@@ -318,7 +318,10 @@ __attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_attenti
     constexpr int THREADS = WAVES * IE_WAVE;
     constexpr int TOK_WG = WAVES * DA_TOK_WAVE;  // tokens per workgroup step
     const int lane0 = threadIdx.x & 63;
-    const int raw0 = lane0 < a.batch ? a.cached_lens[lane0] : 0;  // issued beside num_decoding
+    // The first 64 sequences' lengths and cache slots, issued beside num_decoding: for them the
+    // row to stream is known from registers once the work entry is found.
+    const int raw0 = lane0 < a.batch ? a.cached_lens[lane0] : 0;
+    const int slot0 = lane0 < a.batch ? a.slot_ids[lane0] : 0;
     const int nd = a.num_decoding[0];
     const int hk = a.head_fast ? blockIdx.x : blockIdx.y;
     const int item = a.head_fast ? blockIdx.y : blockIdx.x;
@@ -330,22 +333,45 @@ __attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_attenti
     const int b = uniform(wk.b);
     const int split = uniform(wk.split);
     const int piece = uniform(wk.piece);
-    const int n_end = uniform(a.cached_lens[b] + 1);
+    const int n_end =
+        b < 64 ? __builtin_amdgcn_readlane(raw0, b) + 1 : uniform(a.cached_lens[b] + 1);
     const int t_begin = split * piece;
     const int t_end = min(t_begin + piece, n_end);
-    const int slot = uniform(a.slot_ids[b]);
+    const int slot = b < 64 ? __builtin_amdgcn_readlane(slot0, b) : uniform(a.slot_ids[b]);
 
     const int lane = threadIdx.x & 63, wave = uniform(threadIdx.x >> 6);
     const int g = lane >> 3, cc = lane & 7;
 
+    // Buffer resources over this (slot, kv head) row, bounded at the piece's end.
+    const int8_t* krow = a.c.k + slot * a.c.stride_slot + hk * a.c.stride_head;
+    const int8_t* vrow = a.c.v + slot * a.c.stride_slot + hk * a.c.stride_head;
+    const float* ksrow = a.c.k_scale + slot * a.c.scale_stride_slot + hk * a.c.scale_stride_head;
+    const float* vsrow = a.c.v_scale + slot * a.c.scale_stride_slot + hk * a.c.scale_stride_head;
+    const rsrc_t rk = make_rsrc(krow, (uint32_t)t_end * DA_D);
+    const rsrc_t rv = make_rsrc(vrow, (uint32_t)t_end * DA_D);
+    const rsrc_t rks = make_rsrc(ksrow, (uint32_t)t_end * 4);
+    const rsrc_t rvs = make_rsrc(vsrow, (uint32_t)t_end * 4);
+
     // ---- q of the two heads of this KV head, channels [16cc, 16cc + 16) ----
     half2_t qh[2][8];
     float qoff[2], kmul[2];  // wave-uniform (kept in SGPRs)
+    uint4 qraw[2][2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         const uint16_t* qp = a.q + b * a.q_sb + (2 * hk + h) * a.q_sh + 16 * cc;
-        const uint4 u0 = *reinterpret_cast<const uint4*>(qp);
-        const uint4 u1 = *reinterpret_cast<const uint4*>(qp + 8);
+        qraw[h][0] = *reinterpret_cast<const uint4*>(qp);
+        qraw[h][1] = *reinterpret_cast<const uint4*>(qp + 8);
+    }
+    // The first K/V block is requested with q, in the same memory round trip; the scheduling
+    // barrier keeps the compiler from sinking the requests below q's conversion.
+    int t0 = t_begin + wave * DA_TOK_WAVE;
+    KVRegs kr, vr;
+    load_block(kr, rk, rks, t0 + 4 * g, cc);
+    load_block(vr, rv, rvs, t0 + 4 * g, cc);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const uint4 u0 = qraw[h][0], u1 = qraw[h][1];
         const uint32_t w[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
         float f[16];
         float amax = 0.0f;
@@ -372,16 +398,6 @@ __attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_attenti
         kmul[h] = __int_as_float(uniform(__float_as_int(a.scale_log2 / sc)));
     }
 
-    // Buffer resources over this (slot, kv head) row, bounded at the piece's end.
-    const int8_t* krow = a.c.k + slot * a.c.stride_slot + hk * a.c.stride_head;
-    const int8_t* vrow = a.c.v + slot * a.c.stride_slot + hk * a.c.stride_head;
-    const float* ksrow = a.c.k_scale + slot * a.c.scale_stride_slot + hk * a.c.scale_stride_head;
-    const float* vsrow = a.c.v_scale + slot * a.c.scale_stride_slot + hk * a.c.scale_stride_head;
-    const rsrc_t rk = make_rsrc(krow, (uint32_t)t_end * DA_D);
-    const rsrc_t rv = make_rsrc(vrow, (uint32_t)t_end * DA_D);
-    const rsrc_t rks = make_rsrc(ksrow, (uint32_t)t_end * 4);
-    const rsrc_t rvs = make_rsrc(vsrow, (uint32_t)t_end * 4);
-
     LaneState st;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -404,10 +420,6 @@ __attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_attenti
     int nfull = cw;
     if (cw > 0 && t_begin + DA_TOK_WAVE * (wave + WAVES * (cw - 1)) + DA_TOK_WAVE > t_end)
         --nfull;  // the piece's last, partial block
-    int t0 = t_begin + wave * DA_TOK_WAVE;
-    KVRegs kr, vr;
-    load_block(kr, rk, rks, t0 + 4 * g, cc);
-    load_block(vr, rv, rvs, t0 + 4 * g, cc);
     float s[DA_U][2];
     for (int j = 0; j < nfull; ++j, t0 += TOK_WG) {
         block_scores<false>(s, kr, qh, qoff, t0 + 4 * g, t_end);
@@ -528,12 +540,9 @@ __attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_attenti
         const int idx = threadIdx.x + u * THREADS;
         const int d = idx & 127;
         const int64_t row0 = (int64_t)(2 * hk + ((idx >> 7) & 1)) * a.nwork + (item - split);
-        float pm = -INFINITY;
-        for (int sp = 0; sp < needed; ++sp) pm = fmaxf(pm, ld_dev(a.part_m + row0 + sp));
-        constexpr int CB = 8;  // partial outputs per load batch
-        float nm = 0.0f, dn = 0.0f;
-        for (int s0 = 0; s0 < needed; s0 += CB) {
-            float av[CB], ml[CB][2];
+        constexpr int CB = 8;  // partials per load batch: one memory round trip each
+        float av[CB], ml[CB][2];
+        auto load_batch = [&](int s0) {
 #pragma unroll
             for (int v = 0; v < CB; ++v) {
                 const bool in = s0 + v < needed;
@@ -541,6 +550,24 @@ __attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_attenti
                 ml[v][0] = in ? ld_dev(a.part_m + row0 + s0 + v) : -INFINITY;
                 ml[v][1] = in ? ld_dev(a.part_l + row0 + s0 + v) : 0.0f;
             }
+        };
+        // the largest partial maximum; with at most CB pieces the batch loaded here is the
+        // only one the merge needs
+        load_batch(0);
+        float pm = -INFINITY;
+#pragma unroll
+        for (int v = 0; v < CB; ++v) pm = fmaxf(pm, ml[v][0]);
+        for (int s0 = CB; s0 < needed; s0 += CB) {
+            float mv[CB];
+#pragma unroll
+            for (int v = 0; v < CB; ++v)
+                mv[v] = s0 + v < needed ? ld_dev(a.part_m + row0 + s0 + v) : -INFINITY;
+#pragma unroll
+            for (int v = 0; v < CB; ++v) pm = fmaxf(pm, mv[v]);
+        }
+        float nm = 0.0f, dn = 0.0f;
+        for (int s0 = 0; s0 < needed; s0 += CB) {
+            if (s0 > 0) load_batch(s0);
 #pragma unroll
             for (int v = 0; v < CB; ++v) {
                 if (s0 + v < needed) {
