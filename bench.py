@@ -452,10 +452,13 @@ def line_prefill_config4(args, ie, W, K, dev, alg_bytes, extra):
 
 def line_prefill_long(args, ie, W, K, dev, alg_bytes, extra):
     """Long prefills, where the tile loop rather than the per-launch latency sets the time:
-    4 x 2048 new tokens after 2048 cached, and 4 x 1024 new after 7168 cached."""
+    4 x 2048 new tokens after 2048 cached, 4 x 1024 new after 7168 cached, and 4 x 512 new
+    after 8192 cached (few query rows over long prefixes: the pairs are split into pieces that
+    cross from the prefix into the chunk)."""
     longs = {}
     for name, chunks, max_len in (("4x2048_after_2048", [(2048, 2048)] * 4, 4096),
-                                  ("4x1024_after_7168", [(1024, 7168)] * 4, 8192)):
+                                  ("4x1024_after_7168", [(1024, 7168)] * 4, 8192),
+                                  ("4x512_after_8192", [(512, 8192)] * 4, 8704)):
         pw = W.mixed_to(W.mixed_workload([], chunks, seed=2, block_m=128, max_len=max_len), dev)
         pi = pw.inputs
         op = lambda: K.prefill_attention(

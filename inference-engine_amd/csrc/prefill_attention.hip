@@ -95,6 +95,10 @@ constexpr int PF_VG = 64 / PF_VK;         // V key groups (threads per channel g
 constexpr int PF_MAXP = IE_PREFILL_MAXP;                        // key pieces per sub-block, at most
 constexpr int PF_MIN_PIECE_TILES = IE_PREFILL_MIN_PIECE_TILES;  // tiles per piece, at least
 constexpr float RESCALE_SLACK = 8.0f;  // log2 units
+#ifndef IE_PREFILL_STRADDLE_MARGIN
+#define IE_PREFILL_STRADDLE_MARGIN 2
+#endif
+constexpr int PF_STRADDLE_MARGIN = IE_PREFILL_STRADDLE_MARGIN;  // tiles
 
 // LDS layouts (bytes), padded so that every fragment address is a per-lane base plus an
 // immediate. A fragment read (ds_read_b128, lane (l16, g) at row l16, 16-byte column g) is free of
@@ -196,6 +200,12 @@ __device__ __forceinline__ int piece_count(int npt, int nct, const Divisor& T) {
     const int pp = prefix_pieces(npt, nct, T);
     return pp + min(PF_MAXP - pp, div_ceil(nct, T));
 }
+// Pieces of a pair in the straddling form: its tiles, prefix then chunk, cut evenly into
+// cdiv(n, T) consecutive ranges (at most PF_MAXP); the range that crosses from the prefix into
+// the chunk runs both loops.
+__device__ __forceinline__ int straddle_count(int ntiles, const Divisor& T) {
+    return ntiles == 0 ? 0 : min(PF_MAXP, div_ceil(ntiles, T));
+}
 
 // The launch's work list, computed identically by every workgroup from the tile metadata:
 //  * piece size T (tiles): a (sub-block, kv head) pair becomes piece_count items. T is the
@@ -203,7 +213,13 @@ __device__ __forceinline__ int piece_count(int npt, int nct, const Divisor& T) {
 //    that every split item owns a slot: the search runs from the lower bound
 //    cdiv(sum(n) * Hkv, slots) up to the worst-rounding bound, where every part rounds up by a
 //    whole piece (sum(n / T) + parts) * Hkv <= slots, which always fits. With more (sub-block
-//    part, head) pairs than slots there is enough parallelism without splitting.
+//    part, head) pairs than slots this separate form cannot split. The straddling form
+//    (straddle_count) cuts each pair's tiles into even consecutive ranges whatever the parts,
+//    so it splits whenever the pairs alone fit the slots: a few sub-blocks over long prefixes
+//    (e.g. 16 chunks of 64 tokens each continuing a long context), which the separate form
+//    leaves one workgroup per pair on half the CUs. It is used when its pieces are shorter by
+//    more than PF_STRADDLE_MARGIN tiles (a piece that crosses into the chunk pays a second
+//    loop prologue, about two tiles' time).
 //  * items in launch order: sub-blocks from last to first (later sub-blocks of a sequence see
 //    more keys), then piece, then kv head.
 // schedule(target) finds the sub-block holding item `target`, the offset inside it and the
@@ -220,11 +236,12 @@ constexpr int PF_SCHED_CHUNKS = 4;
 constexpr int PF_LDS_ENTRIES = 512;
 
 struct SubBlock {
-    int r0, r1, seq_start, P, slot, npt, nct, ntiles, npieces, npp;  // npp: prefix pieces
+    // npp: prefix pieces, or -1 in the straddling form
+    int r0, r1, seq_start, P, slot, npt, nct, ntiles, npieces, npp;
 };
 
 __device__ __forceinline__ void fill_sub_block(SubBlock& s, int r0, int r1, int seq_start, int P,
-                                               int slot, const Divisor& T) {
+                                               int slot, const Divisor& T, bool straddle) {
     s.r0 = r0;
     s.r1 = r1;
     s.seq_start = seq_start;
@@ -233,13 +250,14 @@ __device__ __forceinline__ void fill_sub_block(SubBlock& s, int r0, int r1, int 
     s.npt = cdiv_i(P, PF_BN);
     s.nct = cdiv_i(r1 - seq_start, PF_BN);
     s.ntiles = s.npt + s.nct;
-    s.npieces = piece_count(s.npt, s.nct, T);
-    s.npp = prefix_pieces(s.npt, s.nct, T);
+    s.npieces = straddle ? straddle_count(s.ntiles, T) : piece_count(s.npt, s.nct, T);
+    s.npp = straddle ? -1 : prefix_pieces(s.npt, s.nct, T);
 }
 
 struct Loc {
     int sb, off, item_base, T;
     int found;
+    int straddle;
     SubBlock s;       // sub-block sb
 };
 
@@ -332,9 +350,20 @@ __device__ Loc schedule(const PrefillArgs& a, int target, int* tables) {
         return uni(wave_sum_i(n));
     };
     const int spare = a.grid - parts * a.hkv;
+    // the straddling form's lower bound on its piece size; it can only be chosen when its
+    // pieces beat the separate form's by PF_STRADDLE_MARGIN tiles and the pairs, one piece
+    // each, fit the slots
+    int lo = max(PF_MIN_PIECE_TILES, cdiv_i(tot * a.hkv, a.grid));
+    bool straddle_fits = false;
+    auto straddle_check = [&]() {
+        straddle_fits = launch_sum([](const SbInfo& z) { return z.npt + z.nct > 0 ? 1 : 0; }) *
+                            a.hkv < a.grid;
+    };
+    if (spare <= 0) straddle_check();
     Loc L;
     L.found = 0;
-    if (spare > 0 && target >= a.grid) {
+    L.straddle = 0;
+    if ((spare > 0 || straddle_fits) && target >= a.grid) {
         // with spare slots the pairs are split and every item is numbered below a.grid: a
         // workgroup past them has no item (these start late, once resident ones finish, and
         // would otherwise spend the rest of the schedule finding that out)
@@ -355,10 +384,42 @@ __device__ Loc schedule(const PrefillArgs& a, int target, int* tables) {
             }
         }
     }
+    // the straddling form's piece size: the smallest T whose pieces fit the slots (binary
+    // search: the count falls as T grows, and at the longest pair every pair is one piece,
+    // which fits). It replaces the separate form when that is PF_STRADDLE_MARGIN tiles longer
+    // (or does not split at all): a crossing piece pays a second loop prologue. Nothing of
+    // this runs when even the lower bound cannot win by that margin.
+    if (spare > 0 && lo + PF_STRADDLE_MARGIN < L.T) straddle_check();
+    if (straddle_fits && lo + PF_STRADDLE_MARGIN < L.T) {
+        int hi = lo;
+#pragma unroll
+        for (int c = 0; c < PF_SCHED_CHUNKS; ++c) hi = max(hi, zc[c].npt + zc[c].nct);
+        for (int c = PF_SCHED_CHUNKS; c < nchunks; ++c) {
+            const SbInfo z = info(sb_of(c), row_start_of(sb_of(c)));
+            hi = max(hi, z.npt + z.nct);
+        }
+        hi = uni((int)wave_max((float)hi));  // the longest pair (< 2^24 tiles: exact)
+        while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            const Divisor D = divisor(mid);
+            if (launch_sum([&](const SbInfo& z) { return straddle_count(z.npt + z.nct, D); }) *
+                    a.hkv <= a.grid)
+                hi = mid;
+            else
+                lo = mid + 1;
+        }
+        if (lo + PF_STRADDLE_MARGIN < L.T) {
+            L.T = lo;
+            L.straddle = 1;
+        }
+    }
     const Divisor DT = divisor(L.T);
+    const bool straddle = L.straddle != 0;
     int np[PF_SCHED_CHUNKS];  // pieces of the lane's sub-blocks
 #pragma unroll
-    for (int c = 0; c < PF_SCHED_CHUNKS; ++c) np[c] = piece_count(zc[c].npt, zc[c].nct, DT);
+    for (int c = 0; c < PF_SCHED_CHUNKS; ++c)
+        np[c] = straddle ? straddle_count(zc[c].npt + zc[c].nct, DT)
+                         : piece_count(zc[c].npt, zc[c].nct, DT);
     L.found = 0;
     L.sb = L.off = L.item_base = 0;
     int items_before = 0;
@@ -373,7 +434,7 @@ __device__ Loc schedule(const PrefillArgs& a, int target, int* tables) {
             L.item_base = from(incl - items);
             L.off = target - L.item_base;
             fill_sub_block(L.s, from(z.r0), from(z.r1), from(z.seq_start), from(z.P),
-                           from(z.slot), DT);
+                           from(z.slot), DT, straddle);
             L.found = 1;
         }
         items_before = __builtin_amdgcn_readlane(incl, 63);
@@ -384,7 +445,9 @@ __device__ Loc schedule(const PrefillArgs& a, int target, int* tables) {
         if (c < nchunks && visit(c, zc[c], np[c])) return L;
     for (int c = PF_SCHED_CHUNKS; c < nchunks; ++c) {
         const SbInfo z = info(sb_of(c), row_start_of(sb_of(c)));
-        if (visit(c, z, piece_count(z.npt, z.nct, DT))) return L;
+        if (visit(c, z, straddle ? straddle_count(z.npt + z.nct, DT)
+                                 : piece_count(z.npt, z.nct, DT)))
+            return L;
     }
     return L;
 }
@@ -793,9 +856,13 @@ __device__ __forceinline__ void merge_pieces(const PrefillArgs& a, const SubBloc
 // One work item: tiles [kt_begin, kt_end) of piece `piece` of sub-block s for kv head hk.
 __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBlock& s, int hk,
                                              int piece, int item, int item_base, PfLds& lds) {
-    // tiles [kt_begin, kt_end): the whole pair, a prefix piece or a chunk piece
+    // tiles [kt_begin, kt_end): the whole pair, a prefix piece, a chunk piece, or in the
+    // straddling form an even share of all the pair's tiles
     int kt_begin = 0, kt_end = s.ntiles;
-    if (s.npieces > 1) {
+    if (s.npieces > 1 && s.npp < 0) {
+        kt_begin = piece * s.ntiles / s.npieces;
+        kt_end = (piece + 1) * s.ntiles / s.npieces;
+    } else if (s.npieces > 1) {
         const int q = piece - s.npp, nc = s.npieces - s.npp;
         kt_begin = q < 0 ? piece * s.npt / s.npp : s.npt + q * s.nct / nc;
         kt_end = q < 0 ? (piece + 1) * s.npt / s.npp : s.npt + (q + 1) * s.nct / nc;

@@ -84,7 +84,36 @@ def test_prefill_long_sampled(ie, workloads, dev, chunks):
     assert_attn_close(o[rows], ref[rows], f"prefill long {chunks[0]} x {len(chunks)}")
 
 
-@pytest.mark.parametrize("chunks", [[(512, 0), (512, 1536)], [(300, 5000), (64, 9000)]])
+@pytest.mark.parametrize("chunks", [
+    [(64, 1000 + 250 * i) for i in range(16)],
+    [((33, 64, 100, 128)[i % 4], 500 + 175 * i) for i in range(20)],
+])
+def test_prefill_straddling_pieces(ie, workloads, dev, chunks):
+    """A few short chunks over long prefixes: 16 or 20 sub-blocks, each with prefix and chunk
+    tiles, i.e. (sub-block, KV head) pairs that fit a 256-CU device's slots one piece each, while
+    their prefix and chunk parts do not. The launch then splits each pair into even ranges of
+    its tiles, the range crossing into the chunk running both loops. Every row finite; the
+    first, second, middle and last rows of every chunk against the oracle (every piece of a
+    pair adds keys to every row of its sub-block)."""
+    say(f"prefill straddling pieces, {len(chunks)} chunks")
+    max_len = max(L + c for L, c in chunks)
+    wl = workloads.mixed_workload([], chunks, seed=31, block_m=128, max_len=max_len)
+    cu = wl.inputs["cu_seqlens"].numpy()
+    rows = sorted({int(cu[e]) + o for e, (L, _) in enumerate(chunks) for o in (0, 1, L // 2, L - 1)})
+    ins = {n: t.numpy() for n, t in wl.inputs.items()}
+    kp, vp = okv.dequantize_kv_prefix(cache_np(wl.cache), ins["cu_cached"], ins["slot_ids"])
+    ref = oat.prefill_attention(bf16_np(wl.q), bf16_np(wl.k), bf16_np(wl.v), ins["cu_seqlens"],
+                                ins["tile_start"], wl.block_m, kp, vp, ins["cu_cached"],
+                                rows=rows)
+    out = run_gpu(ie, workloads.mixed_to(wl, dev))
+    torch.cuda.synchronize()
+    o = bf16_np(out)
+    assert np.isfinite(o).all()
+    assert_attn_close(o[rows], ref[rows], f"prefill straddling {len(chunks)} chunks")
+
+
+@pytest.mark.parametrize("chunks", [[(512, 0), (512, 1536)], [(300, 5000), (64, 9000)],
+                                    [(64, 1000 + 250 * i) for i in range(16)]])
 def test_prefill_split_merge_fallback(ie, workloads, dev, monkeypatch, chunks):
     """Split pieces wait a bounded time for their pair's other pieces and then merge a share
     each; a piece that gives up leaves its share to the last one to finish. With the wait set to
