@@ -290,7 +290,7 @@ def bench_mixed_step(W, dev):
     return {"us_graph": round(ms * 1e3, 2), "rows": N, "decoders": len(wl.decode_ctx),
             "prefill_tokens": sum(L for L, _ in wl.chunks),
             "kernels": "fused_norm_rope_prefill, quantize_kv_prefill, prefill_attention, "
-                       "fused_rope_kv_decode, decode_attention"}
+                       "decode_attention_rope (fused_rope_kv_decode + decode_attention)"}
 
 
 def bench_step(steps, warmup, dev):
@@ -319,8 +319,9 @@ def bench_step(steps, warmup, dev):
            "batch": B, "layers": step.shape.layers, "ctx_mean": round(
                float(step.cached_lens.float().mean().item()) + 1, 1),
            "graph": "torch.cuda.CUDAGraph (hipGraph) of the full step; attention share = replay "
-                    "time of the step's fused_rope_kv_decode + decode_attention kernels captured "
-                    "alone / step replay time"}
+                    "time of the step's attention kernel (decode_attention_rope: "
+                    "fused_rope_kv_decode + decode_attention in one launch) captured alone / "
+                    "step replay time"}
     del g_step, g_attn, step
     torch.cuda.empty_cache()
     return res

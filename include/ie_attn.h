@@ -176,6 +176,32 @@ hipError_t ie_decode_attention(const ie_bf16* q, int64_t q_stride_b, int64_t q_s
                                size_t workspace_bytes, hipStream_t stream);
 
 /*
+ * ie_fused_rope_kv_decode followed by ie_decode_attention, in one launch: the decode branch of
+ * the attention layer (qwen3-1.7b/architecture.py:113-122, which calls kernels.py:483-544 and
+ * then kernels.py:272-361). No single counterpart in the reference: the two reference calls it
+ * replaces stay available as the two entry points above.
+ *
+ * q: bf16 [B, num_q_heads, head_dim], the QKV projection's raw rows (before norm and RoPE; any
+ * strides with unit channel stride); k, v, q_norm_weight, k_norm_weight, cos, sin, eps as for
+ * ie_fused_rope_kv_decode; the remaining arguments as for ie_decode_attention (same workspace).
+ * For every sequence b < num_decoding[0]: the cache afterwards holds the bits
+ * ie_fused_rope_kv_decode writes (int8 K and V and their scales at column cached_lens[b] of row
+ * slot_ids[b]), and out[b] is decode attention with the q that ie_fused_rope_kv_decode would
+ * return (its bits); q_out itself is not produced. Within the launch the piece of each sequence
+ * that ends at the new token computes that token's K/V row, writes it to the cache and uses it
+ * from registers; no other piece reads that column.
+ */
+hipError_t ie_decode_attention_rope(
+    const ie_bf16* q, int64_t q_stride_b, int64_t q_stride_h, const ie_bf16* k,
+    int64_t k_stride_b, int64_t k_stride_h, const ie_bf16* v, int64_t v_stride_b,
+    int64_t v_stride_h, const ie_bf16* q_norm_weight, const ie_bf16* k_norm_weight,
+    const ie_bf16* cos, int64_t cos_stride_b, const ie_bf16* sin, int64_t sin_stride_b,
+    float eps, int32_t batch, int32_t num_q_heads, const ie_kv_cache* cache,
+    const int32_t* cached_lens, const int32_t* slot_ids, const int32_t* num_decoding,
+    float scale, ie_bf16* out, int64_t out_stride_b, int64_t out_stride_h, void* workspace,
+    size_t workspace_bytes, hipStream_t stream);
+
+/*
  * ie_decode_attention without a workspace argument, for callers that cannot allocate device
  * memory (code under hipGraph capture, serving loops and harnesses that forbid allocation). No
  * counterpart in the reference. The arrival counts and split-K partials live in a static device

@@ -12,6 +12,7 @@ from .kernels import (  # noqa: F401
     LayerKVCache,
     add_rms_norm,
     decode_attention,
+    decode_attention_rope,
     dequantize_kv_prefix,
     fused_norm_rope_prefill,
     fused_rope_kv_decode,

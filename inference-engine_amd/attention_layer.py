@@ -6,18 +6,21 @@ caller of every op in `kernels` (qwen3-1.7b/architecture.py:31-202), the RoPE ta
 `attention` is the body of AttentionLayer.forward between the QKV split and the output
 projection, with the reference's dispatch (architecture.py:98):
 
-  pure decode (cu_seqlens is None)   fused_rope_kv_decode -> decode_attention
+  pure decode (cu_seqlens is None)   decode_attention_rope (= fused_rope_kv_decode ->
+                                     decode_attention, one launch)
   step with prefill                  fused_norm_rope_prefill (every row) -> quantize_kv_prefill
                                      -> prefill_attention (prefix read from the int8 cache)
-                                     -> fused_rope_kv_decode(q[:B]) with B = slot_ids.shape[0]
-                                     -> decode_attention(out=out): the decoding entries' rows
-                                        of the prefill output (decoders come first, one token
-                                        each, so decoding entry b is row b)
+                                     -> decode_attention_rope(q[:B], out=out) with
+                                        B = slot_ids.shape[0]: the decoding entries' rows of the
+                                        prefill output (decoders come first, one token each, so
+                                        decoding entry b is row b)
 
-The one difference from the reference is the one the fused prefill kernel forces: the
+Two differences from the reference. The fused prefill kernel forces one: the
 dequantize_kv_prefix call and its bf16 scratch (architecture.py:151-170) are gone, and
 prefill_attention takes (kv_cache, slot_ids, cu_cached) instead; PrefixScratch keeps its fields
-so the engine's call sites do not change, and only cu_cached is read.
+so the engine's call sites do not change, and only cu_cached is read. The other saves a launch
+per layer: the reference's fused_rope_kv_decode and decode_attention calls run as one launch
+that writes the same cache bits and attends with the same q bits.
 """
 
 from dataclasses import dataclass
@@ -25,8 +28,8 @@ from typing import Callable
 
 import torch
 
-from .kernels import (LayerKVCache, decode_attention, fused_norm_rope_prefill,
-                      fused_rope_kv_decode, linear, prefill_attention, quantize_kv_prefill)
+from .kernels import (LayerKVCache, decode_attention_rope, fused_norm_rope_prefill, linear,
+                      prefill_attention, quantize_kv_prefill)
 
 
 @dataclass
@@ -64,9 +67,8 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, seq_ids, cu_seq
     attention."""
     D = q.shape[-1]
     if cu_seqlens is None:
-        q = fused_rope_kv_decode(q, k, v, q_norm_weight, k_norm_weight, cos, sin, slot_ids,
-                                 kv_cache, cached_lens, num_decoding, eps)
-        return decode_attention(q, kv_cache, cached_lens, slot_ids, num_decoding, D ** -0.5)
+        return decode_attention_rope(q, k, v, q_norm_weight, k_norm_weight, cos, sin, slot_ids,
+                                     kv_cache, cached_lens, num_decoding, eps, D ** -0.5)
     assert seq_ids is not None and tile_start is not None and prefix_scratch is not None
     # every kernel sees the whole packet and skips the entries that are not its own, so nothing
     # here depends on how many entries decode; the decode rows are normed and roped here too
@@ -76,9 +78,8 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, seq_ids, cu_seq
     out = prefill_attention(q_p, k_p, v, seq_ids, cu_seqlens, tile_start, kv_cache, slot_ids,
                             prefix_scratch.cu_cached, prefill_block_m)
     B = slot_ids.shape[0]  # from a shape, not from how many entries decode
-    q_d = fused_rope_kv_decode(q[:B], k[:B], v[:B], q_norm_weight, k_norm_weight, cos[:B],
-                               sin[:B], slot_ids, kv_cache, cached_lens, num_decoding, eps)
-    decode_attention(q_d, kv_cache, cached_lens, slot_ids, num_decoding, D ** -0.5, out=out)
+    decode_attention_rope(q[:B], k[:B], v[:B], q_norm_weight, k_norm_weight, cos[:B], sin[:B],
+                          slot_ids, kv_cache, cached_lens, num_decoding, eps, D ** -0.5, out=out)
     return out
 
 

@@ -27,6 +27,7 @@
 #include <mutex>
 
 #include "ie_common.h"
+#include "kv_math.h"
 
 // Launch shape: 16 waves per CU (the 128-register budget allows 4 waves per SIMD), as 8-wave
 // workgroups, 2 per CU, while the batch fits their per-head target, else 4-wave workgroups
@@ -162,6 +163,20 @@ struct DecodeArgs {
     int target, nwork, hq, hkv;
     int batch;        // rows of q / cached_lens (num_decoding[0] <= batch)
     int head_fast;    // 1: grid (Hkv, pieces), the KV head in blockIdx.x; 0: grid (pieces, Hkv)
+    // The fused form (ie_decode_attention_rope): q holds the QKV projection's raw rows, and the
+    // launch does fused_rope_kv_decode's work itself: q normed, rotated and scaled by the
+    // calibration as that kernel computes it, and the new token's K/V row quantized and written
+    // to the cache by the piece that ends at it.
+    const uint16_t* k_new;
+    int64_t k_sb, k_sh;
+    const uint16_t* v_new;
+    int64_t v_sb, v_sh;
+    const uint16_t* q_norm;
+    const uint16_t* k_norm;
+    const uint16_t* cos;
+    const uint16_t* sin;
+    int64_t cos_sb, sin_sb;
+    float eps;
 };
 
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
@@ -311,7 +326,7 @@ __device__ __forceinline__ void block_pv(LaneState& st, const float (&t)[DA_U][2
 #define IE_DECODE_WAVES_PER_EU 4
 #endif
 
-template <int WAVES>
+template <int WAVES, bool ROPE>
 __global__ __launch_bounds__(WAVES * IE_WAVE)
 __attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_attention_kernel(
     DecodeArgs a) {
@@ -336,8 +351,11 @@ __attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_attenti
     const int n_end =
         b < 64 ? __builtin_amdgcn_readlane(raw0, b) + 1 : uniform(a.cached_lens[b] + 1);
     const int t_begin = split * piece;
-    const int t_end = min(t_begin + piece, n_end);
     const int slot = b < 64 ? __builtin_amdgcn_readlane(slot0, b) : uniform(a.slot_ids[b]);
+    // In the fused form the piece that ends at the new token (the sequence's last) takes that
+    // token from registers, not from the cache it writes it to: it streams one token less.
+    const bool last = ROPE && split == wk.needed - 1;
+    const int t_end = min(t_begin + piece, n_end) - (last ? 1 : 0);
 
     const int lane = threadIdx.x & 63, wave = uniform(threadIdx.x >> 6);
     const int g = lane >> 3, cc = lane & 7;
@@ -356,11 +374,44 @@ __attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_attenti
     half2_t qh[2][8];
     float qoff[2], kmul[2];  // wave-uniform (kept in SGPRs)
     uint4 qraw[2][2];
+    // Fused form: rows r = 0, 1 (query heads 2hk, 2hk + 1) and, for the last piece, r = 2 (the
+    // new K row of head hk) and r = 3 (its V row), one per wave (two with 2-wave workgroups),
+    // in fused_rope_kv_decode's layout: lane i holds channels i and i + 64.
+    constexpr int RR = ROPE ? (WAVES >= 4 ? 1 : 2) : 0;
+    const int nrows = last ? 4 : 2;
+    uint16_t rx1[RR > 0 ? RR : 1], rx2[RR > 0 ? RR : 1], rw1[RR > 0 ? RR : 1],
+        rw2[RR > 0 ? RR : 1], rcs[RR > 0 ? RR : 1], rsn[RR > 0 ? RR : 1];
+    float rc1[RR > 0 ? RR : 1], rc2[RR > 0 ? RR : 1];
+    if constexpr (ROPE) {
+        const float* cal =
+            a.c.k_calibration + slot * a.c.cal_stride_slot + hk * a.c.cal_stride_head;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const uint16_t* qp = a.q + b * a.q_sb + (2 * hk + h) * a.q_sh + 16 * cc;
-        qraw[h][0] = *reinterpret_cast<const uint4*>(qp);
-        qraw[h][1] = *reinterpret_cast<const uint4*>(qp + 8);
+        for (int i = 0; i < RR; ++i) {
+            const int r = wave + i * WAVES;
+            if (r < nrows) {
+                const uint16_t* src = r < 2   ? a.q + b * a.q_sb + (2 * hk + r) * a.q_sh
+                                      : r == 2 ? a.k_new + b * a.k_sb + hk * a.k_sh
+                                               : a.v_new + b * a.v_sb + hk * a.v_sh;
+                rx1[i] = src[lane];
+                rx2[i] = src[lane + 64];
+                if (r < 3) {
+                    const uint16_t* w = r < 2 ? a.q_norm : a.k_norm;
+                    rw1[i] = w[lane];
+                    rw2[i] = w[lane + 64];
+                    rcs[i] = a.cos[b * a.cos_sb + lane];
+                    rsn[i] = a.sin[b * a.sin_sb + lane];
+                    rc1[i] = cal[lane];
+                    rc2[i] = cal[lane + 64];
+                }
+            }
+        }
+    } else {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint16_t* qp = a.q + b * a.q_sb + (2 * hk + h) * a.q_sh + 16 * cc;
+            qraw[h][0] = *reinterpret_cast<const uint4*>(qp);
+            qraw[h][1] = *reinterpret_cast<const uint4*>(qp + 8);
+        }
     }
     // The first K/V block is requested with q, in the same memory round trip; the scheduling
     // barrier keeps the compiler from sinking the requests below q's conversion.
@@ -369,6 +420,53 @@ __attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_attenti
     load_block(kr, rk, rks, t0 + 4 * g, cc);
     load_block(vr, rv, rvs, t0 + 4 * g, cc);
     __builtin_amdgcn_sched_barrier(0);
+    __shared__ __attribute__((aligned(16))) uint16_t s_q[ROPE ? 2 : 1][DA_D];
+    __shared__ __attribute__((aligned(16))) int8_t s_new[ROPE ? 2 : 1][DA_D];
+    __shared__ float s_new_scale[2];
+    if constexpr (ROPE) {
+        // fused_rope_kv_decode's arithmetic (the same device functions): RMSNorm and RoPE, q
+        // times the calibration rounded to bf16, K divided by the calibration, K and V
+        // quantized; the new row goes to the cache at column n_end - 1 and, with its scales,
+        // to LDS for the last piece's own use
+        const int64_t col = n_end - 1;
+        const int64_t base = slot * a.c.stride_slot + hk * a.c.stride_head + col * a.c.stride_tok;
+        const int64_t sidx = slot * a.c.scale_stride_slot + hk * a.c.scale_stride_head + col;
+#pragma unroll
+        for (int i = 0; i < RR; ++i) {
+            const int r = wave + i * WAVES;
+            if (r >= nrows) continue;
+            int32_t q1, q2;
+            float sq;
+            if (r == 3) {
+                sq = quantize_row_wave(bf16_to_f32(rx1[i]), bf16_to_f32(rx2[i]), q1, q2);
+            } else {
+                float o1, o2;
+                norm_rope_row(bf16_to_f32(rx1[i]), bf16_to_f32(rx2[i]), bf16_to_f32(rw1[i]),
+                              bf16_to_f32(rw2[i]), bf16_to_f32(rcs[i]), bf16_to_f32(rsn[i]),
+                              a.eps, o1, o2);
+                if (r < 2) {
+                    s_q[r][lane] = (uint16_t)f32_to_bf16_rne(o1 * rc1[i]);
+                    s_q[r][lane + 64] = (uint16_t)f32_to_bf16_rne(o2 * rc2[i]);
+                    continue;
+                }
+                sq = quantize_row_wave(o1 / rc1[i], o2 / rc2[i], q1, q2);
+            }
+            int8_t* dst = r == 2 ? a.c.k : a.c.v;
+            float* dscale = r == 2 ? a.c.k_scale : a.c.v_scale;
+            dst[base + lane] = (int8_t)q1;
+            dst[base + lane + 64] = (int8_t)q2;
+            if (lane == 0) dscale[sidx] = sq;
+            s_new[r - 2][lane] = (int8_t)q1;
+            s_new[r - 2][lane + 64] = (int8_t)q2;
+            if (lane == 0) s_new_scale[r - 2] = sq;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            qraw[h][0] = *reinterpret_cast<const uint4*>(&s_q[h][16 * cc]);
+            qraw[h][1] = *reinterpret_cast<const uint4*>(&s_q[h][16 * cc + 8]);
+        }
+    }
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         const uint4 u0 = qraw[h][0], u1 = qraw[h][1];
@@ -427,9 +525,30 @@ __attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_attenti
         block_pv(st, s, vr, kmul);
         load_block(vr, rv, rvs, t0 + TOK_WG + 4 * g, cc);
     }
+    // the lane group derived afresh from the thread index for the masked blocks below: kept
+    // from the prologue it is a register the loop needs
+    int tid_m = threadIdx.x;
+    asm volatile("" : "+v"(tid_m));
+    const int gm = (tid_m & 63) >> 3;
     if (nfull < cw) {
-        block_scores<true>(s, kr, qh, qoff, t0 + 4 * g, t_end);
+        block_scores<true>(s, kr, qh, qoff, t0 + 4 * gm, t_end);
         block_pv(st, s, vr, kmul);
+    }
+    if (ROPE && last && wave == WAVES - 1) {
+        // the new token, as a block whose other tokens are masked: lane group 0 holds its row
+        KVRegs kn, vn;
+#pragma unroll
+        for (int u = 0; u < DA_U; ++u) kn.x[u] = vn.x[u] = v4u{0u, 0u, 0u, 0u};
+        kn.scale = vn.scale = v4u{0u, 0u, 0u, 0u};
+        if (gm == 0) {
+            const int cm = tid_m & 7;
+            kn.x[0] = *reinterpret_cast<const v4u*>(&s_new[0][16 * cm]);
+            vn.x[0] = *reinterpret_cast<const v4u*>(&s_new[ROPE ? 1 : 0][16 * cm]);
+            kn.scale[0] = __float_as_uint(s_new_scale[0]);
+            vn.scale[0] = __float_as_uint(s_new_scale[1]);
+        }
+        block_scores<true>(s, kn, qh, qoff, n_end - 1 + 4 * gm, n_end);
+        block_pv(st, s, vn, kmul);
     }
 
     float (&m)[2] = st.m;
@@ -648,18 +767,21 @@ extern "C" size_t ie_decode_attention_workspace_size(int32_t batch, int32_t num_
     return workspace_layout(batch, num_q_heads, std::max(1, num_q_heads / 2)).bytes;
 }
 
+// q_rows16: q is read in 16-byte pieces (the plain form; the fused form reads q two bytes per
+// lane, as fused_rope_kv_decode does).
 static hipError_t check_decode(const ie_bf16* q, int32_t batch, int32_t num_q_heads,
                                const ie_kv_cache* cache, const int32_t* cached_lens,
                                const int32_t* slot_ids, const int32_t* num_decoding,
                                const ie_bf16* out, int64_t q_sb, int64_t q_sh, void* workspace,
-                               size_t workspace_bytes, Layout* L) {
+                               size_t workspace_bytes, Layout* L, bool q_rows16 = true) {
     hipError_t e = check_cache(cache);
     if (e != hipSuccess) return e;
     IE_REQUIRE(batch >= 0, "negative batch");
     IE_REQUIRE(num_q_heads == 2 * cache->num_kv_heads, "num_q_heads must be 2 * num_kv_heads");
     if (batch == 0) return hipSuccess;
     IE_REQUIRE(q && cached_lens && slot_ids && num_decoding && out, "null pointer");
-    IE_REQUIRE((reinterpret_cast<uintptr_t>(q) & 15) == 0 && q_sb % 8 == 0 && q_sh % 8 == 0,
+    IE_REQUIRE(!q_rows16 ||
+                   ((reinterpret_cast<uintptr_t>(q) & 15) == 0 && q_sb % 8 == 0 && q_sh % 8 == 0),
                "q rows must be 16-byte aligned with contiguous head_dim");
     *L = workspace_layout(batch, num_q_heads, (int)cache->num_kv_heads);
     IE_REQUIRE(workspace != nullptr && workspace_bytes >= L->bytes, "workspace too small");
@@ -667,16 +789,14 @@ static hipError_t check_decode(const ie_bf16* q, int32_t batch, int32_t num_q_he
     return hipSuccess;
 }
 
-extern "C" hipError_t ie_decode_attention(
-    const ie_bf16* q, int64_t q_stride_b, int64_t q_stride_h, int32_t batch, int32_t num_q_heads,
-    const ie_kv_cache* cache, const int32_t* cached_lens, const int32_t* slot_ids,
-    const int32_t* num_decoding, float scale, ie_bf16* out, int64_t out_stride_b,
-    int64_t out_stride_h, void* workspace, size_t workspace_bytes, hipStream_t stream) {
-    Layout L{};
-    hipError_t e = check_decode(q, batch, num_q_heads, cache, cached_lens, slot_ids, num_decoding,
-                                out, q_stride_b, q_stride_h, workspace, workspace_bytes, &L);
-    if (e != hipSuccess || batch == 0) return e;
-    DecodeArgs a;
+// The arguments both forms share; the fused form's own fields stay null.
+static DecodeArgs decode_args(const ie_bf16* q, int64_t q_stride_b, int64_t q_stride_h,
+                              int32_t batch, int32_t num_q_heads, const ie_kv_cache* cache,
+                              const int32_t* cached_lens, const int32_t* slot_ids,
+                              const int32_t* num_decoding, float scale, ie_bf16* out,
+                              int64_t out_stride_b, int64_t out_stride_h, void* workspace,
+                              const Layout& L) {
+    DecodeArgs a{};
     a.q = (const uint16_t*)q;
     a.q_sb = q_stride_b;
     a.q_sh = q_stride_h;
@@ -698,6 +818,12 @@ extern "C" hipError_t ie_decode_attention(
     a.hq = num_q_heads;
     a.hkv = (int)cache->num_kv_heads;
     a.batch = batch;
+    return a;
+}
+
+template <bool ROPE>
+static hipError_t decode_launch(DecodeArgs& a, const Layout& L, int32_t batch,
+                                const ie_kv_cache* cache, hipStream_t stream) {
     // pieces number at most target + nd, and at most target when nd <= target (decode_piece):
     // with batch <= target the grid needs no spare workgroups, which would otherwise hold
     // resident slots while they find out that they are idle
@@ -712,11 +838,60 @@ extern "C" hipError_t ie_decode_attention(
     const dim3 grid = a.head_fast ? dim3((unsigned)cache->num_kv_heads, pieces)
                                   : dim3(pieces, (unsigned)cache->num_kv_heads);
     switch (L.waves) {
-        case 8: hipLaunchKernelGGL(decode_attention_kernel<8>, grid, dim3(512), 0, stream, a); break;
-        case 4: hipLaunchKernelGGL(decode_attention_kernel<4>, grid, dim3(256), 0, stream, a); break;
-        default: hipLaunchKernelGGL(decode_attention_kernel<2>, grid, dim3(128), 0, stream, a); break;
+        case 8: hipLaunchKernelGGL((decode_attention_kernel<8, ROPE>), grid, dim3(512), 0, stream, a); break;
+        case 4: hipLaunchKernelGGL((decode_attention_kernel<4, ROPE>), grid, dim3(256), 0, stream, a); break;
+        default: hipLaunchKernelGGL((decode_attention_kernel<2, ROPE>), grid, dim3(128), 0, stream, a); break;
     }
     return hipGetLastError();
+}
+
+extern "C" hipError_t ie_decode_attention(
+    const ie_bf16* q, int64_t q_stride_b, int64_t q_stride_h, int32_t batch, int32_t num_q_heads,
+    const ie_kv_cache* cache, const int32_t* cached_lens, const int32_t* slot_ids,
+    const int32_t* num_decoding, float scale, ie_bf16* out, int64_t out_stride_b,
+    int64_t out_stride_h, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    Layout L{};
+    hipError_t e = check_decode(q, batch, num_q_heads, cache, cached_lens, slot_ids, num_decoding,
+                                out, q_stride_b, q_stride_h, workspace, workspace_bytes, &L);
+    if (e != hipSuccess || batch == 0) return e;
+    DecodeArgs a = decode_args(q, q_stride_b, q_stride_h, batch, num_q_heads, cache, cached_lens,
+                               slot_ids, num_decoding, scale, out, out_stride_b, out_stride_h,
+                               workspace, L);
+    return decode_launch<false>(a, L, batch, cache, stream);
+}
+
+extern "C" hipError_t ie_decode_attention_rope(
+    const ie_bf16* q, int64_t q_stride_b, int64_t q_stride_h, const ie_bf16* k,
+    int64_t k_stride_b, int64_t k_stride_h, const ie_bf16* v, int64_t v_stride_b,
+    int64_t v_stride_h, const ie_bf16* q_norm_weight, const ie_bf16* k_norm_weight,
+    const ie_bf16* cos, int64_t cos_stride_b, const ie_bf16* sin, int64_t sin_stride_b,
+    float eps, int32_t batch, int32_t num_q_heads, const ie_kv_cache* cache,
+    const int32_t* cached_lens, const int32_t* slot_ids, const int32_t* num_decoding,
+    float scale, ie_bf16* out, int64_t out_stride_b, int64_t out_stride_h, void* workspace,
+    size_t workspace_bytes, hipStream_t stream) {
+    Layout L{};
+    hipError_t e = check_decode(q, batch, num_q_heads, cache, cached_lens, slot_ids, num_decoding,
+                                out, q_stride_b, q_stride_h, workspace, workspace_bytes, &L,
+                                false);
+    if (e != hipSuccess || batch == 0) return e;
+    IE_REQUIRE(k && v && q_norm_weight && k_norm_weight && cos && sin, "null pointer");
+    DecodeArgs a = decode_args(q, q_stride_b, q_stride_h, batch, num_q_heads, cache, cached_lens,
+                               slot_ids, num_decoding, scale, out, out_stride_b, out_stride_h,
+                               workspace, L);
+    a.k_new = (const uint16_t*)k;
+    a.k_sb = k_stride_b;
+    a.k_sh = k_stride_h;
+    a.v_new = (const uint16_t*)v;
+    a.v_sb = v_stride_b;
+    a.v_sh = v_stride_h;
+    a.q_norm = (const uint16_t*)q_norm_weight;
+    a.k_norm = (const uint16_t*)k_norm_weight;
+    a.cos = (const uint16_t*)cos;
+    a.sin = (const uint16_t*)sin;
+    a.cos_sb = cos_stride_b;
+    a.sin_sb = sin_stride_b;
+    a.eps = eps;
+    return decode_launch<true>(a, L, batch, cache, stream);
 }
 
 extern "C" int32_t ie_decode_attention_grid(int32_t batch, int32_t num_kv_heads) {

@@ -10,6 +10,7 @@
 // is reproducible on the host. Each row of 128 channels is handled by 16 lanes x 8 channels
 // (prefill) or by one wave, 2 channels per lane (decode).
 #include "ie_common.h"
+#include "kv_math.h"
 
 namespace ie {
 
@@ -37,13 +38,6 @@ __device__ __forceinline__ Row8 load_bf16x8(const uint16_t* p) {
     r.x[4] = bf16lo(u.z); r.x[5] = bf16hi(u.z);
     r.x[6] = bf16lo(u.w); r.x[7] = bf16hi(u.w);
     return r;
-}
-
-__device__ __forceinline__ int32_t quant1(float x, float s) {
-    // clamp(rint(x / s), -127, 127); x / s is an IEEE division, rint rounds half to even.
-    float r = rintf(x / s);
-    r = fminf(fmaxf(r, -127.0f), 127.0f);
-    return static_cast<int32_t>(r);
 }
 
 __device__ __forceinline__ uint2 pack_i8x8(const int32_t* q) {
@@ -283,35 +277,6 @@ __global__ __launch_bounds__(QP_THREADS) void quantize_kv_prefill_kernel(
     }
 }
 
-// RMSNorm then RoPE of one head row, shared by the decode write and the prefill norm/rope
-// (kernels.py:414-436 and :582-646 compute the same thing): lane i holds channels i and i + 64
-// (the pair RoPE rotates); the sum of squares in the fixed butterfly order,
-// rstd = 1 / sqrt(ss / 128 + eps), x * rstd * w, then the rotation with the row's cos/sin.
-// IEEE single-precision operations, no contraction.
-// The three parts: the row's sum of squares (every lane gets it), rstd from it, and the
-// normalization and rotation of the lane's two channels.
-__device__ __forceinline__ float row_sumsq(float x1, float x2) {
-#pragma clang fp contract(off)
-    return wave_sum_butterfly(x1 * x1) + wave_sum_butterfly(x2 * x2);
-}
-__device__ __forceinline__ float row_rstd(float ss, float eps) {
-#pragma clang fp contract(off)
-    const float var = ss / 128.0f + eps;
-    return 1.0f / sqrtf(var);
-}
-__device__ __forceinline__ void row_norm_rope(float x1, float x2, float rstd, float w1, float w2,
-                                              float cs, float sn, float& o1, float& o2) {
-#pragma clang fp contract(off)
-    x1 = (x1 * rstd) * w1;
-    x2 = (x2 * rstd) * w2;
-    o1 = (x1 * cs) - (x2 * sn);
-    o2 = (x1 * sn) + (x2 * cs);
-}
-__device__ __forceinline__ void norm_rope_row(float x1, float x2, float w1, float w2, float cs,
-                                              float sn, float eps, float& o1, float& o2) {
-    row_norm_rope(x1, x2, row_rstd(row_sumsq(x1, x2), eps), w1, w2, cs, sn, o1, o2);
-}
-
 // grid (B, ceil((Hq + Hkv) / 4)), block 256: wave w of workgroup y handles head row
 // r = 4y + w; r < Hq is query head r, else kv head r - Hq (its K and V). Lane i holds channels
 // i and i + 64 (the two halves RoPE pairs, kernels.py:410-436).
@@ -368,20 +333,18 @@ __global__ __launch_bounds__(256) void fused_rope_kv_decode_kernel(
     const int64_t base = slot * c.stride_slot + j * c.stride_head + col * c.stride_tok;
     const int64_t sidx = slot * c.scale_stride_slot + j * c.scale_stride_head + col;
     {
-        const float k1 = o1 / c1, k2 = o2 / c2;
-        const float a = wave_max(fmaxf(fabsf(k1), fabsf(k2)));
-        const float s = fmaxf(a, 1e-6f) / 127.0f;
-        c.k[base + lane] = (int8_t)quant1(k1, s);
-        c.k[base + lane + 64] = (int8_t)quant1(k2, s);
+        int32_t q1, q2;
+        const float s = quantize_row_wave(o1 / c1, o2 / c2, q1, q2);
+        c.k[base + lane] = (int8_t)q1;
+        c.k[base + lane + 64] = (int8_t)q2;
         if (lane == 0) c.k_scale[sidx] = s;
     }
     // V: int8 with its own scale (kernels.py:472-480).
     {
-        const float v1 = bf16_to_f32(vr1), v2 = bf16_to_f32(vr2);
-        const float a = wave_max(fmaxf(fabsf(v1), fabsf(v2)));
-        const float s = fmaxf(a, 1e-6f) / 127.0f;
-        c.v[base + lane] = (int8_t)quant1(v1, s);
-        c.v[base + lane + 64] = (int8_t)quant1(v2, s);
+        int32_t q1, q2;
+        const float s = quantize_row_wave(bf16_to_f32(vr1), bf16_to_f32(vr2), q1, q2);
+        c.v[base + lane] = (int8_t)q1;
+        c.v[base + lane + 64] = (int8_t)q2;
         if (lane == 0) c.v_scale[sidx] = s;
     }
 }

@@ -322,6 +322,42 @@ void decode_attention(const at::Tensor& q, const at::Tensor& k_cache, const at::
        "decode_attention");
 }
 
+// fused_rope_kv_decode then decode_attention in one launch (ie_decode_attention_rope): q, k, v
+// are the QKV projection's raw rows.
+void decode_attention_rope(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
+                           const at::Tensor& q_norm_weight, const at::Tensor& k_norm_weight,
+                           const at::Tensor& cos, const at::Tensor& sin,
+                           const at::Tensor& k_cache, const at::Tensor& v_cache,
+                           const at::Tensor& k_scale, const at::Tensor& v_scale,
+                           const at::Tensor& k_calibration, const at::Tensor& cached_lens,
+                           const at::Tensor& slot_ids, const at::Tensor& num_decoding,
+                           double eps, double scale, const at::Tensor& out) {
+    check_bf16_rows(k, "k", 3);
+    check_bf16_rows(v, "v", 3);
+    check_bf16_rows(q_norm_weight, "q_norm_weight", 1);
+    check_bf16_rows(k_norm_weight, "k_norm_weight", 1);
+    check_bf16_rows(cos, "cos", 3);
+    check_bf16_rows(sin, "sin", 3);
+    const c10::DeviceGuard guard(q.device());
+    DecodeCall d = decode_prep(q, k_cache, v_cache, k_scale, v_scale, k_calibration, cached_lens,
+                               slot_ids, num_decoding, out);
+    TORCH_CHECK(q.size(2) == 128 && k.size(2) == 128 && v.size(2) == 128, "ie: head_dim 128");
+    TORCH_CHECK(k.size(0) >= d.B && v.size(0) >= d.B && k.size(1) == d.c.num_kv_heads &&
+                    v.size(1) == d.c.num_kv_heads,
+                "ie: k/v shape mismatch");
+    TORCH_CHECK(cos.size(0) >= d.B && sin.size(0) >= d.B && cos.size(2) == 64 && sin.size(2) == 64,
+                "ie: cos/sin must be [B,1,64]");
+    at::Tensor ws = persistent_workspace(q, d.ws_bytes, d.B <= 1024 ? 0 : d.B);
+    ok(ie_decode_attention_rope(bf(q), q.stride(0), q.stride(1), bf(k), k.stride(0), k.stride(1),
+                                bf(v), v.stride(0), v.stride(1), bf(q_norm_weight),
+                                bf(k_norm_weight), bf(cos), cos.stride(0), bf(sin),
+                                sin.stride(0), (float)eps, d.B, d.hq, &d.c, i32(cached_lens),
+                                i32(slot_ids), i32(num_decoding), (float)scale, bfm(out),
+                                out.stride(0), out.stride(1), ws.data_ptr(), d.ws_bytes,
+                                stream_of(q)),
+       "decode_attention_rope");
+}
+
 int64_t decode_attention_workspace_size(int64_t batch, int64_t num_q_heads) {
     return (int64_t)ie_decode_attention_workspace_size((int32_t)batch, (int32_t)num_q_heads, 128);
 }
@@ -405,6 +441,11 @@ TORCH_LIBRARY(ie, m) {
         "decode_attention(Tensor q, Tensor k_cache, Tensor v_cache, Tensor k_scale, "
         "Tensor v_scale, Tensor k_calibration, Tensor cached_lens, Tensor slot_ids, "
         "Tensor num_decoding, float scale, Tensor(a!) out) -> ()");
+    m.def(
+        "decode_attention_rope(Tensor q, Tensor k, Tensor v, Tensor q_norm_weight, "
+        "Tensor k_norm_weight, Tensor cos, Tensor sin, Tensor(a!) k_cache, Tensor(b!) v_cache, "
+        "Tensor(c!) k_scale, Tensor(d!) v_scale, Tensor k_calibration, Tensor cached_lens, "
+        "Tensor slot_ids, Tensor num_decoding, float eps, float scale, Tensor(e!) out) -> ()");
     m.def("decode_attention_workspace_size(int batch, int num_q_heads) -> int");
     m.def(
         "dequantize_kv_prefix(Tensor k_cache, Tensor v_cache, Tensor k_scale, Tensor v_scale, "
@@ -427,6 +468,7 @@ TORCH_LIBRARY_IMPL(ie, CUDA, m) {
     m.impl("skinny_matmul", &skinny_matmul);
     m.impl("skinny_matmul_silu_mul", &skinny_matmul_silu_mul);
     m.impl("decode_attention", &decode_attention);
+    m.impl("decode_attention_rope", &decode_attention_rope);
     m.impl("dequantize_kv_prefix", &dequantize_kv_prefix);
     m.impl("prefill_attention", &prefill_attention);
 }

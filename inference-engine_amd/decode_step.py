@@ -4,9 +4,10 @@ as a hipGraph: the harness for the whole-step measurement (tokens/s and the atte
 Mirrors the decode branch of the reference's model (qwen3-1.7b/architecture.py:98-122 inside
 TransformerBlock.forward :262-304 and Qwen3Model.forward :395-413) and its graph capture and
 replay (qwen3-1.7b/engine.py:376-470): per layer, `add_rms_norm` (the first layer: RMSNorm),
-QKV projection, `fused_rope_kv_decode` (norm + RoPE + int8 KV write), `decode_attention`,
-output projection, `add_rms_norm`, gate/up projection and `silu_mul` (one launch,
-`linear_silu_mul`, where the skinny GEMM serves that shape), down projection; then the
+QKV projection, `decode_attention_rope` (`fused_rope_kv_decode`'s norm + RoPE + int8 KV
+write and `decode_attention` in one launch), output projection, `add_rms_norm`, gate/up
+projection and `silu_mul` (one launch, `linear_silu_mul`, where the skinny GEMM serves that
+shape), down projection; then the
 final `add_rms_norm`, the tied-embedding LM head and greedy sampling (`sample` at tau 0,
 kernels.py:1343-1370). All of these are this package's HIP kernels; for each projection
 `linear` (kernels.py:1451-1458) runs this package's skinny GEMM or the library GEMM
@@ -23,8 +24,8 @@ import torch
 import torch.nn.functional as F
 
 from .attention_layer import attention, rope_inv_freq, rope_tables
-from .kernels import (LayerKVCache, add_rms_norm, decode_attention, fused_rope_kv_decode, linear,
-                      linear_silu_mul, make_layer_cache, sample, tune_linear)
+from .kernels import (LayerKVCache, add_rms_norm, decode_attention_rope, linear, linear_silu_mul,
+                      make_layer_cache, sample, tune_linear)
 
 
 @dataclass(frozen=True)
@@ -156,8 +157,9 @@ class DecodeStep:
         return sample(logits, 0.0, self.seed)
 
     def attention_only(self) -> torch.Tensor:
-        """The step's attention kernels alone (per layer: fused_rope_kv_decode and
-        decode_attention on fixed activations), for the attention share of a step."""
+        """The step's attention kernels alone (per layer: decode_attention_rope, i.e.
+        fused_rope_kv_decode and decode_attention in one launch, on fixed activations), for the
+        attention share of a step."""
         s, B = self.shape, self.B
         cos, sin = self._rope()
         if not hasattr(self, "_qkv_fixed"):
@@ -171,11 +173,9 @@ class DecodeStep:
         v = v.view(B, s.num_kv_heads, s.head_dim)
         out = None
         for li, lw in enumerate(self.layers):
-            qo = fused_rope_kv_decode(q, k, v, lw.q_norm, lw.k_norm, cos, sin, self.slot_ids,
-                                      self.caches[li], self.cached_lens, self.num_decoding,
-                                      s.eps)
-            out = decode_attention(qo, self.caches[li], self.cached_lens, self.slot_ids,
-                                   self.num_decoding, s.head_dim ** -0.5)
+            out = decode_attention_rope(q, k, v, lw.q_norm, lw.k_norm, cos, sin, self.slot_ids,
+                                        self.caches[li], self.cached_lens, self.num_decoding,
+                                        s.eps, s.head_dim ** -0.5)
         return out
 
     def capture(self, fn=None):

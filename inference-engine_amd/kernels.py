@@ -93,6 +93,38 @@ def fused_rope_kv_decode(
                                       float(eps))
 
 
+def decode_attention_rope(
+    q: torch.Tensor,  # (B, Hq, D), the QKV projection's rows before norm and RoPE
+    k: torch.Tensor,  # (B, Hkv, D)
+    v: torch.Tensor,
+    q_norm_weight: torch.Tensor,  # (D,)
+    k_norm_weight: torch.Tensor,
+    cos: torch.Tensor,  # (B, 1, D // 2)
+    sin: torch.Tensor,
+    slot_ids: torch.Tensor,  # [B]
+    kv_cache: LayerKVCache,
+    cached_lens: torch.Tensor,  # [B]
+    num_decoding: torch.Tensor,
+    eps: float,
+    scale,
+    out: torch.Tensor | None = None,  # [>= B, Hq, D]
+):
+    """fused_rope_kv_decode (kernels.py:483-544) followed by decode_attention (kernels.py:272-361)
+    in one launch: the same cache writes, bit for bit, and the attention of the q that
+    fused_rope_kv_decode returns, which is not materialized. The decode branch of
+    architecture.py:113-122 without the launch between the two ops."""
+    assert kv_cache.k.stride() == kv_cache.v.stride(), "kernel uses one set of strides for both caches"
+    assert kv_cache.k_scale.stride() == kv_cache.v_scale.stride()
+    B, Hq, D = q.shape
+    if out is None:
+        out = torch.empty(B, Hq, D, device=q.device, dtype=q.dtype)
+    assert out.shape[0] >= B and out.shape[1:] == (Hq, D) and out.stride(-1) == 1
+    ops().decode_attention_rope(q, k, v, q_norm_weight, k_norm_weight, cos, sin,
+                                *_cache_args(kv_cache), cached_lens, slot_ids, num_decoding,
+                                float(eps), float(scale), out)
+    return out
+
+
 def fused_norm_rope_prefill(
     q: torch.Tensor,  # bf16 [N, Hq, D], the prefill rows only: q[num_seqs_decoding:]
     k: torch.Tensor,  # bf16 [N, Hkv, D]

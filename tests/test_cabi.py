@@ -21,7 +21,7 @@ def test_library_exports_every_declared_symbol(native):
 def test_torch_ops_registered(ie):
     ops = ie.kernels.ops()
     for name in ["quantize_kv_prefill", "fused_rope_kv_decode", "fused_norm_rope_prefill",
-                 "decode_attention", "dequantize_kv_prefix",
+                 "decode_attention", "decode_attention_rope", "dequantize_kv_prefix",
                  "prefill_attention", "decode_attention_workspace_size", "sample", "add_rms_norm",
                  "silu_mul", "skinny_matmul", "skinny_matmul_silu_mul"]:
         assert hasattr(ops, name), name
@@ -81,6 +81,24 @@ def test_ops_refuse_cpu_tensors(ie):
     i = torch.zeros(1, dtype=torch.int32)
     with pytest.raises((RuntimeError, NotImplementedError)):
         ie.decode_attention(q, c, i, i, i, 0.1)
+
+
+def test_decode_attention_rope_null_k_rejected_on_host(native):
+    """The fused decode entry point checks its own arguments (here a null k) after the decode
+    ones, on the host, before any launch."""
+    lib = native.cabi()
+    desc = native.KVCacheDesc(256, 256, 256, 256, 256, 2, 8, 64, 128, 8 * 64 * 128, 64 * 128, 128,
+                              8 * 64, 64, 8 * 128, 128)
+    fn = lib.ie_decode_attention_rope
+    fn.restype = ctypes.c_int
+    p, null, i64 = ctypes.c_void_p(256), ctypes.c_void_p(0), ctypes.c_int64
+    ws = lib.ie_decode_attention_workspace_size(1, 16, 128)
+    rc = fn(p, i64(4096), i64(128), null, i64(4096), i64(128), p, i64(4096), i64(128), p, p,
+            p, i64(64), p, i64(64), ctypes.c_float(1e-6), ctypes.c_int32(1), ctypes.c_int32(16),
+            ctypes.byref(desc), p, p, p, ctypes.c_float(0.1), p, i64(2048), i64(128), p,
+            ctypes.c_size_t(ws), null)
+    assert rc == HIP_ERROR_INVALID_VALUE
+    assert b"null" in lib.ie_attn_last_error()
 
 
 def test_quantize_too_many_tokens_rejected_on_host(native):

@@ -37,24 +37,35 @@ def test_decode_step_graph_bitwise(ie, dev):
 
 
 def test_decode_step_attention_matches_parts(ie, dev):
-    """The step's attention sub-block equals the same kernels called one by one."""
+    """The step's attention sub-block equals the same kernels called one by one (QKV projection,
+    decode_attention_rope, output projection), and its attention matches the reference's two
+    calls (fused_rope_kv_decode, then decode_attention) within the bf16 tolerance, writing the
+    same cache bits."""
+    from helpers import assert_attn_close, assert_cache_bitwise, bf16_np, cache_np, cache_to
+
     ds = importlib.import_module("inference-engine_amd.decode_step")
     shape = ds.Qwen3Shape(layers=1, vocab=1024)
     step = ds.make_decode_step(batch=4, ctx_lo=64, ctx_hi=256, shape=shape, device=dev, seed=5)
     cos, sin = step._rope()
     x = torch.randn(4, shape.model_dim, device=dev).bfloat16()
-    got = step.attention(0, x, cos, sin)  # the second call below rewrites the same cache column
+    before = cache_to(step.caches[0], dev, ie.LayerKVCache)
+    got = step.attention(0, x, cos, sin)  # the calls below rewrite the same cache column
     lw = step.layers[0]
     qkv = ie.kernels.linear(x, lw.qkv)  # the step's projection (tuned: skinny or library)
     q, k, v = qkv.split([2048, 1024, 1024], dim=-1)
-    qo = ie.fused_rope_kv_decode(q.view(4, 16, 128), k.view(4, 8, 128), v.view(4, 8, 128),
-                                 lw.q_norm, lw.k_norm, cos, sin, step.slot_ids, step.caches[0],
-                                 step.cached_lens, step.num_decoding, 1e-6)
-    o = ie.decode_attention(qo, step.caches[0], step.cached_lens, step.slot_ids,
-                            step.num_decoding, 128 ** -0.5)
+    q, k, v = q.view(4, 16, 128), k.view(4, 8, 128), v.view(4, 8, 128)
+    o = ie.decode_attention_rope(q, k, v, lw.q_norm, lw.k_norm, cos, sin, step.slot_ids,
+                                 step.caches[0], step.cached_lens, step.num_decoding, 1e-6,
+                                 128 ** -0.5)
     want = ie.kernels.linear(o.view(4, -1), lw.o_proj)
+    qo = ie.fused_rope_kv_decode(q, k, v, lw.q_norm, lw.k_norm, cos, sin, step.slot_ids, before,
+                                 step.cached_lens, step.num_decoding, 1e-6)
+    o2 = ie.decode_attention(qo, before, step.cached_lens, step.slot_ids, step.num_decoding,
+                             128 ** -0.5)
     torch.cuda.synchronize()
     assert torch.equal(got, want)
+    assert_cache_bitwise(step.caches[0], cache_np(before), "fused vs two calls: cache")
+    assert_attn_close(bf16_np(o), bf16_np(o2), "fused vs two calls: attention")
 
 
 def test_config5_full_size(ie, dev):
@@ -122,3 +133,13 @@ def test_config5_full_size(ie, dev):
                               sub.v_scale[i, :, L].view(np.uint32))
     ref = oat.decode_attention(qo_ref, sub, lens, np.arange(len(pick)), len(pick), 128 ** -0.5)
     assert_attn_close(bf16_np(o[pick]), ref, "config 5 layer 0 attention")
+    # the step's own fused launch on the same activations: the same cache bits, the same
+    # attention within tolerance
+    o_f = ie.decode_attention_rope(q, k, v, lw.q_norm, lw.k_norm, cos, sin, step.slot_ids, cache,
+                                   step.cached_lens, step.num_decoding, s.eps, 128 ** -0.5)
+    torch.cuda.synchronize()
+    got_f = cache_np(type(cache)(*(t[slots] for t in (cache.k, cache.v, cache.k_scale,
+                                                        cache.v_scale, cache.k_calibration))))
+    for name in ("k", "v", "k_scale", "v_scale"):
+        assert np.array_equal(getattr(got_f, name), getattr(got, name)), f"fused launch: {name}"
+    assert_attn_close(bf16_np(o_f[pick]), ref, "config 5 layer 0 attention, fused launch")
