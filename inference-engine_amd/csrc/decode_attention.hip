@@ -374,36 +374,38 @@ __attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_attenti
     half2_t qh[2][8];
     float qoff[2], kmul[2];  // wave-uniform (kept in SGPRs)
     uint4 qraw[2][2];
-    // Fused form: rows r = 0, 1 (query heads 2hk, 2hk + 1) and, for the last piece, r = 2 (the
-    // new K row of head hk) and r = 3 (its V row), one per wave (two with 2-wave workgroups),
-    // in fused_rope_kv_decode's layout: lane i holds channels i and i + 64.
-    constexpr int RR = ROPE ? (WAVES >= 4 ? 1 : 2) : 0;
-    const int nrows = last ? 4 : 2;
-    uint16_t rx1[RR > 0 ? RR : 1], rx2[RR > 0 ? RR : 1], rw1[RR > 0 ? RR : 1],
-        rw2[RR > 0 ? RR : 1], rcs[RR > 0 ? RR : 1], rsn[RR > 0 ? RR : 1];
-    float rc1[RR > 0 ? RR : 1], rc2[RR > 0 ? RR : 1];
+    // Fused form, in fused_rope_kv_decode's layout (lane i holds channels i and i + 64): every
+    // wave norms and rotates both query heads itself and moves them to the decode layout
+    // through its own LDS rows (no workgroup barrier); the last wave of the last piece also
+    // quantizes the new K and V rows (rk1.. below) for the cache and for its own use.
+    uint16_t rq1[2], rq2[2], rqw1 = 0, rqw2 = 0, rcs = 0, rsn = 0;
+    uint16_t rk1 = 0, rk2 = 0, rkw1 = 0, rkw2 = 0, rv1 = 0, rv2 = 0;
+    float rc1 = 0.f, rc2 = 0.f;
+    const bool kv_wave = last && wave == WAVES - 1;
     if constexpr (ROPE) {
         const float* cal =
             a.c.k_calibration + slot * a.c.cal_stride_slot + hk * a.c.cal_stride_head;
 #pragma unroll
-        for (int i = 0; i < RR; ++i) {
-            const int r = wave + i * WAVES;
-            if (r < nrows) {
-                const uint16_t* src = r < 2   ? a.q + b * a.q_sb + (2 * hk + r) * a.q_sh
-                                      : r == 2 ? a.k_new + b * a.k_sb + hk * a.k_sh
-                                               : a.v_new + b * a.v_sb + hk * a.v_sh;
-                rx1[i] = src[lane];
-                rx2[i] = src[lane + 64];
-                if (r < 3) {
-                    const uint16_t* w = r < 2 ? a.q_norm : a.k_norm;
-                    rw1[i] = w[lane];
-                    rw2[i] = w[lane + 64];
-                    rcs[i] = a.cos[b * a.cos_sb + lane];
-                    rsn[i] = a.sin[b * a.sin_sb + lane];
-                    rc1[i] = cal[lane];
-                    rc2[i] = cal[lane + 64];
-                }
-            }
+        for (int h = 0; h < 2; ++h) {
+            const uint16_t* src = a.q + b * a.q_sb + (2 * hk + h) * a.q_sh;
+            rq1[h] = src[lane];
+            rq2[h] = src[lane + 64];
+        }
+        rqw1 = a.q_norm[lane];
+        rqw2 = a.q_norm[lane + 64];
+        rcs = a.cos[b * a.cos_sb + lane];
+        rsn = a.sin[b * a.sin_sb + lane];
+        rc1 = cal[lane];
+        rc2 = cal[lane + 64];
+        if (kv_wave) {
+            const uint16_t* kp = a.k_new + b * a.k_sb + hk * a.k_sh;
+            const uint16_t* vp = a.v_new + b * a.v_sb + hk * a.v_sh;
+            rk1 = kp[lane];
+            rk2 = kp[lane + 64];
+            rkw1 = a.k_norm[lane];
+            rkw2 = a.k_norm[lane + 64];
+            rv1 = vp[lane];
+            rv2 = vp[lane + 64];
         }
     } else {
 #pragma unroll
@@ -420,51 +422,58 @@ __attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_attenti
     load_block(kr, rk, rks, t0 + 4 * g, cc);
     load_block(vr, rv, rvs, t0 + 4 * g, cc);
     __builtin_amdgcn_sched_barrier(0);
-    __shared__ __attribute__((aligned(16))) uint16_t s_q[ROPE ? 2 : 1][DA_D];
-    __shared__ __attribute__((aligned(16))) int8_t s_new[ROPE ? 2 : 1][DA_D];
+    __shared__ __attribute__((aligned(16))) uint16_t s_q[ROPE ? WAVES : 1][2][DA_D];
+    __shared__ __attribute__((aligned(16))) int8_t s_new[2][DA_D];
     __shared__ float s_new_scale[2];
     if constexpr (ROPE) {
         // fused_rope_kv_decode's arithmetic (the same device functions): RMSNorm and RoPE, q
         // times the calibration rounded to bf16, K divided by the calibration, K and V
         // quantized; the new row goes to the cache at column n_end - 1 and, with its scales,
-        // to LDS for the last piece's own use
-        const int64_t col = n_end - 1;
-        const int64_t base = slot * a.c.stride_slot + hk * a.c.stride_head + col * a.c.stride_tok;
-        const int64_t sidx = slot * a.c.scale_stride_slot + hk * a.c.scale_stride_head + col;
-#pragma unroll
-        for (int i = 0; i < RR; ++i) {
-            const int r = wave + i * WAVES;
-            if (r >= nrows) continue;
-            int32_t q1, q2;
-            float sq;
-            if (r == 3) {
-                sq = quantize_row_wave(bf16_to_f32(rx1[i]), bf16_to_f32(rx2[i]), q1, q2);
-            } else {
-                float o1, o2;
-                norm_rope_row(bf16_to_f32(rx1[i]), bf16_to_f32(rx2[i]), bf16_to_f32(rw1[i]),
-                              bf16_to_f32(rw2[i]), bf16_to_f32(rcs[i]), bf16_to_f32(rsn[i]),
-                              a.eps, o1, o2);
-                if (r < 2) {
-                    s_q[r][lane] = (uint16_t)f32_to_bf16_rne(o1 * rc1[i]);
-                    s_q[r][lane + 64] = (uint16_t)f32_to_bf16_rne(o2 * rc2[i]);
-                    continue;
-                }
-                sq = quantize_row_wave(o1 / rc1[i], o2 / rc2[i], q1, q2);
-            }
-            int8_t* dst = r == 2 ? a.c.k : a.c.v;
-            float* dscale = r == 2 ? a.c.k_scale : a.c.v_scale;
-            dst[base + lane] = (int8_t)q1;
-            dst[base + lane + 64] = (int8_t)q2;
-            if (lane == 0) dscale[sidx] = sq;
-            s_new[r - 2][lane] = (int8_t)q1;
-            s_new[r - 2][lane + 64] = (int8_t)q2;
-            if (lane == 0) s_new_scale[r - 2] = sq;
-        }
-        __syncthreads();
+        // to LDS for the last wave's own use
+        const float cs = bf16_to_f32(rcs), sn = bf16_to_f32(rsn);
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            qraw[h][0] = *reinterpret_cast<const uint4*>(&s_q[h][16 * cc]);
-            qraw[h][1] = *reinterpret_cast<const uint4*>(&s_q[h][16 * cc + 8]);
+            float o1, o2;
+            norm_rope_row(bf16_to_f32(rq1[h]), bf16_to_f32(rq2[h]), bf16_to_f32(rqw1),
+                          bf16_to_f32(rqw2), cs, sn, a.eps, o1, o2);
+            s_q[wave][h][lane] = (uint16_t)f32_to_bf16_rne(o1 * rc1);
+            s_q[wave][h][lane + 64] = (uint16_t)f32_to_bf16_rne(o2 * rc2);
+        }
+        if (kv_wave) {
+            const int64_t col = n_end - 1;
+            const int64_t base =
+                slot * a.c.stride_slot + hk * a.c.stride_head + col * a.c.stride_tok;
+            const int64_t sidx = slot * a.c.scale_stride_slot + hk * a.c.scale_stride_head + col;
+            float o1, o2;
+            norm_rope_row(bf16_to_f32(rk1), bf16_to_f32(rk2), bf16_to_f32(rkw1),
+                          bf16_to_f32(rkw2), cs, sn, a.eps, o1, o2);
+            int32_t q1, q2;
+            const float sk = quantize_row_wave(o1 / rc1, o2 / rc2, q1, q2);
+            a.c.k[base + lane] = (int8_t)q1;
+            a.c.k[base + lane + 64] = (int8_t)q2;
+            s_new[0][lane] = (int8_t)q1;
+            s_new[0][lane + 64] = (int8_t)q2;
+            const float sv = quantize_row_wave(bf16_to_f32(rv1), bf16_to_f32(rv2), q1, q2);
+            a.c.v[base + lane] = (int8_t)q1;
+            a.c.v[base + lane + 64] = (int8_t)q2;
+            s_new[1][lane] = (int8_t)q1;
+            s_new[1][lane + 64] = (int8_t)q2;
+            if (lane == 0) {
+                a.c.k_scale[sidx] = sk;
+                a.c.v_scale[sidx] = sv;
+                s_new_scale[0] = sk;
+                s_new_scale[1] = sv;
+            }
+        }
+        // the wave's own LDS rows: its writes are visible to its later reads once the LDS
+        // operations are ordered within the wave
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            qraw[h][0] = *reinterpret_cast<const uint4*>(&s_q[wave][h][16 * cc]);
+            qraw[h][1] = *reinterpret_cast<const uint4*>(&s_q[wave][h][16 * cc + 8]);
         }
     }
 #pragma unroll
@@ -534,7 +543,7 @@ __attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_attenti
         block_scores<true>(s, kr, qh, qoff, t0 + 4 * gm, t_end);
         block_pv(st, s, vr, kmul);
     }
-    if (ROPE && last && wave == WAVES - 1) {
+    if (ROPE && kv_wave) {
         // the new token, as a block whose other tokens are masked: lane group 0 holds its row
         KVRegs kn, vn;
 #pragma unroll
@@ -543,7 +552,7 @@ __attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_attenti
         if (gm == 0) {
             const int cm = tid_m & 7;
             kn.x[0] = *reinterpret_cast<const v4u*>(&s_new[0][16 * cm]);
-            vn.x[0] = *reinterpret_cast<const v4u*>(&s_new[ROPE ? 1 : 0][16 * cm]);
+            vn.x[0] = *reinterpret_cast<const v4u*>(&s_new[1][16 * cm]);
             kn.scale[0] = __float_as_uint(s_new_scale[0]);
             vn.scale[0] = __float_as_uint(s_new_scale[1]);
         }
