@@ -359,7 +359,7 @@ __device__ Loc schedule(const PrefillArgs& a, int target, int* tables) {
         straddle_fits = launch_sum([](const SbInfo& z) { return z.npt + z.nct > 0 ? 1 : 0; }) *
                             a.hkv < a.grid;
     };
-    if (spare <= 0) straddle_check();
+    if (__builtin_expect(spare <= 0, 0)) straddle_check();
     Loc L;
     L.found = 0;
     L.straddle = 0;
@@ -389,8 +389,8 @@ __device__ Loc schedule(const PrefillArgs& a, int target, int* tables) {
     // which fits). It replaces the separate form when that is PF_STRADDLE_MARGIN tiles longer
     // (or does not split at all): a crossing piece pays a second loop prologue. Nothing of
     // this runs when even the lower bound cannot win by that margin.
-    if (spare > 0 && lo + PF_STRADDLE_MARGIN < L.T) straddle_check();
-    if (straddle_fits && lo + PF_STRADDLE_MARGIN < L.T) {
+    if (__builtin_expect(spare > 0 && lo + PF_STRADDLE_MARGIN < L.T, 0)) straddle_check();
+    if (__builtin_expect(straddle_fits && lo + PF_STRADDLE_MARGIN < L.T, 0)) {
         int hi = lo;
 #pragma unroll
         for (int c = 0; c < PF_SCHED_CHUNKS; ++c) hi = max(hi, zc[c].npt + zc[c].nct);
