@@ -494,6 +494,28 @@ def line_linear(args, ie, W, K, dev, alg_bytes, extra):
     log(f"linear config5 {extra['linear_config5']}")
 
 
+def line_launch_floor(args, ie, W, K, dev, alg_bytes, extra):
+    """What one small kernel costs inside a hipGraph: 56 dependent add_rms_norm calls at config
+    5's 32 x 2048 (a step's worth) against 56 one-element torch adds (a launch that does no
+    work), each captured in one graph and replayed. A profiler's kernel trace inflates such
+    kernels inside graph replays to about 4.5 us each, torch's own included."""
+    res = torch.randn(32, 2048, device=dev).bfloat16()
+    dl = torch.randn(32, 2048, device=dev).bfloat16()
+    w = torch.randn(2048, device=dev).bfloat16()
+    tiny = torch.zeros(1, device=dev)
+    state = {"r": res}
+
+    def rms():
+        state["r"], _ = K.add_rms_norm(state["r"], dl, w, 1e-6)
+
+    rms_ms = time_graph(rms, calls=56, reps=20)
+    add_ms = time_graph(lambda: tiny.add_(1.0), calls=56, reps=20)
+    extra["graph_launch_floor"] = {"add_rms_norm_us": round(rms_ms * 1e3, 2),
+                                   "torch_add_1elem_us": round(add_ms * 1e3, 2),
+                                   "calls_per_graph": 56, "rows": 32, "dim": 2048}
+    log(f"graph launch floor {extra['graph_launch_floor']}")
+
+
 def line_mixed_step(args, ie, W, K, dev, alg_bytes, extra):
     extra["mixed_step_config4"] = bench_mixed_step(W, dev)
     log(f"mixed step config4 {extra['mixed_step_config4']}")
@@ -525,7 +547,8 @@ def line_sweep(args, ie, W, K, dev, alg_bytes, extra):
 LINES = {"read_probe": line_read_probe, "kv_write": line_kv_write,
          "prefill_config4": line_prefill_config4, "prefill_long": line_prefill_long,
          "norm_rope": line_norm_rope, "sample": line_sample, "linear": line_linear,
-         "mixed_step": line_mixed_step, "step": line_step, "sweep": line_sweep}
+         "launch_floor": line_launch_floor, "mixed_step": line_mixed_step, "step": line_step,
+         "sweep": line_sweep}
 DEFAULT_LINES = [n for n in LINES if n != "sweep"]
 
 
