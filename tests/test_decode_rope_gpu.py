@@ -50,6 +50,7 @@ def _case(ie, lens, nd, seed, max_len):
     ([int(x) for x in np.random.default_rng(5).integers(128, 4096, 32)], 32),  # config 5
     ([4096] * 63 + [1], 64),                             # one piece per sequence, full target
     ([int(x) for x in np.random.default_rng(6).integers(1, 600, 300)], 297),  # 2-wave launch
+    ([int(x) for x in np.random.default_rng(7).integers(1, 1500, 100)], 100),  # 4-wave launch
 ])
 def test_decode_attention_rope(ie, dev, lens, nd):
     say(f"decode_attention_rope B={len(lens)} nd={nd} max ctx {max(lens)}")
