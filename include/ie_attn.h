@@ -188,8 +188,8 @@ hipError_t ie_decode_attention(const ie_bf16* q, int64_t q_stride_b, int64_t q_s
  * ie_fused_rope_kv_decode writes (int8 K and V and their scales at column cached_lens[b] of row
  * slot_ids[b]), and out[b] is decode attention with the q that ie_fused_rope_kv_decode would
  * return (its bits); q_out itself is not produced. Within the launch the piece of each sequence
- * that ends at the new token computes that token's K/V row, writes it to the cache and uses it
- * from registers; no other piece reads that column.
+ * that ends at the new token computes that token's K/V row, writes it to the cache and uses its
+ * own copy (in LDS); no piece reads that column from the cache.
  */
 hipError_t ie_decode_attention_rope(
     const ie_bf16* q, int64_t q_stride_b, int64_t q_stride_h, const ie_bf16* k,
