@@ -289,6 +289,24 @@ __device__ Loc schedule(const PrefillArgs& a, int target, int* tables) {
             if (e < a.nent) s_sl[e] = a.slot_ids[e];
         }
     }
+    // A workgroup past the slots has no item whenever the slots exceed the parts (a sub-block
+    // has a prefix part and a chunk part at most): the sub-blocks of tiles with work bound that
+    // from the tile starts alone, so such a workgroup (these start late, once resident ones
+    // finish) leaves before the entry lookups.
+    if (__builtin_expect(target >= a.grid && nchunks <= PF_SCHED_CHUNKS, 0)) {
+        int busy = 0;
+#pragma unroll
+        for (int c = 0; c < PF_SCHED_CHUNKS; ++c) busy += rs[c] >= 0 ? 1 : 0;
+        if (2 * uni(wave_sum_i(busy)) * a.hkv < a.grid) {
+            Loc L;
+            L.found = 0;
+            L.straddle = 0;
+            L.T = 0;
+            L.sb = L.off = L.item_base = 0;
+            L.s = SubBlock{};
+            return L;
+        }
+    }
     auto info = [&](int sb, int row_start) {
         SbInfo z = {0, 0, 0, 0, 0, 0, 0};
         if (row_start < 0) return z;
