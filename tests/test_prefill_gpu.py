@@ -133,3 +133,19 @@ def test_prefill_split_merge_fallback(ie, workloads, dev, monkeypatch, chunks):
     for i, f in enumerate(fall):
         assert torch.equal(f.view(torch.int16), coop.view(torch.int16)), f"fallback call {i}"
     assert torch.equal(again.view(torch.int16), coop.view(torch.int16))
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_prefill_random_steps(ie, workloads, dev, seed):
+    """Seeded random mixed steps (decoders, 1-4 chunks of 1-320 new tokens over 0-1,500 cached,
+    block_m 64 or 128): whichever of the unsplit, separate-split and straddling forms the launch
+    takes, and with workgroups past the slots, every prefill row matches the oracle."""
+    rng = np.random.default_rng(100 + seed)
+    decoders = [int(x) for x in rng.integers(1, 1500, int(rng.integers(0, 40)))]
+    chunks = [(int(rng.integers(1, 321)), 0 if rng.random() < 0.3 else int(rng.integers(1, 1501)))
+              for _ in range(int(rng.integers(1, 5)))]
+    block_m = int(rng.choice([64, 128]))
+    say(f"prefill random step seed {seed}: {len(decoders)} decoders, chunks {chunks}, "
+        f"block_m {block_m}")
+    wl = workloads.mixed_workload(decoders, chunks, seed=seed, block_m=block_m, max_len=2048)
+    check(ie, workloads, wl, dev, f"prefill random step {seed}")
