@@ -54,6 +54,22 @@ def _case(ie, lens, nd, seed, max_len):
 ])
 def test_decode_attention_rope(ie, dev, lens, nd):
     say(f"decode_attention_rope B={len(lens)} nd={nd} max ctx {max(lens)}")
+    check_rope(ie, dev, lens, nd)
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_decode_attention_rope_random(ie, dev, seed):
+    """Seeded random batches across the three launch shapes (8-, 4- and 2-wave workgroups):
+    1-300 sequences of 1-1,500 tokens, padding rows after num_decoding."""
+    rng = np.random.default_rng(200 + seed)
+    B = int((rng.integers(1, 65), rng.integers(65, 129), rng.integers(129, 301))[seed % 3])
+    lens = [int(x) for x in rng.integers(1, 1501, B)]
+    nd = int(rng.integers(max(1, B - 5), B + 1))
+    say(f"decode_attention_rope random seed {seed}: B={B} nd={nd} max ctx {max(lens)}")
+    check_rope(ie, dev, lens, nd)
+
+
+def check_rope(ie, dev, lens, nd):
     max_len = -(-max(lens) // 64) * 64
     cs = _case(ie, lens, nd, seed=len(lens), max_len=max_len)
     dv = {n: t.to(dev) for n, t in cs.items() if isinstance(t, torch.Tensor)}
