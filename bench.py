@@ -641,11 +641,26 @@ def prefill_phase_stamps(W, dev, warmup):
             steps[f"{names[a]}->{names[b]}"] = {"p50_us": round(float(np.median(d)), 2),
                                                 "p90_us": round(float(np.percentile(d, 90)), 2)}
     pieces = calls[0][:, 8]
+    # workgroup w runs on XCD w mod 8: start and end of the workgroups with work, per XCD
+    by_xcd = {}
+    for x in range(8):
+        st, en = [], []
+        for t in calls:
+            ids = np.arange(len(t))
+            sel = (ids % 8 == x) & (t[:, 8] > 0) & (t[:, 7] > 0)
+            st.append((t[sel, 0] - t[:, 0].min()) * 0.01)
+            en.append((t[sel, 7] - t[:, 0].min()) * 0.01)
+        st, en = np.concatenate(st), np.concatenate(en)
+        if len(st):
+            by_xcd[str(x)] = {"start_p50_us": round(float(np.median(st)), 2),
+                              "end_p50_us": round(float(np.median(en)), 2),
+                              "end_max_us": round(float(en.max()), 2)}
     return {"workload": "prefill_attention config 4 (phase-stamp build)",
             "call_us_last_end": round(float(np.median([(t[:, 7].max() - t[:, 0].min()) * 0.01
                                                        for t in calls])), 2),
             "workgroups_with_work": int((pieces > 0).sum()),
-            "split_pieces": int((pieces > 1).sum()), "phases": res, "steps": steps}
+            "split_pieces": int((pieces > 1).sum()), "phases": res, "steps": steps,
+            "by_xcd": by_xcd}
 
 
 def main():
