@@ -289,9 +289,10 @@ __device__ Loc schedule(const PrefillArgs& a, int target, int* tables) {
             if (e < a.nent) s_sl[e] = a.slot_ids[e];
         }
     }
-    // A workgroup past the slots has no item whenever the slots exceed the parts (a sub-block
-    // has a prefix part and a chunk part at most): the sub-blocks of tiles with work bound that
-    // from the tile starts alone, so such a workgroup (these start late, once resident ones
+    // A workgroup past the slots has no item whenever the slots exceed parts x Hkv (the pairs
+    // are then split and every item is numbered below the slots, see below). A sub-block has at
+    // most a prefix part and a chunk part, so twice the sub-blocks of tiles with work bound the
+    // parts from the tile starts alone: such a workgroup (these start late, once resident ones
     // finish) leaves before the entry lookups.
     if (__builtin_expect(target >= a.grid && nchunks <= PF_SCHED_CHUNKS, 0)) {
         int busy = 0;
