@@ -142,6 +142,15 @@ hipError_t ie_fused_rope_kv_decode(const ie_bf16* q, int64_t q_stride_b, int64_t
  */
 size_t ie_decode_attention_workspace_size(int32_t batch, int32_t num_q_heads, int32_t head_dim);
 
+/*
+ * The leading bytes of a decode workspace for `batch` sequences that must be zero on entry (the
+ * arrival counts: max(batch, 1024) * num_kv_heads uint32, padded to 256 bytes). Zeroing them
+ * resets a workspace, e.g. one whose memory was reused or a launch that did not complete, and
+ * a caller that records the decode call into a hipGraph from freshly allocated memory records
+ * a fill of these bytes first. No counterpart in the reference (its partials need no counts).
+ */
+size_t ie_decode_attention_workspace_counts_bytes(int32_t batch, int32_t num_kv_heads);
+
 /* Upper bound on splits per sequence on the current device: the largest per-KV-head workgroup
  * target of any launch shape (CUs * 8 / num_kv_heads, 2-wave workgroups). */
 int32_t ie_decode_attention_max_splits(int32_t num_kv_heads);
@@ -298,6 +307,10 @@ hipError_t ie_dequantize_kv_prefix(const ie_kv_cache* cache, const int32_t* cu_c
  */
 size_t ie_prefill_attention_workspace_size(int32_t num_tiles, int32_t block_m,
                                            int32_t num_kv_heads);
+/* The leading bytes of a prefill workspace that must be zero on entry (the arrival and finish
+ * words, two uint32 per resident workgroup, padded to 256 bytes); as for
+ * ie_decode_attention_workspace_counts_bytes. No counterpart in the reference. */
+size_t ie_prefill_attention_workspace_counts_bytes(void);
 hipError_t ie_prefill_attention(const ie_bf16* q, int64_t q_stride_tok, int64_t q_stride_head,
                                 const ie_bf16* k, int64_t k_stride_tok, int64_t k_stride_head,
                                 const ie_bf16* v, int64_t v_stride_tok, int64_t v_stride_head,
@@ -309,6 +322,27 @@ hipError_t ie_prefill_attention(const ie_bf16* q, int64_t q_stride_tok, int64_t 
                                 int64_t out_stride_tok,
                                 int64_t out_stride_head, void* workspace, size_t workspace_bytes,
                                 hipStream_t stream);
+
+/*
+ * The prefill launch's work list, for tests and diagnostics (no counterpart in the reference,
+ * whose prefill grid is one program per (tile, query head), kernels.py:1146-1150):
+ * ie_prefill_attention_grid(num_tiles, block_m, num_kv_heads) is the launch's workgroup count,
+ * and ie_prefill_attention_plan writes, for each workgroup w, 16 int32 at rows[16 w]:
+ *   found, sub-block, kv head, piece, pieces of its (sub-block, kv head) pair, first tile,
+ *   end tile, prefix tiles, chunk tiles, first row, end row, the entry's first row, prefix
+ *   length, tiles per piece, straddling form (1) or separate prefix/chunk pieces (0), the
+ *   pair's first item
+ * where sub-blocks are 128-row slices of the tiles, tile t < prefix tiles is the prefix's
+ * 64-key tile t and later tiles are the chunk's 64-key tiles, and a workgroup without work has
+ * an all-zero row. Same index arguments as ie_prefill_attention; rows: int32 [grid, 16]
+ * device memory.
+ */
+int32_t ie_prefill_attention_grid(int32_t num_tiles, int32_t block_m, int32_t num_kv_heads);
+hipError_t ie_prefill_attention_plan(const int32_t* seq_ids, const int32_t* cu_seqlens,
+                                     const int32_t* tile_start, int32_t num_tiles,
+                                     int32_t block_m, int64_t num_tokens, int32_t num_kv_heads,
+                                     const int32_t* slot_ids, const int32_t* cu_cached,
+                                     int32_t num_entries, int32_t* rows, hipStream_t stream);
 
 /*
  * Token sampling: Gumbel-max over the vocabulary, greedy argmax at tau = 0.

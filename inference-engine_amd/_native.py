@@ -52,6 +52,12 @@ def cabi() -> ctypes.CDLL:
         _cabi.ie_decode_attention_max_splits.argtypes = [ctypes.c_int32]
         _cabi.ie_decode_attention_target.restype = ctypes.c_int32
         _cabi.ie_decode_attention_target.argtypes = [ctypes.c_int32, ctypes.c_int32]
+        _cabi.ie_decode_attention_workspace_counts_bytes.restype = ctypes.c_size_t
+        _cabi.ie_decode_attention_workspace_counts_bytes.argtypes = [ctypes.c_int32] * 2
+        _cabi.ie_prefill_attention_workspace_counts_bytes.restype = ctypes.c_size_t
+        _cabi.ie_prefill_attention_workspace_counts_bytes.argtypes = []
+        _cabi.ie_prefill_attention_grid.restype = ctypes.c_int32
+        _cabi.ie_prefill_attention_grid.argtypes = [ctypes.c_int32] * 3
     return _cabi
 
 

@@ -27,6 +27,7 @@ from dataclasses import dataclass
 from typing import Callable
 
 import torch
+from torch.cuda import nvtx
 
 from .kernels import (LayerKVCache, decode_attention_rope, fused_norm_rope_prefill, linear,
                       prefill_attention, quantize_kv_prefill)
@@ -67,19 +68,28 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, seq_ids, cu_seq
     attention."""
     D = q.shape[-1]
     if cu_seqlens is None:
-        return decode_attention_rope(q, k, v, q_norm_weight, k_norm_weight, cos, sin, slot_ids,
-                                     kv_cache, cached_lens, num_decoding, eps, D ** -0.5)
+        # the reference's "rope_kv_write" and "decode_attention" ranges (architecture.py:100,
+        # 115), one launch here
+        with nvtx.range("rope_kv_write+decode_attention"):
+            return decode_attention_rope(q, k, v, q_norm_weight, k_norm_weight, cos, sin,
+                                         slot_ids, kv_cache, cached_lens, num_decoding, eps,
+                                         D ** -0.5)
     assert seq_ids is not None and tile_start is not None and prefix_scratch is not None
     # every kernel sees the whole packet and skips the entries that are not its own, so nothing
     # here depends on how many entries decode; the decode rows are normed and roped here too
     # (unused: the decode kernel below does its own)
-    q_p, k_p = fused_norm_rope_prefill(q, k, q_norm_weight, k_norm_weight, cos, sin, eps)
-    quantize_kv_prefill(k_p, v, cu_seqlens, slot_ids, cached_lens, num_decoding, kv_cache)
-    out = prefill_attention(q_p, k_p, v, seq_ids, cu_seqlens, tile_start, kv_cache, slot_ids,
-                            prefix_scratch.cu_cached, prefill_block_m)
+    with nvtx.range("norm_rope_prefill"):
+        q_p, k_p = fused_norm_rope_prefill(q, k, q_norm_weight, k_norm_weight, cos, sin, eps)
+    with nvtx.range("kv_write"):
+        quantize_kv_prefill(k_p, v, cu_seqlens, slot_ids, cached_lens, num_decoding, kv_cache)
+    with nvtx.range("prefill_attention"):
+        out = prefill_attention(q_p, k_p, v, seq_ids, cu_seqlens, tile_start, kv_cache,
+                                slot_ids, prefix_scratch.cu_cached, prefill_block_m)
     B = slot_ids.shape[0]  # from a shape, not from how many entries decode
-    decode_attention_rope(q[:B], k[:B], v[:B], q_norm_weight, k_norm_weight, cos[:B], sin[:B],
-                          slot_ids, kv_cache, cached_lens, num_decoding, eps, D ** -0.5, out=out)
+    with nvtx.range("rope_kv_write+decode_attention"):
+        decode_attention_rope(q[:B], k[:B], v[:B], q_norm_weight, k_norm_weight, cos[:B],
+                              sin[:B], slot_ids, kv_cache, cached_lens, num_decoding, eps,
+                              D ** -0.5, out=out)
     return out
 
 
@@ -101,12 +111,14 @@ class AttentionLayer:
                 num_decoding) -> torch.Tensor:
         N = x.shape[0]
         D, hq, hkv = self.head_dim, self.num_q_heads, self.num_kv_heads
-        q, k, v = linear(x, self.qkv).split([D * hq, D * hkv, D * hkv], dim=-1)
+        with nvtx.range("qkv_proj"):
+            q, k, v = linear(x, self.qkv).split([D * hq, D * hkv, D * hkv], dim=-1)
         out = attention(q.view(N, hq, D), k.view(N, hkv, D), v.view(N, hkv, D), seq_ids,
                         cu_seqlens, cos, sin, kv_cache, cached_lens, slot_ids, tile_start,
                         prefill_block_m, prefix_scratch, num_decoding, self.q_norm, self.k_norm,
                         self.eps)
-        return linear(out.view(N, -1), self.o_proj)
+        with nvtx.range("o_proj"):
+            return linear(out.view(N, -1), self.o_proj)
 
     __call__ = forward
 

@@ -760,6 +760,12 @@ static Layout workspace_layout(int batch, int hq, int hkv) {
 
 using namespace ie;
 
+extern "C" size_t ie_decode_attention_workspace_counts_bytes(int32_t batch,
+                                                             int32_t num_kv_heads) {
+    if (num_kv_heads <= 0) return 0;
+    return workspace_layout(batch, 2 * num_kv_heads, num_kv_heads).acc_off;
+}
+
 extern "C" int32_t ie_decode_attention_max_splits(int32_t num_kv_heads) {
     return decode_target(num_kv_heads, 2);  // the largest target of any launch shape
 }

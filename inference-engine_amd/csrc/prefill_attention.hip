@@ -164,7 +164,8 @@ struct PrefillArgs {
     float* part_ml;    // [slot][2 heads][PF_BM rows][2]: their (m, l)
     uint32_t* arrivals;  // [2][grid]: arrival and finish words of each split (sub-block, kv
                          // head) pair, at the pair's first item; 0 between launches
-    uint64_t merge_wait_ticks;  // longest wait of a piece for its pair's others (100 MHz clock)
+    uint64_t merge_wait_ticks;   // longest wait of a piece for its pair's others (100 MHz clock)
+    uint64_t merge_stall_ticks;  // ... and longest wait with no other piece arriving
     int block_m, sub_per_tile, hq, hkv;
     int nent;  // entries (length of slot_ids; cu_seqlens and cu_cached hold nent + 1)
     int ntok;  // packed rows (length of seq_ids)
@@ -872,12 +873,13 @@ __device__ __forceinline__ void load_q(bf16x8 (&qf)[2][4], const PrefillArgs& a,
 __device__ __forceinline__ void merge_pieces(const PrefillArgs& a, const SubBlock& s, int hk,
                                              int item_base);
 
-// One work item: tiles [kt_begin, kt_end) of piece `piece` of sub-block s for kv head hk.
-__device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBlock& s, int hk,
-                                             int piece, int item, int item_base, PfLds& lds) {
-    // tiles [kt_begin, kt_end): the whole pair, a prefix piece, a chunk piece, or in the
-    // straddling form an even share of all the pair's tiles
-    int kt_begin = 0, kt_end = s.ntiles;
+// Tiles [kt_begin, kt_end) of piece `piece` of sub-block s (tile kt < npt: prefix tile kt,
+// else chunk tile kt - npt): the whole pair, a prefix piece, a chunk piece, or in the
+// straddling form an even share of all the pair's tiles.
+__device__ __forceinline__ void piece_tiles(const SubBlock& s, int piece, int& kt_begin,
+                                            int& kt_end) {
+    kt_begin = 0;
+    kt_end = s.ntiles;
     if (s.npieces > 1 && s.npp < 0) {
         kt_begin = piece * s.ntiles / s.npieces;
         kt_end = (piece + 1) * s.ntiles / s.npieces;
@@ -886,6 +888,13 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBloc
         kt_begin = q < 0 ? piece * s.npt / s.npp : s.npt + q * s.nct / nc;
         kt_end = q < 0 ? (piece + 1) * s.npt / s.npp : s.npt + (q + 1) * s.nct / nc;
     }
+}
+
+// One work item: tiles [kt_begin, kt_end) of piece `piece` of sub-block s for kv head hk.
+__device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBlock& s, int hk,
+                                             int piece, int item, int item_base, PfLds& lds) {
+    int kt_begin, kt_end;
+    piece_tiles(s, piece, kt_begin, kt_end);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -1129,16 +1138,20 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBloc
 // (row, query head) outputs are cut into npieces shares, and the merge of share k (log-sum-exp
 // in base 2, pieces in order) reads share k's rows of every piece's partial:
 //  * each piece counts itself in at arrivals[item_base + hk] (its arrival index k), then waits
-//    until all pieces have arrived, for at most a.merge_wait_ticks of the 100 MHz real-time
-//    clock, and merges share k; the last to arrive merges its share at once. The wait spreads
-//    the merge over the pair's workgroups (one workgroup alone reads device-coherent data at a
-//    fraction of the rate the pair's pieces reach together);
+//    until all pieces have arrived, and merges share k; the last to arrive merges its share at
+//    once. The wait ends early when no other piece has arrived for a.merge_stall_ticks (the
+//    missing ones may not be resident yet, e.g. on a GPU shared with other work) and after
+//    a.merge_wait_ticks in all (100 MHz real-time clock). The wait spreads the merge over the
+//    pair's workgroups (one workgroup alone reads device-coherent data at a fraction of the
+//    rate the pair's pieces reach together);
 //  * each then adds (1 << 16) | (merged ? 1 << k : 0) to the pair's finish word
 //    (arrivals[grid + item_base + hk]); the last to finish merges every share whose owner gave
 //    up waiting (none, unless a piece ran long after the others) and resets both words to zero.
 // Every wait ends; a piece that gives up costs time, not correctness. The pair's words sit at
 // its first item: split items are numbered below the slot count and no other pair's first item
-// is that one.
+// is that one. The words must be zero on entry (the workspace contract). Should they not be,
+// an arrival index k >= npieces takes no share and sets no bit, so every access stays inside
+// the pair's rows; the pair's output is then not merged by this launch.
 __device__ __forceinline__ void merge_pieces(const PrefillArgs& a, const SubBlock& s, int hk,
                                              int item_base) {
     const int np = s.npieces, nrows = s.r1 - s.r0;
@@ -1148,22 +1161,31 @@ __device__ __forceinline__ void merge_pieces(const PrefillArgs& a, const SubBloc
     wait_stores();  // this wave's partial is written
     __syncthreads();
     if (threadIdx.x == 0) {
-        const int k = (int)__hip_atomic_fetch_add(arr, 1u, __ATOMIC_RELAXED,
+        const uint32_t k = __hip_atomic_fetch_add(arr, 1u, __ATOMIC_RELAXED,
                                                   __HIP_MEMORY_SCOPE_AGENT);
         PF_STAMP(4);
-        int go = k == np - 1;
-        if (!go) {
+        int go = k == (uint32_t)(np - 1);
+        if (k < (uint32_t)(np - 1)) {
             const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+            uint64_t t_seen = t0;
+            uint32_t seen = k + 1;
             for (;;) {
-                if ((int)__hip_atomic_load(arr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= np) {
+                const uint32_t c =
+                    __hip_atomic_load(arr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (c >= (uint32_t)np) {
                     go = 1;
                     break;
                 }
-                if (__builtin_amdgcn_s_memrealtime() - t0 > a.merge_wait_ticks) break;
+                const uint64_t t = __builtin_amdgcn_s_memrealtime();
+                if (c != seen) {
+                    seen = c;
+                    t_seen = t;
+                }
+                if (t - t0 > a.merge_wait_ticks || t - t_seen > a.merge_stall_ticks) break;
                 __builtin_amdgcn_s_sleep(2);
             }
         }
-        s_k = k;
+        s_k = (int)min(k, (uint32_t)PF_MAXP);
         s_go = go;
         PF_STAMP(5);
     }
@@ -1244,10 +1266,10 @@ __device__ __forceinline__ void merge_pieces(const PrefillArgs& a, const SubBloc
             }
         }
     };
-    if (go) merge_share(k);
+    if (go) merge_share(k);  // go only when k < np
     PF_STAMP(6);
     if (threadIdx.x == 0) {
-        const uint32_t mine = (1u << 16) | (go ? 1u << k : 0u);
+        const uint32_t mine = (1u << 16) | (go ? 1u << k : 0u);  // k < np <= PF_MAXP < 16
         const uint32_t old =
             __hip_atomic_fetch_add(fin, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         int missing = -1;  // not the last to finish
@@ -1288,13 +1310,43 @@ __global__ __launch_bounds__(PF_THREADS, IE_PREFILL_WG_PER_CU) void prefill_atte
     prefill_item(a, loc.s, loc.off % a.hkv, loc.off / a.hkv, blockIdx.x, loc.item_base, lds);
 }
 
+// grid (the prefill launch's grid), block 64: the launch's work list, as the main kernel's own
+// schedule computes it, one row of 16 int32 per workgroup index w:
+//   found, sub-block, kv head, piece, pieces of the pair, first tile, end tile, prefix tiles,
+//   chunk tiles, first row, end row, entry's first row, prefix length, tiles per piece T,
+//   straddling form, the pair's first item
+// (tile kt < prefix tiles is prefix tile kt, else chunk tile kt - prefix tiles; rows of a
+// workgroup with no item are zero).
+__global__ __launch_bounds__(IE_WAVE) void prefill_plan_kernel(PrefillArgs a, int32_t* rows) {
+    __shared__ int tables[3 * PF_LDS_ENTRIES + 2];
+    Loc loc = schedule(a, blockIdx.x, tables);
+    {
+        int* f = reinterpret_cast<int*>(&loc);
+#pragma unroll
+        for (int i = 0; i < (int)(sizeof(Loc) / sizeof(int)); ++i) f[i] = uni(f[i]);
+    }
+    if (threadIdx.x != 0) return;
+    int32_t r[16] = {};
+    if (loc.found) {
+        const int hk = loc.off % a.hkv, piece = loc.off / a.hkv;
+        int kb, ke;
+        piece_tiles(loc.s, piece, kb, ke);
+        const int v[16] = {1, loc.sb, hk, piece, loc.s.npieces, kb, ke, loc.s.npt, loc.s.nct,
+                           loc.s.r0, loc.s.r1, loc.s.seq_start, loc.s.P, loc.T, loc.straddle,
+                           loc.item_base};
+        for (int i = 0; i < 16; ++i) r[i] = v[i];
+    }
+    for (int i = 0; i < 16; ++i) rows[16 * blockIdx.x + i] = r[i];
+}
+
 // How long a split piece waits for its pair's other pieces before leaving its share of the
-// merge to the last one to finish, in ticks of the 100 MHz real-time clock: 100 us, or
-// IE_PREFILL_MERGE_WAIT_US (read at every call; 0 makes every piece but the last give up at
-// once, which tests the fallback).
-static uint64_t merge_wait_ticks() {
-    const char* e = std::getenv("IE_PREFILL_MERGE_WAIT_US");
-    const long us = e && *e ? std::strtol(e, nullptr, 10) : 100;
+// merge to the last one to finish, in ticks of the 100 MHz real-time clock: at most 100 us in
+// all (IE_PREFILL_MERGE_WAIT_US) and at most 20 us without another piece arriving
+// (IE_PREFILL_MERGE_STALL_US). Read at every call; a wait of 0 makes every piece but the last
+// give up at once, which tests the fallback.
+static uint64_t env_us_ticks(const char* name, long dflt) {
+    const char* e = std::getenv(name);
+    const long us = e && *e ? std::strtol(e, nullptr, 10) : dflt;
     return (uint64_t)std::max(0L, std::min(us, 10000000L)) * 100;
 }
 
@@ -1320,10 +1372,48 @@ static PrefillWs prefill_ws(int slots) {
 
 using namespace ie;
 
+// The launch's grid: one resident wave of workgroups, or one workgroup per (sub-block, kv head)
+// pair when there are more.
+static int64_t prefill_grid(int64_t nsb, int hkv) {
+    return std::max<int64_t>(prefill_slots(), nsb * hkv);
+}
+
+// The schedule's part of the arguments (index arrays and sizes).
+static hipError_t prefill_index_args(PrefillArgs& a, const int32_t* seq_ids,
+                                     const int32_t* cu_seqlens, const int32_t* tile_start,
+                                     int32_t num_tiles, int32_t block_m, int64_t num_tokens,
+                                     int32_t num_kv_heads, const int32_t* slot_ids,
+                                     const int32_t* cu_cached, int32_t num_entries) {
+    IE_REQUIRE(num_tokens >= 0 && num_tiles >= 0, "negative sizes");
+    IE_REQUIRE(block_m > 0, "block_m must be positive");
+    IE_REQUIRE(num_kv_heads > 0, "num_kv_heads must be positive");
+    IE_REQUIRE(num_entries >= 1, "num_entries (the length of slot_ids) must be at least 1");
+    const int64_t nsb = (int64_t)num_tiles * ((block_m + PF_BM - 1) / PF_BM);
+    IE_REQUIRE(nsb < (1 << 24), "too many tiles");
+    IE_REQUIRE(num_tokens < ((int64_t)1 << 31), "too many tokens");
+    a.seq_ids = seq_ids;
+    a.cu_seqlens = cu_seqlens;
+    a.tile_start = tile_start;
+    a.slot_ids = slot_ids;
+    a.cu_cached = cu_cached;
+    a.block_m = block_m;
+    a.sub_per_tile = (block_m + PF_BM - 1) / PF_BM;
+    a.hkv = num_kv_heads;
+    a.nent = num_entries;
+    a.ntok = (int)num_tokens;
+    a.nsb = (int)nsb;
+    a.grid = prefill_slots();
+    return hipSuccess;
+}
+
 extern "C" size_t ie_prefill_attention_workspace_size(int32_t num_tiles, int32_t block_m,
                                                       int32_t num_kv_heads) {
     if (num_tiles <= 0 || block_m <= 0 || num_kv_heads <= 0) return 0;
     return prefill_ws(prefill_slots()).bytes;
+}
+
+extern "C" size_t ie_prefill_attention_workspace_counts_bytes(void) {
+    return prefill_ws(prefill_slots()).ml_off;
 }
 
 extern "C" hipError_t ie_prefill_attention(
@@ -1337,10 +1427,11 @@ extern "C" hipError_t ie_prefill_attention(
     hipStream_t stream) {
     hipError_t e = check_cache(cache);
     if (e != hipSuccess) return e;
-    IE_REQUIRE(num_tokens >= 0 && num_tiles >= 0, "negative sizes");
-    IE_REQUIRE(block_m > 0, "block_m must be positive");
     IE_REQUIRE(num_q_heads == 2 * cache->num_kv_heads, "num_q_heads must be 2 * num_kv_heads");
-    IE_REQUIRE(num_entries >= 1, "num_entries (the length of slot_ids) must be at least 1");
+    PrefillArgs a{};
+    e = prefill_index_args(a, seq_ids, cu_seqlens, tile_start, num_tiles, block_m, num_tokens,
+                           (int32_t)cache->num_kv_heads, slot_ids, cu_cached, num_entries);
+    if (e != hipSuccess) return e;
     if (num_tokens == 0 || num_tiles == 0) return hipSuccess;
     IE_REQUIRE(q && k && v && seq_ids && cu_seqlens && tile_start && slot_ids && cu_cached && out,
                "null pointer");
@@ -1358,14 +1449,9 @@ extern "C" hipError_t ie_prefill_attention(
     IE_REQUIRE((reinterpret_cast<uintptr_t>(cache->k_calibration) & 15) == 0 &&
                    cache->cal_stride_head % 4 == 0 && cache->cal_stride_slot % 4 == 0,
                "k_calibration rows must be 16-byte aligned");
-    const int64_t nsb = (int64_t)num_tiles * ((block_m + PF_BM - 1) / PF_BM);
-    IE_REQUIRE(nsb < (1 << 24), "too many tiles");
-    const int slots = prefill_slots();
-    const PrefillWs wsl = prefill_ws(slots);
-    const size_t need = wsl.bytes;
-    IE_REQUIRE(workspace != nullptr && workspace_bytes >= need && al16(workspace),
+    const PrefillWs wsl = prefill_ws(a.grid);
+    IE_REQUIRE(workspace != nullptr && workspace_bytes >= wsl.bytes && al16(workspace),
                "workspace too small");
-    PrefillArgs a;
     a.q = (const uint16_t*)q;
     a.q_st = q_stride_tok;
     a.q_sh = q_stride_head;
@@ -1375,11 +1461,6 @@ extern "C" hipError_t ie_prefill_attention(
     a.v = (const uint16_t*)v;
     a.v_st = v_stride_tok;
     a.v_sh = v_stride_head;
-    a.seq_ids = seq_ids;
-    a.cu_seqlens = cu_seqlens;
-    a.tile_start = tile_start;
-    a.slot_ids = slot_ids;
-    a.cu_cached = cu_cached;
     a.c = *cache;
     a.out = (uint16_t*)out;
     a.o_st = out_stride_tok;
@@ -1387,18 +1468,37 @@ extern "C" hipError_t ie_prefill_attention(
     a.arrivals = (uint32_t*)workspace;
     a.part_ml = (float*)((char*)workspace + wsl.ml_off);
     a.part_o = (uint16_t*)((char*)workspace + wsl.o_off);
-    a.block_m = block_m;
-    a.sub_per_tile = (block_m + PF_BM - 1) / PF_BM;
     a.hq = num_q_heads;
-    a.hkv = cache->num_kv_heads;
-    a.nent = num_entries;
-    a.ntok = (int)num_tokens;
-    a.nsb = (int)nsb;
-    a.grid = slots;
     a.qk_scale = (float)(0.08838834764831845 * 1.4426950408889634);  // D^-0.5 * log2(e), D = 128
-    a.merge_wait_ticks = merge_wait_ticks();
-    const unsigned grid = (unsigned)std::max<int64_t>(slots, nsb * cache->num_kv_heads);
+    a.merge_wait_ticks = env_us_ticks("IE_PREFILL_MERGE_WAIT_US", 100);
+    a.merge_stall_ticks = env_us_ticks("IE_PREFILL_MERGE_STALL_US", 20);
+    const unsigned grid = (unsigned)prefill_grid(a.nsb, a.hkv);
     hipLaunchKernelGGL(prefill_attention_kernel, dim3(grid), dim3(PF_THREADS), 0, stream, a);
+    return hipGetLastError();
+}
+
+extern "C" int32_t ie_prefill_attention_grid(int32_t num_tiles, int32_t block_m,
+                                             int32_t num_kv_heads) {
+    if (num_tiles <= 0 || block_m <= 0 || num_kv_heads <= 0) return 0;
+    const int64_t nsb = (int64_t)num_tiles * ((block_m + PF_BM - 1) / PF_BM);
+    return (int32_t)std::min<int64_t>(prefill_grid(nsb, num_kv_heads), INT32_MAX);
+}
+
+extern "C" hipError_t ie_prefill_attention_plan(const int32_t* seq_ids, const int32_t* cu_seqlens,
+                                                const int32_t* tile_start, int32_t num_tiles,
+                                                int32_t block_m, int64_t num_tokens,
+                                                int32_t num_kv_heads, const int32_t* slot_ids,
+                                                const int32_t* cu_cached, int32_t num_entries,
+                                                int32_t* rows, hipStream_t stream) {
+    PrefillArgs a{};
+    hipError_t e = prefill_index_args(a, seq_ids, cu_seqlens, tile_start, num_tiles, block_m,
+                                      num_tokens, num_kv_heads, slot_ids, cu_cached, num_entries);
+    if (e != hipSuccess) return e;
+    if (num_tiles == 0) return hipSuccess;
+    IE_REQUIRE(seq_ids && cu_seqlens && tile_start && slot_ids && cu_cached && rows,
+               "null pointer");
+    const unsigned grid = (unsigned)prefill_grid(a.nsb, a.hkv);
+    hipLaunchKernelGGL(prefill_plan_kernel, dim3(grid), dim3(IE_WAVE), 0, stream, a, rows);
     return hipGetLastError();
 }
 

@@ -293,18 +293,56 @@ DecodeCall decode_prep(const at::Tensor& q, const at::Tensor& k_cache, const at:
 // buffers are kept too: a graph captured with one still addresses it. Calls in stream order
 // never overlap on a buffer. Kinds: prefill; decode of up to 1024 sequences (their count
 // regions coincide); decode of each larger batch size.
+//
+// Under hipGraph capture a call uses its stream's kept workspace when that stream has one (a
+// warm-up on the capture stream made it, outside the capture: the pattern of GraphSet and
+// DecodeStep). Otherwise (e.g. the engine's capture on torch's own capture stream after warming
+// up on another, qwen3-1.7b/engine.py:432-449) the workspace is allocated inside the capture,
+// from the graph's memory pool, and the graph records a fill of its count bytes before the
+// first call that uses it, so every replay starts from zero counts whatever the pool put in
+// that memory in between. Such a workspace serves the rest of the same capture; the reference
+// to it is dropped when the stream starts its next capture (the graph keeps using the memory).
+// A graph that uses a stream's kept workspace shares it with eager calls on that stream and
+// with the other graphs captured there: replay those graphs one at a time and not beside eager
+// calls on that stream, the rule torch already sets for graphs that share a memory pool.
 constexpr int32_t WS_PREFILL = -1;
-at::Tensor persistent_workspace(const at::Tensor& q, size_t bytes, int32_t kind) {
+at::Tensor persistent_workspace(const at::Tensor& q, size_t bytes, size_t count_bytes,
+                                int32_t kind) {
+    using Key = std::tuple<int, hipStream_t, int32_t>;
+    struct Captured {
+        unsigned long long id = 0;
+        std::map<int32_t, std::vector<at::Tensor>> held;
+    };
     static std::mutex mu;
-    static auto* cache =
-        new std::map<std::tuple<int, hipStream_t, int32_t>, std::vector<at::Tensor>>();  // kept
+    static auto* eager = new std::map<Key, std::vector<at::Tensor>>();  // kept for the process
+    static auto* captured = new std::map<std::pair<int, hipStream_t>, Captured>();
+    const hipStream_t s = stream_of(q);
+    const int dev = q.device().index();
+    hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+    unsigned long long id = 0;
+    ok(hipStreamGetCaptureInfo(s, &status, &id), "stream capture status");
+    const int64_t n = (int64_t)std::max<size_t>(bytes, 256);
     std::lock_guard<std::mutex> lock(mu);
-    auto& held = (*cache)[{q.device().index(), stream_of(q), kind}];
-    if (held.empty() || (size_t)held.back().numel() < bytes) {
-        const int64_t n = (int64_t)std::max<size_t>(bytes, 256);
-        held.push_back(at::zeros({n}, q.options().dtype(at::kByte)));
+    auto& held = (*eager)[Key{dev, s, kind}];
+    const bool fits = !held.empty() && held.back().numel() >= n;
+    if (status == hipStreamCaptureStatusNone) {
+        if (!fits) held.push_back(at::zeros({n}, q.options().dtype(at::kByte)));
+        return held.back();
     }
-    return held.back();
+    TORCH_CHECK(status == hipStreamCaptureStatusActive, "ie: the capture stream is invalidated");
+    if (fits) return held.back();
+    Captured& cap = (*captured)[{dev, s}];
+    if (cap.id != id) {  // a new capture on this stream: the previous one has ended
+        cap.id = id;
+        cap.held.clear();
+    }
+    auto& mine = cap.held[kind];
+    if (mine.empty() || mine.back().numel() < n) {
+        at::Tensor w = at::empty({n}, q.options().dtype(at::kByte));
+        w.narrow(0, 0, (int64_t)std::min<size_t>(count_bytes, (size_t)n)).zero_();  // recorded
+        mine.push_back(w);
+    }
+    return mine.back();
 }
 
 void decode_attention(const at::Tensor& q, const at::Tensor& k_cache, const at::Tensor& v_cache,
@@ -315,7 +353,9 @@ void decode_attention(const at::Tensor& q, const at::Tensor& k_cache, const at::
     const c10::DeviceGuard guard(q.device());
     DecodeCall d = decode_prep(q, k_cache, v_cache, k_scale, v_scale, k_calibration, cached_lens,
                                slot_ids, num_decoding, out);
-    at::Tensor ws = persistent_workspace(q, d.ws_bytes, d.B <= 1024 ? 0 : d.B);
+    at::Tensor ws = persistent_workspace(
+        q, d.ws_bytes, ie_decode_attention_workspace_counts_bytes(d.B, (int32_t)d.c.num_kv_heads),
+        d.B <= 1024 ? 0 : d.B);
     ok(ie_decode_attention(bf(q), q.stride(0), q.stride(1), d.B, d.hq, &d.c, i32(cached_lens),
                            i32(slot_ids), i32(num_decoding), (float)scale, bfm(out),
                            out.stride(0), out.stride(1), ws.data_ptr(), d.ws_bytes, stream_of(q)),
@@ -347,7 +387,9 @@ void decode_attention_rope(const at::Tensor& q, const at::Tensor& k, const at::T
                 "ie: k/v shape mismatch");
     TORCH_CHECK(cos.size(0) >= d.B && sin.size(0) >= d.B && cos.size(2) == 64 && sin.size(2) == 64,
                 "ie: cos/sin must be [B,1,64]");
-    at::Tensor ws = persistent_workspace(q, d.ws_bytes, d.B <= 1024 ? 0 : d.B);
+    at::Tensor ws = persistent_workspace(
+        q, d.ws_bytes, ie_decode_attention_workspace_counts_bytes(d.B, (int32_t)d.c.num_kv_heads),
+        d.B <= 1024 ? 0 : d.B);
     ok(ie_decode_attention_rope(bf(q), q.stride(0), q.stride(1), bf(k), k.stride(0), k.stride(1),
                                 bf(v), v.stride(0), v.stride(1), bf(q_norm_weight),
                                 bf(k_norm_weight), bf(cos), cos.stride(0), bf(sin),
@@ -406,7 +448,8 @@ at::Tensor prefill_attention(const at::Tensor& q, const at::Tensor& k, const at:
     at::Tensor out = at::empty({N, q.size(1), q.size(2)}, q.options());
     const size_t ws_bytes = ie_prefill_attention_workspace_size(
         (int32_t)tile_start.size(0), (int32_t)block_m, c.num_kv_heads);
-    at::Tensor ws = persistent_workspace(q, ws_bytes, WS_PREFILL);
+    at::Tensor ws = persistent_workspace(q, ws_bytes,
+                                         ie_prefill_attention_workspace_counts_bytes(), WS_PREFILL);
     ok(ie_prefill_attention(bf(q), q.stride(0), q.stride(1), bf(k), k.stride(0), k.stride(1),
                             bf(v), v.stride(0), v.stride(1), N, (int32_t)q.size(1), i32(seq_ids),
                             i32(cu_seqlens), i32(tile_start), (int32_t)tile_start.size(0),

@@ -22,6 +22,7 @@ from dataclasses import dataclass
 
 import torch
 import torch.nn.functional as F
+from torch.cuda import nvtx
 
 from .attention_layer import attention, rope_inv_freq, rope_tables
 from .kernels import (LayerKVCache, add_rms_norm, decode_attention_rope, linear, linear_silu_mul,
@@ -127,7 +128,8 @@ class DecodeStep:
         """AttentionLayer.forward, pure-decode branch (architecture.py:85-122), through
         attention_layer.attention."""
         s, lw, B = self.shape, self.layers[li], self.B
-        qkv = linear(normed, lw.qkv)
+        with nvtx.range("qkv_proj"):
+            qkv = linear(normed, lw.qkv)
         q, k, v = qkv.split([s.num_q_heads * s.head_dim, s.num_kv_heads * s.head_dim,
                              s.num_kv_heads * s.head_dim], dim=-1)
         q = q.view(B, s.num_q_heads, s.head_dim)
@@ -136,25 +138,35 @@ class DecodeStep:
         out = attention(q, k, v, None, None, cos, sin, self.caches[li], self.cached_lens,
                         self.slot_ids, None, 0, None, self.num_decoding, lw.q_norm, lw.k_norm,
                         s.eps)
-        return linear(out.view(B, -1), lw.o_proj)
+        with nvtx.range("o_proj"):
+            return linear(out.view(B, -1), lw.o_proj)
 
     def forward(self) -> torch.Tensor:
         """One step: returns the greedy next token of every sequence, int64 [B, 1]."""
-        cos, sin = self._rope()
-        x = F.embedding(self.ids, self.embed)
+        # the reference's ranges (architecture.py:278-304, 379-413, 477; engine.py:216)
+        with nvtx.range("embed"):
+            x = F.embedding(self.ids, self.embed)
+        with nvtx.range("metadata"):
+            cos, sin = self._rope()
         residual = None
         eps = self.shape.eps
         for li, lw in enumerate(self.layers):
-            if residual is None:  # architecture.py:280-281: the first block norms its input
-                residual, normed = x, self._rms(x, lw.input_norm)
-            else:
-                residual, normed = add_rms_norm(residual, x, lw.input_norm, eps)
-            attn = self.attention(li, normed, cos, sin)
-            residual, normed = add_rms_norm(residual, attn, lw.post_norm, eps)
-            x = linear(linear_silu_mul(normed, lw.gate_up), lw.down)
-        _, h = add_rms_norm(residual, x, self.final_norm, eps)
-        logits = linear(h, self.embed)
-        return sample(logits, 0.0, self.seed)
+            with nvtx.range("layer"):
+                with nvtx.range("attn"):
+                    if residual is None:  # architecture.py:280-281: the first block norms its input
+                        residual, normed = x, self._rms(x, lw.input_norm)
+                    else:
+                        residual, normed = add_rms_norm(residual, x, lw.input_norm, eps)
+                    attn = self.attention(li, normed, cos, sin)
+                with nvtx.range("mlp"):
+                    residual, normed = add_rms_norm(residual, attn, lw.post_norm, eps)
+                    x = linear(linear_silu_mul(normed, lw.gate_up), lw.down)
+        with nvtx.range("final_norm"):
+            _, h = add_rms_norm(residual, x, self.final_norm, eps)
+        with nvtx.range("lm_head"):
+            logits = linear(h, self.embed)
+        with nvtx.range("sample"):
+            return sample(logits, 0.0, self.seed)
 
     def attention_only(self) -> torch.Tensor:
         """The step's attention kernels alone (per layer: decode_attention_rope, i.e.

@@ -114,3 +114,37 @@ def test_quantize_too_many_tokens_rejected_on_host(native):
             ctypes.byref(desc), ctypes.c_void_p(0))
     assert rc == HIP_ERROR_INVALID_VALUE
     assert b"too many tokens" in lib.ie_attn_last_error()
+
+
+def test_workspace_count_regions_and_prefill_grid(native):
+    """The bytes a caller clears to reset a workspace: the decode arrival counts (max(B, 1024)
+    * Hkv uint32, padded to 256 bytes: the offset of the partials in the size formula above) and
+    the prefill arrival and finish words (two per resident workgroup, padded to 256 bytes, within
+    the prefill workspace). The prefill launch's grid: one resident wave of workgroups or one
+    workgroup per (128-row sub-block, KV head), whichever is more."""
+    lib = native.cabi()
+    for B in (1, 64, 1024, 1025, 3000):
+        want = -(-(max(B, 1024) * 8 * 4) // 256) * 256
+        assert lib.ie_decode_attention_workspace_counts_bytes(B, 8) == want
+    lib.ie_prefill_attention_workspace_size.restype = ctypes.c_size_t
+    ws = lib.ie_prefill_attention_workspace_size(ctypes.c_int32(8), ctypes.c_int32(128),
+                                                 ctypes.c_int32(8))
+    cb = lib.ie_prefill_attention_workspace_counts_bytes()
+    slots = lib.ie_prefill_attention_grid(1, 128, 8)  # one sub-block: the resident wave
+    assert cb == -(-(2 * slots * 4) // 256) * 256 and 0 < cb < ws
+    for tiles, bm in ((1, 128), (64, 128), (300, 128), (300, 192), (1000, 16)):
+        nsb = tiles * -(-bm // 128)
+        assert lib.ie_prefill_attention_grid(tiles, bm, 8) == max(slots, nsb * 8)
+
+
+def test_prefill_plan_rejects_bad_sizes_on_host(native):
+    lib = native.cabi()
+    fn = lib.ie_prefill_attention_plan
+    fn.restype = ctypes.c_int
+    p, null = ctypes.c_void_p(256), ctypes.c_void_p(0)
+    rc = fn(p, p, p, ctypes.c_int32(4), ctypes.c_int32(0), ctypes.c_int64(100), ctypes.c_int32(8),
+            p, p, ctypes.c_int32(3), p, null)
+    assert rc == HIP_ERROR_INVALID_VALUE and b"block_m" in lib.ie_attn_last_error()
+    rc = fn(p, p, p, ctypes.c_int32(4), ctypes.c_int32(128), ctypes.c_int64(100),
+            ctypes.c_int32(8), p, p, ctypes.c_int32(0), p, null)
+    assert rc == HIP_ERROR_INVALID_VALUE and b"num_entries" in lib.ie_attn_last_error()

@@ -79,3 +79,41 @@ def test_decode_graph_replay_bitwise(ie, dev):
     torch.cuda.synchronize()
     assert torch.equal(out, eager), "replay after input mutation differs from eager"
     assert not torch.equal(out, ref)
+
+
+def test_reference_capture_pattern_shared_pool(ie, workloads, dev):
+    """The engine's own capture (engine.py:432-449): warm-up twice on a fresh side stream, then
+    torch.cuda.graph(g, pool=pool) on torch's capture stream, where no op has run before. The
+    ops' workspaces are then allocated inside each capture from the shared pool, with a recorded
+    fill of their arrival counts, so they stay correct when the pool hands the same memory to
+    the next graph. Two graphs in one pool (a 3-layer decode step, config 4's prefill attention)
+    replay in alternating order, each equal to its eager result every time."""
+    step, _ = _make_step(ie, dev)
+    wl = workloads.mixed_to(workloads.config4(seed=3), dev)
+    gi = wl.inputs
+
+    def prefill():
+        return ie.prefill_attention(wl.q, wl.k, wl.v, gi["seq_ids"], gi["cu_seqlens"],
+                                    gi["tile_start"], wl.cache, gi["slot_ids"], gi["cu_cached"],
+                                    wl.block_m)
+
+    refs = [step().clone(), prefill().clone()]
+    pool = torch.cuda.graph_pool_handle()
+    graphs = []
+    for fn in (step, prefill):
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for _ in range(2):
+                fn()
+        torch.cuda.current_stream().wait_stream(s)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, pool=pool):
+            out = fn()
+        graphs.append((g, out))
+    for i, which in enumerate([1, 0, 1, 1, 0, 0, 1]):
+        g, out = graphs[which]
+        g.replay()
+        torch.cuda.synchronize()
+        say(f"shared-pool replay {i}: graph {which}")
+        assert torch.equal(out, refs[which]), f"replay {i} of graph {which} differs from eager"
