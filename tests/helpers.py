@@ -44,10 +44,13 @@ def rel_err(got, ref):
     return np.abs(got - ref) / scale
 
 
-def assert_attn_close(got, ref, what="", rel=True):
+def assert_attn_close(got, ref, what="", rel=True, abs_scale=1.0):
     """The north star's bf16 attention tolerance (max abs <= 2e-2, mean abs <= 2e-3) on
     unit-scale data, and the same bounds on the scale-normalised error (rel_err), so that an
-    error that grows with the output's magnitude cannot hide behind small outputs."""
+    error that grows with the output's magnitude cannot hide behind small outputs. abs_scale
+    multiplies the absolute bounds for data that is not unit-scale (V scaled by 1e2, or peaked
+    attention whose outputs are single V rows of magnitude up to ~4, where one bf16 rounding
+    step of an output is already 2^-6); the scale-normalised bounds do not change."""
     got = np.asarray(got, np.float64)
     ref = np.asarray(ref, np.float64)
     assert got.shape == ref.shape
@@ -56,7 +59,7 @@ def assert_attn_close(got, ref, what="", rel=True):
     r = rel_err(got, ref)
     say(f"{what}: max abs err {err.max():.3e} mean {err.mean():.3e}; "
         f"scaled max {r.max():.3e} mean {r.mean():.3e}")
-    assert err.max() <= TOL_MAX and err.mean() <= TOL_MEAN, what
+    assert err.max() <= TOL_MAX * abs_scale and err.mean() <= TOL_MEAN * abs_scale, what
     if rel:
         assert r.max() <= TOL_MAX and r.mean() <= TOL_MEAN, f"{what} (scale-normalised)"
 

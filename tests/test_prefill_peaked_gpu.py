@@ -11,9 +11,11 @@ tile, so these tests build inputs where it must:
   to u, so each tile's scores sit step * 128 * D^-0.5 * log2(e) (16.3 per unit step) above the
   previous tile's: the max moves at every tile boundary of every piece;
 * planted: near-flat scores plus one key per work piece (from the device's own work list,
-  ie_prefill_attention_plan) in a non-first tile of the piece, scoring about 11 log2 units above
-  the rest, so the jump moves the max while the keys before it still carry a share of the
-  softmax mass that a wrong rescale factor would misweigh;
+  ie_prefill_attention_plan) in a non-first tile of the piece: in the prefix 11.2 log2 units
+  above the rest, so the jump moves the max while the keys before it still carry a share of the
+  softmax mass that a wrong rescale factor would misweigh; in the chunk 11.2 more per chunk
+  tile (sub-blocks of one entry cut their chunk tiles into pieces at different places, so a key
+  planted for one sub-block can sit in another's first tile, and a later key must still jump);
 * a config-4 mixed step through the attention layer with q/k norm weights times 4 (scores of
   standard deviation ~23 log2 units).
 
@@ -97,8 +99,9 @@ def ramp_workload(workloads, chunks, seed, step=1.0, knoise=1.0, v_mult=1.0, blo
 
 def planted_workload(workloads, native, dev, chunks, seed, v_mult=1.0, block_m=128):
     """Near-flat scores (keys 0.1 N(0, 1)) and, for every piece of two or more tiles in the
-    device's work list, one key u * 11/16 (11.2 log2 units) at a random position of a random
-    non-first tile of the piece."""
+    device's work list, one key at a random position of a random non-first tile of the piece:
+    u * 11/16 (11.2 log2 units) in the prefix, u * 11/16 * (2 + chunk tile) in the chunk, at a
+    position of the tile that at least half the sub-block's rows see."""
     max_len = -(-max(L + c for L, c in chunks) // 64) * 64
     wl = workloads.mixed_workload([], chunks, seed=seed, block_m=block_m, max_len=max_len)
     rng = np.random.default_rng(seed + 2000)
@@ -129,8 +132,8 @@ def planted_workload(workloads, native, dev, chunks, seed, v_mult=1.0, block_m=1
             kpre[e][:, pos] = us[e] * (11 / 16)
         else:  # a chunk key, visible to the sub-block's rows at or after it
             n_vis = int(r[F["r1"]]) - s0
-            pos = 64 * (t - npt) + int(rng.integers(0, min(64, n_vis - 64 * (t - npt))))
-            k[s0 + pos] = us[e] * (11 / 16)
+            pos = 64 * (t - npt) + int(rng.integers(0, min(8, n_vis - 64 * (t - npt))))
+            k[s0 + pos] = us[e] * (11 / 16) * (2 + t - npt)
         planted += 1
     for e, (L, P) in enumerate(chunks):
         _set_prefix(wl.cache, e, kpre[e], rng.standard_normal((HKV, P, D)) * v_mult)
@@ -205,24 +208,33 @@ def oracle_prefill(wl):
                                  ins["tile_start"], wl.block_m, kp, vp, ins["cu_cached"])
 
 
-def run_and_check(ie, workloads, native, dev, wl, what, min_frac, forms_needed=()):
+def run_and_check(ie, workloads, native, dev, wl, what, min_frac, v_mult, forms_needed=(),
+                  min_pieces_moving=1.0):
+    """Coverage first: in every piece of two or more tiles, at least min_frac of the (row, head)
+    pairs that see its later tiles take the rescale branch, and at least min_pieces_moving of
+    those pieces have one that does; then the outputs against the oracle."""
     g = workloads.mixed_to(wl, dev)
     plan = prefill_plan(native, g)
     ins = {n: t.numpy() for n, t in wl.inputs.items()}
     fr, moved, forms = rescale_coverage(plan, bf16_np(wl.q), bf16_np(wl.k), cache_np(wl.cache),
                                         ins)
     say(f"{what}: pieces {forms}; rescale branch for {moved} (row, head) pairs, per-piece "
-        f"fraction min {fr.min():.2f} mean {fr.mean():.2f}")
+        f"fraction min {fr.min():.3f} mean {fr.mean():.3f}, pieces with a move "
+        f"{np.mean(fr > 0):.3f}")
     for f in forms_needed:
         assert forms[f] > 0, f"{what}: the work list has no {f} piece"
-    assert len(fr) > 0 and fr.min() >= min_frac, f"{what}: construction misses the branch"
+    assert len(fr) > 0 and np.mean(fr > 0) >= min_pieces_moving, \
+        f"{what}: pieces without the branch"
+    assert np.mean(fr[fr > 0] >= min_frac) >= min_pieces_moving, \
+        f"{what}: construction misses the branch"
     ref = oracle_prefill(wl)
     gi = g.inputs
     out = ie.prefill_attention(g.q, g.k, g.v, gi["seq_ids"], gi["cu_seqlens"], gi["tile_start"],
                                g.cache, gi["slot_ids"], gi["cu_cached"], g.block_m)
     torch.cuda.synchronize()
     cov = ~np.isnan(ref[:, 0, 0])
-    assert_attn_close(bf16_np(out)[cov], ref[cov], what)
+    assert_attn_close(bf16_np(out)[cov], ref[cov], what,
+                      abs_scale=max(1.0, v_mult) * max(1.0, float(np.abs(ref[cov]).max())))
 
 
 @pytest.mark.parametrize("v_mult", [1.0, 1e-3, 1e2])
@@ -233,9 +245,13 @@ def run_and_check(ie, workloads, native, dev, wl, what, min_frac, forms_needed=(
     ([(700, 0)], ("unsplit",)),                 # a chunk alone: unsplit causal pieces
 ])
 def test_prefill_ramp_moves_every_tile(ie, workloads, native, dev, chunks, forms, v_mult):
+    """Every piece takes the branch, for at least 95 % of the (row, head) pairs that see its
+    later tiles (a row that sees only the first few keys of a causal diagonal tile can fall
+    short of the jump; the mean is above 99 %)."""
     say(f"prefill ramp {len(chunks)} chunks {chunks[:2]}..., v x {v_mult}")
     wl = ramp_workload(workloads, chunks, seed=41, v_mult=v_mult)
-    run_and_check(ie, workloads, native, dev, wl, f"ramp {chunks[:2]} v x {v_mult}", 1.0, forms)
+    run_and_check(ie, workloads, native, dev, wl, f"ramp {chunks[:2]} v x {v_mult}", 0.95,
+                  v_mult, forms)
 
 
 @pytest.mark.parametrize("v_mult", [1.0, 1e-3, 1e2])
@@ -243,9 +259,13 @@ def test_prefill_ramp_moves_every_tile(ie, workloads, native, dev, chunks, forms
     [(512, 1536)], [(64, 1000 + 250 * i) for i in range(16)], [(300, 5000), (64, 9000)],
 ])
 def test_prefill_planted_key_per_piece(ie, workloads, native, dev, chunks, v_mult):
+    """Every piece takes the branch, for at least a quarter of the (row, head) pairs that see
+    its later tiles (all of them in prefix pieces; rows before a planted chunk key do not see
+    it)."""
     say(f"prefill planted {len(chunks)} chunks {chunks[:2]}..., v x {v_mult}")
     wl = planted_workload(workloads, native, dev, chunks, seed=43, v_mult=v_mult)
-    run_and_check(ie, workloads, native, dev, wl, f"planted {chunks[:2]} v x {v_mult}", 0.05)
+    run_and_check(ie, workloads, native, dev, wl, f"planted {chunks[:2]} v x {v_mult}", 0.25,
+                  v_mult)
 
 
 @pytest.mark.parametrize("v_mult", [1.0, 1e2])
@@ -280,6 +300,10 @@ def test_mixed_step_peaked_config4(ie, workloads, native, dev, v_mult):
     torch.cuda.synchronize()
     o = bf16_np(out)
     rows = ~np.isnan(ref[:, 0, 0])
-    assert_attn_close(o[:nd], ref[:nd], f"peaked config 4 v x {v_mult}: decode rows")
-    assert_attn_close(o[rows], ref[rows], f"peaked config 4 v x {v_mult}: all rows")
+    # peaked outputs are single V rows (magnitude up to ~4): one bf16 step is 2^-6 there
+    sc = max(1.0, v_mult) * max(1.0, float(np.abs(ref[rows]).max()))
+    assert_attn_close(o[:nd], ref[:nd], f"peaked config 4 v x {v_mult}: decode rows",
+                      abs_scale=sc)
+    assert_attn_close(o[rows], ref[rows], f"peaked config 4 v x {v_mult}: all rows",
+                      abs_scale=sc)
     assert_cache_bitwise(g.cache, ref_cache, "peaked config 4 cache")
