@@ -1,13 +1,15 @@
 // int8 KV cache writes and reads for gfx950.
 //
 //   quantize_kv_prefill_kernel   prefill quantize-on-write (+ K calibration on a first chunk)
-//   kcal_init/kcal_max_kernel    first-chunk K calibration ahead of it, for long steps
+//   kcal_max_kernel              first-chunk K calibration ahead of the quantize, long steps
+//   quantize_kv_stream_kernel    the quantize launch of long steps (resident grid, prefetch)
 //   fused_rope_kv_decode_kernel  decode q/k RMSNorm + RoPE, q * calibration, K/V quantize
 //   dequantize_kv_prefix_kernel  int8 prefix -> bf16
 //
-// Bit-level contract: every value written is produced by IEEE round-to-nearest-even fp32
-// operations in the order stated at each step (no contraction into fused multiply-add), so it
-// is reproducible on the host. Each row of 128 channels is handled by 16 lanes x 8 channels
+// Bit-level contract: every value written is the one IEEE round-to-nearest-even fp32
+// operations in the order stated at each step produce (no contraction into fused multiply-add),
+// so it is reproducible on the host; the prefill quantizers reach the IEEE quotients through
+// reciprocals where that is exact (div_recip). Each row of 128 channels is handled by 16 lanes x 8 channels
 // (prefill) or by one wave, 2 channels per lane (decode).
 #include "ie_common.h"
 #include "kv_math.h"
@@ -24,20 +26,26 @@ constexpr int QP_CAL_BATCH = 32;           // calibration rows in flight per thr
 // longer steps compute it in two launches of linear cost first.
 constexpr int64_t QP_INLINE_CAL_MAX_TOKENS = 1536;
 constexpr int QP_CAL_BLOCK = 256;  // chunk rows per workgroup of the separate calibration launch
+// The long steps' quantize launch (quantize_kv_stream_kernel): rows per block, and workgroups
+// per CU of its resident grid (measured on a 12,288-token step: 32 rows and 4 workgroups per CU
+// against 64 rows at 3 or 4 per CU +4-7 %, 128 rows at 2 per CU +22 %, 2 per CU +5 %; workgroups
+// that hold every KV head of their tokens, so that a wave reads 1 KB of a token row, +6 %).
+#ifndef IE_QS_BLOCK
+#define IE_QS_BLOCK 32
+#endif
+#ifndef IE_QS_WG_PER_CU
+#define IE_QS_WG_PER_CU 4
+#endif
+constexpr int QS_BLOCK = IE_QS_BLOCK;
+constexpr int QS_WG_PER_CU = IE_QS_WG_PER_CU;
 
+// 8 consecutive bf16 (16 bytes), packed two per word.
 struct Row8 {
-    float x[8];
+    uint32_t w[4];
 };
-
-// 8 consecutive bf16 (16 bytes) -> fp32.
 __device__ __forceinline__ Row8 load_bf16x8(const uint16_t* p) {
     const uint4 u = *reinterpret_cast<const uint4*>(p);
-    Row8 r;
-    r.x[0] = bf16lo(u.x); r.x[1] = bf16hi(u.x);
-    r.x[2] = bf16lo(u.y); r.x[3] = bf16hi(u.y);
-    r.x[4] = bf16lo(u.z); r.x[5] = bf16hi(u.z);
-    r.x[6] = bf16lo(u.w); r.x[7] = bf16hi(u.w);
-    return r;
+    return Row8{{u.x, u.y, u.z, u.w}};
 }
 
 __device__ __forceinline__ uint2 pack_i8x8(const int32_t* q) {
@@ -57,6 +65,106 @@ __device__ __forceinline__ float quantize_row8(const float* x, int32_t* q) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) q[j] = quant1(x[j], s);
     return s;
+}
+
+// x / b from y = 1 / b (IEEE division): q0 = x * y, r = fma(-q0, b, x) (exact), q0 + r * y
+// fused (Markstein's correction step). This is the IEEE quotient unless the quotient or the
+// remainder underflows or overflows: 3 instructions where an IEEE division compiles to 11. The
+// quantizers use it only for rows whose |x| stay below 2^100 (RECIP_MAX_BITS; row_needs_ieee
+// sends other rows, inf and NaN included, to the IEEE division), where tests/divcheck checks it
+// on the host against the IEEE quotient: every bf16 x against every calibration the writes
+// produce (wherever the quotient is at least 2^-64: smaller ones quantize to 0 against any row
+// scale, and a row maximum below 1e-6 is raised to 1e-6 before it becomes a scale), the int8
+// value of every bf16 x against every bf16 row maximum, and 10^9 random fp32 pairs each for K
+// rows after the calibration division and for other calibrations.
+__device__ __forceinline__ float div_recip(float x, float b, float y) {
+#pragma clang fp contract(off)
+    const float q0 = x * y;
+    const float r = __builtin_fmaf(-q0, b, x);
+    return __builtin_fmaf(r, y, q0);
+}
+constexpr uint32_t RECIP_MAX_BITS = 0x71800000u;  // fp32 bits of 2^100
+
+// Whether the 16-lane row group of this lane holds a bf16 value (8 per lane, packed in w) the
+// reciprocal division does not serve: |x| >= 2^100, inf or NaN. Uniform within the row group.
+__device__ __forceinline__ bool row_needs_ieee(const uint32_t (&w)[4]) {
+    bool big = false;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        big |= (w[j] & 0x7fff0000u) >= RECIP_MAX_BITS || ((w[j] << 16) & 0x7fffffffu) >= RECIP_MAX_BITS;
+    const uint64_t m = __ballot(big);
+    return ((m >> (threadIdx.x & 48)) & 0xffffu) != 0;
+}
+
+// quantize_row8 through the scale's reciprocal, for the rows row_needs_ieee lets through (also
+// after the calibration division): the same int8 values and scale, packed as pack_i8x8 packs
+// them. Two exact shortcuts: rint (half to even) of a quotient q with |q| < 2^22 is the sum
+// q + 1.5 * 2^23 rounded to nearest even, whose low mantissa byte is the integer as int8 (the
+// sum is 0x4B400000 + rint(q) in bits), so a byte permute packs four of them; and the clamp to
+// +-127 never binds: s = max(a, 1e-6) / 127 with a = max |x| gives |x / s| <= 127 (1 + 2^-24).
+__device__ __forceinline__ float quantize_row8_recip(const float* x, uint2& packed) {
+#pragma clang fp contract(off)
+    float a = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) a = fmaxf(a, fabsf(x[j]));
+    a = max16(a);
+    const float s = fmaxf(a, 1e-6f) / 127.0f;
+    const float y = 1.0f / s;
+    uint32_t b[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) b[j] = __float_as_uint(div_recip(x[j], s, y) + 12582912.0f);
+    // bytes 0 of b0..b3 (and b4..b7): two permutes to pair them, one to join the pairs
+    packed.x = __builtin_amdgcn_perm(__builtin_amdgcn_perm(b[3], b[2], 0x0c0c0400u),
+                                     __builtin_amdgcn_perm(b[1], b[0], 0x0c0c0400u), 0x05040100u);
+    packed.y = __builtin_amdgcn_perm(__builtin_amdgcn_perm(b[7], b[6], 0x0c0c0400u),
+                                     __builtin_amdgcn_perm(b[5], b[4], 0x0c0c0400u), 0x05040100u);
+    return s;
+}
+
+// One row of K and V (8 channels of this lane): K divided by the calibration (cal, its
+// reciprocal rcal), both quantized and stored with their scales at column col. The reciprocal
+// forms serve the row unless it holds a value they do not (row_needs_ieee).
+__device__ __forceinline__ void quantize_store_kv_row(const uint32_t (&kw)[4],
+                                                      const uint32_t (&vw)[4], const float* cal,
+                                                      const float* rcal, int8_t* kc, int8_t* vc,
+                                                      float* ks, float* vs, int64_t col,
+                                                      int64_t stride_tok, int c16) {
+#pragma clang fp contract(off)
+    float xk[8], xv[8];
+    int32_t qv[8];
+    uint2 packed;
+    float sk, sv;
+    if (!row_needs_ieee(kw)) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            xk[2 * j] = div_recip(bf16lo(kw[j]), cal[2 * j], rcal[2 * j]);
+            xk[2 * j + 1] = div_recip(bf16hi(kw[j]), cal[2 * j + 1], rcal[2 * j + 1]);
+        }
+        sk = quantize_row8_recip(xk, packed);
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            xk[2 * j] = bf16lo(kw[j]) / cal[2 * j];
+            xk[2 * j + 1] = bf16hi(kw[j]) / cal[2 * j + 1];
+        }
+        sk = quantize_row8(xk, qv);
+        packed = pack_i8x8(qv);
+    }
+    *reinterpret_cast<uint2*>(kc + col * stride_tok) = packed;
+    if (c16 == 0) ks[col] = sk;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        xv[2 * j] = bf16lo(vw[j]);
+        xv[2 * j + 1] = bf16hi(vw[j]);
+    }
+    if (!row_needs_ieee(vw)) {
+        sv = quantize_row8_recip(xv, packed);
+    } else {
+        sv = quantize_row8(xv, qv);
+        packed = pack_i8x8(qv);
+    }
+    *reinterpret_cast<uint2*>(vc + col * stride_tok) = packed;
+    if (c16 == 0) vs[col] = sv;
 }
 
 // The prefilling entries' chunks are cut into blocks of ROWS rows, numbered entry by entry.
@@ -104,19 +212,18 @@ __device__ __forceinline__ QpBlock qp_locate(int u, const int32_t* __restrict__ 
 }
 
 // Calibration rows longer than a few blocks are computed ahead of the quantize launch, in
-// linear time: kcal_init_kernel sets the calibration row of every entry with cached_len == 0
-// to the floor 1e-3, then kcal_max_kernel's workgroups (one per block of QP_CAL_BLOCK rows)
-// raise it to their rows' max |k| per channel with atomic max on the float bits (max is exact
-// and order-free, so the result equals the sequential one). Blocks of 256 rows keep the atomics
-// per calibration word few (they serialize at the memory side).
-// grid (num_entries, Hkv), block HEAD_DIM.
-__global__ __launch_bounds__(HEAD_DIM) void kcal_init_kernel(
-    const int32_t* __restrict__ cu_seqlens, const int32_t* __restrict__ slot_ids,
-    const int32_t* __restrict__ cached_lens, const int32_t* __restrict__ num_decoding,
-    ie_kv_cache c) {
-    const int e = blockIdx.x, h = blockIdx.y;
-    if (e < num_decoding[0] || cached_lens[e] != 0 || cu_seqlens[e + 1] == cu_seqlens[e]) return;
-    c.k_calibration[slot_ids[e] * c.cal_stride_slot + h * c.cal_stride_head + threadIdx.x] = 1e-3f;
+// linear time: kcal_max_kernel's workgroups (one per block of QP_CAL_BLOCK rows) take the max |k|
+// per channel of their rows and combine them in the entry's calibration row with an atomic max
+// on the bits of the NEGATED maximum: the bits of negative floats are all above those of
+// positive ones and grow with the magnitude, so whatever positive calibration the row held
+// before (an earlier sequence's) loses to the first block's value, and the row ends up holding
+// -(max over the chunk) (-0 for an all-zero chunk) with no initialization launch. Max is exact
+// and order-free, so the result equals the sequential one. The quantize launch reads such a row
+// as max(1e-3, -v) (cal_of) and the workgroup holding the chunk's first block stores that,
+// positive, back into the row. Blocks of 256 rows keep the atomics per calibration word few
+// (they serialize at the memory side).
+__device__ __forceinline__ float cal_of(float v) {
+    return (__float_as_uint(v) >> 31) ? fmaxf(1e-3f, -v) : v;
 }
 
 // grid (Hkv, cdiv(N, QP_CAL_BLOCK) + num_entries), block 256.
@@ -160,7 +267,7 @@ __global__ __launch_bounds__(QP_THREADS) void kcal_max_kernel(
 #pragma unroll
         for (int rr = 0; rr < QP_ROWS; ++rr) m = fmaxf(m, s_red[rr][tid]);
         float* calp = c.k_calibration + q.slot * c.cal_stride_slot + h * c.cal_stride_head;
-        atomicMax(reinterpret_cast<unsigned int*>(calp + tid), __float_as_uint(m));
+        atomicMax(reinterpret_cast<unsigned int*>(calp + tid), __float_as_uint(-m));
     }
 }
 
@@ -247,9 +354,12 @@ __global__ __launch_bounds__(QP_THREADS) void quantize_kv_prefill_kernel(
         if (tid < HEAD_DIM) s_cal[tid] = calp[tid];
     }
     __syncthreads();
-    float cal[8];
+    float cal[8], rcal[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) cal[j] = s_cal[8 * c16 + j];
+    for (int j = 0; j < 8; ++j) {
+        cal[j] = s_cal[8 * c16 + j];
+        rcal[j] = 1.0f / cal[j];
+    }
 
     int8_t* kc = c.k + slot * c.stride_slot + h * c.stride_head + 8 * c16;
     int8_t* vc = c.v + slot * c.stride_slot + h * c.stride_head + 8 * c16;
@@ -264,16 +374,131 @@ __global__ __launch_bounds__(QP_THREADS) void quantize_kv_prefill_kernel(
         for (int p = 0; p < 2; ++p) {
             if (p == 1 && !two) break;
             const int64_t col = (int64_t)(c0 + t + p * QP_ROWS);
-            int32_t q[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) ck[p].x[j] = ck[p].x[j] / cal[j];
-            float s = quantize_row8(ck[p].x, q);
-            *reinterpret_cast<uint2*>(kc + col * c.stride_tok) = pack_i8x8(q);
-            if (c16 == 0) ks[col] = s;
-            s = quantize_row8(cv[p].x, q);
-            *reinterpret_cast<uint2*>(vc + col * c.stride_tok) = pack_i8x8(q);
-            if (c16 == 0) vs[col] = s;
+            quantize_store_kv_row(ck[p].w, cv[p].w, cal, rcal, kc, vc, ks, vs, col, c.stride_tok,
+                                  c16);
         }
+    }
+}
+
+// The streaming form of the quantize launch, for long steps (their first chunks' calibration
+// rows come from kcal_max, in the negated form cal_of reads): one resident wave of workgroups, workgroup (h, g) taking
+// blocks g, g + G, ... of ROWS rows for kv head h (G = gridDim.y), with the next block's rows and
+// calibration in flight while the current block is quantized and stored. Up to 64 entries the
+// entry table sits in registers (lane e: entry e), so a block is located without a memory round
+// trip; with more entries each block is located by qp_locate. Same arithmetic, in the same
+// order, as quantize_kv_prefill_kernel: the same bits.
+template <int ROWS>
+struct QsRegs {
+    uint4 k[ROWS / QP_ROWS], v[ROWS / QP_ROWS];
+    float4 cal[2];
+};
+
+template <int ROWS>
+__global__ __launch_bounds__(QP_THREADS) void quantize_kv_stream_kernel(
+    const uint16_t* __restrict__ k, int64_t k_st, int64_t k_sh,
+    const uint16_t* __restrict__ v, int64_t v_st, int64_t v_sh,
+    const int32_t* __restrict__ cu_seqlens, const int32_t* __restrict__ slot_ids,
+    const int32_t* __restrict__ cached_lens, const int32_t* __restrict__ num_decoding,
+    int num_entries, ie_kv_cache c) {
+#pragma clang fp contract(off)
+    constexpr int RPT = ROWS / QP_ROWS;  // rows per thread and block
+    const int h = blockIdx.x, G = gridDim.y;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int c16 = tid & 15, r = tid >> 4;
+
+    // the entry table: lane e holds entry e's chunk, slot, cached length and block count
+    const bool in_regs = num_entries <= IE_WAVE;  // uniform
+    int e_s0 = 0, e_s1 = 0, e_sl = 0, e_cl = 0;
+    const int nd = __builtin_amdgcn_readfirstlane(num_decoding[0]);
+    if (in_regs && lane < num_entries) {
+        e_s0 = cu_seqlens[lane];
+        e_s1 = cu_seqlens[lane + 1];
+        e_sl = slot_ids[lane];
+        e_cl = cached_lens[lane];
+    }
+    const int e_nb = in_regs && lane >= nd && lane < num_entries ? cdiv_i(e_s1 - e_s0, ROWS) : 0;
+    const int e_incl = wave_incl_scan_i(e_nb);
+    auto locate = [&](int u) -> QpBlock {
+        if (!in_regs)
+            return qp_locate<ROWS>(u, cu_seqlens, slot_ids, cached_lens, num_decoding,
+                                   num_entries);
+        const unsigned long long hit = __ballot(e_nb > 0 && u < e_incl && u >= e_incl - e_nb);
+        if (!hit) return QpBlock{-1, 0, 0, 0, 0, 0};
+        const int src = __builtin_ctzll(hit);
+        auto from = [&](int x) { return __builtin_amdgcn_readlane(x, src); };
+        return QpBlock{src, u - from(e_incl - e_nb), from(e_s0), from(e_s1 - e_s0), from(e_sl),
+                       from(e_cl)};
+    };
+    auto load = [&](const QpBlock& q, QsRegs<ROWS>& x) {
+        const int t0 = q.z * ROWS, t1 = min(q.len, t0 + ROWS);
+        const uint16_t* kh = k + (int64_t)q.start * k_st + h * k_sh + 8 * c16;
+        const uint16_t* vh = v + (int64_t)q.start * v_st + h * v_sh + 8 * c16;
+#pragma unroll
+        for (int i = 0; i < RPT; ++i) {
+            const int t = t0 + r + i * QP_ROWS;
+            if (t < t1) {
+                x.k[i] = *reinterpret_cast<const uint4*>(kh + (int64_t)t * k_st);
+                x.v[i] = *reinterpret_cast<const uint4*>(vh + (int64_t)t * v_st);
+            }
+        }
+        const float* calp =
+            c.k_calibration + q.slot * c.cal_stride_slot + h * c.cal_stride_head + 8 * c16;
+        x.cal[0] = *reinterpret_cast<const float4*>(calp);
+        x.cal[1] = *reinterpret_cast<const float4*>(calp + 4);
+    };
+    float rcal[8];
+    int rcal_slot = -1;
+    auto store = [&](const QpBlock& q, const QsRegs<ROWS>& x) {
+        const int t0 = q.z * ROWS, t1 = min(q.len, t0 + ROWS);
+        int8_t* kc = c.k + q.slot * c.stride_slot + h * c.stride_head + 8 * c16;
+        int8_t* vc = c.v + q.slot * c.stride_slot + h * c.stride_head + 8 * c16;
+        float* ks = c.k_scale + q.slot * c.scale_stride_slot + h * c.scale_stride_head;
+        float* vs = c.v_scale + q.slot * c.scale_stride_slot + h * c.scale_stride_head;
+        // a first chunk's row holds -(max |k|) until its first block's workgroup stores the
+        // calibration itself (cal_of reads either form as the same value)
+        const float cal[8] = {cal_of(x.cal[0].x), cal_of(x.cal[0].y), cal_of(x.cal[0].z),
+                              cal_of(x.cal[0].w), cal_of(x.cal[1].x), cal_of(x.cal[1].y),
+                              cal_of(x.cal[1].z), cal_of(x.cal[1].w)};
+        if (q.c0 == 0 && q.z == 0) {
+            float* calp = c.k_calibration + q.slot * c.cal_stride_slot + h * c.cal_stride_head;
+            if (tid < 16)
+                *reinterpret_cast<float4*>(calp + 8 * c16) = make_float4(cal[0], cal[1], cal[2], cal[3]);
+            else if (tid < 32)
+                *reinterpret_cast<float4*>(calp + 8 * c16 + 4) = make_float4(cal[4], cal[5], cal[6], cal[7]);
+        }
+        if (q.slot != rcal_slot) {  // the calibration's reciprocals, once per entry
+#pragma unroll
+            for (int j = 0; j < 8; ++j) rcal[j] = 1.0f / cal[j];
+            rcal_slot = q.slot;
+        }
+#pragma unroll
+        for (int i = 0; i < RPT; ++i) {
+            const int t = t0 + r + i * QP_ROWS;
+            if (t >= t1) continue;
+            const uint32_t kw[4] = {x.k[i].x, x.k[i].y, x.k[i].z, x.k[i].w};
+            const uint32_t vw[4] = {x.v[i].x, x.v[i].y, x.v[i].z, x.v[i].w};
+            quantize_store_kv_row(kw, vw, cal, rcal, kc, vc, ks, vs, (int64_t)(q.c0 + t),
+                                  c.stride_tok, c16);
+        }
+    };
+    // two register sets alternate: block u + G loads into one while block u, in the other, is
+    // quantized
+    QsRegs<ROWS> xa, xb;
+    int u = blockIdx.y;
+    QpBlock qa = locate(u);
+    if (qa.b < 0) return;
+    load(qa, xa);
+    for (;;) {
+        const QpBlock qb = locate(u + G);
+        if (qb.b >= 0) load(qb, xb);
+        store(qa, xa);
+        if (qb.b < 0) return;
+        u += G;
+        qa = locate(u + G);
+        if (qa.b >= 0) load(qa, xa);
+        store(qb, xb);
+        if (qa.b < 0) return;
+        u += G;
     }
 }
 
@@ -485,16 +710,18 @@ extern "C" hipError_t ie_quantize_kv_prefill(
                            num_decoding, num_entries, *cache);
         return hipGetLastError();
     }
-    hipLaunchKernelGGL(kcal_init_kernel, dim3(num_entries, cache->num_kv_heads), dim3(HEAD_DIM),
-                       0, stream, cu_seqlens, slot_ids, cached_lens, num_decoding, *cache);
     const int64_t cal_blocks = (num_tokens + QP_CAL_BLOCK - 1) / QP_CAL_BLOCK + num_entries;
     hipLaunchKernelGGL(kcal_max_kernel, dim3(cache->num_kv_heads, (unsigned)cal_blocks),
                        dim3(QP_THREADS), 0, stream, (const uint16_t*)k,
                        k_stride_tok, k_stride_head, cu_seqlens, slot_ids, cached_lens,
                        num_decoding, num_entries, *cache);
-    // (blocks of 16, 64 or 128 rows were measured slower than 32 on a 12,288-token step)
-    hipLaunchKernelGGL((quantize_kv_prefill_kernel<false, QP_BLOCK>), grid, dim3(QP_THREADS), 0,
-                       stream,
+    // the streaming form: one resident wave of workgroups looping over blocks
+    const int hkv = (int)cache->num_kv_heads;
+    const int64_t sblocks = (num_tokens + QS_BLOCK - 1) / QS_BLOCK + num_entries;
+    const int64_t resident =
+        std::max<int64_t>(1, (int64_t)device_cu_count() * QS_WG_PER_CU / hkv);
+    const dim3 sgrid((unsigned)hkv, (unsigned)std::min(sblocks, resident));
+    hipLaunchKernelGGL((quantize_kv_stream_kernel<QS_BLOCK>), sgrid, dim3(QP_THREADS), 0, stream,
                        (const uint16_t*)k, k_stride_tok, k_stride_head, (const uint16_t*)v,
                        v_stride_tok, v_stride_head, cu_seqlens, slot_ids, cached_lens,
                        num_decoding, num_entries, *cache);

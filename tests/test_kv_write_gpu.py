@@ -92,3 +92,42 @@ def test_dequantize_kv_prefix_bitwise(ie, workloads, dev):
     assert np.array_equal(kb[:, :total], bf16_bits(ref_k))
     assert np.array_equal(vb[:, :total], bf16_bits(ref_v))
     assert not kb[:, total:].any()
+
+
+@pytest.mark.parametrize("long_step", [False, True])
+def test_quantize_kv_prefill_edge_values_bitwise(ie, workloads, dev, long_step):
+    """Rows the reciprocal division does not serve (a K or V value of magnitude 2^100 or more:
+    those rows take the IEEE division), rows of subnormal and of zero values, V rows whose
+    quotients are exact halves (round half to even), and a continuing chunk whose calibration
+    row holds arbitrary fp32 values: bit-exact against the oracle, in the one-launch form and in
+    the long form (calibration launches, then the streaming quantize launch)."""
+    chunks = [(2000, 0), (300, 150)] if long_step else [(300, 0), (200, 150)]
+    say(f"quantize_kv_prefill edge values, chunks {chunks}")
+    wl = _prefill_case(workloads, [4], chunks, seed=9, max_len=4096)
+    rng = np.random.default_rng(9)
+    k, v = wl.k.float(), wl.v.float()
+    cu = wl.inputs["cu_seqlens"].numpy()
+    r = lambda e: int(cu[e]) + int(rng.integers(0, chunks[e - 1][0]))
+    k[r(1), 3] *= 2.0 ** 105            # first chunk: raises that channel's calibration too
+    k[r(2), 5, 17] = 2.0 ** 101          # continuing chunk: one huge value in a row
+    v[r(1), 2, 7] = -(2.0 ** 110)
+    k[r(1), 6] = torch.from_numpy(rng.choice([-1, 1], 128) * 2.0 ** -130).float()  # subnormal
+    v[r(2), 1] = 0.0
+    halves = torch.from_numpy(np.concatenate([[127.0], np.arange(127) - 63.5])).float()
+    v[r(1), 4] = halves                  # scale 1: quotients -63.5 ... 62.5
+    v[r(2), 0] = -halves
+    wl.k.copy_(k.bfloat16())
+    wl.v.copy_(v.bfloat16())
+    slot_cont = int(wl.inputs["slot_ids"][2])
+    wl.cache.k_calibration[slot_cont] = torch.from_numpy(
+        np.exp(rng.uniform(np.log(1e-3), np.log(50.0), (8, 1, 128)))).float()
+    ins = {n: t.numpy() for n, t in wl.inputs.items()}
+    ref = cache_np(wl.cache)
+    okv.quantize_kv_prefill(bf16_np(wl.k), bf16_np(wl.v), ins["cu_seqlens"], ins["slot_ids"],
+                            ins["cached_lens"], int(ins["num_decoding"][0]), ref)
+    g = workloads.mixed_to(wl, dev)
+    gi = g.inputs
+    ie.quantize_kv_prefill(g.k, g.v, gi["cu_seqlens"], gi["slot_ids"], gi["cached_lens"],
+                           gi["num_decoding"], g.cache)
+    torch.cuda.synchronize()
+    assert_cache_bitwise(g.cache, ref, "quantize_kv_prefill edge values")
