@@ -131,14 +131,15 @@ hipError_t ie_fused_rope_kv_decode(const ie_bf16* q, int64_t q_stride_b, int64_t
                                    int64_t q_out_stride_h, hipStream_t stream);
 
 /*
- * Bytes of device workspace ie_decode_attention needs for `batch` sequences on the current
- * device: the arrival counts (one uint32 per sequence and KV head, with room for max(batch,
- * 1024) sequences, padded to 256 bytes), then fp32 split-K partials, head_dim + 2 values per
- * (query head, work entry), where the work entries are ie_decode_attention_grid(batch,
- * num_q_heads / 2). The arrival counts must be zero when a workspace is first used (allocate it
- * zeroed); every call that completes leaves them zero again, so one workspace serves any number
- * of calls in stream order, of any batch up to 1024 (they share one count region). A workspace
- * used with a batch above 1024 serves that batch size only, unless zeroed again.
+ * Bytes of device workspace ie_decode_attention needs for `batch` sequences of num_q_heads query
+ * heads on the current device, whatever the GQA ratio: the arrival counts (one uint32 per
+ * sequence and query head, the most any ratio uses, with room for max(batch, 1024) sequences,
+ * padded to 256 bytes), then fp32 split-K partials, head_dim + 2 values per (query head, work
+ * entry), where the work entries are at most ie_decode_attention_grid(batch, cdiv(num_q_heads,
+ * 2)). The arrival counts must be zero when a workspace is first used (allocate it zeroed);
+ * every call that completes leaves them zero again, so one workspace serves any number of calls
+ * in stream order, of any batch up to 1024 (they share one count region). A workspace used with
+ * a batch above 1024 serves that batch size only, unless zeroed again.
  */
 size_t ie_decode_attention_workspace_size(int32_t batch, int32_t num_q_heads, int32_t head_dim);
 
@@ -147,26 +148,31 @@ size_t ie_decode_attention_workspace_size(int32_t batch, int32_t num_q_heads, in
  * arrival counts: max(batch, 1024) * num_kv_heads uint32, padded to 256 bytes). Zeroing them
  * resets a workspace, e.g. one whose memory was reused or a launch that did not complete, and
  * a caller that records the decode call into a hipGraph from freshly allocated memory records
- * a fill of these bytes first. No counterpart in the reference (its partials need no counts).
+ * a fill of these bytes first. (max(batch, 1024) * num_q_heads uint32, padded to 256 bytes.) No counterpart in the reference (its partials need no counts).
  */
-size_t ie_decode_attention_workspace_counts_bytes(int32_t batch, int32_t num_kv_heads);
+size_t ie_decode_attention_workspace_counts_bytes(int32_t batch, int32_t num_q_heads);
 
-/* Upper bound on splits per sequence on the current device: the largest per-KV-head workgroup
- * target of any launch shape (CUs * 8 / num_kv_heads, 2-wave workgroups). */
-int32_t ie_decode_attention_max_splits(int32_t num_kv_heads);
+/* Upper bound on splits per sequence on the current device: the largest per-unit workgroup
+ * target of any launch shape (CUs * 8 / num_units, 2-wave workgroups). A unit is a KV head and
+ * one pair of its query heads: num_units = num_kv_heads * cdiv(num_q_heads / num_kv_heads, 2),
+ * num_kv_heads itself at GQA ratio 2. */
+int32_t ie_decode_attention_max_splits(int32_t num_units);
 
 /*
- * The per-KV-head workgroup target of the work split (qwen3-1.7b/kernels.py:20-37 TARGET) that
- * ie_decode_attention uses for `batch` sequences on the current device. The launch fills the CUs
- * with 16 waves each, as 8-wave workgroups (target CUs * 2 / num_kv_heads) while the batch fits
- * that target, else as 4-wave (CUs * 4 / num_kv_heads) or 2-wave (CUs * 8 / num_kv_heads)
- * workgroups, the first whose target holds the batch (the 2-wave one above that).
+ * The per-unit workgroup target of the work split (qwen3-1.7b/kernels.py:20-37 TARGET) that
+ * ie_decode_attention uses for `batch` sequences on the current device (num_units as above). The
+ * launch fills the CUs with 16 waves each, as 8-wave workgroups (target CUs * 2 / num_units)
+ * while the batch fits that target, else as 4-wave (CUs * 4 / num_units) or 2-wave (CUs * 8 /
+ * num_units) workgroups, the first whose target holds the batch (the 2-wave one above that).
  */
-int32_t ie_decode_attention_target(int32_t batch, int32_t num_kv_heads);
+int32_t ie_decode_attention_target(int32_t batch, int32_t num_units);
 
 /*
  * Split-K GQA decode attention over the int8 cache, with the partial-softmax reduce folded into
- * the same launch (the sequence's last piece to finish merges its pieces).
+ * the same launch (the sequence's last piece to finish merges its pieces). Any GQA ratio
+ * num_q_heads / num_kv_heads of 1 to 16 (the reference's q-group padding, kernels.py:118-135),
+ * head_dim 128; a workgroup serves one pair of a KV head's query heads, so ratios above 2 read
+ * each KV row once per pair.
  * Replaces qwen3-1.7b/kernels.py:272-361 `decode_attention(q, kv_cache, cached_lens, slot_ids,
  * num_decoding, scale, out)` (kernels kernels.py:73-213 and 216-264, work split 20-70).
  *
@@ -232,14 +238,14 @@ hipError_t ie_decode_attention_noalloc(const ie_bf16* q, int64_t q_stride_b, int
 /*
  * The decode launch's work list, for tests and diagnostics: the work split of
  * qwen3-1.7b/kernels.py:20-70 (`compute_piece`, `assign_work`) as the decode kernel computes it
- * on the device. ie_decode_attention_grid(batch, num_kv_heads) is the number of work entries
- * (the decode launch's workgroups per KV head); ie_decode_attention_plan writes, for each entry
+ * on the device. ie_decode_attention_grid(batch, num_units) is the number of work entries
+ * (the decode launch's workgroups per unit: KV head x query-head pair, as above); ie_decode_attention_plan writes, for each entry
  * w, rows[4w .. 4w+3] = (sequence b, split index, splits of b, piece size in tokens), with
  * splits = 0 for an entry that has no work. rows: int32 [grid, 4] device memory.
  */
-int32_t ie_decode_attention_grid(int32_t batch, int32_t num_kv_heads);
+int32_t ie_decode_attention_grid(int32_t batch, int32_t num_units);
 hipError_t ie_decode_attention_plan(const int32_t* cached_lens, const int32_t* num_decoding,
-                                    int32_t batch, int32_t num_kv_heads, int32_t* rows,
+                                    int32_t batch, int32_t num_units, int32_t* rows,
                                     hipStream_t stream);
 
 /*
@@ -282,7 +288,8 @@ hipError_t ie_dequantize_kv_prefix(const ie_kv_cache* cache, const int32_t* cu_c
  * Causal chunked-prefill attention that reads each entry's cached prefix straight from the int8
  * cache and runs QK^T and PV on bf16 MFMA: prefix V is dequantized in LDS with the rounding of
  * ie_dequantize_kv_prefix, prefix K is staged as exact integers with its scale and calibration
- * folded into the scores and into q.
+ * folded into the scores and into q. Any GQA ratio num_q_heads / num_kv_heads of 1 to 16,
+ * head_dim 128; a workgroup serves one pair of a KV head's query heads.
  * Replaces qwen3-1.7b/kernels.py:1129-1175 `prefill_attention(q, k, v, seq_ids, cu_seqlens,
  * tile_start, k_prefix, v_prefix, cu_cached, PREFILL_BLOCK_M)` (kernel kernels.py:987-1126)
  * together with the dequantize_kv_prefix call that fed it (qwen3-1.7b/architecture.py:151-170):
@@ -326,23 +333,26 @@ hipError_t ie_prefill_attention(const ie_bf16* q, int64_t q_stride_tok, int64_t 
 /*
  * The prefill launch's work list, for tests and diagnostics (no counterpart in the reference,
  * whose prefill grid is one program per (tile, query head), kernels.py:1146-1150):
- * ie_prefill_attention_grid(num_tiles, block_m, num_kv_heads) is the launch's workgroup count,
- * and ie_prefill_attention_plan writes, for each workgroup w, 16 int32 at rows[16 w]:
- *   found, sub-block, kv head, piece, pieces of its (sub-block, kv head) pair, first tile,
- *   end tile, prefix tiles, chunk tiles, first row, end row, the entry's first row, prefix
- *   length, tiles per piece, straddling form (1) or separate prefix/chunk pieces (0), the
- *   pair's first item
- * where sub-blocks are 128-row slices of the tiles, tile t < prefix tiles is the prefix's
- * 64-key tile t and later tiles are the chunk's 64-key tiles, and a workgroup without work has
- * an all-zero row. Same index arguments as ie_prefill_attention; rows: int32 [grid, 16]
- * device memory.
+ * ie_prefill_attention_grid(num_tiles, block_m, num_q_heads, num_kv_heads) is the launch's
+ * workgroup count, and ie_prefill_attention_plan writes, for each workgroup w, 16 int32 at
+ * rows[16 w]:
+ *   found, sub-block, unit, piece, pieces of its (sub-block, unit) pair, first tile, end tile,
+ *   prefix tiles, chunk tiles, first row, end row, the entry's first row, prefix length, tiles
+ *   per piece, straddling form (1) or separate prefix/chunk pieces (0), the pair's first item
+ * where sub-blocks are 128-row slices of the tiles, a unit is a KV head and one pair of its
+ * query heads (unit = KV head * cdiv(ratio, 2) + pair: the KV head itself at GQA ratio 2), tile
+ * t < prefix tiles is the prefix's 64-key tile t and later tiles are the chunk's 64-key tiles,
+ * and a workgroup without work has an all-zero row. Same index arguments as
+ * ie_prefill_attention; rows: int32 [grid, 16] device memory.
  */
-int32_t ie_prefill_attention_grid(int32_t num_tiles, int32_t block_m, int32_t num_kv_heads);
+int32_t ie_prefill_attention_grid(int32_t num_tiles, int32_t block_m, int32_t num_q_heads,
+                                  int32_t num_kv_heads);
 hipError_t ie_prefill_attention_plan(const int32_t* seq_ids, const int32_t* cu_seqlens,
                                      const int32_t* tile_start, int32_t num_tiles,
-                                     int32_t block_m, int64_t num_tokens, int32_t num_kv_heads,
-                                     const int32_t* slot_ids, const int32_t* cu_cached,
-                                     int32_t num_entries, int32_t* rows, hipStream_t stream);
+                                     int32_t block_m, int64_t num_tokens, int32_t num_q_heads,
+                                     int32_t num_kv_heads, const int32_t* slot_ids,
+                                     const int32_t* cu_cached, int32_t num_entries, int32_t* rows,
+                                     hipStream_t stream);
 
 /*
  * Token sampling: Gumbel-max over the vocabulary, greedy argmax at tau = 0.

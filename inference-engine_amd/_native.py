@@ -57,7 +57,7 @@ def cabi() -> ctypes.CDLL:
         _cabi.ie_prefill_attention_workspace_counts_bytes.restype = ctypes.c_size_t
         _cabi.ie_prefill_attention_workspace_counts_bytes.argtypes = []
         _cabi.ie_prefill_attention_grid.restype = ctypes.c_int32
-        _cabi.ie_prefill_attention_grid.argtypes = [ctypes.c_int32] * 3
+        _cabi.ie_prefill_attention_grid.argtypes = [ctypes.c_int32] * 4
     return _cabi
 
 

@@ -61,18 +61,21 @@ constexpr uint32_t K64 = 0x64646464u;
 constexpr float OFFSET = 1152.0f;  // fp16(0x64xx) = 1024 + byte, byte = x + 128
 
 
-// Per-KV-head workgroup target of workgroups of `waves` waves: one resident round.
-int decode_target(int num_kv_heads, int waves) {
+// Workgroup target per unit (KV head x query-head pair; the KV head at GQA 2) of workgroups of
+// `waves` waves: one resident round.
+int decode_target(int units, int waves) {
     return std::min(DA_MAX_SPLITS, std::max(1, device_cu_count() * (DA_WAVES_PER_CU / waves) /
-                                                   std::max(1, num_kv_heads)));
+                                                   std::max(1, units)));
 }
 // Waves per workgroup for a batch: the largest workgroup whose target holds the batch, else
 // the smallest.
-int decode_waves(int batch, int num_kv_heads) {
+int decode_waves(int batch, int units) {
     for (int w = 8; w > 2; w /= 2)
-        if (batch <= decode_target(num_kv_heads, w)) return w;
+        if (batch <= decode_target(units, w)) return w;
     return 2;
 }
+// Units of a launch: KV heads x query-head pairs per KV head.
+int decode_units(int hq, int hkv) { return hkv * ((hq / std::max(1, hkv) + 1) / 2); }
 
 
 // Piece size for this step; wave-uniform, every lane returns it. The reference's rule
@@ -140,6 +143,11 @@ __device__ Work decode_assign(const int32_t* __restrict__ cached_lens, int nd, i
 }
 
 __device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
+// The lane's index in its wave, from the lane-count instructions: with the wave index (uniform)
+// it rebuilds the thread index after the block loop, so that no register holds it there.
+__device__ __forceinline__ int lane_id() {
+    return (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+}
 __device__ __forceinline__ half2_t as_h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
 __device__ __forceinline__ float fdot2(half2_t a, half2_t b, float c) {
     return __builtin_amdgcn_fdot2(a, b, c, false);
@@ -161,6 +169,9 @@ struct DecodeArgs {
     float* part_l;       // [Hq, nwork]
     uint32_t* arrivals;  // [B, Hkv]: pieces of the sequence done; 0 between calls
     int target, nwork, hq, hkv;
+    int ratio;   // query heads per KV head (GQA ratio, 1 ... 16)
+    int npairs;  // query-head pairs per KV head, cdiv(ratio, 2): a workgroup serves one pair
+    int units;   // hkv * npairs: the grid's second dimension
     int batch;        // rows of q / cached_lens (num_decoding[0] <= batch)
     int head_fast;    // 1: grid (Hkv, pieces), the KV head in blockIdx.x; 0: grid (pieces, Hkv)
     // The fused form (ie_decode_attention_rope): q holds the QKV projection's raw rows, and the
@@ -326,7 +337,9 @@ __device__ __forceinline__ void block_pv(LaneState& st, const float (&t)[DA_U][2
 #define IE_DECODE_WAVES_PER_EU 4
 #endif
 
-template <int WAVES, bool ROPE>
+// GQA2: the launch's GQA ratio is 2 (one query-head pair per KV head), so the pair's query
+// heads are 2 hk and 2 hk + 1 at compile time; other ratios take the generic form.
+template <int WAVES, bool ROPE, bool GQA2>
 __global__ __launch_bounds__(WAVES * IE_WAVE)
 __attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_attention_kernel(
     DecodeArgs a) {
@@ -338,8 +351,15 @@ __attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_attenti
     const int raw0 = lane0 < a.batch ? a.cached_lens[lane0] : 0;
     const int slot0 = lane0 < a.batch ? a.slot_ids[lane0] : 0;
     const int nd = a.num_decoding[0];
+    // the workgroup's (KV head, query-head pair): query heads qh0 = ratio * hk + 2 * pair and
+    // qh0 + 1 (the pair of an odd ratio's last pair is one head: has2 = false)
     const int hk = a.head_fast ? blockIdx.x : blockIdx.y;
+    const int pair = GQA2 ? 0 : (int)blockIdx.z;
     const int item = a.head_fast ? blockIdx.y : blockIdx.x;
+    const int unit = GQA2 ? hk : hk * a.npairs + pair;
+    const int qh0 = GQA2 ? 2 * hk : uniform(a.ratio * hk + 2 * pair);
+    const bool has2 = GQA2 || 2 * pair + 1 < a.ratio;
+    const int qh1 = has2 ? qh0 + 1 : qh0;  // an absent second head repeats the first
     Work wk = decode_assign(a.cached_lens, nd, item, a.target, raw0);
     // Wave-uniform by construction; readfirstlane lets the compiler keep them (and the buffer
     // descriptors built from them) in SGPRs.
@@ -381,13 +401,16 @@ __attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_attenti
     uint16_t rq1[2], rq2[2], rqw1 = 0, rqw2 = 0, rcs = 0, rsn = 0;
     uint16_t rk1 = 0, rk2 = 0, rkw1 = 0, rkw2 = 0, rv1 = 0, rv2 = 0;
     float rc1 = 0.f, rc2 = 0.f;
+    // the new K/V row is written to the cache by the first pair's workgroup only (the others
+    // compute it for their own use)
     const bool kv_wave = last && wave == WAVES - 1;
+    const bool kv_write = kv_wave && pair == 0;
     if constexpr (ROPE) {
         const float* cal =
             a.c.k_calibration + slot * a.c.cal_stride_slot + hk * a.c.cal_stride_head;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            const uint16_t* src = a.q + b * a.q_sb + (2 * hk + h) * a.q_sh;
+            const uint16_t* src = a.q + b * a.q_sb + (h ? qh1 : qh0) * a.q_sh;
             rq1[h] = src[lane];
             rq2[h] = src[lane + 64];
         }
@@ -410,7 +433,7 @@ __attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_attenti
     } else {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            const uint16_t* qp = a.q + b * a.q_sb + (2 * hk + h) * a.q_sh + 16 * cc;
+            const uint16_t* qp = a.q + b * a.q_sb + (h ? qh1 : qh0) * a.q_sh + 16 * cc;
             qraw[h][0] = *reinterpret_cast<const uint4*>(qp);
             qraw[h][1] = *reinterpret_cast<const uint4*>(qp + 8);
         }
@@ -449,18 +472,24 @@ __attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_attenti
                           bf16_to_f32(rkw2), cs, sn, a.eps, o1, o2);
             int32_t q1, q2;
             const float sk = quantize_row_wave(o1 / rc1, o2 / rc2, q1, q2);
-            a.c.k[base + lane] = (int8_t)q1;
-            a.c.k[base + lane + 64] = (int8_t)q2;
+            if (kv_write) {
+                a.c.k[base + lane] = (int8_t)q1;
+                a.c.k[base + lane + 64] = (int8_t)q2;
+            }
             s_new[0][lane] = (int8_t)q1;
             s_new[0][lane + 64] = (int8_t)q2;
             const float sv = quantize_row_wave(bf16_to_f32(rv1), bf16_to_f32(rv2), q1, q2);
-            a.c.v[base + lane] = (int8_t)q1;
-            a.c.v[base + lane + 64] = (int8_t)q2;
+            if (kv_write) {
+                a.c.v[base + lane] = (int8_t)q1;
+                a.c.v[base + lane + 64] = (int8_t)q2;
+            }
             s_new[1][lane] = (int8_t)q1;
             s_new[1][lane + 64] = (int8_t)q2;
             if (lane == 0) {
-                a.c.k_scale[sidx] = sk;
-                a.c.v_scale[sidx] = sv;
+                if (kv_write) {
+                    a.c.k_scale[sidx] = sk;
+                    a.c.v_scale[sidx] = sv;
+                }
                 s_new_scale[0] = sk;
                 s_new_scale[1] = sv;
             }
@@ -536,8 +565,9 @@ __attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_attenti
     }
     // the lane group derived afresh from the thread index for the masked blocks below: kept
     // from the prologue it is a register the loop needs
-    int tid_m = threadIdx.x;
+    int tid_m = lane_id();
     asm volatile("" : "+v"(tid_m));
+    tid_m += IE_WAVE * wave;
     const int gm = (tid_m & 63) >> 3;
     if (nfull < cw) {
         block_scores<true>(s, kr, qh, qoff, t0 + 4 * gm, t_end);
@@ -596,8 +626,9 @@ __attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_attenti
     __shared__ float s_m[WAVES][2], s_l[WAVES][2];
     // the lane's channel group, derived afresh from the thread index: keeping the prologue's copy
     // alive across the loop costs a register the loop needs
-    int tid = threadIdx.x;
+    int tid = lane_id();
     asm volatile("" : "+v"(tid));
+    tid += IE_WAVE * wave;
     const int ccm = tid & 7;
     if (g == 0) {
 #pragma unroll
@@ -617,7 +648,7 @@ __attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_attenti
     float num[PER], den[PER], mxo[PER];
 #pragma unroll
     for (int u = 0; u < PER; ++u) {
-        const int idx = threadIdx.x + u * THREADS;
+        const int idx = tid + u * THREADS;
         const int h = (idx >> 7) & 1, d = idx & 127;
         float mx = -INFINITY;
 #pragma unroll
@@ -634,10 +665,14 @@ __attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_attenti
         mxo[u] = mx;
     }
     auto out_of = [&](int u) {
-        const int idx = threadIdx.x + u * THREADS;
-        return a.out + b * a.o_sb + (2 * hk + ((idx >> 7) & 1)) * a.o_sh + (idx & 127);
+        const int idx = tid + u * THREADS;
+        return a.out + b * a.o_sb + (qh0 + ((idx >> 7) & 1)) * a.o_sh + (idx & 127);
     };
-    auto active = [&](int u) { return threadIdx.x + u * THREADS < 2 * DA_D; };
+    // thread idx's output exists (the second head of a one-head pair does not)
+    auto active = [&](int u) {
+        const int idx = tid + u * THREADS;
+        return idx < (has2 ? 2 : 1) * DA_D;
+    };
     if (wk.needed == 1) {
 #pragma unroll
         for (int u = 0; u < PER; ++u)
@@ -651,23 +686,23 @@ __attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_attenti
 #pragma unroll
     for (int u = 0; u < PER; ++u) {
         if (!active(u)) continue;
-        const int idx = threadIdx.x + u * THREADS;
+        const int idx = tid + u * THREADS;
         const int d = idx & 127;
-        const int64_t row = (int64_t)(2 * hk + ((idx >> 7) & 1)) * a.nwork + item;
+        const int64_t row = (int64_t)(qh0 + ((idx >> 7) & 1)) * a.nwork + item;
         st_dev(a.part_acc + row * DA_D + d, num[u]);
         if (d == 0) {
             st_dev(a.part_m + row, mxo[u]);
             st_dev(a.part_l + row, den[u]);
         }
     }
-    if (!arrive_last(a.arrivals + b * a.hkv + hk, wk.needed)) return;
+    if (!arrive_last(a.arrivals + b * a.units + unit, wk.needed)) return;
     const int needed = wk.needed;
 #pragma unroll
     for (int u = 0; u < PER; ++u) {
         if (!active(u)) continue;
-        const int idx = threadIdx.x + u * THREADS;
+        const int idx = tid + u * THREADS;
         const int d = idx & 127;
-        const int64_t row0 = (int64_t)(2 * hk + ((idx >> 7) & 1)) * a.nwork + (item - split);
+        const int64_t row0 = (int64_t)(qh0 + ((idx >> 7) & 1)) * a.nwork + (item - split);
         constexpr int CB = 8;  // partials per load batch: one memory round trip each
         float av[CB], ml[CB][2];
         auto load_batch = [&](int s0) {
@@ -741,19 +776,27 @@ struct Layout {
     size_t arr_off, acc_off, m_off, l_off, bytes;
 };
 
-static Layout workspace_layout(int batch, int hq, int hkv) {
+// The layout of a launch of `units` units (decode_units). The count region has a count per
+// sequence and query head, the most any GQA ratio needs (one per sequence and unit), so every
+// launch of a batch size finds its counts and partials at the same offsets; the partial rows
+// (one per query head and work entry) fit the largest grid any ratio launches, that of
+// cdiv(hq, 2) units (workspace_size_layout).
+static Layout workspace_layout(int batch, int hq, int units) {
     Layout L;
     batch = std::max(batch, 0);
-    L.waves = decode_waves(batch, hkv);
-    L.target = decode_target(hkv, L.waves);
+    L.waves = decode_waves(batch, units);
+    L.target = decode_target(units, L.waves);
     L.nwork = batch <= L.target ? L.target : L.target + batch;
     const size_t rows = (size_t)hq * L.nwork;
     L.arr_off = 0;
-    L.acc_off = ((size_t)std::max(batch, DA_COUNT_CAP) * hkv * sizeof(uint32_t) + 255) / 256 * 256;
+    L.acc_off = ((size_t)std::max(batch, DA_COUNT_CAP) * hq * sizeof(uint32_t) + 255) / 256 * 256;
     L.m_off = L.acc_off + rows * DA_D * sizeof(float);
     L.l_off = L.m_off + rows * sizeof(float);
     L.bytes = L.l_off + rows * sizeof(float);
     return L;
+}
+static Layout workspace_size_layout(int batch, int hq) {
+    return workspace_layout(batch, hq, std::max(1, (hq + 1) / 2));
 }
 
 }  // namespace ie
@@ -761,25 +804,25 @@ static Layout workspace_layout(int batch, int hq, int hkv) {
 using namespace ie;
 
 extern "C" size_t ie_decode_attention_workspace_counts_bytes(int32_t batch,
-                                                             int32_t num_kv_heads) {
-    if (num_kv_heads <= 0) return 0;
-    return workspace_layout(batch, 2 * num_kv_heads, num_kv_heads).acc_off;
+                                                             int32_t num_q_heads) {
+    if (num_q_heads <= 0) return 0;
+    return workspace_size_layout(batch, num_q_heads).acc_off;
 }
 
-extern "C" int32_t ie_decode_attention_max_splits(int32_t num_kv_heads) {
-    return decode_target(num_kv_heads, 2);  // the largest target of any launch shape
+extern "C" int32_t ie_decode_attention_max_splits(int32_t num_units) {
+    return decode_target(num_units, 2);  // the largest target of any launch shape
 }
 
-extern "C" int32_t ie_decode_attention_target(int32_t batch, int32_t num_kv_heads) {
-    if (batch <= 0 || num_kv_heads <= 0) return 0;
-    return decode_target(num_kv_heads, decode_waves(batch, num_kv_heads));
+extern "C" int32_t ie_decode_attention_target(int32_t batch, int32_t num_units) {
+    if (batch <= 0 || num_units <= 0) return 0;
+    return decode_target(num_units, decode_waves(batch, num_units));
 }
 
 extern "C" size_t ie_decode_attention_workspace_size(int32_t batch, int32_t num_q_heads,
                                                      int32_t head_dim) {
     (void)head_dim;
-    // Hkv = Hq / 2 is the only geometry the kernels take.
-    return workspace_layout(batch, num_q_heads, std::max(1, num_q_heads / 2)).bytes;
+    if (num_q_heads <= 0) return 0;
+    return workspace_size_layout(batch, num_q_heads).bytes;
 }
 
 // q_rows16: q is read in 16-byte pieces (the plain form; the fused form reads q two bytes per
@@ -792,13 +835,16 @@ static hipError_t check_decode(const ie_bf16* q, int32_t batch, int32_t num_q_he
     hipError_t e = check_cache(cache);
     if (e != hipSuccess) return e;
     IE_REQUIRE(batch >= 0, "negative batch");
-    IE_REQUIRE(num_q_heads == 2 * cache->num_kv_heads, "num_q_heads must be 2 * num_kv_heads");
+    IE_REQUIRE(num_q_heads > 0 && num_q_heads % cache->num_kv_heads == 0 &&
+                   num_q_heads / cache->num_kv_heads <= 16,
+               "num_q_heads must be num_kv_heads times a GQA ratio of 1 to 16");
     if (batch == 0) return hipSuccess;
     IE_REQUIRE(q && cached_lens && slot_ids && num_decoding && out, "null pointer");
     IE_REQUIRE(!q_rows16 ||
                    ((reinterpret_cast<uintptr_t>(q) & 15) == 0 && q_sb % 8 == 0 && q_sh % 8 == 0),
                "q rows must be 16-byte aligned with contiguous head_dim");
-    *L = workspace_layout(batch, num_q_heads, (int)cache->num_kv_heads);
+    *L = workspace_layout(batch, num_q_heads,
+                          decode_units(num_q_heads, (int)cache->num_kv_heads));
     IE_REQUIRE(workspace != nullptr && workspace_bytes >= L->bytes, "workspace too small");
     IE_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 15) == 0, "workspace must be aligned");
     return hipSuccess;
@@ -832,6 +878,9 @@ static DecodeArgs decode_args(const ie_bf16* q, int64_t q_stride_b, int64_t q_st
     a.nwork = L.nwork;
     a.hq = num_q_heads;
     a.hkv = (int)cache->num_kv_heads;
+    a.ratio = num_q_heads / a.hkv;
+    a.npairs = (a.ratio + 1) / 2;
+    a.units = a.hkv * a.npairs;
     a.batch = batch;
     return a;
 }
@@ -850,12 +899,20 @@ static hipError_t decode_launch(DecodeArgs& a, const Layout& L, int32_t batch,
     // IE_DECODE_HEAD_FAST_MIN_BATCH (0: never) is set.
     a.head_fast = IE_DECODE_HEAD_FAST_MIN_BATCH > 0 && batch >= IE_DECODE_HEAD_FAST_MIN_BATCH &&
                   pieces <= 65535;  // the grid's y dimension holds at most 65535
-    const dim3 grid = a.head_fast ? dim3((unsigned)cache->num_kv_heads, pieces)
-                                  : dim3(pieces, (unsigned)cache->num_kv_heads);
-    switch (L.waves) {
-        case 8: hipLaunchKernelGGL((decode_attention_kernel<8, ROPE>), grid, dim3(512), 0, stream, a); break;
-        case 4: hipLaunchKernelGGL((decode_attention_kernel<4, ROPE>), grid, dim3(256), 0, stream, a); break;
-        default: hipLaunchKernelGGL((decode_attention_kernel<2, ROPE>), grid, dim3(128), 0, stream, a); break;
+    const dim3 grid = a.head_fast ? dim3((unsigned)a.hkv, pieces, (unsigned)a.npairs)
+                                  : dim3(pieces, (unsigned)a.hkv, (unsigned)a.npairs);
+    if (a.ratio == 2) {
+        switch (L.waves) {
+            case 8: hipLaunchKernelGGL((decode_attention_kernel<8, ROPE, true>), grid, dim3(512), 0, stream, a); break;
+            case 4: hipLaunchKernelGGL((decode_attention_kernel<4, ROPE, true>), grid, dim3(256), 0, stream, a); break;
+            default: hipLaunchKernelGGL((decode_attention_kernel<2, ROPE, true>), grid, dim3(128), 0, stream, a); break;
+        }
+    } else {
+        switch (L.waves) {
+            case 8: hipLaunchKernelGGL((decode_attention_kernel<8, ROPE, false>), grid, dim3(512), 0, stream, a); break;
+            case 4: hipLaunchKernelGGL((decode_attention_kernel<4, ROPE, false>), grid, dim3(256), 0, stream, a); break;
+            default: hipLaunchKernelGGL((decode_attention_kernel<2, ROPE, false>), grid, dim3(128), 0, stream, a); break;
+        }
     }
     return hipGetLastError();
 }
@@ -909,21 +966,21 @@ extern "C" hipError_t ie_decode_attention_rope(
     return decode_launch<true>(a, L, batch, cache, stream);
 }
 
-extern "C" int32_t ie_decode_attention_grid(int32_t batch, int32_t num_kv_heads) {
-    if (batch <= 0 || num_kv_heads <= 0) return 0;
-    const int target = ie_decode_attention_target(batch, num_kv_heads);
+extern "C" int32_t ie_decode_attention_grid(int32_t batch, int32_t num_units) {
+    if (batch <= 0 || num_units <= 0) return 0;
+    const int target = ie_decode_attention_target(batch, num_units);
     return batch <= target ? target : target + batch;
 }
 
 extern "C" hipError_t ie_decode_attention_plan(const int32_t* cached_lens,
                                                const int32_t* num_decoding, int32_t batch,
-                                               int32_t num_kv_heads, int32_t* rows,
+                                               int32_t num_units, int32_t* rows,
                                                hipStream_t stream) {
-    IE_REQUIRE(batch >= 0 && num_kv_heads > 0, "bad sizes");
+    IE_REQUIRE(batch >= 0 && num_units > 0, "bad sizes");
     if (batch == 0) return hipSuccess;
     IE_REQUIRE(cached_lens && num_decoding && rows, "null pointer");
-    const int target = ie_decode_attention_target(batch, num_kv_heads);
-    hipLaunchKernelGGL(decode_plan_kernel, dim3((unsigned)ie_decode_attention_grid(batch, num_kv_heads)),
+    const int target = ie_decode_attention_target(batch, num_units);
+    hipLaunchKernelGGL(decode_plan_kernel, dim3((unsigned)ie_decode_attention_grid(batch, num_units)),
                        dim3(IE_WAVE), 0, stream, cached_lens, num_decoding, batch, target, rows);
     return hipGetLastError();
 }
@@ -975,8 +1032,11 @@ extern "C" hipError_t ie_decode_attention_noalloc(
     if (e != hipSuccess) return e;
     IE_REQUIRE(batch >= 0, "negative batch");
     if (batch == 0) return hipSuccess;
-    IE_REQUIRE(num_q_heads == 2 * cache->num_kv_heads, "num_q_heads must be 2 * num_kv_heads");
-    const Layout L = workspace_layout(batch, num_q_heads, (int)cache->num_kv_heads);
+    IE_REQUIRE(num_q_heads > 0 && num_q_heads % cache->num_kv_heads == 0 &&
+                   num_q_heads / cache->num_kv_heads <= 16,
+               "num_q_heads must be num_kv_heads times a GQA ratio of 1 to 16");
+    const Layout L =
+        workspace_layout(batch, num_q_heads, decode_units(num_q_heads, (int)cache->num_kv_heads));
     IE_REQUIRE(batch <= DA_COUNT_CAP && L.bytes <= DA_SCRATCH_BYTES,
                "batch too large for the no-alloc decode scratch (at most 1024 sequences in "
                "16 MiB; use ie_decode_attention with a workspace)");

@@ -167,6 +167,9 @@ struct PrefillArgs {
     uint64_t merge_wait_ticks;   // longest wait of a piece for its pair's others (100 MHz clock)
     uint64_t merge_stall_ticks;  // ... and longest wait with no other piece arriving
     int block_m, sub_per_tile, hq, hkv;
+    int ratio;   // query heads per KV head (GQA ratio, 1 ... 16)
+    int npairs;  // query-head pairs per KV head, cdiv(ratio, 2)
+    int units;   // hkv * npairs: the work items of a (sub-block, piece), one per (KV head, pair)
     int nent;  // entries (length of slot_ids; cu_seqlens and cu_cached hold nent + 1)
     int ntok;  // packed rows (length of seq_ids)
     int nsb;   // sub-blocks: num_tiles * sub_per_tile
@@ -299,7 +302,7 @@ __device__ Loc schedule(const PrefillArgs& a, int target, int* tables) {
         int busy = 0;
 #pragma unroll
         for (int c = 0; c < PF_SCHED_CHUNKS; ++c) busy += rs[c] >= 0 ? 1 : 0;
-        if (2 * uni(wave_sum_i(busy)) * a.hkv < a.grid) {
+        if (2 * uni(wave_sum_i(busy)) * a.units < a.grid) {
             Loc L;
             L.found = 0;
             L.straddle = 0;
@@ -369,15 +372,15 @@ __device__ Loc schedule(const PrefillArgs& a, int target, int* tables) {
         for (int c = PF_SCHED_CHUNKS; c < nchunks; ++c) n += f(info(sb_of(c), row_start_of(sb_of(c))));
         return uni(wave_sum_i(n));
     };
-    const int spare = a.grid - parts * a.hkv;
+    const int spare = a.grid - parts * a.units;
     // the straddling form's lower bound on its piece size; it can only be chosen when its
     // pieces beat the separate form's by PF_STRADDLE_MARGIN tiles and the pairs, one piece
     // each, fit the slots
-    int lo = max(PF_MIN_PIECE_TILES, cdiv_i(tot * a.hkv, a.grid));
+    int lo = max(PF_MIN_PIECE_TILES, cdiv_i(tot * a.units, a.grid));
     bool straddle_fits = false;
     auto straddle_check = [&]() {
         straddle_fits = launch_sum([](const SbInfo& z) { return z.npt + z.nct > 0 ? 1 : 0; }) *
-                            a.hkv < a.grid;
+                            a.units < a.grid;
     };
     if (__builtin_expect(spare <= 0, 0)) straddle_check();
     Loc L;
@@ -394,10 +397,10 @@ __device__ Loc schedule(const PrefillArgs& a, int target, int* tables) {
     }
     L.T = PF_UNSPLIT;
     if (spare > 0) {
-        L.T = max(PF_MIN_PIECE_TILES, cdiv_i(tot * a.hkv, spare));
-        for (int T = max(PF_MIN_PIECE_TILES, cdiv_i(tot * a.hkv, a.grid)); T < L.T; ++T) {
+        L.T = max(PF_MIN_PIECE_TILES, cdiv_i(tot * a.units, spare));
+        for (int T = max(PF_MIN_PIECE_TILES, cdiv_i(tot * a.units, a.grid)); T < L.T; ++T) {
             const Divisor D = divisor(T);
-            if (launch_sum([&](const SbInfo& z) { return piece_count(z.npt, z.nct, D); }) * a.hkv <=
+            if (launch_sum([&](const SbInfo& z) { return piece_count(z.npt, z.nct, D); }) * a.units <=
                 a.grid) {
                 L.T = T;
                 break;
@@ -423,7 +426,7 @@ __device__ Loc schedule(const PrefillArgs& a, int target, int* tables) {
             const int mid = (lo + hi) >> 1;
             const Divisor D = divisor(mid);
             if (launch_sum([&](const SbInfo& z) { return straddle_count(z.npt + z.nct, D); }) *
-                    a.hkv <= a.grid)
+                    a.units <= a.grid)
                 hi = mid;
             else
                 lo = mid + 1;
@@ -444,7 +447,7 @@ __device__ Loc schedule(const PrefillArgs& a, int target, int* tables) {
     L.sb = L.off = L.item_base = 0;
     int items_before = 0;
     auto visit = [&](int c, const SbInfo& z, int np) {
-        const int items = np * a.hkv;
+        const int items = np * a.units;
         const int incl = wave_incl_scan_i(items) + items_before;
         const unsigned long long hit = __ballot(target < incl && target >= incl - items);
         if (hit) {
@@ -870,8 +873,21 @@ __device__ __forceinline__ void load_q(bf16x8 (&qf)[2][4], const PrefillArgs& a,
 #define IE_PREFILL_WG_PER_CU (8 / IE_PREFILL_WAVES)
 #endif
 
-__device__ __forceinline__ void merge_pieces(const PrefillArgs& a, const SubBlock& s, int hk,
+__device__ __forceinline__ void merge_pieces(const PrefillArgs& a, const SubBlock& s, int unit,
                                              int item_base);
+
+// The (KV head, query-head pair) of work-item unit `unit`: KV head hk, query heads qh0 and
+// qh0 + 1, the second present unless it is an odd ratio's last pair (has2 false: that wave
+// computes a copy of the first head and stores nothing).
+struct PfUnit {
+    int hk, qh0;
+    bool has2;
+};
+__device__ __forceinline__ PfUnit pf_unit(const PrefillArgs& a, int unit) {
+    if (a.npairs == 1) return PfUnit{unit, unit * a.ratio, a.ratio == 2};
+    const int hk = uni(unit / a.npairs), pair = unit - hk * a.npairs;
+    return PfUnit{hk, uni(a.ratio * hk + 2 * pair), 2 * pair + 1 < a.ratio};
+}
 
 // Tiles [kt_begin, kt_end) of piece `piece` of sub-block s (tile kt < npt: prefix tile kt,
 // else chunk tile kt - npt): the whole pair, a prefix piece, a chunk piece, or in the
@@ -890,8 +906,8 @@ __device__ __forceinline__ void piece_tiles(const SubBlock& s, int piece, int& k
     }
 }
 
-// One work item: tiles [kt_begin, kt_end) of piece `piece` of sub-block s for kv head hk.
-__device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBlock& s, int hk,
+// One work item: tiles [kt_begin, kt_end) of piece `piece` of sub-block s for unit `unit`.
+__device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBlock& s, int unit,
                                              int piece, int item, int item_base, PfLds& lds) {
     int kt_begin, kt_end;
     piece_tiles(s, piece, kt_begin, kt_end);
@@ -899,7 +915,10 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBloc
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int l16 = lane & 15, g = lane >> 4;
-    const int h = 2 * hk + (wave & 1);
+    const PfUnit U = pf_unit(a, unit);
+    const int hk = U.hk;
+    const bool stores = U.has2 || (wave & 1) == 0;  // this wave's head exists
+    const int h = U.has2 ? U.qh0 + (wave & 1) : U.qh0;
     const int wr0 = s.r0 + 32 * (wave >> 1);  // first row of this wave
 
     // two tile buffers: tile i is staged into buffer i & 1 while the other one is computed on;
@@ -1099,7 +1118,7 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBloc
     for (int nt = 0; nt < 2; ++nt) {
         const float l = ws.lsum[nt][0];
         const int row = wr0 + 16 * nt + l16;
-        if (row >= s.r1) continue;
+        if (row >= s.r1 || !stores) continue;
         const float rl = l != 0.f ? 1.f / l : 0.f;
         if (s.npieces == 1) {
             uint16_t* o = a.out + row * a.o_st + h * a.o_sh;
@@ -1129,7 +1148,7 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBloc
         PF_STAMP(7);
         return;
     }
-    merge_pieces(a, s, hk, item_base);
+    merge_pieces(a, s, unit, item_base);
     PF_STAMP(7);
 }
 
@@ -1152,11 +1171,12 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBloc
 // is that one. The words must be zero on entry (the workspace contract). Should they not be,
 // an arrival index k >= npieces takes no share and sets no bit, so every access stays inside
 // the pair's rows; the pair's output is then not merged by this launch.
-__device__ __forceinline__ void merge_pieces(const PrefillArgs& a, const SubBlock& s, int hk,
+__device__ __forceinline__ void merge_pieces(const PrefillArgs& a, const SubBlock& s, int unit,
                                              int item_base) {
     const int np = s.npieces, nrows = s.r1 - s.r0;
-    uint32_t* const arr = a.arrivals + item_base + hk;
-    uint32_t* const fin = a.arrivals + a.grid + item_base + hk;
+    const PfUnit pu = pf_unit(a, unit);
+    uint32_t* const arr = a.arrivals + item_base + unit;
+    uint32_t* const fin = a.arrivals + a.grid + item_base + unit;
     __shared__ int s_k, s_go, s_missing;
     wait_stores();  // this wave's partial is written
     __syncthreads();
@@ -1202,7 +1222,7 @@ __device__ __forceinline__ void merge_pieces(const PrefillArgs& a, const SubBloc
     const rsrc_t pml = make_rsrc(a.part_ml, (uint32_t)a.grid * PF_BM * 2 * 2 * 4);
     // piece p's partial slot; the pair q of the share (head-major: head q / nrows, row q % nrows)
     // is slot row rr = head * PF_BM + row
-    auto slot_of = [&](int p) { return item_base + p * a.hkv + hk; };
+    auto slot_of = [&](int p) { return item_base + p * a.units + unit; };
     auto merge_share = [&](int share) {
         const int npairs = 2 * nrows;
         const int pb = share * npairs / np, pe = (share + 1) * npairs / np;
@@ -1259,7 +1279,8 @@ __device__ __forceinline__ void merge_pieces(const PrefillArgs& a, const SubBloc
                     den += w;
                 }
                 const float rd = den != 0.f ? 1.f / den : 0.f;
-                uint16_t* dst = a.out + row * a.o_st + (2 * hk + hh) * a.o_sh + c0;
+                if (hh && !pu.has2) continue;  // an odd ratio's last pair has one head
+                uint16_t* dst = a.out + row * a.o_st + (pu.qh0 + hh) * a.o_sh + c0;
                 *reinterpret_cast<u32x4*>(dst) = u32x4{
                     pack_bf16x2(num[0] * rd, num[1] * rd), pack_bf16x2(num[2] * rd, num[3] * rd),
                     pack_bf16x2(num[4] * rd, num[5] * rd), pack_bf16x2(num[6] * rd, num[7] * rd)};
@@ -1307,7 +1328,7 @@ __global__ __launch_bounds__(PF_THREADS, IE_PREFILL_WG_PER_CU) void prefill_atte
     PF_STAMP(1);
     PF_STAMP_VALUE(8, loc.found ? loc.s.npieces : 0);
     if (!loc.found) return;
-    prefill_item(a, loc.s, loc.off % a.hkv, loc.off / a.hkv, blockIdx.x, loc.item_base, lds);
+    prefill_item(a, loc.s, loc.off % a.units, loc.off / a.units, blockIdx.x, loc.item_base, lds);
 }
 
 // grid (the prefill launch's grid), block 64: the launch's work list, as the main kernel's own
@@ -1328,7 +1349,7 @@ __global__ __launch_bounds__(IE_WAVE) void prefill_plan_kernel(PrefillArgs a, in
     if (threadIdx.x != 0) return;
     int32_t r[16] = {};
     if (loc.found) {
-        const int hk = loc.off % a.hkv, piece = loc.off / a.hkv;
+        const int hk = loc.off % a.units, piece = loc.off / a.units;
         int kb, ke;
         piece_tiles(loc.s, piece, kb, ke);
         const int v[16] = {1, loc.sb, hk, piece, loc.s.npieces, kb, ke, loc.s.npt, loc.s.nct,
@@ -1372,21 +1393,24 @@ static PrefillWs prefill_ws(int slots) {
 
 using namespace ie;
 
-// The launch's grid: one resident wave of workgroups, or one workgroup per (sub-block, kv head)
-// pair when there are more.
-static int64_t prefill_grid(int64_t nsb, int hkv) {
-    return std::max<int64_t>(prefill_slots(), nsb * hkv);
+// The launch's grid: one resident wave of workgroups, or one workgroup per (sub-block, unit)
+// pair when there are more (a unit is a KV head and one pair of its query heads).
+static int64_t prefill_grid(int64_t nsb, int units) {
+    return std::max<int64_t>(prefill_slots(), nsb * units);
 }
 
 // The schedule's part of the arguments (index arrays and sizes).
 static hipError_t prefill_index_args(PrefillArgs& a, const int32_t* seq_ids,
                                      const int32_t* cu_seqlens, const int32_t* tile_start,
                                      int32_t num_tiles, int32_t block_m, int64_t num_tokens,
-                                     int32_t num_kv_heads, const int32_t* slot_ids,
-                                     const int32_t* cu_cached, int32_t num_entries) {
+                                     int32_t num_q_heads, int32_t num_kv_heads,
+                                     const int32_t* slot_ids, const int32_t* cu_cached,
+                                     int32_t num_entries) {
     IE_REQUIRE(num_tokens >= 0 && num_tiles >= 0, "negative sizes");
     IE_REQUIRE(block_m > 0, "block_m must be positive");
-    IE_REQUIRE(num_kv_heads > 0, "num_kv_heads must be positive");
+    IE_REQUIRE(num_kv_heads > 0 && num_q_heads > 0 && num_q_heads % num_kv_heads == 0 &&
+                   num_q_heads / num_kv_heads <= 16,
+               "num_q_heads must be num_kv_heads times a GQA ratio of 1 to 16");
     IE_REQUIRE(num_entries >= 1, "num_entries (the length of slot_ids) must be at least 1");
     const int64_t nsb = (int64_t)num_tiles * ((block_m + PF_BM - 1) / PF_BM);
     IE_REQUIRE(nsb < (1 << 24), "too many tiles");
@@ -1398,7 +1422,11 @@ static hipError_t prefill_index_args(PrefillArgs& a, const int32_t* seq_ids,
     a.cu_cached = cu_cached;
     a.block_m = block_m;
     a.sub_per_tile = (block_m + PF_BM - 1) / PF_BM;
+    a.hq = num_q_heads;
     a.hkv = num_kv_heads;
+    a.ratio = num_q_heads / num_kv_heads;
+    a.npairs = (a.ratio + 1) / 2;
+    a.units = num_kv_heads * a.npairs;
     a.nent = num_entries;
     a.ntok = (int)num_tokens;
     a.nsb = (int)nsb;
@@ -1427,10 +1455,10 @@ extern "C" hipError_t ie_prefill_attention(
     hipStream_t stream) {
     hipError_t e = check_cache(cache);
     if (e != hipSuccess) return e;
-    IE_REQUIRE(num_q_heads == 2 * cache->num_kv_heads, "num_q_heads must be 2 * num_kv_heads");
     PrefillArgs a{};
     e = prefill_index_args(a, seq_ids, cu_seqlens, tile_start, num_tiles, block_m, num_tokens,
-                           (int32_t)cache->num_kv_heads, slot_ids, cu_cached, num_entries);
+                           num_q_heads, (int32_t)cache->num_kv_heads, slot_ids, cu_cached,
+                           num_entries);
     if (e != hipSuccess) return e;
     if (num_tokens == 0 || num_tiles == 0) return hipSuccess;
     IE_REQUIRE(q && k && v && seq_ids && cu_seqlens && tile_start && slot_ids && cu_cached && out,
@@ -1468,36 +1496,40 @@ extern "C" hipError_t ie_prefill_attention(
     a.arrivals = (uint32_t*)workspace;
     a.part_ml = (float*)((char*)workspace + wsl.ml_off);
     a.part_o = (uint16_t*)((char*)workspace + wsl.o_off);
-    a.hq = num_q_heads;
     a.qk_scale = (float)(0.08838834764831845 * 1.4426950408889634);  // D^-0.5 * log2(e), D = 128
     a.merge_wait_ticks = env_us_ticks("IE_PREFILL_MERGE_WAIT_US", 100);
     a.merge_stall_ticks = env_us_ticks("IE_PREFILL_MERGE_STALL_US", 20);
-    const unsigned grid = (unsigned)prefill_grid(a.nsb, a.hkv);
+    const unsigned grid = (unsigned)prefill_grid(a.nsb, a.units);
     hipLaunchKernelGGL(prefill_attention_kernel, dim3(grid), dim3(PF_THREADS), 0, stream, a);
     return hipGetLastError();
 }
 
 extern "C" int32_t ie_prefill_attention_grid(int32_t num_tiles, int32_t block_m,
-                                             int32_t num_kv_heads) {
-    if (num_tiles <= 0 || block_m <= 0 || num_kv_heads <= 0) return 0;
+                                             int32_t num_q_heads, int32_t num_kv_heads) {
+    if (num_tiles <= 0 || block_m <= 0 || num_kv_heads <= 0 || num_q_heads <= 0 ||
+        num_q_heads % num_kv_heads != 0)
+        return 0;
     const int64_t nsb = (int64_t)num_tiles * ((block_m + PF_BM - 1) / PF_BM);
-    return (int32_t)std::min<int64_t>(prefill_grid(nsb, num_kv_heads), INT32_MAX);
+    const int units = num_kv_heads * ((num_q_heads / num_kv_heads + 1) / 2);
+    return (int32_t)std::min<int64_t>(prefill_grid(nsb, units), INT32_MAX);
 }
 
 extern "C" hipError_t ie_prefill_attention_plan(const int32_t* seq_ids, const int32_t* cu_seqlens,
                                                 const int32_t* tile_start, int32_t num_tiles,
                                                 int32_t block_m, int64_t num_tokens,
-                                                int32_t num_kv_heads, const int32_t* slot_ids,
+                                                int32_t num_q_heads, int32_t num_kv_heads,
+                                                const int32_t* slot_ids,
                                                 const int32_t* cu_cached, int32_t num_entries,
                                                 int32_t* rows, hipStream_t stream) {
     PrefillArgs a{};
     hipError_t e = prefill_index_args(a, seq_ids, cu_seqlens, tile_start, num_tiles, block_m,
-                                      num_tokens, num_kv_heads, slot_ids, cu_cached, num_entries);
+                                      num_tokens, num_q_heads, num_kv_heads, slot_ids, cu_cached,
+                                      num_entries);
     if (e != hipSuccess) return e;
     if (num_tiles == 0) return hipSuccess;
     IE_REQUIRE(seq_ids && cu_seqlens && tile_start && slot_ids && cu_cached && rows,
                "null pointer");
-    const unsigned grid = (unsigned)prefill_grid(a.nsb, a.hkv);
+    const unsigned grid = (unsigned)prefill_grid(a.nsb, a.units);
     hipLaunchKernelGGL(prefill_plan_kernel, dim3(grid), dim3(IE_WAVE), 0, stream, a, rows);
     return hipGetLastError();
 }

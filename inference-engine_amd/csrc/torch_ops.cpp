@@ -354,7 +354,7 @@ void decode_attention(const at::Tensor& q, const at::Tensor& k_cache, const at::
     DecodeCall d = decode_prep(q, k_cache, v_cache, k_scale, v_scale, k_calibration, cached_lens,
                                slot_ids, num_decoding, out);
     at::Tensor ws = persistent_workspace(
-        q, d.ws_bytes, ie_decode_attention_workspace_counts_bytes(d.B, (int32_t)d.c.num_kv_heads),
+        q, d.ws_bytes, ie_decode_attention_workspace_counts_bytes(d.B, d.hq),
         d.B <= 1024 ? 0 : d.B);
     ok(ie_decode_attention(bf(q), q.stride(0), q.stride(1), d.B, d.hq, &d.c, i32(cached_lens),
                            i32(slot_ids), i32(num_decoding), (float)scale, bfm(out),
@@ -388,7 +388,7 @@ void decode_attention_rope(const at::Tensor& q, const at::Tensor& k, const at::T
     TORCH_CHECK(cos.size(0) >= d.B && sin.size(0) >= d.B && cos.size(2) == 64 && sin.size(2) == 64,
                 "ie: cos/sin must be [B,1,64]");
     at::Tensor ws = persistent_workspace(
-        q, d.ws_bytes, ie_decode_attention_workspace_counts_bytes(d.B, (int32_t)d.c.num_kv_heads),
+        q, d.ws_bytes, ie_decode_attention_workspace_counts_bytes(d.B, d.hq),
         d.B <= 1024 ? 0 : d.B);
     ok(ie_decode_attention_rope(bf(q), q.stride(0), q.stride(1), bf(k), k.stride(0), k.stride(1),
                                 bf(v), v.stride(0), v.stride(1), bf(q_norm_weight),

@@ -31,13 +31,13 @@ def randn_bf16(shape, gen, device="cpu") -> torch.Tensor:
     return torch.randn(shape, generator=gen, device=device, dtype=torch.float32).to(torch.bfloat16)
 
 
-def empty_cache(pool, max_len, device="cpu") -> LayerKVCache:
+def empty_cache(pool, max_len, device="cpu", hkv: int = HKV) -> LayerKVCache:
     return LayerKVCache(
-        k=torch.zeros(pool, HKV, max_len, D, dtype=torch.int8, device=device),
-        v=torch.zeros(pool, HKV, max_len, D, dtype=torch.int8, device=device),
-        k_scale=torch.zeros(pool, HKV, max_len, dtype=torch.float32, device=device),
-        v_scale=torch.zeros(pool, HKV, max_len, dtype=torch.float32, device=device),
-        k_calibration=torch.ones(pool, HKV, 1, D, dtype=torch.float32, device=device),
+        k=torch.zeros(pool, hkv, max_len, D, dtype=torch.int8, device=device),
+        v=torch.zeros(pool, hkv, max_len, D, dtype=torch.int8, device=device),
+        k_scale=torch.zeros(pool, hkv, max_len, dtype=torch.float32, device=device),
+        v_scale=torch.zeros(pool, hkv, max_len, dtype=torch.float32, device=device),
+        k_calibration=torch.ones(pool, hkv, 1, D, dtype=torch.float32, device=device),
     )
 
 
@@ -49,8 +49,9 @@ def fill_rows(cache: LayerKVCache, slot: int, n: int, gen, calibrate=False,
     if n <= 0:
         return
     dev = cache.k.device
-    k = randn_bf16((HKV, n, D), gen, dev).float()
-    v = randn_bf16((HKV, n, D), gen, dev).float()
+    hkv = cache.k.shape[1]
+    k = randn_bf16((hkv, n, D), gen, dev).float()
+    v = randn_bf16((hkv, n, D), gen, dev).float()
     if v_mult != 1.0:
         v = (v * v_mult).to(torch.bfloat16).float()
     if calibrate:
@@ -85,7 +86,8 @@ class DecodeWorkload:
 
     def algorithmic_bytes(self) -> int:
         """int8 K+V rows and fp32 scales read, bf16 q read and out written."""
-        return sum(self.ctx) * HKV * (2 * D + 2 * 4) + len(self.ctx) * HQ * D * 2 * 2
+        hq, hkv = self.q.shape[1], self.cache.k.shape[1]
+        return sum(self.ctx) * hkv * (2 * D + 2 * 4) + len(self.ctx) * hq * D * 2 * 2
 
 
 def decode_ctx_lens(config: str, seed: int = 0) -> list:
@@ -103,25 +105,26 @@ def decode_ctx_lens(config: str, seed: int = 0) -> list:
 
 def decode_workload(ctx: list, seed: int = 0, device="cpu", max_len=None, pool=None,
                     num_decoding=None, v_mult: float = 1.0,
-                    sink_alpha: float = 0.0) -> DecodeWorkload:
+                    sink_alpha: float = 0.0, hq: int = HQ, hkv: int = HKV) -> DecodeWorkload:
     """Decode batch with the given per-sequence contexts; slots are a seeded permutation.
 
     v_mult scales the V source (the V scales scale with it). sink_alpha > 0 makes token 0 of
     every sequence an attention sink for the first query head of each KV head: its K is
     sink_alpha * q of that head (quantized like every row), so that token's score stands
-    sink_alpha * |q|^2 / sqrt(D) above the N(0, 1) scores of the other tokens."""
+    sink_alpha * |q|^2 / sqrt(D) above the N(0, 1) scores of the other tokens. hq, hkv: query
+    and KV heads (default Qwen3-1.7B's 16 and 8)."""
     B = len(ctx)
     gen = torch.Generator(device=device).manual_seed(seed)
     max_len = max_len or int(math.ceil(max(ctx) / 64) * 64)
     pool = pool or B + 1
-    q = randn_bf16((B, HQ, D), gen, device)
+    q = randn_bf16((B, hq, D), gen, device)
     perm = torch.randperm(pool, generator=torch.Generator().manual_seed(seed + 1))[:B]
-    cache = empty_cache(pool, max_len, device)
+    cache = empty_cache(pool, max_len, device, hkv)
     for b in range(B):
         fill_rows(cache, int(perm[b]), ctx[b], gen, v_mult=v_mult)
         if sink_alpha:
             slot = int(perm[b])
-            k0 = (q[b, 0::HQ // HKV].float() * sink_alpha).to(torch.bfloat16).float()  # [HKV, D]
+            k0 = (q[b, 0::hq // hkv].float() * sink_alpha).to(torch.bfloat16).float()  # [hkv, D]
             kq, ks = quantize_rows(k0)
             cache.k[slot, :, 0] = kq
             cache.k_scale[slot, :, 0] = ks
@@ -148,12 +151,14 @@ class MixedWorkload:
 
 def mixed_workload(decode_ctx: list, chunks: list, seed: int = 0, block_m: int = 128,
                    max_len: int = 4096, num_entries: int | None = None, pool: int | None = None,
-                   n_pad: int | None = None, device="cpu") -> MixedWorkload:
+                   n_pad: int | None = None, device="cpu", hq: int = HQ,
+                   hkv: int = HKV) -> MixedWorkload:
     """Config-4-shaped step: decoders with `decode_ctx` tokens attended, then prefill chunks
     (chunk_len, cached_len). A prefilling entry's cached prefix is filled with calibration
     (its first chunk computed one), decoders' rows without. Entry b uses cache slot b; the
     last slot of the pool (default num_entries + 1 slots) is the scratch slot of the padding
-    and unused entries. n_pad (default: the token count) pads the step to a token bucket."""
+    and unused entries. n_pad (default: the token count) pads the step to a token bucket. hq,
+    hkv: query and KV heads (default 16 and 8)."""
     gen = torch.Generator().manual_seed(seed)
     nd = len(decode_ctx)
     B = nd + len(chunks)
@@ -161,7 +166,7 @@ def mixed_workload(decode_ctx: list, chunks: list, seed: int = 0, block_m: int =
     pool = pool or S + 1
     assert pool > B
     scratch = pool - 1
-    cache = empty_cache(pool, max_len)
+    cache = empty_cache(pool, max_len, hkv=hkv)
     plan = []
     for i, c in enumerate(decode_ctx):
         fill_rows(cache, i, c - 1, gen)  # the new token is written by fused_rope_kv_decode
@@ -172,10 +177,10 @@ def mixed_workload(decode_ctx: list, chunks: list, seed: int = 0, block_m: int =
         plan.append((cached, slot, [0] * L))
     N = n_pad or sum(len(t) for _, _, t in plan)
     step = fill_inputs(plan, nd, N, S, block_m, scratch)
-    qkv = randn_bf16((N, (HQ + 2 * HKV) * D), gen)
-    q = qkv[:, : HQ * D].reshape(N, HQ, D).contiguous()
-    k = qkv[:, HQ * D:(HQ + HKV) * D].reshape(N, HKV, D).contiguous()
-    v = qkv.view(N, HQ + 2 * HKV, D)[:, HQ + HKV:]
+    qkv = randn_bf16((N, (hq + 2 * hkv) * D), gen)
+    q = qkv[:, : hq * D].reshape(N, hq, D).contiguous()
+    k = qkv[:, hq * D:(hq + hkv) * D].reshape(N, hkv, D).contiguous()
+    v = qkv.view(N, hq + 2 * hkv, D)[:, hq + hkv:]
     inputs = step.to_device("cpu")
     wl = MixedWorkload(q, k, v, cache, inputs, block_m, list(decode_ctx), list(chunks))
     return wl if device == "cpu" else mixed_to(wl, device)
@@ -185,10 +190,10 @@ def mixed_to(wl: MixedWorkload, device) -> MixedWorkload:
     c = wl.cache
     qkv_v = wl.v.to(device) if wl.v.is_contiguous() else None
     if qkv_v is None:  # keep v a strided view with the same token stride
-        N = wl.v.shape[0]
-        base = torch.empty(N, (HQ + 2 * HKV), D, dtype=wl.v.dtype, device=device)
-        base[:, HQ + HKV:] = wl.v.to(device)
-        qkv_v = base[:, HQ + HKV:]
+        N, hq, hkv = wl.v.shape[0], wl.q.shape[1], wl.k.shape[1]
+        base = torch.empty(N, (hq + 2 * hkv), D, dtype=wl.v.dtype, device=device)
+        base[:, hq + hkv:] = wl.v.to(device)
+        qkv_v = base[:, hq + hkv:]
     return MixedWorkload(
         wl.q.to(device), wl.k.to(device), qkv_v,
         LayerKVCache(*(t.to(device) for t in (c.k, c.v, c.k_scale, c.v_scale, c.k_calibration))),

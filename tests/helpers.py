@@ -72,23 +72,26 @@ PLAN_FIELDS = ("found", "sb", "hk", "piece", "npieces", "kt_begin", "kt_end", "n
                "r1", "seq_start", "P", "T", "straddle", "item_base")
 
 
-def prefill_plan(native, g, num_kv_heads: int = 8) -> np.ndarray:
+def prefill_plan(native, g) -> np.ndarray:
     """The prefill launch's work list for the device-resident mixed workload `g`, as the kernel's
     own schedule computes it (ie_prefill_attention_plan through the C ABI): one row per
-    workgroup of the launch, fields PLAN_FIELDS; only rows with found == 1 carry work."""
+    workgroup of the launch, fields PLAN_FIELDS ("hk" is the work unit: KV head x query-head
+    pair, the KV head itself at GQA 2); only rows with found == 1 carry work."""
     import ctypes
 
     lib = native.cabi()
     gi = g.inputs
     ts = gi["tile_start"]
+    hq, hkv = g.q.shape[1], g.cache.k.shape[1]
     grid = lib.ie_prefill_attention_grid(ctypes.c_int32(ts.shape[0]), ctypes.c_int32(g.block_m),
-                                         ctypes.c_int32(num_kv_heads))
+                                         ctypes.c_int32(hq), ctypes.c_int32(hkv))
     rows = torch.full((grid, 16), -7, dtype=torch.int32, device=ts.device)
     fn = lib.ie_prefill_attention_plan
     fn.restype = ctypes.c_int
     p = lambda t: ctypes.c_void_p(t.data_ptr())
     rc = fn(p(gi["seq_ids"]), p(gi["cu_seqlens"]), p(ts), ctypes.c_int32(ts.shape[0]),
-            ctypes.c_int32(g.block_m), ctypes.c_int64(g.q.shape[0]), ctypes.c_int32(num_kv_heads),
+            ctypes.c_int32(g.block_m), ctypes.c_int64(g.q.shape[0]), ctypes.c_int32(hq),
+            ctypes.c_int32(hkv),
             p(gi["slot_ids"]), p(gi["cu_cached"]), ctypes.c_int32(gi["slot_ids"].shape[0]),
             p(rows), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
     assert rc == 0, lib.ie_attn_last_error()

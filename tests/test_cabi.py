@@ -54,10 +54,9 @@ def test_bad_geometry_rejected_on_host(native):
 
 
 def test_workspace_size_formula(native):
-    """The arrival counts (one uint32 per sequence and KV head, room for at least 1024 sequences,
-    padded to 256 bytes), then one
-    fp32 partial (128 outputs, m, l) per query head and work entry; the work entries are the
-    launch's grid: the target, or target + B above it."""
+    """The arrival counts (one uint32 per sequence and query head, room for at least 1024
+    sequences, padded to 256 bytes), then one fp32 partial (128 outputs, m, l) per query head and
+    work entry; the work entries are the launch's grid: the target, or target + B above it."""
     lib = native.cabi()
     t_max = lib.ie_decode_attention_max_splits(8)
     assert t_max >= 1
@@ -71,8 +70,10 @@ def test_workspace_size_formula(native):
         prev = target
         grid = lib.ie_decode_attention_grid(ctypes.c_int32(B), ctypes.c_int32(8))
         assert grid == (target if B <= target else target + B)
-        plan = -(-(max(B, 1024) * 8) * 4 // 256) * 256
-        assert lib.ie_decode_attention_workspace_size(B, 16, 128) == plan + 16 * grid * 130 * 4
+        # counts: one per sequence and query head (the most any GQA ratio uses); partials: one
+        # per query head and work entry of the largest grid (cdiv(Hq, 2) units: GQA 2)
+        counts = -(-(max(B, 1024) * 16) * 4 // 256) * 256
+        assert lib.ie_decode_attention_workspace_size(B, 16, 128) == counts + 16 * grid * 130 * 4
 
 
 def test_ops_refuse_cpu_tensors(ie):
@@ -124,17 +125,22 @@ def test_workspace_count_regions_and_prefill_grid(native):
     workgroup per (128-row sub-block, KV head), whichever is more."""
     lib = native.cabi()
     for B in (1, 64, 1024, 1025, 3000):
-        want = -(-(max(B, 1024) * 8 * 4) // 256) * 256
-        assert lib.ie_decode_attention_workspace_counts_bytes(B, 8) == want
+        for hq in (16, 32, 2):
+            want = -(-(max(B, 1024) * hq * 4) // 256) * 256
+            assert lib.ie_decode_attention_workspace_counts_bytes(B, hq) == want
     lib.ie_prefill_attention_workspace_size.restype = ctypes.c_size_t
     ws = lib.ie_prefill_attention_workspace_size(ctypes.c_int32(8), ctypes.c_int32(128),
                                                  ctypes.c_int32(8))
     cb = lib.ie_prefill_attention_workspace_counts_bytes()
-    slots = lib.ie_prefill_attention_grid(1, 128, 8)  # one sub-block: the resident wave
+    slots = lib.ie_prefill_attention_grid(1, 128, 16, 8)  # one sub-block: the resident wave
     assert cb == -(-(2 * slots * 4) // 256) * 256 and 0 < cb < ws
     for tiles, bm in ((1, 128), (64, 128), (300, 128), (300, 192), (1000, 16)):
         nsb = tiles * -(-bm // 128)
-        assert lib.ie_prefill_attention_grid(tiles, bm, 8) == max(slots, nsb * 8)
+        # one workgroup per (sub-block, KV head x query-head pair) when they outnumber the slots
+        for hq, hkv in ((16, 8), (32, 8), (40, 8), (8, 8), (2, 1)):
+            units = hkv * ((hq // hkv + 1) // 2)
+            assert lib.ie_prefill_attention_grid(tiles, bm, hq, hkv) == max(slots, nsb * units)
+    assert lib.ie_prefill_attention_grid(4, 128, 12, 8) == 0  # not a multiple: no launch
 
 
 def test_prefill_plan_rejects_bad_sizes_on_host(native):
@@ -142,9 +148,12 @@ def test_prefill_plan_rejects_bad_sizes_on_host(native):
     fn = lib.ie_prefill_attention_plan
     fn.restype = ctypes.c_int
     p, null = ctypes.c_void_p(256), ctypes.c_void_p(0)
-    rc = fn(p, p, p, ctypes.c_int32(4), ctypes.c_int32(0), ctypes.c_int64(100), ctypes.c_int32(8),
-            p, p, ctypes.c_int32(3), p, null)
+    i32 = ctypes.c_int32
+    rc = fn(p, p, p, i32(4), i32(0), ctypes.c_int64(100), i32(16), i32(8), p, p, i32(3), p, null)
     assert rc == HIP_ERROR_INVALID_VALUE and b"block_m" in lib.ie_attn_last_error()
-    rc = fn(p, p, p, ctypes.c_int32(4), ctypes.c_int32(128), ctypes.c_int64(100),
-            ctypes.c_int32(8), p, p, ctypes.c_int32(0), p, null)
+    rc = fn(p, p, p, i32(4), i32(128), ctypes.c_int64(100), i32(16), i32(8), p, p, i32(0), p, null)
     assert rc == HIP_ERROR_INVALID_VALUE and b"num_entries" in lib.ie_attn_last_error()
+    for hq, hkv in ((12, 8), (136, 8)):  # not a multiple; a ratio above 16
+        rc = fn(p, p, p, i32(4), i32(128), ctypes.c_int64(100), i32(hq), i32(hkv), p, p, i32(3),
+                p, null)
+        assert rc == HIP_ERROR_INVALID_VALUE and b"GQA ratio" in lib.ie_attn_last_error()
