@@ -68,11 +68,28 @@ def time_decode(ie, wls, steps, warmup):
     return e0.elapsed_time(e1) / steps
 
 
+SETTLE_S = 0.15  # minimum warm-up wall time of an extra line (--settle-ms)
+
+
+def settle(fn):
+    """Keeps calling fn until SETTLE_S seconds have passed since the first call. After a second
+    of idle the device's clocks need tens of milliseconds of load to come back up: a 241 µs
+    prefill ran its first 25 calls at 290 µs on average and reached 241 µs only after ~150 calls,
+    so a few warm-up calls leave the timed calls in the ramp."""
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < SETTLE_S:
+        for _ in range(10):
+            fn()
+        torch.cuda.synchronize()
+
+
 def time_op(fn, steps, warmup):
     """Average time of back-to-back calls between two events: events around every call of a
-    microsecond-scale kernel would add several microseconds of their own per call."""
+    microsecond-scale kernel would add several microseconds of their own per call. Warm-up: the
+    `warmup` calls, then more until SETTLE_S seconds have passed (untimed)."""
     for _ in range(warmup):
         fn()
+    settle(fn)
     torch.cuda.synchronize()
     e0, e1 = _events(2)
     e0.record()
@@ -117,8 +134,7 @@ def time_graph(fn, calls=20, reps=5):
     with torch.cuda.graph(g, stream=s):  # the warmed-up stream: its workspaces exist
         for _ in range(calls):
             fn()
-    g.replay()
-    torch.cuda.synchronize()
+    settle(g.replay)
     e0, e1 = _events(2)
     e0.record()
     for _ in range(reps):
@@ -190,8 +206,7 @@ def time_graph_calls(fns, reps=3):
     with torch.cuda.graph(g, stream=s):
         for f in fns:
             f()
-    g.replay()
-    torch.cuda.synchronize()
+    settle(g.replay)
     e0, e1 = _events(2)
     e0.record()
     for _ in range(reps):
@@ -283,11 +298,17 @@ def bench_mixed_step(W, dev):
     w = torch.ones(2, 128, dtype=torch.bfloat16, device=dev)
     cos, sin = al.rope_tables(gi["positions"], al.rope_inv_freq(128, 1e6, dev))
     ps = al.PrefixScratch(None, None, gi["cu_cached"])
-    op = lambda: al.attention(q, k, v, gi["seq_ids"], gi["cu_seqlens"], cos, sin, wl.cache,
-                              gi["cached_lens"], gi["slot_ids"], gi["tile_start"], wl.block_m, ps,
-                              gi["num_decoding"], w[0], w[1], 1e-6)
+    op = lambda plan=None: al.attention(q, k, v, gi["seq_ids"], gi["cu_seqlens"], cos, sin,
+                                        wl.cache, gi["cached_lens"], gi["slot_ids"],
+                                        gi["tile_start"], wl.block_m, ps, gi["num_decoding"],
+                                        w[0], w[1], 1e-6, plan)
     ms = time_graph(op)
-    return {"us_graph": round(ms * 1e3, 2), "rows": N, "decoders": len(wl.decode_ctx),
+    plan = importlib.import_module("inference-engine_amd.kernels").prefill_plan(
+        gi["seq_ids"], gi["cu_seqlens"], gi["tile_start"], gi["slot_ids"], gi["cu_cached"], N,
+        16, 8, wl.block_m)
+    ms_planned = time_graph(lambda: op(plan))
+    return {"us_graph": round(ms * 1e3, 2), "us_graph_planned": round(ms_planned * 1e3, 2),
+            "rows": N, "decoders": len(wl.decode_ctx),
             "prefill_tokens": sum(L for L, _ in wl.chunks),
             "kernels": "fused_norm_rope_prefill, quantize_kv_prefill, prefill_attention, "
                        "decode_attention_rope (fused_rope_kv_decode + decode_attention)"}
@@ -304,7 +325,7 @@ def bench_step(steps, warmup, dev):
     def t(graph):
         for _ in range(warmup):
             graph.replay()
-        torch.cuda.synchronize()
+        settle(graph.replay)
         e0, e1 = _events(2)
         e0.record()
         for _ in range(steps):
@@ -441,14 +462,31 @@ def line_prefill_config4(args, ie, W, K, dev, alg_bytes, extra):
         gi["slot_ids"], gi["cu_cached"], mw.block_m)
     pf_ms = time_op(pf_op, args.steps, args.warmup)
     pf_gms = time_graph(pf_op)
+    # the work list computed once per step (every layer of the step reuses it)
+    plan_op = lambda: K.prefill_plan(gi["seq_ids"], gi["cu_seqlens"], gi["tile_start"],
+                                     gi["slot_ids"], gi["cu_cached"], mw.q.shape[0],
+                                     mw.q.shape[1], mw.cache.k.shape[1], mw.block_m)
+    plan = plan_op()
+    pp_op = lambda: K.prefill_attention(
+        mw.q, mw.k, mw.v, gi["seq_ids"], gi["cu_seqlens"], gi["tile_start"], mw.cache,
+        gi["slot_ids"], gi["cu_cached"], mw.block_m, plan)
+    pp_ms = time_op(pp_op, args.steps, args.warmup)
+    pp_gms = time_graph(pp_op)
+    plan_gms = time_graph(plan_op)
     tf = flops / (pf_ms * 1e-3) / 1e12
+    frac = lambda ms: round(flops / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)
     extra["prefill_config4"] = {"us": round(pf_ms * 1e3, 3), "TFLOPs": round(tf, 1),
                                 "mfma_frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
                                 "us_graph": round(pf_gms * 1e3, 3),
-                                "mfma_frac_graph": round(
-                                    flops / (pf_gms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+                                "mfma_frac_graph": frac(pf_gms),
+                                "planned": {"us": round(pp_ms * 1e3, 3), "mfma_frac": frac(pp_ms),
+                                            "us_graph": round(pp_gms * 1e3, 3),
+                                            "mfma_frac_graph": frac(pp_gms),
+                                            "plan_us_graph": round(plan_gms * 1e3, 3),
+                                            "note": "prefill_plan once per step, its rows read "
+                                                    "by every layer's launch"},
                                 "flops": flops}
-    log(f"prefill config4 {pf_ms*1e3:.2f} us {tf:.1f} TFLOP/s")
+    log(f"prefill config4 {pf_ms*1e3:.2f} us {tf:.1f} TFLOP/s; planned {pp_ms*1e3:.2f} us")
 
 
 def line_prefill_long(args, ie, W, K, dev, alg_bytes, extra):
@@ -673,6 +711,9 @@ def main():
     ap.add_argument("--batch", type=int, default=64)
     ap.add_argument("--ctx", type=int, default=4096)
     ap.add_argument("--rotate", type=int, default=2, help="distinct cache sets cycled per step")
+    ap.add_argument("--settle-ms", type=float, default=150.0,
+                    help="minimum warm-up wall time of each line beside the headline, after its "
+                         "--warmup calls (untimed; lets the clocks come up, see settle())")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="minimum CPU-baseline decode work (whole batch, repeated); the config-4 "
@@ -694,6 +735,8 @@ def main():
                          "phase-stamp build (python inference-engine_amd/build.py --stamps), "
                          "per-phase medians of its workgroups as one JSON line")
     args = ap.parse_args()
+    global SETTLE_S
+    SETTLE_S = args.settle_ms * 1e-3
     args.lines = [x for x in args.lines.split(",") if x]
     bad = [x for x in args.lines if x not in LINES]
     if bad:

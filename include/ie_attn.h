@@ -331,19 +331,21 @@ hipError_t ie_prefill_attention(const ie_bf16* q, int64_t q_stride_tok, int64_t 
                                 hipStream_t stream);
 
 /*
- * The prefill launch's work list, for tests and diagnostics (no counterpart in the reference,
- * whose prefill grid is one program per (tile, query head), kernels.py:1146-1150):
+ * The prefill launch's work list (no counterpart in the reference, whose prefill grid is one
+ * program per (tile, query head), kernels.py:1146-1150):
  * ie_prefill_attention_grid(num_tiles, block_m, num_q_heads, num_kv_heads) is the launch's
  * workgroup count, and ie_prefill_attention_plan writes, for each workgroup w, 16 int32 at
  * rows[16 w]:
  *   found, sub-block, unit, piece, pieces of its (sub-block, unit) pair, first tile, end tile,
- *   prefix tiles, chunk tiles, first row, end row, the entry's first row, prefix length, tiles
- *   per piece, straddling form (1) or separate prefix/chunk pieces (0), the pair's first item
+ *   prefix tiles, chunk tiles, first row, end row, the entry's first row, prefix length, cache
+ *   slot, straddling form (1) or separate prefix/chunk pieces (0), the pair's first item
  * where sub-blocks are 128-row slices of the tiles, a unit is a KV head and one pair of its
  * query heads (unit = KV head * cdiv(ratio, 2) + pair: the KV head itself at GQA ratio 2), tile
  * t < prefix tiles is the prefix's 64-key tile t and later tiles are the chunk's 64-key tiles,
  * and a workgroup without work has an all-zero row. Same index arguments as
- * ie_prefill_attention; rows: int32 [grid, 16] device memory.
+ * ie_prefill_attention; rows: int32 [grid, 16] device memory. The list depends on the index
+ * arrays' values, the head counts and the device's CU count only, so one list serves every
+ * layer of a step.
  */
 int32_t ie_prefill_attention_grid(int32_t num_tiles, int32_t block_m, int32_t num_q_heads,
                                   int32_t num_kv_heads);
@@ -353,6 +355,25 @@ hipError_t ie_prefill_attention_plan(const int32_t* seq_ids, const int32_t* cu_s
                                      int32_t num_kv_heads, const int32_t* slot_ids,
                                      const int32_t* cu_cached, int32_t num_entries, int32_t* rows,
                                      hipStream_t stream);
+/*
+ * ie_prefill_attention with its work list precomputed (no counterpart in the reference): the
+ * same arguments and results, plus `plan`, the rows ie_prefill_attention_plan wrote for the
+ * same index arrays (same values), head counts, block_m and device, and plan_rows, their count
+ * (at least the grid). Each workgroup then reads its row in one load instead of deriving the
+ * list from the tile metadata, which every workgroup of ie_prefill_attention does. The index
+ * arrays are not read. For engines that run several layers over one step's metadata: compute
+ * the plan once per step. A plan that does not match the arguments is undefined behaviour (its
+ * rows name the cache slots, rows and tiles each workgroup reads and writes).
+ */
+hipError_t ie_prefill_attention_planned(
+    const ie_bf16* q, int64_t q_stride_tok, int64_t q_stride_head, const ie_bf16* k,
+    int64_t k_stride_tok, int64_t k_stride_head, const ie_bf16* v, int64_t v_stride_tok,
+    int64_t v_stride_head, int64_t num_tokens, int32_t num_q_heads, const int32_t* seq_ids,
+    const int32_t* cu_seqlens, const int32_t* tile_start, int32_t num_tiles, int32_t block_m,
+    const ie_kv_cache* cache, const int32_t* slot_ids, const int32_t* cu_cached,
+    int32_t num_entries, const int32_t* plan, int64_t plan_rows, ie_bf16* out,
+    int64_t out_stride_tok, int64_t out_stride_head, void* workspace, size_t workspace_bytes,
+    hipStream_t stream);
 
 /*
  * Token sampling: Gumbel-max over the vocabulary, greedy argmax at tau = 0.

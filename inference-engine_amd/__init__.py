@@ -18,6 +18,7 @@ from .kernels import (  # noqa: F401
     fused_rope_kv_decode,
     make_layer_cache,
     prefill_attention,
+    prefill_plan,
     quantize_kv_prefill,
     sample,
     silu_mul,

@@ -61,11 +61,12 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, seq_ids, cu_seq
               cached_lens: torch.Tensor, slot_ids: torch.Tensor, tile_start,
               prefill_block_m: int, prefix_scratch, num_decoding: torch.Tensor,
               q_norm_weight: torch.Tensor, k_norm_weight: torch.Tensor,
-              eps: float = 1e-6) -> torch.Tensor:
+              eps: float = 1e-6, prefill_plan: torch.Tensor | None = None) -> torch.Tensor:
     """architecture.py:98-197. q [N, Hq, D], k/v [N, Hkv, D] (views of the QKV projection's
     output, before norm and RoPE). Returns [N, Hq, D]: in a step with prefill, rows of the
     prefilling entries from prefill attention and rows [0, num_decoding) from decode
-    attention."""
+    attention. prefill_plan: kernels.prefill_plan of the step's metadata, computed once per step
+    for all layers (None: each prefill launch derives its work list itself)."""
     D = q.shape[-1]
     if cu_seqlens is None:
         # the reference's "rope_kv_write" and "decode_attention" ranges (architecture.py:100,
@@ -84,7 +85,8 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, seq_ids, cu_seq
         quantize_kv_prefill(k_p, v, cu_seqlens, slot_ids, cached_lens, num_decoding, kv_cache)
     with nvtx.range("prefill_attention"):
         out = prefill_attention(q_p, k_p, v, seq_ids, cu_seqlens, tile_start, kv_cache,
-                                slot_ids, prefix_scratch.cu_cached, prefill_block_m)
+                                slot_ids, prefix_scratch.cu_cached, prefill_block_m,
+                                prefill_plan)
     B = slot_ids.shape[0]  # from a shape, not from how many entries decode
     with nvtx.range("rope_kv_write+decode_attention"):
         decode_attention_rope(q[:B], k[:B], v[:B], q_norm_weight, k_norm_weight, cos[:B],

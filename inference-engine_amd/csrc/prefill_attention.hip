@@ -162,6 +162,8 @@ struct PrefillArgs {
                        // partial O of split items, in the accumulators' order (a store of 16
                        // rows x 16 channels is 512 contiguous bytes)
     float* part_ml;    // [slot][2 heads][PF_BM rows][2]: their (m, l)
+    const int32_t* plan;  // null, or the launch's work list as ie_prefill_attention_plan writes
+                          // it (16 int32 per workgroup): then no workgroup computes it
     uint32_t* arrivals;  // [2][grid]: arrival and finish words of each split (sub-block, kv
                          // head) pair, at the pair's first item; 0 between launches
     uint64_t merge_wait_ticks;   // longest wait of a piece for its pair's others (100 MHz clock)
@@ -188,6 +190,7 @@ struct SbInfo {
 };
 
 constexpr int PF_UNSPLIT = 1 << 28;  // piece size that never splits a pair
+constexpr int PF_PLAN_FIELDS = 16;   // int32 per workgroup in an exported work list
 
 
 // Pieces of a pair with npt prefix and nct chunk tiles at piece size T. A pair of at most T
@@ -906,12 +909,10 @@ __device__ __forceinline__ void piece_tiles(const SubBlock& s, int piece, int& k
     }
 }
 
-// One work item: tiles [kt_begin, kt_end) of piece `piece` of sub-block s for unit `unit`.
+// One work item: tiles [kt_begin, kt_end) of sub-block s (one of its pieces) for unit `unit`.
 __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBlock& s, int unit,
-                                             int piece, int item, int item_base, PfLds& lds) {
-    int kt_begin, kt_end;
-    piece_tiles(s, piece, kt_begin, kt_end);
-
+                                             int kt_begin, int kt_end, int item, int item_base,
+                                             PfLds& lds) {
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int l16 = lane & 15, g = lane >> 4;
@@ -1319,25 +1320,55 @@ __global__ __launch_bounds__(PF_THREADS, IE_PREFILL_WG_PER_CU) void prefill_atte
     // every wave reads the tile metadata and derives the workgroup's item itself
     __shared__ __attribute__((aligned(16))) PfLds lds;
     PF_STAMP(0);
-    Loc loc = schedule(a, blockIdx.x, reinterpret_cast<int*>(lds.k[1]));
-    {
-        int* f = reinterpret_cast<int*>(&loc);
+    SubBlock s;
+    int unit, kt_begin, kt_end, item_base;
+    if (a.plan) {
+        // the workgroup's row of the precomputed work list: one 64-byte load
+        const int lane = threadIdx.x & 63;
+        const int v = lane < PF_PLAN_FIELDS ? a.plan[PF_PLAN_FIELDS * blockIdx.x + lane] : 0;
+        auto f = [&](int i) { return __builtin_amdgcn_readlane(v, i); };
+        PF_STAMP(1);
+        PF_STAMP_VALUE(8, f(0) ? f(4) : 0);
+        if (!f(0)) return;
+        unit = f(2);
+        s.npieces = f(4);
+        kt_begin = f(5);
+        kt_end = f(6);
+        s.npt = f(7);
+        s.nct = f(8);
+        s.ntiles = s.npt + s.nct;
+        s.r0 = f(9);
+        s.r1 = f(10);
+        s.seq_start = f(11);
+        s.P = f(12);
+        s.slot = f(13);
+        s.npp = 0;  // not read: the tile range comes with the row
+        item_base = f(15);
+    } else {
+        Loc loc = schedule(a, blockIdx.x, reinterpret_cast<int*>(lds.k[1]));
+        {
+            int* f = reinterpret_cast<int*>(&loc);
 #pragma unroll
-        for (int i = 0; i < (int)(sizeof(Loc) / sizeof(int)); ++i) f[i] = uni(f[i]);
+            for (int i = 0; i < (int)(sizeof(Loc) / sizeof(int)); ++i) f[i] = uni(f[i]);
+        }
+        PF_STAMP(1);
+        PF_STAMP_VALUE(8, loc.found ? loc.s.npieces : 0);
+        if (!loc.found) return;
+        s = loc.s;
+        unit = loc.off % a.units;
+        item_base = loc.item_base;
+        piece_tiles(loc.s, loc.off / a.units, kt_begin, kt_end);
     }
-    PF_STAMP(1);
-    PF_STAMP_VALUE(8, loc.found ? loc.s.npieces : 0);
-    if (!loc.found) return;
-    prefill_item(a, loc.s, loc.off % a.units, loc.off / a.units, blockIdx.x, loc.item_base, lds);
+    prefill_item(a, s, unit, kt_begin, kt_end, blockIdx.x, item_base, lds);
 }
 
 // grid (the prefill launch's grid), block 64: the launch's work list, as the main kernel's own
-// schedule computes it, one row of 16 int32 per workgroup index w:
-//   found, sub-block, kv head, piece, pieces of the pair, first tile, end tile, prefix tiles,
-//   chunk tiles, first row, end row, entry's first row, prefix length, tiles per piece T,
+// schedule computes it, one row of PF_PLAN_FIELDS int32 per workgroup index w:
+//   found, sub-block, unit, piece, pieces of the pair, first tile, end tile, prefix tiles,
+//   chunk tiles, first row, end row, entry's first row, prefix length, cache slot,
 //   straddling form, the pair's first item
 // (tile kt < prefix tiles is prefix tile kt, else chunk tile kt - prefix tiles; rows of a
-// workgroup with no item are zero).
+// workgroup with no item are zero). The main kernel runs from these rows when given them.
 __global__ __launch_bounds__(IE_WAVE) void prefill_plan_kernel(PrefillArgs a, int32_t* rows) {
     __shared__ int tables[3 * PF_LDS_ENTRIES + 2];
     Loc loc = schedule(a, blockIdx.x, tables);
@@ -1347,17 +1378,17 @@ __global__ __launch_bounds__(IE_WAVE) void prefill_plan_kernel(PrefillArgs a, in
         for (int i = 0; i < (int)(sizeof(Loc) / sizeof(int)); ++i) f[i] = uni(f[i]);
     }
     if (threadIdx.x != 0) return;
-    int32_t r[16] = {};
+    int32_t r[PF_PLAN_FIELDS] = {};
     if (loc.found) {
         const int hk = loc.off % a.units, piece = loc.off / a.units;
         int kb, ke;
         piece_tiles(loc.s, piece, kb, ke);
         const int v[16] = {1, loc.sb, hk, piece, loc.s.npieces, kb, ke, loc.s.npt, loc.s.nct,
-                           loc.s.r0, loc.s.r1, loc.s.seq_start, loc.s.P, loc.T, loc.straddle,
-                           loc.item_base};
-        for (int i = 0; i < 16; ++i) r[i] = v[i];
+                           loc.s.r0, loc.s.r1, loc.s.seq_start, loc.s.P, loc.s.slot,
+                           loc.straddle, loc.item_base};
+        for (int i = 0; i < PF_PLAN_FIELDS; ++i) r[i] = v[i];
     }
-    for (int i = 0; i < 16; ++i) rows[16 * blockIdx.x + i] = r[i];
+    for (int i = 0; i < PF_PLAN_FIELDS; ++i) rows[PF_PLAN_FIELDS * blockIdx.x + i] = r[i];
 }
 
 // How long a split piece waits for its pair's other pieces before leaving its share of the
@@ -1444,14 +1475,15 @@ extern "C" size_t ie_prefill_attention_workspace_counts_bytes(void) {
     return prefill_ws(prefill_slots()).ml_off;
 }
 
-extern "C" hipError_t ie_prefill_attention(
+// ie_prefill_attention and ie_prefill_attention_planned (plan: null, or the launch's work list).
+static hipError_t prefill_launch(
     const ie_bf16* q, int64_t q_stride_tok, int64_t q_stride_head, const ie_bf16* k,
     int64_t k_stride_tok, int64_t k_stride_head, const ie_bf16* v, int64_t v_stride_tok,
     int64_t v_stride_head, int64_t num_tokens, int32_t num_q_heads, const int32_t* seq_ids,
     const int32_t* cu_seqlens, const int32_t* tile_start, int32_t num_tiles, int32_t block_m,
     const ie_kv_cache* cache, const int32_t* slot_ids, const int32_t* cu_cached,
-    int32_t num_entries, ie_bf16* out,
-    int64_t out_stride_tok, int64_t out_stride_head, void* workspace, size_t workspace_bytes,
+    int32_t num_entries, ie_bf16* out, int64_t out_stride_tok, int64_t out_stride_head,
+    void* workspace, size_t workspace_bytes, const int32_t* plan, int64_t plan_rows,
     hipStream_t stream) {
     hipError_t e = check_cache(cache);
     if (e != hipSuccess) return e;
@@ -1499,9 +1531,48 @@ extern "C" hipError_t ie_prefill_attention(
     a.qk_scale = (float)(0.08838834764831845 * 1.4426950408889634);  // D^-0.5 * log2(e), D = 128
     a.merge_wait_ticks = env_us_ticks("IE_PREFILL_MERGE_WAIT_US", 100);
     a.merge_stall_ticks = env_us_ticks("IE_PREFILL_MERGE_STALL_US", 20);
-    const unsigned grid = (unsigned)prefill_grid(a.nsb, a.units);
-    hipLaunchKernelGGL(prefill_attention_kernel, dim3(grid), dim3(PF_THREADS), 0, stream, a);
+    const int64_t grid = prefill_grid(a.nsb, a.units);
+    if (plan) {
+        IE_REQUIRE(plan_rows >= grid && (reinterpret_cast<uintptr_t>(plan) & 3) == 0,
+                   "plan must hold ie_prefill_attention_grid(...) rows of 16 int32");
+        a.plan = plan;
+    }
+    hipLaunchKernelGGL(prefill_attention_kernel, dim3((unsigned)grid), dim3(PF_THREADS), 0, stream,
+                       a);
     return hipGetLastError();
+}
+
+extern "C" hipError_t ie_prefill_attention(
+    const ie_bf16* q, int64_t q_stride_tok, int64_t q_stride_head, const ie_bf16* k,
+    int64_t k_stride_tok, int64_t k_stride_head, const ie_bf16* v, int64_t v_stride_tok,
+    int64_t v_stride_head, int64_t num_tokens, int32_t num_q_heads, const int32_t* seq_ids,
+    const int32_t* cu_seqlens, const int32_t* tile_start, int32_t num_tiles, int32_t block_m,
+    const ie_kv_cache* cache, const int32_t* slot_ids, const int32_t* cu_cached,
+    int32_t num_entries, ie_bf16* out,
+    int64_t out_stride_tok, int64_t out_stride_head, void* workspace, size_t workspace_bytes,
+    hipStream_t stream) {
+    return prefill_launch(q, q_stride_tok, q_stride_head, k, k_stride_tok, k_stride_head, v,
+                          v_stride_tok, v_stride_head, num_tokens, num_q_heads, seq_ids,
+                          cu_seqlens, tile_start, num_tiles, block_m, cache, slot_ids, cu_cached,
+                          num_entries, out, out_stride_tok, out_stride_head, workspace,
+                          workspace_bytes, nullptr, 0, stream);
+}
+
+extern "C" hipError_t ie_prefill_attention_planned(
+    const ie_bf16* q, int64_t q_stride_tok, int64_t q_stride_head, const ie_bf16* k,
+    int64_t k_stride_tok, int64_t k_stride_head, const ie_bf16* v, int64_t v_stride_tok,
+    int64_t v_stride_head, int64_t num_tokens, int32_t num_q_heads, const int32_t* seq_ids,
+    const int32_t* cu_seqlens, const int32_t* tile_start, int32_t num_tiles, int32_t block_m,
+    const ie_kv_cache* cache, const int32_t* slot_ids, const int32_t* cu_cached,
+    int32_t num_entries, const int32_t* plan, int64_t plan_rows, ie_bf16* out,
+    int64_t out_stride_tok, int64_t out_stride_head, void* workspace, size_t workspace_bytes,
+    hipStream_t stream) {
+    IE_REQUIRE(plan != nullptr, "null plan");
+    return prefill_launch(q, q_stride_tok, q_stride_head, k, k_stride_tok, k_stride_head, v,
+                          v_stride_tok, v_stride_head, num_tokens, num_q_heads, seq_ids,
+                          cu_seqlens, tile_start, num_tiles, block_m, cache, slot_ids, cu_cached,
+                          num_entries, out, out_stride_tok, out_stride_head, workspace,
+                          workspace_bytes, plan, plan_rows, stream);
 }
 
 extern "C" int32_t ie_prefill_attention_grid(int32_t num_tiles, int32_t block_m,

@@ -47,6 +47,7 @@ const ie_bf16* bf(const at::Tensor& t) {
 }
 ie_bf16* bfm(const at::Tensor& t) { return reinterpret_cast<ie_bf16*>(t.data_ptr()); }
 const int32_t* i32(const at::Tensor& t) { return t.data_ptr<int32_t>(); }
+int32_t* i32m(const at::Tensor& t) { return t.data_ptr<int32_t>(); }
 
 // LayerKVCache (qwen3-1.7b/kernels.py:11-17) -> descriptor; same stride asserts as
 // kernels.py:284-287.
@@ -428,7 +429,7 @@ at::Tensor prefill_attention(const at::Tensor& q, const at::Tensor& k, const at:
                              const at::Tensor& v_cache, const at::Tensor& k_scale,
                              const at::Tensor& v_scale, const at::Tensor& k_calibration,
                              const at::Tensor& slot_ids, const at::Tensor& cu_cached,
-                             int64_t block_m) {
+                             int64_t block_m, const c10::optional<at::Tensor>& plan) {
     check_bf16_rows(q, "q", 3);
     check_bf16_rows(k, "k", 3);
     check_bf16_rows(v, "v", 3);
@@ -450,6 +451,21 @@ at::Tensor prefill_attention(const at::Tensor& q, const at::Tensor& k, const at:
         (int32_t)tile_start.size(0), (int32_t)block_m, c.num_kv_heads);
     at::Tensor ws = persistent_workspace(q, ws_bytes,
                                          ie_prefill_attention_workspace_counts_bytes(), WS_PREFILL);
+    if (plan.has_value()) {
+        const at::Tensor& p = *plan;
+        check_dev(p, "plan");
+        TORCH_CHECK(p.scalar_type() == at::kInt && p.dim() == 2 && p.size(1) == 16 &&
+                        p.is_contiguous(),
+                    "ie: plan must be the [grid, 16] int32 tensor prefill_plan returns");
+        ok(ie_prefill_attention_planned(
+               bf(q), q.stride(0), q.stride(1), bf(k), k.stride(0), k.stride(1), bf(v),
+               v.stride(0), v.stride(1), N, (int32_t)q.size(1), i32(seq_ids), i32(cu_seqlens),
+               i32(tile_start), (int32_t)tile_start.size(0), (int32_t)block_m, &c, i32(slot_ids),
+               i32(cu_cached), (int32_t)slot_ids.size(0), i32(p), p.size(0), bfm(out),
+               out.stride(0), out.stride(1), ws.data_ptr(), ws_bytes, stream_of(q)),
+           "prefill_attention (planned)");
+        return out;
+    }
     ok(ie_prefill_attention(bf(q), q.stride(0), q.stride(1), bf(k), k.stride(0), k.stride(1),
                             bf(v), v.stride(0), v.stride(1), N, (int32_t)q.size(1), i32(seq_ids),
                             i32(cu_seqlens), i32(tile_start), (int32_t)tile_start.size(0),
@@ -458,6 +474,33 @@ at::Tensor prefill_attention(const at::Tensor& q, const at::Tensor& k, const at:
                             out.stride(0), out.stride(1), ws.data_ptr(), ws_bytes, stream_of(q)),
        "prefill_attention");
     return out;
+}
+
+// The prefill launch's work list for one step's metadata (see ie_prefill_attention_plan):
+// [grid, 16] int32 on the metadata's device, to pass to every layer's prefill_attention.
+at::Tensor prefill_plan(const at::Tensor& seq_ids, const at::Tensor& cu_seqlens,
+                        const at::Tensor& tile_start, const at::Tensor& slot_ids,
+                        const at::Tensor& cu_cached, int64_t num_tokens, int64_t num_q_heads,
+                        int64_t num_kv_heads, int64_t block_m) {
+    for (auto* t : {&seq_ids, &cu_seqlens, &tile_start, &slot_ids, &cu_cached})
+        check_i32(*t, "index");
+    const c10::DeviceGuard guard(seq_ids.device());
+    TORCH_CHECK(slot_ids.size(0) >= 1 && cu_seqlens.size(0) == slot_ids.size(0) + 1 &&
+                    cu_cached.size(0) == slot_ids.size(0) + 1,
+                "ie: cu_seqlens and cu_cached must hold len(slot_ids) + 1 entries");
+    TORCH_CHECK(seq_ids.size(0) >= num_tokens, "ie: seq_ids must hold one entry per packed row");
+    const int32_t nt = (int32_t)tile_start.size(0);
+    const int32_t grid = ie_prefill_attention_grid(nt, (int32_t)block_m, (int32_t)num_q_heads,
+                                                   (int32_t)num_kv_heads);
+    // the plan kernel writes every row of a launch (a workgroup without work: zeros)
+    at::Tensor rows = grid > 0 ? at::empty({grid, 16}, seq_ids.options())
+                               : at::zeros({1, 16}, seq_ids.options());
+    ok(ie_prefill_attention_plan(i32(seq_ids), i32(cu_seqlens), i32(tile_start), nt,
+                                 (int32_t)block_m, num_tokens, (int32_t)num_q_heads,
+                                 (int32_t)num_kv_heads, i32(slot_ids), i32(cu_cached),
+                                 (int32_t)slot_ids.size(0), i32m(rows), stream_of(seq_ids)),
+       "prefill_plan");
+    return rows;
 }
 
 }  // namespace
@@ -497,7 +540,12 @@ TORCH_LIBRARY(ie, m) {
     m.def(
         "prefill_attention(Tensor q, Tensor k, Tensor v, Tensor seq_ids, Tensor cu_seqlens, "
         "Tensor tile_start, Tensor k_cache, Tensor v_cache, Tensor k_scale, Tensor v_scale, "
-        "Tensor k_calibration, Tensor slot_ids, Tensor cu_cached, int block_m) -> Tensor");
+        "Tensor k_calibration, Tensor slot_ids, Tensor cu_cached, int block_m, "
+        "Tensor? plan=None) -> Tensor");
+    m.def(
+        "prefill_plan(Tensor seq_ids, Tensor cu_seqlens, Tensor tile_start, Tensor slot_ids, "
+        "Tensor cu_cached, int num_tokens, int num_q_heads, int num_kv_heads, int block_m) "
+        "-> Tensor");
     m.impl("decode_attention_workspace_size", &decode_attention_workspace_size);
 }
 
@@ -514,4 +562,5 @@ TORCH_LIBRARY_IMPL(ie, CUDA, m) {
     m.impl("decode_attention_rope", &decode_attention_rope);
     m.impl("dequantize_kv_prefix", &dequantize_kv_prefix);
     m.impl("prefill_attention", &prefill_attention);
+    m.impl("prefill_plan", &prefill_plan);
 }

@@ -183,13 +183,28 @@ def prefill_attention(
     slot_ids: torch.Tensor,  # [B]
     cu_cached: torch.Tensor,  # [B + 1] int32, prefix lengths of every entry, cumulative
     PREFILL_BLOCK_M: int,  # must be the value tile_start was built with
+    plan: torch.Tensor | None = None,  # prefill_plan(...) of the same metadata, or None
 ) -> torch.Tensor:
-    """qwen3-1.7b/kernels.py:1129-1175 fused with the prefix dequantize (architecture.py:151-170)."""
+    """qwen3-1.7b/kernels.py:1129-1175 fused with the prefix dequantize (architecture.py:151-170).
+    `plan` (not in the reference): the launch's work list from `prefill_plan` over the same
+    step metadata and head counts; every workgroup then reads its item instead of deriving the
+    list from the metadata. Same results."""
     N, Hq, D = q.shape
     assert q.stride(-1) == 1 and k.stride(-1) == 1 and v.stride(-1) == 1
     return ops().prefill_attention(q, k, v, seq_ids, cu_seqlens, tile_start,
                                    *_cache_args(kv_cache), slot_ids, cu_cached,
-                                   int(PREFILL_BLOCK_M))
+                                   int(PREFILL_BLOCK_M), plan)
+
+
+def prefill_plan(seq_ids: torch.Tensor, cu_seqlens: torch.Tensor, tile_start: torch.Tensor,
+                 slot_ids: torch.Tensor, cu_cached: torch.Tensor, num_tokens: int,
+                 num_q_heads: int, num_kv_heads: int, PREFILL_BLOCK_M: int) -> torch.Tensor:
+    """The work list of prefill_attention over one step's metadata ([grid, 16] int32 on the
+    device, one row per workgroup: see ie_prefill_attention_plan), computed once per step and
+    passed as `plan` to every layer's prefill_attention (no counterpart in the reference)."""
+    return ops().prefill_plan(seq_ids, cu_seqlens, tile_start, slot_ids, cu_cached,
+                              int(num_tokens), int(num_q_heads), int(num_kv_heads),
+                              int(PREFILL_BLOCK_M))
 
 
 def sample(logits: torch.Tensor, tau: float, seed: torch.Tensor) -> torch.Tensor:

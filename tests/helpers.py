@@ -69,7 +69,7 @@ def bf16_np(t: torch.Tensor) -> np.ndarray:
 
 
 PLAN_FIELDS = ("found", "sb", "hk", "piece", "npieces", "kt_begin", "kt_end", "npt", "nct", "r0",
-               "r1", "seq_start", "P", "T", "straddle", "item_base")
+               "r1", "seq_start", "P", "slot", "straddle", "item_base")
 
 
 def prefill_plan(native, g) -> np.ndarray:

@@ -157,3 +157,30 @@ def test_prefill_plan_rejects_bad_sizes_on_host(native):
         rc = fn(p, p, p, i32(4), i32(128), ctypes.c_int64(100), i32(hq), i32(hkv), p, p, i32(3),
                 p, null)
         assert rc == HIP_ERROR_INVALID_VALUE and b"GQA ratio" in lib.ie_attn_last_error()
+
+
+def test_prefill_planned_rejects_bad_plans_on_host(native):
+    """ie_prefill_attention_planned: a null plan, and a plan with fewer rows than the launch's
+    grid, are refused before any launch (the pointers here are never dereferenced)."""
+    lib = native.cabi()
+    fn = lib.ie_prefill_attention_planned
+    fn.restype = ctypes.c_int
+    lib.ie_prefill_attention_workspace_size.restype = ctypes.c_size_t
+    i32, i64 = ctypes.c_int32, ctypes.c_int64
+    p = ctypes.c_void_p(1 << 20)  # aligned stand-in address
+    desc = native.KVCacheDesc(1 << 20, 1 << 20, 1 << 20, 1 << 20, 1 << 20, 4, 8, 1024, 128,
+                              8 * 1024 * 128, 1024 * 128, 128, 8 * 1024, 1024, 8 * 128, 128)
+    tiles, bm, hq, hkv = 8, 128, 16, 8
+    grid = lib.ie_prefill_attention_grid(tiles, bm, hq, hkv)
+    ws = lib.ie_prefill_attention_workspace_size(i32(tiles), i32(bm), i32(hkv))
+
+    def call(plan, rows):
+        return fn(p, i64(2048), i64(128), p, i64(1024), i64(128), p, i64(1024), i64(128),
+                  i64(1024), i32(hq), p, p, p, i32(tiles), i32(bm), ctypes.byref(desc), p, p,
+                  i32(3), plan, i64(rows), p, i64(2048), i64(128), p, ctypes.c_size_t(ws),
+                  ctypes.c_void_p(0))
+
+    assert call(ctypes.c_void_p(0), grid) == HIP_ERROR_INVALID_VALUE
+    assert b"null plan" in lib.ie_attn_last_error()
+    assert call(p, grid - 1) == HIP_ERROR_INVALID_VALUE
+    assert b"plan must hold" in lib.ie_attn_last_error()
