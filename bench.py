@@ -603,12 +603,13 @@ def extras(args, ie, W, K, dev, alg_bytes) -> dict:
     return extra
 
 
-def prefill_phase_stamps(W, dev, warmup):
+def prefill_phase_stamps(W, dev, warmup, planned=False):
     """Config 4's prefill attention through the C ABI of the phase-stamp build
     (inference-engine_amd/lib/stamps/libie_attn.so: the same kernel with a 100 MHz clock read
     by thread 0 of every workgroup at each phase boundary). Per call: the time from the first
     workgroup's start to each workgroup's phase boundaries; medians over five calls after
-    `warmup` calls that bring the clocks up."""
+    `warmup` calls that bring the clocks up. planned: the work list is computed once
+    (ie_prefill_attention_plan) and every call reads it (ie_prefill_attention_planned)."""
     import ctypes
     import numpy as np
     path = REPO / "inference-engine_amd" / "lib" / "stamps" / "libie_attn.so"
@@ -627,16 +628,27 @@ def prefill_phase_stamps(W, dev, warmup):
     ws = torch.zeros(int(wsb), dtype=torch.uint8, device=dev)
     out = torch.empty_like(mw.q)
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    i64, i32 = ctypes.c_int64, ctypes.c_int32
+    grid = lib.ie_prefill_attention_grid(i32(nt), i32(mw.block_m), i32(16), i32(8))
+    rows = torch.empty(grid, 16, dtype=torch.int32, device=dev)
+    if planned:
+        assert lib.ie_prefill_attention_plan(
+            p(gi["seq_ids"]), p(gi["cu_seqlens"]), p(gi["tile_start"]), i32(nt),
+            i32(mw.block_m), i64(N), i32(16), i32(8), p(gi["slot_ids"]), p(gi["cu_cached"]),
+            i32(gi["slot_ids"].shape[0]), p(rows), stream) == 0, lib.ie_attn_last_error()
 
     def run():
-        i64, i32 = ctypes.c_int64, ctypes.c_int32
-        rc = lib.ie_prefill_attention(
-            p(mw.q), i64(mw.q.stride(0)), i64(mw.q.stride(1)), p(mw.k), i64(mw.k.stride(0)),
-            i64(mw.k.stride(1)), p(mw.v), i64(mw.v.stride(0)), i64(mw.v.stride(1)), i64(N),
-            i32(16), p(gi["seq_ids"]), p(gi["cu_seqlens"]), p(gi["tile_start"]), i32(nt),
-            i32(mw.block_m), ctypes.byref(desc), p(gi["slot_ids"]), p(gi["cu_cached"]),
-            i32(gi["slot_ids"].shape[0]), p(out), i64(out.stride(0)), i64(out.stride(1)), p(ws),
-            ctypes.c_size_t(wsb), stream)
+        head = (p(mw.q), i64(mw.q.stride(0)), i64(mw.q.stride(1)), p(mw.k), i64(mw.k.stride(0)),
+                i64(mw.k.stride(1)), p(mw.v), i64(mw.v.stride(0)), i64(mw.v.stride(1)), i64(N),
+                i32(16), p(gi["seq_ids"]), p(gi["cu_seqlens"]), p(gi["tile_start"]), i32(nt),
+                i32(mw.block_m), ctypes.byref(desc), p(gi["slot_ids"]), p(gi["cu_cached"]),
+                i32(gi["slot_ids"].shape[0]))
+        tail = (p(out), i64(out.stride(0)), i64(out.stride(1)), p(ws), ctypes.c_size_t(wsb),
+                stream)
+        if planned:
+            rc = lib.ie_prefill_attention_planned(*head, p(rows), i64(grid), *tail)
+        else:
+            rc = lib.ie_prefill_attention(*head, *tail)
         assert rc == 0, lib.ie_attn_last_error()
 
     for _ in range(warmup):
@@ -693,7 +705,8 @@ def prefill_phase_stamps(W, dev, warmup):
             by_xcd[str(x)] = {"start_p50_us": round(float(np.median(st)), 2),
                               "end_p50_us": round(float(np.median(en)), 2),
                               "end_max_us": round(float(en.max()), 2)}
-    return {"workload": "prefill_attention config 4 (phase-stamp build)",
+    return {"workload": "prefill_attention config 4 (phase-stamp build" +
+                        (", precomputed work list)" if planned else ")"),
             "call_us_last_end": round(float(np.median([(t[:, 7].max() - t[:, 0].min()) * 0.01
                                                        for t in calls])), 2),
             "workgroups_with_work": int((pieces > 0).sum()),
@@ -730,10 +743,11 @@ def main():
                          "every decode launch of the run is then a headline launch)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run a plain device copy of MIB MiB 3 times (PMC calibration)")
-    ap.add_argument("--prefill-stamps", action="store_true",
+    ap.add_argument("--prefill-stamps", nargs="?", const="self", choices=["self", "planned"],
                     help="instead of the bench line: config 4's prefill attention on the "
                          "phase-stamp build (python inference-engine_amd/build.py --stamps), "
-                         "per-phase medians of its workgroups as one JSON line")
+                         "per-phase medians of its workgroups as one JSON line; 'planned': "
+                         "the launch that reads a precomputed work list")
     args = ap.parse_args()
     global SETTLE_S
     SETTLE_S = args.settle_ms * 1e-3
@@ -759,7 +773,8 @@ def main():
     torch.cuda.set_device(0)
 
     if args.prefill_stamps:
-        print(json.dumps(prefill_phase_stamps(W, dev, args.warmup)), flush=True)
+        print(json.dumps(prefill_phase_stamps(W, dev, args.warmup,
+                                              args.prefill_stamps == "planned")), flush=True)
         return
 
     if args.copy_probe:
