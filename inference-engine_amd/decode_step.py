@@ -230,8 +230,18 @@ def _main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--replays", type=int, default=20)
     ap.add_argument("--attention-only", action="store_true")
+    ap.add_argument("--eager", type=int, default=0, metavar="N",
+                    help="run N steps without a graph instead (their NVTX/roctx stage ranges "
+                         "are then recorded at every step, for a marker trace)")
     args = ap.parse_args()
     step = make_decode_step(device="cuda:0")
+    if args.eager:
+        for _ in range(args.eager):
+            out = step.forward()
+        torch.cuda.synchronize()
+        print(f"ran {args.eager} eager steps; first tokens {out.view(-1)[:4].tolist()}",
+              flush=True)
+        return
     graph, out = step.capture(step.attention_only if args.attention_only else None)
     for _ in range(args.replays):
         graph.replay()
