@@ -91,10 +91,10 @@ hipError_t ie_hbm_read_probe(const void* p, size_t bytes, uint32_t never, uint32
  * recomputed as max(1e-3, max_t |k[t, d]|) over the chunk and stored; otherwise it is read.
  * Per token and head: x = k / cal; s = max(max|x|, 1e-6) / 127; q = clamp(rint(x / s), ±127).
  * V uses the same formula with cal = 1.
- * One launch when num_tokens <= 1536 (each workgroup derives the calibration itself); three
- * launches otherwise (calibration floor, per-channel max, quantize), so the cost stays linear in
- * the chunk length. Both forms write identical bytes. cdiv(num_tokens, 32) + num_entries must
- * not exceed 65535 (about two million tokens per step).
+ * One launch when num_tokens <= 1536 (each workgroup derives the calibration itself); two
+ * launches otherwise (the per-channel max of every first chunk, then a streaming quantize
+ * launch), so the cost stays linear in the chunk length. Both forms write identical bytes.
+ * cdiv(num_tokens, 32) + num_entries must not exceed 65535 (about two million tokens per step).
  */
 hipError_t ie_quantize_kv_prefill(const ie_bf16* k, int64_t k_stride_tok, int64_t k_stride_head,
                                   const ie_bf16* v, int64_t v_stride_tok, int64_t v_stride_head,
