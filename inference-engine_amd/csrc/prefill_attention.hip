@@ -14,19 +14,21 @@
 // another place, well inside bf16 attention tolerance). Prefix V is staged dequantized,
 // bf16(v_int8 * v_scale), exactly as the reference rounds it.
 //
-// Work: sub-blocks of up to 64 packed rows of one tile of `block_m` rows (tile_start, -1 = no
-// work), both query heads of one KV head per workgroup. Every workgroup reads the tile metadata
-// (one wave, a few hundred sub-blocks at most) and derives the same work list: the key range of
-// a (sub-block, kv head) pair (prefix tiles, then chunk tiles up to its last row) is one piece,
-// or, when longer than T 64-key tiles, prefix pieces and chunk pieces of at most T tiles, T the
-// smallest size whose pieces fit one resident wave of workgroups (2 per CU). Workgroup w runs
-// piece w of the list (largest sub-blocks first). Unsplit pieces write `out`; split pieces
+// Work: sub-blocks of up to PF_BM (128) packed rows of one tile of `block_m` rows (tile_start,
+// -1 = no work), one query-head pair of one KV head (a unit) per workgroup. Every workgroup reads
+// the tile metadata (one wave, a few hundred sub-blocks at most) and derives the same work list:
+// the key range of a (sub-block, unit) pair (prefix tiles, then chunk tiles up to its last row)
+// is one piece, or, when longer than T 64-key tiles, prefix pieces and chunk pieces of at most T
+// tiles (or even consecutive ranges that may straddle the two), T the smallest size whose pieces
+// fit one resident wave of workgroups (one per CU). Workgroup w runs piece w of the list
+// (largest sub-blocks first). Unsplit pieces write `out`; split pieces
 // write a bf16 partial O (normalized) and fp32 (m, l) to their slot and count themselves in,
 // and the piece of a (sub-block, kv head) that arrives last merges them all (log-sum-exp) into
-// `out` in the same launch.
+// `out` in the same launch. The work list can also be computed once (prefill_plan_kernel, 16
+// int32 per workgroup) and handed to the launch, whose workgroups then read their row instead.
 //
 // Per 64-key tile: the workgroup stages K as [key][d] and V transposed as [d][key] in LDS, and
-// the tile's score scales; wave w (query head 2hk + (w & 1), rows 32 (w >> 1)..+32) computes
+// the tile's score scales; wave w (the unit's query head w & 1, rows 32 (w >> 1)..+32) computes
 //   S^T (64 keys x 32 rows) = K . Q^T   v_mfma_f32_16x16x32_bf16, A = K from LDS, B = Q^T in VGPRs
 //   online softmax on S^T (a lane holds one row's scores for 16 keys)
 //   O^T (128 d x 32 rows) += V^T . P^T  A = V^T from LDS, B = P^T straight from the S^T
