@@ -18,9 +18,9 @@ SCALE = 128 ** -0.5
 def _call(lib, native, g, out, ws=None):
     p = lambda t: ctypes.c_void_p(t.data_ptr())
     desc = native.KVCacheDesc.of(g.cache)
-    B = g.q.shape[0]
+    B, hq = g.q.shape[0], g.q.shape[1]
     args = [p(g.q), ctypes.c_int64(g.q.stride(0)), ctypes.c_int64(g.q.stride(1)),
-            ctypes.c_int32(B), ctypes.c_int32(16), ctypes.byref(desc), p(g.cached_lens),
+            ctypes.c_int32(B), ctypes.c_int32(hq), ctypes.byref(desc), p(g.cached_lens),
             p(g.slot_ids), p(g.num_decoding), ctypes.c_float(SCALE), p(out),
             ctypes.c_int64(out.stride(0)), ctypes.c_int64(out.stride(1))]
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
@@ -35,23 +35,26 @@ def _call(lib, native, g, out, ws=None):
     assert rc == 0, lib.ie_attn_last_error()
 
 
-def test_noalloc_matches_workspace_entry(ie, workloads, native, dev):
+@pytest.mark.parametrize("hq,hkv", [(16, 8), (32, 8), (40, 8), (2, 1)])
+def test_noalloc_matches_workspace_entry(ie, workloads, native, dev, hq, hkv):
     lib = native.cabi()
     lib.ie_decode_attention_noalloc_max_bytes.restype = ctypes.c_size_t
+    lib.ie_decode_attention_workspace_size.restype = ctypes.c_size_t
     cap = lib.ie_decode_attention_noalloc_max_bytes()
     assert cap == 16 << 20
     # two calls in a row, the second with a smaller batch: the first call's plan and partials
-    # are still in the array when the second runs
+    # are still in the array when the second runs (any head geometry: the count region is laid
+    # out per query head)
     for ctx, seed in (([3000, 40, 9000, 128, 1, 4096] * 12 + [20000], 61),
                       ([700, 2, 5000], 62)):
         B = len(ctx)
-        say(f"noalloc decode B={B} max ctx {max(ctx)}")
-        g = workloads.decode_workload(ctx, seed=seed, device=dev)
-        ws_bytes = lib.ie_decode_attention_workspace_size(B, 16, 128)
+        say(f"noalloc decode hq={hq} hkv={hkv} B={B} max ctx {max(ctx)}")
+        g = workloads.decode_workload(ctx, seed=seed, device=dev, hq=hq, hkv=hkv)
+        ws_bytes = lib.ie_decode_attention_workspace_size(B, hq, 128)
         assert ws_bytes <= cap
         ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)  # arrival counts start at 0
-        ref = torch.full((B, 16, 128), 5.0, dtype=torch.bfloat16, device=dev)
-        got = torch.full((B, 16, 128), 6.0, dtype=torch.bfloat16, device=dev)
+        ref = torch.full((B, hq, 128), 5.0, dtype=torch.bfloat16, device=dev)
+        got = torch.full((B, hq, 128), 6.0, dtype=torch.bfloat16, device=dev)
         _call(lib, native, g, ref, ws)
         _call(lib, native, g, got)
         torch.cuda.synchronize()
