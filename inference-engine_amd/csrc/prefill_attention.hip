@@ -833,10 +833,32 @@ __device__ __forceinline__ void tile_pv(WaveState& w, const uint32_t (&pfrag)[2]
 // The 32 rows x 256 bytes are loaded 16 lanes per row (loads in the fragment layout, 16 rows x
 // 64 bytes per wave instruction, moved a third of the bytes per clock) into the wave's own LDS
 // region `qreg` (rows of QS_STRIDE bytes, 32 mod 64: conflict-free fragment reads) and read back
-// in the fragment layout. The region lies in the V^T buffers: the caller keeps them unstaged
-// until every wave has passed a barrier after this call.
+// in the fragment layout (q_frags). With 8-wave workgroups the region is the wave's own and
+// keeps the raw rows; with 4-wave ones it lies in the V^T buffers: the caller keeps them
+// unstaged until every wave has passed a barrier after this call.
 static_assert(PF_WAVES == 8 || PF_WAVES * 32 * QS_STRIDE <= 2 * PF_D * VT_STRIDE,
               "Q regions must fit the V^T buffers");
+template <bool PREFIX>
+__device__ __forceinline__ void q_frags(bf16x8 (&qf)[2][4], const float* cal, int l16, int g,
+                                        const uint8_t* qreg) {
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            u32x4 w = *reinterpret_cast<const u32x4*>(qreg + (16 * nt + l16) * QS_STRIDE +
+                                                      16 * (4 * ks + g));
+            if (PREFIX) {
+                const f32x4 c0 = *reinterpret_cast<const f32x4*>(cal + 32 * ks + 8 * g);
+                const f32x4 c1 = *reinterpret_cast<const f32x4*>(cal + 32 * ks + 8 * g + 4);
+                w = u32x4{pack_bf16x2(bf16lo(w.x) * c0[0], bf16hi(w.x) * c0[1]),
+                          pack_bf16x2(bf16lo(w.y) * c0[2], bf16hi(w.y) * c0[3]),
+                          pack_bf16x2(bf16lo(w.z) * c1[0], bf16hi(w.z) * c1[1]),
+                          pack_bf16x2(bf16lo(w.w) * c1[2], bf16hi(w.w) * c1[3])};
+            }
+            qf[nt][ks] = __builtin_bit_cast(bf16x8, w);
+        }
+    }
+}
 template <bool PREFIX>
 __device__ __forceinline__ void load_q(bf16x8 (&qf)[2][4], const PrefillArgs& a, int wr0, int r1,
                                        int h, const float* cal, int l16, int g, uint8_t* qreg) {
@@ -855,23 +877,7 @@ __device__ __forceinline__ void load_q(bf16x8 (&qf)[2][4], const PrefillArgs& a,
         for (int j = 0; j < 4; ++j)
             *reinterpret_cast<u32x4*>(qreg + (16 * half + 4 * j + qr) * QS_STRIDE + 16 * qc) = raw[j];
     }
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            u32x4 w = *reinterpret_cast<const u32x4*>(qreg + (16 * nt + l16) * QS_STRIDE +
-                                                      16 * (4 * ks + g));
-            if (PREFIX) {
-                const f32x4 c0 = *reinterpret_cast<const f32x4*>(cal + 32 * ks + 8 * g);
-                const f32x4 c1 = *reinterpret_cast<const f32x4*>(cal + 32 * ks + 8 * g + 4);
-                w = u32x4{pack_bf16x2(bf16lo(w.x) * c0[0], bf16hi(w.x) * c0[1]),
-                          pack_bf16x2(bf16lo(w.y) * c0[2], bf16hi(w.y) * c0[3]),
-                          pack_bf16x2(bf16lo(w.z) * c1[0], bf16hi(w.z) * c1[1]),
-                          pack_bf16x2(bf16lo(w.w) * c1[2], bf16hi(w.w) * c1[3])};
-            }
-            qf[nt][ks] = __builtin_bit_cast(bf16x8, w);
-        }
-    }
+    q_frags<PREFIX>(qf, cal, l16, g, qreg);
 }
 
 #ifndef IE_PREFILL_WG_PER_CU
@@ -1061,7 +1067,14 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const SubBloc
             load_ck(ck, src, kb0);
             load_cv(cv, src, kb0);
             if (n > 1) load_ck(ck1, src, kb0 + PF_BN);
-            load_q<false>(qf, a, wr0, s.r1, h, cal, l16, g, qreg);
+#if IE_PREFILL_WAVES == 8
+            // a piece that ran the prefix loop: the raw Q rows are still in this wave's own LDS
+            // region, so the chunk loop's fragments need no second global load
+            if (kt > kt_begin)
+                q_frags<false>(qf, cal, l16, g, qreg);
+            else
+#endif
+                load_q<false>(qf, a, wr0, s.r1, h, cal, l16, g, qreg);
             stage_ck(ck, s_k[0]);
             __syncthreads();  // every wave has read its Q region (in the V^T buffers)
             stage_cv(cv, s_vt[0]);
