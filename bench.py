@@ -339,11 +339,23 @@ def bench_step(steps, warmup, dev):
            "attention_ms": round(ms_attn, 4), "attention_share": round(ms_attn / ms_step, 4),
            "batch": B, "layers": step.shape.layers, "ctx_mean": round(
                float(step.cached_lens.float().mean().item()) + 1, 1),
+           "fused_layers": step.fused,
            "graph": "torch.cuda.CUDAGraph (hipGraph) of the full step; attention share = replay "
                     "time of the step's attention kernel (decode_attention_rope: "
                     "fused_rope_kv_decode + decode_attention in one launch) captured alone / "
-                    "step replay time"}
+                    "step replay time; fused_layers: both add_rms_norm launches of every layer "
+                    "inside the projections (RMSNorm weights folded into qkv and gate_up, "
+                    "residual adds in o_proj and down)"}
     del g_step, g_attn, step
+    torch.cuda.empty_cache()
+    # the reference's layer form (add_rms_norm launches between the projections), same seed
+    step = ds.make_decode_step(batch=B, ctx_lo=128, ctx_hi=4096, device=dev, seed=0,
+                               fused=False)
+    g_ref, _ = step.capture()
+    ms_ref = t(g_ref)
+    res["reference_form"] = {"tokens_per_s": round(B / (ms_ref * 1e-3), 1),
+                             "ms_per_step": round(ms_ref, 4)}
+    del g_ref, step
     torch.cuda.empty_cache()
     return res
 

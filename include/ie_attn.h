@@ -7,8 +7,9 @@
  * `cached_lens`, `cu_seqlens`, ...) on the device only, so every call can be captured into a
  * hipGraph. Grids depend on shapes alone.
  *
- * Geometry supported by the kernels: head_dim 128, 2 query heads per KV head (Qwen3-1.7B:
- * 16 query heads over 8 KV heads). Other geometries return hipErrorInvalidValue.
+ * Geometry supported by the attention and KV-cache kernels: head_dim 128 and 1 to 16 query
+ * heads per KV head (Qwen3-1.7B: 16 query heads over 8 KV heads, ratio 2, the tuned case).
+ * Other geometries return hipErrorInvalidValue.
  *
  * Each entry point replaces one Python wrapper of kbwal/inference-engine's Triton kernel API,
  * cited as qwen3-1.7b/kernels.py:<line>, with the same argument meaning. Bit-level contracts:
@@ -451,6 +452,34 @@ hipError_t ie_skinny_gemm_silu_mul(const ie_bf16* x, int64_t x_stride, int32_t m
                                    const ie_bf16* weight, int64_t weight_stride, int32_t n,
                                    int32_t k, int32_t n_tiles, ie_bf16* y, int64_t y_stride,
                                    hipStream_t stream);
+
+/*
+ * The skinny GEMM with a decoder layer's residual add and RMSNorm fused in (no counterpart in
+ * the reference, whose block calls add_rms_norm between its projections, kernels.py:1260-1283
+ * at architecture.py:280-300): for engines that fold each RMSNorm's weight into the weight
+ * columns of the projections it feeds, which removes both add_rms_norm launches of a layer.
+ * flags:
+ *   0                 y = x . weight^T (ie_skinny_gemm);
+ *   IE_SKINNY_SILU_MUL   the gate/up form of ie_skinny_gemm_silu_mul;
+ *   IE_SKINNY_NORM    x is the residual stream h (new_residual of add_rms_norm) and weight holds
+ *                     bf16(W[n, k] * g[k]) for the norm weight g: every fp32 sum of row m is
+ *                     multiplied by rstd_m = 1 / sqrt(sum_k h[m, k]^2 / k + eps) (IEEE) before
+ *                     it is rounded, i.e. the GEMM of RMSNorm(h) * g up to where the rounding
+ *                     to bf16 falls (the weight is rounded after the product with g instead of
+ *                     the normalized row); combines with IE_SKINNY_SILU_MUL;
+ *   IE_SKINNY_RESIDUAL   y holds the residual stream on entry and becomes
+ *                     bf16(y + bf16(x . weight^T)) in place: add_rms_norm's new_residual for the
+ *                     projection's output as delta, bit for bit.
+ * Sizes, strides and n_tiles as for the plain or the gate/up form. The sum of squares is taken
+ * from the bf16 rows of x over all k columns (eight partial sums combined in a fixed order).
+ */
+#define IE_SKINNY_NORM 1
+#define IE_SKINNY_SILU_MUL 2
+#define IE_SKINNY_RESIDUAL 4
+hipError_t ie_skinny_gemm_fused(const ie_bf16* x, int64_t x_stride, int32_t m,
+                                const ie_bf16* weight, int64_t weight_stride, int32_t n, int32_t k,
+                                int32_t n_tiles, int32_t flags, float eps, ie_bf16* y,
+                                int64_t y_stride, hipStream_t stream);
 
 #ifdef __cplusplus
 }

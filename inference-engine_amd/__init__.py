@@ -14,6 +14,7 @@ from .kernels import (  # noqa: F401
     decode_attention,
     decode_attention_rope,
     dequantize_kv_prefix,
+    fold_rms_norm_weight,
     fused_norm_rope_prefill,
     fused_rope_kv_decode,
     make_layer_cache,
@@ -25,6 +26,8 @@ from .kernels import (  # noqa: F401
     skinny_matmul,
     skinny_matmul_silu_mul,
     linear,
+    linear_norm,
+    linear_residual_,
     linear_silu_mul,
     tune_linear,
 )

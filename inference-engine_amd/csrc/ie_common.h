@@ -198,18 +198,17 @@ __device__ __forceinline__ uint64_t ld_dev64(const void* p) {
 __device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 // Counts the calling workgroup in at `count` (thread 0's device-scope atomic, after a barrier
 // that follows every wave's wait_stores) and returns, to every thread, whether it was the last
-// of `needed`; the last one resets the count to zero for the next launch.
+// of `needed`. The count is a wrapping increment (old >= needed - 1 stores 0), so the last one
+// leaves it zero for the next launch in the same operation, and a count left stale by a caller
+// (a workspace that was not zeroed) is cleared by the first arrival that meets it instead of
+// keeping every later merge from running.
 __device__ __forceinline__ bool arrive_last(uint32_t* count, int needed) {
     __shared__ uint32_t s_last;
     wait_stores();
     __syncthreads();
-    if (threadIdx.x == 0) {
-        const bool last =
-            __hip_atomic_fetch_add(count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-            (uint32_t)(needed - 1);
-        if (last) __hip_atomic_store(count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = last;
-    }
+    if (threadIdx.x == 0)
+        s_last = __builtin_amdgcn_atomic_inc32(count, (uint32_t)(needed - 1), __ATOMIC_RELAXED,
+                                               "agent") == (uint32_t)(needed - 1);
     __syncthreads();
     return s_last != 0;
 }

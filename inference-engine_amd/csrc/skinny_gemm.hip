@@ -17,13 +17,18 @@
 // region (rows of 160 bytes: both the row-wise stores and the fragment reads are free of bank
 // conflicts) and reads the MFMA fragments back. Batch b + 1 is loaded into registers while
 // batch b goes through LDS and the MFMAs. The eight partial D tiles are summed through LDS in
-// wave order and written as bf16. Launch modes below: 8-row n-tiles for narrow weights, and the
-// gate/up projection with the SiLU-gated product fused (ie_skinny_gemm_silu_mul).
+// wave order and written as bf16. Launch modes below: 8-row n-tiles for narrow weights, the
+// gate/up projection with the SiLU-gated product fused (ie_skinny_gemm_silu_mul), and the
+// residual add and RMSNorm of a decoder layer fused in (ie_skinny_gemm_fused): an RMSNorm
+// before the GEMM costs nothing but a sum of squares over the x fragments the waves already
+// hold, once its weight is folded into the GEMM's weight columns, and a residual add after it
+// is local to each output element.
 #include "ie_common.h"
 
 namespace ie {
 
 typedef __bf16 sg_bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 sg_bf16x2 __attribute__((ext_vector_type(2)));
 typedef float sg_f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t sg_u32x4 __attribute__((ext_vector_type(4)));
 
@@ -33,11 +38,16 @@ constexpr int SG_BK = 64;      // k per batch: 128 bytes of a row, one 8-lane lo
 constexpr int SG_LROW = 160;   // LDS row stride (bytes)
 constexpr int SG_MAX_TILES = 6;  // weight + x tiles, at most (LDS: 8 waves x 16 tiles' rows x 160 B)
 
-// Launch modes: plain n-tiles of 16 rows; one n-tile of 8 rows (HALF); GLU, the gate/up
+// Launch modes (bits): plain n-tiles of 16 rows; one n-tile of 8 rows (HALF); GLU, the gate/up
 // projection with the SiLU-gated product fused: n-tile t pairs gate rows [16 NT t, +16 NT) with
 // the up rows nh further (the weight is [gate; up], 2 nh rows) and the workgroup writes
-// bf16(silu(g) * u) from the bf16-rounded g and u, as silu_mul does with the GEMM's output.
-enum : int { SG_PLAIN = 0, SG_HALF = 1, SG_GLU = 2 };
+// bf16(silu(g) * u) from the bf16-rounded g and u, as silu_mul does with the GEMM's output;
+// NORM, x is a residual stream h whose RMSNorm feeds the GEMM: every fp32 sum of row m is scaled
+// by rstd_m = 1 / sqrt(sum_k h[m,k]^2 / K + eps) before it is rounded, the norm's weight having
+// been folded into the weight's columns by the caller (y = rstd_m * sum_k h[m,k] (g_k W[n,k]) is
+// the GEMM of the normalized rows); RES, y holds the residual stream on entry and each output
+// becomes bf16(y + bf16(sum)), in place (add_rms_norm's new residual, kernels.py:1240-1242).
+enum : int { SG_PLAIN = 0, SG_HALF = 1, SG_GLU = 2, SG_NORM = 4, SG_RES = 8 };
 
 template <int WT, int MT, int PT>
 struct SgLds {
@@ -45,6 +55,7 @@ struct SgLds {
         uint8_t t[SG_WAVES][16 * (WT + MT) * SG_LROW];  // per-wave transpose regions
         sg_f32x4 acc[SG_WAVES][PT * MT][IE_WAVE];       // partial D tiles (after the loop)
     };
+    float ss[SG_WAVES][16 * MT];  // NORM: each wave's sums of squares of x rows over its K slice
 };
 
 // MT m-tiles of 16 rows (M <= 16 MT), NT n-tiles of 16 weight rows per workgroup (every x
@@ -54,8 +65,9 @@ struct SgLds {
 template <int MT, int NT, int MODE>
 __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
     const uint16_t* __restrict__ x, int64_t xs, int M, const uint16_t* __restrict__ w, int64_t ws,
-    int K, uint16_t* __restrict__ y, int64_t ys, int nh) {
-    constexpr bool HALF = MODE == SG_HALF, GLU = MODE == SG_GLU;
+    int K, uint16_t* __restrict__ y, int64_t ys, int nh, float eps) {
+    constexpr bool HALF = MODE & SG_HALF, GLU = MODE & SG_GLU, NORM = MODE & SG_NORM,
+                   RES = MODE & SG_RES;
     constexpr int WT = GLU ? 2 * NT : NT;  // weight tiles: NT (GLU: NT gate, then NT up tiles)
     static_assert(WT + MT <= SG_MAX_TILES, "LDS transpose region too large");
     static_assert(!HALF || NT == 1, "8-row n-tiles come one per workgroup");
@@ -95,6 +107,11 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
     for (int nt = 0; nt < WT; ++nt)
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = sg_f32x4{0.f, 0.f, 0.f, 0.f};
+    // NORM: lane (l16, g) sums the squares of the x elements it holds (row 16 mt + l16, 8 of every
+    // 32 k of the slice); the four g lanes and eight waves together cover each row once
+    float ss[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) ss[mt] = 0.f;
 
     typedef sg_u32x4 Batch[TILES][2];
     // batch b: k [64 b, 64 b + 64) of the slice; chunks past the slice (or past the last batch)
@@ -131,6 +148,17 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
                 for (int mt = 0; mt < MT; ++mt)
                     acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f[nt], f[WT + mt],
                                                                          acc[nt][mt], 0, 0, 0);
+            if (NORM) {
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    const sg_bf16x8 v = f[WT + mt];
+#pragma unroll
+                    for (int j = 0; j < 8; j += 2) {
+                        const sg_bf16x2 p = {v[j], v[j + 1]};
+                        ss[mt] = __builtin_amdgcn_fdot2_f32_bf16(p, p, ss[mt], false);
+                    }
+                }
+            }
         }
     };
     // The batch loads are unconditional and each is pinned ahead of the work it overlaps with a
@@ -153,6 +181,14 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
     // through LDS first and the up tiles second, and the wave holding gate tile (nt, mt) keeps
     // its bf16-rounded values for the product with up tile (nt, mt) of the second round.
     float gate[4] = {0.f, 0.f, 0.f, 0.f};
+    if (NORM) {  // row sums over the four g lanes (xor 16, 32: fixed order), one slot per wave
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            ss[mt] += __shfl_xor(ss[mt], 16);
+            ss[mt] += __shfl_xor(ss[mt], 32);
+            if (g == 0) lds.ss[wave][16 * mt + l16] = ss[mt];
+        }
+    }
 #pragma unroll
     for (int round = 0; round < (GLU ? 2 : 1); ++round) {
         __syncthreads();  // every wave is done with its transpose region / the previous round
@@ -168,6 +204,14 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
             for (int v = 1; v < SG_WAVES; ++v) t += lds.acc[v][tile][lane];
             const int nt = tile / MT, mt = tile % MT;
             const int m = 16 * mt + l16;
+            if (NORM) {  // the row's sum of squares in wave order, then rstd (IEEE division, sqrt)
+                float s = lds.ss[0][m];
+#pragma unroll
+                for (int v = 1; v < SG_WAVES; ++v) s += lds.ss[v][m];
+                const float rstd = 1.0f / sqrtf(s / (float)K + eps);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) t[i] *= rstd;
+            }
             if (GLU) {
 #pragma clang fp contract(off)
 #pragma unroll
@@ -184,6 +228,14 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
             }
             if (m < M && (!HALF || g < 2)) {
                 uint16_t* dst = y + (int64_t)m * ys + n0 + 16 * nt + 4 * g;
+                if (RES) {  // bf16(residual + bf16(sum)) in fp32, as add_rms_norm adds
+                    const uint2 r = *reinterpret_cast<const uint2*>(dst);
+                    const uint32_t rw[2] = {r.x, r.y};
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        t[i] = bf16_to_f32((uint16_t)(rw[i / 2] >> (16 * (i % 2)))) +
+                               bf16_to_f32(f32_to_bf16_rne(t[i]));
+                }
                 *reinterpret_cast<uint2*>(dst) =
                     make_uint2(pack_bf16x2(t[0], t[1]), pack_bf16x2(t[2], t[3]));
             }
@@ -195,7 +247,7 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
 
 using namespace ie;
 
-// Shared argument checks of the two entry points (n: weight rows).
+// Argument checks shared by the entry points (n: weight rows).
 static hipError_t skinny_check(const ie_bf16* x, int64_t x_stride, int32_t m, const ie_bf16* weight,
                                int64_t weight_stride, int32_t n, int32_t k, int32_t n_tiles,
                                const ie_bf16* y, int64_t y_stride) {
@@ -217,71 +269,122 @@ static hipError_t skinny_check(const ie_bf16* x, int64_t x_stride, int32_t m, co
     return hipSuccess;
 }
 
-#define IE_SG_ARGS                                                                          \
-    (const uint16_t*)x, x_stride, m, (const uint16_t*)weight, weight_stride, k, (uint16_t*)y, \
-        y_stride, nh
+namespace {
+
+struct SgCall {
+    const uint16_t* x;
+    int64_t xs;
+    int m;
+    const uint16_t* w;
+    int64_t ws;
+    int k;
+    uint16_t* y;
+    int64_t ys;
+    int nh;
+    float eps;
+};
+
+template <int MT, int NT, int MODE>
+void sg_go(dim3 grid, hipStream_t s, const SgCall& c) {
+    hipLaunchKernelGGL((skinny_gemm_kernel<MT, NT, MODE>), grid, dim3(SG_THREADS), 0, s, c.x,
+                       c.xs, c.m, c.w, c.ws, c.k, c.y, c.ys, c.nh, c.eps);
+}
+
+// One weight row block per workgroup: n_tiles 0 (8 rows), 1, 2 or 4 n-tiles of 16 rows (4 only
+// where the LDS transpose region holds MT + 4 tiles; the caller has lowered n_tiles to fit).
+template <int MT, int EXTRA>
+void sg_rows(int n_tiles, dim3 grid, hipStream_t s, const SgCall& c) {
+    switch (n_tiles) {
+        case 0: sg_go<MT, 1, SG_HALF | EXTRA>(grid, s, c); break;
+        case 1: sg_go<MT, 1, EXTRA>(grid, s, c); break;
+        case 2: sg_go<MT, 2, EXTRA>(grid, s, c); break;
+        default:
+            if constexpr (MT + 4 <= SG_MAX_TILES) sg_go<MT, 4, EXTRA>(grid, s, c);
+            break;
+    }
+}
+
+template <int EXTRA>
+void sg_rows_mt(int mt, int n_tiles, dim3 grid, hipStream_t s, const SgCall& c) {
+    switch (mt) {
+        case 1: sg_rows<1, EXTRA>(n_tiles, grid, s, c); break;
+        case 2: sg_rows<2, EXTRA>(n_tiles, grid, s, c); break;
+        case 3: sg_rows<3, EXTRA>(n_tiles, grid, s, c); break;
+        default: sg_rows<4, EXTRA>(n_tiles, grid, s, c); break;
+    }
+}
+
+// Gate/up pairs: n_tiles 1 or 2 (2 only for MT <= 2, where the LDS region holds 2 + 2 + MT tiles).
+template <int EXTRA>
+void sg_glu_mt(int mt, int n_tiles, dim3 grid, hipStream_t s, const SgCall& c) {
+    switch (mt) {
+        case 1:
+            if (n_tiles == 2) sg_go<1, 2, SG_GLU | EXTRA>(grid, s, c);
+            else sg_go<1, 1, SG_GLU | EXTRA>(grid, s, c);
+            break;
+        case 2:
+            if (n_tiles == 2) sg_go<2, 2, SG_GLU | EXTRA>(grid, s, c);
+            else sg_go<2, 1, SG_GLU | EXTRA>(grid, s, c);
+            break;
+        case 3: sg_go<3, 1, SG_GLU | EXTRA>(grid, s, c); break;
+        default: sg_go<4, 1, SG_GLU | EXTRA>(grid, s, c); break;
+    }
+}
+
+}  // namespace
+
+extern "C" hipError_t ie_skinny_gemm_fused(const ie_bf16* x, int64_t x_stride, int32_t m,
+                                           const ie_bf16* weight, int64_t weight_stride,
+                                           int32_t n, int32_t k, int32_t n_tiles, int32_t flags,
+                                           float eps, ie_bf16* y, int64_t y_stride,
+                                           hipStream_t stream) {
+    IE_REQUIRE(m >= 0 && n >= 0 && k >= 0, "negative sizes");
+    IE_REQUIRE(flags == 0 || flags == IE_SKINNY_NORM || flags == IE_SKINNY_SILU_MUL ||
+                   flags == (IE_SKINNY_NORM | IE_SKINNY_SILU_MUL) || flags == IE_SKINNY_RESIDUAL,
+               "flags: 0, NORM, SILU_MUL, NORM | SILU_MUL or RESIDUAL");
+    const bool norm = flags & IE_SKINNY_NORM, glu = flags & IE_SKINNY_SILU_MUL,
+               res = flags & IE_SKINNY_RESIDUAL;
+    IE_REQUIRE(!norm || (eps >= 0.f && eps < 1e30f), "eps must be finite and >= 0");
+    if (m == 0 || n == 0) return hipSuccess;
+    if (glu) {
+        IE_REQUIRE(n_tiles == 1 || n_tiles == 2, "n_tiles must be 1 or 2");
+        IE_REQUIRE(n % 2 == 0 && (n / 2) % (16 * n_tiles) == 0,
+                   "n must be even and n / 2 a multiple of 16 n_tiles");
+    }
+    hipError_t e = skinny_check(x, x_stride, m, weight, weight_stride, n, k, n_tiles, y, y_stride);
+    if (e != hipSuccess) return e;
+    const int mt = (m + 15) / 16;
+    SgCall c{(const uint16_t*)x, x_stride, m, (const uint16_t*)weight, weight_stride, k,
+             (uint16_t*)y, y_stride, glu ? n / 2 : 0, eps};
+    if (glu) {
+        // gate and up tiles: lowered to one n-tile where m leaves too little LDS for two
+        if (2 * n_tiles + mt > SG_MAX_TILES) n_tiles = 1;
+        const dim3 grid((unsigned)(n / 2 / (16 * n_tiles)));
+        if (norm) sg_glu_mt<SG_NORM>(mt, n_tiles, grid, stream, c);
+        else sg_glu_mt<SG_PLAIN>(mt, n_tiles, grid, stream, c);
+        return hipGetLastError();
+    }
+    // n_tiles is a performance choice: it is lowered until the LDS transpose region fits
+    while (n_tiles > 1 && n_tiles + mt > SG_MAX_TILES) n_tiles >>= 1;
+    const dim3 grid((unsigned)(n_tiles == 0 ? n / 8 : n / (16 * n_tiles)));
+    if (norm) sg_rows_mt<SG_NORM>(mt, n_tiles, grid, stream, c);
+    else if (res) sg_rows_mt<SG_RES>(mt, n_tiles, grid, stream, c);
+    else sg_rows_mt<SG_PLAIN>(mt, n_tiles, grid, stream, c);
+    return hipGetLastError();
+}
 
 extern "C" hipError_t ie_skinny_gemm(const ie_bf16* x, int64_t x_stride, int32_t m,
                                      const ie_bf16* weight, int64_t weight_stride, int32_t n,
                                      int32_t k, int32_t n_tiles, ie_bf16* y, int64_t y_stride,
                                      hipStream_t stream) {
-    IE_REQUIRE(m >= 0 && n >= 0 && k >= 0, "negative sizes");
-    if (m == 0 || n == 0) return hipSuccess;
-    hipError_t e = skinny_check(x, x_stride, m, weight, weight_stride, n, k, n_tiles, y, y_stride);
-    if (e != hipSuccess) return e;
-    const int mt = (m + 15) / 16, nh = 0;
-    // n_tiles is a performance choice: it is lowered until the LDS transpose region fits
-    while (n_tiles > 1 && n_tiles + mt > SG_MAX_TILES) n_tiles >>= 1;
-    const bool half = n_tiles == 0;
-    const dim3 grid((unsigned)(half ? n / 8 : n / (16 * n_tiles)));
-#define IE_SG_LAUNCH(MT, NT, MODE) \
-    hipLaunchKernelGGL((skinny_gemm_kernel<MT, NT, MODE>), grid, dim3(SG_THREADS), 0, stream, IE_SG_ARGS)
-#define IE_SG_NT4(MT)                                   \
-    switch (n_tiles) {                                  \
-        case 0: IE_SG_LAUNCH(MT, 1, SG_HALF); break;    \
-        case 1: IE_SG_LAUNCH(MT, 1, SG_PLAIN); break;   \
-        case 2: IE_SG_LAUNCH(MT, 2, SG_PLAIN); break;   \
-        default: IE_SG_LAUNCH(MT, 4, SG_PLAIN); break;  \
-    }
-#define IE_SG_NT2(MT)                                   \
-    switch (n_tiles) {                                  \
-        case 0: IE_SG_LAUNCH(MT, 1, SG_HALF); break;    \
-        case 1: IE_SG_LAUNCH(MT, 1, SG_PLAIN); break;   \
-        default: IE_SG_LAUNCH(MT, 2, SG_PLAIN); break;  \
-    }
-    switch (mt) {  // (MT, NT) pairs within SG_MAX_TILES
-        case 1: IE_SG_NT4(1); break;
-        case 2: IE_SG_NT4(2); break;
-        case 3: IE_SG_NT2(3); break;
-        default: IE_SG_NT2(4); break;
-    }
-#undef IE_SG_NT4
-#undef IE_SG_NT2
-    return hipGetLastError();
+    return ie_skinny_gemm_fused(x, x_stride, m, weight, weight_stride, n, k, n_tiles, 0, 0.f, y,
+                                y_stride, stream);
 }
 
 extern "C" hipError_t ie_skinny_gemm_silu_mul(const ie_bf16* x, int64_t x_stride, int32_t m,
                                               const ie_bf16* weight, int64_t weight_stride,
                                               int32_t n, int32_t k, int32_t n_tiles, ie_bf16* y,
                                               int64_t y_stride, hipStream_t stream) {
-    IE_REQUIRE(m >= 0 && n >= 0 && k >= 0, "negative sizes");
-    if (m == 0 || n == 0) return hipSuccess;
-    IE_REQUIRE(n_tiles == 1 || n_tiles == 2, "n_tiles must be 1 or 2");
-    IE_REQUIRE(n % 2 == 0 && (n / 2) % (16 * n_tiles) == 0,
-               "n must be even and n / 2 a multiple of 16 n_tiles");
-    hipError_t e = skinny_check(x, x_stride, m, weight, weight_stride, n, k, n_tiles, y, y_stride);
-    if (e != hipSuccess) return e;
-    const int mt = (m + 15) / 16, nh = n / 2;
-    // gate and up tiles: lowered to one n-tile where m leaves too little LDS for two
-    if (2 * n_tiles + mt > SG_MAX_TILES) n_tiles = 1;
-    const dim3 grid((unsigned)(nh / (16 * n_tiles)));
-    switch (mt) {
-        case 1: if (n_tiles == 2) IE_SG_LAUNCH(1, 2, SG_GLU); else IE_SG_LAUNCH(1, 1, SG_GLU); break;
-        case 2: if (n_tiles == 2) IE_SG_LAUNCH(2, 2, SG_GLU); else IE_SG_LAUNCH(2, 1, SG_GLU); break;
-        case 3: IE_SG_LAUNCH(3, 1, SG_GLU); break;
-        default: IE_SG_LAUNCH(4, 1, SG_GLU); break;
-    }
-#undef IE_SG_LAUNCH
-    return hipGetLastError();
+    return ie_skinny_gemm_fused(x, x_stride, m, weight, weight_stride, n, k, n_tiles,
+                                IE_SKINNY_SILU_MUL, 0.f, y, y_stride, stream);
 }
-#undef IE_SG_ARGS

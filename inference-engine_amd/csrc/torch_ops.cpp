@@ -261,6 +261,44 @@ at::Tensor skinny_matmul_silu_mul(const at::Tensor& x, const at::Tensor& weight,
     return y;
 }
 
+// The GEMM of RMSNorm(h) with the norm weight folded into `weight` (ie_skinny_gemm_fused with
+// IE_SKINNY_NORM, and IE_SKINNY_SILU_MUL for the gate/up form).
+at::Tensor skinny_matmul_norm(const at::Tensor& h, const at::Tensor& weight, int64_t n_tiles,
+                              bool silu_mul, double eps) {
+    check_bf16_rows(h, "h", 2);
+    check_bf16_rows(weight, "weight", 2);
+    const c10::DeviceGuard guard(h.device());
+    const int64_t M = h.size(0), K = h.size(1), N = weight.size(0);
+    TORCH_CHECK(weight.size(1) == K, "ie: weight must be [N, K]");
+    TORCH_CHECK(!silu_mul || N % 2 == 0, "ie: weight must hold the gate rows then the up rows");
+    at::Tensor y = at::empty({M, silu_mul ? N / 2 : N}, h.options());
+    ok(ie_skinny_gemm_fused(bf(h), h.stride(0), (int32_t)M, bf(weight), weight.stride(0),
+                            (int32_t)N, (int32_t)K, (int32_t)n_tiles,
+                            IE_SKINNY_NORM | (silu_mul ? IE_SKINNY_SILU_MUL : 0), (float)eps,
+                            bfm(y), y.stride(0), stream_of(h)),
+       "skinny_matmul_norm");
+    return y;
+}
+
+// residual <- bf16(residual + bf16(x . weight^T)) in place (IE_SKINNY_RESIDUAL).
+at::Tensor skinny_matmul_residual_(const at::Tensor& x, const at::Tensor& weight, int64_t n_tiles,
+                                   at::Tensor residual) {
+    check_bf16_rows(x, "x", 2);
+    check_bf16_rows(weight, "weight", 2);
+    check_bf16_rows(residual, "residual", 2);
+    const c10::DeviceGuard guard(x.device());
+    const int64_t M = x.size(0), K = x.size(1), N = weight.size(0);
+    TORCH_CHECK(weight.size(1) == K, "ie: weight must be [N, K]");
+    TORCH_CHECK(residual.size(0) == M && residual.size(1) == N, "ie: residual must be [M, N]");
+    TORCH_CHECK(residual.device() == x.device() && weight.device() == x.device(),
+                "ie: x, weight and residual must be on one device");
+    ok(ie_skinny_gemm_fused(bf(x), x.stride(0), (int32_t)M, bf(weight), weight.stride(0),
+                            (int32_t)N, (int32_t)K, (int32_t)n_tiles, IE_SKINNY_RESIDUAL, 0.f,
+                            bfm(residual), residual.stride(0), stream_of(x)),
+       "skinny_matmul_residual_");
+    return residual;
+}
+
 struct DecodeCall {
     ie_kv_cache c;
     int32_t B, hq;
@@ -524,6 +562,12 @@ TORCH_LIBRARY(ie, m) {
     m.def("skinny_matmul(Tensor x, Tensor weight, int n_tiles=1) -> Tensor");
     m.def("skinny_matmul_silu_mul(Tensor x, Tensor weight, int n_tiles=1) -> Tensor");
     m.def(
+        "skinny_matmul_norm(Tensor h, Tensor weight, int n_tiles, bool silu_mul, float eps) "
+        "-> Tensor");
+    m.def(
+        "skinny_matmul_residual_(Tensor x, Tensor weight, int n_tiles, Tensor(a!) residual) "
+        "-> Tensor(a!)");
+    m.def(
         "decode_attention(Tensor q, Tensor k_cache, Tensor v_cache, Tensor k_scale, "
         "Tensor v_scale, Tensor k_calibration, Tensor cached_lens, Tensor slot_ids, "
         "Tensor num_decoding, float scale, Tensor(a!) out) -> ()");
@@ -558,6 +602,8 @@ TORCH_LIBRARY_IMPL(ie, CUDA, m) {
     m.impl("silu_mul", &silu_mul);
     m.impl("skinny_matmul", &skinny_matmul);
     m.impl("skinny_matmul_silu_mul", &skinny_matmul_silu_mul);
+    m.impl("skinny_matmul_norm", &skinny_matmul_norm);
+    m.impl("skinny_matmul_residual_", &skinny_matmul_residual_);
     m.impl("decode_attention", &decode_attention);
     m.impl("decode_attention_rope", &decode_attention_rope);
     m.impl("dequantize_kv_prefix", &dequantize_kv_prefix);

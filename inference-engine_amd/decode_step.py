@@ -14,6 +14,15 @@ kernels.py:1343-1370). All of these are this package's HIP kernels; for each pro
 (hipBLASLt), whichever `tune_linear` measured faster for that weight shape at the step's row
 count before capture, as the reference's engine does (engine.py:352-374).
 
+Fused form (`fused=True`, the default wherever the skinny GEMM serves all four layer
+projections): both add_rms_norm launches of a layer go into the projections beside them. Each
+RMSNorm weight is folded into the weight columns of the projection it feeds (input_norm into
+qkv, post_norm into gate_up: `fold_rms_norm_weight`), which then normalizes the residual
+stream's rows inside its own launch (`linear_norm`), and o_proj and down add their output to the
+residual stream in place (`linear_residual_`, bit for bit add_rms_norm's new residual). Per
+layer five launches instead of seven; the normalized rows differ from the two-launch form only
+in where the bf16 rounding falls (the folded weight is rounded instead of the normalized row).
+
 Weights are random (bf16, std 0.02) and the caches hold random int8 K/V: there is no checkpoint
 here, and the step's cost does not depend on the values.
 """
@@ -25,8 +34,9 @@ import torch.nn.functional as F
 from torch.cuda import nvtx
 
 from .attention_layer import attention, rope_inv_freq, rope_tables
-from .kernels import (LayerKVCache, add_rms_norm, decode_attention_rope, linear, linear_silu_mul,
-                      make_layer_cache, sample, tune_linear)
+from .kernels import (LayerKVCache, add_rms_norm, decode_attention_rope, fold_rms_norm_weight,
+                      linear, linear_norm, linear_residual_, linear_silu_mul, make_layer_cache,
+                      sample, tune_linear, use_skinny, use_skinny_glu)
 
 
 @dataclass(frozen=True)
@@ -102,8 +112,16 @@ class DecodeStep:
     cached_lens and slot_ids from fixed tensors, which the caller rewrites between replays."""
 
     def __init__(self, shape: Qwen3Shape, layers, embed, final_norm, caches: list[LayerKVCache],
-                 batch: int, device):
+                 batch: int, device, fused: bool = False):
+        """fused: fold every layer's input_norm into its qkv weight and post_norm into its
+        gate_up weight, in place (the layers then serve only the fused form)."""
         self.shape, self.layers, self.embed, self.final_norm = shape, layers, embed, final_norm
+        self.fused = fused
+        if fused:
+            for lw in layers:
+                lw.qkv = fold_rms_norm_weight(lw.qkv, lw.input_norm)
+                lw.gate_up = fold_rms_norm_weight(lw.gate_up, lw.post_norm)
+            self._zero = torch.zeros(batch, shape.model_dim, device=device, dtype=torch.bfloat16)
         self.caches = caches
         self.B = batch
         pool = caches[0].k.shape[0]
@@ -127,27 +145,42 @@ class DecodeStep:
     def attention(self, li, normed, cos, sin):
         """AttentionLayer.forward, pure-decode branch (architecture.py:85-122), through
         attention_layer.attention."""
-        s, lw, B = self.shape, self.layers[li], self.B
+        lw, B = self.layers[li], self.B
+        assert not self.fused
         with nvtx.range("qkv_proj"):
             qkv = linear(normed, lw.qkv)
+        out = self._attend(li, qkv, cos, sin)
+        with nvtx.range("o_proj"):
+            return linear(out.view(B, -1), lw.o_proj)
+
+    def _attend(self, li, qkv, cos, sin):
+        s, lw, B = self.shape, self.layers[li], self.B
         q, k, v = qkv.split([s.num_q_heads * s.head_dim, s.num_kv_heads * s.head_dim,
                              s.num_kv_heads * s.head_dim], dim=-1)
         q = q.view(B, s.num_q_heads, s.head_dim)
         k = k.view(B, s.num_kv_heads, s.head_dim)
         v = v.view(B, s.num_kv_heads, s.head_dim)
-        out = attention(q, k, v, None, None, cos, sin, self.caches[li], self.cached_lens,
-                        self.slot_ids, None, 0, None, self.num_decoding, lw.q_norm, lw.k_norm,
-                        s.eps)
-        with nvtx.range("o_proj"):
-            return linear(out.view(B, -1), lw.o_proj)
+        return attention(q, k, v, None, None, cos, sin, self.caches[li], self.cached_lens,
+                         self.slot_ids, None, 0, None, self.num_decoding, lw.q_norm, lw.k_norm,
+                         s.eps)
 
     def forward(self) -> torch.Tensor:
         """One step: returns the greedy next token of every sequence, int64 [B, 1]."""
+        h = self.hidden()
+        with nvtx.range("lm_head"):
+            logits = linear(h, self.embed)
+        with nvtx.range("sample"):
+            return sample(logits, 0.0, self.seed)
+
+    def hidden(self) -> torch.Tensor:
+        """The step up to the final RMSNorm: bf16 [B, model_dim], the LM head's input."""
         # the reference's ranges (architecture.py:278-304, 379-413, 477; engine.py:216)
         with nvtx.range("embed"):
             x = F.embedding(self.ids, self.embed)
         with nvtx.range("metadata"):
             cos, sin = self._rope()
+        if self.fused:
+            return self._hidden_fused(x, cos, sin)
         residual = None
         eps = self.shape.eps
         for li, lw in enumerate(self.layers):
@@ -163,10 +196,26 @@ class DecodeStep:
                     x = linear(linear_silu_mul(normed, lw.gate_up), lw.down)
         with nvtx.range("final_norm"):
             _, h = add_rms_norm(residual, x, self.final_norm, eps)
-        with nvtx.range("lm_head"):
-            logits = linear(h, self.embed)
-        with nvtx.range("sample"):
-            return sample(logits, 0.0, self.seed)
+        return h
+
+    def _hidden_fused(self, x, cos, sin):
+        """The layers in the fused form: h, the residual stream, is the embedding's output
+        (a new tensor every step), updated in place by o_proj and down."""
+        eps, h = self.shape.eps, x
+        for li, lw in enumerate(self.layers):
+            with nvtx.range("layer"):
+                with nvtx.range("attn"):
+                    with nvtx.range("qkv_proj"):  # input_norm inside (folded into lw.qkv)
+                        qkv = linear_norm(h, lw.qkv, eps)
+                    out = self._attend(li, qkv, cos, sin)
+                    with nvtx.range("o_proj"):  # + the residual add of the post-norm
+                        linear_residual_(out.view(self.B, -1), lw.o_proj, h)
+                with nvtx.range("mlp"):  # post_norm inside (folded into lw.gate_up)
+                    act = linear_norm(h, lw.gate_up, eps, silu_mul=True)
+                    linear_residual_(act, lw.down, h)
+        with nvtx.range("final_norm"):  # h already holds the last down projection's sum
+            _, hn = add_rms_norm(h, self._zero, self.final_norm, eps)
+        return hn
 
     def attention_only(self) -> torch.Tensor:
         """The step's attention kernels alone (per layer: decode_attention_rope, i.e.
@@ -207,19 +256,31 @@ class DecodeStep:
 
 
 def make_decode_step(batch=32, ctx_lo=128, ctx_hi=4096, shape=Qwen3Shape(), device="cuda",
-                     seed=0, tune=True):
+                     seed=0, tune=True, fused=None, norm_std=0.0):
     """Config-5 step: B sequences with cached lengths ~ U[ctx_lo, ctx_hi) - 1 (the new token is
-    the ctx-th), slots 0..B-1 of a pool of B + 1 (the last row is the engine's scratch slot)."""
+    the ctx-th), slots 0..B-1 of a pool of B + 1 (the last row is the engine's scratch slot).
+    fused=None: the fused form wherever tune_linear chose the skinny GEMM for all four layer
+    projections at this batch (always the case at B = 32). norm_std > 0: RMSNorm weights
+    1 + norm_std * N(0, 1) instead of ones."""
     layers, embed, final_norm = random_weights(shape, device, seed)
+    if norm_std > 0:
+        g = torch.Generator(device=device).manual_seed(seed + 2)
+        for t in [final_norm] + [n for lw in layers for n in (lw.input_norm, lw.post_norm)]:
+            t.copy_(1 + norm_std * torch.randn(t.shape, generator=g, device=device))
     caches = random_caches(shape, batch + 1, ctx_hi, device, seed)
-    step = DecodeStep(shape, layers, embed, final_norm, caches, batch, device)
+    if tune:  # one weight of every shape (the table is keyed by shape)
+        lw = layers[0]
+        tune_linear([lw.qkv, lw.o_proj, lw.gate_up, lw.down, embed], [batch])
+    if fused is None:
+        lw = layers[0]
+        fused = all(use_skinny.get((w.shape[0], w.shape[1], batch)) is not None
+                    for w in (lw.qkv, lw.o_proj, lw.gate_up, lw.down)) and \
+            (lw.gate_up.shape[0], lw.gate_up.shape[1], batch) in use_skinny_glu
+    step = DecodeStep(shape, layers, embed, final_norm, caches, batch, device, fused=fused)
     g = torch.Generator().manual_seed(seed)
     ctx = torch.randint(ctx_lo, ctx_hi, (batch,), generator=g)
     step.cached_lens.copy_((ctx - 1).to(torch.int32))
     step.ids.copy_(torch.randint(0, shape.vocab, (batch,), generator=g))
-    if tune:  # one weight of every shape (the table is keyed by shape)
-        lw = layers[0]
-        tune_linear([lw.qkv, lw.o_proj, lw.gate_up, lw.down, embed], [batch])
     return step
 
 

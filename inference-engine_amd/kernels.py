@@ -271,6 +271,52 @@ def linear_silu_mul(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     return silu_mul(torch.nn.functional.linear(x, weight))
 
 
+def fold_rms_norm_weight(weight: torch.Tensor, norm_weight: torch.Tensor) -> torch.Tensor:
+    """bf16(W[n, k] * g[k]): the weight of a projection whose input is RMSNorm(h) * g, folded
+    once (at load) for linear_norm, which then normalizes the rows inside the GEMM."""
+    assert weight.dim() == 2 and norm_weight.shape == (weight.shape[1],)
+    return (weight.float() * norm_weight.float()[None, :]).bfloat16()
+
+
+def _skinny_tiles(table: dict, key: tuple, default: int) -> int:
+    nt = table.get(key)
+    return default if nt is None else nt
+
+
+def linear_norm(h: torch.Tensor, weight_folded: torch.Tensor, eps: float,
+                silu_mul: bool = False) -> torch.Tensor:
+    """linear(add_rms_norm's normed output, W) (silu_mul: then silu_mul, the gate/up form) from
+    the residual stream h itself, in one skinny-GEMM launch (ie_skinny_gemm_fused with
+    IE_SKINNY_NORM): weight_folded = fold_rms_norm_weight(W, g). The rows' sums of squares come
+    from the GEMM's own reads of h, so the RMSNorm costs no launch (the reference runs
+    add_rms_norm, kernels.py:1260-1283, before each such projection, architecture.py:280-300).
+    M <= 64 rows; the tile width is the one tune_linear chose for the weight's shape."""
+    M, K = h.shape
+    N = weight_folded.shape[0]
+    assert h.stride(-1) == 1 and weight_folded.stride(-1) == 1 and M <= 64
+    key = (N, K, M)
+    if silu_mul:
+        nt = _skinny_tiles(use_skinny_glu, key, 1)
+        assert (N // 2) % (16 * nt) == 0 and K % 256 == 0
+    else:
+        nt = _skinny_tiles(use_skinny, key, 1)
+        assert N % (16 * max(1, nt)) == 0 and K % 256 == 0
+    return ops().skinny_matmul_norm(h, weight_folded, int(nt), bool(silu_mul), float(eps))
+
+
+def linear_residual_(x: torch.Tensor, weight: torch.Tensor, residual: torch.Tensor) -> torch.Tensor:
+    """residual <- bf16(residual + linear(x, weight)) in place and returned: add_rms_norm's
+    new residual for a projection's output (kernels.py:1240-1242), bit for bit, in the
+    projection's own launch (ie_skinny_gemm_fused with IE_SKINNY_RESIDUAL). M <= 64 rows."""
+    M, K = x.shape
+    N = weight.shape[0]
+    assert x.stride(-1) == 1 and weight.stride(-1) == 1 and M <= 64
+    assert residual.shape == (M, N) and residual.stride(-1) == 1
+    nt = _skinny_tiles(use_skinny, (N, K, M), 1)
+    assert N % (16 * max(1, nt)) == 0 and K % 256 == 0
+    return ops().skinny_matmul_residual_(x, weight, int(nt), residual)
+
+
 def linear(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     """qwen3-1.7b/kernels.py:1451-1458: [M, K] @ [N, K].T -> [M, N], with whichever measured
     faster."""

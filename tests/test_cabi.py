@@ -23,7 +23,8 @@ def test_torch_ops_registered(ie):
     for name in ["quantize_kv_prefill", "fused_rope_kv_decode", "fused_norm_rope_prefill",
                  "decode_attention", "decode_attention_rope", "dequantize_kv_prefix",
                  "prefill_attention", "decode_attention_workspace_size", "sample", "add_rms_norm",
-                 "silu_mul", "skinny_matmul", "skinny_matmul_silu_mul"]:
+                 "silu_mul", "skinny_matmul", "skinny_matmul_silu_mul", "skinny_matmul_norm",
+                 "skinny_matmul_residual_", "prefill_plan"]:
         assert hasattr(ops, name), name
 
 
@@ -184,3 +185,27 @@ def test_prefill_planned_rejects_bad_plans_on_host(native):
     assert b"null plan" in lib.ie_attn_last_error()
     assert call(p, grid - 1) == HIP_ERROR_INVALID_VALUE
     assert b"plan must hold" in lib.ie_attn_last_error()
+
+
+def test_skinny_gemm_fused_rejects_bad_flags_on_host(native):
+    """ie_skinny_gemm_fused: an undefined flag combination, a negative or infinite eps with
+    IE_SKINNY_NORM, and the gate/up form with n_tiles 4 are refused before any launch (the
+    pointers here are never dereferenced)."""
+    lib = native.cabi()
+    fn = lib.ie_skinny_gemm_fused
+    fn.restype = ctypes.c_int
+    i32, i64, f32 = ctypes.c_int32, ctypes.c_int64, ctypes.c_float
+    p = ctypes.c_void_p(1 << 20)
+
+    def call(flags, eps=1e-6, n_tiles=1):
+        return fn(p, i64(2048), i32(32), p, i64(2048), i32(4096), i32(2048), i32(n_tiles),
+                  i32(flags), f32(eps), p, i64(4096), ctypes.c_void_p(0))
+
+    for flags in (8, 1 | 4, 2 | 4, 7, -1):
+        assert call(flags) == HIP_ERROR_INVALID_VALUE, flags
+        assert b"flags" in lib.ie_attn_last_error()
+    for eps in (-1.0, float("inf"), float("nan")):
+        assert call(1, eps) == HIP_ERROR_INVALID_VALUE, eps
+        assert b"eps" in lib.ie_attn_last_error()
+    assert call(2, n_tiles=4) == HIP_ERROR_INVALID_VALUE
+    assert b"n_tiles" in lib.ie_attn_last_error()

@@ -1,0 +1,152 @@
+"""The skinny GEMM with a decoder layer's residual add and RMSNorm fused in (ie_skinny_gemm_fused,
+`linear_residual_`, `linear_norm`), which the decode step uses in place of the reference's
+add_rms_norm launches between its projections (qwen3-1.7b/kernels.py:1216-1283 at
+architecture.py:280-300):
+
+* the residual form is add_rms_norm's new residual bit for bit, given the plain GEMM's output:
+  bf16(residual + bf16(x W^T)) with the plain launch of the same tile width;
+* the norm form against the oracle's add_rms_norm followed by a float32 matmul, under a bound
+  that holds for any summation order: the folded weight bf16(g W) and the oracle's normalized
+  row bf16(h rstd g) each round one factor of every product once (at most 2^-9 relative each),
+  and the output is rounded once more;
+* rstd exactly as add_rms_norm computes it (IEEE 1 / sqrt(sum / K + eps)): rows with two nonzero
+  entries at opposite ends of K (summed by different waves) against integer weights, where
+  every product and sum is exact and the expected output is known bit for bit;
+* the gate/up form against the norm form's output passed through silu_mul.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import bf16_np, say
+from oracle import norm_act as ona
+from oracle.numerics import bf16_bits
+
+pytestmark = pytest.mark.gpu
+SHAPES = [(4096, 2048), (2048, 2048), (2048, 6144), (512, 256)]
+EPS = 1e-6
+
+
+def _tiles(N):
+    return [nt for nt in (0, 1, 2, 4) if N % (16 * max(1, nt)) == 0]
+
+
+@pytest.mark.parametrize("N,K", SHAPES)
+@pytest.mark.parametrize("M", [1, 17, 32, 64])
+def test_residual_form_is_add_rms_norm_residual(ie, dev, N, K, M):
+    g = torch.Generator().manual_seed(N + K + M + 100)
+    w = (0.02 * torch.randn(N, K, generator=g)).bfloat16().to(dev)
+    x = torch.randn(M, K, generator=g).bfloat16().to(dev)
+    res0 = (3 * torch.randn(M, N, generator=g)).bfloat16().to(dev)
+    K_ = ie.kernels
+    for nt in _tiles(N):
+        y = ie.skinny_matmul(x, w, nt)
+        res = res0.clone()
+        out = K_.ops().skinny_matmul_residual_(x, w, nt, res)
+        torch.cuda.synchronize()
+        assert out.data_ptr() == res.data_ptr()
+        want, _ = ona.add_rms_norm(bf16_np(res0), bf16_np(y), np.ones(N, np.float32), EPS)
+        bad = np.argwhere(bf16_bits(bf16_np(res)) != bf16_bits(want))
+        assert bad.size == 0, f"N={N} K={K} M={M} nt={nt}: {len(bad)} mismatches {bad[:4]}"
+    say(f"residual form N={N} K={K} M={M}: bit-exact")
+
+
+def _norm_inputs(M, K, N, seed, dev):
+    g = torch.Generator().manual_seed(seed)
+    h = (2 * torch.randn(M, K, generator=g)).bfloat16()
+    if M > 2:  # a large and a tiny row (rstd far from 1 both ways)
+        h[1] *= 300
+        h[2] *= 1e-3
+    gam = (1 + 0.3 * torch.randn(K, generator=g)).bfloat16()
+    w = (0.02 * torch.randn(N, K, generator=g)).bfloat16()
+    return h.to(dev), gam.to(dev), w.to(dev)
+
+
+def _check_norm(y, h, gam, w, what):
+    """|y - ref| <= 2^-8 * sum_k |h_k rstd g_k W_nk| + 2^-8 |ref|, ref = bf16 normalized rows of
+    the oracle's add_rms_norm times W in float32 (2^-8 covers the two 2^-9 roundings)."""
+    M, K = h.shape
+    _, normed = ona.add_rms_norm(bf16_np(h), np.zeros(h.shape, np.float32), bf16_np(gam), EPS)
+    ref = normed.astype(np.float64) @ bf16_np(w).astype(np.float64).T
+    _, nrm1 = ona.add_rms_norm(bf16_np(h), np.zeros(h.shape, np.float32), np.ones(K, np.float32),
+                               EPS)  # h * rstd without the weight, bf16-rounded
+    absterm = np.abs(nrm1).astype(np.float64) @ np.abs(
+        bf16_np(gam).astype(np.float64)[None, :] * bf16_np(w).astype(np.float64)).T
+    err = np.abs(bf16_np(y).astype(np.float64) - ref)
+    bound = 2.0 ** -8 * (absterm * 1.01 + np.abs(ref)) + 1e-30
+    assert np.all(err <= bound), f"{what}: max err/bound {np.max(err / bound):.3f}"
+
+
+@pytest.mark.parametrize("N,K", SHAPES)
+@pytest.mark.parametrize("M", [1, 17, 32, 64])
+def test_norm_form_against_oracle(ie, dev, N, K, M):
+    h, gam, w = _norm_inputs(M, K, N, N + K + M + 200, dev)
+    wf = ie.fold_rms_norm_weight(w, gam)
+    for nt in _tiles(N):
+        y = ie.kernels.ops().skinny_matmul_norm(h, wf, nt, False, EPS)
+        torch.cuda.synchronize()
+        assert y.shape == (M, N)
+        _check_norm(y, h, gam, w, f"norm form N={N} K={K} M={M} nt={nt}")
+    say(f"norm form N={N} K={K} M={M}: ok")
+
+
+@pytest.mark.parametrize("K", [256, 2048, 6144])
+def test_norm_form_rstd_exact(ie, dev, K):
+    """Row m holds a_m at k = 3 (the first wave's slice) and b_m at k = K - 5 (the last
+    wave's), W' small integers: a W'_3 + b W'_(K-5) and a^2 + b^2 are exact in float32, so the
+    output is bf16(rstd * that) with rstd = 1 / sqrt((a^2 + b^2) / K + eps), bit for bit."""
+    M, N = 20, 64
+    g = torch.Generator().manual_seed(K)
+    a = torch.tensor([1.5, -2.0, 0.25, 3.0, 0.0] * 4)
+    b = torch.tensor([-2.0, 0.5, 0.0, 96.0, 0.125] * 4)
+    h = torch.zeros(M, K)
+    h[:, 3], h[:, K - 5] = a, b
+    wf = torch.randint(-8, 9, (N, K), generator=g).float()
+    y = ie.kernels.ops().skinny_matmul_norm(h.bfloat16().to(dev), wf.bfloat16().to(dev), 1,
+                                            False, EPS)
+    torch.cuda.synchronize()
+    f32 = np.float32
+    an, bn, wn = a.numpy().astype(f32), b.numpy().astype(f32), wf.numpy().astype(f32)
+    ss = an * an + bn * bn
+    rstd = (f32(1) / np.sqrt((ss / f32(K) + f32(EPS)).astype(f32))).astype(f32)
+    acc = an[:, None] * wn[None, :, 3] + bn[:, None] * wn[None, :, K - 5]
+    want = (acc * rstd[:, None]).astype(f32)
+    from oracle.numerics import bf16_round
+    assert np.array_equal(bf16_bits(bf16_np(y)), bf16_bits(bf16_round(want))), f"K={K}"
+
+
+@pytest.mark.parametrize("N,K", [(12288, 2048), (1024, 512)])
+@pytest.mark.parametrize("M", [1, 17, 32, 64])
+def test_norm_gate_up_form(ie, dev, N, K, M):
+    h, gam, w = _norm_inputs(M, K, N, N + K + M + 300, dev)
+    wf = ie.fold_rms_norm_weight(w, gam)
+    for nt in (1, 2):
+        y = ie.kernels.ops().skinny_matmul_norm(h, wf, nt, True, EPS)
+        two = ie.silu_mul(ie.kernels.ops().skinny_matmul_norm(h, wf, nt, False, EPS))
+        torch.cuda.synchronize()
+        assert y.shape == (M, N // 2)
+        ref = two.float()
+        err = (y.float() - ref).abs()
+        # the gate and up sums may round to neighbouring bf16 values (another summation order)
+        bound = ref.abs() * 2 ** -7 + 2e-3 * ref.abs().max()
+        assert torch.all(err <= bound), f"N={N} K={K} M={M} nt={nt}: {err.max().item():.3e}"
+    say(f"norm gate/up form N={N} K={K} M={M}: ok")
+
+
+def test_linear_wrappers_follow_tuning_table(ie, dev):
+    """linear_norm / linear_residual_ take the tile width tune_linear chose (1 where none)."""
+    K_ = ie.kernels
+    h, gam, w = _norm_inputs(8, 512, 1024, 7, dev)
+    wf = ie.fold_rms_norm_weight(w, gam)
+    for choice in (None, 0, 2, 4):
+        K_.use_skinny[(1024, 512, 8)] = choice
+        _check_norm(K_.linear_norm(h, wf, EPS), h, gam, w, f"linear_norm table={choice}")
+        res0 = torch.randn(8, 1024, device=dev).bfloat16()
+        res = res0.clone()
+        K_.linear_residual_(h, w, res)
+        want = (res0.float() + K_.skinny_matmul(h, w, 1 if choice is None else choice).float())
+        torch.cuda.synchronize()
+        assert torch.equal(res, want.bfloat16()), f"linear_residual_ table={choice}"
+    K_.use_skinny.pop((1024, 512, 8))
+
