@@ -469,7 +469,7 @@ hipError_t ie_skinny_gemm_silu_mul(const ie_bf16* x, int64_t x_stride, int32_t m
  *                     the normalized row); combines with IE_SKINNY_SILU_MUL;
  *   IE_SKINNY_RESIDUAL   y holds the residual stream on entry and becomes
  *                     bf16(y + bf16(x . weight^T)) in place: add_rms_norm's new_residual for the
- *                     projection's output as delta, bit for bit.
+ *                     projection's output as delta, bit for bit (x must not overlap y).
  * Sizes, strides and n_tiles as for the plain or the gate/up form. The sum of squares is taken
  * from the bf16 rows of x over all k columns (eight partial sums combined in a fixed order).
  */
