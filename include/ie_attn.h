@@ -134,13 +134,15 @@ hipError_t ie_fused_rope_kv_decode(const ie_bf16* q, int64_t q_stride_b, int64_t
 /*
  * Bytes of device workspace ie_decode_attention needs for `batch` sequences of num_q_heads query
  * heads on the current device, whatever the GQA ratio: the arrival counts (one uint32 per
- * sequence and query head, the most any ratio uses, with room for max(batch, 1024) sequences,
- * padded to 256 bytes), then fp32 split-K partials, head_dim + 2 values per (query head, work
- * entry), where the work entries are at most ie_decode_attention_grid(batch, cdiv(num_q_heads,
- * 2)). The arrival counts must be zero when a workspace is first used (allocate it zeroed);
- * every call that completes leaves them zero again, so one workspace serves any number of calls
- * in stream order, of any batch up to 1024 (they share one count region). A workspace used with
- * a batch above 1024 serves that batch size only, unless zeroed again.
+ * sequence and query head, the most any ratio uses, with room for max(batch, 1024) sequences of
+ * max(num_q_heads, 128) heads, padded to 256 bytes), then fp32 split-K partials, head_dim + 2
+ * values per (query head, work entry), where the work entries are at most
+ * ie_decode_attention_grid(batch, cdiv(num_q_heads, 2)). The arrival counts must be zero when a
+ * workspace is first used (allocate it zeroed); every call that completes leaves them zero
+ * again, so one workspace (of the largest size any of them needs) serves any number of calls in
+ * stream order of any batch up to 1024 and any num_q_heads up to 128 (they share one count
+ * region). A workspace used with a larger batch or head count serves that shape only, unless
+ * zeroed again.
  */
 size_t ie_decode_attention_workspace_size(int32_t batch, int32_t num_q_heads, int32_t head_dim);
 
@@ -248,6 +250,33 @@ int32_t ie_decode_attention_grid(int32_t batch, int32_t num_units);
 hipError_t ie_decode_attention_plan(const int32_t* cached_lens, const int32_t* num_decoding,
                                     int32_t batch, int32_t num_units, int32_t* rows,
                                     hipStream_t stream);
+
+/*
+ * ie_decode_attention and ie_decode_attention_rope with their work list precomputed (no
+ * counterpart in the reference): the same arguments and results, plus `plan`, the rows
+ * ie_decode_attention_plan wrote for the same cached_lens and num_decoding values, batch,
+ * num_units (KV heads x query-head pairs) and device, 16-byte aligned, and plan_rows, their
+ * count (at least ie_decode_attention_grid(batch, num_units)). Each workgroup reads its entry in
+ * one load instead of deriving the work split from cached_lens. For engines that run every
+ * layer of a decode step over one step's metadata: compute the plan once per step. A plan that
+ * does not match the arguments is undefined behaviour (its rows name the sequences, pieces and
+ * merges of each workgroup).
+ */
+hipError_t ie_decode_attention_planned(
+    const ie_bf16* q, int64_t q_stride_b, int64_t q_stride_h, int32_t batch, int32_t num_q_heads,
+    const ie_kv_cache* cache, const int32_t* cached_lens, const int32_t* slot_ids,
+    const int32_t* num_decoding, const int32_t* plan, int64_t plan_rows, float scale,
+    ie_bf16* out, int64_t out_stride_b, int64_t out_stride_h, void* workspace,
+    size_t workspace_bytes, hipStream_t stream);
+hipError_t ie_decode_attention_rope_planned(
+    const ie_bf16* q, int64_t q_stride_b, int64_t q_stride_h, const ie_bf16* k,
+    int64_t k_stride_b, int64_t k_stride_h, const ie_bf16* v, int64_t v_stride_b,
+    int64_t v_stride_h, const ie_bf16* q_norm_weight, const ie_bf16* k_norm_weight,
+    const ie_bf16* cos, int64_t cos_stride_b, const ie_bf16* sin, int64_t sin_stride_b,
+    float eps, int32_t batch, int32_t num_q_heads, const ie_kv_cache* cache,
+    const int32_t* cached_lens, const int32_t* slot_ids, const int32_t* num_decoding,
+    const int32_t* plan, int64_t plan_rows, float scale, ie_bf16* out, int64_t out_stride_b,
+    int64_t out_stride_h, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /*
  * Prefill-side q/k RMSNorm + RoPE over packed tokens.

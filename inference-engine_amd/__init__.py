@@ -13,6 +13,7 @@ from .kernels import (  # noqa: F401
     add_rms_norm,
     decode_attention,
     decode_attention_rope,
+    decode_plan,
     dequantize_kv_prefix,
     fold_rms_norm_weight,
     fused_norm_rope_prefill,

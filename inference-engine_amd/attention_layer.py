@@ -61,12 +61,15 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, seq_ids, cu_seq
               cached_lens: torch.Tensor, slot_ids: torch.Tensor, tile_start,
               prefill_block_m: int, prefix_scratch, num_decoding: torch.Tensor,
               q_norm_weight: torch.Tensor, k_norm_weight: torch.Tensor,
-              eps: float = 1e-6, prefill_plan: torch.Tensor | None = None) -> torch.Tensor:
+              eps: float = 1e-6, prefill_plan: torch.Tensor | None = None,
+              decode_plan: torch.Tensor | None = None) -> torch.Tensor:
     """architecture.py:98-197. q [N, Hq, D], k/v [N, Hkv, D] (views of the QKV projection's
     output, before norm and RoPE). Returns [N, Hq, D]: in a step with prefill, rows of the
     prefilling entries from prefill attention and rows [0, num_decoding) from decode
     attention. prefill_plan: kernels.prefill_plan of the step's metadata, computed once per step
-    for all layers (None: each prefill launch derives its work list itself)."""
+    for all layers (None: each prefill launch derives its work list itself); decode_plan:
+    likewise kernels.decode_plan(cached_lens, num_decoding, len(slot_ids), Hq, Hkv) for the
+    decode launch."""
     D = q.shape[-1]
     if cu_seqlens is None:
         # the reference's "rope_kv_write" and "decode_attention" ranges (architecture.py:100,
@@ -74,7 +77,7 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, seq_ids, cu_seq
         with nvtx.range("rope_kv_write+decode_attention"):
             return decode_attention_rope(q, k, v, q_norm_weight, k_norm_weight, cos, sin,
                                          slot_ids, kv_cache, cached_lens, num_decoding, eps,
-                                         D ** -0.5)
+                                         D ** -0.5, plan=decode_plan)
     assert seq_ids is not None and tile_start is not None and prefix_scratch is not None
     # every kernel sees the whole packet and skips the entries that are not its own, so nothing
     # here depends on how many entries decode; the decode rows are normed and roped here too
@@ -91,7 +94,7 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, seq_ids, cu_seq
     with nvtx.range("rope_kv_write+decode_attention"):
         decode_attention_rope(q[:B], k[:B], v[:B], q_norm_weight, k_norm_weight, cos[:B],
                               sin[:B], slot_ids, kv_cache, cached_lens, num_decoding, eps,
-                              D ** -0.5, out=out)
+                              D ** -0.5, out=out, plan=decode_plan)
     return out
 
 

@@ -168,6 +168,9 @@ struct DecodeArgs {
     float* part_m;       // [Hq, nwork]
     float* part_l;       // [Hq, nwork]
     uint32_t* arrivals;  // [B, Hkv]: pieces of the sequence done; 0 between calls
+    // The work list precomputed for this step (ie_decode_attention_plan: row w = (b, split,
+    // needed, piece) of workgroup index w), or null: every workgroup derives its entry itself.
+    const int32_t* plan;
     int target, nwork, hq, hkv;
     int ratio;   // query heads per KV head (GQA ratio, 1 ... 16)
     int npairs;  // query-head pairs per KV head, cdiv(ratio, 2): a workgroup serves one pair
@@ -360,7 +363,13 @@ __attribute__((amdgpu_waves_per_eu(IE_DECODE_WAVES_PER_EU))) void decode_attenti
     const int qh0 = GQA2 ? 2 * hk : uniform(a.ratio * hk + 2 * pair);
     const bool has2 = GQA2 || 2 * pair + 1 < a.ratio;
     const int qh1 = has2 ? qh0 + 1 : qh0;  // an absent second head repeats the first
-    Work wk = decode_assign(a.cached_lens, nd, item, a.target, raw0);
+    Work wk;
+    if (a.plan) {  // one 16-byte row, requested with the loads above
+        const int4 r = *reinterpret_cast<const int4*>(a.plan + 4 * item);
+        wk = Work{r.x, r.y, r.z, r.w};
+    } else {
+        wk = decode_assign(a.cached_lens, nd, item, a.target, raw0);
+    }
     // Wave-uniform by construction; readfirstlane lets the compiler keep them (and the buffer
     // descriptors built from them) in SGPRs.
     wk.needed = uniform(wk.needed);
@@ -767,10 +776,14 @@ __global__ __launch_bounds__(64) void decode_plan_kernel(const int32_t* __restri
 // Workspace: the arrival counts (one per sequence and KV head; zero on entry, and every call
 // leaves them zero), then fp32 partials (acc, m, l) of every (query head, work entry): one per
 // piece, since pieces never outnumber the decode launch's work entries per KV head. The count
-// region has room for DA_COUNT_CAP sequences whatever the batch, so calls of any batch up to
-// that size agree on where the counts are and their partials never land on them: one workspace
-// serves them all. A larger batch gets a count region of its own size.
+// region has room for DA_COUNT_CAP sequences and DA_COUNT_HEADS query heads whatever the batch
+// and the head count, so calls of any batch and head count up to those agree on where the
+// counts are and their partials never land on them: one workspace serves them all. (Sized by
+// the call's own head count, a call with fewer query heads would write partials over the count
+// words of a later call with more sequences or heads.) A larger batch or head count gets a
+// count region of its own size.
 constexpr int DA_COUNT_CAP = 1024;
+constexpr int DA_COUNT_HEADS = 128;
 struct Layout {
     int waves, target, nwork;
     size_t arr_off, acc_off, m_off, l_off, bytes;
@@ -789,7 +802,8 @@ static Layout workspace_layout(int batch, int hq, int units) {
     L.nwork = batch <= L.target ? L.target : L.target + batch;
     const size_t rows = (size_t)hq * L.nwork;
     L.arr_off = 0;
-    L.acc_off = ((size_t)std::max(batch, DA_COUNT_CAP) * hq * sizeof(uint32_t) + 255) / 256 * 256;
+    L.acc_off = ((size_t)std::max(batch, DA_COUNT_CAP) * std::max(hq, DA_COUNT_HEADS) *
+                     sizeof(uint32_t) + 255) / 256 * 256;
     L.m_off = L.acc_off + rows * DA_D * sizeof(float);
     L.l_off = L.m_off + rows * sizeof(float);
     L.bytes = L.l_off + rows * sizeof(float);
@@ -917,39 +931,76 @@ static hipError_t decode_launch(DecodeArgs& a, const Layout& L, int32_t batch,
     return hipGetLastError();
 }
 
+// A precomputed work list must cover the launch's grid (plan_rows >= its work entries).
+static hipError_t check_plan(const int32_t* plan, int64_t plan_rows, const Layout& L) {
+    IE_REQUIRE(plan != nullptr, "null plan");
+    IE_REQUIRE(plan_rows >= L.nwork,
+               "plan must hold ie_decode_attention_grid(batch, units) rows");
+    IE_REQUIRE((reinterpret_cast<uintptr_t>(plan) & 15) == 0, "plan must be 16-byte aligned");
+    return hipSuccess;
+}
+
+static hipError_t decode_plain(const ie_bf16* q, int64_t q_stride_b, int64_t q_stride_h,
+                               int32_t batch, int32_t num_q_heads, const ie_kv_cache* cache,
+                               const int32_t* cached_lens, const int32_t* slot_ids,
+                               const int32_t* num_decoding, float scale, ie_bf16* out,
+                               int64_t out_stride_b, int64_t out_stride_h, void* workspace,
+                               size_t workspace_bytes, const int32_t* plan, int64_t plan_rows,
+                               bool planned, hipStream_t stream) {
+    Layout L{};
+    hipError_t e = check_decode(q, batch, num_q_heads, cache, cached_lens, slot_ids, num_decoding,
+                                out, q_stride_b, q_stride_h, workspace, workspace_bytes, &L);
+    if (e != hipSuccess || batch == 0) return e;
+    if (planned && (e = check_plan(plan, plan_rows, L)) != hipSuccess) return e;
+    DecodeArgs a = decode_args(q, q_stride_b, q_stride_h, batch, num_q_heads, cache, cached_lens,
+                               slot_ids, num_decoding, scale, out, out_stride_b, out_stride_h,
+                               workspace, L);
+    a.plan = planned ? plan : nullptr;
+    return decode_launch<false>(a, L, batch, cache, stream);
+}
+
 extern "C" hipError_t ie_decode_attention(
     const ie_bf16* q, int64_t q_stride_b, int64_t q_stride_h, int32_t batch, int32_t num_q_heads,
     const ie_kv_cache* cache, const int32_t* cached_lens, const int32_t* slot_ids,
     const int32_t* num_decoding, float scale, ie_bf16* out, int64_t out_stride_b,
     int64_t out_stride_h, void* workspace, size_t workspace_bytes, hipStream_t stream) {
-    Layout L{};
-    hipError_t e = check_decode(q, batch, num_q_heads, cache, cached_lens, slot_ids, num_decoding,
-                                out, q_stride_b, q_stride_h, workspace, workspace_bytes, &L);
-    if (e != hipSuccess || batch == 0) return e;
-    DecodeArgs a = decode_args(q, q_stride_b, q_stride_h, batch, num_q_heads, cache, cached_lens,
-                               slot_ids, num_decoding, scale, out, out_stride_b, out_stride_h,
-                               workspace, L);
-    return decode_launch<false>(a, L, batch, cache, stream);
+    return decode_plain(q, q_stride_b, q_stride_h, batch, num_q_heads, cache, cached_lens,
+                        slot_ids, num_decoding, scale, out, out_stride_b, out_stride_h, workspace,
+                        workspace_bytes, nullptr, 0, false, stream);
 }
 
-extern "C" hipError_t ie_decode_attention_rope(
+extern "C" hipError_t ie_decode_attention_planned(
+    const ie_bf16* q, int64_t q_stride_b, int64_t q_stride_h, int32_t batch, int32_t num_q_heads,
+    const ie_kv_cache* cache, const int32_t* cached_lens, const int32_t* slot_ids,
+    const int32_t* num_decoding, const int32_t* plan, int64_t plan_rows, float scale,
+    ie_bf16* out, int64_t out_stride_b, int64_t out_stride_h, void* workspace,
+    size_t workspace_bytes, hipStream_t stream) {
+    return decode_plain(q, q_stride_b, q_stride_h, batch, num_q_heads, cache, cached_lens,
+                        slot_ids, num_decoding, scale, out, out_stride_b, out_stride_h, workspace,
+                        workspace_bytes, plan, plan_rows, true, stream);
+}
+
+static hipError_t decode_rope(
     const ie_bf16* q, int64_t q_stride_b, int64_t q_stride_h, const ie_bf16* k,
     int64_t k_stride_b, int64_t k_stride_h, const ie_bf16* v, int64_t v_stride_b,
     int64_t v_stride_h, const ie_bf16* q_norm_weight, const ie_bf16* k_norm_weight,
     const ie_bf16* cos, int64_t cos_stride_b, const ie_bf16* sin, int64_t sin_stride_b,
     float eps, int32_t batch, int32_t num_q_heads, const ie_kv_cache* cache,
     const int32_t* cached_lens, const int32_t* slot_ids, const int32_t* num_decoding,
-    float scale, ie_bf16* out, int64_t out_stride_b, int64_t out_stride_h, void* workspace,
-    size_t workspace_bytes, hipStream_t stream) {
+    const int32_t* plan, int64_t plan_rows, bool planned, float scale, ie_bf16* out,
+    int64_t out_stride_b, int64_t out_stride_h, void* workspace, size_t workspace_bytes,
+    hipStream_t stream) {
     Layout L{};
     hipError_t e = check_decode(q, batch, num_q_heads, cache, cached_lens, slot_ids, num_decoding,
                                 out, q_stride_b, q_stride_h, workspace, workspace_bytes, &L,
                                 false);
     if (e != hipSuccess || batch == 0) return e;
     IE_REQUIRE(k && v && q_norm_weight && k_norm_weight && cos && sin, "null pointer");
+    if (planned && (e = check_plan(plan, plan_rows, L)) != hipSuccess) return e;
     DecodeArgs a = decode_args(q, q_stride_b, q_stride_h, batch, num_q_heads, cache, cached_lens,
                                slot_ids, num_decoding, scale, out, out_stride_b, out_stride_h,
                                workspace, L);
+    a.plan = planned ? plan : nullptr;
     a.k_new = (const uint16_t*)k;
     a.k_sb = k_stride_b;
     a.k_sh = k_stride_h;
@@ -964,6 +1015,38 @@ extern "C" hipError_t ie_decode_attention_rope(
     a.sin_sb = sin_stride_b;
     a.eps = eps;
     return decode_launch<true>(a, L, batch, cache, stream);
+}
+
+extern "C" hipError_t ie_decode_attention_rope(
+    const ie_bf16* q, int64_t q_stride_b, int64_t q_stride_h, const ie_bf16* k,
+    int64_t k_stride_b, int64_t k_stride_h, const ie_bf16* v, int64_t v_stride_b,
+    int64_t v_stride_h, const ie_bf16* q_norm_weight, const ie_bf16* k_norm_weight,
+    const ie_bf16* cos, int64_t cos_stride_b, const ie_bf16* sin, int64_t sin_stride_b,
+    float eps, int32_t batch, int32_t num_q_heads, const ie_kv_cache* cache,
+    const int32_t* cached_lens, const int32_t* slot_ids, const int32_t* num_decoding,
+    float scale, ie_bf16* out, int64_t out_stride_b, int64_t out_stride_h, void* workspace,
+    size_t workspace_bytes, hipStream_t stream) {
+    return decode_rope(q, q_stride_b, q_stride_h, k, k_stride_b, k_stride_h, v, v_stride_b,
+                       v_stride_h, q_norm_weight, k_norm_weight, cos, cos_stride_b, sin,
+                       sin_stride_b, eps, batch, num_q_heads, cache, cached_lens, slot_ids,
+                       num_decoding, nullptr, 0, false, scale, out, out_stride_b, out_stride_h,
+                       workspace, workspace_bytes, stream);
+}
+
+extern "C" hipError_t ie_decode_attention_rope_planned(
+    const ie_bf16* q, int64_t q_stride_b, int64_t q_stride_h, const ie_bf16* k,
+    int64_t k_stride_b, int64_t k_stride_h, const ie_bf16* v, int64_t v_stride_b,
+    int64_t v_stride_h, const ie_bf16* q_norm_weight, const ie_bf16* k_norm_weight,
+    const ie_bf16* cos, int64_t cos_stride_b, const ie_bf16* sin, int64_t sin_stride_b,
+    float eps, int32_t batch, int32_t num_q_heads, const ie_kv_cache* cache,
+    const int32_t* cached_lens, const int32_t* slot_ids, const int32_t* num_decoding,
+    const int32_t* plan, int64_t plan_rows, float scale, ie_bf16* out, int64_t out_stride_b,
+    int64_t out_stride_h, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    return decode_rope(q, q_stride_b, q_stride_h, k, k_stride_b, k_stride_h, v, v_stride_b,
+                       v_stride_h, q_norm_weight, k_norm_weight, cos, cos_stride_b, sin,
+                       sin_stride_b, eps, batch, num_q_heads, cache, cached_lens, slot_ids,
+                       num_decoding, plan, plan_rows, true, scale, out, out_stride_b,
+                       out_stride_h, workspace, workspace_bytes, stream);
 }
 
 extern "C" int32_t ie_decode_attention_grid(int32_t batch, int32_t num_units) {
@@ -1037,9 +1120,10 @@ extern "C" hipError_t ie_decode_attention_noalloc(
                "num_q_heads must be num_kv_heads times a GQA ratio of 1 to 16");
     const Layout L =
         workspace_layout(batch, num_q_heads, decode_units(num_q_heads, (int)cache->num_kv_heads));
-    IE_REQUIRE(batch <= DA_COUNT_CAP && L.bytes <= DA_SCRATCH_BYTES,
-               "batch too large for the no-alloc decode scratch (at most 1024 sequences in "
-               "16 MiB; use ie_decode_attention with a workspace)");
+    IE_REQUIRE(batch <= DA_COUNT_CAP && num_q_heads <= DA_COUNT_HEADS &&
+                   L.bytes <= DA_SCRATCH_BYTES,
+               "batch too large for the no-alloc decode scratch (at most 1024 sequences and "
+               "128 query heads in 16 MiB; use ie_decode_attention with a workspace)");
     void* ws = nullptr;
     e = scratch_address(&ws);
     if (e != hipSuccess) return e;

@@ -305,6 +305,22 @@ struct DecodeCall {
     size_t ws_bytes;
 };
 
+// A decode work list from decode_plan: int32 [rows, 4], contiguous, on q's device.
+void check_decode_plan(const at::Tensor& plan, const at::Tensor& q) {
+    check_dev(plan, "plan");
+    TORCH_CHECK(plan.scalar_type() == at::kInt && plan.dim() == 2 && plan.size(1) == 4 &&
+                    plan.is_contiguous(),
+                "ie: plan must be a contiguous int32 [rows, 4] tensor (decode_plan)");
+    TORCH_CHECK(plan.device() == q.device(), "ie: plan must be on q's device");
+}
+
+// The kept decode workspace a call uses: calls of up to 1024 sequences and 128 query heads
+// share one (their count regions coincide), every larger shape has one of its own.
+int32_t decode_ws_kind(const DecodeCall& d) {
+    if (d.B <= 1024 && d.hq <= 128) return 0;
+    return (int32_t)std::min<int64_t>((int64_t)d.B * 1024 + std::min(d.hq, 1023), INT32_MAX);
+}
+
 DecodeCall decode_prep(const at::Tensor& q, const at::Tensor& k_cache, const at::Tensor& v_cache,
                        const at::Tensor& k_scale, const at::Tensor& v_scale,
                        const at::Tensor& k_calibration, const at::Tensor& cached_lens,
@@ -388,13 +404,23 @@ void decode_attention(const at::Tensor& q, const at::Tensor& k_cache, const at::
                       const at::Tensor& k_scale, const at::Tensor& v_scale,
                       const at::Tensor& k_calibration, const at::Tensor& cached_lens,
                       const at::Tensor& slot_ids, const at::Tensor& num_decoding, double scale,
-                      const at::Tensor& out) {
+                      const at::Tensor& out, const c10::optional<at::Tensor>& plan) {
     const c10::DeviceGuard guard(q.device());
     DecodeCall d = decode_prep(q, k_cache, v_cache, k_scale, v_scale, k_calibration, cached_lens,
                                slot_ids, num_decoding, out);
     at::Tensor ws = persistent_workspace(
         q, d.ws_bytes, ie_decode_attention_workspace_counts_bytes(d.B, d.hq),
-        d.B <= 1024 ? 0 : d.B);
+        decode_ws_kind(d));
+    if (plan.has_value()) {
+        check_decode_plan(*plan, q);
+        ok(ie_decode_attention_planned(bf(q), q.stride(0), q.stride(1), d.B, d.hq, &d.c,
+                                       i32(cached_lens), i32(slot_ids), i32(num_decoding),
+                                       i32(*plan), plan->size(0), (float)scale, bfm(out),
+                                       out.stride(0), out.stride(1), ws.data_ptr(), d.ws_bytes,
+                                       stream_of(q)),
+           "decode_attention");
+        return;
+    }
     ok(ie_decode_attention(bf(q), q.stride(0), q.stride(1), d.B, d.hq, &d.c, i32(cached_lens),
                            i32(slot_ids), i32(num_decoding), (float)scale, bfm(out),
                            out.stride(0), out.stride(1), ws.data_ptr(), d.ws_bytes, stream_of(q)),
@@ -410,7 +436,8 @@ void decode_attention_rope(const at::Tensor& q, const at::Tensor& k, const at::T
                            const at::Tensor& k_scale, const at::Tensor& v_scale,
                            const at::Tensor& k_calibration, const at::Tensor& cached_lens,
                            const at::Tensor& slot_ids, const at::Tensor& num_decoding,
-                           double eps, double scale, const at::Tensor& out) {
+                           double eps, double scale, const at::Tensor& out,
+                           const c10::optional<at::Tensor>& plan) {
     check_bf16_rows(k, "k", 3);
     check_bf16_rows(v, "v", 3);
     check_bf16_rows(q_norm_weight, "q_norm_weight", 1);
@@ -428,7 +455,19 @@ void decode_attention_rope(const at::Tensor& q, const at::Tensor& k, const at::T
                 "ie: cos/sin must be [B,1,64]");
     at::Tensor ws = persistent_workspace(
         q, d.ws_bytes, ie_decode_attention_workspace_counts_bytes(d.B, d.hq),
-        d.B <= 1024 ? 0 : d.B);
+        decode_ws_kind(d));
+    if (plan.has_value()) {
+        check_decode_plan(*plan, q);
+        ok(ie_decode_attention_rope_planned(
+               bf(q), q.stride(0), q.stride(1), bf(k), k.stride(0), k.stride(1), bf(v),
+               v.stride(0), v.stride(1), bf(q_norm_weight), bf(k_norm_weight), bf(cos),
+               cos.stride(0), bf(sin), sin.stride(0), (float)eps, d.B, d.hq, &d.c,
+               i32(cached_lens), i32(slot_ids), i32(num_decoding), i32(*plan), plan->size(0),
+               (float)scale, bfm(out), out.stride(0), out.stride(1), ws.data_ptr(), d.ws_bytes,
+               stream_of(q)),
+           "decode_attention_rope");
+        return;
+    }
     ok(ie_decode_attention_rope(bf(q), q.stride(0), q.stride(1), bf(k), k.stride(0), k.stride(1),
                                 bf(v), v.stride(0), v.stride(1), bf(q_norm_weight),
                                 bf(k_norm_weight), bf(cos), cos.stride(0), bf(sin),
@@ -437,6 +476,27 @@ void decode_attention_rope(const at::Tensor& q, const at::Tensor& k, const at::T
                                 out.stride(0), out.stride(1), ws.data_ptr(), d.ws_bytes,
                                 stream_of(q)),
        "decode_attention_rope");
+}
+
+// The decode launch's work list for one step's metadata (ie_decode_attention_plan): int32
+// [grid, 4] on cached_lens' device, to pass to every layer's decode launch of that step.
+at::Tensor decode_plan(const at::Tensor& cached_lens, const at::Tensor& num_decoding,
+                       int64_t batch, int64_t num_q_heads, int64_t num_kv_heads) {
+    check_i32(cached_lens, "cached_lens");
+    check_i32(num_decoding, "num_decoding");
+    const c10::DeviceGuard guard(cached_lens.device());
+    TORCH_CHECK(batch >= 0 && cached_lens.size(0) >= batch, "ie: cached_lens too short");
+    TORCH_CHECK(num_kv_heads > 0 && num_q_heads > 0 && num_q_heads % num_kv_heads == 0 &&
+                    num_q_heads / num_kv_heads <= 16,
+                "ie: num_q_heads must be num_kv_heads times a GQA ratio of 1 to 16");
+    const int32_t units =
+        (int32_t)(num_kv_heads * ((num_q_heads / num_kv_heads + 1) / 2));
+    const int32_t grid = ie_decode_attention_grid((int32_t)batch, units);
+    at::Tensor rows = at::empty({std::max(grid, 1), 4}, cached_lens.options());
+    ok(ie_decode_attention_plan(i32(cached_lens), i32(num_decoding), (int32_t)batch, units,
+                                i32m(rows), stream_of(cached_lens)),
+       "decode_plan");
+    return rows;
 }
 
 int64_t decode_attention_workspace_size(int64_t batch, int64_t num_q_heads) {
@@ -570,12 +630,16 @@ TORCH_LIBRARY(ie, m) {
     m.def(
         "decode_attention(Tensor q, Tensor k_cache, Tensor v_cache, Tensor k_scale, "
         "Tensor v_scale, Tensor k_calibration, Tensor cached_lens, Tensor slot_ids, "
-        "Tensor num_decoding, float scale, Tensor(a!) out) -> ()");
+        "Tensor num_decoding, float scale, Tensor(a!) out, Tensor? plan=None) -> ()");
     m.def(
         "decode_attention_rope(Tensor q, Tensor k, Tensor v, Tensor q_norm_weight, "
         "Tensor k_norm_weight, Tensor cos, Tensor sin, Tensor(a!) k_cache, Tensor(b!) v_cache, "
         "Tensor(c!) k_scale, Tensor(d!) v_scale, Tensor k_calibration, Tensor cached_lens, "
-        "Tensor slot_ids, Tensor num_decoding, float eps, float scale, Tensor(e!) out) -> ()");
+        "Tensor slot_ids, Tensor num_decoding, float eps, float scale, Tensor(e!) out, "
+        "Tensor? plan=None) -> ()");
+    m.def(
+        "decode_plan(Tensor cached_lens, Tensor num_decoding, int batch, int num_q_heads, "
+        "int num_kv_heads) -> Tensor");
     m.def("decode_attention_workspace_size(int batch, int num_q_heads) -> int");
     m.def(
         "dequantize_kv_prefix(Tensor k_cache, Tensor v_cache, Tensor k_scale, Tensor v_scale, "
@@ -609,4 +673,5 @@ TORCH_LIBRARY_IMPL(ie, CUDA, m) {
     m.impl("dequantize_kv_prefix", &dequantize_kv_prefix);
     m.impl("prefill_attention", &prefill_attention);
     m.impl("prefill_plan", &prefill_plan);
+    m.impl("decode_plan", &decode_plan);
 }

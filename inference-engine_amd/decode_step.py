@@ -34,9 +34,10 @@ import torch.nn.functional as F
 from torch.cuda import nvtx
 
 from .attention_layer import attention, rope_inv_freq, rope_tables
-from .kernels import (LayerKVCache, add_rms_norm, decode_attention_rope, fold_rms_norm_weight,
-                      linear, linear_norm, linear_residual_, linear_silu_mul, make_layer_cache,
-                      sample, tune_linear, use_skinny, use_skinny_glu)
+from .kernels import (LayerKVCache, add_rms_norm, decode_attention_rope, decode_plan,
+                      fold_rms_norm_weight, linear, linear_norm, linear_residual_,
+                      linear_silu_mul, make_layer_cache, sample, tune_linear, use_skinny,
+                      use_skinny_glu)
 
 
 @dataclass(frozen=True)
@@ -153,7 +154,7 @@ class DecodeStep:
         with nvtx.range("o_proj"):
             return linear(out.view(B, -1), lw.o_proj)
 
-    def _attend(self, li, qkv, cos, sin):
+    def _attend(self, li, qkv, cos, sin, plan=None):
         s, lw, B = self.shape, self.layers[li], self.B
         q, k, v = qkv.split([s.num_q_heads * s.head_dim, s.num_kv_heads * s.head_dim,
                              s.num_kv_heads * s.head_dim], dim=-1)
@@ -162,7 +163,7 @@ class DecodeStep:
         v = v.view(B, s.num_kv_heads, s.head_dim)
         return attention(q, k, v, None, None, cos, sin, self.caches[li], self.cached_lens,
                          self.slot_ids, None, 0, None, self.num_decoding, lw.q_norm, lw.k_norm,
-                         s.eps)
+                         s.eps, decode_plan=plan)
 
     def forward(self) -> torch.Tensor:
         """One step: returns the greedy next token of every sequence, int64 [B, 1]."""
@@ -201,13 +202,16 @@ class DecodeStep:
     def _hidden_fused(self, x, cos, sin):
         """The layers in the fused form: h, the residual stream, is the embedding's output
         (a new tensor every step), updated in place by o_proj and down."""
-        eps, h = self.shape.eps, x
+        eps, h, s = self.shape.eps, x, self.shape
+        with nvtx.range("metadata"):  # the decode launch's work list, once for every layer
+            plan = decode_plan(self.cached_lens, self.num_decoding, self.B, s.num_q_heads,
+                               s.num_kv_heads)
         for li, lw in enumerate(self.layers):
             with nvtx.range("layer"):
                 with nvtx.range("attn"):
                     with nvtx.range("qkv_proj"):  # input_norm inside (folded into lw.qkv)
                         qkv = linear_norm(h, lw.qkv, eps)
-                    out = self._attend(li, qkv, cos, sin)
+                    out = self._attend(li, qkv, cos, sin, plan)
                     with nvtx.range("o_proj"):  # + the residual add of the post-norm
                         linear_residual_(out.view(self.B, -1), lw.o_proj, h)
                 with nvtx.range("mlp"):  # post_norm inside (folded into lw.gate_up)

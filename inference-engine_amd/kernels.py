@@ -56,9 +56,12 @@ def decode_attention(
     num_decoding: torch.Tensor,  # int32 [1], how many entries are decoding
     scale,
     out: torch.Tensor | None = None,  # [>= B, Hq, D]; decoding entry b's output goes to row b
+    plan: torch.Tensor | None = None,  # decode_plan of this step's metadata (optional)
 ):
     """qwen3-1.7b/kernels.py:272-361. One launch on the current stream: the split-K kernel, whose
-    last piece per sequence also does the reference's reduce (kernels.py:216-264)."""
+    last piece per sequence also does the reference's reduce (kernels.py:216-264). With `plan`
+    (decode_plan over the same cached_lens / num_decoding values, batch and heads), each
+    workgroup reads its work entry instead of deriving it: the same results."""
     k_cache, v_cache = kv_cache.k, kv_cache.v
     assert k_cache.stride() == v_cache.stride(), "kernel uses one set of strides for k and v"
     assert kv_cache.k_scale.stride() == kv_cache.v_scale.stride()
@@ -67,7 +70,7 @@ def decode_attention(
         out = torch.empty(B, Hq, D, device=q.device, dtype=q.dtype)
     assert out.shape[0] >= B and out.shape[1:] == (Hq, D) and out.stride(-1) == 1
     ops().decode_attention(q, *_cache_args(kv_cache), cached_lens, slot_ids, num_decoding,
-                           float(scale), out)
+                           float(scale), out, plan)
     return out
 
 
@@ -108,11 +111,13 @@ def decode_attention_rope(
     eps: float,
     scale,
     out: torch.Tensor | None = None,  # [>= B, Hq, D]
+    plan: torch.Tensor | None = None,  # decode_plan of this step's metadata (optional)
 ):
     """fused_rope_kv_decode (kernels.py:483-544) followed by decode_attention (kernels.py:272-361)
     in one launch: the same cache writes, bit for bit, and the attention of the q that
     fused_rope_kv_decode returns, which is not materialized. The decode branch of
-    architecture.py:113-122 without the launch between the two ops."""
+    architecture.py:113-122 without the launch between the two ops. `plan` as for
+    decode_attention."""
     assert kv_cache.k.stride() == kv_cache.v.stride(), "kernel uses one set of strides for both caches"
     assert kv_cache.k_scale.stride() == kv_cache.v_scale.stride()
     B, Hq, D = q.shape
@@ -121,7 +126,7 @@ def decode_attention_rope(
     assert out.shape[0] >= B and out.shape[1:] == (Hq, D) and out.stride(-1) == 1
     ops().decode_attention_rope(q, k, v, q_norm_weight, k_norm_weight, cos, sin,
                                 *_cache_args(kv_cache), cached_lens, slot_ids, num_decoding,
-                                float(eps), float(scale), out)
+                                float(eps), float(scale), out, plan)
     return out
 
 
@@ -205,6 +210,15 @@ def prefill_plan(seq_ids: torch.Tensor, cu_seqlens: torch.Tensor, tile_start: to
     return ops().prefill_plan(seq_ids, cu_seqlens, tile_start, slot_ids, cu_cached,
                               int(num_tokens), int(num_q_heads), int(num_kv_heads),
                               int(PREFILL_BLOCK_M))
+
+
+def decode_plan(cached_lens: torch.Tensor, num_decoding: torch.Tensor, batch: int,
+                num_q_heads: int, num_kv_heads: int) -> torch.Tensor:
+    """The work list of decode_attention / decode_attention_rope over one step's metadata
+    ([grid, 4] int32 on the device: see ie_decode_attention_plan), computed once per step and
+    passed as `plan` to every layer's decode launch (no counterpart in the reference)."""
+    return ops().decode_plan(cached_lens, num_decoding, int(batch), int(num_q_heads),
+                             int(num_kv_heads))
 
 
 def sample(logits: torch.Tensor, tau: float, seed: torch.Tensor) -> torch.Tensor:

@@ -24,7 +24,7 @@ def test_torch_ops_registered(ie):
                  "decode_attention", "decode_attention_rope", "dequantize_kv_prefix",
                  "prefill_attention", "decode_attention_workspace_size", "sample", "add_rms_norm",
                  "silu_mul", "skinny_matmul", "skinny_matmul_silu_mul", "skinny_matmul_norm",
-                 "skinny_matmul_residual_", "prefill_plan"]:
+                 "skinny_matmul_residual_", "prefill_plan", "decode_plan"]:
         assert hasattr(ops, name), name
 
 
@@ -56,8 +56,9 @@ def test_bad_geometry_rejected_on_host(native):
 
 def test_workspace_size_formula(native):
     """The arrival counts (one uint32 per sequence and query head, room for at least 1024
-    sequences, padded to 256 bytes), then one fp32 partial (128 outputs, m, l) per query head and
-    work entry; the work entries are the launch's grid: the target, or target + B above it."""
+    sequences of 128 heads, padded to 256 bytes), then one fp32 partial (128 outputs, m, l) per
+    query head and work entry; the work entries are the launch's grid: the target, or target + B
+    above it."""
     lib = native.cabi()
     t_max = lib.ie_decode_attention_max_splits(8)
     assert t_max >= 1
@@ -71,9 +72,10 @@ def test_workspace_size_formula(native):
         prev = target
         grid = lib.ie_decode_attention_grid(ctypes.c_int32(B), ctypes.c_int32(8))
         assert grid == (target if B <= target else target + B)
-        # counts: one per sequence and query head (the most any GQA ratio uses); partials: one
-        # per query head and work entry of the largest grid (cdiv(Hq, 2) units: GQA 2)
-        counts = -(-(max(B, 1024) * 16) * 4 // 256) * 256
+        # counts: one per sequence and query head (the most any GQA ratio uses), for at least
+        # 1024 sequences and 128 heads; partials: one per query head and work entry of the
+        # largest grid (cdiv(Hq, 2) units: GQA 2)
+        counts = -(-(max(B, 1024) * 128) * 4 // 256) * 256
         assert lib.ie_decode_attention_workspace_size(B, 16, 128) == counts + 16 * grid * 130 * 4
 
 
@@ -120,14 +122,15 @@ def test_quantize_too_many_tokens_rejected_on_host(native):
 
 def test_workspace_count_regions_and_prefill_grid(native):
     """The bytes a caller clears to reset a workspace: the decode arrival counts (max(B, 1024)
-    * Hkv uint32, padded to 256 bytes: the offset of the partials in the size formula above) and
+    * max(Hq, 128) uint32, padded to 256 bytes: the offset of the partials in the size formula
+    above, the same for every call of up to 1024 sequences and 128 heads) and
     the prefill arrival and finish words (two per resident workgroup, padded to 256 bytes, within
     the prefill workspace). The prefill launch's grid: one resident wave of workgroups or one
     workgroup per (128-row sub-block, KV head), whichever is more."""
     lib = native.cabi()
     for B in (1, 64, 1024, 1025, 3000):
-        for hq in (16, 32, 2):
-            want = -(-(max(B, 1024) * hq * 4) // 256) * 256
+        for hq in (16, 32, 2, 256):
+            want = -(-(max(B, 1024) * max(hq, 128) * 4) // 256) * 256
             assert lib.ie_decode_attention_workspace_counts_bytes(B, hq) == want
     lib.ie_prefill_attention_workspace_size.restype = ctypes.c_size_t
     ws = lib.ie_prefill_attention_workspace_size(ctypes.c_int32(8), ctypes.c_int32(128),
@@ -209,3 +212,42 @@ def test_skinny_gemm_fused_rejects_bad_flags_on_host(native):
         assert b"eps" in lib.ie_attn_last_error()
     assert call(2, n_tiles=4) == HIP_ERROR_INVALID_VALUE
     assert b"n_tiles" in lib.ie_attn_last_error()
+
+
+def test_decode_planned_rejects_bad_plans_on_host(native):
+    """ie_decode_attention_planned / ie_decode_attention_rope_planned: a null plan, fewer rows
+    than the launch's work entries, and a misaligned plan are refused before any launch (the
+    pointers here are never dereferenced)."""
+    lib = native.cabi()
+    lib.ie_decode_attention_workspace_size.restype = ctypes.c_size_t
+    i32, i64, f32 = ctypes.c_int32, ctypes.c_int64, ctypes.c_float
+    p = ctypes.c_void_p(1 << 20)
+    desc = native.KVCacheDesc(1 << 20, 1 << 20, 1 << 20, 1 << 20, 1 << 20, 4, 8, 1024, 128,
+                              8 * 1024 * 128, 1024 * 128, 128, 8 * 1024, 1024, 8 * 128, 128)
+    B, hq = 3, 16
+    ws = lib.ie_decode_attention_workspace_size(i32(B), i32(hq), i32(128))
+    grid = lib.ie_decode_attention_grid(i32(B), i32(8))
+    assert grid > 0
+    plain = lib.ie_decode_attention_planned
+    plain.restype = ctypes.c_int
+    rope = lib.ie_decode_attention_rope_planned
+    rope.restype = ctypes.c_int
+
+    def call_plain(plan, rows):
+        return plain(p, i64(2048), i64(128), i32(B), i32(hq), ctypes.byref(desc), p, p, p, plan,
+                     i64(rows), f32(0.1), p, i64(2048), i64(128), p, ctypes.c_size_t(ws),
+                     ctypes.c_void_p(0))
+
+    def call_rope(plan, rows):
+        return rope(p, i64(4096), i64(128), p, i64(4096), i64(128), p, i64(4096), i64(128), p,
+                    p, p, i64(64), p, i64(64), f32(1e-6), i32(B), i32(hq), ctypes.byref(desc),
+                    p, p, p, plan, i64(rows), f32(0.1), p, i64(2048), i64(128), p,
+                    ctypes.c_size_t(ws), ctypes.c_void_p(0))
+
+    for call in (call_plain, call_rope):
+        assert call(ctypes.c_void_p(0), grid) == HIP_ERROR_INVALID_VALUE
+        assert b"null plan" in lib.ie_attn_last_error()
+        assert call(p, grid - 1) == HIP_ERROR_INVALID_VALUE
+        assert b"plan must hold" in lib.ie_attn_last_error()
+        assert call(ctypes.c_void_p((1 << 20) + 4), grid) == HIP_ERROR_INVALID_VALUE
+        assert b"aligned" in lib.ie_attn_last_error()

@@ -151,3 +151,24 @@ def test_mixed_step_geometry(ie, workloads, dev, hq, hkv):
     assert_attn_close(o[:30], ref[:30], f"mixed {hq}/{hkv}: decode rows")
     assert_attn_close(o[rows], ref[rows], f"mixed {hq}/{hkv}: all rows")
     assert_cache_bitwise(g.cache, ref_cache, f"mixed {hq}/{hkv} cache")
+
+
+def test_workspace_shared_across_head_counts(ie, workloads, dev):
+    """Decode calls of different head counts on one stream share the op's kept workspace: a
+    2/1 call (two query heads: few count words, partials right after them) followed by a 16/8
+    call of 300 sequences, whose count words for sequences 256 and up lie where the 2/1 call's
+    partials would have been had the count region been sized by the call's own head count.
+    Every row of the second call against the oracle."""
+    small = workloads.decode_workload([3000, 700, 4096, 20], seed=26, hq=2, hkv=1).to(dev)
+    ie.decode_attention(small.q, small.cache, small.cached_lens, small.slot_ids,
+                        small.num_decoding, SCALE)
+    ctx = [int(x) for x in np.random.default_rng(27).integers(1, 601, 300)]
+    wl = workloads.decode_workload(ctx, seed=27, num_decoding=299)
+    ref = _decode_ref(wl)
+    g = wl.to(dev)
+    for rep in range(2):
+        out = ie.decode_attention(g.q, g.cache, g.cached_lens, g.slot_ids, g.num_decoding, SCALE)
+        torch.cuda.synchronize()
+        assert_attn_close(bf16_np(out)[:299], ref[:299], f"16/8 after 2/1, call {rep}")
+        ie.decode_attention(small.q, small.cache, small.cached_lens, small.slot_ids,
+                            small.num_decoding, SCALE)
