@@ -298,16 +298,19 @@ def bench_mixed_step(W, dev):
     w = torch.ones(2, 128, dtype=torch.bfloat16, device=dev)
     cos, sin = al.rope_tables(gi["positions"], al.rope_inv_freq(128, 1e6, dev))
     ps = al.PrefixScratch(None, None, gi["cu_cached"])
-    op = lambda plan=None: al.attention(q, k, v, gi["seq_ids"], gi["cu_seqlens"], cos, sin,
-                                        wl.cache, gi["cached_lens"], gi["slot_ids"],
-                                        gi["tile_start"], wl.block_m, ps, gi["num_decoding"],
-                                        w[0], w[1], 1e-6, plan)
+    op = lambda plan=None, dplan=None: al.attention(
+        q, k, v, gi["seq_ids"], gi["cu_seqlens"], cos, sin, wl.cache, gi["cached_lens"],
+        gi["slot_ids"], gi["tile_start"], wl.block_m, ps, gi["num_decoding"], w[0], w[1], 1e-6,
+        plan, dplan)
     ms = time_graph(op)
-    plan = importlib.import_module("inference-engine_amd.kernels").prefill_plan(
-        gi["seq_ids"], gi["cu_seqlens"], gi["tile_start"], gi["slot_ids"], gi["cu_cached"], N,
-        16, 8, wl.block_m)
-    ms_planned = time_graph(lambda: op(plan))
+    K = importlib.import_module("inference-engine_amd.kernels")
+    plan = K.prefill_plan(gi["seq_ids"], gi["cu_seqlens"], gi["tile_start"], gi["slot_ids"],
+                          gi["cu_cached"], N, 16, 8, wl.block_m)
+    dplan = K.decode_plan(gi["cached_lens"], gi["num_decoding"], gi["slot_ids"].shape[0], 16, 8)
+    ms_planned = time_graph(lambda: op(plan, dplan))
     return {"us_graph": round(ms * 1e3, 2), "us_graph_planned": round(ms_planned * 1e3, 2),
+            "planned": "the step's prefill and decode work lists computed once per step (not "
+                       "timed here: 28 layers share them) and read by the launches",
             "rows": N, "decoders": len(wl.decode_ctx),
             "prefill_tokens": sum(L for L, _ in wl.chunks),
             "kernels": "fused_norm_rope_prefill, quantize_kv_prefill, prefill_attention, "

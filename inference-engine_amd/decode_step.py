@@ -223,8 +223,9 @@ class DecodeStep:
 
     def attention_only(self) -> torch.Tensor:
         """The step's attention kernels alone (per layer: decode_attention_rope, i.e.
-        fused_rope_kv_decode and decode_attention in one launch, on fixed activations), for the
-        attention share of a step."""
+        fused_rope_kv_decode and decode_attention in one launch, on fixed activations; in the
+        fused form with the step's decode work list, as the step runs them), for the attention
+        share of a step."""
         s, B = self.shape, self.B
         cos, sin = self._rope()
         if not hasattr(self, "_qkv_fixed"):
@@ -237,10 +238,12 @@ class DecodeStep:
         k = k.view(B, s.num_kv_heads, s.head_dim)
         v = v.view(B, s.num_kv_heads, s.head_dim)
         out = None
+        plan = decode_plan(self.cached_lens, self.num_decoding, B, s.num_q_heads,
+                           s.num_kv_heads) if self.fused else None
         for li, lw in enumerate(self.layers):
             out = decode_attention_rope(q, k, v, lw.q_norm, lw.k_norm, cos, sin, self.slot_ids,
                                         self.caches[li], self.cached_lens, self.num_decoding,
-                                        s.eps, s.head_dim ** -0.5)
+                                        s.eps, s.head_dim ** -0.5, plan=plan)
         return out
 
     def capture(self, fn=None):

@@ -139,7 +139,8 @@ def test_planned_prefill_in_graph(ie, workloads, dev):
 
 
 def test_attention_layer_with_plan(ie, workloads, dev):
-    """The attention layer's step with prefill_plan: the same output and cache bits."""
+    """The attention layer's step with prefill_plan and decode_plan: the same output and cache
+    bits."""
     ms = importlib.import_module("test_mixed_step_gpu")
     K = ie.kernels
     wl = workloads.config4(seed=40)
@@ -152,7 +153,9 @@ def test_attention_layer_with_plan(ie, workloads, dev):
     out2 = al.attention(q, k, v, gi2["seq_ids"], gi2["cu_seqlens"], cos, sin, g2.cache,
                         gi2["cached_lens"], gi2["slot_ids"], gi2["tile_start"], g2.block_m,
                         al.PrefixScratch(None, None, gi2["cu_cached"]), gi2["num_decoding"], qw,
-                        kw, ms.EPS, prefill_plan=plan)
+                        kw, ms.EPS, prefill_plan=plan,
+                        decode_plan=K.decode_plan(gi2["cached_lens"], gi2["num_decoding"],
+                                                  gi2["slot_ids"].shape[0], 16, 8))
     torch.cuda.synchronize()
     assert torch.equal(out, out2)
     for a, b in zip((g.cache.k, g.cache.v, g.cache.k_scale, g.cache.v_scale,
