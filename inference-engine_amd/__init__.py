@@ -26,6 +26,7 @@ from .kernels import (  # noqa: F401
     silu_mul,
     skinny_matmul,
     skinny_matmul_silu_mul,
+    swizzle_weight,
     linear,
     linear_norm,
     linear_residual_,

@@ -46,13 +46,17 @@ constexpr int SG_MAX_TILES = 6;  // weight + x tiles, at most (LDS: 8 waves x 16
 // by rstd_m = 1 / sqrt(sum_k h[m,k]^2 / K + eps) before it is rounded, the norm's weight having
 // been folded into the weight's columns by the caller (y = rstd_m * sum_k h[m,k] (g_k W[n,k]) is
 // the GEMM of the normalized rows); RES, y holds the residual stream on entry and each output
-// becomes bf16(y + bf16(sum)), in place (add_rms_norm's new residual, kernels.py:1240-1242).
-enum : int { SG_PLAIN = 0, SG_HALF = 1, SG_GLU = 2, SG_NORM = 4, SG_RES = 8 };
+// becomes bf16(y + bf16(sum)), in place (add_rms_norm's new residual, kernels.py:1240-1242);
+// SWZ, the weight comes in the fragment order skinny_weight_swizzle_kernel writes: each
+// 16-row group's 32-column steps as 1 KB blocks, lane (r, g)'s 16 bytes at 16 (16 g + r), so a
+// wave reads a weight fragment as one contiguous 1 KB load, straight into its registers (no LDS
+// round trip for the weight; the same fragments, so the same sums, as the row-major form).
+enum : int { SG_PLAIN = 0, SG_HALF = 1, SG_GLU = 2, SG_NORM = 4, SG_RES = 8, SG_SWZ = 16 };
 
-template <int WT, int MT, int PT>
+template <int TT, int MT, int PT>
 struct SgLds {
     union {
-        uint8_t t[SG_WAVES][16 * (WT + MT) * SG_LROW];  // per-wave transpose regions
+        uint8_t t[SG_WAVES][16 * TT * SG_LROW];          // per-wave transpose regions
         sg_f32x4 acc[SG_WAVES][PT * MT][IE_WAVE];       // partial D tiles (after the loop)
     };
     float ss[SG_WAVES][16 * MT];  // NORM: each wave's sums of squares of x rows over its K slice
@@ -67,13 +71,15 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
     const uint16_t* __restrict__ x, int64_t xs, int M, const uint16_t* __restrict__ w, int64_t ws,
     int K, uint16_t* __restrict__ y, int64_t ys, int nh, float eps) {
     constexpr bool HALF = MODE & SG_HALF, GLU = MODE & SG_GLU, NORM = MODE & SG_NORM,
-                   RES = MODE & SG_RES;
+                   RES = MODE & SG_RES, SWZ = MODE & SG_SWZ;
     constexpr int WT = GLU ? 2 * NT : NT;  // weight tiles: NT (GLU: NT gate, then NT up tiles)
     static_assert(WT + MT <= SG_MAX_TILES, "LDS transpose region too large");
     static_assert(!HALF || NT == 1, "8-row n-tiles come one per workgroup");
     static_assert(!GLU || NT * MT <= SG_WAVES, "GLU: at most one output tile per wave");
+    static_assert(!(SWZ && HALF), "the fragment-ordered weight comes in 16-row groups");
     constexpr int WROWS = HALF ? 8 : 16 * NT;  // weight rows per workgroup (per half in GLU)
     constexpr int TILES = WT + MT;  // W tiles 0..WT-1, then x tiles
+    constexpr int T0 = SWZ ? WT : 0;  // the first tile that goes through LDS (its LDS row: 16 (i - T0))
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l16 = lane & 15, g = lane >> 4;
@@ -83,21 +89,29 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
     // parts of x at any moment instead of all hitting the same L2 lines
     const int kw = K / SG_WAVES, k_begin = (int)((wave + blockIdx.x) % SG_WAVES) * kw;
     // W rows [n0, n0 + WROWS) (GLU: and the up rows [nh + n0, +WROWS)) and x rows [0, M): the
-    // buffer ranges zero the rows of x past M
-    const rsrc_t rw = make_rsrc(w + (int64_t)n0 * ws, (uint32_t)(WROWS * ws * 2));
-    const rsrc_t ru = make_rsrc(w + ((int64_t)nh + n0) * ws, (uint32_t)(GLU ? WROWS * ws * 2 : 0));
+    // buffer ranges zero the rows of x past M. SWZ: the same rows' 1 KB blocks, 16-row group by
+    // group (K / 32 blocks each)
+    const int64_t wrow = SWZ ? (int64_t)(K / 32) * 512 / 16 : ws;  // elements per weight row
+    const rsrc_t rw = make_rsrc(w + (int64_t)n0 * wrow, (uint32_t)(WROWS * wrow * 2));
+    const rsrc_t ru =
+        make_rsrc(w + ((int64_t)nh + n0) * wrow, (uint32_t)(GLU ? WROWS * wrow * 2 : 0));
     const rsrc_t rx = make_rsrc(x, (uint32_t)(M * xs * 2));
-    // byte offsets of this lane's two 8-row halves of every tile at the slice start
+    // byte offsets of this lane's two 8-row halves of every tile at the slice start (SWZ weight
+    // tiles: of its two 32-column steps' blocks)
     int loff[TILES][2];
 #pragma unroll
     for (int i = 0; i < TILES; ++i)
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
+            if (SWZ && i < WT) {
+                loff[i][h] = ((i % NT) * (K / 32) + k_begin / 32 + h) * 1024 + 16 * lane;
+                continue;
+            }
             const int row = 16 * (i < WT ? i % NT : i - WT) + 8 * h + lr;
             loff[i][h] = (row * (int)(i < WT ? ws : xs) + k_begin + 8 * lc) * 2;
         }
 
-    __shared__ __attribute__((aligned(16))) SgLds<WT, MT, NT> lds;
+    __shared__ __attribute__((aligned(16))) SgLds<TILES - T0, MT, NT> lds;
     uint8_t* reg = lds.t[wave];
     uint8_t* wdst = reg + lr * SG_LROW + 16 * lc;          // + (16 i + 8 h) rows
     const uint8_t* rsrc = reg + l16 * SG_LROW + 16 * g;   // + 16 i rows + 64 t
@@ -123,25 +137,33 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 if (HALF && i < NT && h == 1) continue;
+                if (SWZ && i < WT) {  // 32-column step h of the batch: one 1 KB block
+                    r[i][h] = __builtin_amdgcn_raw_buffer_load_b128(
+                        i < NT ? rw : ru, SG_BK * b + 32 * h < kw ? loff[i][h] + 2048 * b : -1, 0,
+                        0);
+                    continue;
+                }
                 r[i][h] = __builtin_amdgcn_raw_buffer_load_b128(
                     i < NT ? rw : (i < WT ? ru : rx), in ? loff[i][h] + 128 * b : -1, 0, 0);
             }
     };
     auto compute = [&](const Batch& r) {
 #pragma unroll
-        for (int i = 0; i < TILES; ++i)
+        for (int i = T0; i < TILES; ++i)
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 if (HALF && i < NT && h == 1) continue;  // weight rows 8..15: not stored
-                *reinterpret_cast<sg_u32x4*>(wdst + (16 * i + 8 * h) * SG_LROW) = r[i][h];
+                *reinterpret_cast<sg_u32x4*>(wdst + (16 * (i - T0) + 8 * h) * SG_LROW) = r[i][h];
             }
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
             sg_bf16x8 f[TILES];
 #pragma unroll
             for (int i = 0; i < TILES; ++i)
-                f[i] = __builtin_bit_cast(
-                    sg_bf16x8, *reinterpret_cast<const sg_u32x4*>(rsrc + 16 * i * SG_LROW + 64 * t));
+                f[i] = i < T0 ? __builtin_bit_cast(sg_bf16x8, r[i][t])
+                              : __builtin_bit_cast(sg_bf16x8,
+                                                   *reinterpret_cast<const sg_u32x4*>(
+                                                       rsrc + 16 * (i - T0) * SG_LROW + 64 * t));
 #pragma unroll
             for (int nt = 0; nt < WT; ++nt)
 #pragma unroll
@@ -295,7 +317,9 @@ void sg_go(dim3 grid, hipStream_t s, const SgCall& c) {
 template <int MT, int EXTRA>
 void sg_rows(int n_tiles, dim3 grid, hipStream_t s, const SgCall& c) {
     switch (n_tiles) {
-        case 0: sg_go<MT, 1, SG_HALF | EXTRA>(grid, s, c); break;
+        case 0:
+            if constexpr (!(EXTRA & SG_SWZ)) sg_go<MT, 1, SG_HALF | EXTRA>(grid, s, c);
+            break;
         case 1: sg_go<MT, 1, EXTRA>(grid, s, c); break;
         case 2: sg_go<MT, 2, EXTRA>(grid, s, c); break;
         default:
@@ -331,6 +355,17 @@ void sg_glu_mt(int mt, int n_tiles, dim3 grid, hipStream_t s, const SgCall& c) {
     }
 }
 
+template <int EXTRA>
+void sg_dispatch(bool glu, int mt, int n_tiles, dim3 grid, hipStream_t s, const SgCall& c) {
+    if constexpr (!(EXTRA & SG_RES)) {  // the residual form has no gate/up variant
+        if (glu) {
+            sg_glu_mt<EXTRA>(mt, n_tiles, grid, s, c);
+            return;
+        }
+    }
+    sg_rows_mt<EXTRA>(mt, n_tiles, grid, s, c);
+}
+
 }  // namespace
 
 extern "C" hipError_t ie_skinny_gemm_fused(const ie_bf16* x, int64_t x_stride, int32_t m,
@@ -339,12 +374,15 @@ extern "C" hipError_t ie_skinny_gemm_fused(const ie_bf16* x, int64_t x_stride, i
                                            float eps, ie_bf16* y, int64_t y_stride,
                                            hipStream_t stream) {
     IE_REQUIRE(m >= 0 && n >= 0 && k >= 0, "negative sizes");
-    IE_REQUIRE(flags == 0 || flags == IE_SKINNY_NORM || flags == IE_SKINNY_SILU_MUL ||
-                   flags == (IE_SKINNY_NORM | IE_SKINNY_SILU_MUL) || flags == IE_SKINNY_RESIDUAL,
-               "flags: 0, NORM, SILU_MUL, NORM | SILU_MUL or RESIDUAL");
+    const int form = flags & ~IE_SKINNY_SWIZZLED;
+    IE_REQUIRE(form == 0 || form == IE_SKINNY_NORM || form == IE_SKINNY_SILU_MUL ||
+                   form == (IE_SKINNY_NORM | IE_SKINNY_SILU_MUL) || form == IE_SKINNY_RESIDUAL,
+               "flags: 0, NORM, SILU_MUL, NORM | SILU_MUL or RESIDUAL, each optionally | SWIZZLED");
     const bool norm = flags & IE_SKINNY_NORM, glu = flags & IE_SKINNY_SILU_MUL,
-               res = flags & IE_SKINNY_RESIDUAL;
+               res = flags & IE_SKINNY_RESIDUAL, swz = flags & IE_SKINNY_SWIZZLED;
     IE_REQUIRE(!norm || (eps >= 0.f && eps < 1e30f), "eps must be finite and >= 0");
+    IE_REQUIRE(!swz || (n_tiles >= 1 && weight_stride == k),
+               "a swizzled weight takes n_tiles 1, 2 or 4 and weight_stride k");
     if (m == 0 || n == 0) return hipSuccess;
     if (glu) {
         IE_REQUIRE(n_tiles == 1 || n_tiles == 2, "n_tiles must be 1 or 2");
@@ -356,20 +394,63 @@ extern "C" hipError_t ie_skinny_gemm_fused(const ie_bf16* x, int64_t x_stride, i
     const int mt = (m + 15) / 16;
     SgCall c{(const uint16_t*)x, x_stride, m, (const uint16_t*)weight, weight_stride, k,
              (uint16_t*)y, y_stride, glu ? n / 2 : 0, eps};
+    dim3 grid;
     if (glu) {
         // gate and up tiles: lowered to one n-tile where m leaves too little LDS for two
         if (2 * n_tiles + mt > SG_MAX_TILES) n_tiles = 1;
-        const dim3 grid((unsigned)(n / 2 / (16 * n_tiles)));
-        if (norm) sg_glu_mt<SG_NORM>(mt, n_tiles, grid, stream, c);
-        else sg_glu_mt<SG_PLAIN>(mt, n_tiles, grid, stream, c);
-        return hipGetLastError();
+        grid = dim3((unsigned)(n / 2 / (16 * n_tiles)));
+    } else {
+        // n_tiles is a performance choice: it is lowered until the LDS transpose region fits
+        while (n_tiles > 1 && n_tiles + mt > SG_MAX_TILES) n_tiles >>= 1;
+        grid = dim3((unsigned)(n_tiles == 0 ? n / 8 : n / (16 * n_tiles)));
     }
-    // n_tiles is a performance choice: it is lowered until the LDS transpose region fits
-    while (n_tiles > 1 && n_tiles + mt > SG_MAX_TILES) n_tiles >>= 1;
-    const dim3 grid((unsigned)(n_tiles == 0 ? n / 8 : n / (16 * n_tiles)));
-    if (norm) sg_rows_mt<SG_NORM>(mt, n_tiles, grid, stream, c);
-    else if (res) sg_rows_mt<SG_RES>(mt, n_tiles, grid, stream, c);
-    else sg_rows_mt<SG_PLAIN>(mt, n_tiles, grid, stream, c);
+    const int mode = (norm ? SG_NORM : 0) | (res ? SG_RES : 0);
+#define IE_SG_DISPATCH(SW)                                                                 \
+    switch (mode) {                                                                        \
+        case SG_NORM: sg_dispatch<SG_NORM | SW>(glu, mt, n_tiles, grid, stream, c); break; \
+        case SG_RES: sg_dispatch<SG_RES | SW>(false, mt, n_tiles, grid, stream, c); break; \
+        default: sg_dispatch<SG_PLAIN | SW>(glu, mt, n_tiles, grid, stream, c); break;     \
+    }
+    if (swz) {
+        IE_SG_DISPATCH(SG_SWZ)
+    } else {
+        IE_SG_DISPATCH(0)
+    }
+#undef IE_SG_DISPATCH
+    return hipGetLastError();
+}
+
+// The fragment order of the SWZ form: output 1 KB block (R, S) (16-row group R, 32-column step
+// S, at block index R * k / 32 + S) holds, at 16 bytes per lane L = 16 g + r, weight row
+// 16 R + r, columns 32 S + 8 g .. + 8. One wave per block.
+__global__ __launch_bounds__(256) void skinny_weight_swizzle_kernel(const uint16_t* __restrict__ w,
+                                                                    int64_t ws, int n, int k,
+                                                                    uint16_t* __restrict__ out) {
+    const int lane = threadIdx.x & 63;
+    const int64_t blk = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int64_t steps = k / 32;
+    if (blk >= (int64_t)(n / 16) * steps) return;
+    const int64_t R = blk / steps, S = blk % steps;
+    const int r = lane & 15, g = lane >> 4;
+    const uint4 v = *reinterpret_cast<const uint4*>(w + (16 * R + r) * ws + 32 * S + 8 * g);
+    *reinterpret_cast<uint4*>(out + blk * 512 + 8 * lane) = v;
+}
+
+extern "C" hipError_t ie_skinny_weight_swizzle(const ie_bf16* weight, int64_t weight_stride,
+                                               int32_t n, int32_t k, ie_bf16* out,
+                                               hipStream_t stream) {
+    IE_REQUIRE(n >= 0 && k >= 0, "negative sizes");
+    if (n == 0 || k == 0) return hipSuccess;
+    IE_REQUIRE(weight && out, "null pointer");
+    IE_REQUIRE(n % 16 == 0 && k % 32 == 0, "n must be a multiple of 16 and k of 32");
+    IE_REQUIRE(weight_stride >= k && weight_stride % 8 == 0 &&
+                   (reinterpret_cast<uintptr_t>(weight) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(out) & 15) == 0,
+               "rows must be 16-byte aligned");
+    const int64_t blocks = (int64_t)(n / 16) * (k / 32);
+    hipLaunchKernelGGL(skinny_weight_swizzle_kernel, dim3((unsigned)((blocks + 3) / 4)),
+                       dim3(256), 0, stream, (const uint16_t*)weight, weight_stride, n, k,
+                       (uint16_t*)out);
     return hipGetLastError();
 }
 

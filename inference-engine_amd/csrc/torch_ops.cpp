@@ -233,40 +233,65 @@ at::Tensor silu_mul(const at::Tensor& gate_up) {
     return out;
 }
 
-at::Tensor skinny_matmul(const at::Tensor& x, const at::Tensor& weight, int64_t n_tiles) {
+// A weight from skinny_weight_swizzle: a contiguous [N, K] bf16 tensor in fragment order.
+void check_swizzled(const at::Tensor& weight, bool swizzled) {
+    TORCH_CHECK(!swizzled || weight.is_contiguous(),
+                "ie: a swizzled weight is the contiguous output of skinny_weight_swizzle");
+}
+
+at::Tensor skinny_matmul(const at::Tensor& x, const at::Tensor& weight, int64_t n_tiles,
+                         bool swizzled) {
     check_bf16_rows(x, "x", 2);
     check_bf16_rows(weight, "weight", 2);
+    check_swizzled(weight, swizzled);
     const c10::DeviceGuard guard(x.device());
     const int64_t M = x.size(0), K = x.size(1), N = weight.size(0);
     TORCH_CHECK(weight.size(1) == K, "ie: weight must be [N, K]");
     at::Tensor y = at::empty({M, N}, x.options());
-    ok(ie_skinny_gemm(bf(x), x.stride(0), (int32_t)M, bf(weight), weight.stride(0), (int32_t)N,
-                      (int32_t)K, (int32_t)n_tiles, bfm(y), y.stride(0), stream_of(x)),
+    ok(ie_skinny_gemm_fused(bf(x), x.stride(0), (int32_t)M, bf(weight), weight.stride(0),
+                            (int32_t)N, (int32_t)K, (int32_t)n_tiles,
+                            swizzled ? IE_SKINNY_SWIZZLED : 0, 0.f, bfm(y), y.stride(0),
+                            stream_of(x)),
        "skinny_matmul");
     return y;
 }
 
-at::Tensor skinny_matmul_silu_mul(const at::Tensor& x, const at::Tensor& weight, int64_t n_tiles) {
+at::Tensor skinny_matmul_silu_mul(const at::Tensor& x, const at::Tensor& weight, int64_t n_tiles,
+                                  bool swizzled) {
     check_bf16_rows(x, "x", 2);
     check_bf16_rows(weight, "weight", 2);
+    check_swizzled(weight, swizzled);
     const c10::DeviceGuard guard(x.device());
     const int64_t M = x.size(0), K = x.size(1), N = weight.size(0);
     TORCH_CHECK(weight.size(1) == K, "ie: weight must be [N, K]");
     TORCH_CHECK(N % 2 == 0, "ie: weight must hold the gate rows then the up rows");
     at::Tensor y = at::empty({M, N / 2}, x.options());
-    ok(ie_skinny_gemm_silu_mul(bf(x), x.stride(0), (int32_t)M, bf(weight), weight.stride(0),
-                               (int32_t)N, (int32_t)K, (int32_t)n_tiles, bfm(y), y.stride(0),
-                               stream_of(x)),
+    ok(ie_skinny_gemm_fused(bf(x), x.stride(0), (int32_t)M, bf(weight), weight.stride(0),
+                            (int32_t)N, (int32_t)K, (int32_t)n_tiles,
+                            IE_SKINNY_SILU_MUL | (swizzled ? IE_SKINNY_SWIZZLED : 0), 0.f,
+                            bfm(y), y.stride(0), stream_of(x)),
        "skinny_matmul_silu_mul");
     return y;
+}
+
+// The weight in the skinny GEMM's fragment order (ie_skinny_weight_swizzle), for swizzled=True.
+at::Tensor skinny_weight_swizzle(const at::Tensor& weight) {
+    check_bf16_rows(weight, "weight", 2);
+    const c10::DeviceGuard guard(weight.device());
+    at::Tensor out = at::empty(weight.sizes(), weight.options());
+    ok(ie_skinny_weight_swizzle(bf(weight), weight.stride(0), (int32_t)weight.size(0),
+                                (int32_t)weight.size(1), bfm(out), stream_of(weight)),
+       "skinny_weight_swizzle");
+    return out;
 }
 
 // The GEMM of RMSNorm(h) with the norm weight folded into `weight` (ie_skinny_gemm_fused with
 // IE_SKINNY_NORM, and IE_SKINNY_SILU_MUL for the gate/up form).
 at::Tensor skinny_matmul_norm(const at::Tensor& h, const at::Tensor& weight, int64_t n_tiles,
-                              bool silu_mul, double eps) {
+                              bool silu_mul, double eps, bool swizzled) {
     check_bf16_rows(h, "h", 2);
     check_bf16_rows(weight, "weight", 2);
+    check_swizzled(weight, swizzled);
     const c10::DeviceGuard guard(h.device());
     const int64_t M = h.size(0), K = h.size(1), N = weight.size(0);
     TORCH_CHECK(weight.size(1) == K, "ie: weight must be [N, K]");
@@ -274,7 +299,9 @@ at::Tensor skinny_matmul_norm(const at::Tensor& h, const at::Tensor& weight, int
     at::Tensor y = at::empty({M, silu_mul ? N / 2 : N}, h.options());
     ok(ie_skinny_gemm_fused(bf(h), h.stride(0), (int32_t)M, bf(weight), weight.stride(0),
                             (int32_t)N, (int32_t)K, (int32_t)n_tiles,
-                            IE_SKINNY_NORM | (silu_mul ? IE_SKINNY_SILU_MUL : 0), (float)eps,
+                            IE_SKINNY_NORM | (silu_mul ? IE_SKINNY_SILU_MUL : 0) |
+                                (swizzled ? IE_SKINNY_SWIZZLED : 0),
+                            (float)eps,
                             bfm(y), y.stride(0), stream_of(h)),
        "skinny_matmul_norm");
     return y;
@@ -282,9 +309,10 @@ at::Tensor skinny_matmul_norm(const at::Tensor& h, const at::Tensor& weight, int
 
 // residual <- bf16(residual + bf16(x . weight^T)) in place (IE_SKINNY_RESIDUAL).
 at::Tensor skinny_matmul_residual_(const at::Tensor& x, const at::Tensor& weight, int64_t n_tiles,
-                                   at::Tensor residual) {
+                                   at::Tensor residual, bool swizzled) {
     check_bf16_rows(x, "x", 2);
     check_bf16_rows(weight, "weight", 2);
+    check_swizzled(weight, swizzled);
     check_bf16_rows(residual, "residual", 2);
     const c10::DeviceGuard guard(x.device());
     const int64_t M = x.size(0), K = x.size(1), N = weight.size(0);
@@ -293,7 +321,8 @@ at::Tensor skinny_matmul_residual_(const at::Tensor& x, const at::Tensor& weight
     TORCH_CHECK(residual.device() == x.device() && weight.device() == x.device(),
                 "ie: x, weight and residual must be on one device");
     ok(ie_skinny_gemm_fused(bf(x), x.stride(0), (int32_t)M, bf(weight), weight.stride(0),
-                            (int32_t)N, (int32_t)K, (int32_t)n_tiles, IE_SKINNY_RESIDUAL, 0.f,
+                            (int32_t)N, (int32_t)K, (int32_t)n_tiles,
+                            IE_SKINNY_RESIDUAL | (swizzled ? IE_SKINNY_SWIZZLED : 0), 0.f,
                             bfm(residual), residual.stride(0), stream_of(x)),
        "skinny_matmul_residual_");
     return residual;
@@ -619,14 +648,17 @@ TORCH_LIBRARY(ie, m) {
     m.def("sample(Tensor logits, float tau, Tensor(a!) seed) -> Tensor");
     m.def("add_rms_norm(Tensor residual, Tensor delta, Tensor weight, float eps) -> (Tensor, Tensor)");
     m.def("silu_mul(Tensor gate_up) -> Tensor");
-    m.def("skinny_matmul(Tensor x, Tensor weight, int n_tiles=1) -> Tensor");
-    m.def("skinny_matmul_silu_mul(Tensor x, Tensor weight, int n_tiles=1) -> Tensor");
+    m.def("skinny_matmul(Tensor x, Tensor weight, int n_tiles=1, bool swizzled=False) -> Tensor");
     m.def(
-        "skinny_matmul_norm(Tensor h, Tensor weight, int n_tiles, bool silu_mul, float eps) "
+        "skinny_matmul_silu_mul(Tensor x, Tensor weight, int n_tiles=1, bool swizzled=False) "
         "-> Tensor");
     m.def(
-        "skinny_matmul_residual_(Tensor x, Tensor weight, int n_tiles, Tensor(a!) residual) "
-        "-> Tensor(a!)");
+        "skinny_matmul_norm(Tensor h, Tensor weight, int n_tiles, bool silu_mul, float eps, "
+        "bool swizzled=False) -> Tensor");
+    m.def(
+        "skinny_matmul_residual_(Tensor x, Tensor weight, int n_tiles, Tensor(a!) residual, "
+        "bool swizzled=False) -> Tensor(a!)");
+    m.def("skinny_weight_swizzle(Tensor weight) -> Tensor");
     m.def(
         "decode_attention(Tensor q, Tensor k_cache, Tensor v_cache, Tensor k_scale, "
         "Tensor v_scale, Tensor k_calibration, Tensor cached_lens, Tensor slot_ids, "
@@ -668,6 +700,7 @@ TORCH_LIBRARY_IMPL(ie, CUDA, m) {
     m.impl("skinny_matmul_silu_mul", &skinny_matmul_silu_mul);
     m.impl("skinny_matmul_norm", &skinny_matmul_norm);
     m.impl("skinny_matmul_residual_", &skinny_matmul_residual_);
+    m.impl("skinny_weight_swizzle", &skinny_weight_swizzle);
     m.impl("decode_attention", &decode_attention);
     m.impl("decode_attention_rope", &decode_attention_rope);
     m.impl("dequantize_kv_prefix", &dequantize_kv_prefix);

@@ -36,8 +36,8 @@ from torch.cuda import nvtx
 from .attention_layer import attention, rope_inv_freq, rope_tables
 from .kernels import (LayerKVCache, add_rms_norm, decode_attention_rope, decode_plan,
                       fold_rms_norm_weight, linear, linear_norm, linear_residual_,
-                      linear_silu_mul, make_layer_cache, sample, tune_linear, use_skinny,
-                      use_skinny_glu)
+                      linear_silu_mul, make_layer_cache, sample, skinny_matmul, swizzle_weight,
+                      tune_linear, use_skinny, use_skinny_glu)
 
 
 @dataclass(frozen=True)
@@ -113,16 +113,35 @@ class DecodeStep:
     cached_lens and slot_ids from fixed tensors, which the caller rewrites between replays."""
 
     def __init__(self, shape: Qwen3Shape, layers, embed, final_norm, caches: list[LayerKVCache],
-                 batch: int, device, fused: bool = False):
+                 batch: int, device, fused: bool = False, swizzle: bool | None = None):
         """fused: fold every layer's input_norm into its qkv weight and post_norm into its
-        gate_up weight, in place (the layers then serve only the fused form)."""
+        gate_up weight, in place (the layers then serve only the fused form). swizzle (default:
+        with fused): every projection weight whose tuned skinny GEMM tile width is at least one
+        16-row tile is reordered in place into the GEMM's fragment order (swizzle_weight; the
+        same result bits); the LM head gets a reordered copy of the embedding."""
         self.shape, self.layers, self.embed, self.final_norm = shape, layers, embed, final_norm
         self.fused = fused
+        self.swz = dict.fromkeys(("qkv", "o_proj", "gate_up", "down", "lm_head"), False)
+        self.lm_head_w = embed
         if fused:
             for lw in layers:
                 lw.qkv = fold_rms_norm_weight(lw.qkv, lw.input_norm)
                 lw.gate_up = fold_rms_norm_weight(lw.gate_up, lw.post_norm)
             self._zero = torch.zeros(batch, shape.model_dim, device=device, dtype=torch.bfloat16)
+            if swizzle is None or swizzle:
+                lw = layers[0]
+                tiles = lambda w: use_skinny.get((w.shape[0], w.shape[1], batch))
+                for name in ("qkv", "o_proj", "down"):
+                    self.swz[name] = tiles(getattr(lw, name)) not in (None, 0)
+                self.swz["gate_up"] = (lw.gate_up.shape[0], lw.gate_up.shape[1],
+                                       batch) in use_skinny_glu
+                self.swz["lm_head"] = tiles(embed) not in (None, 0)
+                for lw in layers:
+                    for name in ("qkv", "o_proj", "gate_up", "down"):
+                        if self.swz[name]:
+                            setattr(lw, name, swizzle_weight(getattr(lw, name)))
+                if self.swz["lm_head"]:
+                    self.lm_head_w = swizzle_weight(embed)
         self.caches = caches
         self.B = batch
         pool = caches[0].k.shape[0]
@@ -169,7 +188,12 @@ class DecodeStep:
         """One step: returns the greedy next token of every sequence, int64 [B, 1]."""
         h = self.hidden()
         with nvtx.range("lm_head"):
-            logits = linear(h, self.embed)
+            if self.swz["lm_head"]:
+                V, H = self.embed.shape
+                logits = skinny_matmul(h, self.lm_head_w, use_skinny[(V, H, self.B)],
+                                       swizzled=True)
+            else:
+                logits = linear(h, self.embed)
         with nvtx.range("sample"):
             return sample(logits, 0.0, self.seed)
 
@@ -202,7 +226,7 @@ class DecodeStep:
     def _hidden_fused(self, x, cos, sin):
         """The layers in the fused form: h, the residual stream, is the embedding's output
         (a new tensor every step), updated in place by o_proj and down."""
-        eps, h, s = self.shape.eps, x, self.shape
+        eps, h, s, sw = self.shape.eps, x, self.shape, self.swz
         with nvtx.range("metadata"):  # the decode launch's work list, once for every layer
             plan = decode_plan(self.cached_lens, self.num_decoding, self.B, s.num_q_heads,
                                s.num_kv_heads)
@@ -210,13 +234,14 @@ class DecodeStep:
             with nvtx.range("layer"):
                 with nvtx.range("attn"):
                     with nvtx.range("qkv_proj"):  # input_norm inside (folded into lw.qkv)
-                        qkv = linear_norm(h, lw.qkv, eps)
+                        qkv = linear_norm(h, lw.qkv, eps, swizzled=sw["qkv"])
                     out = self._attend(li, qkv, cos, sin, plan)
                     with nvtx.range("o_proj"):  # + the residual add of the post-norm
-                        linear_residual_(out.view(self.B, -1), lw.o_proj, h)
+                        linear_residual_(out.view(self.B, -1), lw.o_proj, h,
+                                         swizzled=sw["o_proj"])
                 with nvtx.range("mlp"):  # post_norm inside (folded into lw.gate_up)
-                    act = linear_norm(h, lw.gate_up, eps, silu_mul=True)
-                    linear_residual_(act, lw.down, h)
+                    act = linear_norm(h, lw.gate_up, eps, silu_mul=True, swizzled=sw["gate_up"])
+                    linear_residual_(act, lw.down, h, swizzled=sw["down"])
         with nvtx.range("final_norm"):  # h already holds the last down projection's sum
             _, hn = add_rms_norm(h, self._zero, self.final_norm, eps)
         return hn
@@ -263,7 +288,7 @@ class DecodeStep:
 
 
 def make_decode_step(batch=32, ctx_lo=128, ctx_hi=4096, shape=Qwen3Shape(), device="cuda",
-                     seed=0, tune=True, fused=None, norm_std=0.0):
+                     seed=0, tune=True, fused=None, norm_std=0.0, swizzle=None):
     """Config-5 step: B sequences with cached lengths ~ U[ctx_lo, ctx_hi) - 1 (the new token is
     the ctx-th), slots 0..B-1 of a pool of B + 1 (the last row is the engine's scratch slot).
     fused=None: the fused form wherever tune_linear chose the skinny GEMM for all four layer
@@ -283,7 +308,8 @@ def make_decode_step(batch=32, ctx_lo=128, ctx_hi=4096, shape=Qwen3Shape(), devi
         fused = all(use_skinny.get((w.shape[0], w.shape[1], batch)) is not None
                     for w in (lw.qkv, lw.o_proj, lw.gate_up, lw.down)) and \
             (lw.gate_up.shape[0], lw.gate_up.shape[1], batch) in use_skinny_glu
-    step = DecodeStep(shape, layers, embed, final_norm, caches, batch, device, fused=fused)
+    step = DecodeStep(shape, layers, embed, final_norm, caches, batch, device, fused=fused,
+                      swizzle=swizzle)
     g = torch.Generator().manual_seed(seed)
     ctx = torch.randint(ctx_lo, ctx_hi, (batch,), generator=g)
     step.cached_lens.copy_((ctx - 1).to(torch.int32))

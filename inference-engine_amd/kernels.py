@@ -241,16 +241,26 @@ def silu_mul(gate_up: torch.Tensor) -> torch.Tensor:
     return ops().silu_mul(gate_up)
 
 
-def skinny_matmul(x: torch.Tensor, weight: torch.Tensor, n_tiles: int = 1) -> torch.Tensor:
+def skinny_matmul(x: torch.Tensor, weight: torch.Tensor, n_tiles: int = 1,
+                  swizzled: bool = False) -> torch.Tensor:
     """qwen3-1.7b/kernels.py:1406-1443: [M, K] bf16 @ [N, K].T bf16 -> [M, N] bf16 for M <= 64.
     `n_tiles` (1, 2, 4; 0 = 8 rows): weight rows per workgroup / 16, the launch shape tune_linear
-    picks."""
+    picks. swizzled: weight is swizzle_weight(W) (n_tiles 1, 2 or 4), the same result bits."""
     M, K = x.shape
     N = weight.shape[0]
     assert x.stride(-1) == 1 and weight.stride(-1) == 1
     assert M <= 64, "big M is compute bound, the library GEMM is faster there"
     assert n_tiles in (0, 1, 2, 4) and N % (16 * max(1, n_tiles)) == 0 and K % 256 == 0
-    return ops().skinny_matmul(x, weight, int(n_tiles))
+    assert not swizzled or n_tiles >= 1
+    return ops().skinny_matmul(x, weight, int(n_tiles), bool(swizzled))
+
+
+def swizzle_weight(weight: torch.Tensor) -> torch.Tensor:
+    """The weight in the skinny GEMM's fragment order (ie_skinny_weight_swizzle: each 16-row
+    group's 32-column steps as 1 KB blocks that a wave loads whole, straight into MFMA operand
+    registers). Reordered once at load; the GEMMs then take it with swizzled=True. [N, K] like
+    the weight (N a multiple of 16, K of 32), only for the skinny GEMM."""
+    return ops().skinny_weight_swizzle(weight)
 
 
 # (N, K, M) -> the n_tiles of skinny_matmul when it beat the library GEMM for that weight shape
@@ -262,7 +272,8 @@ use_skinny: dict = {}
 use_skinny_glu: dict = {}
 
 
-def skinny_matmul_silu_mul(x: torch.Tensor, weight: torch.Tensor, n_tiles: int = 1) -> torch.Tensor:
+def skinny_matmul_silu_mul(x: torch.Tensor, weight: torch.Tensor, n_tiles: int = 1,
+                           swizzled: bool = False) -> torch.Tensor:
     """silu_mul(skinny_matmul(x, weight)) in one launch (qwen3-1.7b/kernels.py:1451-1458 then
     :1178-1213): weight [2D, K] holds the gate rows then the up rows, result [M, D]."""
     M, K = x.shape
@@ -270,7 +281,7 @@ def skinny_matmul_silu_mul(x: torch.Tensor, weight: torch.Tensor, n_tiles: int =
     assert x.stride(-1) == 1 and weight.stride(-1) == 1
     assert M <= 64 and N % 2 == 0 and n_tiles in (1, 2)
     assert (N // 2) % (16 * n_tiles) == 0 and K % 256 == 0
-    return ops().skinny_matmul_silu_mul(x, weight, int(n_tiles))
+    return ops().skinny_matmul_silu_mul(x, weight, int(n_tiles), bool(swizzled))
 
 
 def linear_silu_mul(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
@@ -298,13 +309,14 @@ def _skinny_tiles(table: dict, key: tuple, default: int) -> int:
 
 
 def linear_norm(h: torch.Tensor, weight_folded: torch.Tensor, eps: float,
-                silu_mul: bool = False) -> torch.Tensor:
+                silu_mul: bool = False, swizzled: bool = False) -> torch.Tensor:
     """linear(add_rms_norm's normed output, W) (silu_mul: then silu_mul, the gate/up form) from
     the residual stream h itself, in one skinny-GEMM launch (ie_skinny_gemm_fused with
     IE_SKINNY_NORM): weight_folded = fold_rms_norm_weight(W, g). The rows' sums of squares come
     from the GEMM's own reads of h, so the RMSNorm costs no launch (the reference runs
     add_rms_norm, kernels.py:1260-1283, before each such projection, architecture.py:280-300).
-    M <= 64 rows; the tile width is the one tune_linear chose for the weight's shape."""
+    M <= 64 rows; the tile width is the one tune_linear chose for the weight's shape (at least
+    one 16-row tile for a swizzled weight, swizzle_weight of the folded weight)."""
     M, K = h.shape
     N = weight_folded.shape[0]
     assert h.stride(-1) == 1 and weight_folded.stride(-1) == 1 and M <= 64
@@ -314,11 +326,15 @@ def linear_norm(h: torch.Tensor, weight_folded: torch.Tensor, eps: float,
         assert (N // 2) % (16 * nt) == 0 and K % 256 == 0
     else:
         nt = _skinny_tiles(use_skinny, key, 1)
+        if swizzled:
+            nt = max(nt, 1)
         assert N % (16 * max(1, nt)) == 0 and K % 256 == 0
-    return ops().skinny_matmul_norm(h, weight_folded, int(nt), bool(silu_mul), float(eps))
+    return ops().skinny_matmul_norm(h, weight_folded, int(nt), bool(silu_mul), float(eps),
+                                    bool(swizzled))
 
 
-def linear_residual_(x: torch.Tensor, weight: torch.Tensor, residual: torch.Tensor) -> torch.Tensor:
+def linear_residual_(x: torch.Tensor, weight: torch.Tensor, residual: torch.Tensor,
+                     swizzled: bool = False) -> torch.Tensor:
     """residual <- bf16(residual + linear(x, weight)) in place and returned: add_rms_norm's
     new residual for a projection's output (kernels.py:1240-1242), bit for bit, in the
     projection's own launch (ie_skinny_gemm_fused with IE_SKINNY_RESIDUAL). M <= 64 rows."""
@@ -327,8 +343,10 @@ def linear_residual_(x: torch.Tensor, weight: torch.Tensor, residual: torch.Tens
     assert x.stride(-1) == 1 and weight.stride(-1) == 1 and M <= 64
     assert residual.shape == (M, N) and residual.stride(-1) == 1
     nt = _skinny_tiles(use_skinny, (N, K, M), 1)
+    if swizzled:
+        nt = max(nt, 1)
     assert N % (16 * max(1, nt)) == 0 and K % 256 == 0
-    return ops().skinny_matmul_residual_(x, weight, int(nt), residual)
+    return ops().skinny_matmul_residual_(x, weight, int(nt), residual, bool(swizzled))
 
 
 def linear(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:

@@ -192,8 +192,8 @@ def test_prefill_planned_rejects_bad_plans_on_host(native):
 
 def test_skinny_gemm_fused_rejects_bad_flags_on_host(native):
     """ie_skinny_gemm_fused: an undefined flag combination, a negative or infinite eps with
-    IE_SKINNY_NORM, and the gate/up form with n_tiles 4 are refused before any launch (the
-    pointers here are never dereferenced)."""
+    IE_SKINNY_NORM, the gate/up form with n_tiles 4, and a swizzled weight with 8-row tiles are
+    refused before any launch (the pointers here are never dereferenced)."""
     lib = native.cabi()
     fn = lib.ie_skinny_gemm_fused
     fn.restype = ctypes.c_int
@@ -204,9 +204,12 @@ def test_skinny_gemm_fused_rejects_bad_flags_on_host(native):
         return fn(p, i64(2048), i32(32), p, i64(2048), i32(4096), i32(2048), i32(n_tiles),
                   i32(flags), f32(eps), p, i64(4096), ctypes.c_void_p(0))
 
-    for flags in (8, 1 | 4, 2 | 4, 7, -1):
+    for flags in (16, 1 | 4, 2 | 4, 7, 8 | 1 | 4, -1):
         assert call(flags) == HIP_ERROR_INVALID_VALUE, flags
         assert b"flags" in lib.ie_attn_last_error()
+    for flags in (8, 8 | 1, 8 | 4):  # a swizzled weight: no 8-row tiles
+        assert call(flags, n_tiles=0) == HIP_ERROR_INVALID_VALUE, flags
+        assert b"swizzled" in lib.ie_attn_last_error()
     for eps in (-1.0, float("inf"), float("nan")):
         assert call(1, eps) == HIP_ERROR_INVALID_VALUE, eps
         assert b"eps" in lib.ie_attn_last_error()

@@ -136,8 +136,10 @@ def test_config5_full_size(ie, dev):
     s, lw, B = step.shape, step.layers[0], step.B
     cos, sin = step._rope()
     x = torch.nn.functional.embedding(step.ids, step.embed)
-    normed = step._rms(x, lw.input_norm)
-    qkv = ie.kernels.linear(normed, lw.qkv)
+    if step.fused:  # the step's own projection: RMSNorm inside, the weight folded (swizzled)
+        qkv = ie.kernels.linear_norm(x, lw.qkv, s.eps, swizzled=step.swz["qkv"])
+    else:
+        qkv = ie.kernels.linear(step._rms(x, lw.input_norm), lw.qkv)
     q = qkv[:, :2048].view(B, 16, 128)
     k = qkv[:, 2048:3072].view(B, 8, 128)
     v = qkv[:, 3072:].view(B, 8, 128)

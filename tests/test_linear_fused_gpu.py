@@ -150,3 +150,46 @@ def test_linear_wrappers_follow_tuning_table(ie, dev):
         assert torch.equal(res, want.bfloat16()), f"linear_residual_ table={choice}"
     K_.use_skinny.pop((1024, 512, 8))
 
+
+
+def test_swizzle_layout(ie, dev):
+    """swizzle_weight against the layout it documents, restated on the CPU: 1 KB block
+    R * K / 32 + S holds, at 16 bytes per lane 16 g + r, row 16 R + r, columns 32 S + 8 g .. +8
+    (a strided source too)."""
+    N, K = 48, 256
+    g = torch.Generator().manual_seed(5)
+    wide = torch.randn(N, K + 64, generator=g).bfloat16()
+    w = wide[:, 32:32 + K]
+    out = ie.swizzle_weight(w.to(dev)).cpu()
+    want = (w.reshape(N // 16, 16, K // 32, 4, 8)  # R, r, S, g, 8
+            .permute(0, 2, 3, 1, 4)                 # R, S, g, r, 8
+            .reshape(N, K))
+    assert torch.equal(out.view(torch.int16), want.contiguous().view(torch.int16))
+
+
+@pytest.mark.parametrize("mode", ["plain", "glu", "norm", "norm_glu", "residual"])
+@pytest.mark.parametrize("M", [1, 17, 32, 64])
+def test_swizzled_weight_same_bits(ie, dev, mode, M):
+    """Every form of the skinny GEMM on the swizzled weight: bit for bit the row-major form's
+    result at the same tile width."""
+    ops = ie.kernels.ops()
+    N, K = (12288, 2048) if "glu" in mode else (4096, 2048)
+    h, gam, w = _norm_inputs(M, K, N, 500 + M, dev)
+    sw = ie.swizzle_weight(w)
+    for nt in ((1, 2) if "glu" in mode else (1, 2, 4)):
+        if mode == "plain":
+            a, b = ops.skinny_matmul(h, w, nt, False), ops.skinny_matmul(h, sw, nt, True)
+        elif mode == "glu":
+            a = ops.skinny_matmul_silu_mul(h, w, nt, False)
+            b = ops.skinny_matmul_silu_mul(h, sw, nt, True)
+        elif mode in ("norm", "norm_glu"):
+            glu = mode == "norm_glu"
+            a = ops.skinny_matmul_norm(h, w, nt, glu, EPS, False)
+            b = ops.skinny_matmul_norm(h, sw, nt, glu, EPS, True)
+        else:
+            res0 = torch.randn(M, N, device=dev).bfloat16()
+            a = ops.skinny_matmul_residual_(h, w, nt, res0.clone(), False)
+            b = ops.skinny_matmul_residual_(h, sw, nt, res0.clone(), True)
+        torch.cuda.synchronize()
+        assert torch.equal(a, b), f"{mode} M={M} nt={nt}"
+    say(f"swizzled {mode} M={M}: bit-exact")
