@@ -444,6 +444,17 @@ hipError_t ie_add_rms_norm(const ie_bf16* residual, int64_t residual_stride, con
                            hipStream_t stream);
 
 /*
+ * RoPE tables of a step's positions, for the q/k RoPE of the other entry points (no separate
+ * function in the reference, which computes them with PyTorch at architecture.py:382-390):
+ * cos_out[t, j] = bf16(cos(float(positions[t]) * inv_freq[j])), sin_out likewise, for t < n,
+ * j < half_dim (one fp32 product, the device library's cosf/sinf, round to nearest even);
+ * outputs [n, half_dim] contiguous (the [n, 1, head_dim / 2] tables the kernels take).
+ */
+hipError_t ie_rope_tables(const int32_t* positions, int64_t n, const float* inv_freq,
+                          int32_t half_dim, ie_bf16* cos_out, ie_bf16* sin_out,
+                          hipStream_t stream);
+
+/*
  * SiLU-gated product. Replaces qwen3-1.7b/kernels.py:1204-1213 `silu_mul(gate_up) -> out`
  * (kernel kernels.py:1178-1201): gate_up bf16 [num_tokens, 2 * dim] (gate then up), out bf16
  * [num_tokens, dim] = bf16((g * sigmoid(g)) * u), sigmoid(g) = 1 / (1 + exp(-g)) in fp32.

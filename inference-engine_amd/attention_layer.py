@@ -29,6 +29,7 @@ from typing import Callable
 import torch
 from torch.cuda import nvtx
 
+from ._native import ops
 from .kernels import (LayerKVCache, decode_attention_rope, fused_norm_rope_prefill, linear,
                       prefill_attention, quantize_kv_prefill)
 
@@ -51,9 +52,13 @@ def rope_inv_freq(head_dim: int, base: float, device) -> torch.Tensor:
 
 def rope_tables(positions: torch.Tensor, inv_freq: torch.Tensor, dtype=torch.bfloat16):
     """architecture.py:382-390: angles = positions x inv_freq ([N, 1, D/2], fp32), then cos and
-    sin cast to the activation dtype. A decode step's positions are its cached_lens."""
-    angles = positions[:, None, None] * inv_freq[None, None, :]
-    return angles.cos().to(dtype), angles.sin().to(dtype)
+    sin cast to the activation dtype (bf16). A decode step's positions are its cached_lens.
+    One launch (ie_rope_tables: the same fp32 product, cosf/sinf, round to nearest even)
+    instead of PyTorch's five elementwise kernels."""
+    assert dtype == torch.bfloat16
+    if positions.dtype != torch.int32:
+        positions = positions.int()
+    return ops().rope_tables(positions, inv_freq)
 
 
 def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, seq_ids, cu_seqlens,

@@ -9,6 +9,8 @@
 // order; rstd = 1 / sqrt(ss / D + eps) (IEEE); normed = bf16((r * rstd) * w).
 // silu_mul_kernel, grid (N, cdiv(D, 2048)), 256 threads x 8 elements: bf16((g * sigmoid(g)) * u).
 // Both are HBM-bound streams (each byte read or written once).
+// rope_tables_kernel: the RoPE cos/sin tables of a step's positions (architecture.py:382-390) in
+// one launch instead of PyTorch's five elementwise ones.
 #include "ie_common.h"
 
 namespace ie {
@@ -145,5 +147,39 @@ extern "C" hipError_t ie_silu_mul(const ie_bf16* gate_up, int64_t gate_up_stride
     dim3 grid((unsigned)num_tokens, (unsigned)((dim + NA_STEP - 1) / NA_STEP));
     hipLaunchKernelGGL(silu_mul_kernel, grid, dim3(NA_THREADS), 0, stream,
                        (const uint16_t*)gate_up, gate_up_stride, dim, (uint16_t*)out, out_stride);
+    return hipGetLastError();
+}
+
+namespace ie {
+
+// angle = float(position) * inv_freq[j] (one IEEE fp32 product), then cos and sin of it (the
+// device library's cosf/sinf) rounded to bf16: the arithmetic of the reference's
+// `positions[:, None, None] * inv_freq` then `.cos().to(bf16)`, `.sin().to(bf16)`.
+__global__ __launch_bounds__(256) void rope_tables_kernel(const int32_t* __restrict__ pos,
+                                                          int64_t n, const float* __restrict__ inv,
+                                                          int half, uint16_t* __restrict__ cosv,
+                                                          uint16_t* __restrict__ sinv) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n * half) return;
+    const int64_t t = i / half;
+    const int j = (int)(i - t * half);
+    const float a = (float)pos[t] * inv[j];  // a product alone: nothing to contract
+    cosv[i] = (uint16_t)f32_to_bf16_rne(cosf(a));
+    sinv[i] = (uint16_t)f32_to_bf16_rne(sinf(a));
+}
+
+}  // namespace ie
+
+extern "C" hipError_t ie_rope_tables(const int32_t* positions, int64_t n, const float* inv_freq,
+                                     int32_t half_dim, ie_bf16* cos_out, ie_bf16* sin_out,
+                                     hipStream_t stream) {
+    IE_REQUIRE(n >= 0 && half_dim > 0, "bad sizes");
+    if (n == 0) return hipSuccess;
+    IE_REQUIRE(positions && inv_freq && cos_out && sin_out, "null pointer");
+    const int64_t total = n * half_dim;
+    IE_REQUIRE(total / 256 < (1LL << 31), "too many table entries");
+    hipLaunchKernelGGL(ie::rope_tables_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                       stream, positions, n, inv_freq, (int)half_dim, (uint16_t*)cos_out,
+                       (uint16_t*)sin_out);
     return hipGetLastError();
 }

@@ -221,6 +221,24 @@ std::tuple<at::Tensor, at::Tensor> add_rms_norm(const at::Tensor& residual,
     return {nres, normed};
 }
 
+// RoPE tables of int32 positions [N] and fp32 inv_freq [D / 2]: bf16 cos, sin [N, 1, D / 2].
+std::tuple<at::Tensor, at::Tensor> rope_tables(const at::Tensor& positions,
+                                               const at::Tensor& inv_freq) {
+    check_i32(positions, "positions");
+    check_dev(inv_freq, "inv_freq");
+    TORCH_CHECK(inv_freq.scalar_type() == at::kFloat && inv_freq.dim() == 1 &&
+                    inv_freq.is_contiguous() && inv_freq.device() == positions.device(),
+                "ie: inv_freq must be a contiguous fp32 vector on the positions' device");
+    const c10::DeviceGuard guard(positions.device());
+    const int64_t N = positions.size(0), H = inv_freq.size(0);
+    auto opt = positions.options().dtype(at::kBFloat16);
+    at::Tensor c = at::empty({N, 1, H}, opt), s = at::empty({N, 1, H}, opt);
+    ok(ie_rope_tables(i32(positions), N, inv_freq.data_ptr<float>(), (int32_t)H, bfm(c), bfm(s),
+                      stream_of(positions)),
+       "rope_tables");
+    return {c, s};
+}
+
 at::Tensor silu_mul(const at::Tensor& gate_up) {
     check_bf16_rows(gate_up, "gate_up", 2);
     const c10::DeviceGuard guard(gate_up.device());
@@ -648,6 +666,7 @@ TORCH_LIBRARY(ie, m) {
     m.def("sample(Tensor logits, float tau, Tensor(a!) seed) -> Tensor");
     m.def("add_rms_norm(Tensor residual, Tensor delta, Tensor weight, float eps) -> (Tensor, Tensor)");
     m.def("silu_mul(Tensor gate_up) -> Tensor");
+    m.def("rope_tables(Tensor positions, Tensor inv_freq) -> (Tensor, Tensor)");
     m.def("skinny_matmul(Tensor x, Tensor weight, int n_tiles=1, bool swizzled=False) -> Tensor");
     m.def(
         "skinny_matmul_silu_mul(Tensor x, Tensor weight, int n_tiles=1, bool swizzled=False) "
@@ -696,6 +715,7 @@ TORCH_LIBRARY_IMPL(ie, CUDA, m) {
     m.impl("sample", &sample);
     m.impl("add_rms_norm", &add_rms_norm);
     m.impl("silu_mul", &silu_mul);
+    m.impl("rope_tables", &rope_tables);
     m.impl("skinny_matmul", &skinny_matmul);
     m.impl("skinny_matmul_silu_mul", &skinny_matmul_silu_mul);
     m.impl("skinny_matmul_norm", &skinny_matmul_norm);

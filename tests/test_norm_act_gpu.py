@@ -58,3 +58,26 @@ def test_empty_rows(ie, dev):
     c = ie.silu_mul(_bf16((0, 4096), 3, dev))
     torch.cuda.synchronize()
     assert a.shape == (0, 2048) and b.shape == (0, 2048) and c.shape == (0, 2048)
+
+
+@pytest.mark.gpu
+def test_rope_tables_match_pytorch(ie, dev):
+    """attention_layer.rope_tables (one HIP launch) against the reference's PyTorch arithmetic
+    (architecture.py:382-390: int32 positions times the fp32 inverse frequencies, cos and sin,
+    cast to bf16) on the device, bit for bit: positions 0 .. 70,000 and a decode step's
+    cached lengths, head_dim 128 (rope base 1e6) and 64 (base 1e4)."""
+    al = ie.attention_layer
+    g = torch.Generator().manual_seed(9)
+    for D, base in ((128, 1e6), (64, 1e4)):
+        inv = al.rope_inv_freq(D, base, dev)
+        for pos in (torch.arange(70000, dtype=torch.int32),
+                    torch.randint(0, 40000, (33,), generator=g, dtype=torch.int32)):
+            p = pos.to(dev)
+            c, s = al.rope_tables(p, inv)
+            ang = p[:, None, None] * inv[None, None, :]
+            rc, rs = ang.cos().to(torch.bfloat16), ang.sin().to(torch.bfloat16)
+            torch.cuda.synchronize()
+            assert c.shape == rc.shape and s.shape == rs.shape
+            dc = (c.view(torch.int16) != rc.view(torch.int16)).sum().item()
+            dsn = (s.view(torch.int16) != rs.view(torch.int16)).sum().item()
+            assert dc == 0 and dsn == 0, f"D={D}: {dc} cos, {dsn} sin entries differ"
