@@ -511,8 +511,9 @@ hipError_t ie_skinny_gemm_silu_mul(const ie_bf16* x, int64_t x_stride, int32_t m
  *                     bf16(y + bf16(x . weight^T)) in place: add_rms_norm's new_residual for the
  *                     projection's output as delta, bit for bit (x must not overlap y).
  *   | IE_SKINNY_SWIZZLED (with any of the above) weight is the output of
- *                     ie_skinny_weight_swizzle (weight_stride = k; n_tiles 1, 2 or 4): the same
- *                     results, bit for bit, as the row-major weight with the same n_tiles.
+ *                     ie_skinny_weight_swizzle for this n_tiles (1, 2 or 4; weight_stride = k;
+ *                     an n_tiles too wide for m is an error, not lowered): the same results, bit
+ *                     for bit, as the row-major weight with the same n_tiles.
  * Sizes, strides and n_tiles as for the plain or the gate/up form. The sum of squares is taken
  * from the bf16 rows of x over all k columns (eight partial sums combined in a fixed order).
  */
@@ -526,17 +527,19 @@ hipError_t ie_skinny_gemm_fused(const ie_bf16* x, int64_t x_stride, int32_t m,
                                 int64_t y_stride, hipStream_t stream);
 
 /*
- * A weight's elements in the order the skinny GEMM's waves consume them (no counterpart in the
- * reference; for weights used many times, e.g. every decode step's projections, reordered once
- * at load): out holds n x k bf16, as 1 KB blocks, block R * k / 32 + S for row group R
- * (rows 16 R .. 16 R + 15) and column step S (columns 32 S .. 32 S + 31), each holding, at
- * byte 16 (16 g + r), row 16 R + r, columns 32 S + 8 g .. 32 S + 8 g + 7. With it a wave reads
- * an MFMA operand fragment as one contiguous 1 KB load instead of staging row-major rows
- * through LDS. weight: bf16 [n, k] rows (16-byte aligned, stride weight_stride); n a multiple
- * of 16, k of 32.
+ * A weight's elements in the order the skinny GEMM's waves consume them for a tile width
+ * n_tiles (1, 2 or 4) (no counterpart in the reference; for weights used many times, e.g. every
+ * decode step's projections, reordered once at load): out holds n x k bf16, as 1 KB blocks,
+ * block ((R / G) * k / 32 + S) * G + R % G (G = n_tiles) for row group R (rows 16 R .. 16 R +
+ * 15) and column step S (columns 32 S .. 32 S + 31), each holding, at byte 16 (16 g + r), row
+ * 16 R + r, columns 32 S + 8 g .. 32 S + 8 g + 7 (each workgroup's G groups interleaved step by
+ * step). With it a wave reads an MFMA operand fragment as one contiguous 1 KB load instead of
+ * staging row-major rows through LDS; the GEMM must take the same n_tiles. weight: bf16 [n, k]
+ * rows (16-byte aligned, stride weight_stride); n a multiple of 16 n_tiles, k of 32.
  */
 hipError_t ie_skinny_weight_swizzle(const ie_bf16* weight, int64_t weight_stride, int32_t n,
-                                    int32_t k, ie_bf16* out, hipStream_t stream);
+                                    int32_t k, int32_t n_tiles, ie_bf16* out,
+                                    hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -47,10 +47,12 @@ constexpr int SG_MAX_TILES = 6;  // weight + x tiles, at most (LDS: 8 waves x 16
 // been folded into the weight's columns by the caller (y = rstd_m * sum_k h[m,k] (g_k W[n,k]) is
 // the GEMM of the normalized rows); RES, y holds the residual stream on entry and each output
 // becomes bf16(y + bf16(sum)), in place (add_rms_norm's new residual, kernels.py:1240-1242);
-// SWZ, the weight comes in the fragment order skinny_weight_swizzle_kernel writes: each
-// 16-row group's 32-column steps as 1 KB blocks, lane (r, g)'s 16 bytes at 16 (16 g + r), so a
-// wave reads a weight fragment as one contiguous 1 KB load, straight into its registers (no LDS
-// round trip for the weight; the same fragments, so the same sums, as the row-major form).
+// SWZ, the weight comes in the fragment order skinny_weight_swizzle_kernel writes for NT: 1 KB
+// blocks, one per (16-row group, 32-column step), lane (r, g)'s 16 bytes at 16 (16 g + r), the
+// NT groups of each workgroup's 16 NT rows interleaved step by step; a wave reads a weight
+// fragment as one contiguous 1 KB load, straight into its registers (no LDS round trip for the
+// weight; the same fragments, so the same sums, as the row-major form), a workgroup reads only
+// its own contiguous rows, and its NT tiles of one step are neighbours in memory.
 enum : int { SG_PLAIN = 0, SG_HALF = 1, SG_GLU = 2, SG_NORM = 4, SG_RES = 8, SG_SWZ = 16 };
 
 template <int TT, int MT, int PT>
@@ -89,12 +91,9 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
     // parts of x at any moment instead of all hitting the same L2 lines
     const int kw = K / SG_WAVES, k_begin = (int)((wave + blockIdx.x) % SG_WAVES) * kw;
     // W rows [n0, n0 + WROWS) (GLU: and the up rows [nh + n0, +WROWS)) and x rows [0, M): the
-    // buffer ranges zero the rows of x past M. SWZ: the same rows' 1 KB blocks, 16-row group by
-    // group (K / 32 blocks each)
-    const int64_t wrow = SWZ ? (int64_t)(K / 32) * 512 / 16 : ws;  // elements per weight row
-    const rsrc_t rw = make_rsrc(w + (int64_t)n0 * wrow, (uint32_t)(WROWS * wrow * 2));
-    const rsrc_t ru =
-        make_rsrc(w + ((int64_t)nh + n0) * wrow, (uint32_t)(GLU ? WROWS * wrow * 2 : 0));
+    // buffer ranges zero the rows of x past M (SWZ: the same rows, as the workgroup's band)
+    const rsrc_t rw = make_rsrc(w + (int64_t)n0 * ws, (uint32_t)(WROWS * ws * 2));
+    const rsrc_t ru = make_rsrc(w + ((int64_t)nh + n0) * ws, (uint32_t)(GLU ? WROWS * ws * 2 : 0));
     const rsrc_t rx = make_rsrc(x, (uint32_t)(M * xs * 2));
     // byte offsets of this lane's two 8-row halves of every tile at the slice start (SWZ weight
     // tiles: of its two 32-column steps' blocks)
@@ -103,8 +102,8 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
     for (int i = 0; i < TILES; ++i)
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            if (SWZ && i < WT) {
-                loff[i][h] = ((i % NT) * (K / 32) + k_begin / 32 + h) * 1024 + 16 * lane;
+            if (SWZ && i < WT) {  // group i % NT of the band, step k_begin / 32 + h
+                loff[i][h] = ((k_begin / 32 + h) * NT + i % NT) * 1024 + 16 * lane;
                 continue;
             }
             const int row = 16 * (i < WT ? i % NT : i - WT) + 8 * h + lr;
@@ -139,8 +138,8 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
                 if (HALF && i < NT && h == 1) continue;
                 if (SWZ && i < WT) {  // 32-column step h of the batch: one 1 KB block
                     r[i][h] = __builtin_amdgcn_raw_buffer_load_b128(
-                        i < NT ? rw : ru, SG_BK * b + 32 * h < kw ? loff[i][h] + 2048 * b : -1, 0,
-                        0);
+                        i < NT ? rw : ru,
+                        SG_BK * b + 32 * h < kw ? loff[i][h] + 2048 * NT * b : -1, 0, 0);
                     continue;
                 }
                 r[i][h] = __builtin_amdgcn_raw_buffer_load_b128(
@@ -382,7 +381,8 @@ extern "C" hipError_t ie_skinny_gemm_fused(const ie_bf16* x, int64_t x_stride, i
                res = flags & IE_SKINNY_RESIDUAL, swz = flags & IE_SKINNY_SWIZZLED;
     IE_REQUIRE(!norm || (eps >= 0.f && eps < 1e30f), "eps must be finite and >= 0");
     IE_REQUIRE(!swz || (n_tiles >= 1 && weight_stride == k),
-               "a swizzled weight takes n_tiles 1, 2 or 4 and weight_stride k");
+               "a swizzled weight takes the n_tiles (1, 2 or 4) it was swizzled for and "
+               "weight_stride k");
     if (m == 0 || n == 0) return hipSuccess;
     if (glu) {
         IE_REQUIRE(n_tiles == 1 || n_tiles == 2, "n_tiles must be 1 or 2");
@@ -395,6 +395,9 @@ extern "C" hipError_t ie_skinny_gemm_fused(const ie_bf16* x, int64_t x_stride, i
     SgCall c{(const uint16_t*)x, x_stride, m, (const uint16_t*)weight, weight_stride, k,
              (uint16_t*)y, y_stride, glu ? n / 2 : 0, eps};
     dim3 grid;
+    IE_REQUIRE(!swz || (glu ? 2 * n_tiles : n_tiles) + mt <= SG_MAX_TILES,
+               "a swizzled weight's n_tiles is too wide for this many rows (its layout depends "
+               "on n_tiles, which cannot be lowered)");
     if (glu) {
         // gate and up tiles: lowered to one n-tile where m leaves too little LDS for two
         if (2 * n_tiles + mt > SG_MAX_TILES) n_tiles = 1;
@@ -420,11 +423,12 @@ extern "C" hipError_t ie_skinny_gemm_fused(const ie_bf16* x, int64_t x_stride, i
     return hipGetLastError();
 }
 
-// The fragment order of the SWZ form: output 1 KB block (R, S) (16-row group R, 32-column step
-// S, at block index R * k / 32 + S) holds, at 16 bytes per lane L = 16 g + r, weight row
-// 16 R + r, columns 32 S + 8 g .. + 8. One wave per block.
+// The fragment order of the SWZ form for n_tiles G: the 1 KB block of 16-row group R and
+// 32-column step S, at block index ((R / G) * k / 32 + S) * G + R % G, holds, at 16 bytes per
+// lane L = 16 g + r, weight row 16 R + r, columns 32 S + 8 g .. + 8. One wave per block.
 __global__ __launch_bounds__(256) void skinny_weight_swizzle_kernel(const uint16_t* __restrict__ w,
                                                                     int64_t ws, int n, int k,
+                                                                    int G,
                                                                     uint16_t* __restrict__ out) {
     const int lane = threadIdx.x & 63;
     const int64_t blk = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -433,16 +437,19 @@ __global__ __launch_bounds__(256) void skinny_weight_swizzle_kernel(const uint16
     const int64_t R = blk / steps, S = blk % steps;
     const int r = lane & 15, g = lane >> 4;
     const uint4 v = *reinterpret_cast<const uint4*>(w + (16 * R + r) * ws + 32 * S + 8 * g);
-    *reinterpret_cast<uint4*>(out + blk * 512 + 8 * lane) = v;
+    const int64_t dst = ((R / G) * steps + S) * G + R % G;
+    *reinterpret_cast<uint4*>(out + dst * 512 + 8 * lane) = v;
 }
 
 extern "C" hipError_t ie_skinny_weight_swizzle(const ie_bf16* weight, int64_t weight_stride,
-                                               int32_t n, int32_t k, ie_bf16* out,
-                                               hipStream_t stream) {
+                                               int32_t n, int32_t k, int32_t n_tiles,
+                                               ie_bf16* out, hipStream_t stream) {
     IE_REQUIRE(n >= 0 && k >= 0, "negative sizes");
+    IE_REQUIRE(n_tiles == 1 || n_tiles == 2 || n_tiles == 4, "n_tiles must be 1, 2 or 4");
     if (n == 0 || k == 0) return hipSuccess;
     IE_REQUIRE(weight && out, "null pointer");
-    IE_REQUIRE(n % 16 == 0 && k % 32 == 0, "n must be a multiple of 16 and k of 32");
+    IE_REQUIRE(n % (16 * n_tiles) == 0 && k % 32 == 0,
+               "n must be a multiple of 16 n_tiles and k of 32");
     IE_REQUIRE(weight_stride >= k && weight_stride % 8 == 0 &&
                    (reinterpret_cast<uintptr_t>(weight) & 15) == 0 &&
                    (reinterpret_cast<uintptr_t>(out) & 15) == 0,
@@ -450,7 +457,7 @@ extern "C" hipError_t ie_skinny_weight_swizzle(const ie_bf16* weight, int64_t we
     const int64_t blocks = (int64_t)(n / 16) * (k / 32);
     hipLaunchKernelGGL(skinny_weight_swizzle_kernel, dim3((unsigned)((blocks + 3) / 4)),
                        dim3(256), 0, stream, (const uint16_t*)weight, weight_stride, n, k,
-                       (uint16_t*)out);
+                       (int)n_tiles, (uint16_t*)out);
     return hipGetLastError();
 }
 

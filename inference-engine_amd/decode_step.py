@@ -117,8 +117,9 @@ class DecodeStep:
         """fused: fold every layer's input_norm into its qkv weight and post_norm into its
         gate_up weight, in place (the layers then serve only the fused form). swizzle (default:
         with fused): every projection weight whose tuned skinny GEMM tile width is at least one
-        16-row tile is reordered in place into the GEMM's fragment order (swizzle_weight; the
-        same result bits); the LM head gets a reordered copy of the embedding."""
+        16-row tile is reordered in place into the GEMM's fragment order for that width
+        (swizzle_weight; the same result bits); the LM head gets a reordered copy of the
+        embedding."""
         self.shape, self.layers, self.embed, self.final_norm = shape, layers, embed, final_norm
         self.fused = fused
         self.swz = dict.fromkeys(("qkv", "o_proj", "gate_up", "down", "lm_head"), False)
@@ -130,18 +131,19 @@ class DecodeStep:
             self._zero = torch.zeros(batch, shape.model_dim, device=device, dtype=torch.bfloat16)
             if swizzle is None or swizzle:
                 lw = layers[0]
-                tiles = lambda w: use_skinny.get((w.shape[0], w.shape[1], batch))
-                for name in ("qkv", "o_proj", "down"):
-                    self.swz[name] = tiles(getattr(lw, name)) not in (None, 0)
-                self.swz["gate_up"] = (lw.gate_up.shape[0], lw.gate_up.shape[1],
-                                       batch) in use_skinny_glu
-                self.swz["lm_head"] = tiles(embed) not in (None, 0)
+                key = lambda w: (w.shape[0], w.shape[1], batch)
+                nt = {name: use_skinny.get(key(getattr(lw, name)))
+                      for name in ("qkv", "o_proj", "down")}
+                nt["gate_up"] = use_skinny_glu.get(key(lw.gate_up))
+                nt["lm_head"] = use_skinny.get(key(embed))
+                for name, t in nt.items():
+                    self.swz[name] = t not in (None, 0)
                 for lw in layers:
                     for name in ("qkv", "o_proj", "gate_up", "down"):
                         if self.swz[name]:
-                            setattr(lw, name, swizzle_weight(getattr(lw, name)))
+                            setattr(lw, name, swizzle_weight(getattr(lw, name), nt[name]))
                 if self.swz["lm_head"]:
-                    self.lm_head_w = swizzle_weight(embed)
+                    self.lm_head_w = swizzle_weight(embed, nt["lm_head"])
         self.caches = caches
         self.B = batch
         pool = caches[0].k.shape[0]

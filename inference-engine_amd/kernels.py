@@ -255,12 +255,15 @@ def skinny_matmul(x: torch.Tensor, weight: torch.Tensor, n_tiles: int = 1,
     return ops().skinny_matmul(x, weight, int(n_tiles), bool(swizzled))
 
 
-def swizzle_weight(weight: torch.Tensor) -> torch.Tensor:
-    """The weight in the skinny GEMM's fragment order (ie_skinny_weight_swizzle: each 16-row
-    group's 32-column steps as 1 KB blocks that a wave loads whole, straight into MFMA operand
-    registers). Reordered once at load; the GEMMs then take it with swizzled=True. [N, K] like
-    the weight (N a multiple of 16, K of 32), only for the skinny GEMM."""
-    return ops().skinny_weight_swizzle(weight)
+def swizzle_weight(weight: torch.Tensor, n_tiles: int) -> torch.Tensor:
+    """The weight in the skinny GEMM's fragment order for tile width n_tiles (1, 2 or 4;
+    ie_skinny_weight_swizzle: 1 KB blocks of 16 rows x 32 columns that a wave loads whole,
+    straight into MFMA operand registers, each workgroup's n_tiles row groups interleaved step by
+    step). Reordered once at load; the GEMMs then take it with swizzled=True and the same
+    n_tiles (the tuned one, from the tables tune_linear fills). [N, K] like the weight (N a
+    multiple of 16 n_tiles, K of 32), only for the skinny GEMM."""
+    assert n_tiles in (1, 2, 4)
+    return ops().skinny_weight_swizzle(weight, int(n_tiles))
 
 
 # (N, K, M) -> the n_tiles of skinny_matmul when it beat the library GEMM for that weight shape
