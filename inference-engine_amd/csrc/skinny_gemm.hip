@@ -52,8 +52,12 @@ constexpr int SG_MAX_TILES = 6;  // weight + x tiles, at most (LDS: 8 waves x 16
 // NT groups of each workgroup's 16 NT rows interleaved step by step; a wave reads a weight
 // fragment as one contiguous 1 KB load, straight into its registers (no LDS round trip for the
 // weight; the same fragments, so the same sums, as the row-major form), a workgroup reads only
-// its own contiguous rows, and its NT tiles of one step are neighbours in memory.
-enum : int { SG_PLAIN = 0, SG_HALF = 1, SG_GLU = 2, SG_NORM = 4, SG_RES = 8, SG_SWZ = 16 };
+// its own contiguous rows, and its NT tiles of one step are neighbours in memory;
+// LOOP, the grid is one workgroup per CU and each loops over the row blocks b, b + grid, ...,
+// the next block's first batch in flight during the current block's reduction (for weights of
+// many more blocks than CUs: the LM head), each block summed exactly as its own workgroup would.
+enum : int { SG_PLAIN = 0, SG_HALF = 1, SG_GLU = 2, SG_NORM = 4, SG_RES = 8, SG_SWZ = 16,
+             SG_LOOP = 32 };
 
 template <int TT, int MT, int PT>
 struct SgLds {
@@ -71,14 +75,15 @@ struct SgLds {
 template <int MT, int NT, int MODE>
 __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
     const uint16_t* __restrict__ x, int64_t xs, int M, const uint16_t* __restrict__ w, int64_t ws,
-    int K, uint16_t* __restrict__ y, int64_t ys, int nh, float eps) {
+    int K, uint16_t* __restrict__ y, int64_t ys, int nh, float eps, int nblk) {
     constexpr bool HALF = MODE & SG_HALF, GLU = MODE & SG_GLU, NORM = MODE & SG_NORM,
-                   RES = MODE & SG_RES, SWZ = MODE & SG_SWZ;
+                   RES = MODE & SG_RES, SWZ = MODE & SG_SWZ, LOOP = MODE & SG_LOOP;
     constexpr int WT = GLU ? 2 * NT : NT;  // weight tiles: NT (GLU: NT gate, then NT up tiles)
     static_assert(WT + MT <= SG_MAX_TILES, "LDS transpose region too large");
     static_assert(!HALF || NT == 1, "8-row n-tiles come one per workgroup");
     static_assert(!GLU || NT * MT <= SG_WAVES, "GLU: at most one output tile per wave");
     static_assert(!(SWZ && HALF), "the fragment-ordered weight comes in 16-row groups");
+    static_assert(!LOOP || !(GLU || NORM || RES || HALF), "the looping grid: plain launches only");
     constexpr int WROWS = HALF ? 8 : 16 * NT;  // weight rows per workgroup (per half in GLU)
     constexpr int TILES = WT + MT;  // W tiles 0..WT-1, then x tiles
     constexpr int T0 = SWZ ? WT : 0;  // the first tile that goes through LDS (its LDS row: 16 (i - T0))
@@ -86,29 +91,34 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l16 = lane & 15, g = lane >> 4;
     const int lr = lane >> 3, lc = lane & 7;  // load mapping: row lr of 8, 16-byte chunk lc
-    const int n0 = blockIdx.x * WROWS;
-    // wave w of workgroup b takes K slice (w + b) mod 8: neighbouring workgroups read different
-    // parts of x at any moment instead of all hitting the same L2 lines
-    const int kw = K / SG_WAVES, k_begin = (int)((wave + blockIdx.x) % SG_WAVES) * kw;
-    // W rows [n0, n0 + WROWS) (GLU: and the up rows [nh + n0, +WROWS)) and x rows [0, M): the
-    // buffer ranges zero the rows of x past M (SWZ: the same rows, as the workgroup's band)
-    const rsrc_t rw = make_rsrc(w + (int64_t)n0 * ws, (uint32_t)(WROWS * ws * 2));
-    const rsrc_t ru = make_rsrc(w + ((int64_t)nh + n0) * ws, (uint32_t)(GLU ? WROWS * ws * 2 : 0));
+    const int kw = K / SG_WAVES;
     const rsrc_t rx = make_rsrc(x, (uint32_t)(M * xs * 2));
-    // byte offsets of this lane's two 8-row halves of every tile at the slice start (SWZ weight
-    // tiles: of its two 32-column steps' blocks)
+    rsrc_t rw, ru;
     int loff[TILES][2];
+    // Row block bk: W rows [bk WROWS, +WROWS) (GLU: and the up rows nh further) and x rows
+    // [0, M): the buffer ranges zero the rows of x past M (SWZ: the same rows, as the
+    // workgroup's band). Wave w takes K slice (w + bk) mod 8: neighbouring workgroups read
+    // different parts of x at any moment instead of all hitting the same L2 lines. loff: byte
+    // offsets of this lane's two 8-row halves of every tile at the slice start (SWZ weight tiles:
+    // of its two 32-column steps' blocks).
+    auto setup = [&](int bk) {
+        const int n0 = bk * WROWS, k_begin = (int)((wave + bk) % SG_WAVES) * kw;
+        rw = make_rsrc(w + (int64_t)n0 * ws, (uint32_t)(WROWS * ws * 2));
+        ru = make_rsrc(w + ((int64_t)nh + n0) * ws, (uint32_t)(GLU ? WROWS * ws * 2 : 0));
 #pragma unroll
-    for (int i = 0; i < TILES; ++i)
+        for (int i = 0; i < TILES; ++i)
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            if (SWZ && i < WT) {  // group i % NT of the band, step k_begin / 32 + h
-                loff[i][h] = ((k_begin / 32 + h) * NT + i % NT) * 1024 + 16 * lane;
-                continue;
+            for (int h = 0; h < 2; ++h) {
+                if (SWZ && i < WT) {  // group i % NT of the band, step k_begin / 32 + h
+                    loff[i][h] = ((k_begin / 32 + h) * NT + i % NT) * 1024 + 16 * lane;
+                    continue;
+                }
+                const int row = 16 * (i < WT ? i % NT : i - WT) + 8 * h + lr;
+                loff[i][h] = (row * (int)(i < WT ? ws : xs) + k_begin + 8 * lc) * 2;
             }
-            const int row = 16 * (i < WT ? i % NT : i - WT) + 8 * h + lr;
-            loff[i][h] = (row * (int)(i < WT ? ws : xs) + k_begin + 8 * lc) * 2;
-        }
+    };
+    int blk = blockIdx.x;
+    setup(blk);
 
     __shared__ __attribute__((aligned(16))) SgLds<TILES - T0, MT, NT> lds;
     uint8_t* reg = lds.t[wave];
@@ -116,10 +126,6 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
     const uint8_t* rsrc = reg + l16 * SG_LROW + 16 * g;   // + 16 i rows + 64 t
 
     sg_f32x4 acc[WT][MT];
-#pragma unroll
-    for (int nt = 0; nt < WT; ++nt)
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = sg_f32x4{0.f, 0.f, 0.f, 0.f};
     // NORM: lane (l16, g) sums the squares of the x elements it holds (row 16 mt + l16, 8 of every
     // 32 k of the slice); the four g lanes and eight waves together cover each row once
     float ss[MT];
@@ -188,6 +194,11 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
     const int nb = (kw + SG_BK - 1) / SG_BK;
     Batch ra, rb;
     load(ra, 0);
+    for (;;) {  // once, or (LOOP) over the workgroup's row blocks
+#pragma unroll
+    for (int nt = 0; nt < WT; ++nt)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = sg_f32x4{0.f, 0.f, 0.f, 0.f};
     for (int b = 0; b < nb; b += 2) {
         load(rb, b + 1);
         __builtin_amdgcn_sched_barrier(0);
@@ -195,6 +206,13 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
         load(ra, b + 2);
         __builtin_amdgcn_sched_barrier(0);
         compute(rb);
+    }
+    const int n0 = blk * WROWS;
+    const int next = blk + (int)gridDim.x;
+    if (LOOP && next < nblk) {  // the next block's first batch, in flight during the reduction
+        setup(next);
+        load(ra, 0);
+        __builtin_amdgcn_sched_barrier(0);
     }
 
     // D lane (l16, g) element i: n = n0 + 16 nt + 4g + i, m = 16 mt + l16. The waves' partial
@@ -262,6 +280,10 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
             }
         }
     }
+    if (!LOOP || next >= nblk) break;
+    __syncthreads();  // every wave is done reading the partial tiles before the next transposes
+    blk = next;
+    }
 }
 
 }  // namespace ie
@@ -303,12 +325,14 @@ struct SgCall {
     int64_t ys;
     int nh;
     float eps;
+    int nblk;  // row blocks (the looping grid: more than its workgroups)
 };
 
 template <int MT, int NT, int MODE>
 void sg_go(dim3 grid, hipStream_t s, const SgCall& c) {
     hipLaunchKernelGGL((skinny_gemm_kernel<MT, NT, MODE>), grid, dim3(SG_THREADS), 0, s, c.x,
-                       c.xs, c.m, c.w, c.ws, c.k, c.y, c.ys, c.nh, c.eps);
+                       c.xs, c.m, c.w, c.ws, c.k, c.y, c.ys, c.nh, c.eps,
+                       c.nblk > 0 ? c.nblk : (int)grid.x);
 }
 
 // One weight row block per workgroup: n_tiles 0 (8 rows), 1, 2 or 4 n-tiles of 16 rows (4 only
@@ -393,7 +417,7 @@ extern "C" hipError_t ie_skinny_gemm_fused(const ie_bf16* x, int64_t x_stride, i
     if (e != hipSuccess) return e;
     const int mt = (m + 15) / 16;
     SgCall c{(const uint16_t*)x, x_stride, m, (const uint16_t*)weight, weight_stride, k,
-             (uint16_t*)y, y_stride, glu ? n / 2 : 0, eps};
+             (uint16_t*)y, y_stride, glu ? n / 2 : 0, eps, 0};
     dim3 grid;
     IE_REQUIRE(!swz || (glu ? 2 * n_tiles : n_tiles) + mt <= SG_MAX_TILES,
                "a swizzled weight's n_tiles is too wide for this many rows (its layout depends "
@@ -414,7 +438,11 @@ extern "C" hipError_t ie_skinny_gemm_fused(const ie_bf16* x, int64_t x_stride, i
         case SG_RES: sg_dispatch<SG_RES | SW>(false, mt, n_tiles, grid, stream, c); break; \
         default: sg_dispatch<SG_PLAIN | SW>(glu, mt, n_tiles, grid, stream, c); break;     \
     }
-    if (swz) {
+    if (swz && !glu && mode == 0 && n_tiles > 0 && (int)grid.x > 4 * device_cu_count()) {
+        // a weight of many more row blocks than CUs (the LM head): one looping workgroup per CU
+        c.nblk = (int)grid.x;
+        sg_rows_mt<SG_SWZ | SG_LOOP>(mt, n_tiles, dim3((unsigned)device_cu_count()), stream, c);
+    } else if (swz) {
         IE_SG_DISPATCH(SG_SWZ)
     } else {
         IE_SG_DISPATCH(0)
