@@ -36,7 +36,14 @@ constexpr int SG_WAVES = 8;
 constexpr int SG_THREADS = SG_WAVES * IE_WAVE;
 constexpr int SG_BK = 64;      // k per batch: 128 bytes of a row, one 8-lane load group
 constexpr int SG_LROW = 160;   // LDS row stride (bytes)
-constexpr int SG_MAX_TILES = 6;  // weight + x tiles, at most (LDS: 8 waves x 16 tiles' rows x 160 B)
+constexpr int SG_MAX_TILES = 6;
+// Weight loads carry the non-temporal cache policy (aux bit 1, "nt"): each weight byte is read
+// once per launch, and streaming it past the caches took the LM head from 117 to 105 us and each
+// layer projection 0.2-0.9 us lower at 32 rows (x keeps the default policy: every workgroup
+// reads it).
+#ifndef IE_SKINNY_W_AUX
+#define IE_SKINNY_W_AUX 2
+#endif  // weight + x tiles, at most (LDS: 8 waves x 16 tiles' rows x 160 B)
 
 // Launch modes (bits): plain n-tiles of 16 rows; one n-tile of 8 rows (HALF); GLU, the gate/up
 // projection with the SiLU-gated product fused: n-tile t pairs gate rows [16 NT t, +16 NT) with
@@ -55,9 +62,14 @@ constexpr int SG_MAX_TILES = 6;  // weight + x tiles, at most (LDS: 8 waves x 16
 // its own contiguous rows, and its NT tiles of one step are neighbours in memory;
 // LOOP, the grid is one workgroup per CU and each loops over the row blocks b, b + grid, ...,
 // the next block's first batch in flight during the current block's reduction (for weights of
-// many more blocks than CUs: the LM head), each block summed exactly as its own workgroup would.
+// many more blocks than CUs: the LM head), each block summed exactly as its own workgroup would;
+// XREG (with LOOP and SWZ, K = 2048): each wave keeps one K slice for every block and holds its
+// x fragments over that slice in registers, loaded once per launch, so the loop streams only
+// the weight (no x reloads, no LDS round trip); the partial tiles are summed in the slice order
+// of the one-block-per-workgroup form, so every block's result bits stay the same.
 enum : int { SG_PLAIN = 0, SG_HALF = 1, SG_GLU = 2, SG_NORM = 4, SG_RES = 8, SG_SWZ = 16,
-             SG_LOOP = 32 };
+             SG_LOOP = 32, SG_XREG = 64 };
+constexpr int SG_XREG_K = SG_WAVES * 4 * SG_BK;  // the one K of the XREG form: 4 batches a wave
 
 template <int TT, int MT, int PT>
 struct SgLds {
@@ -77,13 +89,16 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
     const uint16_t* __restrict__ x, int64_t xs, int M, const uint16_t* __restrict__ w, int64_t ws,
     int K, uint16_t* __restrict__ y, int64_t ys, int nh, float eps, int nblk) {
     constexpr bool HALF = MODE & SG_HALF, GLU = MODE & SG_GLU, NORM = MODE & SG_NORM,
-                   RES = MODE & SG_RES, SWZ = MODE & SG_SWZ, LOOP = MODE & SG_LOOP;
+                   RES = MODE & SG_RES, SWZ = MODE & SG_SWZ, LOOP = MODE & SG_LOOP,
+                   XREG = MODE & SG_XREG;
     constexpr int WT = GLU ? 2 * NT : NT;  // weight tiles: NT (GLU: NT gate, then NT up tiles)
     static_assert(WT + MT <= SG_MAX_TILES, "LDS transpose region too large");
     static_assert(!HALF || NT == 1, "8-row n-tiles come one per workgroup");
     static_assert(!GLU || NT * MT <= SG_WAVES, "GLU: at most one output tile per wave");
     static_assert(!(SWZ && HALF), "the fragment-ordered weight comes in 16-row groups");
     static_assert(!LOOP || !(GLU || NORM || RES || HALF), "the looping grid: plain launches only");
+    static_assert(!XREG || (LOOP && SWZ), "x in registers: the looping grid over a swizzled weight");
+    constexpr int XNB = XREG ? SG_XREG_K / SG_WAVES / SG_BK : 1;  // batches of x held per wave
     constexpr int WROWS = HALF ? 8 : 16 * NT;  // weight rows per workgroup (per half in GLU)
     constexpr int TILES = WT + MT;  // W tiles 0..WT-1, then x tiles
     constexpr int T0 = SWZ ? WT : 0;  // the first tile that goes through LDS (its LDS row: 16 (i - T0))
@@ -98,11 +113,12 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
     // Row block bk: W rows [bk WROWS, +WROWS) (GLU: and the up rows nh further) and x rows
     // [0, M): the buffer ranges zero the rows of x past M (SWZ: the same rows, as the
     // workgroup's band). Wave w takes K slice (w + bk) mod 8: neighbouring workgroups read
-    // different parts of x at any moment instead of all hitting the same L2 lines. loff: byte
-    // offsets of this lane's two 8-row halves of every tile at the slice start (SWZ weight tiles:
-    // of its two 32-column steps' blocks).
+    // different parts of x at any moment instead of all hitting the same L2 lines (XREG: slice
+    // w for every block). loff: byte offsets of this lane's two 8-row halves of every tile at
+    // the slice start (SWZ weight tiles: of its two 32-column steps' blocks).
     auto setup = [&](int bk) {
-        const int n0 = bk * WROWS, k_begin = (int)((wave + bk) % SG_WAVES) * kw;
+        const int n0 = bk * WROWS,
+                  k_begin = (int)(XREG ? wave : (wave + bk) % SG_WAVES) * kw;
         rw = make_rsrc(w + (int64_t)n0 * ws, (uint32_t)(WROWS * ws * 2));
         ru = make_rsrc(w + ((int64_t)nh + n0) * ws, (uint32_t)(GLU ? WROWS * ws * 2 : 0));
 #pragma unroll
@@ -119,6 +135,24 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
     };
     int blk = blockIdx.x;
     setup(blk);
+    // XREG: the MFMA B fragments of x over the wave's slice, xf[b][t][mt] = x row 16 mt + l16,
+    // k = 64 b + 32 t + 8 g .. + 8 of the slice (rows past M read zeros)
+    typedef sg_bf16x8 XFrag[2][MT];
+    XFrag xf[XNB];
+    if constexpr (XREG) {
+#pragma unroll
+        for (int b = 0; b < XNB; ++b)
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+                    xf[b][t][mt] = __builtin_bit_cast(
+                        sg_bf16x8, __builtin_amdgcn_raw_buffer_load_b128(
+                                       rx,
+                                       ((16 * mt + l16) * (int)xs + wave * kw + SG_BK * b +
+                                        32 * t + 8 * g) * 2,
+                                       0, 0));
+    }
 
     __shared__ __attribute__((aligned(16))) SgLds<TILES - T0, MT, NT> lds;
     uint8_t* reg = lds.t[wave];
@@ -135,26 +169,31 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
     typedef sg_u32x4 Batch[TILES][2];
     // batch b: k [64 b, 64 b + 64) of the slice; chunks past the slice (or past the last batch)
     // load out of range, i.e. zeros without a memory access
-    auto load = [&](Batch& r, int b) {
-        const bool in = SG_BK * b + 8 * lc < kw;
+    auto load = [&](Batch& r, int b, bool on = true) {  // on = false: zeros, no memory access
+        const bool in = on && SG_BK * b + 8 * lc < kw;
 #pragma unroll
-        for (int i = 0; i < TILES; ++i)
+        for (int i = 0; i < (XREG ? WT : TILES); ++i)
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 if (HALF && i < NT && h == 1) continue;
                 if (SWZ && i < WT) {  // 32-column step h of the batch: one 1 KB block
                     r[i][h] = __builtin_amdgcn_raw_buffer_load_b128(
                         i < NT ? rw : ru,
-                        SG_BK * b + 32 * h < kw ? loff[i][h] + 2048 * NT * b : -1, 0, 0);
+                        on && SG_BK * b + 32 * h < kw ? loff[i][h] + 2048 * NT * b : -1, 0,
+                        IE_SKINNY_W_AUX);
                     continue;
                 }
-                r[i][h] = __builtin_amdgcn_raw_buffer_load_b128(
-                    i < NT ? rw : (i < WT ? ru : rx), in ? loff[i][h] + 128 * b : -1, 0, 0);
+                if (i < WT)
+                    r[i][h] = __builtin_amdgcn_raw_buffer_load_b128(
+                        i < NT ? rw : ru, in ? loff[i][h] + 128 * b : -1, 0, IE_SKINNY_W_AUX);
+                else
+                    r[i][h] = __builtin_amdgcn_raw_buffer_load_b128(
+                        rx, in ? loff[i][h] + 128 * b : -1, 0, 0);
             }
     };
-    auto compute = [&](const Batch& r) {
+    auto compute = [&](const Batch& r, const XFrag& xb) {
 #pragma unroll
-        for (int i = T0; i < TILES; ++i)
+        for (int i = T0; i < (XREG ? T0 : TILES); ++i)
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 if (HALF && i < NT && h == 1) continue;  // weight rows 8..15: not stored
@@ -165,7 +204,8 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
             sg_bf16x8 f[TILES];
 #pragma unroll
             for (int i = 0; i < TILES; ++i)
-                f[i] = i < T0 ? __builtin_bit_cast(sg_bf16x8, r[i][t])
+                f[i] = i < T0   ? __builtin_bit_cast(sg_bf16x8, r[i][t])
+                       : XREG ? xb[t][i - T0]
                               : __builtin_bit_cast(sg_bf16x8,
                                                    *reinterpret_cast<const sg_u32x4*>(
                                                        rsrc + 16 * (i - T0) * SG_LROW + 64 * t));
@@ -192,31 +232,54 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
     // sched_barrier: loads under a branch make the compiler's wait counts assume the worst at the
     // join, and left alone the scheduler sinks them below the MFMAs.
     const int nb = (kw + SG_BK - 1) / SG_BK;
-    Batch ra, rb;
+    Batch ra, rb, rc, rd;  // rc, rd: XREG only
     load(ra, 0);
+    if constexpr (XREG) {  // a ring of four batches, three in flight ahead of the MFMAs
+        load(rb, 1);
+        load(rc, 2);
+    }
     for (;;) {  // once, or (LOOP) over the workgroup's row blocks
 #pragma unroll
     for (int nt = 0; nt < WT; ++nt)
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = sg_f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int b = 0; b < nb; b += 2) {
-        load(rb, b + 1);
-        __builtin_amdgcn_sched_barrier(0);
-        compute(ra);
-        load(ra, b + 2);
-        __builtin_amdgcn_sched_barrier(0);
-        compute(rb);
-    }
     const int n0 = blk * WROWS;
     const int next = blk + (int)gridDim.x;
-    if (LOOP && next < nblk) {  // the next block's first batch, in flight during the reduction
+    if constexpr (XREG) {  // nb == XNB == 4; the next block's batches follow this block's
+        static_assert(XNB == 4, "the ring holds one block's four batches");
+        const bool more = next < nblk;
+        load(rd, 3);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(ra, xf[0]);
+        setup(more ? next : blk);
+        load(ra, 0, more);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(rb, xf[1]);
+        load(rb, 1, more);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(rc, xf[2]);
+        load(rc, 2, more);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(rd, xf[3]);
+    } else {
+        for (int b = 0; b < nb; b += 2) {
+            load(rb, b + 1);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(ra, xf[0]);
+            load(ra, b + 2);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(rb, xf[0]);
+        }
+    }
+    if (LOOP && !XREG && next < nblk) {  // the next block's first batch, in flight during the reduction
         setup(next);
         load(ra, 0);
         __builtin_amdgcn_sched_barrier(0);
     }
 
     // D lane (l16, g) element i: n = n0 + 16 nt + 4g + i, m = 16 mt + l16. The waves' partial
-    // tiles are summed in wave order, one (nt, mt) tile per wave; in GLU the gate tiles go
+    // tiles are summed in wave order (XREG: in the slice order wave order gives the other forms,
+    // slice (v + blk) mod 8 at position v), one (nt, mt) tile per wave; in GLU the gate tiles go
     // through LDS first and the up tiles second, and the wave holding gate tile (nt, mt) keeps
     // its bf16-rounded values for the product with up tile (nt, mt) of the second round.
     float gate[4] = {0.f, 0.f, 0.f, 0.f};
@@ -238,9 +301,10 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
                 lds.acc[wave][nt * MT + mt][lane] = acc[round * NT + nt][mt];
         __syncthreads();
         for (int tile = wave; tile < NT * MT; tile += SG_WAVES) {
-            sg_f32x4 t = lds.acc[0][tile][lane];
+            const int rot = XREG ? blk % SG_WAVES : 0;
+            sg_f32x4 t = lds.acc[rot][tile][lane];
 #pragma unroll
-            for (int v = 1; v < SG_WAVES; ++v) t += lds.acc[v][tile][lane];
+            for (int v = 1; v < SG_WAVES; ++v) t += lds.acc[(v + rot) % SG_WAVES][tile][lane];
             const int nt = tile / MT, mt = tile % MT;
             const int m = 16 * mt + l16;
             if (NORM) {  // the row's sum of squares in wave order, then rstd (IEEE division, sqrt)
@@ -441,7 +505,9 @@ extern "C" hipError_t ie_skinny_gemm_fused(const ie_bf16* x, int64_t x_stride, i
     if (swz && !glu && mode == 0 && n_tiles > 0 && (int)grid.x > 4 * device_cu_count()) {
         // a weight of many more row blocks than CUs (the LM head): one looping workgroup per CU
         c.nblk = (int)grid.x;
-        sg_rows_mt<SG_SWZ | SG_LOOP>(mt, n_tiles, dim3((unsigned)device_cu_count()), stream, c);
+        const dim3 cus((unsigned)device_cu_count());
+        if (k == SG_XREG_K) sg_rows_mt<SG_SWZ | SG_LOOP | SG_XREG>(mt, n_tiles, cus, stream, c);
+        else sg_rows_mt<SG_SWZ | SG_LOOP>(mt, n_tiles, cus, stream, c);
     } else if (swz) {
         IE_SG_DISPATCH(SG_SWZ)
     } else {

@@ -199,17 +199,19 @@ def test_swizzled_weight_same_bits(ie, dev, mode, M):
     say(f"swizzled {mode} M={M}: bit-exact")
 
 
+@pytest.mark.parametrize("K", [2048, 1024])
 @pytest.mark.parametrize("nt", [1, 2, 4])
-def test_swizzled_wide_weight_looping_grid(ie, dev, nt):
+def test_swizzled_wide_weight_looping_grid(ie, dev, nt, K):
     """A swizzled weight of many more row blocks than CUs (81,920 rows: 1,280 to 5,120 blocks,
-    the LM head's case) runs on a grid of one looping workgroup per CU: bit for bit the
-    row-major one-block-per-workgroup result, at 32 and 17 rows."""
+    the LM head's case) runs on a grid of one looping workgroup per CU (at K = 2048 with each
+    wave's x fragments held in registers over a fixed K slice): bit for bit the row-major
+    one-block-per-workgroup result, at 32, 17 and 5 rows."""
     ops = ie.kernels.ops()
-    N, K = 81920, 2048
-    g = torch.Generator().manual_seed(600 + nt)
+    N = 81920
+    g = torch.Generator().manual_seed(600 + nt + K)
     w = (0.02 * torch.randn(N, K, generator=g)).bfloat16().to(dev)
     sw = ie.swizzle_weight(w, nt)
-    for M in (32, 17):
+    for M in (32, 17, 5):
         x = torch.randn(M, K, generator=g).bfloat16().to(dev)
         a, b = ops.skinny_matmul(x, w, nt, False), ops.skinny_matmul(x, sw, nt, True)
         torch.cuda.synchronize()
