@@ -36,8 +36,26 @@ constexpr int QP_CAL_BLOCK = 256;  // chunk rows per workgroup of the separate c
 #ifndef IE_QS_WG_PER_CU
 #define IE_QS_WG_PER_CU 4
 #endif
+// The quantizers store int8 rows and scales with the non-temporal cache policy: the cache is
+// written once here and read by later steps' attention, not by this launch (12,288-token step
+// 22.8 -> 20.4 us; config 4 level). Non-temporal loads of the bf16 rows measured slower.
+#ifndef IE_KV_NT_STORE
+#define IE_KV_NT_STORE 1
+#endif
 constexpr int QS_BLOCK = IE_QS_BLOCK;
 constexpr int QS_WG_PER_CU = IE_QS_WG_PER_CU;
+
+typedef uint32_t kv_u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void row_store8(int8_t* p, uint2 v) {
+    if constexpr (IE_KV_NT_STORE)
+        __builtin_nontemporal_store(kv_u32x2{v.x, v.y}, reinterpret_cast<kv_u32x2*>(p));
+    else
+        *reinterpret_cast<uint2*>(p) = v;
+}
+__device__ __forceinline__ void scale_store(float* p, float v) {
+    if constexpr (IE_KV_NT_STORE) __builtin_nontemporal_store(v, p);
+    else *p = v;
+}
 
 // 8 consecutive bf16 (16 bytes), packed two per word.
 struct Row8 {
@@ -150,8 +168,8 @@ __device__ __forceinline__ void quantize_store_kv_row(const uint32_t (&kw)[4],
         sk = quantize_row8(xk, qv);
         packed = pack_i8x8(qv);
     }
-    *reinterpret_cast<uint2*>(kc + col * stride_tok) = packed;
-    if (c16 == 0) ks[col] = sk;
+    row_store8(kc + col * stride_tok, packed);
+    if (c16 == 0) scale_store(ks + col, sk);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         xv[2 * j] = bf16lo(vw[j]);
@@ -163,8 +181,8 @@ __device__ __forceinline__ void quantize_store_kv_row(const uint32_t (&kw)[4],
         sv = quantize_row8(xv, qv);
         packed = pack_i8x8(qv);
     }
-    *reinterpret_cast<uint2*>(vc + col * stride_tok) = packed;
-    if (c16 == 0) vs[col] = sv;
+    row_store8(vc + col * stride_tok, packed);
+    if (c16 == 0) scale_store(vs + col, sv);
 }
 
 // The prefilling entries' chunks are cut into blocks of ROWS rows, numbered entry by entry.

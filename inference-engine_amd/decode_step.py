@@ -37,7 +37,7 @@ from .attention_layer import attention, rope_inv_freq, rope_tables
 from .kernels import (LayerKVCache, add_rms_norm, decode_attention_rope, decode_plan,
                       fold_rms_norm_weight, linear, linear_norm, linear_residual_,
                       linear_silu_mul, make_layer_cache, sample, skinny_matmul, swizzle_weight,
-                      tune_linear, use_skinny, use_skinny_glu)
+                      swizzled_tiles, tune_linear, use_skinny, use_skinny_glu)
 
 
 @dataclass(frozen=True)
@@ -116,13 +116,14 @@ class DecodeStep:
                  batch: int, device, fused: bool = False, swizzle: bool | None = None):
         """fused: fold every layer's input_norm into its qkv weight and post_norm into its
         gate_up weight, in place (the layers then serve only the fused form). swizzle (default:
-        with fused): every projection weight whose tuned skinny GEMM tile width is at least one
-        16-row tile is reordered in place into the GEMM's fragment order for that width
-        (swizzle_weight; the same result bits); the LM head gets a reordered copy of the
-        embedding."""
+        with fused): every projection weight for which tune_linear timed the skinny GEMM faster
+        on the weight in the GEMM's fragment order (swizzled_tiles: the tile width) is reordered
+        in place into that order for that width (swizzle_weight; the row-major weight's result
+        bits at that width); the LM head gets a reordered copy of the embedding."""
         self.shape, self.layers, self.embed, self.final_norm = shape, layers, embed, final_norm
         self.fused = fused
         self.swz = dict.fromkeys(("qkv", "o_proj", "gate_up", "down", "lm_head"), False)
+        self.swz_tiles = dict.fromkeys(self.swz)
         self.lm_head_w = embed
         if fused:
             for lw in layers:
@@ -131,13 +132,13 @@ class DecodeStep:
             self._zero = torch.zeros(batch, shape.model_dim, device=device, dtype=torch.bfloat16)
             if swizzle is None or swizzle:
                 lw = layers[0]
-                key = lambda w: (w.shape[0], w.shape[1], batch)
-                nt = {name: use_skinny.get(key(getattr(lw, name)))
-                      for name in ("qkv", "o_proj", "down")}
-                nt["gate_up"] = use_skinny_glu.get(key(lw.gate_up))
-                nt["lm_head"] = use_skinny.get(key(embed))
+                tiles = lambda w, glu=False: swizzled_tiles(w.shape[0], w.shape[1], batch, glu)
+                nt = {name: tiles(getattr(lw, name)) for name in ("qkv", "o_proj", "down")}
+                nt["gate_up"] = tiles(lw.gate_up, True)
+                nt["lm_head"] = tiles(embed)
+                self.swz_tiles = nt
                 for name, t in nt.items():
-                    self.swz[name] = t not in (None, 0)
+                    self.swz[name] = t is not None
                 for lw in layers:
                     for name in ("qkv", "o_proj", "gate_up", "down"):
                         if self.swz[name]:
@@ -192,7 +193,7 @@ class DecodeStep:
         with nvtx.range("lm_head"):
             if self.swz["lm_head"]:
                 V, H = self.embed.shape
-                logits = skinny_matmul(h, self.lm_head_w, use_skinny[(V, H, self.B)],
+                logits = skinny_matmul(h, self.lm_head_w, self.swz_tiles["lm_head"],
                                        swizzled=True)
             else:
                 logits = linear(h, self.embed)

@@ -273,6 +273,17 @@ use_skinny: dict = {}
 # (N, K, M) -> n_tiles of the fused gate/up + SiLU-gated launch, timed by tune_linear beside the
 # plain choice (the fused launch's best tile width can differ from the plain GEMM's).
 use_skinny_glu: dict = {}
+# (N, K, M) -> n_tiles of the skinny GEMM on the weight reordered by swizzle_weight for that
+# width, where tune_linear timed it faster than the row-major choice; None: keep the weight
+# row-major. The _glu table holds the same for the fused gate/up launch.
+use_skinny_swz: dict = {}
+use_skinny_glu_swz: dict = {}
+
+
+def swizzled_tiles(N: int, K: int, M: int, silu_mul: bool = False):
+    """The tile width to reorder an [N, K] weight for (swizzle_weight) and to run it with at M
+    rows, or None where the row-major weight is the faster or nothing was tuned."""
+    return (use_skinny_glu_swz if silu_mul else use_skinny_swz).get((N, K, M))
 
 
 def skinny_matmul_silu_mul(x: torch.Tensor, weight: torch.Tensor, n_tiles: int = 1,
@@ -326,11 +337,13 @@ def linear_norm(h: torch.Tensor, weight_folded: torch.Tensor, eps: float,
     key = (N, K, M)
     if silu_mul:
         nt = _skinny_tiles(use_skinny_glu, key, 1)
+        if swizzled:
+            nt = swizzled_tiles(N, K, M, True) or nt
         assert (N // 2) % (16 * nt) == 0 and K % 256 == 0
     else:
         nt = _skinny_tiles(use_skinny, key, 1)
         if swizzled:
-            nt = max(nt, 1)
+            nt = swizzled_tiles(N, K, M) or max(nt, 1)
         assert N % (16 * max(1, nt)) == 0 and K % 256 == 0
     return ops().skinny_matmul_norm(h, weight_folded, int(nt), bool(silu_mul), float(eps),
                                     bool(swizzled))
@@ -347,7 +360,7 @@ def linear_residual_(x: torch.Tensor, weight: torch.Tensor, residual: torch.Tens
     assert residual.shape == (M, N) and residual.stride(-1) == 1
     nt = _skinny_tiles(use_skinny, (N, K, M), 1)
     if swizzled:
-        nt = max(nt, 1)
+        nt = swizzled_tiles(N, K, M) or max(nt, 1)
     assert N % (16 * max(1, nt)) == 0 and K % 256 == 0
     return ops().skinny_matmul_residual_(x, weight, int(nt), residual, bool(swizzled))
 
@@ -369,7 +382,9 @@ def tune_linear(weights: list, rows: list, calls: int = 20) -> None:
     exceed the 256 MB last-level cache, so the weights come from HBM as every layer's do in a
     step (the reference clears the cache before each timing for the same reason). Where the
     skinny kernel wins and N allows it, the fused gate/up + SiLU-gated launch is timed at each
-    tile width as well, for linear_silu_mul."""
+    tile width as well, for linear_silu_mul; and both forms on the weight reordered by
+    swizzle_weight at each width, recorded (use_skinny_swz, use_skinny_glu_swz) where faster than
+    the row-major choice."""
     for weight in weights:
         N, K = weight.shape
         todo = [M for M in rows if M <= 64 and (N, K, M) not in use_skinny]
@@ -379,7 +394,7 @@ def tune_linear(weights: list, rows: list, calls: int = 20) -> None:
         copies = [weight] + [weight.clone() for _ in range(max(0, -(-(512 << 20) // nbytes) - 1))]
         for M in todo:
             x = torch.randn(M, K, device=weight.device, dtype=weight.dtype)
-            cycle = lambda f: [lambda w=w: f(w) for w in copies] * max(1, calls // len(copies))
+            cycle = lambda f, ws=copies: [lambda w=w: f(w) for w in ws] * max(1, calls // len(ws))
             lib = _graph_time(cycle(lambda w: torch.nn.functional.linear(x, w)))
             best, choice = 0.98 * lib, None
             if K % 256 == 0:
@@ -390,10 +405,28 @@ def tune_linear(weights: list, rows: list, calls: int = 20) -> None:
                     if t < best:
                         best, choice = t, nt
             use_skinny[(N, K, M)] = choice
+            glu = {}
             if choice is not None and N % 64 == 0:
                 glu = {nt: _graph_time(cycle(lambda w, nt=nt: skinny_matmul_silu_mul(x, w, nt)))
                        for nt in (1, 2) if (N // 2) % (16 * nt) == 0}
                 use_skinny_glu[(N, K, M)] = min(glu, key=glu.get)
+            if choice is None:
+                continue
+            mt = -(-M // 16)  # the reordered weight's width cannot be lowered to fit the LDS
+            swz, swz_glu = {}, {}
+            for nt in (1, 2, 4):
+                if N % (16 * nt) or nt + mt > 6:
+                    continue
+                sw = [swizzle_weight(w, nt) for w in copies]
+                swz[nt] = _graph_time(cycle(lambda w, nt=nt: skinny_matmul(x, w, nt, True), sw))
+                if nt in glu and 2 * nt + mt <= 6:
+                    swz_glu[nt] = _graph_time(
+                        cycle(lambda w, nt=nt: skinny_matmul_silu_mul(x, w, nt, True), sw))
+                del sw
+            pick = lambda t, ref: (min(t, key=t.get) if t and min(t.values()) < ref else None)
+            use_skinny_swz[(N, K, M)] = pick(swz, best)
+            if glu:
+                use_skinny_glu_swz[(N, K, M)] = pick(swz_glu, min(glu.values()))
         del copies
 
 

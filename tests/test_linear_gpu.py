@@ -50,19 +50,26 @@ def test_linear_follows_tuning_table(ie, dev):
     g = torch.Generator().manual_seed(2)
     w = (0.02 * torch.randn(4096, 2048, generator=g)).bfloat16().to(dev)
     K = ie.kernels
-    K.use_skinny.clear()
-    K.use_skinny_glu.clear()
+    tables = (K.use_skinny, K.use_skinny_glu, K.use_skinny_swz, K.use_skinny_glu_swz)
+    for t in tables:
+        t.clear()
     K.tune_linear([w], [8, 32, 100])
     assert (4096, 2048, 100) not in K.use_skinny  # > 64 rows: always the library
     assert K.use_skinny[(4096, 2048, 8)] in (None, 0, 1, 2, 4)
     if K.use_skinny[(4096, 2048, 8)] is not None:
         assert K.use_skinny_glu[(4096, 2048, 8)] in (1, 2)
-    say(f"tuned: {K.use_skinny}")
+        assert K.swizzled_tiles(4096, 2048, 8) in (None, 1, 2, 4)
+        assert K.swizzled_tiles(4096, 2048, 8, True) in (None, 1, 2)
+    say(f"tuned: {K.use_skinny} swizzled: {K.use_skinny_swz} {K.use_skinny_glu_swz}")
     for M in (8, 32, 100):
         x = torch.randn(M, 2048, generator=g).bfloat16().to(dev)
         _check(K.linear(x, w), x, w, f"linear M={M}")
-    K.use_skinny.clear()
-    K.use_skinny_glu.clear()
+        nt = K.swizzled_tiles(4096, 2048, M)
+        if nt is not None:  # the reordered weight at the width tuned for it
+            sw = K.swizzle_weight(w, nt)
+            _check(K.skinny_matmul(x, sw, nt, swizzled=True), x, w, f"swizzled M={M} nt={nt}")
+    for t in tables:
+        t.clear()
 
 
 def _check_glu(y, x, w, what):
