@@ -513,7 +513,10 @@ hipError_t ie_skinny_gemm_silu_mul(const ie_bf16* x, int64_t x_stride, int32_t m
  *   | IE_SKINNY_SWIZZLED (with any of the above) weight is the output of
  *                     ie_skinny_weight_swizzle for this n_tiles (1, 2 or 4; weight_stride = k;
  *                     an n_tiles too wide for m is an error, not lowered): the same results, bit
- *                     for bit, as the row-major weight with the same n_tiles.
+ *                     for bit, as the row-major weight with the same n_tiles; with
+ *                     IE_SKINNY_SILU_MUL, the output of ie_skinny_weight_swizzle_gate_up for this
+ *                     n_tiles (1 ... 4, 8 n_tiles output columns per workgroup): for even n_tiles
+ *                     the row-major gate/up form's results at n_tiles / 2, bit for bit.
  * Sizes, strides and n_tiles as for the plain or the gate/up form. The sum of squares is taken
  * from the bf16 rows of x over all k columns (eight partial sums combined in a fixed order).
  */
@@ -540,6 +543,18 @@ hipError_t ie_skinny_gemm_fused(const ie_bf16* x, int64_t x_stride, int32_t m,
 hipError_t ie_skinny_weight_swizzle(const ie_bf16* weight, int64_t weight_stride, int32_t n,
                                     int32_t k, int32_t n_tiles, ie_bf16* out,
                                     hipStream_t stream);
+
+/*
+ * The gate/up weight of ie_skinny_gemm_silu_mul (n / 2 gate rows, then the n / 2 up rows) in the
+ * order of ie_skinny_weight_swizzle after pairing its rows (no counterpart in the reference):
+ * 16-row group R holds gate rows 8 R .. 8 R + 7, then up rows n / 2 + 8 R .. n / 2 + 8 R + 7, so
+ * one MFMA tile yields 8 gate sums and their 8 up sums. For ie_skinny_gemm_fused with
+ * IE_SKINNY_SILU_MUL | IE_SKINNY_SWIZZLED and the same n_tiles (1, 2, 3 or 4; n a multiple of
+ * 16 n_tiles, k of 32).
+ */
+hipError_t ie_skinny_weight_swizzle_gate_up(const ie_bf16* weight, int64_t weight_stride,
+                                            int32_t n, int32_t k, int32_t n_tiles, ie_bf16* out,
+                                            hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -59,7 +59,11 @@ constexpr int SG_MAX_TILES = 6;
 // NT groups of each workgroup's 16 NT rows interleaved step by step; a wave reads a weight
 // fragment as one contiguous 1 KB load, straight into its registers (no LDS round trip for the
 // weight; the same fragments, so the same sums, as the row-major form), a workgroup reads only
-// its own contiguous rows, and its NT tiles of one step are neighbours in memory;
+// its own contiguous rows, and its NT tiles of one step are neighbours in memory; with GLU, the
+// gate/up weight in the paired order of skinny_weight_swizzle_kernel (16-row tile T = gate rows
+// [8 T, +8) then the matching up rows): each MFMA tile yields 8 gate and their 8 up sums, the
+// product needs one lane exchange instead of a second reduction round, and a workgroup writes
+// 8 NT output columns (NT = 3 gives Qwen3-1.7B's 6144 columns one workgroup per CU);
 // LOOP, the grid is one workgroup per CU and each loops over the row blocks b, b + grid, ...,
 // the next block's first batch in flight during the current block's reduction (for weights of
 // many more blocks than CUs: the LM head), each block summed exactly as its own workgroup would;
@@ -91,10 +95,11 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
     constexpr bool HALF = MODE & SG_HALF, GLU = MODE & SG_GLU, NORM = MODE & SG_NORM,
                    RES = MODE & SG_RES, SWZ = MODE & SG_SWZ, LOOP = MODE & SG_LOOP,
                    XREG = MODE & SG_XREG;
-    constexpr int WT = GLU ? 2 * NT : NT;  // weight tiles: NT (GLU: NT gate, then NT up tiles)
+    constexpr bool PAIR = GLU && SWZ;  // gate and up rows paired inside each 16-row tile
+    constexpr int WT = GLU && !PAIR ? 2 * NT : NT;  // weight tiles (GLU: NT gate, then NT up)
     static_assert(WT + MT <= SG_MAX_TILES, "LDS transpose region too large");
     static_assert(!HALF || NT == 1, "8-row n-tiles come one per workgroup");
-    static_assert(!GLU || NT * MT <= SG_WAVES, "GLU: at most one output tile per wave");
+    static_assert(!GLU || SWZ || NT * MT <= SG_WAVES, "GLU: at most one output tile per wave");
     static_assert(!(SWZ && HALF), "the fragment-ordered weight comes in 16-row groups");
     static_assert(!LOOP || !(GLU || NORM || RES || HALF), "the looping grid: plain launches only");
     static_assert(!XREG || (LOOP && SWZ), "x in registers: the looping grid over a swizzled weight");
@@ -120,7 +125,7 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
         const int n0 = bk * WROWS,
                   k_begin = (int)(XREG ? wave : (wave + bk) % SG_WAVES) * kw;
         rw = make_rsrc(w + (int64_t)n0 * ws, (uint32_t)(WROWS * ws * 2));
-        ru = make_rsrc(w + ((int64_t)nh + n0) * ws, (uint32_t)(GLU ? WROWS * ws * 2 : 0));
+        ru = make_rsrc(w + ((int64_t)nh + n0) * ws, (uint32_t)(GLU && !PAIR ? WROWS * ws * 2 : 0));
 #pragma unroll
         for (int i = 0; i < TILES; ++i)
 #pragma unroll
@@ -292,7 +297,7 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
         }
     }
 #pragma unroll
-    for (int round = 0; round < (GLU ? 2 : 1); ++round) {
+    for (int round = 0; round < (GLU && !PAIR ? 2 : 1); ++round) {
         __syncthreads();  // every wave is done with its transpose region / the previous round
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt)
@@ -315,7 +320,20 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
 #pragma unroll
                 for (int i = 0; i < 4; ++i) t[i] *= rstd;
             }
-            if (GLU) {
+            if (PAIR) {  // lanes g < 2 hold gate rows 4 g + i, lanes g + 2 their up rows
+#pragma clang fp contract(off)
+                float u[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    t[i] = bf16_to_f32(f32_to_bf16_rne(t[i]));
+                    u[i] = __shfl_xor(t[i], 32);
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {  // silu_mul's arithmetic: (g * (1 / (1 + e^-g))) * u
+                    const float sg = 1.0f / (1.0f + expf(-t[i]));
+                    t[i] = (t[i] * sg) * u[i];
+                }
+            } else if (GLU) {
 #pragma clang fp contract(off)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
@@ -329,8 +347,9 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
                 }
                 if (round == 0) continue;
             }
-            if (m < M && (!HALF || g < 2)) {
-                uint16_t* dst = y + (int64_t)m * ys + n0 + 16 * nt + 4 * g;
+            if (m < M && (!(HALF || PAIR) || g < 2)) {
+                uint16_t* dst = y + (int64_t)m * ys + 4 * g +
+                                (PAIR ? 8 * (blk * NT + nt) : n0 + 16 * nt);
                 if (RES) {  // bf16(residual + bf16(sum)) in fp32, as add_rms_norm adds
                     const uint2 r = *reinterpret_cast<const uint2*>(dst);
                     const uint32_t rw[2] = {r.x, r.y};
@@ -425,9 +444,34 @@ void sg_rows_mt(int mt, int n_tiles, dim3 grid, hipStream_t s, const SgCall& c) 
     }
 }
 
-// Gate/up pairs: n_tiles 1 or 2 (2 only for MT <= 2, where the LDS region holds 2 + 2 + MT tiles).
+// The swizzled gate/up weight (paired tiles): n_tiles 1 ... 4 with MT + n_tiles <= 6.
+template <int MT, int EXTRA>
+void sg_pair_nt(int n_tiles, dim3 grid, hipStream_t s, const SgCall& c) {
+    switch (n_tiles) {
+        case 1: sg_go<MT, 1, SG_GLU | EXTRA>(grid, s, c); break;
+        case 2: sg_go<MT, 2, SG_GLU | EXTRA>(grid, s, c); break;
+        case 3:
+            if constexpr (MT + 3 <= SG_MAX_TILES) sg_go<MT, 3, SG_GLU | EXTRA>(grid, s, c);
+            break;
+        default:
+            if constexpr (MT + 4 <= SG_MAX_TILES) sg_go<MT, 4, SG_GLU | EXTRA>(grid, s, c);
+            break;
+    }
+}
+
+// Gate/up pairs: n_tiles 1 or 2 (2 only for MT <= 2, where the LDS region holds 2 + 2 + MT tiles);
+// on the swizzled weight, sg_pair_nt.
 template <int EXTRA>
 void sg_glu_mt(int mt, int n_tiles, dim3 grid, hipStream_t s, const SgCall& c) {
+    if constexpr (EXTRA & SG_SWZ) {
+        switch (mt) {
+            case 1: sg_pair_nt<1, EXTRA>(n_tiles, grid, s, c); break;
+            case 2: sg_pair_nt<2, EXTRA>(n_tiles, grid, s, c); break;
+            case 3: sg_pair_nt<3, EXTRA>(n_tiles, grid, s, c); break;
+            default: sg_pair_nt<4, EXTRA>(n_tiles, grid, s, c); break;
+        }
+        return;
+    }
     switch (mt) {
         case 1:
             if (n_tiles == 2) sg_go<1, 2, SG_GLU | EXTRA>(grid, s, c);
@@ -469,24 +513,32 @@ extern "C" hipError_t ie_skinny_gemm_fused(const ie_bf16* x, int64_t x_stride, i
                res = flags & IE_SKINNY_RESIDUAL, swz = flags & IE_SKINNY_SWIZZLED;
     IE_REQUIRE(!norm || (eps >= 0.f && eps < 1e30f), "eps must be finite and >= 0");
     IE_REQUIRE(!swz || (n_tiles >= 1 && weight_stride == k),
-               "a swizzled weight takes the n_tiles (1, 2 or 4) it was swizzled for and "
-               "weight_stride k");
+               "a swizzled weight takes the n_tiles (1, 2 or 4; 1 ... 4 for the gate/up form) it "
+               "was swizzled for and weight_stride k");
+    IE_REQUIRE(n_tiles != 3 || (glu && swz),
+               "n_tiles must be 0, 1, 2 or 4 (3: only the swizzled gate/up form)");
     if (m == 0 || n == 0) return hipSuccess;
-    if (glu) {
+    if (glu && swz) {
+        IE_REQUIRE(n_tiles <= 4 && n % 2 == 0 && (n / 2) % (8 * n_tiles) == 0,
+                   "n must be even and n / 2 a multiple of 8 n_tiles (n_tiles 1 ... 4)");
+    } else if (glu) {
         IE_REQUIRE(n_tiles == 1 || n_tiles == 2, "n_tiles must be 1 or 2");
         IE_REQUIRE(n % 2 == 0 && (n / 2) % (16 * n_tiles) == 0,
                    "n must be even and n / 2 a multiple of 16 n_tiles");
     }
-    hipError_t e = skinny_check(x, x_stride, m, weight, weight_stride, n, k, n_tiles, y, y_stride);
+    hipError_t e = skinny_check(x, x_stride, m, weight, weight_stride, n, k,
+                                n_tiles == 3 ? 1 : n_tiles, y, y_stride);
     if (e != hipSuccess) return e;
     const int mt = (m + 15) / 16;
     SgCall c{(const uint16_t*)x, x_stride, m, (const uint16_t*)weight, weight_stride, k,
              (uint16_t*)y, y_stride, glu ? n / 2 : 0, eps, 0};
     dim3 grid;
-    IE_REQUIRE(!swz || (glu ? 2 * n_tiles : n_tiles) + mt <= SG_MAX_TILES,
+    IE_REQUIRE(!swz || n_tiles + mt <= SG_MAX_TILES,
                "a swizzled weight's n_tiles is too wide for this many rows (its layout depends "
                "on n_tiles, which cannot be lowered)");
-    if (glu) {
+    if (glu && swz) {  // paired tiles: 8 output columns each
+        grid = dim3((unsigned)(n / 2 / (8 * n_tiles)));
+    } else if (glu) {
         // gate and up tiles: lowered to one n-tile where m leaves too little LDS for two
         if (2 * n_tiles + mt > SG_MAX_TILES) n_tiles = 1;
         grid = dim3((unsigned)(n / 2 / (16 * n_tiles)));
@@ -520,9 +572,11 @@ extern "C" hipError_t ie_skinny_gemm_fused(const ie_bf16* x, int64_t x_stride, i
 // The fragment order of the SWZ form for n_tiles G: the 1 KB block of 16-row group R and
 // 32-column step S, at block index ((R / G) * k / 32 + S) * G + R % G, holds, at 16 bytes per
 // lane L = 16 g + r, weight row 16 R + r, columns 32 S + 8 g .. + 8. One wave per block.
+// pair: the gate/up weight (n / 2 gate rows, then the up rows) in paired order, 16-row tile R
+// holding gate rows [8 R, +8) then up rows [n / 2 + 8 R, +8).
 __global__ __launch_bounds__(256) void skinny_weight_swizzle_kernel(const uint16_t* __restrict__ w,
                                                                     int64_t ws, int n, int k,
-                                                                    int G,
+                                                                    int G, int pair,
                                                                     uint16_t* __restrict__ out) {
     const int lane = threadIdx.x & 63;
     const int64_t blk = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -530,16 +584,18 @@ __global__ __launch_bounds__(256) void skinny_weight_swizzle_kernel(const uint16
     if (blk >= (int64_t)(n / 16) * steps) return;
     const int64_t R = blk / steps, S = blk % steps;
     const int r = lane & 15, g = lane >> 4;
-    const uint4 v = *reinterpret_cast<const uint4*>(w + (16 * R + r) * ws + 32 * S + 8 * g);
+    const int64_t row = !pair ? 16 * R + r : r < 8 ? 8 * R + r : n / 2 + 8 * R + r - 8;
+    const uint4 v = *reinterpret_cast<const uint4*>(w + row * ws + 32 * S + 8 * g);
     const int64_t dst = ((R / G) * steps + S) * G + R % G;
     *reinterpret_cast<uint4*>(out + dst * 512 + 8 * lane) = v;
 }
 
-extern "C" hipError_t ie_skinny_weight_swizzle(const ie_bf16* weight, int64_t weight_stride,
-                                               int32_t n, int32_t k, int32_t n_tiles,
-                                               ie_bf16* out, hipStream_t stream) {
+static hipError_t weight_swizzle(const ie_bf16* weight, int64_t weight_stride, int32_t n,
+                                 int32_t k, int32_t n_tiles, bool pair, ie_bf16* out,
+                                 hipStream_t stream) {
     IE_REQUIRE(n >= 0 && k >= 0, "negative sizes");
-    IE_REQUIRE(n_tiles == 1 || n_tiles == 2 || n_tiles == 4, "n_tiles must be 1, 2 or 4");
+    if (pair) IE_REQUIRE(n_tiles >= 1 && n_tiles <= 4, "n_tiles must be 1, 2, 3 or 4");
+    else IE_REQUIRE(n_tiles == 1 || n_tiles == 2 || n_tiles == 4, "n_tiles must be 1, 2 or 4");
     if (n == 0 || k == 0) return hipSuccess;
     IE_REQUIRE(weight && out, "null pointer");
     IE_REQUIRE(n % (16 * n_tiles) == 0 && k % 32 == 0,
@@ -551,8 +607,21 @@ extern "C" hipError_t ie_skinny_weight_swizzle(const ie_bf16* weight, int64_t we
     const int64_t blocks = (int64_t)(n / 16) * (k / 32);
     hipLaunchKernelGGL(skinny_weight_swizzle_kernel, dim3((unsigned)((blocks + 3) / 4)),
                        dim3(256), 0, stream, (const uint16_t*)weight, weight_stride, n, k,
-                       (int)n_tiles, (uint16_t*)out);
+                       (int)n_tiles, pair ? 1 : 0, (uint16_t*)out);
     return hipGetLastError();
+}
+
+extern "C" hipError_t ie_skinny_weight_swizzle(const ie_bf16* weight, int64_t weight_stride,
+                                               int32_t n, int32_t k, int32_t n_tiles,
+                                               ie_bf16* out, hipStream_t stream) {
+    return weight_swizzle(weight, weight_stride, n, k, n_tiles, false, out, stream);
+}
+
+extern "C" hipError_t ie_skinny_weight_swizzle_gate_up(const ie_bf16* weight,
+                                                       int64_t weight_stride, int32_t n,
+                                                       int32_t k, int32_t n_tiles, ie_bf16* out,
+                                                       hipStream_t stream) {
+    return weight_swizzle(weight, weight_stride, n, k, n_tiles, true, out, stream);
 }
 
 extern "C" hipError_t ie_skinny_gemm(const ie_bf16* x, int64_t x_stride, int32_t m,

@@ -292,15 +292,16 @@ at::Tensor skinny_matmul_silu_mul(const at::Tensor& x, const at::Tensor& weight,
     return y;
 }
 
-// The weight in the skinny GEMM's fragment order for n_tiles (ie_skinny_weight_swizzle), for
-// swizzled=True calls with the same n_tiles.
-at::Tensor skinny_weight_swizzle(const at::Tensor& weight, int64_t n_tiles) {
+// The weight in the skinny GEMM's fragment order for n_tiles (ie_skinny_weight_swizzle; the
+// gate/up weight of the SiLU-gated form in paired order with gate_up,
+// ie_skinny_weight_swizzle_gate_up), for swizzled=True calls with the same n_tiles.
+at::Tensor skinny_weight_swizzle(const at::Tensor& weight, int64_t n_tiles, bool gate_up) {
     check_bf16_rows(weight, "weight", 2);
     const c10::DeviceGuard guard(weight.device());
     at::Tensor out = at::empty(weight.sizes(), weight.options());
-    ok(ie_skinny_weight_swizzle(bf(weight), weight.stride(0), (int32_t)weight.size(0),
-                                (int32_t)weight.size(1), (int32_t)n_tiles, bfm(out),
-                                stream_of(weight)),
+    auto fn = gate_up ? ie_skinny_weight_swizzle_gate_up : ie_skinny_weight_swizzle;
+    ok(fn(bf(weight), weight.stride(0), (int32_t)weight.size(0), (int32_t)weight.size(1),
+          (int32_t)n_tiles, bfm(out), stream_of(weight)),
        "skinny_weight_swizzle");
     return out;
 }
@@ -679,7 +680,7 @@ TORCH_LIBRARY(ie, m) {
     m.def(
         "skinny_matmul_residual_(Tensor x, Tensor weight, int n_tiles, Tensor(a!) residual, "
         "bool swizzled=False) -> Tensor(a!)");
-    m.def("skinny_weight_swizzle(Tensor weight, int n_tiles) -> Tensor");
+    m.def("skinny_weight_swizzle(Tensor weight, int n_tiles, bool gate_up=False) -> Tensor");
     m.def(
         "decode_attention(Tensor q, Tensor k_cache, Tensor v_cache, Tensor k_scale, "
         "Tensor v_scale, Tensor k_calibration, Tensor cached_lens, Tensor slot_ids, "

@@ -142,7 +142,8 @@ class DecodeStep:
                 for lw in layers:
                     for name in ("qkv", "o_proj", "gate_up", "down"):
                         if self.swz[name]:
-                            setattr(lw, name, swizzle_weight(getattr(lw, name), nt[name]))
+                            setattr(lw, name, swizzle_weight(getattr(lw, name), nt[name],
+                                                             gate_up=name == "gate_up"))
                 if self.swz["lm_head"]:
                     self.lm_head_w = swizzle_weight(embed, nt["lm_head"])
         self.caches = caches

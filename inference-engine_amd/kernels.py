@@ -255,15 +255,18 @@ def skinny_matmul(x: torch.Tensor, weight: torch.Tensor, n_tiles: int = 1,
     return ops().skinny_matmul(x, weight, int(n_tiles), bool(swizzled))
 
 
-def swizzle_weight(weight: torch.Tensor, n_tiles: int) -> torch.Tensor:
+def swizzle_weight(weight: torch.Tensor, n_tiles: int, gate_up: bool = False) -> torch.Tensor:
     """The weight in the skinny GEMM's fragment order for tile width n_tiles (1, 2 or 4;
     ie_skinny_weight_swizzle: 1 KB blocks of 16 rows x 32 columns that a wave loads whole,
     straight into MFMA operand registers, each workgroup's n_tiles row groups interleaved step by
-    step). Reordered once at load; the GEMMs then take it with swizzled=True and the same
-    n_tiles (the tuned one, from the tables tune_linear fills). [N, K] like the weight (N a
-    multiple of 16 n_tiles, K of 32), only for the skinny GEMM."""
-    assert n_tiles in (1, 2, 4)
-    return ops().skinny_weight_swizzle(weight, int(n_tiles))
+    step). gate_up: the [gate; up] weight of the SiLU-gated form, its rows paired first (16-row
+    tile R = gate rows 8R.. and the matching up rows; ie_skinny_weight_swizzle_gate_up; n_tiles
+    1 ... 4, 8 n_tiles output columns per workgroup). Reordered once at load; the GEMMs then take
+    it with swizzled=True and the same n_tiles (the tuned one, from the tables tune_linear
+    fills). [N, K] like the weight (N a multiple of 16 n_tiles, K of 32), only for the skinny
+    GEMM."""
+    assert n_tiles in ((1, 2, 3, 4) if gate_up else (1, 2, 4))
+    return ops().skinny_weight_swizzle(weight, int(n_tiles), bool(gate_up))
 
 
 # (N, K, M) -> the n_tiles of skinny_matmul when it beat the library GEMM for that weight shape
@@ -275,7 +278,8 @@ use_skinny: dict = {}
 use_skinny_glu: dict = {}
 # (N, K, M) -> n_tiles of the skinny GEMM on the weight reordered by swizzle_weight for that
 # width, where tune_linear timed it faster than the row-major choice; None: keep the weight
-# row-major. The _glu table holds the same for the fused gate/up launch.
+# row-major. The _glu table holds the same for the fused gate/up launch on the weight reordered
+# with gate_up=True (paired tiles of 8 output columns).
 use_skinny_swz: dict = {}
 use_skinny_glu_swz: dict = {}
 
@@ -293,8 +297,11 @@ def skinny_matmul_silu_mul(x: torch.Tensor, weight: torch.Tensor, n_tiles: int =
     M, K = x.shape
     N = weight.shape[0]
     assert x.stride(-1) == 1 and weight.stride(-1) == 1
-    assert M <= 64 and N % 2 == 0 and n_tiles in (1, 2)
-    assert (N // 2) % (16 * n_tiles) == 0 and K % 256 == 0
+    assert M <= 64 and N % 2 == 0
+    if swizzled:  # swizzle_weight(..., gate_up=True): 8 n_tiles output columns per workgroup
+        assert n_tiles in (1, 2, 3, 4) and (N // 2) % (8 * n_tiles) == 0 and K % 256 == 0
+    else:
+        assert n_tiles in (1, 2) and (N // 2) % (16 * n_tiles) == 0 and K % 256 == 0
     return ops().skinny_matmul_silu_mul(x, weight, int(n_tiles), bool(swizzled))
 
 
@@ -329,17 +336,20 @@ def linear_norm(h: torch.Tensor, weight_folded: torch.Tensor, eps: float,
     IE_SKINNY_NORM): weight_folded = fold_rms_norm_weight(W, g). The rows' sums of squares come
     from the GEMM's own reads of h, so the RMSNorm costs no launch (the reference runs
     add_rms_norm, kernels.py:1260-1283, before each such projection, architecture.py:280-300).
-    M <= 64 rows; the tile width is the one tune_linear chose for the weight's shape (at least
-    one 16-row tile for a swizzled weight, swizzle_weight of the folded weight)."""
+    M <= 64 rows; the tile width is the one tune_linear chose for the weight's shape (for a
+    swizzled weight, swizzle_weight of the folded weight at swizzled_tiles' width, with gate_up
+    for the SiLU-gated form)."""
     M, K = h.shape
     N = weight_folded.shape[0]
     assert h.stride(-1) == 1 and weight_folded.stride(-1) == 1 and M <= 64
     key = (N, K, M)
     if silu_mul:
         nt = _skinny_tiles(use_skinny_glu, key, 1)
-        if swizzled:
-            nt = swizzled_tiles(N, K, M, True) or nt
-        assert (N // 2) % (16 * nt) == 0 and K % 256 == 0
+        if swizzled:  # paired tiles of 8 output columns: twice the row-major width
+            nt = swizzled_tiles(N, K, M, True) or 2 * nt
+            assert (N // 2) % (8 * nt) == 0 and K % 256 == 0
+        else:
+            assert (N // 2) % (16 * nt) == 0 and K % 256 == 0
     else:
         nt = _skinny_tiles(use_skinny, key, 1)
         if swizzled:
@@ -419,9 +429,13 @@ def tune_linear(weights: list, rows: list, calls: int = 20) -> None:
                     continue
                 sw = [swizzle_weight(w, nt) for w in copies]
                 swz[nt] = _graph_time(cycle(lambda w, nt=nt: skinny_matmul(x, w, nt, True), sw))
-                if nt in glu and 2 * nt + mt <= 6:
-                    swz_glu[nt] = _graph_time(
-                        cycle(lambda w, nt=nt: skinny_matmul_silu_mul(x, w, nt, True), sw))
+                del sw
+            for nt in ((1, 2, 3, 4) if glu else ()):  # paired gate/up tiles
+                if (N // 2) % (8 * nt) or nt + mt > 6:
+                    continue
+                sw = [swizzle_weight(w, nt, gate_up=True) for w in copies]
+                swz_glu[nt] = _graph_time(
+                    cycle(lambda w, nt=nt: skinny_matmul_silu_mul(x, w, nt, True), sw))
                 del sw
             pick = lambda t, ref: (min(t, key=t.get) if t and min(t.values()) < ref else None)
             use_skinny_swz[(N, K, M)] = pick(swz, best)

@@ -216,6 +216,11 @@ def test_skinny_gemm_fused_rejects_bad_flags_on_host(native):
         assert b"eps" in lib.ie_attn_last_error()
     assert call(2, n_tiles=4) == HIP_ERROR_INVALID_VALUE
     assert b"n_tiles" in lib.ie_attn_last_error()
+    for flags in (0, 2, 8, 8 | 1):  # 3 tiles: only the swizzled gate/up form
+        assert call(flags, n_tiles=3) == HIP_ERROR_INVALID_VALUE, flags
+        assert b"n_tiles" in lib.ie_attn_last_error()
+    assert call(8 | 2, n_tiles=5) == HIP_ERROR_INVALID_VALUE  # paired gate/up: 1 ... 4
+    assert b"n_tiles" in lib.ie_attn_last_error()
 
 
 def test_decode_planned_rejects_bad_plans_on_host(native):

@@ -152,17 +152,22 @@ def test_linear_wrappers_follow_tuning_table(ie, dev):
 
 
 
-@pytest.mark.parametrize("nt", [1, 2, 4])
-def test_swizzle_layout(ie, dev, nt):
+@pytest.mark.parametrize("nt,gate_up", [(1, False), (2, False), (4, False), (1, True),
+                                        (2, True), (3, True), (4, True)])
+def test_swizzle_layout(ie, dev, nt, gate_up):
     """swizzle_weight against the layout it documents, restated on the CPU: for tile width G,
     the 1 KB block of 16-row group R and 32-column step S, at block index
     ((R / G) K / 32 + S) G + R % G, holds at 16 bytes per lane 16 g + r row 16 R + r, columns
-    32 S + 8 g .. +8 (a strided source too)."""
+    32 S + 8 g .. +8 (a strided source too); gate_up: of the weight whose 16-row group R is
+    gate rows 8 R .. 8 R + 7 then up rows N / 2 + 8 R .. (the [gate; up] rows paired)."""
     N, K = 192, 256
     g = torch.Generator().manual_seed(5)
     wide = torch.randn(N, K + 64, generator=g).bfloat16()
     w = wide[:, 32:32 + K]
-    out = ie.swizzle_weight(w.to(dev), nt).cpu()
+    out = ie.swizzle_weight(w.to(dev), nt, gate_up=gate_up).cpu()
+    if gate_up:  # the paired row order, then the same layout
+        w = torch.stack([w[:N // 2].reshape(N // 16, 8, K), w[N // 2:].reshape(N // 16, 8, K)],
+                        dim=1).reshape(N, K)
     want = (w.reshape(N // (16 * nt), nt, 16, K // 32, 4, 8)  # band, R % G, r, S, g, 8
             .permute(0, 3, 1, 4, 2, 5)                         # band, S, R % G, g, r, 8
             .reshape(N, K))
@@ -173,30 +178,38 @@ def test_swizzle_layout(ie, dev, nt):
 @pytest.mark.parametrize("M", [1, 17, 32, 64])
 def test_swizzled_weight_same_bits(ie, dev, mode, M):
     """Every form of the skinny GEMM on the swizzled weight: bit for bit the row-major form's
-    result at the same tile width."""
+    result at the same tile width (the gate/up forms, whose swizzled tiles pair 8 gate with 8 up
+    rows, at half the width: the same output columns per workgroup; at odd widths, whose blocks
+    the row-major form has no counterpart for, within the bound of another summation order)."""
     ops = ie.kernels.ops()
-    N, K = (12288, 2048) if "glu" in mode else (4096, 2048)
+    glu = "glu" in mode
+    N, K = (12288, 2048) if glu else (4096, 2048)
     h, gam, w = _norm_inputs(M, K, N, 500 + M, dev)
-    for nt in ((1, 2) if "glu" in mode else (1, 2, 4)):
-        if (2 * nt if "glu" in mode else nt) + -(-M // 16) > 6:
+    for nt in ((1, 2, 3, 4) if glu else (1, 2, 4)):
+        if nt + -(-M // 16) > 6:
             continue  # too wide for this many rows: refused for a swizzled weight
-        sw = ie.swizzle_weight(w, nt)
+        sw = ie.swizzle_weight(w, nt, gate_up=glu)
+        rm = max(1, nt // 2) if glu else nt  # the row-major width with the same blocks
         if mode == "plain":
             a, b = ops.skinny_matmul(h, w, nt, False), ops.skinny_matmul(h, sw, nt, True)
         elif mode == "glu":
-            a = ops.skinny_matmul_silu_mul(h, w, nt, False)
+            a = ops.skinny_matmul_silu_mul(h, w, rm, False)
             b = ops.skinny_matmul_silu_mul(h, sw, nt, True)
         elif mode in ("norm", "norm_glu"):
-            glu = mode == "norm_glu"
-            a = ops.skinny_matmul_norm(h, w, nt, glu, EPS, False)
+            a = ops.skinny_matmul_norm(h, w, rm, glu, EPS, False)
             b = ops.skinny_matmul_norm(h, sw, nt, glu, EPS, True)
         else:
             res0 = torch.randn(M, N, device=dev).bfloat16()
             a = ops.skinny_matmul_residual_(h, w, nt, res0.clone(), False)
             b = ops.skinny_matmul_residual_(h, sw, nt, res0.clone(), True)
         torch.cuda.synchronize()
-        assert torch.equal(a, b), f"{mode} M={M} nt={nt}"
-    say(f"swizzled {mode} M={M}: bit-exact")
+        if glu and nt % 2:
+            ref = a.float()
+            bound = ref.abs() * 2 ** -7 + 2e-3 * ref.abs().max()
+            assert torch.all((b.float() - ref).abs() <= bound), f"{mode} M={M} nt={nt}"
+        else:
+            assert torch.equal(a, b), f"{mode} M={M} nt={nt}"
+    say(f"swizzled {mode} M={M}: ok")
 
 
 @pytest.mark.parametrize("K", [2048, 1024])
