@@ -69,8 +69,9 @@ constexpr int SG_MAX_TILES = 6;
 // many more blocks than CUs: the LM head), each block summed exactly as its own workgroup would;
 // XREG (with LOOP and SWZ, K = 2048): each wave keeps one K slice for every block and holds its
 // x fragments over that slice in registers, loaded once per launch, so the loop streams only
-// the weight (no x reloads, no LDS round trip); the partial tiles are summed in the slice order
-// of the one-block-per-workgroup form, so every block's result bits stay the same.
+// the weight (no x reloads, no LDS round trip), and NORM's sums of squares are taken once; the
+// partial tiles and sums of squares are summed in the slice order of the one-block-per-workgroup
+// form, so every block's result bits stay the same.
 enum : int { SG_PLAIN = 0, SG_HALF = 1, SG_GLU = 2, SG_NORM = 4, SG_RES = 8, SG_SWZ = 16,
              SG_LOOP = 32, SG_XREG = 64 };
 constexpr int SG_XREG_K = SG_WAVES * 4 * SG_BK;  // the one K of the XREG form: 4 batches a wave
@@ -101,7 +102,8 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
     static_assert(!HALF || NT == 1, "8-row n-tiles come one per workgroup");
     static_assert(!GLU || SWZ || NT * MT <= SG_WAVES, "GLU: at most one output tile per wave");
     static_assert(!(SWZ && HALF), "the fragment-ordered weight comes in 16-row groups");
-    static_assert(!LOOP || !(GLU || NORM || RES || HALF), "the looping grid: plain launches only");
+    static_assert(!LOOP || !(GLU || RES || HALF || (NORM && !XREG)),
+                  "the looping grid: plain launches (NORM: with x in registers)");
     static_assert(!XREG || (LOOP && SWZ), "x in registers: the looping grid over a swizzled weight");
     constexpr int XNB = XREG ? SG_XREG_K / SG_WAVES / SG_BK : 1;  // batches of x held per wave
     constexpr int WROWS = HALF ? 8 : 16 * NT;  // weight rows per workgroup (per half in GLU)
@@ -140,6 +142,7 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
     };
     int blk = blockIdx.x;
     setup(blk);
+    __shared__ __attribute__((aligned(16))) SgLds<TILES - T0, MT, NT> lds;
     // XREG: the MFMA B fragments of x over the wave's slice, xf[b][t][mt] = x row 16 mt + l16,
     // k = 64 b + 32 t + 8 g .. + 8 of the slice (rows past M read zeros)
     typedef sg_bf16x8 XFrag[2][MT];
@@ -157,9 +160,30 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
                                        ((16 * mt + l16) * (int)xs + wave * kw + SG_BK * b +
                                         32 * t + 8 * g) * 2,
                                        0, 0));
+        if constexpr (NORM) {  // the slice's sums of squares, in the order compute() takes them
+            float sq[MT];
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) sq[mt] = 0.f;
+#pragma unroll
+            for (int b = 0; b < XNB; ++b)
+#pragma unroll
+                for (int t = 0; t < 2; ++t)
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                        for (int j = 0; j < 8; j += 2) {
+                            const sg_bf16x2 p = {xf[b][t][mt][j], xf[b][t][mt][j + 1]};
+                            sq[mt] = __builtin_amdgcn_fdot2_f32_bf16(p, p, sq[mt], false);
+                        }
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                sq[mt] += __shfl_xor(sq[mt], 16);
+                sq[mt] += __shfl_xor(sq[mt], 32);
+                if (g == 0) lds.ss[wave][16 * mt + l16] = sq[mt];
+            }
+        }
     }
 
-    __shared__ __attribute__((aligned(16))) SgLds<TILES - T0, MT, NT> lds;
     uint8_t* reg = lds.t[wave];
     uint8_t* wdst = reg + lr * SG_LROW + 16 * lc;          // + (16 i + 8 h) rows
     const uint8_t* rsrc = reg + l16 * SG_LROW + 16 * g;   // + 16 i rows + 64 t
@@ -220,7 +244,7 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
                 for (int mt = 0; mt < MT; ++mt)
                     acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f[nt], f[WT + mt],
                                                                          acc[nt][mt], 0, 0, 0);
-            if (NORM) {
+            if (NORM && !XREG) {
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt) {
                     const sg_bf16x8 v = f[WT + mt];
@@ -288,7 +312,7 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
     // through LDS first and the up tiles second, and the wave holding gate tile (nt, mt) keeps
     // its bf16-rounded values for the product with up tile (nt, mt) of the second round.
     float gate[4] = {0.f, 0.f, 0.f, 0.f};
-    if (NORM) {  // row sums over the four g lanes (xor 16, 32: fixed order), one slot per wave
+    if (NORM && !XREG) {  // row sums over the four g lanes (xor 16, 32: fixed order), one slot per wave
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
             ss[mt] += __shfl_xor(ss[mt], 16);
@@ -313,9 +337,9 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
             const int nt = tile / MT, mt = tile % MT;
             const int m = 16 * mt + l16;
             if (NORM) {  // the row's sum of squares in wave order, then rstd (IEEE division, sqrt)
-                float s = lds.ss[0][m];
+                float s = lds.ss[rot][m];
 #pragma unroll
-                for (int v = 1; v < SG_WAVES; ++v) s += lds.ss[v][m];
+                for (int v = 1; v < SG_WAVES; ++v) s += lds.ss[(v + rot) % SG_WAVES][m];
                 const float rstd = 1.0f / sqrtf(s / (float)K + eps);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) t[i] *= rstd;
@@ -554,12 +578,17 @@ extern "C" hipError_t ie_skinny_gemm_fused(const ie_bf16* x, int64_t x_stride, i
         case SG_RES: sg_dispatch<SG_RES | SW>(false, mt, n_tiles, grid, stream, c); break; \
         default: sg_dispatch<SG_PLAIN | SW>(glu, mt, n_tiles, grid, stream, c); break;     \
     }
-    if (swz && !glu && mode == 0 && n_tiles > 0 && (int)grid.x > 4 * device_cu_count()) {
+    if (swz && !glu && (mode == 0 || (mode == SG_NORM && k == SG_XREG_K)) && n_tiles > 0 &&
+        (int)grid.x > 4 * device_cu_count()) {
         // a weight of many more row blocks than CUs (the LM head): one looping workgroup per CU
         c.nblk = (int)grid.x;
         const dim3 cus((unsigned)device_cu_count());
-        if (k == SG_XREG_K) sg_rows_mt<SG_SWZ | SG_LOOP | SG_XREG>(mt, n_tiles, cus, stream, c);
-        else sg_rows_mt<SG_SWZ | SG_LOOP>(mt, n_tiles, cus, stream, c);
+        if (mode == SG_NORM)
+            sg_rows_mt<SG_NORM | SG_SWZ | SG_LOOP | SG_XREG>(mt, n_tiles, cus, stream, c);
+        else if (k == SG_XREG_K)
+            sg_rows_mt<SG_SWZ | SG_LOOP | SG_XREG>(mt, n_tiles, cus, stream, c);
+        else
+            sg_rows_mt<SG_SWZ | SG_LOOP>(mt, n_tiles, cus, stream, c);
     } else if (swz) {
         IE_SG_DISPATCH(SG_SWZ)
     } else {

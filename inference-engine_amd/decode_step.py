@@ -144,8 +144,9 @@ class DecodeStep:
                         if self.swz[name]:
                             setattr(lw, name, swizzle_weight(getattr(lw, name), nt[name],
                                                              gate_up=name == "gate_up"))
-                if self.swz["lm_head"]:
-                    self.lm_head_w = swizzle_weight(embed, nt["lm_head"])
+                if self.swz["lm_head"]:  # the final RMSNorm's weight folded in as well
+                    self.lm_head_w = swizzle_weight(fold_rms_norm_weight(embed, final_norm),
+                                                    nt["lm_head"])
         self.caches = caches
         self.B = batch
         pool = caches[0].k.shape[0]
@@ -190,26 +191,31 @@ class DecodeStep:
 
     def forward(self) -> torch.Tensor:
         """One step: returns the greedy next token of every sequence, int64 [B, 1]."""
-        h = self.hidden()
-        with nvtx.range("lm_head"):
-            if self.swz["lm_head"]:
-                V, H = self.embed.shape
-                logits = skinny_matmul(h, self.lm_head_w, self.swz_tiles["lm_head"],
-                                       swizzled=True)
-            else:
-                logits = linear(h, self.embed)
+        logits = self.logits()
         with nvtx.range("sample"):
             return sample(logits, 0.0, self.seed)
 
-    def hidden(self) -> torch.Tensor:
-        """The step up to the final RMSNorm: bf16 [B, model_dim], the LM head's input."""
+    def logits(self) -> torch.Tensor:
+        """The step up to the LM head: bf16 [B, vocab]. With a reordered LM head weight (the
+        fused form) the final RMSNorm runs inside the LM head's launch, its weight folded into
+        that copy of the embedding."""
+        fold = self.swz["lm_head"]
+        h = self.hidden(final_norm=not fold)
+        with nvtx.range("lm_head"):
+            if fold:  # the residual stream's RMSNorm inside the GEMM (IE_SKINNY_NORM)
+                return linear_norm(h, self.lm_head_w, self.shape.eps, swizzled=True)
+            return linear(h, self.embed)
+
+    def hidden(self, final_norm: bool = True) -> torch.Tensor:
+        """The step up to the final RMSNorm: bf16 [B, model_dim], the LM head's input
+        (final_norm=False, fused form: the residual stream before that norm)."""
         # the reference's ranges (architecture.py:278-304, 379-413, 477; engine.py:216)
         with nvtx.range("embed"):
             x = F.embedding(self.ids, self.embed)
         with nvtx.range("metadata"):
             cos, sin = self._rope()
         if self.fused:
-            return self._hidden_fused(x, cos, sin)
+            return self._hidden_fused(x, cos, sin, final_norm)
         residual = None
         eps = self.shape.eps
         for li, lw in enumerate(self.layers):
@@ -227,7 +233,7 @@ class DecodeStep:
             _, h = add_rms_norm(residual, x, self.final_norm, eps)
         return h
 
-    def _hidden_fused(self, x, cos, sin):
+    def _hidden_fused(self, x, cos, sin, final_norm=True):
         """The layers in the fused form: h, the residual stream, is the embedding's output
         (a new tensor every step), updated in place by o_proj and down."""
         eps, h, s, sw = self.shape.eps, x, self.shape, self.swz
@@ -246,6 +252,8 @@ class DecodeStep:
                 with nvtx.range("mlp"):  # post_norm inside (folded into lw.gate_up)
                     act = linear_norm(h, lw.gate_up, eps, silu_mul=True, swizzled=sw["gate_up"])
                     linear_residual_(act, lw.down, h, swizzled=sw["down"])
+        if not final_norm:
+            return h
         with nvtx.range("final_norm"):  # h already holds the last down projection's sum
             _, hn = add_rms_norm(h, self._zero, self.final_norm, eps)
         return hn

@@ -130,6 +130,13 @@ def test_config5_full_size(ie, dev):
     agraph.replay()
     torch.cuda.synchronize()
     assert torch.equal(aout, att_eager), "attention-only replay differs from eager"
+    if step.swz["lm_head"]:  # the final RMSNorm inside the LM head's launch (weight folded)
+        lg = step.logits().float()
+        ref = torch.nn.functional.linear(step.hidden(), step.embed).float()
+        torch.cuda.synchronize()
+        err = (lg - ref).abs()  # the two round at different points: ~0.4 % of the magnitude
+        assert err.max() <= 2e-2 * ref.abs().max(), f"LM head max err {err.max().item():.3e}"
+        assert err.mean() <= 1e-2 * ref.abs().mean(), f"LM head mean err {err.mean().item():.3e}"
 
     # layer 0 on the step's own activations, against the oracle on sampled sequences
     pick = [0, 7, 19, 31]

@@ -218,7 +218,8 @@ def test_swizzled_wide_weight_looping_grid(ie, dev, nt, K):
     """A swizzled weight of many more row blocks than CUs (81,920 rows: 1,280 to 5,120 blocks,
     the LM head's case) runs on a grid of one looping workgroup per CU (at K = 2048 with each
     wave's x fragments held in registers over a fixed K slice): bit for bit the row-major
-    one-block-per-workgroup result, at 32, 17 and 5 rows."""
+    one-block-per-workgroup result, at 32, 17 and 5 rows, plain and (K = 2048) with the RMSNorm
+    inside."""
     ops = ie.kernels.ops()
     N = 81920
     g = torch.Generator().manual_seed(600 + nt + K)
@@ -229,3 +230,8 @@ def test_swizzled_wide_weight_looping_grid(ie, dev, nt, K):
         a, b = ops.skinny_matmul(x, w, nt, False), ops.skinny_matmul(x, sw, nt, True)
         torch.cuda.synchronize()
         assert torch.equal(a, b), f"nt={nt} M={M}"
+        # the RMSNorm form (the LM head with the final norm inside), likewise
+        a = ops.skinny_matmul_norm(x, w, nt, False, EPS, False)
+        b = ops.skinny_matmul_norm(x, sw, nt, False, EPS, True)
+        torch.cuda.synchronize()
+        assert torch.equal(a, b), f"norm nt={nt} M={M}"
