@@ -352,7 +352,9 @@ def _main():
     for _ in range(args.replays):
         graph.replay()
     torch.cuda.synchronize()
-    print(f"replayed {args.replays} steps; first tokens {out.view(-1)[:4].tolist()}", flush=True)
+    print(f"replayed {args.replays} steps; first tokens {out.view(-1)[:4].tolist()}; "
+          f"tuned skinny tile widths: row-major {use_skinny}, gate/up {use_skinny_glu}, "
+          f"reordered weights {step.swz_tiles}", flush=True)
 
 
 if __name__ == "__main__":
