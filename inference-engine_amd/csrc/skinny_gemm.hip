@@ -36,14 +36,14 @@ constexpr int SG_WAVES = 8;
 constexpr int SG_THREADS = SG_WAVES * IE_WAVE;
 constexpr int SG_BK = 64;      // k per batch: 128 bytes of a row, one 8-lane load group
 constexpr int SG_LROW = 160;   // LDS row stride (bytes)
-constexpr int SG_MAX_TILES = 6;
+constexpr int SG_MAX_TILES = 6;  // weight + x tiles, at most (LDS: 8 waves x 16 tiles' rows x 160 B)
 // Weight loads carry the non-temporal cache policy (aux bit 1, "nt"): each weight byte is read
 // once per launch, and streaming it past the caches took the LM head from 117 to 105 us and each
 // layer projection 0.2-0.9 us lower at 32 rows (x keeps the default policy: every workgroup
 // reads it).
 #ifndef IE_SKINNY_W_AUX
 #define IE_SKINNY_W_AUX 2
-#endif  // weight + x tiles, at most (LDS: 8 waves x 16 tiles' rows x 160 B)
+#endif
 
 // Launch modes (bits): plain n-tiles of 16 rows; one n-tile of 8 rows (HALF); GLU, the gate/up
 // projection with the SiLU-gated product fused: n-tile t pairs gate rows [16 NT t, +16 NT) with
