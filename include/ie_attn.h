@@ -516,7 +516,15 @@ hipError_t ie_skinny_gemm_silu_mul(const ie_bf16* x, int64_t x_stride, int32_t m
  *                     for bit, as the row-major weight with the same n_tiles; with
  *                     IE_SKINNY_SILU_MUL, the output of ie_skinny_weight_swizzle_gate_up for this
  *                     n_tiles (1 ... 4, 8 n_tiles output columns per workgroup): for even n_tiles
- *                     the row-major gate/up form's results at n_tiles / 2, bit for bit.
+ *                     the row-major gate/up form's results at n_tiles / 2, bit for bit;
+ *   | IE_SKINNY_Y_FRAGMENTS (the swizzled gate/up form; y_stride = n / 2, n / 2 a multiple of
+ *                     32) y is written in MFMA fragment order: y holds cdiv(m, 16) * 16 x n / 2
+ *                     bf16 as 1 KB blocks, block S * cdiv(m, 16) + t for column step S (columns
+ *                     32 S .. 32 S + 31) and row tile t, holding at byte 16 (16 g + r) row
+ *                     16 t + r, columns 32 S + 8 g .. 32 S + 8 g + 7 (rows past m not written);
+ *   | IE_SKINNY_X_FRAGMENTS (the plain or residual form; x_stride = k) x is in that order (the
+ *                     y of an IE_SKINNY_Y_FRAGMENTS call with the same m), read as contiguous
+ *                     1 KB blocks without the LDS round trip: the same results, bit for bit.
  * Sizes, strides and n_tiles as for the plain or the gate/up form. The sum of squares is taken
  * from the bf16 rows of x over all k columns (eight partial sums combined in a fixed order).
  */
@@ -524,6 +532,8 @@ hipError_t ie_skinny_gemm_silu_mul(const ie_bf16* x, int64_t x_stride, int32_t m
 #define IE_SKINNY_SILU_MUL 2
 #define IE_SKINNY_RESIDUAL 4
 #define IE_SKINNY_SWIZZLED 8
+#define IE_SKINNY_X_FRAGMENTS 16
+#define IE_SKINNY_Y_FRAGMENTS 32
 hipError_t ie_skinny_gemm_fused(const ie_bf16* x, int64_t x_stride, int32_t m,
                                 const ie_bf16* weight, int64_t weight_stride, int32_t n, int32_t k,
                                 int32_t n_tiles, int32_t flags, float eps, ie_bf16* y,

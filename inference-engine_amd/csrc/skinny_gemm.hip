@@ -72,8 +72,13 @@ constexpr int SG_MAX_TILES = 6;  // weight + x tiles, at most (LDS: 8 waves x 16
 // the weight (no x reloads, no LDS round trip), and NORM's sums of squares are taken once; the
 // partial tiles and sums of squares are summed in the slice order of the one-block-per-workgroup
 // form, so every block's result bits stay the same.
+// XFRAG: x comes in MFMA fragment order (1 KB block per (32-column step S, m-tile mt) at
+// block index S * MT + mt, lane (r, g)'s 16 bytes at 16 (16 g + r): row 16 mt + r, columns
+// 32 S + 8 g .. + 8), loaded straight into registers like a swizzled weight; YFRAG (paired
+// gate/up form): y is written in that order, for a next GEMM that takes it as XFRAG (the MLP's
+// down projection), rows past M not written.
 enum : int { SG_PLAIN = 0, SG_HALF = 1, SG_GLU = 2, SG_NORM = 4, SG_RES = 8, SG_SWZ = 16,
-             SG_LOOP = 32, SG_XREG = 64 };
+             SG_LOOP = 32, SG_XREG = 64, SG_XFRAG = 128, SG_YFRAG = 256 };
 constexpr int SG_XREG_K = SG_WAVES * 4 * SG_BK;  // the one K of the XREG form: 4 batches a wave
 
 template <int TT, int MT, int PT>
@@ -95,7 +100,7 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
     int K, uint16_t* __restrict__ y, int64_t ys, int nh, float eps, int nblk) {
     constexpr bool HALF = MODE & SG_HALF, GLU = MODE & SG_GLU, NORM = MODE & SG_NORM,
                    RES = MODE & SG_RES, SWZ = MODE & SG_SWZ, LOOP = MODE & SG_LOOP,
-                   XREG = MODE & SG_XREG;
+                   XREG = MODE & SG_XREG, XFRAG = MODE & SG_XFRAG, YFRAG = MODE & SG_YFRAG;
     constexpr bool PAIR = GLU && SWZ;  // gate and up rows paired inside each 16-row tile
     constexpr int WT = GLU && !PAIR ? 2 * NT : NT;  // weight tiles (GLU: NT gate, then NT up)
     static_assert(WT + MT <= SG_MAX_TILES, "LDS transpose region too large");
@@ -105,6 +110,8 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
     static_assert(!LOOP || !(GLU || RES || HALF || (NORM && !XREG)),
                   "the looping grid: plain launches (NORM: with x in registers)");
     static_assert(!XREG || (LOOP && SWZ), "x in registers: the looping grid over a swizzled weight");
+    static_assert(!XFRAG || !(XREG || LOOP), "x in fragment order: one block per workgroup");
+    static_assert(!YFRAG || PAIR, "y in fragment order: the paired gate/up form");
     constexpr int XNB = XREG ? SG_XREG_K / SG_WAVES / SG_BK : 1;  // batches of x held per wave
     constexpr int WROWS = HALF ? 8 : 16 * NT;  // weight rows per workgroup (per half in GLU)
     constexpr int TILES = WT + MT;  // W tiles 0..WT-1, then x tiles
@@ -114,7 +121,8 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
     const int l16 = lane & 15, g = lane >> 4;
     const int lr = lane >> 3, lc = lane & 7;  // load mapping: row lr of 8, 16-byte chunk lc
     const int kw = K / SG_WAVES;
-    const rsrc_t rx = make_rsrc(x, (uint32_t)(M * xs * 2));
+    const rsrc_t rx = make_rsrc(x, (uint32_t)(XFRAG ? K / 32 * MT * 1024 : M * xs * 2));
+    int kstep0 = 0;  // XFRAG: the wave's first 32-column step
     rsrc_t rw, ru;
     int loff[TILES][2];
     // Row block bk: W rows [bk WROWS, +WROWS) (GLU: and the up rows nh further) and x rows
@@ -126,6 +134,7 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
     auto setup = [&](int bk) {
         const int n0 = bk * WROWS,
                   k_begin = (int)(XREG ? wave : (wave + bk) % SG_WAVES) * kw;
+        kstep0 = k_begin / 32;
         rw = make_rsrc(w + (int64_t)n0 * ws, (uint32_t)(WROWS * ws * 2));
         ru = make_rsrc(w + ((int64_t)nh + n0) * ws, (uint32_t)(GLU && !PAIR ? WROWS * ws * 2 : 0));
 #pragma unroll
@@ -215,6 +224,13 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
                 if (i < WT)
                     r[i][h] = __builtin_amdgcn_raw_buffer_load_b128(
                         i < NT ? rw : ru, in ? loff[i][h] + 128 * b : -1, 0, IE_SKINNY_W_AUX);
+                else if (XFRAG)  // 32-column step h of the batch, m-tile i - WT: one 1 KB block
+                    r[i][h] = __builtin_amdgcn_raw_buffer_load_b128(
+                        rx,
+                        on && SG_BK * b + 32 * h < kw
+                            ? ((kstep0 + 2 * b + h) * MT + (i - WT)) * 1024 + 16 * lane
+                            : -1,
+                        0, 0);
                 else
                     r[i][h] = __builtin_amdgcn_raw_buffer_load_b128(
                         rx, in ? loff[i][h] + 128 * b : -1, 0, 0);
@@ -222,7 +238,7 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
     };
     auto compute = [&](const Batch& r, const XFrag& xb) {
 #pragma unroll
-        for (int i = T0; i < (XREG ? T0 : TILES); ++i)
+        for (int i = T0; i < (XREG ? T0 : XFRAG ? WT : TILES); ++i)
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 if (HALF && i < NT && h == 1) continue;  // weight rows 8..15: not stored
@@ -233,7 +249,7 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
             sg_bf16x8 f[TILES];
 #pragma unroll
             for (int i = 0; i < TILES; ++i)
-                f[i] = i < T0   ? __builtin_bit_cast(sg_bf16x8, r[i][t])
+                f[i] = i < T0 || (XFRAG && i >= WT) ? __builtin_bit_cast(sg_bf16x8, r[i][t])
                        : XREG ? xb[t][i - T0]
                               : __builtin_bit_cast(sg_bf16x8,
                                                    *reinterpret_cast<const sg_u32x4*>(
@@ -372,8 +388,13 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
                 if (round == 0) continue;
             }
             if (m < M && (!(HALF || PAIR) || g < 2)) {
-                uint16_t* dst = y + (int64_t)m * ys + 4 * g +
-                                (PAIR ? 8 * (blk * NT + nt) : n0 + 16 * nt);
+                // YFRAG: columns 8T + 4g .. + 4 (T = blk NT + nt) of row m are 8 bytes of lane
+                // (16 (T mod 4) + l16) in block (T / 4) MT + mt
+                const int T = blk * NT + nt;
+                uint16_t* dst = YFRAG ? y + ((int64_t)(T / 4) * MT + mt) * 512 +
+                                            8 * (16 * (T % 4) + l16) + 4 * g
+                                      : y + (int64_t)m * ys + 4 * g +
+                                            (PAIR ? 8 * T : n0 + 16 * nt);
                 if (RES) {  // bf16(residual + bf16(sum)) in fp32, as add_rms_norm adds
                     const uint2 r = *reinterpret_cast<const uint2*>(dst);
                     const uint32_t rw[2] = {r.x, r.y};
@@ -518,7 +539,7 @@ void sg_dispatch(bool glu, int mt, int n_tiles, dim3 grid, hipStream_t s, const 
             return;
         }
     }
-    sg_rows_mt<EXTRA>(mt, n_tiles, grid, s, c);
+    if constexpr (!(EXTRA & SG_YFRAG)) sg_rows_mt<EXTRA>(mt, n_tiles, grid, s, c);
 }
 
 }  // namespace
@@ -529,12 +550,19 @@ extern "C" hipError_t ie_skinny_gemm_fused(const ie_bf16* x, int64_t x_stride, i
                                            float eps, ie_bf16* y, int64_t y_stride,
                                            hipStream_t stream) {
     IE_REQUIRE(m >= 0 && n >= 0 && k >= 0, "negative sizes");
-    const int form = flags & ~IE_SKINNY_SWIZZLED;
+    const int form = flags & ~(IE_SKINNY_SWIZZLED | IE_SKINNY_X_FRAGMENTS | IE_SKINNY_Y_FRAGMENTS);
     IE_REQUIRE(form == 0 || form == IE_SKINNY_NORM || form == IE_SKINNY_SILU_MUL ||
                    form == (IE_SKINNY_NORM | IE_SKINNY_SILU_MUL) || form == IE_SKINNY_RESIDUAL,
                "flags: 0, NORM, SILU_MUL, NORM | SILU_MUL or RESIDUAL, each optionally | SWIZZLED");
     const bool norm = flags & IE_SKINNY_NORM, glu = flags & IE_SKINNY_SILU_MUL,
-               res = flags & IE_SKINNY_RESIDUAL, swz = flags & IE_SKINNY_SWIZZLED;
+               res = flags & IE_SKINNY_RESIDUAL, swz = flags & IE_SKINNY_SWIZZLED,
+               xfrag = flags & IE_SKINNY_X_FRAGMENTS;
+    IE_REQUIRE(!xfrag || ((form == 0 || form == IE_SKINNY_RESIDUAL) && x_stride == k),
+               "x in fragment order: the plain or residual form, x_stride k");
+    const bool yfrag = flags & IE_SKINNY_Y_FRAGMENTS;
+    IE_REQUIRE(!yfrag || (glu && swz && n % 64 == 0 && y_stride == n / 2),
+               "y in fragment order: the swizzled gate/up form, n / 2 a multiple of 32, "
+               "y_stride n / 2");
     IE_REQUIRE(!norm || (eps >= 0.f && eps < 1e30f), "eps must be finite and >= 0");
     IE_REQUIRE(!swz || (n_tiles >= 1 && weight_stride == k),
                "a swizzled weight takes the n_tiles (1, 2 or 4; 1 ... 4 for the gate/up form) it "
@@ -578,8 +606,19 @@ extern "C" hipError_t ie_skinny_gemm_fused(const ie_bf16* x, int64_t x_stride, i
         case SG_RES: sg_dispatch<SG_RES | SW>(false, mt, n_tiles, grid, stream, c); break; \
         default: sg_dispatch<SG_PLAIN | SW>(glu, mt, n_tiles, grid, stream, c); break;     \
     }
-    if (swz && !glu && (mode == 0 || (mode == SG_NORM && k == SG_XREG_K)) && n_tiles > 0 &&
-        (int)grid.x > 4 * device_cu_count()) {
+    if (yfrag) {
+        if (norm) sg_dispatch<SG_NORM | SG_SWZ | SG_YFRAG>(true, mt, n_tiles, grid, stream, c);
+        else sg_dispatch<SG_SWZ | SG_YFRAG>(true, mt, n_tiles, grid, stream, c);
+    } else if (xfrag) {
+        if (swz) {
+            if (res) sg_rows_mt<SG_RES | SG_SWZ | SG_XFRAG>(mt, n_tiles, grid, stream, c);
+            else sg_rows_mt<SG_SWZ | SG_XFRAG>(mt, n_tiles, grid, stream, c);
+        } else {
+            if (res) sg_rows_mt<SG_RES | SG_XFRAG>(mt, n_tiles, grid, stream, c);
+            else sg_rows_mt<SG_XFRAG>(mt, n_tiles, grid, stream, c);
+        }
+    } else if (swz && !glu && (mode == 0 || (mode == SG_NORM && k == SG_XREG_K)) && n_tiles > 0 &&
+               (int)grid.x > 4 * device_cu_count()) {
         // a weight of many more row blocks than CUs (the LM head): one looping workgroup per CU
         c.nblk = (int)grid.x;
         const dim3 cus((unsigned)device_cu_count());

@@ -307,9 +307,10 @@ at::Tensor skinny_weight_swizzle(const at::Tensor& weight, int64_t n_tiles, bool
 }
 
 // The GEMM of RMSNorm(h) with the norm weight folded into `weight` (ie_skinny_gemm_fused with
-// IE_SKINNY_NORM, and IE_SKINNY_SILU_MUL for the gate/up form).
+// IE_SKINNY_NORM, and IE_SKINNY_SILU_MUL for the gate/up form; fragments: the swizzled gate/up
+// form's output in MFMA fragment order, IE_SKINNY_Y_FRAGMENTS, [cdiv(M, 16) 16, N / 2]).
 at::Tensor skinny_matmul_norm(const at::Tensor& h, const at::Tensor& weight, int64_t n_tiles,
-                              bool silu_mul, double eps, bool swizzled) {
+                              bool silu_mul, double eps, bool swizzled, bool fragments) {
     check_bf16_rows(h, "h", 2);
     check_bf16_rows(weight, "weight", 2);
     check_swizzled(weight, swizzled);
@@ -317,33 +318,43 @@ at::Tensor skinny_matmul_norm(const at::Tensor& h, const at::Tensor& weight, int
     const int64_t M = h.size(0), K = h.size(1), N = weight.size(0);
     TORCH_CHECK(weight.size(1) == K, "ie: weight must be [N, K]");
     TORCH_CHECK(!silu_mul || N % 2 == 0, "ie: weight must hold the gate rows then the up rows");
-    at::Tensor y = at::empty({M, silu_mul ? N / 2 : N}, h.options());
+    TORCH_CHECK(!fragments || (silu_mul && swizzled),
+                "ie: fragment-order output: the swizzled gate/up form");
+    at::Tensor y = at::empty({fragments ? (M + 15) / 16 * 16 : M, silu_mul ? N / 2 : N},
+                             h.options());
     ok(ie_skinny_gemm_fused(bf(h), h.stride(0), (int32_t)M, bf(weight), weight.stride(0),
                             (int32_t)N, (int32_t)K, (int32_t)n_tiles,
                             IE_SKINNY_NORM | (silu_mul ? IE_SKINNY_SILU_MUL : 0) |
-                                (swizzled ? IE_SKINNY_SWIZZLED : 0),
+                                (swizzled ? IE_SKINNY_SWIZZLED : 0) |
+                                (fragments ? IE_SKINNY_Y_FRAGMENTS : 0),
                             (float)eps,
                             bfm(y), y.stride(0), stream_of(h)),
        "skinny_matmul_norm");
     return y;
 }
 
-// residual <- bf16(residual + bf16(x . weight^T)) in place (IE_SKINNY_RESIDUAL).
+// residual <- bf16(residual + bf16(x . weight^T)) in place (IE_SKINNY_RESIDUAL; x_fragments: x
+// is a fragment-order output of skinny_matmul_norm with the same M, IE_SKINNY_X_FRAGMENTS).
 at::Tensor skinny_matmul_residual_(const at::Tensor& x, const at::Tensor& weight, int64_t n_tiles,
-                                   at::Tensor residual, bool swizzled) {
+                                   at::Tensor residual, bool swizzled, bool x_fragments) {
     check_bf16_rows(x, "x", 2);
     check_bf16_rows(weight, "weight", 2);
     check_swizzled(weight, swizzled);
     check_bf16_rows(residual, "residual", 2);
     const c10::DeviceGuard guard(x.device());
-    const int64_t M = x.size(0), K = x.size(1), N = weight.size(0);
+    const int64_t M = residual.size(0), K = x.size(1), N = weight.size(0);
+    TORCH_CHECK(x_fragments ? x.size(0) == (M + 15) / 16 * 16 && x.is_contiguous()
+                            : x.size(0) == M,
+                "ie: x must be [M, K] ([cdiv(M, 16) 16, K] contiguous in fragment order)");
     TORCH_CHECK(weight.size(1) == K, "ie: weight must be [N, K]");
     TORCH_CHECK(residual.size(0) == M && residual.size(1) == N, "ie: residual must be [M, N]");
     TORCH_CHECK(residual.device() == x.device() && weight.device() == x.device(),
                 "ie: x, weight and residual must be on one device");
     ok(ie_skinny_gemm_fused(bf(x), x.stride(0), (int32_t)M, bf(weight), weight.stride(0),
                             (int32_t)N, (int32_t)K, (int32_t)n_tiles,
-                            IE_SKINNY_RESIDUAL | (swizzled ? IE_SKINNY_SWIZZLED : 0), 0.f,
+                            IE_SKINNY_RESIDUAL | (swizzled ? IE_SKINNY_SWIZZLED : 0) |
+                                (x_fragments ? IE_SKINNY_X_FRAGMENTS : 0),
+                            0.f,
                             bfm(residual), residual.stride(0), stream_of(x)),
        "skinny_matmul_residual_");
     return residual;
@@ -676,10 +687,10 @@ TORCH_LIBRARY(ie, m) {
         "-> Tensor");
     m.def(
         "skinny_matmul_norm(Tensor h, Tensor weight, int n_tiles, bool silu_mul, float eps, "
-        "bool swizzled=False) -> Tensor");
+        "bool swizzled=False, bool fragments=False) -> Tensor");
     m.def(
         "skinny_matmul_residual_(Tensor x, Tensor weight, int n_tiles, Tensor(a!) residual, "
-        "bool swizzled=False) -> Tensor(a!)");
+        "bool swizzled=False, bool x_fragments=False) -> Tensor(a!)");
     m.def("skinny_weight_swizzle(Tensor weight, int n_tiles, bool gate_up=False) -> Tensor");
     m.def(
         "decode_attention(Tensor q, Tensor k_cache, Tensor v_cache, Tensor k_scale, "

@@ -250,8 +250,12 @@ class DecodeStep:
                         linear_residual_(out.view(self.B, -1), lw.o_proj, h,
                                          swizzled=sw["o_proj"])
                 with nvtx.range("mlp"):  # post_norm inside (folded into lw.gate_up)
-                    act = linear_norm(h, lw.gate_up, eps, silu_mul=True, swizzled=sw["gate_up"])
-                    linear_residual_(act, lw.down, h, swizzled=sw["down"])
+                    # a paired gate/up weight writes the activation in the fragment order the
+                    # down projection reads without an LDS round trip
+                    frag = sw["gate_up"]
+                    act = linear_norm(h, lw.gate_up, eps, silu_mul=True, swizzled=frag,
+                                      fragments=frag)
+                    linear_residual_(act, lw.down, h, swizzled=sw["down"], x_fragments=frag)
         if not final_norm:
             return h
         with nvtx.range("final_norm"):  # h already holds the last down projection's sum

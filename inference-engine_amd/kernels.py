@@ -330,7 +330,8 @@ def _skinny_tiles(table: dict, key: tuple, default: int) -> int:
 
 
 def linear_norm(h: torch.Tensor, weight_folded: torch.Tensor, eps: float,
-                silu_mul: bool = False, swizzled: bool = False) -> torch.Tensor:
+                silu_mul: bool = False, swizzled: bool = False,
+                fragments: bool = False) -> torch.Tensor:
     """linear(add_rms_norm's normed output, W) (silu_mul: then silu_mul, the gate/up form) from
     the residual stream h itself, in one skinny-GEMM launch (ie_skinny_gemm_fused with
     IE_SKINNY_NORM): weight_folded = fold_rms_norm_weight(W, g). The rows' sums of squares come
@@ -338,7 +339,9 @@ def linear_norm(h: torch.Tensor, weight_folded: torch.Tensor, eps: float,
     add_rms_norm, kernels.py:1260-1283, before each such projection, architecture.py:280-300).
     M <= 64 rows; the tile width is the one tune_linear chose for the weight's shape (for a
     swizzled weight, swizzle_weight of the folded weight at swizzled_tiles' width, with gate_up
-    for the SiLU-gated form)."""
+    for the SiLU-gated form). fragments (the swizzled SiLU-gated form): the output in MFMA
+    fragment order ([cdiv(M, 16) 16, N / 2], IE_SKINNY_Y_FRAGMENTS), only for linear_residual_
+    with x_fragments=True, which reads it without an LDS round trip."""
     M, K = h.shape
     N = weight_folded.shape[0]
     assert h.stride(-1) == 1 and weight_folded.stride(-1) == 1 and M <= 64
@@ -355,16 +358,19 @@ def linear_norm(h: torch.Tensor, weight_folded: torch.Tensor, eps: float,
         if swizzled:
             nt = swizzled_tiles(N, K, M) or max(nt, 1)
         assert N % (16 * max(1, nt)) == 0 and K % 256 == 0
+    assert not fragments or (silu_mul and swizzled)
     return ops().skinny_matmul_norm(h, weight_folded, int(nt), bool(silu_mul), float(eps),
-                                    bool(swizzled))
+                                    bool(swizzled), bool(fragments))
 
 
 def linear_residual_(x: torch.Tensor, weight: torch.Tensor, residual: torch.Tensor,
-                     swizzled: bool = False) -> torch.Tensor:
+                     swizzled: bool = False, x_fragments: bool = False) -> torch.Tensor:
     """residual <- bf16(residual + linear(x, weight)) in place and returned: add_rms_norm's
     new residual for a projection's output (kernels.py:1240-1242), bit for bit, in the
-    projection's own launch (ie_skinny_gemm_fused with IE_SKINNY_RESIDUAL). M <= 64 rows."""
-    M, K = x.shape
+    projection's own launch (ie_skinny_gemm_fused with IE_SKINNY_RESIDUAL). M <= 64 rows.
+    x_fragments: x is linear_norm(..., fragments=True)'s output for the same rows (the same
+    result bits)."""
+    M, K = residual.shape[0], x.shape[1]
     N = weight.shape[0]
     assert x.stride(-1) == 1 and weight.stride(-1) == 1 and M <= 64
     assert residual.shape == (M, N) and residual.stride(-1) == 1
@@ -372,7 +378,8 @@ def linear_residual_(x: torch.Tensor, weight: torch.Tensor, residual: torch.Tens
     if swizzled:
         nt = swizzled_tiles(N, K, M) or max(nt, 1)
     assert N % (16 * max(1, nt)) == 0 and K % 256 == 0
-    return ops().skinny_matmul_residual_(x, weight, int(nt), residual, bool(swizzled))
+    return ops().skinny_matmul_residual_(x, weight, int(nt), residual, bool(swizzled),
+                                         bool(x_fragments))
 
 
 def linear(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:

@@ -193,8 +193,9 @@ def test_prefill_planned_rejects_bad_plans_on_host(native):
 
 def test_skinny_gemm_fused_rejects_bad_flags_on_host(native):
     """ie_skinny_gemm_fused: an undefined flag combination, a negative or infinite eps with
-    IE_SKINNY_NORM, the gate/up form with n_tiles 4, and a swizzled weight with 8-row tiles are
-    refused before any launch (the pointers here are never dereferenced)."""
+    IE_SKINNY_NORM, the gate/up form with n_tiles 4, a swizzled weight with 8-row tiles, 3 tiles
+    outside the swizzled gate/up form and the fragment-order flags outside the forms that take
+    them are refused before any launch (the pointers here are never dereferenced)."""
     lib = native.cabi()
     fn = lib.ie_skinny_gemm_fused
     fn.restype = ctypes.c_int
@@ -205,7 +206,7 @@ def test_skinny_gemm_fused_rejects_bad_flags_on_host(native):
         return fn(p, i64(2048), i32(32), p, i64(2048), i32(4096), i32(2048), i32(n_tiles),
                   i32(flags), f32(eps), p, i64(4096), ctypes.c_void_p(0))
 
-    for flags in (16, 1 | 4, 2 | 4, 7, 8 | 1 | 4, -1):
+    for flags in (64, 1 | 4, 2 | 4, 7, 8 | 1 | 4, -1):
         assert call(flags) == HIP_ERROR_INVALID_VALUE, flags
         assert b"flags" in lib.ie_attn_last_error()
     for flags in (8, 8 | 1, 8 | 4):  # a swizzled weight: no 8-row tiles
@@ -221,6 +222,12 @@ def test_skinny_gemm_fused_rejects_bad_flags_on_host(native):
         assert b"n_tiles" in lib.ie_attn_last_error()
     assert call(8 | 2, n_tiles=5) == HIP_ERROR_INVALID_VALUE  # paired gate/up: 1 ... 4
     assert b"n_tiles" in lib.ie_attn_last_error()
+    for flags in (32, 32 | 2, 32 | 8, 32 | 1 | 8):  # y in fragment order: swizzled gate/up only
+        assert call(flags) == HIP_ERROR_INVALID_VALUE, flags
+        assert b"fragment" in lib.ie_attn_last_error()
+    for flags in (16 | 1, 16 | 2, 16 | 8 | 2):  # x in fragment order: plain or residual only
+        assert call(flags) == HIP_ERROR_INVALID_VALUE, flags
+        assert b"fragment" in lib.ie_attn_last_error()
 
 
 def test_decode_planned_rejects_bad_plans_on_host(native):

@@ -235,3 +235,47 @@ def test_swizzled_wide_weight_looping_grid(ie, dev, nt, K):
         b = ops.skinny_matmul_norm(x, sw, nt, False, EPS, True)
         torch.cuda.synchronize()
         assert torch.equal(a, b), f"norm nt={nt} M={M}"
+
+
+@pytest.mark.parametrize("M", [1, 17, 32, 64])
+def test_fragment_order_activation(ie, dev, M):
+    """The swizzled gate/up form's output in MFMA fragment order (IE_SKINNY_Y_FRAGMENTS) against
+    the row-major output permuted on the CPU into the documented order (block S cdiv(M, 16) + t
+    for column step S and row tile t, lane 16 g + r's 8 values: row 16 t + r, columns
+    32 S + 8 g ..), bit for bit on the rows < M; and the down-projection-shaped residual GEMM
+    reading it (IE_SKINNY_X_FRAGMENTS) equal to the same GEMM on the row-major activation, bit
+    for bit, at every tile width, on the row-major and the swizzled weight."""
+    ops = ie.kernels.ops()
+    N, K = 12288, 2048
+    h, gam, w = _norm_inputs(M, K, N, 700 + M, dev)
+    mt = -(-M // 16)
+    D = N // 2
+    g = torch.Generator().manual_seed(701 + M)
+    wd = (0.02 * torch.randn(2048, D, generator=g)).bfloat16().to(dev)
+    res0 = torch.randn(M, 2048, generator=g).bfloat16().to(dev)
+    for nt in (1, 2, 3, 4):
+        if nt + mt > 6:
+            continue
+        sw = ie.swizzle_weight(w, nt, gate_up=True)
+        rm = ops.skinny_matmul_norm(h, sw, nt, True, EPS, True)
+        fr = ops.skinny_matmul_norm(h, sw, nt, True, EPS, True, True)
+        torch.cuda.synchronize()
+        assert fr.shape == (mt * 16, D)
+        pad = torch.zeros(mt * 16, D, dtype=torch.bfloat16)
+        pad[:M] = rm.cpu()
+        want = pad.view(mt, 16, D // 32, 4, 8).permute(2, 0, 3, 1, 4).reshape(-1, 8)
+        got = fr.cpu().reshape(-1, 8)
+        rows = torch.arange(mt * 16).view(mt, 16)[None, :, None, :].expand(D // 32, mt, 4, 16)
+        keep = (rows.reshape(-1) < M)  # rows past M are not written
+        assert torch.equal(got[keep].view(torch.int16), want[keep].view(torch.int16)), \
+            f"fragment order M={M} nt={nt}"
+        for dnt in (0, 1, 2):
+            for swz in ((False, True) if dnt else (False,)):
+                wdd = ie.swizzle_weight(wd, dnt) if swz else wd
+                if swz and dnt + mt > 6:
+                    continue
+                a = ops.skinny_matmul_residual_(rm, wdd, dnt, res0.clone(), swz)
+                b = ops.skinny_matmul_residual_(fr, wdd, dnt, res0.clone(), swz, True)
+                torch.cuda.synchronize()
+                assert torch.equal(a, b), f"x fragments M={M} nt={nt} down nt={dnt} swz={swz}"
+    say(f"fragment-order activation M={M}: bit-exact")
