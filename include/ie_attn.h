@@ -252,6 +252,22 @@ hipError_t ie_decode_attention_plan(const int32_t* cached_lens, const int32_t* n
                                     hipStream_t stream);
 
 /*
+ * A decode step's per-step inputs in one launch (no counterpart in the reference, which runs
+ * the embedding lookup, the RoPE table arithmetic and the attention metadata as separate
+ * kernels, architecture.py:379-413 / engine.py:216): the work list of ie_decode_attention_plan
+ * (rows, as that call writes them), the RoPE tables of ie_rope_tables for positions
+ * cached_lens[0 .. batch) (cos_out / sin_out: bf16 [batch, half_dim]), and the embedding rows
+ * x[b, :] = embed[ids[b], :] (bf16, model_dim a multiple of 8, 16-byte aligned rows; an id
+ * outside [0, vocab) gives a zero row). The same bits as the three separate calls.
+ */
+hipError_t ie_decode_step_prologue(const int32_t* cached_lens, const int32_t* num_decoding,
+                                   int32_t batch, int32_t num_units, int32_t* rows,
+                                   const float* inv_freq, int32_t half_dim, ie_bf16* cos_out,
+                                   ie_bf16* sin_out, const int64_t* ids, const ie_bf16* embed,
+                                   int64_t embed_stride, int64_t vocab, int32_t model_dim,
+                                   ie_bf16* x, int64_t x_stride, hipStream_t stream);
+
+/*
  * ie_decode_attention and ie_decode_attention_rope with their work list precomputed (no
  * counterpart in the reference): the same arguments and results, plus `plan`, the rows
  * ie_decode_attention_plan wrote for the same cached_lens and num_decoding values, batch,

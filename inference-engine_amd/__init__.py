@@ -14,6 +14,7 @@ from .kernels import (  # noqa: F401
     decode_attention,
     decode_attention_rope,
     decode_plan,
+    decode_step_prologue,
     dequantize_kv_prefix,
     fold_rms_norm_weight,
     fused_norm_rope_prefill,

@@ -773,6 +773,50 @@ __global__ __launch_bounds__(64) void decode_plan_kernel(const int32_t* __restri
     }
 }
 
+// A decode step's per-step launch (ie_decode_step_prologue): the first ngather workgroups copy
+// 512-element pieces of the embedding rows x[b] = embed[ids[b]] (zeros for an id outside
+// [0, vocab)), one 16-byte load per lane; the next nrope ones the RoPE tables of positions
+// cached_lens[0, batch) (64 entries each, rope_table_entry); the rest the work list, as
+// decode_plan_kernel writes it.
+__global__ __launch_bounds__(64) void decode_prologue_kernel(
+    const int32_t* __restrict__ cached_lens, const int32_t* __restrict__ num_decoding, int batch,
+    int target, int32_t* __restrict__ rows, const float* __restrict__ inv, int half,
+    uint16_t* __restrict__ cosv, uint16_t* __restrict__ sinv, int nrope,
+    const int64_t* __restrict__ ids, const uint16_t* __restrict__ embed, int64_t es,
+    int64_t vocab, int dim, uint16_t* __restrict__ x, int64_t xs) {
+    const int lane = threadIdx.x;
+    const int pieces = (dim + 8 * IE_WAVE - 1) / (8 * IE_WAVE);
+    const int ngather = batch * pieces;
+    int w = blockIdx.x;
+    if (w < ngather) {
+        const int b = w / pieces, c = (w % pieces) * 8 * IE_WAVE + 8 * lane;
+        if (c >= dim) return;  // dim a multiple of 8
+        const int64_t id = ids[b];
+        const bool ok = id >= 0 && id < vocab;
+        const uint4 v = ok ? *reinterpret_cast<const uint4*>(embed + id * es + c)
+                           : make_uint4(0u, 0u, 0u, 0u);
+        *reinterpret_cast<uint4*>(x + (int64_t)b * xs + c) = v;
+        return;
+    }
+    w -= ngather;
+    if (w < nrope) {
+        const int64_t i = (int64_t)w * IE_WAVE + lane;
+        if (i < (int64_t)batch * half) rope_table_entry(cached_lens, inv, i, half, cosv, sinv);
+        return;
+    }
+    w -= nrope;
+    const int raw0 = lane < batch ? cached_lens[lane] : 0;
+    const int nd = num_decoding[0];
+    const Work wk = decode_assign(cached_lens, nd, w, target, raw0);
+    if (lane == 0) {
+        int32_t* r = rows + 4 * w;
+        r[0] = wk.b;
+        r[1] = wk.split;
+        r[2] = wk.needed;
+        r[3] = wk.piece;
+    }
+}
+
 // Workspace: the arrival counts (one per sequence and KV head; zero on entry, and every call
 // leaves them zero), then fp32 partials (acc, m, l) of every (query head, work entry): one per
 // piece, since pieces never outnumber the decode launch's work entries per KV head. The count
@@ -1053,6 +1097,34 @@ extern "C" int32_t ie_decode_attention_grid(int32_t batch, int32_t num_units) {
     if (batch <= 0 || num_units <= 0) return 0;
     const int target = ie_decode_attention_target(batch, num_units);
     return batch <= target ? target : target + batch;
+}
+
+extern "C" hipError_t ie_decode_step_prologue(
+    const int32_t* cached_lens, const int32_t* num_decoding, int32_t batch, int32_t num_units,
+    int32_t* rows, const float* inv_freq, int32_t half_dim, ie_bf16* cos_out, ie_bf16* sin_out,
+    const int64_t* ids, const ie_bf16* embed, int64_t embed_stride, int64_t vocab,
+    int32_t model_dim, ie_bf16* x, int64_t x_stride, hipStream_t stream) {
+    IE_REQUIRE(batch >= 0 && num_units > 0 && half_dim > 0 && vocab > 0 && model_dim > 0,
+               "bad sizes");
+    if (batch == 0) return hipSuccess;
+    IE_REQUIRE(cached_lens && num_decoding && rows && inv_freq && cos_out && sin_out && ids &&
+                   embed && x,
+               "null pointer");
+    IE_REQUIRE(model_dim % 8 == 0 && embed_stride % 8 == 0 && x_stride % 8 == 0 &&
+                   (reinterpret_cast<uintptr_t>(embed) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(x) & 15) == 0,
+               "embedding and x rows must be 16-byte aligned, model_dim a multiple of 8");
+    const int target = ie_decode_attention_target(batch, num_units);
+    const int nplan = ie_decode_attention_grid(batch, num_units);
+    const int64_t nrope = ((int64_t)batch * half_dim + IE_WAVE - 1) / IE_WAVE;
+    const int64_t ngather = (int64_t)batch * ((model_dim + 8 * IE_WAVE - 1) / (8 * IE_WAVE));
+    IE_REQUIRE(nplan + nrope + ngather < (1LL << 31), "too many workgroups");
+    hipLaunchKernelGGL(decode_prologue_kernel, dim3((unsigned)(ngather + nrope + nplan)),
+                       dim3(IE_WAVE), 0, stream, cached_lens, num_decoding, batch, target,
+                       rows, inv_freq, (int)half_dim, (uint16_t*)cos_out, (uint16_t*)sin_out,
+                       (int)nrope, ids, (const uint16_t*)embed, embed_stride, vocab,
+                       (int)model_dim, (uint16_t*)x, x_stride);
+    return hipGetLastError();
 }
 
 extern "C" hipError_t ie_decode_attention_plan(const int32_t* cached_lens,

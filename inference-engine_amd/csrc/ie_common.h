@@ -213,6 +213,20 @@ __device__ __forceinline__ bool arrive_last(uint32_t* count, int needed) {
     return s_last != 0;
 }
 
+// One entry i = t half + j of the RoPE tables (architecture.py:382-390): the fp32 product of
+// position t and inverse frequency j, then cosf / sinf rounded to nearest even bf16 (the
+// arithmetic of PyTorch's kernels for angles = positions x inv_freq, cos, sin, cast).
+__device__ __forceinline__ void rope_table_entry(const int32_t* __restrict__ pos,
+                                                 const float* __restrict__ inv, int64_t i,
+                                                 int half, uint16_t* __restrict__ cosv,
+                                                 uint16_t* __restrict__ sinv) {
+    const int64_t t = i / half;
+    const int j = (int)(i - t * half);
+    const float a = (float)pos[t] * inv[j];  // a product alone: nothing to contract
+    cosv[i] = (uint16_t)f32_to_bf16_rne(cosf(a));
+    sinv[i] = (uint16_t)f32_to_bf16_rne(sinf(a));
+}
+
 // ---------------------------------------------------------------------------------------------
 // Host-side checks.
 // ---------------------------------------------------------------------------------------------

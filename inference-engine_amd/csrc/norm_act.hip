@@ -161,11 +161,7 @@ __global__ __launch_bounds__(256) void rope_tables_kernel(const int32_t* __restr
                                                           uint16_t* __restrict__ sinv) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= n * half) return;
-    const int64_t t = i / half;
-    const int j = (int)(i - t * half);
-    const float a = (float)pos[t] * inv[j];  // a product alone: nothing to contract
-    cosv[i] = (uint16_t)f32_to_bf16_rne(cosf(a));
-    sinv[i] = (uint16_t)f32_to_bf16_rne(sinf(a));
+    rope_table_entry(pos, inv, i, half, cosv, sinv);
 }
 
 }  // namespace ie

@@ -560,6 +560,46 @@ at::Tensor decode_plan(const at::Tensor& cached_lens, const at::Tensor& num_deco
     return rows;
 }
 
+// A decode step's per-step inputs in one launch (ie_decode_step_prologue): the embedding rows
+// of ids, the decode work list (as decode_plan) and the RoPE tables of positions cached_lens
+// (as rope_tables). Returns (x [B, D], plan, cos [B, 1, H], sin).
+std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> decode_step_prologue(
+    const at::Tensor& ids, const at::Tensor& embed, const at::Tensor& cached_lens,
+    const at::Tensor& num_decoding, int64_t num_q_heads, int64_t num_kv_heads,
+    const at::Tensor& inv_freq) {
+    check_i32(cached_lens, "cached_lens");
+    check_i32(num_decoding, "num_decoding");
+    check_bf16_rows(embed, "embed", 2);
+    check_dev(ids, "ids");
+    check_dev(inv_freq, "inv_freq");
+    TORCH_CHECK(ids.scalar_type() == at::kLong && ids.is_contiguous() &&
+                    ids.device() == cached_lens.device() && embed.device() == ids.device(),
+                "ie: ids must be contiguous int64 on the device of cached_lens and embed");
+    TORCH_CHECK(inv_freq.scalar_type() == at::kFloat && inv_freq.dim() == 1 &&
+                    inv_freq.is_contiguous() && inv_freq.device() == cached_lens.device(),
+                "ie: inv_freq must be a contiguous fp32 vector on the cached_lens' device");
+    TORCH_CHECK(num_kv_heads > 0 && num_q_heads > 0 && num_q_heads % num_kv_heads == 0 &&
+                    num_q_heads / num_kv_heads <= 16,
+                "ie: num_q_heads must be num_kv_heads times a GQA ratio of 1 to 16");
+    const c10::DeviceGuard guard(cached_lens.device());
+    const int64_t B = ids.numel(), D = embed.size(1), H = inv_freq.size(0);
+    TORCH_CHECK(cached_lens.size(0) >= B, "ie: cached_lens too short");
+    const int32_t units =
+        (int32_t)(num_kv_heads * ((num_q_heads / num_kv_heads + 1) / 2));
+    const int32_t grid = ie_decode_attention_grid((int32_t)B, units);
+    at::Tensor rows = at::empty({std::max(grid, 1), 4}, cached_lens.options());
+    auto bopt = embed.options();
+    at::Tensor x = at::empty({B, D}, bopt), c = at::empty({B, 1, H}, bopt),
+               s = at::empty({B, 1, H}, bopt);
+    ok(ie_decode_step_prologue(i32(cached_lens), i32(num_decoding), (int32_t)B, units,
+                               i32m(rows), inv_freq.data_ptr<float>(), (int32_t)H, bfm(c),
+                               bfm(s), ids.data_ptr<int64_t>(), bf(embed), embed.stride(0),
+                               embed.size(0), (int32_t)D, bfm(x), x.stride(0),
+                               stream_of(cached_lens)),
+       "decode_step_prologue");
+    return {x, rows, c, s};
+}
+
 int64_t decode_attention_workspace_size(int64_t batch, int64_t num_q_heads) {
     return (int64_t)ie_decode_attention_workspace_size((int32_t)batch, (int32_t)num_q_heads, 128);
 }
@@ -705,6 +745,9 @@ TORCH_LIBRARY(ie, m) {
     m.def(
         "decode_plan(Tensor cached_lens, Tensor num_decoding, int batch, int num_q_heads, "
         "int num_kv_heads) -> Tensor");
+    m.def(
+        "decode_step_prologue(Tensor ids, Tensor embed, Tensor cached_lens, Tensor num_decoding, "
+        "int num_q_heads, int num_kv_heads, Tensor inv_freq) -> (Tensor, Tensor, Tensor, Tensor)");
     m.def("decode_attention_workspace_size(int batch, int num_q_heads) -> int");
     m.def(
         "dequantize_kv_prefix(Tensor k_cache, Tensor v_cache, Tensor k_scale, Tensor v_scale, "
@@ -734,6 +777,7 @@ TORCH_LIBRARY_IMPL(ie, CUDA, m) {
     m.impl("skinny_matmul_silu_mul", &skinny_matmul_silu_mul);
     m.impl("skinny_matmul_norm", &skinny_matmul_norm);
     m.impl("skinny_matmul_residual_", &skinny_matmul_residual_);
+    m.impl("decode_step_prologue", &decode_step_prologue);
     m.impl("skinny_weight_swizzle", &skinny_weight_swizzle);
     m.impl("decode_attention", &decode_attention);
     m.impl("decode_attention_rope", &decode_attention_rope);

@@ -35,6 +35,7 @@ from torch.cuda import nvtx
 
 from .attention_layer import attention, rope_inv_freq, rope_tables
 from .kernels import (LayerKVCache, add_rms_norm, decode_attention_rope, decode_plan,
+                      decode_step_prologue,
                       fold_rms_norm_weight, linear, linear_norm, linear_residual_,
                       linear_silu_mul, make_layer_cache, sample, skinny_matmul, swizzle_weight,
                       swizzled_tiles, tune_linear, use_skinny, use_skinny_glu)
@@ -210,12 +211,17 @@ class DecodeStep:
         """The step up to the final RMSNorm: bf16 [B, model_dim], the LM head's input
         (final_norm=False, fused form: the residual stream before that norm)."""
         # the reference's ranges (architecture.py:278-304, 379-413, 477; engine.py:216)
+        if self.fused:  # embedding rows, RoPE tables and the decode work list: one launch
+            s = self.shape
+            with nvtx.range("embed+metadata"):
+                x, plan, cos, sin = decode_step_prologue(
+                    self.ids, self.embed, self.cached_lens, self.num_decoding, s.num_q_heads,
+                    s.num_kv_heads, self.inv_freq)
+            return self._hidden_fused(x, cos, sin, plan, final_norm)
         with nvtx.range("embed"):
             x = F.embedding(self.ids, self.embed)
         with nvtx.range("metadata"):
             cos, sin = self._rope()
-        if self.fused:
-            return self._hidden_fused(x, cos, sin, final_norm)
         residual = None
         eps = self.shape.eps
         for li, lw in enumerate(self.layers):
@@ -233,13 +239,11 @@ class DecodeStep:
             _, h = add_rms_norm(residual, x, self.final_norm, eps)
         return h
 
-    def _hidden_fused(self, x, cos, sin, final_norm=True):
+    def _hidden_fused(self, x, cos, sin, plan, final_norm=True):
         """The layers in the fused form: h, the residual stream, is the embedding's output
-        (a new tensor every step), updated in place by o_proj and down."""
-        eps, h, s, sw = self.shape.eps, x, self.shape, self.swz
-        with nvtx.range("metadata"):  # the decode launch's work list, once for every layer
-            plan = decode_plan(self.cached_lens, self.num_decoding, self.B, s.num_q_heads,
-                               s.num_kv_heads)
+        (a new tensor every step), updated in place by o_proj and down; plan, the decode
+        launch's work list, serves every layer."""
+        eps, h, sw = self.shape.eps, x, self.swz
         for li, lw in enumerate(self.layers):
             with nvtx.range("layer"):
                 with nvtx.range("attn"):

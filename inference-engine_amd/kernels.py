@@ -221,6 +221,17 @@ def decode_plan(cached_lens: torch.Tensor, num_decoding: torch.Tensor, batch: in
                              int(num_kv_heads))
 
 
+def decode_step_prologue(ids: torch.Tensor, embed: torch.Tensor, cached_lens: torch.Tensor,
+                         num_decoding: torch.Tensor, num_q_heads: int, num_kv_heads: int,
+                         inv_freq: torch.Tensor):
+    """A decode step's per-step inputs in one launch (ie_decode_step_prologue; no counterpart
+    in the reference): (x, plan, cos, sin) = (F.embedding(ids, embed), decode_plan(cached_lens,
+    num_decoding, len(ids), num_q_heads, num_kv_heads), *rope_tables(cached_lens, inv_freq)),
+    the same bits as those three calls."""
+    return ops().decode_step_prologue(ids.reshape(-1), embed, cached_lens, num_decoding,
+                                      int(num_q_heads), int(num_kv_heads), inv_freq)
+
+
 def sample(logits: torch.Tensor, tau: float, seed: torch.Tensor) -> torch.Tensor:
     """qwen3-1.7b/kernels.py:1343-1370: [B, 1] int64 tokens (Gumbel-max; greedy at tau = 0);
     increments the int64 device `seed` by one."""

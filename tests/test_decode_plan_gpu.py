@@ -136,3 +136,29 @@ def test_one_plan_two_layers_in_graph(ie, dev):
             assert torch.equal(outs[i], refs[i]), f"replay {rep} layer {i}"
             for a, b in zip(_fields(caches[i]), _fields(ref_caches[i])):
                 assert torch.equal(a, b), f"replay {rep} layer {i} cache"
+
+
+def test_step_prologue_equals_separate_calls(ie, dev):
+    """decode_step_prologue (one launch) against the three calls it replaces on the same inputs:
+    the embedding rows, decode_plan's work list and rope_tables' cos / sin, bit for bit; an id
+    outside the vocabulary gives a zero row."""
+    import torch.nn.functional as F
+    g = torch.Generator().manual_seed(81)
+    V, D, B = 1000, 256, 32
+    embed = torch.randn(V, D, generator=g).bfloat16().to(dev)
+    ids = torch.randint(0, V, (B, 1), generator=g).to(dev)
+    lens = torch.randint(1, 4096, (B,), generator=g).int().to(dev)
+    nd = torch.tensor([B - 3], dtype=torch.int32, device=dev)
+    inv = ie.attention_layer.rope_inv_freq(128, 1e6, dev)
+    x, plan, cos, sin = ie.decode_step_prologue(ids, embed, lens, nd, 16, 8, inv)
+    x0 = F.embedding(ids.view(-1), embed)
+    plan0 = ie.decode_plan(lens, nd, B, 16, 8)
+    cos0, sin0 = ie.attention_layer.rope_tables(lens, inv)
+    torch.cuda.synchronize()
+    assert torch.equal(x, x0) and torch.equal(plan, plan0)
+    assert torch.equal(cos, cos0) and torch.equal(sin, sin0)
+    bad = ids.clone()
+    bad[5, 0] = V + 7
+    xb = ie.decode_step_prologue(bad, embed, lens, nd, 16, 8, inv)[0]
+    torch.cuda.synchronize()
+    assert torch.all(xb[5] == 0) and torch.equal(xb[:5], x0[:5])
