@@ -8,8 +8,9 @@ reference's stage points, qwen3-1.7b/architecture.py:84-200 and engine.py:145-22
 
 Each kernel is attributed to the innermost range open on the host thread when its launch call
 started (the kernel record and its launch call share a correlation id); the first `--skip`
-steps (a step starts at its "embed" range) are left out. Ranges are recorded while a graph is
-captured, not when it replays, hence the eager steps. Prints a markdown table.
+steps (a step starts at its "embed" or "embed+metadata" range) are left out. Ranges are
+recorded while a graph is captured, not when it replays, hence the eager steps. Prints a
+markdown table.
 """
 
 import argparse
@@ -32,7 +33,7 @@ def report(d: str, skip: int = 1) -> str:
                 for r in _rows(d, "hip_api_trace.csv")}
     kernels = _rows(d, "kernel_trace.csv")
     ranges = [(int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Function"]) for r in marks]
-    steps = sorted(r for r in ranges if r[2] == "embed")
+    steps = sorted(r for r in ranges if r[2].startswith("embed"))
     if len(steps) <= skip:
         raise SystemExit(f"{len(steps)} steps in the trace, {skip} skipped")
     t_first, n = steps[skip][0], len(steps) - skip
