@@ -571,6 +571,25 @@ hipError_t ie_skinny_weight_swizzle(const ie_bf16* weight, int64_t weight_stride
                                     hipStream_t stream);
 
 /*
+ * The LM head and greedy sampling in one launch (no counterpart in the reference, which runs
+ * kernels.py:1451-1458 `linear` then kernels.py:1343-1370 `sample` at tau = 0): logits =
+ * ie_skinny_gemm_fused(x, weight, flags) (flags 0 or IE_SKINNY_NORM; weight swizzled for
+ * n_tiles 1, 2 or 4, k = 2048, on one looping workgroup per CU: the same logits bits as that
+ * call), tokens[r * tokens_stride] = the first column of the largest logit of row r (sample's
+ * greedy choice on these logits, NaN never chosen, 0x7fffffff for an all-NaN row), and *seed
+ * advanced by one as sample advances it. workspace: ie_skinny_lm_head_greedy_workspace_size()
+ * bytes, 16-byte aligned, zero before the first call (every call leaves it zero); calls that
+ * overlap on one workspace race. m <= 64.
+ */
+size_t ie_skinny_lm_head_greedy_workspace_size(void);
+hipError_t ie_skinny_lm_head_greedy(const ie_bf16* x, int64_t x_stride, int32_t m,
+                                    const ie_bf16* weight, int32_t n, int32_t k, int32_t n_tiles,
+                                    int32_t flags, float eps, ie_bf16* logits,
+                                    int64_t logits_stride, int64_t* tokens, int64_t tokens_stride,
+                                    int64_t* seed, void* workspace, size_t workspace_bytes,
+                                    hipStream_t stream);
+
+/*
  * The gate/up weight of ie_skinny_gemm_silu_mul (n / 2 gate rows, then the n / 2 up rows) in the
  * order of ie_skinny_weight_swizzle after pairing its rows (no counterpart in the reference):
  * 16-row group R holds gate rows 8 R .. 8 R + 7, then up rows n / 2 + 8 R .. n / 2 + 8 R + 7, so

@@ -32,5 +32,6 @@ from .kernels import (  # noqa: F401
     linear_norm,
     linear_residual_,
     linear_silu_mul,
+    lm_head_greedy,
     tune_linear,
 )

@@ -77,8 +77,36 @@ constexpr int SG_MAX_TILES = 6;  // weight + x tiles, at most (LDS: 8 waves x 16
 // 32 S + 8 g .. + 8), loaded straight into registers like a swizzled weight; YFRAG (paired
 // gate/up form): y is written in that order, for a next GEMM that takes it as XFRAG (the MLP's
 // down projection), rows past M not written.
+// AMAX (with LOOP and XREG: the LM head): also the greedy token of every row, the first column
+// of the largest bf16 output (sample's greedy rule at tau = 0: larger value, then smaller index;
+// NaN never chosen): each lane keeps its best over its blocks, each workgroup folds its lanes'
+// and counts itself into a device-scope 64-bit max per row, and the last workgroup to finish
+// writes the tokens, clears the maxima and advances the sampler's seed.
 enum : int { SG_PLAIN = 0, SG_HALF = 1, SG_GLU = 2, SG_NORM = 4, SG_RES = 8, SG_SWZ = 16,
-             SG_LOOP = 32, SG_XREG = 64, SG_XFRAG = 128, SG_YFRAG = 256 };
+             SG_LOOP = 32, SG_XREG = 64, SG_XFRAG = 128, SG_YFRAG = 256, SG_AMAX = 512 };
+
+// AMAX's outputs: per-row maxima keys[M] and a count (zero on entry, left zero), tokens (int64,
+// stride os) and the sampler's seed.
+struct SgAmax {
+    uint64_t* keys;
+    uint32_t* count;
+    int64_t* out;
+    int64_t os;
+    int64_t* seed;
+};
+
+// (value, index) ordered as the reference's greedy argmax: the larger value, then the smaller
+// index; NaN is never larger.
+__device__ __forceinline__ bool amax_better(float av, int ai, float bv, int bi) {
+    return av > bv || (av == bv && ai < bi);
+}
+// The pair as a key whose unsigned order is that order: the value's bits made monotonic (-0
+// as +0) above the inverted index.
+__device__ __forceinline__ uint64_t amax_key(float v, int i) {
+    const uint32_t u = __float_as_uint(v == 0.0f ? 0.0f : v);
+    const uint32_t o = (u >> 31) ? ~u : (u | 0x80000000u);
+    return ((uint64_t)o << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
+}
 constexpr int SG_XREG_K = SG_WAVES * 4 * SG_BK;  // the one K of the XREG form: 4 batches a wave
 
 template <int TT, int MT, int PT>
@@ -97,10 +125,11 @@ struct SgLds {
 template <int MT, int NT, int MODE>
 __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
     const uint16_t* __restrict__ x, int64_t xs, int M, const uint16_t* __restrict__ w, int64_t ws,
-    int K, uint16_t* __restrict__ y, int64_t ys, int nh, float eps, int nblk) {
+    int K, uint16_t* __restrict__ y, int64_t ys, int nh, float eps, int nblk, SgAmax am) {
     constexpr bool HALF = MODE & SG_HALF, GLU = MODE & SG_GLU, NORM = MODE & SG_NORM,
                    RES = MODE & SG_RES, SWZ = MODE & SG_SWZ, LOOP = MODE & SG_LOOP,
-                   XREG = MODE & SG_XREG, XFRAG = MODE & SG_XFRAG, YFRAG = MODE & SG_YFRAG;
+                   XREG = MODE & SG_XREG, XFRAG = MODE & SG_XFRAG, YFRAG = MODE & SG_YFRAG,
+                   AMAX = MODE & SG_AMAX;
     constexpr bool PAIR = GLU && SWZ;  // gate and up rows paired inside each 16-row tile
     constexpr int WT = GLU && !PAIR ? 2 * NT : NT;  // weight tiles (GLU: NT gate, then NT up)
     static_assert(WT + MT <= SG_MAX_TILES, "LDS transpose region too large");
@@ -112,6 +141,10 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
     static_assert(!XREG || (LOOP && SWZ), "x in registers: the looping grid over a swizzled weight");
     static_assert(!XFRAG || !(XREG || LOOP), "x in fragment order: one block per workgroup");
     static_assert(!YFRAG || PAIR, "y in fragment order: the paired gate/up form");
+    static_assert(!AMAX || (XREG && !GLU && NT * MT <= SG_WAVES),
+                  "greedy tokens: the looping LM head, one output tile per wave");
+    float abv = -INFINITY;  // AMAX: this lane's best output so far, and its column
+    int abi = 0x7fffffff;
     constexpr int XNB = XREG ? SG_XREG_K / SG_WAVES / SG_BK : 1;  // batches of x held per wave
     constexpr int WROWS = HALF ? 8 : 16 * NT;  // weight rows per workgroup (per half in GLU)
     constexpr int TILES = WT + MT;  // W tiles 0..WT-1, then x tiles
@@ -405,12 +438,66 @@ __global__ __launch_bounds__(SG_THREADS) void skinny_gemm_kernel(
                 }
                 *reinterpret_cast<uint2*>(dst) =
                     make_uint2(pack_bf16x2(t[0], t[1]), pack_bf16x2(t[2], t[3]));
+                if (AMAX) {  // the stored (bf16) values, columns in increasing order
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float v = bf16_to_f32(f32_to_bf16_rne(t[i]));
+                        const int n = n0 + 16 * nt + 4 * g + i;
+                        if (amax_better(v, n, abv, abi)) {
+                            abv = v;
+                            abi = n;
+                        }
+                    }
+                }
             }
         }
     }
     if (!LOOP || next >= nblk) break;
     __syncthreads();  // every wave is done reading the partial tiles before the next transposes
     blk = next;
+    }
+    if constexpr (AMAX) {
+        __shared__ float s_bv[SG_WAVES][16];
+        __shared__ int s_bi[SG_WAVES][16];
+#pragma unroll
+        for (int x = 16; x <= 32; x <<= 1) {  // the four g lanes of row 16 mt + l16
+            const float ov = __shfl_xor(abv, x);
+            const int oi = __shfl_xor(abi, x);
+            if (amax_better(ov, oi, abv, abi)) {
+                abv = ov;
+                abi = oi;
+            }
+        }
+        if (wave < NT * MT && g == 0) {  // wave w holds output tile w: (nt, mt) = (w / MT, w % MT)
+            s_bv[wave][l16] = abv;
+            s_bi[wave][l16] = abi;
+        }
+        __syncthreads();
+        if (tid < M) {  // row m = tid: its tiles are nt MT + m / 16
+            float v = -INFINITY;
+            int i = 0x7fffffff;
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                const int tile = nt * MT + tid / 16;
+                if (amax_better(s_bv[tile][tid % 16], s_bi[tile][tid % 16], v, i)) {
+                    v = s_bv[tile][tid % 16];
+                    i = s_bi[tile][tid % 16];
+                }
+            }
+            if (i != 0x7fffffff)  // a column was taken (any value but NaN)
+                __hip_atomic_fetch_max(am.keys + tid, amax_key(v, i), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (arrive_last(am.count, (int)(gridDim.x * gridDim.y * gridDim.z))) {
+            if (tid < M) {  // the row's largest key; 0: no column taken (every value NaN)
+                const uint64_t key = __hip_atomic_exchange(am.keys + tid, (uint64_t)0,
+                                                           __ATOMIC_RELAXED,
+                                                           __HIP_MEMORY_SCOPE_AGENT);
+                am.out[(int64_t)tid * am.os] =
+                    key ? (int64_t)(0xffffffffu - (uint32_t)key) : (int64_t)0x7fffffff;
+            }
+            if (tid == 0) am.seed[0] += 1;
+        }
     }
 }
 
@@ -454,13 +541,14 @@ struct SgCall {
     int nh;
     float eps;
     int nblk;  // row blocks (the looping grid: more than its workgroups)
+    SgAmax am;  // the greedy tokens (AMAX only)
 };
 
 template <int MT, int NT, int MODE>
 void sg_go(dim3 grid, hipStream_t s, const SgCall& c) {
     hipLaunchKernelGGL((skinny_gemm_kernel<MT, NT, MODE>), grid, dim3(SG_THREADS), 0, s, c.x,
                        c.xs, c.m, c.w, c.ws, c.k, c.y, c.ys, c.nh, c.eps,
-                       c.nblk > 0 ? c.nblk : (int)grid.x);
+                       c.nblk > 0 ? c.nblk : (int)grid.x, c.am);
 }
 
 // One weight row block per workgroup: n_tiles 0 (8 rows), 1, 2 or 4 n-tiles of 16 rows (4 only
@@ -634,6 +722,46 @@ extern "C" hipError_t ie_skinny_gemm_fused(const ie_bf16* x, int64_t x_stride, i
         IE_SG_DISPATCH(0)
     }
 #undef IE_SG_DISPATCH
+    return hipGetLastError();
+}
+
+// The LM head with the greedy tokens (AMAX): the looping form of ie_skinny_gemm_fused, plain or
+// NORM, over a weight swizzled for n_tiles, plus tokens[m] and the seed advanced by one.
+constexpr int SG_AMAX_ROWS = 64;
+extern "C" size_t ie_skinny_lm_head_greedy_workspace_size(void) {
+    return SG_AMAX_ROWS * sizeof(uint64_t) + 256;  // the row maxima, then the count
+}
+
+extern "C" hipError_t ie_skinny_lm_head_greedy(
+    const ie_bf16* x, int64_t x_stride, int32_t m, const ie_bf16* weight, int32_t n, int32_t k,
+    int32_t n_tiles, int32_t flags, float eps, ie_bf16* logits, int64_t logits_stride,
+    int64_t* tokens, int64_t tokens_stride, int64_t* seed, void* workspace,
+    size_t workspace_bytes, hipStream_t stream) {
+    IE_REQUIRE(m >= 0 && n >= 0 && k >= 0, "negative sizes");
+    IE_REQUIRE(flags == 0 || flags == IE_SKINNY_NORM, "flags: 0 or NORM");
+    IE_REQUIRE(flags == 0 || (eps >= 0.f && eps < 1e30f), "eps must be finite and >= 0");
+    IE_REQUIRE(n_tiles == 1 || n_tiles == 2 || n_tiles == 4, "n_tiles must be 1, 2 or 4");
+    if (m == 0) return hipSuccess;
+    IE_REQUIRE(n > 0 && k == SG_XREG_K, "the looping LM head form: k 2048");
+    IE_REQUIRE(tokens && seed && workspace, "null pointer");
+    IE_REQUIRE(workspace_bytes >= ie_skinny_lm_head_greedy_workspace_size() &&
+                   (reinterpret_cast<uintptr_t>(workspace) & 15) == 0,
+               "workspace too small or misaligned");
+    hipError_t e = skinny_check(x, x_stride, m, weight, k, n, k, n_tiles, logits, logits_stride);
+    if (e != hipSuccess) return e;
+    const int mt = (m + 15) / 16;
+    IE_REQUIRE(n_tiles + mt <= SG_MAX_TILES, "n_tiles too wide for this many rows");
+    SgCall c{(const uint16_t*)x, x_stride, m, (const uint16_t*)weight, k, k,
+             (uint16_t*)logits, logits_stride, 0, eps, n / (16 * n_tiles)};
+    c.am = SgAmax{reinterpret_cast<uint64_t*>(workspace),
+                  reinterpret_cast<uint32_t*>(reinterpret_cast<uint64_t*>(workspace) +
+                                              SG_AMAX_ROWS),
+                  tokens, tokens_stride, seed};
+    const dim3 grid((unsigned)std::min(c.nblk, device_cu_count()));
+    if (flags == IE_SKINNY_NORM)
+        sg_rows_mt<SG_NORM | SG_SWZ | SG_LOOP | SG_XREG | SG_AMAX>(mt, n_tiles, grid, stream, c);
+    else
+        sg_rows_mt<SG_SWZ | SG_LOOP | SG_XREG | SG_AMAX>(mt, n_tiles, grid, stream, c);
     return hipGetLastError();
 }
 

@@ -560,6 +560,35 @@ at::Tensor decode_plan(const at::Tensor& cached_lens, const at::Tensor& num_deco
     return rows;
 }
 
+// The LM head and greedy sampling in one launch (ie_skinny_lm_head_greedy): h [M, K] (the
+// residual stream with norm, else the normed rows), weight swizzled for n_tiles; returns
+// (logits [M, N], tokens [M, 1] int64) and advances seed by one, as sample does at tau 0.
+constexpr int32_t WS_LM_HEAD = -2;
+std::tuple<at::Tensor, at::Tensor> lm_head_greedy(const at::Tensor& h, const at::Tensor& weight,
+                                                  int64_t n_tiles, double eps, bool norm,
+                                                  const at::Tensor& seed) {
+    check_bf16_rows(h, "h", 2);
+    check_bf16_rows(weight, "weight", 2);
+    TORCH_CHECK(seed.is_cuda() && seed.scalar_type() == at::kLong && seed.numel() >= 1 &&
+                    seed.is_contiguous() && seed.device() == h.device() &&
+                    weight.device() == h.device(),
+                "ie: seed must be an int64 tensor on h's device, with the weight");
+    const c10::DeviceGuard guard(h.device());
+    const int64_t M = h.size(0), K = h.size(1), N = weight.size(0);
+    TORCH_CHECK(weight.size(1) == K && weight.is_contiguous(), "ie: weight must be [N, K]");
+    at::Tensor logits = at::empty({M, N}, h.options());
+    at::Tensor tokens = at::empty({M, 1}, h.options().dtype(at::kLong));
+    const size_t wsb = ie_skinny_lm_head_greedy_workspace_size();
+    at::Tensor ws = persistent_workspace(h, wsb, wsb, WS_LM_HEAD);
+    ok(ie_skinny_lm_head_greedy(bf(h), h.stride(0), (int32_t)M, bf(weight), (int32_t)N,
+                                (int32_t)K, (int32_t)n_tiles, norm ? IE_SKINNY_NORM : 0,
+                                (float)eps, bfm(logits), logits.stride(0),
+                                tokens.data_ptr<int64_t>(), tokens.stride(0),
+                                seed.data_ptr<int64_t>(), ws.data_ptr(), wsb, stream_of(h)),
+       "lm_head_greedy");
+    return {logits, tokens};
+}
+
 // A decode step's per-step inputs in one launch (ie_decode_step_prologue): the embedding rows
 // of ids, the decode work list (as decode_plan) and the RoPE tables of positions cached_lens
 // (as rope_tables). Returns (x [B, D], plan, cos [B, 1, H], sin).
@@ -746,6 +775,9 @@ TORCH_LIBRARY(ie, m) {
         "decode_plan(Tensor cached_lens, Tensor num_decoding, int batch, int num_q_heads, "
         "int num_kv_heads) -> Tensor");
     m.def(
+        "lm_head_greedy(Tensor h, Tensor weight, int n_tiles, float eps, bool norm, "
+        "Tensor(a!) seed) -> (Tensor, Tensor)");
+    m.def(
         "decode_step_prologue(Tensor ids, Tensor embed, Tensor cached_lens, Tensor num_decoding, "
         "int num_q_heads, int num_kv_heads, Tensor inv_freq) -> (Tensor, Tensor, Tensor, Tensor)");
     m.def("decode_attention_workspace_size(int batch, int num_q_heads) -> int");
@@ -778,6 +810,7 @@ TORCH_LIBRARY_IMPL(ie, CUDA, m) {
     m.impl("skinny_matmul_norm", &skinny_matmul_norm);
     m.impl("skinny_matmul_residual_", &skinny_matmul_residual_);
     m.impl("decode_step_prologue", &decode_step_prologue);
+    m.impl("lm_head_greedy", &lm_head_greedy);
     m.impl("skinny_weight_swizzle", &skinny_weight_swizzle);
     m.impl("decode_attention", &decode_attention);
     m.impl("decode_attention_rope", &decode_attention_rope);

@@ -37,7 +37,8 @@ from .attention_layer import attention, rope_inv_freq, rope_tables
 from .kernels import (LayerKVCache, add_rms_norm, decode_attention_rope, decode_plan,
                       decode_step_prologue,
                       fold_rms_norm_weight, linear, linear_norm, linear_residual_,
-                      linear_silu_mul, make_layer_cache, sample, skinny_matmul, swizzle_weight,
+                      linear_silu_mul, lm_head_greedy, make_layer_cache, sample, skinny_matmul,
+                      swizzle_weight,
                       swizzled_tiles, tune_linear, use_skinny, use_skinny_glu)
 
 
@@ -192,6 +193,11 @@ class DecodeStep:
 
     def forward(self) -> torch.Tensor:
         """One step: returns the greedy next token of every sequence, int64 [B, 1]."""
+        if self.swz["lm_head"] and self.embed.shape[1] == 2048:
+            # LM head (final RMSNorm inside) and greedy sampling in one launch
+            h = self.hidden(final_norm=False)
+            with nvtx.range("lm_head+sample"):
+                return lm_head_greedy(h, self.lm_head_w, self.seed, self.shape.eps)[1]
         logits = self.logits()
         with nvtx.range("sample"):
             return sample(logits, 0.0, self.seed)

@@ -221,6 +221,20 @@ def decode_plan(cached_lens: torch.Tensor, num_decoding: torch.Tensor, batch: in
                              int(num_kv_heads))
 
 
+def lm_head_greedy(h: torch.Tensor, weight: torch.Tensor, seed: torch.Tensor, eps: float = 0.0,
+                   norm: bool = True):
+    """The LM head and greedy sampling in one launch (ie_skinny_lm_head_greedy; no counterpart
+    in the reference): (logits, tokens) with logits = linear_norm(h, weight, eps, swizzled=True)
+    (norm; else skinny_matmul on the swizzled weight) and tokens = sample(logits, 0.0, seed)
+    (which it also advances by one), the same bits as those calls. weight: swizzle_weight of the
+    (norm-folded) LM head weight at swizzled_tiles' width; K = 2048, M <= 64."""
+    M, K = h.shape
+    N = weight.shape[0]
+    nt = swizzled_tiles(N, K, M)
+    assert nt in (1, 2, 4) and M <= 64 and K == 2048
+    return ops().lm_head_greedy(h, weight, int(nt), float(eps), bool(norm), seed)
+
+
 def decode_step_prologue(ids: torch.Tensor, embed: torch.Tensor, cached_lens: torch.Tensor,
                          num_decoding: torch.Tensor, num_q_heads: int, num_kv_heads: int,
                          inv_freq: torch.Tensor):

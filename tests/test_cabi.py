@@ -25,7 +25,7 @@ def test_torch_ops_registered(ie):
                  "prefill_attention", "decode_attention_workspace_size", "sample", "add_rms_norm",
                  "silu_mul", "skinny_matmul", "skinny_matmul_silu_mul", "skinny_matmul_norm",
                  "skinny_matmul_residual_", "prefill_plan", "decode_plan", "rope_tables",
-                 "skinny_weight_swizzle", "decode_step_prologue"]:
+                 "skinny_weight_swizzle", "decode_step_prologue", "lm_head_greedy"]:
         assert hasattr(ops, name), name
 
 

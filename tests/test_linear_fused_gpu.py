@@ -279,3 +279,41 @@ def test_fragment_order_activation(ie, dev, M):
                 torch.cuda.synchronize()
                 assert torch.equal(a, b), f"x fragments M={M} nt={nt} down nt={dnt} swz={swz}"
     say(f"fragment-order activation M={M}: bit-exact")
+
+
+@pytest.mark.parametrize("M", [1, 17, 32])
+def test_lm_head_greedy(ie, dev, M):
+    """lm_head_greedy (the looping LM head with the greedy choice in the same launch): logits bit
+    for bit those of linear_norm on the same reordered weight, tokens those of sample(logits, 0)
+    on them, the seed advanced by one per call as sample advances it, at every tile width and
+    on two calls in a row (the launch leaves its workspace zero). Planted: two equal columns
+    that are every row's maximum, the later one in an earlier row block (the first column
+    wins), and a NaN column (never chosen)."""
+    K_ = ie.kernels
+    N, K = 81920, 2048
+    g = torch.Generator().manual_seed(900 + M)
+    h = (torch.rand(M, K, generator=g) + 0.1).bfloat16().to(dev)  # positive rows
+    w = (0.01 * torch.randn(N, K, generator=g))
+    a, b, nan_col = 70000, 69840, 123
+    w[a] = 0.05
+    w[b] = 0.05
+    w[nan_col] = float("nan")
+    w = w.bfloat16().to(dev)
+    for nt in (1, 2, 4):
+        if nt + -(-M // 16) > 6:
+            continue
+        K_.use_skinny_swz[(N, K, M)] = nt
+        sw = ie.swizzle_weight(w, nt)
+        seed, seed_ref = (torch.full((1,), 5, dtype=torch.int64, device=dev) for _ in range(2))
+        for call in range(2):
+            logits, tok = ie.lm_head_greedy(h, sw, seed, EPS)
+            ref = K_.linear_norm(h, sw, EPS, swizzled=True)
+            want = ie.sample(ref, 0.0, seed_ref)
+            torch.cuda.synchronize()
+            assert torch.equal(logits.view(torch.int16), ref.view(torch.int16)), \
+                f"logits M={M} nt={nt} call {call}"
+            assert torch.equal(tok, want), f"tokens M={M} nt={nt} call {call}"
+            assert torch.all(tok == b), f"tie: the first column wins, M={M} nt={nt}"
+            assert seed.item() == seed_ref.item() == 6 + call
+        K_.use_skinny_swz.pop((N, K, M))
+    say(f"lm_head_greedy M={M}: bit-exact")
