@@ -267,3 +267,38 @@ def test_decode_planned_rejects_bad_plans_on_host(native):
         assert b"plan must hold" in lib.ie_attn_last_error()
         assert call(ctypes.c_void_p((1 << 20) + 4), grid) == HIP_ERROR_INVALID_VALUE
         assert b"aligned" in lib.ie_attn_last_error()
+
+
+def test_lm_head_greedy_and_prologue_reject_bad_arguments_on_host(native):
+    """ie_skinny_lm_head_greedy: flags other than 0 / NORM, k other than 2048, a null tokens
+    pointer and a short workspace; ie_decode_step_prologue: a model_dim that is not a multiple
+    of 8 and a null embedding: refused before any launch (the pointers are never dereferenced)."""
+    lib = native.cabi()
+    i32, i64, f32 = ctypes.c_int32, ctypes.c_int64, ctypes.c_float
+    p = ctypes.c_void_p(1 << 20)
+    null = ctypes.c_void_p(0)
+    lib.ie_skinny_lm_head_greedy_workspace_size.restype = ctypes.c_size_t
+    wsb = lib.ie_skinny_lm_head_greedy_workspace_size()
+    assert wsb >= 64 * 8 + 4
+    fn = lib.ie_skinny_lm_head_greedy
+    fn.restype = ctypes.c_int
+
+    def greedy(flags=1, k=2048, tokens=p, ws_bytes=wsb):
+        return fn(p, i64(k), i32(32), p, i32(81920), i32(k), i32(2), i32(flags), f32(1e-6), p,
+                  i64(81920), tokens, i64(1), p, p, ctypes.c_size_t(ws_bytes), null)
+
+    for kw, msg in ((dict(flags=2), b"flags"), (dict(k=1024), b"2048"),
+                    (dict(tokens=null), b"null"), (dict(ws_bytes=wsb - 8), b"workspace")):
+        assert greedy(**kw) == HIP_ERROR_INVALID_VALUE, kw
+        assert msg in lib.ie_attn_last_error(), kw
+    pro = lib.ie_decode_step_prologue
+    pro.restype = ctypes.c_int
+
+    def prologue(dim=2048, embed=p):
+        return pro(p, p, i32(32), i32(8), p, p, i32(64), p, p, p, embed, i64(2048), i64(1000),
+                   i32(dim), p, i64(2048), null)
+
+    assert prologue(dim=100) == HIP_ERROR_INVALID_VALUE
+    assert b"multiple of 8" in lib.ie_attn_last_error()
+    assert prologue(embed=null) == HIP_ERROR_INVALID_VALUE
+    assert b"null" in lib.ie_attn_last_error()
