@@ -22,7 +22,11 @@
 // residual add and RMSNorm of a decoder layer fused in (ie_skinny_gemm_fused): an RMSNorm
 // before the GEMM costs nothing but a sum of squares over the x fragments the waves already
 // hold, once its weight is folded into the GEMM's weight columns, and a residual add after it
-// is local to each output element.
+// is local to each output element. Weights reordered once into the MFMA fragment order skip the
+// LDS round trip (SWZ; the gate/up weight with gate and up rows paired per tile), as does an
+// activation written in that order by the gate/up launch for the down projection (YFRAG /
+// XFRAG); the LM head loops one workgroup per CU over its row blocks with x in registers
+// (LOOP, XREG) and can pick the greedy next token in the same launch (AMAX).
 #include "ie_common.h"
 
 namespace ie {
